@@ -1,0 +1,230 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X q4 x int8 matmul path (libkq4) on BASELINE.json's workload.
+
+Workload: the full decode-step linear set of a Qwen3-VL-2B-shaped
+decoder - QKV (2048 -> 16 q + 8 kv heads x 128), O (2048 -> 2048, + residual), gate/up
+(2048 -> 6144, one fused launch) and down (6144 -> 2048, + residual) - for all 28 layers, at
+M = 1 token (M = 4 reported alongside). One step = one token through the 28 layers' linear sets
+(quantize + matmul launches, 8 launches per layer). The 28 layers are distinct HBM copies
+(28 x 28.3 MB = 793 MB > the 256 MB Infinity Cache), so every step streams its weights from HBM.
+Inputs are resident in HBM before the timed region.
+
+value = algorithmic bytes per step (weights N*K*18/32 + activations M*K*4 + outputs M*N*4 +
+residuals M*N*4) / step time, in GB/s. roofline: the dominant kernel (the fused gate/up GEMV),
+timed on its own stream with HIP events, against MI355X HBM peak 8 TB/s. cpu_baseline: the
+reference's own x86-64 path (oracle/_ref, built from /root/reference) on a bounded sample.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--m 1] [--no-cpu]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "kestrel-llm_amd"))
+
+import numpy as np  # noqa: E402
+
+import synth  # noqa: E402
+
+METRIC = "q4 GEMV µs/call + HBM GB/s (% peak); prefill GEMM int8 TOPS (% peak)"
+HBM_PEAK_GBS = 8000.0
+CFG = synth.QWEN3VL_2B
+
+
+def layer_mats():
+    return {name: (rows, cols) for name, rows, cols in synth.layer_shapes(CFG)}
+
+
+def step_bytes(m):
+    """Algorithmic bytes of one layer's linear set at m tokens (x counted once per launch)."""
+    s = layer_mats()
+    wb = sum(r * c * 18 // 32 for r, c in s.values())
+    h, q, kv, f = CFG["hidden"], s["q"][0], s["k"][0], CFG["ffn"]
+    act = m * 4 * (h + q + h + f)                     # x of QKV, O, gate/up, down
+    out = m * 4 * (q + 2 * kv + h + 2 * f + h)
+    res = m * 4 * (h + h)                             # residual reads of O and down
+    return wb + act + out + res
+
+
+def gate_up_bytes(m):
+    h, f = CFG["hidden"], CFG["ffn"]
+    return 2 * f * h * 18 // 32 + m * h * 4 + 2 * m * f * 4
+
+
+def make_model(torch, n_layers, seed=1):
+    """One layer of seeded weights, copied to n_layers distinct HBM buffers."""
+    base = {name: synth.make_q4_weights(r, c, seed + i, **synth.SCALE_2B)
+            for i, (name, (r, c)) in enumerate(layer_mats().items())}
+    dev0 = {k: torch.from_numpy(v.reshape(-1)).cuda() for k, v in base.items()}
+    return [{k: v.clone() for k, v in dev0.items()} for _ in range(n_layers)], base
+
+
+def run_gpu(args):
+    import torch
+
+    import kq4
+
+    kq4.init(0)
+    torch.cuda.set_device(0)
+    stream = torch.cuda.current_stream()
+    m = args.m
+    s = layer_mats()
+    h, q, kv, f = CFG["hidden"], s["q"][0], s["k"][0], CFG["ffn"]
+    layers, _ = make_model(torch, CFG["layers"])
+    dev = lambda shape: torch.empty(shape, dtype=torch.float32, device="cuda")  # noqa: E731
+    x = torch.from_numpy(synth.make_activations(m, h, 7)).cuda()
+    attn = torch.from_numpy(synth.make_activations(m, q, 8)).cuda()
+    act = torch.from_numpy(synth.make_activations(m, f, 9)).cuda()
+    resid = torch.from_numpy(synth.make_activations(m, h, 10)).cuda()
+    oq, ok_, ov, oo, og, ou, od = dev((m, q)), dev((m, kv)), dev((m, kv)), dev((m, h)), \
+        dev((m, f)), dev((m, f)), dev((m, h))
+
+    def step():
+        for L in layers:
+            kq4.matmul_multi_dev([oq, ok_, ov], x, [L["q"], L["k"], L["v"]], [q, kv, kv], h,
+                                 stream=stream)
+            kq4.matmul_dev(oo, attn, L["o"], h, q, residual=resid, stream=stream)
+            kq4.matmul_multi_dev([og, ou], x, [L["gate"], L["up"]], [f, f], h, stream=stream)
+            kq4.matmul_dev(od, act, L["down"], h, f, residual=resid, stream=stream)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(args.steps):
+        step()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms_step = e0.elapsed_time(e1) / args.steps
+    total_bytes = step_bytes(m) * CFG["layers"]
+    value = total_bytes / (ms_step * 1e-3) / 1e9
+
+    # dominant kernel alone: fused gate/up GEMV from pre-quantized activations, rotating layers
+    xq = torch.empty((m, h), dtype=torch.int8, device="cuda")
+    xd = dev((m, h // 32))
+    kq4.quantize_dev(x, xq, xd, stream=stream)
+    reps = max(args.steps, 20)
+    for L in layers[:4]:
+        kq4.matmul_multi_q_dev([og, ou], xq, xd, [L["gate"], L["up"]], [f, f], h, m,
+                               stream=stream)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for i in range(reps):
+        L = layers[i % len(layers)]
+        kq4.matmul_multi_q_dev([og, ou], xq, xd, [L["gate"], L["up"]], [f, f], h, m,
+                               stream=stream)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    us_launch = e0.elapsed_time(e1) * 1e3 / reps
+    achieved = gate_up_bytes(m) / (us_launch * 1e-6) / 1e9
+    return dict(ms_per_step=ms_step, value=value, us_gate_up=us_launch, achieved=achieved,
+                total_bytes=total_bytes)
+
+
+def cpu_baseline(m, budget_s=12.0):
+    """The reference's x86-64 op wrappers (fp32/int16 activation arithmetic; a timing
+    baseline, not a parity reference) on a bounded sample: layers cycled over enough distinct
+    weight copies to exceed the host LLC, for ~budget_s seconds."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle
+
+    threads = int(os.environ.get("KQ4_CPU_THREADS", os.cpu_count() or 1))
+    kind = "reference" if oracle.ref_available() else "port"
+    s = layer_mats()
+    h, q, kv, f = CFG["hidden"], s["q"][0], s["k"][0], CFG["ffn"]
+    n_copies = 10
+    rng = np.random.default_rng(3)
+    layers = [{k: rng.integers(0, 256, size=v.size, dtype=np.uint8) for k, v in
+               {n: np.empty(r * c * 18 // 32, np.uint8) for n, (r, c) in s.items()}.items()}
+              for _ in range(n_copies)]
+    scales = np.frombuffer(np.float16([0.02] * 4).tobytes(), np.uint8)
+    for L in layers:                                   # random nibbles, finite f16 scales
+        for name, (r, c) in s.items():
+            L[name].reshape(r // 4, c // 32, 72)[:, :, :8] = scales
+    x = synth.make_activations(m, h, 7)
+    attn = synth.make_activations(m, q, 8)
+    actv = synth.make_activations(m, f, 9)
+    res = synth.make_activations(m, h, 10)
+    bufs = {k: np.empty((m, n), np.float32) for k, n in
+            dict(q=q, k=kv, v=kv, o=h, g=f, u=f, d=h).items()}
+    P = lambda a: a.ctypes.data  # noqa: E731
+    if kind == "reference":
+        r = oracle.ref(threads)
+
+        def layer(L):
+            r.kref_qkv_batched(P(bufs["q"]), P(bufs["k"]), P(bufs["v"]), P(L["q"]), P(L["k"]),
+                               P(L["v"]), P(x), q, kv, h, m)
+            r.kref_o_residual_batched(P(bufs["o"]), P(res), P(L["o"]), P(attn), h, q, m)
+            r.kref_gate_up_batched(P(bufs["g"]), P(bufs["u"]), P(L["gate"]), P(L["up"]), P(x),
+                                   f, h, m)
+            r.kref_down_residual_batched(P(bufs["d"]), P(res), P(L["down"]), P(actv), h, f, m)
+    else:
+        threads = 1
+
+        def layer(L):
+            for name, (rr, cc) in s.items():
+                src = {"q": x, "k": x, "v": x, "o": attn, "gate": x, "up": x, "down": actv}[name]
+                oracle.matmul(L[name], src, rr, cc)
+
+    layer(layers[0])
+    n = 0
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < budget_s:
+        layer(layers[n % n_copies])
+        n += 1
+    dt = (time.perf_counter() - t0) / n
+    gbs = step_bytes(m) / dt / 1e9
+    return dict(value=round(gbs, 3), unit="GB/s", cores=threads, kind=kind,
+                sample=f"{n} layer linear sets (QKV+O+gate/up+down, M={m}) over {n_copies} "
+                       f"distinct weight copies, {dt * 1e3:.2f} ms per layer")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--m", type=int, default=1, help="tokens per step (decode batch)")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
+              "(the path would shard along weight rows / experts, see DESIGN.md)",
+              file=sys.stderr)
+        sys.exit(2)
+    g = run_gpu(args)
+    line = {
+        "metric": METRIC,
+        "value": round(g["value"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(g["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic",
+        "config": {"workload": f"qwen3-vl-2b decode-step linear set (QKV, O+res, gate/up, "
+                               f"down+res) x {CFG['layers']} layers, M={args.m}",
+                   "global_batch": args.m, "bytes_per_step": g["total_bytes"],
+                   "weights": "q4_0 4x4 tiles, int8 block-32 activations"},
+        "gate_up_us_per_call": round(g["us_gate_up"], 3),
+        "roofline": {"bound": "hbm", "achieved": round(g["achieved"], 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(g["achieved"] / HBM_PEAK_GBS, 4),
+                     "traffic": None,
+                     "kernel": "kq4_gemv_kernel (fused gate/up, 2 x 6144x2048)"},
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(args.m, args.cpu_seconds)
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

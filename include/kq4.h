@@ -1,0 +1,153 @@
+/* kq4.h - C ABI of libkq4.so, the MI355X (gfx950) Q4_0 x int8 block-quantized matmul.
+ *
+ * This is the drop-in boundary for kestrel-llm's quantized-matmul op family. The reference
+ * runs the op inside src/model/vllm_safetensors.c as `static` C11 functions; its only
+ * accelerator boundary is the NPU hook, which returns 1 = executed / 0 = run the CPU path and
+ * keys a persistent device weight cache by `wkey = layer<<32 | proj`
+ * (st_npu_try_gemm_batched_q4 vllm_safetensors.c:3371-3506, vllm_npu_gemm_gw
+ * include/npu/vllm_npu.h:135-159). The host-pointer entry points below follow that contract;
+ * the device-pointer entry points are the same ops for callers whose tensors already live in
+ * HBM. Plain C types only (no HIP/torch types): a HIP stream is passed as `void *`
+ * (NULL = the default stream).
+ *
+ * Data formats (identical to the reference's):
+ *   weights   VQF 4x4 tiles: [rows/4 groups][cols/32 blocks] x 72 B; a tile holds 4 f16 row
+ *             scales then 64 nibble bytes, byte 8+16k+4r+i = legacy qs byte 4k+i of row r,
+ *             XOR 0x88 (vqf_convert/src/qk_repack.c:19-46, VQF_FLAG_Q4_4X4
+ *             include/model/vqf_format.h:32)
+ *   x / out   fp32 token-major [n_batch][cols] / [n_batch][rows]
+ *   residual  fp32 [n_batch][rows]; out = residual + W.x (fused O / down projections)
+ * Preconditions (as the reference's 4x4 path): rows % 4 == 0, cols % 32 == 0.
+ *
+ * Threading: like the reference op (called only from the single inference thread,
+ * vllm_safetensors.c:4670-4672), the library keeps one workspace per device; calls that
+ * overlap on one device (different host threads or different streams) race on it.
+ *
+ * Error convention: device-pointer calls return KQ4_OK (0) or a negative KQ4_E* code;
+ * host-pointer drop-in calls return 1 (done on the GPU) or 0 (not done: the caller runs its
+ * CPU path). kq4_last_error() describes the last failure of the calling thread.
+ */
+#ifndef KQ4_H
+#define KQ4_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KQ4_OK 0
+#define KQ4_EINVAL (-1)   /* bad shape / argument */
+#define KQ4_EHIP (-2)     /* HIP runtime error */
+#define KQ4_ENOMEM (-3)   /* device allocation failed */
+#define KQ4_ENODEV (-4)   /* no usable gfx950 device */
+
+/* fp32 accumulation chain (how per-block products are summed; integer block sums are the
+ * same in all of them). AUTO is the reference's dispatch (q4x4_gemm_batched
+ * vllm_safetensors.c:4593-4631): n_batch <= 3 -> CTILE; n_batch > 3 -> ASM on the first
+ * n_batch & ~3 tokens and CTILE on the rest. */
+#define KQ4_CHAIN_AUTO 0
+#define KQ4_CHAIN_CTILE 1   /* q4x4_dot1_group16, vllm_safetensors.c:4180-4216 */
+#define KQ4_CHAIN_GEMV32 2  /* q4x4_dot1_group16_gemv (M4f), :4229-4251 */
+#define KQ4_CHAIN_ASM 3     /* llama 4x4 asm GEMM, f16-rounded activation scale, :4328-4368 */
+
+/* Most weight matrices one fused call may take (QKV = 3, gate/up = 2). */
+#define KQ4_MAX_MATS 4
+
+/* ---- lifetime ---------------------------------------------------------------------------- */
+
+/* Selects `device` (a gfx950 GPU) for the calling thread and prepares its workspace.
+ * Replaces the NPU open/probe step (vllm_npu_available include/npu/vllm_npu.h:88-100). */
+int kq4_init(int device);
+/* Frees every device buffer the library owns (workspaces, weight cache). */
+void kq4_shutdown(void);
+const char *kq4_last_error(void);
+/* Library version string. */
+const char *kq4_version(void);
+
+/* ---- host-pointer drop-in API (synchronous; 1 = done, 0 = caller falls back) -------------- */
+
+/* Uploads 4x4 q4 weights once and keeps them under `wkey` (layer<<32 | proj), as the NPU
+ * weight cache does (st_npu_gw_get/build vllm_safetensors.c:2780-3040). */
+int kq4_weights_upload(uint64_t wkey, const uint8_t *w4x4, int rows, int cols);
+int kq4_weights_evict(uint64_t wkey);
+
+/* out = [residual +] W.x for n_batch tokens; replaces q4x4_gemm_batched / dyn_matvec_q4_q8*
+ * (vllm_safetensors.c:4593-4631, 6147-6174, 8628-8786) behind st_npu_try_gemm_batched_q4's
+ * 1/0 contract (:3371-3506). wkey != 0 uses (or fills) the weight cache; wkey == 0 copies the
+ * weights for this call only. */
+int kq4_matmul(float *out, const float *x, const float *residual, const uint8_t *w4x4, int rows,
+               int cols, int n_batch, int chain, uint64_t wkey);
+
+/* Up to KQ4_MAX_MATS matrices sharing one activation (fused QKV / gate+up wrappers); wkeys may
+ * be NULL (no caching) or hold one key per matrix (0 = no caching for that matrix). */
+int kq4_matmul_multi(int n_mats, float *const *out, const float *const *residual,
+                     const uint8_t *const *w4x4, const int *rows, int cols, const float *x,
+                     int n_batch, int chain, const uint64_t *wkeys);
+
+/* MoE FFN of T tokens with top-k routing given as expert ids `sel` [T][tk] and weights `pr`
+ * [T][tk]; int8 activation track (VLLM_ACTQ=1) of st_moe_ffn_sparse_q4 / _batch_arm
+ * (vllm_safetensors.c:12921-13398, 14894-15064). G/U: [ne*ef rows][d cols], D: [d rows]
+ * [ne*ef cols], all 4x4 tiles. wkey != 0 caches G/U/D under wkey, wkey+1, wkey+2. */
+int kq4_moe_ffn(float *Y, const float *X, const int *sel, const float *pr, int T, int tk,
+                const uint8_t *G, const uint8_t *U, const uint8_t *D, int ne, int d, int ef,
+                uint64_t wkey);
+
+/* ---- device-pointer API (stream-ordered, asynchronous) ----------------------------------- */
+
+/* Activation quantizer (quantize_row_q8_0_act vllm_safetensors.c:7893-7920) for n_batch rows:
+ * xq int8 [n_batch][cols], xd f32 [n_batch][cols/32]. xde (may be NULL) receives the scale
+ * each token's chain multiplies by: f32(f16_rne(xd)) for ASM-chain tokens, xd otherwise. */
+int kq4_quantize_dev(int8_t *xq, float *xd, float *xde, const float *x, int n_batch, int cols,
+                     int chain, void *stream);
+
+/* Quantize x once, then out = [residual +] W.x. */
+int kq4_matmul_dev(float *out, const float *x, const float *residual, const uint8_t *w,
+                   int rows, int cols, int n_batch, int chain, void *stream);
+
+/* Up to KQ4_MAX_MATS weight matrices sharing one activation (one quantization, one launch):
+ * fused QKV (dyn_matvec_q4_q8_fused_qkv_batched :8684) and gate/up (:8738). residual[i] may
+ * be NULL. */
+int kq4_matmul_multi_dev(int n_mats, float *const *out, const float *const *residual,
+                         const uint8_t *const *w, const int *rows, int cols, const float *x,
+                         int n_batch, int chain, void *stream);
+
+/* Same op from already-quantized activations (xq/xd as kq4_quantize_dev writes them). */
+int kq4_matmul_q_dev(float *out, const int8_t *xq, const float *xd, const float *residual,
+                     const uint8_t *w, int rows, int cols, int n_batch, int chain, void *stream);
+
+/* Several matrices from one already-quantized activation: the reference's batched wrappers
+ * quantize once and run q/k/v or gate/up from the same xq/xd (:6670-6706, :6846-6870). */
+int kq4_matmul_multi_q_dev(int n_mats, float *const *out, const float *const *residual,
+                           const uint8_t *const *w, const int *rows, int cols, const int8_t *xq,
+                           const float *xd, int n_batch, int chain, void *stream);
+
+/* Debug/verification: the exact integer block sums S_lo / S_hi [n_batch][rows][cols/32]
+ * computed by the same device dot-product routine the matmul kernels use. */
+int kq4_block_sums_dev(int32_t *s_lo, int32_t *s_hi, const int8_t *xq, const uint8_t *w,
+                       int rows, int cols, int n_batch, void *stream);
+
+/* MoE routing on the device: deterministic top-k (ties -> smaller id) + softmax over the k
+ * selected (vllm_safetensors.c:12968-12984). logits [T][ne] -> sel [T][tk], pr [T][tk]. */
+int kq4_moe_route_dev(int *sel, float *pr, const float *logits, int T, int ne, int tk,
+                      void *stream);
+
+/* MoE FFN on device buffers (see kq4_moe_ffn). */
+int kq4_moe_ffn_dev(float *Y, const float *X, const int *sel, const float *pr, int T, int tk,
+                    const uint8_t *G, const uint8_t *U, const uint8_t *D, int ne, int d, int ef,
+                    void *stream);
+
+/* Verification variant of kq4_moe_ffn_dev exposing the stages the reference's own A/B checks
+ * compare (VLLM_MOE_2B_VERIFY, vllm_safetensors.c:14604-14625): gate_out/up_out/av_out
+ * [T*tk][ef] (each may be NULL; gate_out and up_out together), and av_in [T*tk][ef] which, when
+ * not NULL, replaces the computed SiLU product as the input of the down projection. */
+int kq4_moe_ffn_stages_dev(float *Y, const float *X, const int *sel, const float *pr, int T,
+                           int tk, const uint8_t *G, const uint8_t *U, const uint8_t *D, int ne,
+                           int d, int ef, float *gate_out, float *up_out, float *av_out,
+                           const float *av_in, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* KQ4_H */

@@ -1,0 +1,570 @@
+// kq4_api.hip - C ABI of libkq4.so (declared in include/kq4.h): argument checks, per-device
+// workspaces, the weight cache of the host-pointer drop-in API, and kernel dispatch.
+#include "../../include/kq4.h"
+#include "kq4_internal.h"
+
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <mutex>
+#include <unordered_map>
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char *fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+#define KQ4_HIP(call)                                                                   \
+  do {                                                                                  \
+    hipError_t e_ = (call);                                                             \
+    if (e_ != hipSuccess) return fail(KQ4_EHIP, "%s: %s", #call, hipGetErrorString(e_)); \
+  } while (0)
+
+struct Buf {
+  void *p = nullptr;
+  size_t cap = 0;
+};
+
+struct WEntry {
+  uint8_t *p;
+  size_t bytes;
+};
+
+const int kMaxDev = 16;
+
+struct DevState {
+  bool ready = false;
+  Buf ws;    // quantized activations, split-K partials, MoE staging
+  Buf cnt;   // split-K arrival counters, kept zero between launches
+  Buf hx, hres, hout, hw, hsel, hpr;   // staging for the host-pointer API
+  std::unordered_map<uint64_t, WEntry> wcache;
+};
+
+DevState g_dev[kMaxDev];
+std::mutex g_mu;   // guards lazy init / cache maps (the op itself is single-caller)
+
+inline size_t al256(size_t n) { return (n + 255) & ~(size_t)255; }
+
+int cur_dev(DevState **out) {
+  int d = 0;
+  KQ4_HIP(hipGetDevice(&d));
+  if (d < 0 || d >= kMaxDev) return fail(KQ4_ENODEV, "device %d out of range", d);
+  if (!g_dev[d].ready) {
+    int rc = kq4_init(d);
+    if (rc != KQ4_OK) return rc;
+  }
+  *out = &g_dev[d];
+  return KQ4_OK;
+}
+
+int ensure(Buf &b, size_t bytes, bool zero = false) {
+  if (b.cap >= bytes) return KQ4_OK;
+  size_t n = al256(bytes > 4096 ? bytes + bytes / 4 : 4096);
+  if (b.p) {
+    KQ4_HIP(hipDeviceSynchronize());   // in-flight kernels may still read the old buffer
+    KQ4_HIP(hipFree(b.p));
+    b.p = nullptr;
+    b.cap = 0;
+  }
+  if (hipMalloc(&b.p, n) != hipSuccess) {
+    b.p = nullptr;
+    return fail(KQ4_ENOMEM, "hipMalloc(%zu) failed", n);
+  }
+  if (zero) KQ4_HIP(hipMemset(b.p, 0, n));
+  b.cap = n;
+  return KQ4_OK;
+}
+
+struct Carve {   // bump allocator over a workspace
+  char *base;
+  size_t off = 0;
+  template <class T>
+  T *take(size_t count) {
+    T *p = reinterpret_cast<T *>(base + off);
+    off += al256(count * sizeof(T));
+    return p;
+  }
+};
+
+bool shape_ok(int rows, int cols) { return rows > 0 && rows % 4 == 0 && cols > 0 && cols % 32 == 0; }
+
+int asm_tokens_for(int chain, int n) {
+  if (chain == KQ4_CHAIN_ASM) return n;
+  if (chain == KQ4_CHAIN_AUTO) return n > 3 ? (n & ~3) : 0;
+  return 0;
+}
+
+// GEMV over n_mats matrices for n tokens (n <= 8) from token-major xq/xd.
+int run_gemv(DevState *ds, int n_mats, float *const *out, const float *const *res,
+             const uint8_t *const *w, const int *rows, int cols, const int8_t *xq, const float *xd,
+             int n, int asm_tokens, Carve &cv, size_t ws_limit, hipStream_t s) {
+  const int nb = cols / 32;
+  int slabs_total = 0;
+  long wg_est = 0;
+  for (int i = 0; i < n_mats; ++i) {
+    slabs_total += (rows[i] + 15) / 16;
+    wg_est += (long)((rows[i] + 15) / 16) * ((nb + 63) / 64);
+  }
+  const int ppl = wg_est >= 1024 ? 2 : 1;
+  const int bpw = 32 * ppl;
+  const int ks = (nb + bpw - 1) / bpw;
+  KQ4GemvArgs a;
+  memset(&a, 0, sizeof(a));
+  a.nmat = n_mats;
+  a.xq = xq;
+  a.xd = xd;
+  a.asm_tokens = asm_tokens;
+  a.cols = cols;
+  a.nb = nb;
+  a.blocks_per_wg = bpw;
+  int rc = ensure(ds->cnt, (size_t)slabs_total * sizeof(unsigned), true);
+  if (rc) return rc;
+  unsigned *cnt = static_cast<unsigned *>(ds->cnt.p);
+  int wg = 0;
+  for (int i = 0; i < n_mats; ++i) {
+    const int slabs = (rows[i] + 15) / 16;
+    KQ4GemvMat &m = a.mat[i];
+    m.w = w[i];
+    m.out = out[i];
+    m.res = res ? res[i] : nullptr;
+    m.rows = rows[i];
+    m.ks = ks;
+    m.wg_begin = wg;
+    m.cnt = cnt;
+    cnt += slabs;
+    m.part = nullptr;
+    if (ks > 1) m.part = cv.take<float>((size_t)slabs * ks * n * 16);
+    wg += slabs * ks;
+  }
+  if (cv.off > ws_limit) return fail(KQ4_EINVAL, "internal: workspace carve overflow");
+  KQ4_HIP((hipError_t)kq4_launch_gemv(a, n, ppl, wg, s));
+  return KQ4_OK;
+}
+
+size_t gemv_part_bytes(int n_mats, const int *rows, int cols, int n) {
+  const int nb = cols / 32;
+  size_t b = 0;
+  for (int i = 0; i < n_mats; ++i) {
+    const int slabs = (rows[i] + 15) / 16;
+    b += al256((size_t)slabs * ((nb + 31) / 32) * n * 16 * sizeof(float));
+  }
+  return b;
+}
+
+int matmul_impl(int n_mats, float *const *out, const float *const *res, const uint8_t *const *w,
+                const int *rows, int cols, const float *x, const int8_t *xq_in,
+                const float *xd_in, int n, int chain, hipStream_t s) {
+  if (n_mats < 1 || n_mats > KQ4_MAX_MATS) return fail(KQ4_EINVAL, "n_mats=%d", n_mats);
+  if (chain < KQ4_CHAIN_AUTO || chain > KQ4_CHAIN_ASM) return fail(KQ4_EINVAL, "chain=%d", chain);
+  if (n < 0) return fail(KQ4_EINVAL, "n_batch=%d", n);
+  for (int i = 0; i < n_mats; ++i) {
+    if (!shape_ok(rows[i], cols))
+      return fail(KQ4_EINVAL, "rows=%d cols=%d: need rows%%4==0, cols%%32==0", rows[i], cols);
+    if (!w[i] || !out[i]) return fail(KQ4_EINVAL, "null weight/output pointer");
+  }
+  if (n == 0) return KQ4_OK;
+  DevState *ds = nullptr;
+  int rc = cur_dev(&ds);
+  if (rc) return rc;
+  const int nb = cols / 32;
+  const size_t qbytes = al256((size_t)n * cols) + al256((size_t)n * nb * sizeof(float));
+
+  if (n <= KQ4_GEMV_MAX_M) {
+    const size_t need = qbytes + gemv_part_bytes(n_mats, rows, cols, n);
+    if ((rc = ensure(ds->ws, need))) return rc;
+    Carve cv{static_cast<char *>(ds->ws.p)};
+    const int8_t *xq = xq_in;
+    const float *xd = xd_in;
+    if (x) {
+      int8_t *q = cv.take<int8_t>((size_t)n * cols);
+      float *d = cv.take<float>((size_t)n * nb);
+      KQ4_HIP((hipError_t)kq4_launch_quantize(x, q, d, nullptr, n, cols, 0, s, 0));
+      xq = q;
+      xd = d;
+    } else {
+      cv.off = qbytes;
+    }
+    return run_gemv(ds, n_mats, out, res, w, rows, cols, xq, xd, n,
+                    asm_tokens_for(chain, n), cv, need, s);
+  }
+
+  // prefill: int8-MFMA GEMM on the main segment, GEMV on the 1..3-token CTILE tail (AUTO)
+  const int main_n = chain == KQ4_CHAIN_AUTO ? (n & ~3) : n;
+  const int tail = n - main_n;
+  const int main_chain = chain == KQ4_CHAIN_AUTO ? KQ4_CHAIN_ASM : chain;
+  size_t need = qbytes;
+  if (tail) need += gemv_part_bytes(n_mats, rows, cols, tail);
+  if ((rc = ensure(ds->ws, need))) return rc;
+  Carve cv{static_cast<char *>(ds->ws.p)};
+  KQ4GemmAct act;
+  const int8_t *xq_t = nullptr;
+  const float *xd_t = nullptr;
+  if (x) {
+    int8_t *q = cv.take<int8_t>((size_t)n * cols);
+    float *d = cv.take<float>((size_t)n * nb);
+    // main tokens block-major (contiguous 32-byte token rows per block for the MFMA staging)
+    KQ4_HIP((hipError_t)kq4_launch_quantize(x, q, d, nullptr, main_n, cols, 0, s, 1));
+    act = KQ4GemmAct{q, 32, (long)main_n * 32, d, 1, main_n};
+    if (tail) {
+      int8_t *qt = q + (size_t)main_n * cols;
+      float *dt = d + (size_t)main_n * nb;
+      KQ4_HIP((hipError_t)kq4_launch_quantize(x + (size_t)main_n * cols, qt, dt, nullptr, tail,
+                                              cols, 0, s, 0));
+      xq_t = qt;
+      xd_t = dt;
+    }
+  } else {
+    cv.off = qbytes;
+    act = KQ4GemmAct{xq_in, cols, 32, xd_in, nb, 1};
+    xq_t = xq_in + (size_t)main_n * cols;
+    xd_t = xd_in + (size_t)main_n * nb;
+  }
+  for (int i = 0; i < n_mats; ++i)
+    KQ4_HIP((hipError_t)kq4_launch_gemm(out[i], res ? res[i] : nullptr, w[i], act, rows[i], cols,
+                                        main_n, main_chain, s));
+  if (tail) {
+    float *o2[KQ4_MAX_MATS];
+    const float *r2[KQ4_MAX_MATS];
+    for (int i = 0; i < n_mats; ++i) {
+      o2[i] = out[i] + (size_t)main_n * rows[i];
+      r2[i] = (res && res[i]) ? res[i] + (size_t)main_n * rows[i] : nullptr;
+    }
+    return run_gemv(ds, n_mats, o2, r2, w, rows, cols, xq_t, xd_t, tail, 0, cv, need, s);
+  }
+  return KQ4_OK;
+}
+
+int moe_impl(float *Y, const float *X, const int *sel, const float *pr, int T, int tk,
+             const uint8_t *G, const uint8_t *U, const uint8_t *D, int ne, int d, int ef,
+             float *g_out, float *u_out, float *av_out, const float *av_in, hipStream_t s) {
+  if (T < 0 || tk < 1 || tk > 32 || ne < 1 || d <= 0 || d % 32 || ef <= 0 || ef % 32)
+    return fail(KQ4_EINVAL, "moe: T=%d tk=%d ne=%d d=%d ef=%d", T, tk, ne, d, ef);
+  if (T == 0) return KQ4_OK;
+  DevState *ds = nullptr;
+  int rc = cur_dev(&ds);
+  if (rc) return rc;
+  const size_t np = (size_t)T * tk;
+  const size_t need = al256((ne + 1) * sizeof(int)) + al256(np * sizeof(int)) +
+                      al256((size_t)T * d) + al256((size_t)T * (d / 32) * sizeof(float)) +
+                      al256(np * ef * sizeof(float)) + al256(np * ef) +
+                      al256(np * (ef / 32) * sizeof(float)) + al256(np * d * sizeof(float));
+  if ((rc = ensure(ds->ws, need))) return rc;
+  Carve cv{static_cast<char *>(ds->ws.p)};
+  KQ4MoeWs ws;
+  ws.ex_off = cv.take<int>(ne + 1);
+  ws.ex_pair = cv.take<int>(np);
+  ws.xq = cv.take<int8_t>((size_t)T * d);
+  ws.xd = cv.take<float>((size_t)T * (d / 32));
+  ws.av = av_out ? av_out : cv.take<float>(np * ef);
+  if (av_out) cv.take<float>(np * ef);
+  ws.avq = cv.take<int8_t>(np * ef);
+  ws.avd = cv.take<float>(np * (ef / 32));
+  ws.P = cv.take<float>(np * d);
+  KQ4_HIP((hipError_t)kq4_launch_moe_dbg(Y, X, sel, pr, T, tk, G, U, D, ne, d, ef, ws, g_out,
+                                         u_out, av_in, s));
+  return KQ4_OK;
+}
+
+// ---- host-pointer API helpers --------------------------------------------------------------
+int dev_weights(DevState *ds, uint64_t wkey, const uint8_t *w, size_t bytes, Buf &tmp,
+                const uint8_t **dev) {
+  if (wkey) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    auto it = ds->wcache.find(wkey);
+    if (it != ds->wcache.end() && it->second.bytes == bytes) {
+      *dev = it->second.p;
+      return KQ4_OK;
+    }
+  }
+  if (wkey) {
+    void *p = nullptr;
+    if (hipMalloc(&p, bytes) != hipSuccess) return fail(KQ4_ENOMEM, "weights %zu B", bytes);
+    hipError_t e = hipMemcpy(p, w, bytes, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+      hipFree(p);
+      return fail(KQ4_EHIP, "weight upload: %s", hipGetErrorString(e));
+    }
+    std::lock_guard<std::mutex> lk(g_mu);
+    auto it = ds->wcache.find(wkey);
+    if (it != ds->wcache.end()) hipFree(it->second.p);
+    ds->wcache[wkey] = WEntry{static_cast<uint8_t *>(p), bytes};
+    *dev = static_cast<uint8_t *>(p);
+    return KQ4_OK;
+  }
+  int rc = ensure(tmp, bytes);
+  if (rc) return rc;
+  KQ4_HIP(hipMemcpy(tmp.p, w, bytes, hipMemcpyHostToDevice));
+  *dev = static_cast<uint8_t *>(tmp.p);
+  return KQ4_OK;
+}
+
+size_t wbytes(int rows, int cols) { return (size_t)(rows / 4) * (cols / 32) * 72; }
+
+}  // namespace
+
+extern "C" {
+
+const char *kq4_version(void) { return "kq4 0.1 (gfx950)"; }
+
+const char *kq4_last_error(void) { return g_err; }
+
+int kq4_init(int device) {
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) return fail(KQ4_ENODEV, "no HIP device");
+  if (device < 0 || device >= n || device >= kMaxDev)
+    return fail(KQ4_ENODEV, "device %d of %d", device, n);
+  KQ4_HIP(hipSetDevice(device));
+  hipDeviceProp_t prop;
+  KQ4_HIP(hipGetDeviceProperties(&prop, device));
+  if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+    return fail(KQ4_ENODEV, "device %d is %s; libkq4 is built for gfx950", device,
+                prop.gcnArchName);
+  std::lock_guard<std::mutex> lk(g_mu);
+  g_dev[device].ready = true;
+  return KQ4_OK;
+}
+
+void kq4_shutdown(void) {
+  int cur = 0;
+  hipGetDevice(&cur);
+  for (int d = 0; d < kMaxDev; ++d) {
+    DevState &s = g_dev[d];
+    if (!s.ready) continue;
+    hipSetDevice(d);
+    hipDeviceSynchronize();
+    Buf *bufs[] = {&s.ws, &s.cnt, &s.hx, &s.hres, &s.hout, &s.hw, &s.hsel, &s.hpr};
+    for (Buf *b : bufs) {
+      if (b->p) hipFree(b->p);
+      *b = Buf();
+    }
+    for (auto &kv : s.wcache) hipFree(kv.second.p);
+    s.wcache.clear();
+    s.ready = false;
+  }
+  hipSetDevice(cur);
+}
+
+int kq4_quantize_dev(int8_t *xq, float *xd, float *xde, const float *x, int n_batch, int cols,
+                     int chain, void *stream) {
+  if (n_batch < 0 || cols <= 0 || cols % 32 || !xq || !xd || (!x && n_batch))
+    return fail(KQ4_EINVAL, "quantize: n_batch=%d cols=%d", n_batch, cols);
+  KQ4_HIP((hipError_t)kq4_launch_quantize(x, xq, xd, xde, n_batch, cols,
+                                          asm_tokens_for(chain, n_batch),
+                                          (hipStream_t)stream, 0));
+  return KQ4_OK;
+}
+
+int kq4_matmul_dev(float *out, const float *x, const float *residual, const uint8_t *w, int rows,
+                   int cols, int n_batch, int chain, void *stream) {
+  if (!x && n_batch) return fail(KQ4_EINVAL, "null x");
+  const float *res[1] = {residual};
+  return matmul_impl(1, &out, res, &w, &rows, cols, x, nullptr, nullptr, n_batch, chain,
+                     (hipStream_t)stream);
+}
+
+int kq4_matmul_multi_dev(int n_mats, float *const *out, const float *const *residual,
+                         const uint8_t *const *w, const int *rows, int cols, const float *x,
+                         int n_batch, int chain, void *stream) {
+  if (!x && n_batch) return fail(KQ4_EINVAL, "null x");
+  if (!out || !w || !rows) return fail(KQ4_EINVAL, "null array argument");
+  return matmul_impl(n_mats, out, residual, w, rows, cols, x, nullptr, nullptr, n_batch, chain,
+                     (hipStream_t)stream);
+}
+
+int kq4_matmul_q_dev(float *out, const int8_t *xq, const float *xd, const float *residual,
+                     const uint8_t *w, int rows, int cols, int n_batch, int chain, void *stream) {
+  if ((!xq || !xd) && n_batch) return fail(KQ4_EINVAL, "null xq/xd");
+  const float *res[1] = {residual};
+  return matmul_impl(1, &out, res, &w, &rows, cols, nullptr, xq, xd, n_batch, chain,
+                     (hipStream_t)stream);
+}
+
+int kq4_matmul_multi_q_dev(int n_mats, float *const *out, const float *const *residual,
+                           const uint8_t *const *w, const int *rows, int cols, const int8_t *xq,
+                           const float *xd, int n_batch, int chain, void *stream) {
+  if ((!xq || !xd) && n_batch) return fail(KQ4_EINVAL, "null xq/xd");
+  if (!out || !w || !rows) return fail(KQ4_EINVAL, "null array argument");
+  return matmul_impl(n_mats, out, residual, w, rows, cols, nullptr, xq, xd, n_batch, chain,
+                     (hipStream_t)stream);
+}
+
+int kq4_block_sums_dev(int32_t *s_lo, int32_t *s_hi, const int8_t *xq, const uint8_t *w, int rows,
+                       int cols, int n_batch, void *stream) {
+  if (!shape_ok(rows, cols) || n_batch < 0) return fail(KQ4_EINVAL, "block_sums shape");
+  KQ4_HIP((hipError_t)kq4_launch_block_sums(s_lo, s_hi, xq, w, rows, cols, n_batch,
+                                            (hipStream_t)stream));
+  return KQ4_OK;
+}
+
+int kq4_moe_route_dev(int *sel, float *pr, const float *logits, int T, int ne, int tk,
+                      void *stream) {
+  if (T < 0 || ne < 1 || tk < 1 || tk > 32 || tk > ne)
+    return fail(KQ4_EINVAL, "route: T=%d ne=%d tk=%d", T, ne, tk);
+  if (T == 0) return KQ4_OK;
+  KQ4_HIP((hipError_t)kq4_launch_moe_route(sel, pr, logits, T, ne, tk, (hipStream_t)stream));
+  return KQ4_OK;
+}
+
+int kq4_moe_ffn_dev(float *Y, const float *X, const int *sel, const float *pr, int T, int tk,
+                    const uint8_t *G, const uint8_t *U, const uint8_t *D, int ne, int d, int ef,
+                    void *stream) {
+  return moe_impl(Y, X, sel, pr, T, tk, G, U, D, ne, d, ef, nullptr, nullptr, nullptr, nullptr,
+                  (hipStream_t)stream);
+}
+
+int kq4_moe_ffn_stages_dev(float *Y, const float *X, const int *sel, const float *pr, int T,
+                           int tk, const uint8_t *G, const uint8_t *U, const uint8_t *D, int ne,
+                           int d, int ef, float *gate_out, float *up_out, float *av_out,
+                           const float *av_in, void *stream) {
+  if ((gate_out == nullptr) != (up_out == nullptr))
+    return fail(KQ4_EINVAL, "gate_out and up_out go together");
+  return moe_impl(Y, X, sel, pr, T, tk, G, U, D, ne, d, ef, gate_out, up_out, av_out, av_in,
+                  (hipStream_t)stream);
+}
+
+// ---- host-pointer drop-in API ----------------------------------------------------------------
+
+int kq4_weights_upload(uint64_t wkey, const uint8_t *w4x4, int rows, int cols) {
+  if (!wkey || !w4x4 || !shape_ok(rows, cols)) {
+    fail(KQ4_EINVAL, "weights_upload: key=%llu rows=%d cols=%d", (unsigned long long)wkey, rows,
+         cols);
+    return 0;
+  }
+  DevState *ds = nullptr;
+  if (cur_dev(&ds)) return 0;
+  const uint8_t *dev = nullptr;
+  Buf unused;
+  {
+    std::lock_guard<std::mutex> lk(g_mu);
+    auto it = ds->wcache.find(wkey);
+    if (it != ds->wcache.end()) {
+      hipFree(it->second.p);
+      ds->wcache.erase(it);
+    }
+  }
+  return dev_weights(ds, wkey, w4x4, wbytes(rows, cols), unused, &dev) == KQ4_OK ? 1 : 0;
+}
+
+int kq4_weights_evict(uint64_t wkey) {
+  DevState *ds = nullptr;
+  if (cur_dev(&ds)) return 0;
+  std::lock_guard<std::mutex> lk(g_mu);
+  auto it = ds->wcache.find(wkey);
+  if (it == ds->wcache.end()) return 0;
+  hipDeviceSynchronize();
+  hipFree(it->second.p);
+  ds->wcache.erase(it);
+  return 1;
+}
+
+int kq4_matmul_multi(int n_mats, float *const *out, const float *const *residual,
+                     const uint8_t *const *w4x4, const int *rows, int cols, const float *x,
+                     int n_batch, int chain, const uint64_t *wkeys) {
+  if (n_mats < 1 || n_mats > KQ4_MAX_MATS || !out || !w4x4 || !rows || !x || n_batch < 1) {
+    fail(KQ4_EINVAL, "matmul: n_mats=%d n_batch=%d", n_mats, n_batch);
+    return 0;
+  }
+  for (int i = 0; i < n_mats; ++i)
+    if (!out[i] || !w4x4[i] || !shape_ok(rows[i], cols)) {
+      fail(KQ4_EINVAL, "matmul: rows=%d cols=%d", rows[i], cols);
+      return 0;
+    }
+  DevState *ds = nullptr;
+  if (cur_dev(&ds)) return 0;
+  // one staging buffer for x, all outputs and all residuals
+  size_t ob[KQ4_MAX_MATS], total_o = 0;
+  for (int i = 0; i < n_mats; ++i) {
+    ob[i] = (size_t)n_batch * rows[i] * sizeof(float);
+    total_o += al256(ob[i]);
+  }
+  const size_t xb = (size_t)n_batch * cols * sizeof(float);
+  Buf tw[KQ4_MAX_MATS];
+  const uint8_t *dw[KQ4_MAX_MATS];
+  int rc = KQ4_OK;
+  for (int i = 0; i < n_mats && !rc; ++i)
+    rc = dev_weights(ds, wkeys ? wkeys[i] : 0, w4x4[i], wbytes(rows[i], cols),
+                     i == 0 ? ds->hw : tw[i], &dw[i]);
+  int ok = 0;
+  if (!rc && !ensure(ds->hx, xb) && !ensure(ds->hout, total_o) && !ensure(ds->hres, total_o)) {
+    float *dout[KQ4_MAX_MATS];
+    const float *dres[KQ4_MAX_MATS];
+    char *po = static_cast<char *>(ds->hout.p), *pr = static_cast<char *>(ds->hres.p);
+    bool good = hipMemcpy(ds->hx.p, x, xb, hipMemcpyHostToDevice) == hipSuccess;
+    for (int i = 0; i < n_mats && good; ++i) {
+      dout[i] = reinterpret_cast<float *>(po);
+      dres[i] = nullptr;
+      if (residual && residual[i]) {
+        dres[i] = reinterpret_cast<const float *>(pr);
+        good = hipMemcpy(pr, residual[i], ob[i], hipMemcpyHostToDevice) == hipSuccess;
+      }
+      po += al256(ob[i]);
+      pr += al256(ob[i]);
+    }
+    if (good &&
+        matmul_impl(n_mats, dout, dres, dw, rows, cols, static_cast<const float *>(ds->hx.p),
+                    nullptr, nullptr, n_batch, chain, nullptr) == KQ4_OK) {
+      ok = 1;
+      for (int i = 0; i < n_mats && ok; ++i)
+        if (hipMemcpy(out[i], dout[i], ob[i], hipMemcpyDeviceToHost) != hipSuccess) {
+          fail(KQ4_EHIP, "matmul readback failed");
+          ok = 0;
+        }
+    }
+  }
+  bool any_tmp = false;
+  for (int i = 1; i < n_mats; ++i) any_tmp = any_tmp || tw[i].p;
+  if (any_tmp) hipDeviceSynchronize();
+  for (int i = 1; i < n_mats; ++i)
+    if (tw[i].p) hipFree(tw[i].p);
+  return ok;
+}
+
+int kq4_matmul(float *out, const float *x, const float *residual, const uint8_t *w4x4, int rows,
+               int cols, int n_batch, int chain, uint64_t wkey) {
+  const float *res[1] = {residual};
+  return kq4_matmul_multi(1, &out, res, &w4x4, &rows, cols, x, n_batch, chain, &wkey);
+}
+
+int kq4_moe_ffn(float *Y, const float *X, const int *sel, const float *pr, int T, int tk,
+                const uint8_t *G, const uint8_t *U, const uint8_t *D, int ne, int d, int ef,
+                uint64_t wkey) {
+  if (!Y || !X || !sel || !pr || !G || !U || !D || T < 1) {
+    fail(KQ4_EINVAL, "moe_ffn: null argument or T<1");
+    return 0;
+  }
+  DevState *ds = nullptr;
+  if (cur_dev(&ds)) return 0;
+  const size_t gb = wbytes(ne * ef, d), db = wbytes(d, ne * ef);
+  const uint8_t *dG, *dU, *dD;
+  Buf tg, tu, td;
+  int rc = dev_weights(ds, wkey, G, gb, tg, &dG);
+  if (!rc) rc = dev_weights(ds, wkey ? wkey + 1 : 0, U, gb, tu, &dU);
+  if (!rc) rc = dev_weights(ds, wkey ? wkey + 2 : 0, D, db, td, &dD);
+  int ok = 0;
+  const size_t xb = (size_t)T * d * sizeof(float), sb = (size_t)T * tk * sizeof(int);
+  if (!rc && !ensure(ds->hx, xb) && !ensure(ds->hout, xb) && !ensure(ds->hsel, sb) &&
+      !ensure(ds->hpr, sb) &&
+      hipMemcpy(ds->hx.p, X, xb, hipMemcpyHostToDevice) == hipSuccess &&
+      hipMemcpy(ds->hsel.p, sel, sb, hipMemcpyHostToDevice) == hipSuccess &&
+      hipMemcpy(ds->hpr.p, pr, sb, hipMemcpyHostToDevice) == hipSuccess &&
+      kq4_moe_ffn_dev(static_cast<float *>(ds->hout.p), static_cast<const float *>(ds->hx.p),
+                      static_cast<const int *>(ds->hsel.p), static_cast<const float *>(ds->hpr.p),
+                      T, tk, dG, dU, dD, ne, d, ef, nullptr) == KQ4_OK &&
+      hipMemcpy(Y, ds->hout.p, xb, hipMemcpyDeviceToHost) == hipSuccess)
+    ok = 1;
+  if (tg.p || tu.p || td.p) hipDeviceSynchronize();
+  if (tg.p) hipFree(tg.p);
+  if (tu.p) hipFree(tu.p);
+  if (td.p) hipFree(td.p);
+  return ok;
+}
+
+}  // extern "C"

@@ -1,0 +1,222 @@
+// kq4_gemm.hip - prefill GEMM over VQF 4x4 q4 tiles x int8 activations with int8 MFMA (gfx950).
+//
+// One v_mfma_i32_32x32x32_i8 covers exactly one 32-element quantization block, so its int32
+// result is the block sum 16*S for a 32-token x 32-row tile (weights enter the matrix core as
+// 16*(n-8) bytes, see kq4_lo16/kq4_hi16). Each lane owns the same (token, row) outputs for the
+// whole K loop, so the per-block fp32 epilogue replays the reference chain exactly:
+//   ASM    acc = fma(S, fl(wd * f16r(xd)), acc)  (llama_gemm_q4_0_4x4_asm.c:151-161, the
+//          reference's n_batch&~3 main segment, vllm_safetensors.c:4604-4609)
+//   GEMV32 the same with the f32 xd (q4x4_dot1_group16_gemv :4229-4251)
+//   CTILE  lo/hi accumulators fed by two half-K MFMAs, out = fl(lo + hi) (:4180-4216)
+// and out = fl(residual + acc) when fused. The epilogue (convert, scale, fma per output per
+// block) runs on the VALU; it, not the matrix core, bounds this kernel.
+//
+// Tiling: workgroup = 4 waves = 128 tokens x 128 rows, each wave 64 x 64 (2 x 2 MFMA tiles).
+// Per stage of KB = 4 blocks the workgroup stages into LDS (rows padded to 48 B so the 16-byte
+// fragment reads are bank-conflict free):
+//   A  block-major activations [block][token][32] (contiguous 4 KB per block)
+//   B  weights unpacked from the 72-byte tiles to 16*(n-8) int8 [block][row][32]
+//   sW per-row scale wd/16, sX per-token activation scale
+// The workgroup -> tile map keeps the tiles of one XCD (workgroup id mod 8) in one contiguous
+// range, token tiles fastest, so the weight tiles a workgroup streams are shared in its L2.
+#include "kq4_common.h"
+#include "kq4_internal.h"
+#include "../../include/kq4.h"
+
+typedef int kq4_v4i __attribute__((ext_vector_type(4)));
+typedef int kq4_v16i __attribute__((ext_vector_type(16)));
+
+#define KQ4_GEMM_BM 128
+#define KQ4_GEMM_BN 128
+#define KQ4_GEMM_KB 4
+#define KQ4_LDS_ROW 48
+
+// MFMA 32x32 output element held by (lane, register v): column = lane % 32 (weight row),
+// row = 8*(v/4) + 4*(lane/32) + v%4 (token).
+KQ4_DEV int kq4_mfma_tok(int v, int half) { return 8 * (v >> 2) + 4 * half + (v & 3); }
+
+template <int CHAIN>
+__global__ __launch_bounds__(256, 2) void kq4_gemm_kernel(
+    float *__restrict__ out, const float *__restrict__ res, const uint8_t *__restrict__ w,
+    const KQ4GemmAct act, int rows, int n_tok, int nb, int mtiles, int ntiles) {
+  __shared__ __align__(16) int8_t sA[KQ4_GEMM_KB][KQ4_GEMM_BM * KQ4_LDS_ROW];
+  __shared__ __align__(16) int8_t sB[KQ4_GEMM_KB][KQ4_GEMM_BN * KQ4_LDS_ROW];
+  __shared__ __align__(16) float sW[KQ4_GEMM_KB][KQ4_GEMM_BN];
+  __shared__ __align__(16) float sX[KQ4_GEMM_KB][KQ4_GEMM_BM];
+
+  // XCD-aware tile order: workgroup ids go round-robin over the 8 XCDs; give XCD x the
+  // contiguous tile range [start(x), start(x) + count(x)) (a bijection for any tile count).
+  const int ntile = mtiles * ntiles;
+  const int wg = blockIdx.x;
+  const int xcd = wg & 7, q8 = ntile >> 3, r8 = ntile & 7;
+  const int tile = xcd * q8 + (xcd < r8 ? xcd : r8) + (wg >> 3);
+  const int mt = tile % mtiles;
+  const int nt = tile / mtiles;
+  const int m0 = mt * KQ4_GEMM_BM;
+  const int n0 = nt * KQ4_GEMM_BN;
+
+  const int t = threadIdx.x;
+  const int lane = t & 63;
+  const int wave = t >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int l32 = lane & 31, half = lane >> 5;
+  const int groups = rows >> 2;
+
+  float acc[2][2][16];
+  float acc_hi[2][2][16];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int jn = 0; jn < 2; ++jn)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        acc[i][jn][v] = 0.0f;
+        acc_hi[i][jn][v] = 0.0f;
+      }
+
+  for (int b0 = 0; b0 < nb; b0 += KQ4_GEMM_KB) {
+    __syncthreads();
+    // ---- stage A: KB blocks x 128 tokens x 32 B, 16 B per thread per block
+#pragma unroll
+    for (int u = 0; u < KQ4_GEMM_KB; ++u) {
+      const int tok = t >> 1, hh = t & 1;
+      const int b = b0 + u;
+      uint4 v = make_uint4(0, 0, 0, 0);
+      if (b < nb && m0 + tok < n_tok)
+        v = *reinterpret_cast<const uint4 *>(act.xq + (long)(m0 + tok) * act.q_ts +
+                                             (long)b * act.q_bs + hh * 16);
+      *reinterpret_cast<uint4 *>(&sA[u][tok * KQ4_LDS_ROW + hh * 16]) = v;
+    }
+    // ---- stage B: 32 groups x KB tiles x 16 nibble dwords, unpacked to 16*(n-8)
+#pragma unroll
+    for (int u = 0; u < 2 * KQ4_GEMM_KB; ++u) {
+      const int c = t + 256 * u;                 // (group, tile, dword) with dword fastest
+      const int kd = c & 15;
+      const int bl = (c >> 4) % KQ4_GEMM_KB;
+      const int gl = c / (16 * KQ4_GEMM_KB);
+      const int gg = (n0 >> 2) + gl;
+      const int b = b0 + bl;
+      uint32_t wv = 0;                           // padding rows: weight 0
+      if (b < nb && gg < groups)
+        wv = *reinterpret_cast<const uint32_t *>(w + ((size_t)gg * nb + b) * 72 + 8 + 4 * kd);
+      const int r = kd & 3, k = kd >> 2;
+      int8_t *rowp = &sB[bl][(4 * gl + r) * KQ4_LDS_ROW];
+      *reinterpret_cast<uint32_t *>(rowp + 4 * k) = kq4_lo16(wv);
+      *reinterpret_cast<uint32_t *>(rowp + 16 + 4 * k) = kq4_hi16(wv);
+    }
+    // ---- row scales (2 per dword) and token scales
+    if (t < 32 * KQ4_GEMM_KB * 2) {
+      const int c = t;                           // (group, tile, word) : 32 x KB x 2
+      const int wd_i = c & 1;
+      const int bl = (c >> 1) % KQ4_GEMM_KB;
+      const int gl = c / (2 * KQ4_GEMM_KB);
+      const int gg = (n0 >> 2) + gl;
+      const int b = b0 + bl;
+      uint32_t sv = 0;
+      if (b < nb && gg < groups)
+        sv = *reinterpret_cast<const uint32_t *>(w + ((size_t)gg * nb + b) * 72 + 4 * wd_i);
+      sW[bl][4 * gl + 2 * wd_i] = kq4_h2f(sv) * 0.0625f;
+      sW[bl][4 * gl + 2 * wd_i + 1] = kq4_h2f(sv >> 16) * 0.0625f;
+    }
+#pragma unroll
+    for (int u = 0; u < KQ4_GEMM_KB * KQ4_GEMM_BM / 256; ++u) {
+      const int c = t + 256 * u;
+      const int bl = c / KQ4_GEMM_BM, tok = c % KQ4_GEMM_BM;
+      const int b = b0 + bl;
+      float xv = 0.0f;
+      if (b < nb && m0 + tok < n_tok) xv = act.xd[(long)(m0 + tok) * act.d_ts + (long)b * act.d_bs];
+      // ASM chain: the reference's asm GEMM multiplies by the f16-rounded activation scale
+      sX[bl][tok] = (CHAIN == KQ4_CHAIN_ASM) ? kq4_f16_round(xv) : xv;
+    }
+    __syncthreads();
+
+    // ---- compute: per block, 2 x 2 MFMA tiles per wave + exact per-block epilogue
+#pragma unroll
+    for (int bl = 0; bl < KQ4_GEMM_KB; ++bl) {
+      if (b0 + bl >= nb) break;
+      kq4_v4i af[2], bf[2];
+      float wdv[2];
+      float xsv[2][16];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        af[i] = *reinterpret_cast<const kq4_v4i *>(
+            &sA[bl][(64 * wm + 32 * i + l32) * KQ4_LDS_ROW + 16 * half]);
+        bf[i] = *reinterpret_cast<const kq4_v4i *>(
+            &sB[bl][(64 * wn + 32 * i + l32) * KQ4_LDS_ROW + 16 * half]);
+        wdv[i] = sW[bl][64 * wn + 32 * i + l32];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float4 x4 =
+              *reinterpret_cast<const float4 *>(&sX[bl][64 * wm + 32 * i + 8 * q + 4 * half]);
+          xsv[i][4 * q + 0] = x4.x;
+          xsv[i][4 * q + 1] = x4.y;
+          xsv[i][4 * q + 2] = x4.z;
+          xsv[i][4 * q + 3] = x4.w;
+        }
+      }
+      const kq4_v16i zero = {0};
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int jn = 0; jn < 2; ++jn) {
+          if (CHAIN == KQ4_CHAIN_CTILE) {
+            // lane half 0 carries elements 0..15 (low nibbles), half 1 elements 16..31
+            const kq4_v4i z = {0, 0, 0, 0};
+            const kq4_v4i blo = half == 0 ? bf[jn] : z;
+            const kq4_v4i bhi = half == 1 ? bf[jn] : z;
+            const kq4_v16i clo = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], blo, zero, 0, 0, 0);
+            const kq4_v16i chi = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bhi, zero, 0, 0, 0);
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+              const float s = wdv[jn] * xsv[i][v];
+              acc[i][jn][v] = fmaf((float)clo[v], s, acc[i][jn][v]);
+              acc_hi[i][jn][v] = fmaf((float)chi[v], s, acc_hi[i][jn][v]);
+            }
+          } else {
+            const kq4_v16i c = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[jn], zero, 0, 0, 0);
+#pragma unroll
+            for (int v = 0; v < 16; ++v)
+              acc[i][jn][v] = fmaf((float)c[v], wdv[jn] * xsv[i][v], acc[i][jn][v]);
+          }
+        }
+    }
+  }
+
+  // ---- epilogue: out = [res +] acc (CTILE: fl(lo + hi) first)
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int jn = 0; jn < 2; ++jn) {
+      const int row = n0 + 64 * wn + 32 * jn + l32;
+      if (row >= rows) continue;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int tok = m0 + 64 * wm + 32 * i + kq4_mfma_tok(v, half);
+        if (tok >= n_tok) continue;
+        float r = acc[i][jn][v];
+        if (CHAIN == KQ4_CHAIN_CTILE) r = acc[i][jn][v] + acc_hi[i][jn][v];
+        const size_t o = (size_t)tok * rows + row;
+        out[o] = res ? res[o] + r : r;
+      }
+    }
+}
+
+int kq4_launch_gemm(float *out, const float *res, const uint8_t *w, const KQ4GemmAct &act,
+                    int rows, int cols, int n_tok, int chain, hipStream_t s) {
+  const int nb = cols / 32;
+  const int mtiles = (n_tok + KQ4_GEMM_BM - 1) / KQ4_GEMM_BM;
+  const int ntiles = (rows + KQ4_GEMM_BN - 1) / KQ4_GEMM_BN;
+  const int grid = mtiles * ntiles;
+  if (grid <= 0) return 0;
+#define KQ4_GEMM_LAUNCH(C)                                                                        \
+  hipLaunchKernelGGL((kq4_gemm_kernel<C>), dim3(grid), dim3(256), 0, s, out, res, w, act, rows,   \
+                     n_tok, nb, mtiles, ntiles)
+  if (chain == KQ4_CHAIN_CTILE)
+    KQ4_GEMM_LAUNCH(KQ4_CHAIN_CTILE);
+  else if (chain == KQ4_CHAIN_GEMV32)
+    KQ4_GEMM_LAUNCH(KQ4_CHAIN_GEMV32);
+  else
+    KQ4_GEMM_LAUNCH(KQ4_CHAIN_ASM);
+#undef KQ4_GEMM_LAUNCH
+  return (int)hipGetLastError();
+}

@@ -1,0 +1,75 @@
+// kq4_internal.h - launch interfaces shared by the kernel files and the C-ABI layer.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define KQ4_GEMV_MAX_M 8
+#define KQ4_MAXMAT 4
+
+// One weight matrix of a (possibly fused) GEMV launch. All matrices share the activation.
+struct KQ4GemvMat {
+  const uint8_t *w;     // 4x4 tiles [rows/4][nb][72]
+  float *out;           // [M][rows]
+  const float *res;     // [M][rows] or nullptr
+  float *part;          // split-K partials [slabs][ks][M][16]
+  unsigned *cnt;        // split-K arrival counters [slabs] (zero between launches)
+  int rows;
+  int ks;               // K chunks (workgroups) per 16-row slab
+  int wg_begin;         // first workgroup index of this matrix in the launch
+};
+
+struct KQ4GemvArgs {
+  KQ4GemvMat mat[KQ4_MAXMAT];
+  int nmat;
+  const int8_t *xq;     // [M][cols]
+  const float *xd;      // [M][nb] activation scales
+  int asm_tokens;       // tokens [0, asm_tokens) multiply by f32(f16_rne(xd)) (ASM chain)
+  int cols;
+  int nb;
+  int blocks_per_wg;    // 32 * pairs-per-lane
+};
+
+int kq4_launch_quantize(const float *x, int8_t *xq, float *xd, float *xde, int n_batch, int cols,
+                        int asm_tokens, hipStream_t stream, int block_major = 0);
+
+// n_batch in [1, KQ4_GEMV_MAX_M]; ppl = tile pairs per lane (1 or 2); total_wg from the
+// matrices' wg_begin/ks.
+int kq4_launch_gemv(const KQ4GemvArgs &args, int n_batch, int ppl, int total_wg,
+                    hipStream_t stream);
+
+int kq4_launch_block_sums(int32_t *s_lo, int32_t *s_hi, const int8_t *xq, const uint8_t *w,
+                          int rows, int cols, int n_batch, hipStream_t stream);
+
+// Prefill GEMM (int8 MFMA) with the exact reference chain `chain` (ASM, GEMV32 or CTILE) for
+// tokens [0, n_tok). Activation (token t, block b) is at xq + t*q_ts + b*q_bs (bytes) and its
+// scale at xd + t*d_ts + b*d_bs, so token-major and block-major layouts both work.
+struct KQ4GemmAct {
+  const int8_t *xq;
+  long q_ts, q_bs;
+  const float *xd;
+  long d_ts, d_bs;
+};
+int kq4_launch_gemm(float *out, const float *res, const uint8_t *w, const KQ4GemmAct &act,
+                    int rows, int cols, int n_tok, int chain, hipStream_t stream);
+
+// MoE
+int kq4_launch_moe_route(int *sel, float *pr, const float *logits, int T, int ne, int tk,
+                         hipStream_t stream);
+struct KQ4MoeWs {
+  int *ex_off;   // [ne+1]
+  int *ex_pair;  // [T*tk] (t*tk+j) grouped by expert
+  int8_t *xq;    // [T][d]
+  float *xd;     // [T][d/32]
+  float *av;     // [T*tk][ef]
+  int8_t *avq;   // [T*tk][ef]
+  float *avd;    // [T*tk][ef/32]
+  float *P;      // [T*tk][d]
+};
+int kq4_launch_moe_dbg(float *Y, const float *X, const int *sel, const float *pr, int T, int tk,
+                       const uint8_t *G, const uint8_t *U, const uint8_t *D, int ne, int d,
+                       int ef, const KQ4MoeWs &ws, float *g_out, float *u_out,
+                       const float *av_in, hipStream_t s);
+int kq4_launch_moe(float *Y, const float *X, const int *sel, const float *pr, int T, int tk,
+                   const uint8_t *G, const uint8_t *U, const uint8_t *D, int ne, int d, int ef,
+                   const KQ4MoeWs &ws, hipStream_t stream);

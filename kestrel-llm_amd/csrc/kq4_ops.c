@@ -1,0 +1,141 @@
+/* kq4_ops.c - C11 host side: kestrel-llm's quantized-matmul op family on top of libkq4.
+ * See include/kq4_ops.h for the contract; each wrapper cites the reference function it mirrors. */
+#include "kq4_ops.h"
+
+#include <math.h>
+#include <stdlib.h>
+
+#include "kq4.h"
+
+static uint64_t key_of(const void *p) { return (uint64_t)(uintptr_t)p; }
+
+int kq4_dyn_matvec_q4_q8(float *out, const uint8_t *q4_w, const float *x, int rows, int cols) {
+    return kq4_matmul(out, x, NULL, q4_w, rows, cols, 1, KQ4_CHAIN_GEMV32, key_of(q4_w));
+}
+
+int kq4_dyn_matvec_q4_q8_fused_gate_up(float *gate_out, float *up_out, const uint8_t *q4_gate,
+                                       const uint8_t *q4_up, const float *x, int rows, int cols) {
+    float *out[2] = {gate_out, up_out};
+    const uint8_t *w[2] = {q4_gate, q4_up};
+    const int r[2] = {rows, rows};
+    const uint64_t k[2] = {key_of(q4_gate), key_of(q4_up)};
+    return kq4_matmul_multi(2, out, NULL, w, r, cols, x, 1, KQ4_CHAIN_GEMV32, k);
+}
+
+int kq4_dyn_matvec_q4_q8_fused_qkv(float *q_out, float *k_out, float *v_out,
+                                   const uint8_t *q4_q, const uint8_t *q4_k, const uint8_t *q4_v,
+                                   const float *x, int q_rows, int kv_rows, int cols) {
+    float *out[3] = {q_out, k_out, v_out};
+    const uint8_t *w[3] = {q4_q, q4_k, q4_v};
+    const int r[3] = {q_rows, kv_rows, kv_rows};
+    const uint64_t k[3] = {key_of(q4_q), key_of(q4_k), key_of(q4_v)};
+    return kq4_matmul_multi(3, out, NULL, w, r, cols, x, 1, KQ4_CHAIN_GEMV32, k);
+}
+
+int kq4_dyn_matvec_q4_q8_fused_o_residual(float *x, const float *residual, const uint8_t *q4_o,
+                                          const float *attn_in, int rows, int cols) {
+    return kq4_matmul(x, attn_in, residual, q4_o, rows, cols, 1, KQ4_CHAIN_GEMV32, key_of(q4_o));
+}
+
+int kq4_dyn_matvec_q4_q8_fused_down_residual(float *x, const float *residual,
+                                             const uint8_t *q4_down, const float *activated,
+                                             int hidden_dim, int ffn_dim) {
+    return kq4_matmul(x, activated, residual, q4_down, hidden_dim, ffn_dim, 1, KQ4_CHAIN_GEMV32,
+                      key_of(q4_down));
+}
+
+int kq4_dyn_matvec_q4_q8_fused_qkv_batched(float *q_out, float *k_out, float *v_out,
+                                           const uint8_t *q4_q, const uint8_t *q4_k,
+                                           const uint8_t *q4_v, const float *x_batch, int q_rows,
+                                           int kv_rows, int cols, int n_batch,
+                                           const uint8_t *x8_q, const uint8_t *x8_k,
+                                           const uint8_t *x8_v) {
+    (void)x8_q; (void)x8_k; (void)x8_v;
+    float *out[3] = {q_out, k_out, v_out};
+    const uint8_t *w[3] = {q4_q, q4_k, q4_v};
+    const int r[3] = {q_rows, kv_rows, kv_rows};
+    const uint64_t k[3] = {key_of(q4_q), key_of(q4_k), key_of(q4_v)};
+    return kq4_matmul_multi(3, out, NULL, w, r, cols, x_batch, n_batch, KQ4_CHAIN_AUTO, k);
+}
+
+int kq4_dyn_matvec_q4_q8_fused_o_residual_batched(float *x_batch, const float *residual_batch,
+                                                  const uint8_t *q4_o, const float *attn_batch,
+                                                  int rows, int cols, int n_batch,
+                                                  const uint8_t *x8_o) {
+    (void)x8_o;
+    return kq4_matmul(x_batch, attn_batch, residual_batch, q4_o, rows, cols, n_batch,
+                      KQ4_CHAIN_AUTO, key_of(q4_o));
+}
+
+int kq4_dyn_matvec_q4_q8_fused_gate_up_batched(float *gate_out, float *up_out,
+                                               const uint8_t *q4_gate, const uint8_t *q4_up,
+                                               const float *x_batch, int rows, int cols,
+                                               int n_batch, const uint8_t *x8_gate,
+                                               const uint8_t *x8_up) {
+    (void)x8_gate; (void)x8_up;
+    float *out[2] = {gate_out, up_out};
+    const uint8_t *w[2] = {q4_gate, q4_up};
+    const int r[2] = {rows, rows};
+    const uint64_t k[2] = {key_of(q4_gate), key_of(q4_up)};
+    return kq4_matmul_multi(2, out, NULL, w, r, cols, x_batch, n_batch, KQ4_CHAIN_AUTO, k);
+}
+
+int kq4_dyn_matvec_q4_q8_fused_down_residual_batched(float *x_batch, const float *residual_batch,
+                                                     const uint8_t *q4_down,
+                                                     const float *activated_batch, int hidden_dim,
+                                                     int ffn_dim, int n_batch,
+                                                     const uint8_t *x8_down) {
+    (void)x8_down;
+    return kq4_matmul(x_batch, activated_batch, residual_batch, q4_down, hidden_dim, ffn_dim,
+                      n_batch, KQ4_CHAIN_AUTO, key_of(q4_down));
+}
+
+/* Router logits (serial fp32 dot, i ascending) and deterministic top-k + softmax over the k
+ * selected, as st_moe_ffn_sparse_q4 computes them on the host (vllm_safetensors.c:12959-12985;
+ * batched router :14931-14989 computes the same per-token values). */
+static int route_token(const kq4_moe_layer *w, const float *x, int *sel, float *pr) {
+    const int ne = w->n_experts, tk = w->top_k, d = w->dim;
+    float sv[64];
+    if (tk < 1 || tk > 64) return 0;
+    for (int k = 0; k < tk; k++) { sel[k] = -1; sv[k] = -INFINITY; }
+    for (int e = 0; e < ne; e++) {
+        const float *rw = w->router + (size_t)e * d;
+        float s = 0.0f;
+        for (int i = 0; i < d; i++) s += rw[i] * x[i];
+        for (int k = 0; k < tk; k++) {
+            if (s > sv[k] || (s == sv[k] && (sel[k] < 0 || e < sel[k]))) {
+                for (int j = tk - 1; j > k; j--) { sel[j] = sel[j - 1]; sv[j] = sv[j - 1]; }
+                sel[k] = e;
+                sv[k] = s;
+                break;
+            }
+        }
+    }
+    float mx = -INFINITY;
+    for (int k = 0; k < tk; k++) if (sv[k] > mx) mx = sv[k];
+    float sum = 0.0f;
+    for (int k = 0; k < tk; k++) { pr[k] = expf(sv[k] - mx); sum += pr[k]; }
+    const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
+    for (int k = 0; k < tk; k++) pr[k] *= inv;
+    return 1;
+}
+
+int kq4_st_moe_ffn_sparse_q4_batch(const kq4_moe_layer *w, int nb, const float *X, float *Y) {
+    if (!w || !X || !Y || nb < 1 || w->top_k < 1 || w->top_k > 32) return 0;
+    const int tk = w->top_k, d = w->dim;
+    int *sel = (int *)malloc((size_t)nb * tk * sizeof(int));
+    float *pr = (float *)malloc((size_t)nb * tk * sizeof(float));
+    int ok = sel && pr;
+    for (int t = 0; ok && t < nb; t++)
+        ok = route_token(w, X + (size_t)t * d, sel + (size_t)t * tk, pr + (size_t)t * tk);
+    if (ok)
+        ok = kq4_moe_ffn(Y, X, sel, pr, nb, tk, w->G, w->U, w->D, w->n_experts, d, w->ef,
+                         key_of(w->G));
+    free(sel);
+    free(pr);
+    return ok;
+}
+
+int kq4_st_moe_ffn_sparse_q4(const kq4_moe_layer *w, const float *x_ffn, float *y) {
+    return kq4_st_moe_ffn_sparse_q4_batch(w, 1, x_ffn, y);
+}

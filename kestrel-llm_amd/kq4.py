@@ -1,0 +1,234 @@
+"""Python binding of libkq4.so (include/kq4.h) over ctypes.
+
+Host side for tests and the benchmark: numpy arrays go through the host-pointer drop-in API
+(1 = done on the GPU / 0 = not done, as the reference's NPU hook), device tensors (torch on ROCm,
+used only as HBM allocations and streams) through the device-pointer API. There is no CPU path
+here: if the library is missing or a call fails, the call raises.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libkq4.so")
+
+CHAIN_AUTO, CHAIN_CTILE, CHAIN_GEMV32, CHAIN_ASM = 0, 1, 2, 3
+MAX_MATS = 4
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_U64 = ctypes.c_uint64
+
+# (name, restype, argtypes) for every entry point include/kq4.h declares
+SIGNATURES = [
+    ("kq4_init", _I, [_I]),
+    ("kq4_shutdown", None, []),
+    ("kq4_last_error", ctypes.c_char_p, []),
+    ("kq4_version", ctypes.c_char_p, []),
+    ("kq4_weights_upload", _I, [_U64, _P, _I, _I]),
+    ("kq4_weights_evict", _I, [_U64]),
+    ("kq4_matmul", _I, [_P, _P, _P, _P, _I, _I, _I, _I, _U64]),
+    ("kq4_matmul_multi", _I, [_I, _P, _P, _P, _P, _I, _P, _I, _I, _P]),
+    ("kq4_moe_ffn", _I, [_P, _P, _P, _P, _I, _I, _P, _P, _P, _I, _I, _I, _U64]),
+    ("kq4_quantize_dev", _I, [_P, _P, _P, _P, _I, _I, _I, _P]),
+    ("kq4_matmul_dev", _I, [_P, _P, _P, _P, _I, _I, _I, _I, _P]),
+    ("kq4_matmul_multi_dev", _I, [_I, _P, _P, _P, _P, _I, _P, _I, _I, _P]),
+    ("kq4_matmul_q_dev", _I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _P]),
+    ("kq4_matmul_multi_q_dev", _I, [_I, _P, _P, _P, _P, _I, _P, _P, _I, _I, _P]),
+    ("kq4_block_sums_dev", _I, [_P, _P, _P, _P, _I, _I, _I, _P]),
+    ("kq4_moe_route_dev", _I, [_P, _P, _P, _I, _I, _I, _P]),
+    ("kq4_moe_ffn_dev", _I, [_P, _P, _P, _P, _I, _I, _P, _P, _P, _I, _I, _I, _P]),
+    ("kq4_moe_ffn_stages_dev", _I,
+     [_P, _P, _P, _P, _I, _I, _P, _P, _P, _I, _I, _I, _P, _P, _P, _P, _P]),
+    # C11 op wrappers (include/kq4_ops.h)
+    ("kq4_dyn_matvec_q4_q8", _I, [_P, _P, _P, _I, _I]),
+    ("kq4_dyn_matvec_q4_q8_fused_gate_up", _I, [_P, _P, _P, _P, _P, _I, _I]),
+    ("kq4_dyn_matvec_q4_q8_fused_qkv", _I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I]),
+    ("kq4_dyn_matvec_q4_q8_fused_o_residual", _I, [_P, _P, _P, _P, _I, _I]),
+    ("kq4_dyn_matvec_q4_q8_fused_down_residual", _I, [_P, _P, _P, _P, _I, _I]),
+    ("kq4_dyn_matvec_q4_q8_fused_qkv_batched", _I,
+     [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _P]),
+    ("kq4_dyn_matvec_q4_q8_fused_o_residual_batched", _I, [_P, _P, _P, _P, _I, _I, _I, _P]),
+    ("kq4_dyn_matvec_q4_q8_fused_gate_up_batched", _I,
+     [_P, _P, _P, _P, _P, _I, _I, _I, _P, _P]),
+    ("kq4_dyn_matvec_q4_q8_fused_down_residual_batched", _I, [_P, _P, _P, _P, _I, _I, _I, _P]),
+    ("kq4_st_moe_ffn_sparse_q4", _I, [_P, _P, _P]),
+    ("kq4_st_moe_ffn_sparse_q4_batch", _I, [_P, _I, _P, _P]),
+]
+
+
+class KQ4Error(RuntimeError):
+    pass
+
+
+class MoeLayer(ctypes.Structure):
+    """kq4_moe_layer (include/kq4_ops.h)."""
+    _fields_ = [("router", _P), ("G", _P), ("U", _P), ("D", _P), ("n_experts", _I),
+                ("top_k", _I), ("dim", _I), ("ef", _I)]
+
+
+_lib = None
+
+
+def lib():
+    """Loads libkq4.so (built in-tree by `make -C kestrel-llm_amd`); raises if absent."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise KQ4Error(f"{LIB_PATH} is missing: build it with `make -C kestrel-llm_amd` "
+                           "(or __graft_entry__.build())")
+        handle = ctypes.CDLL(LIB_PATH)
+        for name, res, args in SIGNATURES:
+            fn = getattr(handle, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = handle
+    return _lib
+
+
+def last_error():
+    return lib().kq4_last_error().decode(errors="replace")
+
+
+def check(rc, what):
+    """Device API: 0 = ok, negative = error."""
+    if rc != 0:
+        raise KQ4Error(f"{what} failed ({rc}): {last_error()}")
+
+
+def check_done(rc, what):
+    """Host drop-in API: 1 = done on the GPU, 0 = not done."""
+    if rc != 1:
+        raise KQ4Error(f"{what} not executed: {last_error()}")
+
+
+def init(device=0):
+    check(lib().kq4_init(device), "kq4_init")
+
+
+def _np_ptr(a):
+    return a.ctypes.data if a is not None else None
+
+
+def _c(a, dtype):
+    return np.ascontiguousarray(a, dtype=dtype)
+
+
+def _ptr_array(ptrs):
+    return (ctypes.c_void_p * len(ptrs))(*ptrs)
+
+
+# ---- host-pointer API (numpy) ---------------------------------------------------------------
+
+def matmul(w, x, rows, cols, residual=None, chain=CHAIN_AUTO, wkey=0):
+    """out[n_batch][rows] = [residual +] W.x through kq4_matmul (host pointers)."""
+    x = _c(x, np.float32).reshape(-1, cols)
+    w = _c(w, np.uint8)
+    out = np.empty((x.shape[0], rows), np.float32)
+    res = None if residual is None else _c(residual, np.float32).reshape(x.shape[0], rows)
+    check_done(lib().kq4_matmul(_np_ptr(out), _np_ptr(x), _np_ptr(res), _np_ptr(w), rows, cols,
+                                x.shape[0], chain, wkey), "kq4_matmul")
+    return out
+
+
+def matmul_multi(ws, rows, x, cols, residuals=None, chain=CHAIN_AUTO, wkeys=None):
+    x = _c(x, np.float32).reshape(-1, cols)
+    n = x.shape[0]
+    ws = [_c(w, np.uint8) for w in ws]
+    outs = [np.empty((n, r), np.float32) for r in rows]
+    res = [None] * len(ws) if residuals is None else [
+        None if r is None else _c(r, np.float32) for r in residuals]
+    keys = None if wkeys is None else (ctypes.c_uint64 * len(ws))(*wkeys)
+    rc = lib().kq4_matmul_multi(len(ws), _ptr_array([o.ctypes.data for o in outs]),
+                                _ptr_array([_np_ptr(r) for r in res]),
+                                _ptr_array([w.ctypes.data for w in ws]),
+                                (ctypes.c_int * len(rows))(*rows), cols, _np_ptr(x), n, chain,
+                                keys)
+    check_done(rc, "kq4_matmul_multi")
+    return outs
+
+
+def moe_ffn(X, sel, pr, G, U, D, ne, d, ef, wkey=0):
+    X = _c(X, np.float32).reshape(-1, d)
+    T = X.shape[0]
+    sel = _c(sel, np.int32).reshape(T, -1)
+    pr = _c(pr, np.float32).reshape(T, -1)
+    Y = np.empty((T, d), np.float32)
+    check_done(lib().kq4_moe_ffn(_np_ptr(Y), _np_ptr(X), _np_ptr(sel), _np_ptr(pr), T,
+                                 sel.shape[1], _np_ptr(_c(G, np.uint8)), _np_ptr(_c(U, np.uint8)),
+                                 _np_ptr(_c(D, np.uint8)), ne, d, ef, wkey), "kq4_moe_ffn")
+    return Y
+
+
+# ---- device-pointer API (torch tensors as HBM buffers) ----------------------------------------
+
+def _tp(t):
+    return None if t is None else t.data_ptr()
+
+
+def _stream_ptr(stream):
+    return None if stream is None else stream.cuda_stream
+
+
+def quantize_dev(x, xq, xd, xde=None, chain=CHAIN_AUTO, stream=None):
+    n, cols = x.shape
+    check(lib().kq4_quantize_dev(_tp(xq), _tp(xd), _tp(xde), _tp(x), n, cols, chain,
+                                 _stream_ptr(stream)), "kq4_quantize_dev")
+
+
+def matmul_dev(out, x, w, rows, cols, residual=None, chain=CHAIN_AUTO, stream=None):
+    n = x.shape[0]
+    check(lib().kq4_matmul_dev(_tp(out), _tp(x), _tp(residual), _tp(w), rows, cols, n, chain,
+                               _stream_ptr(stream)), "kq4_matmul_dev")
+
+
+def matmul_multi_dev(outs, x, ws, rows, cols, residuals=None, chain=CHAIN_AUTO, stream=None):
+    n = x.shape[0]
+    res = [None] * len(ws) if residuals is None else residuals
+    check(lib().kq4_matmul_multi_dev(len(ws), _ptr_array([_tp(o) for o in outs]),
+                                     _ptr_array([_tp(r) for r in res]),
+                                     _ptr_array([_tp(w) for w in ws]),
+                                     (ctypes.c_int * len(rows))(*rows), cols, _tp(x), n, chain,
+                                     _stream_ptr(stream)), "kq4_matmul_multi_dev")
+
+
+def matmul_q_dev(out, xq, xd, w, rows, cols, n, residual=None, chain=CHAIN_AUTO, stream=None):
+    check(lib().kq4_matmul_q_dev(_tp(out), _tp(xq), _tp(xd), _tp(residual), _tp(w), rows, cols,
+                                 n, chain, _stream_ptr(stream)), "kq4_matmul_q_dev")
+
+
+def matmul_multi_q_dev(outs, xq, xd, ws, rows, cols, n, residuals=None, chain=CHAIN_AUTO,
+                       stream=None):
+    res = [None] * len(ws) if residuals is None else residuals
+    check(lib().kq4_matmul_multi_q_dev(len(ws), _ptr_array([_tp(o) for o in outs]),
+                                       _ptr_array([_tp(r) for r in res]),
+                                       _ptr_array([_tp(w) for w in ws]),
+                                       (ctypes.c_int * len(rows))(*rows), cols, _tp(xq), _tp(xd),
+                                       n, chain, _stream_ptr(stream)), "kq4_matmul_multi_q_dev")
+
+
+def block_sums_dev(s_lo, s_hi, xq, w, rows, cols, n, stream=None):
+    check(lib().kq4_block_sums_dev(_tp(s_lo), _tp(s_hi), _tp(xq), _tp(w), rows, cols, n,
+                                   _stream_ptr(stream)), "kq4_block_sums_dev")
+
+
+def moe_route_dev(sel, pr, logits, tk, stream=None):
+    T, ne = logits.shape
+    check(lib().kq4_moe_route_dev(_tp(sel), _tp(pr), _tp(logits), T, ne, tk,
+                                  _stream_ptr(stream)), "kq4_moe_route_dev")
+
+
+def moe_ffn_dev(Y, X, sel, pr, G, U, D, ne, d, ef, stream=None):
+    T, tk = sel.shape
+    check(lib().kq4_moe_ffn_dev(_tp(Y), _tp(X), _tp(sel), _tp(pr), T, tk, _tp(G), _tp(U),
+                                _tp(D), ne, d, ef, _stream_ptr(stream)), "kq4_moe_ffn_dev")
+
+
+def moe_ffn_stages_dev(Y, X, sel, pr, G, U, D, ne, d, ef, gate=None, up=None, av=None,
+                       av_in=None, stream=None):
+    T, tk = sel.shape
+    check(lib().kq4_moe_ffn_stages_dev(_tp(Y), _tp(X), _tp(sel), _tp(pr), T, tk, _tp(G), _tp(U),
+                                       _tp(D), ne, d, ef, _tp(gate), _tp(up), _tp(av),
+                                       _tp(av_in), _stream_ptr(stream)),
+          "kq4_moe_ffn_stages_dev")

@@ -1,0 +1,454 @@
+/* kq4_oracle.c - scalar C restatement of kestrel-llm's Q4_0 x int8 matmul (the parity oracle).
+ *
+ * TEST INFRASTRUCTURE ONLY (see kq4_oracle.h). Compiled with -O2 -ffp-contract=off and without
+ * fast-math so every fp32 step below is exactly one IEEE binary32 operation; fmaf() is a single
+ * fused multiply-add (the reference's vfmaq_f32 / fmla).
+ *
+ * The reference computes this path only in AArch64 NEON code (src/model/vllm_safetensors.c
+ * "#if ST_HAVE_NEON" sections), which cannot be built here; every step below restates that
+ * source text. Notation in comments: fl() = one binary32 rounding, S = integer block sum.
+ *
+ * The four fp32 chains (all start from 0, blocks b ascending):
+ *   V1 C-tile  (q4x4_dot1_group16 vllm_safetensors.c:4180-4216, worker :4516-4557):
+ *        s = fl(wd*xd); lo = fma(S_lo, s, lo); hi = fma(S_hi, s, hi); out = fl(lo+hi)
+ *   V2 M4f     (q4x4_dot1_group16_gemv :4229-4251, worker :6107-6121):
+ *        acc = fma(S, fl(wd*xd), acc); out = acc
+ *   V3 asm     (llama_gemm_q4_0_4x4_asm.c:151-161 via repack_q8_0_4x4 :4086-4119):
+ *        as V2 with xd replaced by f32(f16_rne(xd))
+ *   V4 MoE int8 (q4x4_gup_actq_neon :11861-11903, moe_q4_down_group_actq_neon :11927-11968):
+ *        acc = fl(acc + fl(fl(sc*xd) * S))
+ *   residual (fused O / down): out = fl(resid + out)  (:4544-4549, :4317-4326, :6428-6431)
+ * Dispatch (q4x4_gemm_batched :4593-4631): n_batch <= 3 -> V1 for all tokens;
+ *   n_batch > 3 -> V3 on the first n_batch & ~3 tokens, V1 on the remaining 1..3.
+ */
+#include "kq4_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ---------------------------------------------------------------- f16 <-> f32 */
+
+/* Exact f16 -> f32 bit pattern, subnormals normalised (vllm_safetensors.c:3614-3631; the MoE
+ * decoder vq_f16 :10976-10998 computes the same value). Pinned exhaustively against numpy's
+ * float16 -> float32 conversion over all 65536 codes. */
+uint32_t kqo_f16_to_f32_bits(uint16_t h) {
+    uint32_t sign = (uint32_t)(h >> 15) & 1u;
+    uint32_t ex = (uint32_t)(h >> 10) & 0x1Fu;
+    uint32_t mant = (uint32_t)h & 0x3FFu;
+    if (ex == 0) {
+        if (mant == 0) return sign << 31;
+        int shift = 0;
+        while (mant < 0x400u) { mant <<= 1; shift++; }
+        return (sign << 31) | ((uint32_t)(113 - shift) << 23) | ((mant & 0x3FFu) << 13);
+    }
+    if (ex == 0x1F) return (sign << 31) | (0xFFu << 23) | (mant << 13);
+    return (sign << 31) | ((ex + 112u) << 23) | (mant << 13);
+}
+
+float kqo_f16_to_f32(uint16_t h) {
+    uint32_t b = kqo_f16_to_f32_bits(h);
+    float f;
+    memcpy(&f, &b, 4);
+    return f;
+}
+
+/* f32 -> f16, round-to-nearest-even incl. subnormals, overflow -> inf
+ * (vllm_safetensors.c:3639-3670). Pinned against numpy float32 -> float16 (IEEE RNE) over
+ * every f16 midpoint, its neighbours and random bit patterns. */
+uint16_t kqo_f32_to_f16_bits(float x) {
+    uint32_t u;
+    memcpy(&u, &x, 4);
+    uint32_t sign = (u >> 16) & 0x8000u;
+    uint32_t ef = (u >> 23) & 0xFFu;
+    uint32_t mant = u & 0x7FFFFFu;
+    if (ef == 0xFFu) return (uint16_t)(sign | 0x7C00u | (mant ? 0x200u : 0u));
+    int32_t e = (int32_t)ef - 127 + 15;
+    if (e >= 0x1F) return (uint16_t)(sign | 0x7C00u);
+    if (e <= 0) {
+        if (e < -10) return (uint16_t)sign;
+        mant |= 0x800000u;
+        uint32_t sh = (uint32_t)(14 - e);
+        uint32_t half = 1u << (sh - 1);
+        uint32_t rem = mant & ((1u << sh) - 1u);
+        mant >>= sh;
+        if (rem > half || (rem == half && (mant & 1u))) mant++;
+        return (uint16_t)(sign | mant);
+    }
+    uint32_t rem = mant & 0x1FFFu;
+    mant >>= 13;
+    if (rem > 0x1000u || (rem == 0x1000u && (mant & 1u))) {
+        if (++mant == 0x400u) {
+            mant = 0;
+            if (++e >= 0x1F) return (uint16_t)(sign | 0x7C00u);
+        }
+    }
+    return (uint16_t)(sign | ((uint32_t)e << 10) | mant);
+}
+
+/* ---------------------------------------------------------------- weight codec */
+
+/* Legacy Q4_0 encoder: d = (signed max)/-8, nib = clamp((int)(x*(1/d) + 8.5), 0, 15)
+ * (vqf_convert/src/quant_kernels.c:118-151). Element j -> low nibble of qs[j], element
+ * 16+j -> high nibble. Pinned against the reference encoder built in oracle/_ref. */
+void kqo_f32_to_q4_0(uint8_t *q4_out, const float *f32_in, int n_elements) {
+    int n_blocks = n_elements / 32;
+    for (int b = 0; b < n_blocks; b++) {
+        const float *xb = f32_in + (size_t)b * 32;
+        float amax = 0.0f, maxv = 0.0f;
+        for (int i = 0; i < 32; i++) {
+            float av = fabsf(xb[i]);
+            if (av > amax) { amax = av; maxv = xb[i]; }
+        }
+        float d = maxv / -8.0f;
+        if (d == 0.0f) d = 1.0f;
+        float id = 1.0f / d;
+        uint16_t h = kqo_f32_to_f16_bits(d);
+        memcpy(q4_out + (size_t)b * 18, &h, 2);
+        uint8_t *qs = q4_out + (size_t)b * 18 + 2;
+        for (int j = 0; j < 16; j++) {
+            volatile float x0 = xb[j] * id;
+            volatile float x1 = xb[16 + j] * id;
+            int i0 = (int)(x0 + 8.5f), i1 = (int)(x1 + 8.5f);
+            if (i0 > 15) i0 = 15;
+            if (i0 < 0) i0 = 0;
+            if (i1 > 15) i1 = 15;
+            if (i1 < 0) i1 = 0;
+            qs[j] = (uint8_t)(i0 | (i1 << 4));
+        }
+    }
+}
+
+/* Legacy (4 rows x 18 B per block) -> 4x4 tile (72 B): bytes [0,8) = 4 row scales (f16, row
+ * order); chunk c (c = 0..15) at 8 + 4c = legacy qs bytes [(c>>2)*4, +4) of row (c&3), each
+ * byte XOR 0x88 (vqf_convert/src/qk_repack.c:19-46). Pinned against the reference repack
+ * built in oracle/_ref and by the round trip with kqo_unpack_4x4_to_q4_0. */
+int kqo_repack_q4_0_4x4(const uint8_t *legacy, uint8_t *tiles, int rows, int cols) {
+    if (rows % 4 != 0 || cols % 32 != 0) return -1;
+    int nb = cols / 32;
+    size_t row_stride = (size_t)nb * 18;
+    for (int g = 0; g < rows / 4; g++) {
+        const uint8_t *src = legacy + (size_t)g * 4 * row_stride;
+        for (int b = 0; b < nb; b++) {
+            uint8_t *out = tiles + ((size_t)g * nb + b) * 72;
+            for (int r = 0; r < 4; r++) memcpy(out + 2 * r, src + r * row_stride + (size_t)b * 18, 2);
+            for (int c = 0; c < 16; c++)
+                for (int i = 0; i < 4; i++)
+                    out[8 + 4 * c + i] =
+                        (uint8_t)(src[(c & 3) * row_stride + (size_t)b * 18 + 2 + (c >> 2) * 4 + i] ^ 0x88u);
+        }
+    }
+    return 0;
+}
+
+int kqo_unpack_4x4_to_q4_0(const uint8_t *tiles, uint8_t *legacy, int rows, int cols) {
+    if (rows % 4 != 0 || cols % 32 != 0) return -1;
+    int nb = cols / 32;
+    size_t row_stride = (size_t)nb * 18;
+    for (int g = 0; g < rows / 4; g++) {
+        uint8_t *dst = legacy + (size_t)g * 4 * row_stride;
+        for (int b = 0; b < nb; b++) {
+            const uint8_t *t = tiles + ((size_t)g * nb + b) * 72;
+            for (int r = 0; r < 4; r++) memcpy(dst + r * row_stride + (size_t)b * 18, t + 2 * r, 2);
+            for (int c = 0; c < 16; c++)
+                for (int i = 0; i < 4; i++)
+                    dst[(c & 3) * row_stride + (size_t)b * 18 + 2 + (c >> 2) * 4 + i] =
+                        (uint8_t)(t[8 + 4 * c + i] ^ 0x88u);
+        }
+    }
+    return 0;
+}
+
+/* Element e (0..31) of row r (0..3) in one tile, as the signed weight n-8 in [-8, 7]:
+ * byte j = e & 15 sits at 8 + (j>>2)*16 + r*4 + (j&3); low nibble for e < 16, high otherwise;
+ * the stored nibble is n^8, i.e. the 4-bit two's complement of n-8 (layout doc
+ * vllm_safetensors.c:4121-4132, MoE accessor vq4x4_w :11000-11011). */
+int kqo_tile_weight(const uint8_t *tile, int r, int e) {
+    int j = e & 15;
+    uint8_t byte = tile[8 + (j >> 2) * 16 + r * 4 + (j & 3)];
+    int nib = (e < 16) ? (byte & 15) : (byte >> 4);
+    return ((nib ^ 8) & 15) - 8;
+}
+
+/* ---------------------------------------------------------------- activation quantizer */
+
+/* quantize_row_q8_0_act (vllm_safetensors.c:7893-7920; NEON twin q8q32_block_neon :7858-7883):
+ *   amax = max(1e-10f, max|x|); d = fl(amax/127); q = clamp((int)fl(fl(x/d) + 0.5f), -127, 127)
+ * (int) truncates toward zero, so -amax maps to -126. True IEEE division, never a reciprocal.
+ * Pinned against the reference quantizer built in oracle/_ref and by closed-form special
+ * cases (all-zero block, +-amax, .5 ties, saturation) in tests/test_oracle_quant.py. */
+void kqo_quantize_row_q8_0_act(const float *x, int8_t *q, float *d, int cols) {
+    int nb = cols / 32;
+    for (int b = 0; b < nb; b++) {
+        const float *xb = x + (size_t)b * 32;
+        float amax = 1e-10f;
+        for (int i = 0; i < 32; i++) {
+            float av = fabsf(xb[i]);
+            if (av > amax) amax = av;
+        }
+        float scale = amax / 127.0f;
+        d[b] = scale;
+        for (int i = 0; i < 32; i++) {
+            int v = (int)(xb[i] / scale + 0.5f);
+            if (v > 127) v = 127;
+            if (v < -127) v = -127;
+            q[(size_t)b * 32 + i] = (int8_t)v;
+        }
+    }
+}
+
+void kqo_quantize_rows(const float *x, int8_t *q, float *d, int n_batch, int cols) {
+    int nb = cols / 32;
+    for (int t = 0; t < n_batch; t++)
+        kqo_quantize_row_q8_0_act(x + (size_t)t * cols, q + (size_t)t * cols, d + (size_t)t * nb, cols);
+}
+
+/* ---------------------------------------------------------------- integer block sums */
+
+/* S_lo = sum_{e<16}(n_e-8) q_e, S_hi = sum_{e>=16}: what the sdot lanes produce before the
+ * exact /16 (vllm_safetensors.c:4133-4151, :4190-4216). Pinned by brute force through
+ * kqo_tile_weight on tiny inputs and the int32 bound |S| <= 32*8*127. */
+static void tile_sums(const uint8_t *tile, int r, const int8_t *q, int32_t *lo, int32_t *hi) {
+    int32_t a = 0, c = 0;
+    for (int e = 0; e < 16; e++) a += kqo_tile_weight(tile, r, e) * (int32_t)q[e];
+    for (int e = 16; e < 32; e++) c += kqo_tile_weight(tile, r, e) * (int32_t)q[e];
+    *lo = a;
+    *hi = c;
+}
+
+void kqo_block_sums(const uint8_t *w, const int8_t *xq, int rows, int cols, int n_batch,
+                    int32_t *s_lo, int32_t *s_hi) {
+    int nb = cols / 32;
+    for (int t = 0; t < n_batch; t++)
+        for (int n = 0; n < rows; n++)
+            for (int b = 0; b < nb; b++) {
+                const uint8_t *tile = w + ((size_t)(n >> 2) * nb + b) * 72;
+                size_t o = ((size_t)t * rows + n) * nb + b;
+                tile_sums(tile, n & 3, xq + (size_t)t * cols + (size_t)b * 32, &s_lo[o], &s_hi[o]);
+            }
+}
+
+/* ---------------------------------------------------------------- fp32 chains */
+
+static int token_chain(int chain, int t, int n_batch) {
+    if (chain != KQO_CHAIN_AUTO) return chain;
+    if (n_batch > 3 && t < (n_batch & ~3)) return KQO_CHAIN_ASM;
+    return KQO_CHAIN_CTILE;
+}
+
+static float f16r(float x) { return kqo_f16_to_f32(kqo_f32_to_f16_bits(x)); }
+
+/* One output (token t, row n) under chain c. */
+static float chain_out(const uint8_t *w, const int8_t *xq_t, const float *xd_t, int n, int nb,
+                       int c) {
+    const uint8_t *grp = w + (size_t)(n >> 2) * nb * 72;
+    int r = n & 3;
+    if (c == KQO_CHAIN_CTILE) {
+        float lo = 0.0f, hi = 0.0f;
+        for (int b = 0; b < nb; b++) {
+            const uint8_t *tile = grp + (size_t)b * 72;
+            int32_t sl, sh;
+            tile_sums(tile, r, xq_t + (size_t)b * 32, &sl, &sh);
+            uint16_t h;
+            memcpy(&h, tile + 2 * r, 2);
+            float s = kqo_f16_to_f32(h) * xd_t[b];
+            lo = fmaf((float)sl, s, lo);
+            hi = fmaf((float)sh, s, hi);
+        }
+        return lo + hi;
+    }
+    float acc = 0.0f;
+    for (int b = 0; b < nb; b++) {
+        const uint8_t *tile = grp + (size_t)b * 72;
+        int32_t sl, sh;
+        tile_sums(tile, r, xq_t + (size_t)b * 32, &sl, &sh);
+        uint16_t h;
+        memcpy(&h, tile + 2 * r, 2);
+        float xs = (c == KQO_CHAIN_ASM) ? f16r(xd_t[b]) : xd_t[b];
+        float s = kqo_f16_to_f32(h) * xs;
+        acc = fmaf((float)(sl + sh), s, acc);
+    }
+    return acc;
+}
+
+int kqo_matmul_q(float *out, const int8_t *xq, const float *xd, const float *residual,
+                 const uint8_t *w, int rows, int cols, int n_batch, int chain) {
+    if (rows <= 0 || rows % 4 || cols <= 0 || cols % 32 || n_batch < 0) return -1;
+    int nb = cols / 32;
+    for (int t = 0; t < n_batch; t++) {
+        int c = token_chain(chain, t, n_batch);
+        for (int n = 0; n < rows; n++) {
+            float v = chain_out(w, xq + (size_t)t * cols, xd + (size_t)t * nb, n, nb, c);
+            if (residual) v = residual[(size_t)t * rows + n] + v;
+            out[(size_t)t * rows + n] = v;
+        }
+    }
+    return 0;
+}
+
+int kqo_matmul_q_sample(float *out, const int8_t *xq, const float *xd, const float *residual,
+                        const uint8_t *w, int rows, int cols, int n_batch, int chain,
+                        const int *tok, const int *row, int n_sample) {
+    if (rows <= 0 || rows % 4 || cols <= 0 || cols % 32) return -1;
+    int nb = cols / 32;
+    for (int i = 0; i < n_sample; i++) {
+        int t = tok[i], n = row[i];
+        if (t < 0 || t >= n_batch || n < 0 || n >= rows) return -1;
+        float v = chain_out(w, xq + (size_t)t * cols, xd + (size_t)t * nb, n, nb,
+                            token_chain(chain, t, n_batch));
+        if (residual) v = residual[(size_t)t * rows + n] + v;
+        out[i] = v;
+    }
+    return 0;
+}
+
+int kqo_matmul(float *out, const float *x, const float *residual, const uint8_t *w, int rows,
+               int cols, int n_batch, int chain) {
+    if (rows <= 0 || rows % 4 || cols <= 0 || cols % 32 || n_batch < 0) return -1;
+    int nb = cols / 32;
+    int8_t *xq = (int8_t *)malloc((size_t)n_batch * cols + 1);
+    float *xd = (float *)malloc(((size_t)n_batch * nb + 1) * sizeof(float));
+    if (!xq || !xd) { free(xq); free(xd); return -1; }
+    kqo_quantize_rows(x, xq, xd, n_batch, cols);
+    int rc = kqo_matmul_q(out, xq, xd, residual, w, rows, cols, n_batch, chain);
+    free(xq);
+    free(xd);
+    return rc;
+}
+
+void kqo_matmul_f64(double *out, const int8_t *xq, const float *xd, const uint8_t *w, int rows,
+                    int cols, int n_batch) {
+    int nb = cols / 32;
+    for (int t = 0; t < n_batch; t++)
+        for (int n = 0; n < rows; n++) {
+            double acc = 0.0;
+            for (int b = 0; b < nb; b++) {
+                const uint8_t *tile = w + ((size_t)(n >> 2) * nb + b) * 72;
+                int32_t sl, sh;
+                tile_sums(tile, n & 3, xq + (size_t)t * cols + (size_t)b * 32, &sl, &sh);
+                uint16_t h;
+                memcpy(&h, tile + 2 * (n & 3), 2);
+                acc += (double)kqo_f16_to_f32(h) * (double)xd[(size_t)t * nb + b] * (double)(sl + sh);
+            }
+            out[(size_t)t * rows + n] = acc;
+        }
+}
+
+/* ---------------------------------------------------------------- MoE */
+
+/* Router logit: serial fp32 dot s = fl(s + fl(w*x)), i ascending (st_moe_ffn_sparse_q4
+ * vllm_safetensors.c:12961-12967; the reference build uses -ffp-contract=off). */
+void kqo_router_logits(const float *router, const float *x, int ne, int d, float *logits) {
+    for (int e = 0; e < ne; e++) {
+        const float *rw = router + (size_t)e * d;
+        float s = 0.0f;
+        for (int i = 0; i < d; i++) s += rw[i] * x[i];
+        logits[e] = s;
+    }
+}
+
+/* Deterministic top-k by insertion, ties -> smaller expert id; softmax over the k selected:
+ * p = fl(expf(l - max) * fl(1/sum)), sum accumulated k ascending
+ * (vllm_safetensors.c:12968-12984; batched twin :14963-14989). Pinned by closed-form cases
+ * (ties, equal logits -> uniform 1/k) and by the reference's own x86 MoE built in oracle/_ref. */
+void kqo_moe_route(const float *lg, int ne, int tk, int *sel, float *pr) {
+    float sv[64];
+    for (int k = 0; k < tk; k++) { sel[k] = -1; sv[k] = -INFINITY; }
+    for (int e = 0; e < ne; e++) {
+        for (int k = 0; k < tk; k++) {
+            if (lg[e] > sv[k] || (lg[e] == sv[k] && (sel[k] < 0 || e < sel[k]))) {
+                for (int j = tk - 1; j > k; j--) { sel[j] = sel[j - 1]; sv[j] = sv[j - 1]; }
+                sel[k] = e;
+                sv[k] = lg[e];
+                break;
+            }
+        }
+    }
+    float mx = -INFINITY;
+    for (int k = 0; k < tk; k++) if (sv[k] > mx) mx = sv[k];
+    float sum = 0.0f;
+    for (int k = 0; k < tk; k++) { pr[k] = expf(sv[k] - mx); sum += pr[k]; }
+    float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
+    for (int k = 0; k < tk; k++) pr[k] *= inv;
+}
+
+/* av = fl(fl(g / fl(1 + expf(-g))) * u)  (vllm_safetensors.c:12671-12675, :14752). The expf
+ * bits come from this host's libm; the reference's on-board libm is not reachable here, which
+ * is why the down stage is pinned stage-wise (kqo_moe_ffn av_in). */
+float kqo_silu_mul(float g, float u) { return (g / (1.0f + expf(-g))) * u; }
+
+/* V4 tile step for one row: S over all 32 elements, acc = fl(acc + fl(fl(sc*xd) * S))
+ * (q4x4_gup_actq_neon :11893-11902, moe_q4_down_group_actq_neon :11947-11963). */
+static float v4_row(const uint8_t *tiles, int ntile, int r, const int8_t *q, const float *qd) {
+    float acc = 0.0f;
+    for (int cb = 0; cb < ntile; cb++) {
+        const uint8_t *tile = tiles + (size_t)cb * 72;
+        int32_t sl, sh;
+        tile_sums(tile, r, q + (size_t)cb * 32, &sl, &sh);
+        uint16_t h;
+        memcpy(&h, tile + 2 * r, 2);
+        float sc = kqo_f16_to_f32(h) * qd[cb];
+        acc = acc + sc * (float)(sl + sh);
+    }
+    return acc;
+}
+
+/* Grouped MoE FFN, int8 track (VLLM_ACTQ=1): per (token t, rank j) with expert e = sel:
+ *   gate/up rows [e*ef, e*ef+ef) of G/U (4-row groups e*ef/4 ..), x quantized once per token;
+ *   av = silu(g)*u, re-quantized per (t, j) with quantize_row_q8_0_act;
+ *   down: rows 0..d-1 of D over the column band [e*ef, e*ef+ef) (tiles e*ef/32 .. +ef/32);
+ *   y = fl(y + fl(p * acc)) for j = 0..tk-1 ascending from y = 0.
+ * (st_moe_ffn_sparse_q4 :12921-13398 with arm_dn_actq_worker :12895-12902; batched
+ * st_moe_ffn_sparse_q4_batch_arm :14894-15064 computes the same per (t, j) values.) */
+int kqo_moe_ffn(float *Y, const float *X, const int *sel, const float *pr, int T, int tk,
+                const uint8_t *G, const uint8_t *U, const uint8_t *D, int ne, int d, int ef,
+                float *gate_o, float *up_o, float *av_o, int8_t *avq_o, float *avd_o, float *P_o,
+                const float *av_in) {
+    if (d <= 0 || d % 32 || ef <= 0 || ef % 32 || ne <= 0 || tk <= 0 || tk > 64) return -1;
+    int nbG = d / 32, cbe = ef / 32, ff = ne * ef, nbD = ff / 32;
+    size_t ggB = (size_t)nbG * 72, gdB = (size_t)nbD * 72;
+    int8_t *xq = (int8_t *)malloc((size_t)d);
+    float *xd = (float *)malloc((size_t)nbG * sizeof(float));
+    float *gv = (float *)malloc((size_t)ef * sizeof(float));
+    float *uv = (float *)malloc((size_t)ef * sizeof(float));
+    float *av = (float *)malloc((size_t)ef * sizeof(float));
+    int8_t *aq = (int8_t *)malloc((size_t)ef);
+    float *ad = (float *)malloc((size_t)cbe * sizeof(float));
+    if (!xq || !xd || !gv || !uv || !av || !aq || !ad) {
+        free(xq); free(xd); free(gv); free(uv); free(av); free(aq); free(ad);
+        return -1;
+    }
+    for (int t = 0; t < T; t++) {
+        float *y = Y + (size_t)t * d;
+        for (int i = 0; i < d; i++) y[i] = 0.0f;
+        kqo_quantize_row_q8_0_act(X + (size_t)t * d, xq, xd, d);
+        for (int j = 0; j < tk; j++) {
+            int e = sel[(size_t)t * tk + j];
+            size_t sj = (size_t)t * tk + j;
+            if (e < 0 || e >= ne) continue;
+            for (int n = 0; n < ef; n++) {
+                size_t g = (size_t)(e * ef + n) >> 2;
+                gv[n] = v4_row(G + g * ggB, nbG, n & 3, xq, xd);
+                uv[n] = v4_row(U + g * ggB, nbG, n & 3, xq, xd);
+                av[n] = kqo_silu_mul(gv[n], uv[n]);
+            }
+            if (gate_o) memcpy(gate_o + sj * ef, gv, (size_t)ef * sizeof(float));
+            if (up_o) memcpy(up_o + sj * ef, uv, (size_t)ef * sizeof(float));
+            if (av_o) memcpy(av_o + sj * ef, av, (size_t)ef * sizeof(float));
+            const float *avs = av_in ? av_in + sj * ef : av;
+            kqo_quantize_row_q8_0_act(avs, aq, ad, ef);
+            if (avq_o) memcpy(avq_o + sj * ef, aq, (size_t)ef);
+            if (avd_o) memcpy(avd_o + sj * cbe, ad, (size_t)cbe * sizeof(float));
+            float p = pr[sj];
+            size_t cb0 = (size_t)e * ef / 32;
+            for (int n = 0; n < d; n++) {
+                const uint8_t *band = D + (size_t)(n >> 2) * gdB + cb0 * 72;
+                float acc = v4_row(band, cbe, n & 3, aq, ad);
+                if (P_o) P_o[sj * d + n] = acc;
+                y[n] = y[n] + p * acc;
+            }
+        }
+    }
+    free(xq); free(xd); free(gv); free(uv); free(av); free(aq); free(ad);
+    return 0;
+}

@@ -1,0 +1,145 @@
+"""GPU parity of the dense op (quantizer, integer block sums, decode GEMV, prefill GEMM) against
+the oracle, through the C ABI.
+
+Bars: activation codes/scales and integer block sums bit-exact; prefill GEMM outputs bit-exact
+(it replays the reference chain per output); decode GEMV outputs within
+max|got-ref| / max|ref| <= 1e-5 (split-K summation order; the reference's metric,
+vllm_safetensors.c:1177-1181), max-abs reported."""
+import numpy as np
+import pytest
+
+import synth
+from conftest import rel_err
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-5
+
+
+def to_dev(torch, a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    return t.cpu().numpy()
+
+
+def case(rows, cols, n, seed, sigma=0.02, floor=1e-4):
+    w = synth.make_q4_weights(rows, cols, seed, sigma, floor)
+    x = synth.make_activations(n, cols, seed + 1)
+    return w, x
+
+
+def test_quantize_bit_exact(kq4, torch_dev, orc):
+    torch = torch_dev
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal((7, 512)).astype(np.float32)
+    x[0, :32] = 0
+    x[1, :32] *= 1e-30
+    x[2, 32:64] = 127.0
+    x[2, 40] = -127.0
+    x[3, :32] = 1e-41                                   # subnormal inputs
+    x[4] *= 1e4
+    x[5, 64:96] = np.float32(0.49999997)
+    xq_o, xd_o = orc.quantize(x, 512)
+    X = to_dev(torch, x)
+    xq = torch.empty((7, 512), dtype=torch.int8, device="cuda")
+    xd = torch.empty((7, 16), dtype=torch.float32, device="cuda")
+    xde = torch.empty_like(xd)
+    kq4.quantize_dev(X, xq, xd, xde, chain=kq4.CHAIN_ASM)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(xq), xq_o)
+    assert np.array_equal(host(xd).view(np.uint32), xd_o.view(np.uint32))
+    assert np.array_equal(host(xde), xd_o.astype(np.float16).astype(np.float32))
+
+
+@pytest.mark.parametrize("rows,cols,n", [(8, 64, 1), (20, 160, 3), (64, 2048, 5)])
+def test_block_sums_exact(kq4, torch_dev, orc, rows, cols, n):
+    torch = torch_dev
+    w, x = case(rows, cols, n, 10 + n)
+    xq, xd = orc.quantize(x, cols)
+    lo_o, hi_o = orc.block_sums(w, xq, rows, cols)
+    lo = torch.empty((n, rows, cols // 32), dtype=torch.int32, device="cuda")
+    hi = torch.empty_like(lo)
+    kq4.block_sums_dev(lo, hi, to_dev(torch, xq), to_dev(torch, w), rows, cols, n)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(lo), lo_o) and np.array_equal(host(hi), hi_o)
+
+
+GEMV_SHAPES = [(16, 256), (20, 160), (4, 32), (132, 4096), (6144, 2048), (2048, 6144)]
+
+
+@pytest.mark.parametrize("n", [1, 2, 3, 4, 5, 8])
+@pytest.mark.parametrize("rows,cols", GEMV_SHAPES)
+def test_gemv(kq4, torch_dev, orc, rows, cols, n):
+    torch = torch_dev
+    w, x = case(rows, cols, n, rows + cols + n)
+    want = orc.matmul(w, x, rows, cols)
+    out = torch.empty((n, rows), dtype=torch.float32, device="cuda")
+    kq4.matmul_dev(out, to_dev(torch, x), to_dev(torch, w), rows, cols)
+    torch.cuda.synchronize()
+    r, a = rel_err(host(out), want)
+    print(f"gemv rows={rows} cols={cols} n={n}: rel={r:.3e} maxabs={a:.3e}")
+    assert r <= TOL
+
+
+@pytest.mark.parametrize("chain", [1, 2, 3])
+def test_gemv_chains_and_residual(kq4, torch_dev, orc, chain):
+    torch = torch_dev
+    rows, cols, n = 96, 1024, 6
+    w, x = case(rows, cols, n, 77, sigma=0.015, floor=0.0)
+    res = np.random.default_rng(5).standard_normal((n, rows)).astype(np.float32)
+    want = orc.matmul(w, x, rows, cols, residual=res, chain=chain)
+    out = torch.empty((n, rows), dtype=torch.float32, device="cuda")
+    kq4.matmul_dev(out, to_dev(torch, x), to_dev(torch, w), rows, cols,
+                   residual=to_dev(torch, res), chain=chain)
+    torch.cuda.synchronize()
+    r, a = rel_err(host(out), want)
+    assert r <= TOL, (r, a)
+
+
+def test_gemv_multi_qkv(kq4, torch_dev, orc):
+    torch = torch_dev
+    cols, n = 2048, 4
+    rows = [2048, 1024, 1024]
+    ws = [synth.make_q4_weights(r, cols, 200 + i) for i, r in enumerate(rows)]
+    x = synth.make_activations(n, cols, 300)
+    outs = [torch.empty((n, r), dtype=torch.float32, device="cuda") for r in rows]
+    kq4.matmul_multi_dev(outs, to_dev(torch, x), [to_dev(torch, w) for w in ws], rows, cols)
+    torch.cuda.synchronize()
+    for o, w, r in zip(outs, ws, rows):
+        rr, _ = rel_err(host(o), orc.matmul(w, x, r, cols))
+        assert rr <= TOL
+
+
+@pytest.mark.parametrize("n", [12, 64, 130, 257])
+@pytest.mark.parametrize("chain", [0, 1, 2, 3])
+def test_gemm_bit_exact(kq4, torch_dev, orc, n, chain):
+    torch = torch_dev
+    rows, cols = 260, 512
+    w, x = case(rows, cols, n, 400 + n)
+    res = np.random.default_rng(n).standard_normal((n, rows)).astype(np.float32)
+    want = orc.matmul(w, x, rows, cols, residual=res, chain=chain)
+    out = torch.empty((n, rows), dtype=torch.float32, device="cuda")
+    kq4.matmul_dev(out, to_dev(torch, x), to_dev(torch, w), rows, cols,
+                   residual=to_dev(torch, res), chain=chain)
+    torch.cuda.synchronize()
+    got = host(out)
+    main = (n & ~3) if chain == 0 else n
+    exact = np.array_equal(got[:main].view(np.uint32), want[:main].view(np.uint32))
+    r, a = rel_err(got, want)
+    print(f"gemm n={n} chain={chain}: main bit-exact={exact} rel={r:.3e} maxabs={a:.3e}")
+    assert exact
+    assert r <= TOL
+
+
+def test_gemm_from_prequantized(kq4, torch_dev, orc):
+    torch = torch_dev
+    rows, cols, n = 128, 1024, 40
+    w, x = case(rows, cols, n, 501)
+    xq, xd = orc.quantize(x, cols)
+    want = orc.matmul_q(w, xq, xd, rows, cols)
+    out = torch.empty((n, rows), dtype=torch.float32, device="cuda")
+    kq4.matmul_q_dev(out, to_dev(torch, xq), to_dev(torch, xd), to_dev(torch, w), rows, cols, n)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(out), want)

@@ -1,0 +1,96 @@
+"""GPU parity of the MoE FFN (int8 track) against the oracle (which is pinned bit-exact to the
+reference's own MoE in tests/test_oracle_moe.py), stage by stage:
+  routing (device top-k/softmax)          sel exact, pr within 2 ulp (expf bits)
+  gate / up (V4 chains)                   bit-exact
+  SiLU product av                          within 2 ulp (exp evaluated on the device)
+  down partials fed with the oracle's av   bit-exact (then Y bit-exact with the oracle's routing)
+  end to end Y                             max|dY|/max|Y| <= 1e-5, max-abs reported
+"""
+import numpy as np
+import pytest
+
+import synth
+from conftest import rel_err
+
+pytestmark = pytest.mark.gpu
+
+
+def to_dev(torch, a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    return t.cpu().numpy()
+
+
+def ulps(a, b):
+    a = np.asarray(a, np.float32).view(np.int32).astype(np.int64)
+    b = np.asarray(b, np.float32).view(np.int32).astype(np.int64)
+    return np.abs(a - b).max() if a.size else 0
+
+
+SHAPES = {"small": dict(hidden=256, experts=16, top_k=4, ef=64),
+          "qwen3_30b_a3b": synth.QWEN3_30B_A3B_MOE}
+
+
+def test_route(kq4, torch_dev, orc):
+    torch = torch_dev
+    lg = synth.make_logits(64, 128, 3)
+    lg[:, 7] = lg[:, 3]
+    sel_o, pr_o = orc.moe_route(lg, 8)
+    sel = torch.empty((64, 8), dtype=torch.int32, device="cuda")
+    pr = torch.empty((64, 8), dtype=torch.float32, device="cuda")
+    kq4.moe_route_dev(sel, pr, to_dev(torch, lg), 8)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(sel), sel_o)
+    assert ulps(host(pr), pr_o) <= 2
+
+
+@pytest.mark.parametrize("T", [1, 7, 64])
+@pytest.mark.parametrize("shape", ["small", "qwen3_30b_a3b"])
+def test_moe_stages(kq4, torch_dev, orc, shape, T):
+    torch = torch_dev
+    cfg = SHAPES[shape]
+    d, ne, tk, ef = cfg["hidden"], cfg["experts"], cfg["top_k"], cfg["ef"]
+    G, U, D = synth.make_moe(cfg, 40 + T)
+    X = synth.make_activations(T, d, 50 + T)
+    sel, pr = orc.moe_route(synth.make_logits(T, ne, 60 + T), tk)
+    Y_o, st = orc.moe_ffn(X, sel, pr, G, U, D, ne, d, ef, stages=True)
+
+    dG, dU, dD = (to_dev(torch, a) for a in (G, U, D))
+    dX, dsel, dpr = to_dev(torch, X), to_dev(torch, sel), to_dev(torch, pr)
+    Y = torch.empty((T, d), dtype=torch.float32, device="cuda")
+    gate = torch.zeros((T * tk, ef), dtype=torch.float32, device="cuda")
+    up = torch.zeros_like(gate)
+    av = torch.zeros_like(gate)
+    kq4.moe_ffn_stages_dev(Y, dX, dsel, dpr, dG, dU, dD, ne, d, ef, gate=gate, up=up, av=av)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(gate).view(np.uint32), st["gate"].view(np.uint32))
+    assert np.array_equal(host(up).view(np.uint32), st["up"].view(np.uint32))
+    assert ulps(host(av), st["av"]) <= 2
+    r, a = rel_err(host(Y), Y_o)
+    print(f"moe {shape} T={T}: Y rel={r:.3e} maxabs={a:.3e} "
+          f"bit-exact={np.array_equal(host(Y), Y_o)}")
+    assert r <= 1e-5
+
+    # down stage fed with the oracle's av: bit-exact partials and output
+    Y2 = torch.empty_like(Y)
+    kq4.moe_ffn_stages_dev(Y2, dX, dsel, dpr, dG, dU, dD, ne, d, ef,
+                           av_in=to_dev(torch, st["av"]))
+    torch.cuda.synchronize()
+    assert np.array_equal(host(Y2).view(np.uint32), Y_o.view(np.uint32))
+
+
+def test_moe_invalid_expert_ids_skipped(kq4, torch_dev, orc):
+    torch = torch_dev
+    cfg = SHAPES["small"]
+    d, ne, tk, ef = cfg["hidden"], cfg["experts"], cfg["top_k"], cfg["ef"]
+    G, U, D = synth.make_moe(cfg, 90)
+    X = synth.make_activations(3, d, 91)
+    sel, pr = orc.moe_route(synth.make_logits(3, ne, 92), tk)
+    sel[1, 2] = -1
+    sel[2, 0] = ne + 5
+    Y_o = orc.moe_ffn(X, sel, pr, G, U, D, ne, d, ef)
+    Y = kq4.moe_ffn(X, sel, pr, G, U, D, ne, d, ef)
+    r, _ = rel_err(Y, Y_o)
+    assert r <= 1e-5
