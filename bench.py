@@ -125,6 +125,100 @@ def run_gpu(args):
                 total_bytes=total_bytes)
 
 
+def _time_loop(torch, stream, fn, reps, warm=3):
+    for i in range(warm):
+        fn(i)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for i in range(reps):
+        fn(i)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / reps   # us per call
+
+
+def run_extras(reps=20):
+    """BASELINE.json configs 3-5 (reported beside the headline line, each on its own):
+    Qwen3-8B decode GEMVs at M in {1,2,4,8} (us/call, GB/s), prefill GEMM at M in {512, 2048}
+    (int8 TOPS vs 5.0 POPS dense), Qwen3-30B-A3B MoE FFN at T in {1, 64}."""
+    import torch
+
+    import kq4
+
+    stream = torch.cuda.current_stream()
+    cfg = synth.QWEN3_8B
+    h, f = cfg["hidden"], cfg["ffn"]
+    qkv = (cfg["q_heads"] + 2 * cfg["kv_heads"]) * cfg["head_dim"]
+    n_copies = 6                                       # 6 x 99 MB > 256 MB Infinity Cache
+    base = {"gate": synth.make_q4_weights(f, h, 11, **synth.SCALE_8B),
+            "up": synth.make_q4_weights(f, h, 12, **synth.SCALE_8B),
+            "down": synth.make_q4_weights(h, f, 13, **synth.SCALE_8B),
+            "qkv": synth.make_q4_weights(qkv, h, 14, **synth.SCALE_8B)}
+    d0 = {k: torch.from_numpy(v.reshape(-1)).cuda() for k, v in base.items()}
+    copies = [{k: v.clone() for k, v in d0.items()} for _ in range(n_copies)]
+    out = {}
+    dec = {}
+    for m in (1, 2, 4, 8):
+        x = torch.from_numpy(synth.make_activations(m, h, 20 + m)).cuda()
+        xf = torch.from_numpy(synth.make_activations(m, f, 30 + m)).cuda()
+        og, ou = torch.empty((m, f), device="cuda"), torch.empty((m, f), device="cuda")
+        od, oq = torch.empty((m, h), device="cuda"), torch.empty((m, qkv), device="cuda")
+        t_gu = _time_loop(torch, stream, lambda i: kq4.matmul_multi_dev(
+            [og, ou], x, [copies[i % n_copies]["gate"], copies[i % n_copies]["up"]], [f, f], h,
+            stream=stream), reps)
+        t_dn = _time_loop(torch, stream, lambda i: kq4.matmul_dev(
+            od, xf, copies[i % n_copies]["down"], h, f, stream=stream), reps)
+        t_q = _time_loop(torch, stream, lambda i: kq4.matmul_dev(
+            oq, x, copies[i % n_copies]["qkv"], qkv, h, stream=stream), reps)
+        b_gu = 2 * f * h * 18 // 32 + m * h * 4 + 2 * m * f * 4
+        b_dn = h * f * 18 // 32 + m * f * 4 + m * h * 4
+        b_q = qkv * h * 18 // 32 + m * h * 4 + m * qkv * 4
+        dec[f"M{m}"] = {
+            "gate_up_us": round(t_gu, 2), "gate_up_GBs": round(b_gu / t_gu / 1e3, 1),
+            "down_us": round(t_dn, 2), "down_GBs": round(b_dn / t_dn / 1e3, 1),
+            "qkv_us": round(t_q, 2), "qkv_GBs": round(b_q / t_q / 1e3, 1)}
+    out["qwen3_8b_decode"] = dec
+    pre = {}
+    for m in (512, 2048):
+        x = torch.from_numpy(synth.make_activations(m, h, 40)).cuda()
+        xf = torch.from_numpy(synth.make_activations(m, f, 41)).cuda()
+        og = torch.empty((m, f), device="cuda")
+        od = torch.empty((m, h), device="cuda")
+        r = max(3, reps // 4)
+        t_g = _time_loop(torch, stream, lambda i: kq4.matmul_dev(
+            og, x, copies[i % 2]["gate"], f, h, stream=stream), r, warm=1)
+        t_d = _time_loop(torch, stream, lambda i: kq4.matmul_dev(
+            od, xf, copies[i % 2]["down"], h, f, stream=stream), r, warm=1)
+        ops = 2.0 * m * f * h
+        pre[f"M{m}"] = {"gate_us": round(t_g, 1), "gate_TOPS": round(ops / t_g / 1e6, 1),
+                        "down_us": round(t_d, 1), "down_TOPS": round(ops / t_d / 1e6, 1),
+                        "frac_int8_peak": round(ops / min(t_g, t_d) / 1e6 / 5000.0, 4)}
+    out["qwen3_8b_prefill"] = pre
+    del copies, d0
+    mcfg = synth.QWEN3_30B_A3B_MOE
+    d, ne, tk, ef = mcfg["hidden"], mcfg["experts"], mcfg["top_k"], mcfg["ef"]
+    layers = []
+    for c in range(2):
+        G, U, D = synth.make_moe(mcfg, 50 + 3 * c)
+        layers.append([torch.from_numpy(a.reshape(-1)).cuda() for a in (G, U, D)])
+    moe = {}
+    for T in (1, 64):
+        X = torch.from_numpy(synth.make_activations(T, d, 60)).cuda()
+        lg = torch.from_numpy(synth.make_logits(T, ne, 61)).cuda()
+        sel = torch.empty((T, tk), dtype=torch.int32, device="cuda")
+        pr = torch.empty((T, tk), device="cuda")
+        Y = torch.empty((T, d), device="cuda")
+        kq4.moe_route_dev(sel, pr, lg, tk, stream=stream)
+        t = _time_loop(torch, stream, lambda i: kq4.moe_ffn_dev(
+            Y, X, sel, pr, *layers[i % 2], ne, d, ef, stream=stream), reps)
+        n_exp = len(set(sel.cpu().numpy().reshape(-1).tolist()))
+        byts = n_exp * 3 * ef * d * 18 // 32 + T * d * 8
+        moe[f"T{T}"] = {"us": round(t, 2), "experts": n_exp, "GBs": round(byts / t / 1e3, 1)}
+    out["qwen3_30b_a3b_moe"] = moe
+    return out
+
+
 def cpu_baseline(m, budget_s=12.0):
     """The reference's x86-64 op wrappers (fp32/int16 activation arithmetic; a timing
     baseline, not a parity reference) on a bounded sample: layers cycled over enough distinct
@@ -136,7 +230,7 @@ def cpu_baseline(m, budget_s=12.0):
     kind = "reference" if oracle.ref_available() else "port"
     s = layer_mats()
     h, q, kv, f = CFG["hidden"], s["q"][0], s["k"][0], CFG["ffn"]
-    n_copies = 10
+    n_copies = CFG["layers"]                          # 28 x 28.3 MB: beyond any host LLC
     rng = np.random.default_rng(3)
     layers = [{k: rng.integers(0, 256, size=v.size, dtype=np.uint8) for k, v in
                {n: np.empty(r * c * 18 // 32, np.uint8) for n, (r, c) in s.items()}.items()}
@@ -190,6 +284,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--m", type=int, default=1, help="tokens per step (decode batch)")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-extras", action="store_true",
+                    help="skip the config 3-5 sub-results (8B decode, prefill GEMM, MoE)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     args = ap.parse_args()
     if args.gpus != 1:
@@ -221,6 +317,8 @@ def main():
                      "traffic": None,
                      "kernel": "kq4_gemv_kernel (fused gate/up, 2 x 6144x2048)"},
     }
+    if not args.no_extras:
+        line["extras"] = run_extras()
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(args.m, args.cpu_seconds)
     print(json.dumps(line))

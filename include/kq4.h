@@ -72,6 +72,10 @@ const char *kq4_version(void);
  * weight cache does (st_npu_gw_get/build vllm_safetensors.c:2780-3040). */
 int kq4_weights_upload(uint64_t wkey, const uint8_t *w4x4, int rows, int cols);
 int kq4_weights_evict(uint64_t wkey);
+/* Drops every cached weight matrix of the current device; returns how many were dropped.
+ * A cached entry is also re-uploaded when its host bytes no longer match (sampled
+ * fingerprint), so a key reused for different weights is never served stale. */
+int kq4_weights_clear(void);
 
 /* out = [residual +] W.x for n_batch tokens; replaces q4x4_gemm_batched / dyn_matvec_q4_q8*
  * (vllm_safetensors.c:4593-4631, 6147-6174, 8628-8786) behind st_npu_try_gemm_batched_q4's

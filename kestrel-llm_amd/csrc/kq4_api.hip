@@ -5,6 +5,7 @@
 
 #include <stdarg.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <mutex>
@@ -36,6 +37,7 @@ struct Buf {
 struct WEntry {
   uint8_t *p;
   size_t bytes;
+  uint64_t fp;   // fingerprint of the host bytes it was uploaded from
 };
 
 const int kMaxDev = 16;
@@ -43,7 +45,6 @@ const int kMaxDev = 16;
 struct DevState {
   bool ready = false;
   Buf ws;    // quantized activations, split-K partials, MoE staging
-  Buf cnt;   // split-K arrival counters, kept zero between launches
   Buf hx, hres, hout, hw, hsel, hpr;   // staging for the host-pointer API
   std::unordered_map<uint64_t, WEntry> wcache;
 };
@@ -65,7 +66,7 @@ int cur_dev(DevState **out) {
   return KQ4_OK;
 }
 
-int ensure(Buf &b, size_t bytes, bool zero = false) {
+int ensure(Buf &b, size_t bytes) {
   if (b.cap >= bytes) return KQ4_OK;
   size_t n = al256(bytes > 4096 ? bytes + bytes / 4 : 4096);
   if (b.p) {
@@ -78,7 +79,6 @@ int ensure(Buf &b, size_t bytes, bool zero = false) {
     b.p = nullptr;
     return fail(KQ4_ENOMEM, "hipMalloc(%zu) failed", n);
   }
-  if (zero) KQ4_HIP(hipMemset(b.p, 0, n));
   b.cap = n;
   return KQ4_OK;
 }
@@ -96,6 +96,19 @@ struct Carve {   // bump allocator over a workspace
 
 bool shape_ok(int rows, int cols) { return rows > 0 && rows % 4 == 0 && cols > 0 && cols % 32 == 0; }
 
+// Token counts up to this quantize their activations inside the GEMV (no separate launch).
+// KQ4_FUSED_QUANT_MAX_M (0..4) overrides it, e.g. to compare both paths.
+int fused_quant_max_m() {
+  static int v = -1;
+  if (v < 0) {
+    const char *e = getenv("KQ4_FUSED_QUANT_MAX_M");
+    v = e ? atoi(e) : KQ4_GEMV_FQ_MAX_M;
+    if (v < 0) v = 0;
+    if (v > KQ4_GEMV_FQ_MAX_M) v = KQ4_GEMV_FQ_MAX_M;
+  }
+  return v;
+}
+
 int asm_tokens_for(int chain, int n) {
   if (chain == KQ4_CHAIN_ASM) return n;
   if (chain == KQ4_CHAIN_AUTO) return n > 3 ? (n & ~3) : 0;
@@ -103,60 +116,35 @@ int asm_tokens_for(int chain, int n) {
 }
 
 // GEMV over n_mats matrices for n tokens (n <= 8) from token-major xq/xd.
-int run_gemv(DevState *ds, int n_mats, float *const *out, const float *const *res,
-             const uint8_t *const *w, const int *rows, int cols, const int8_t *xq, const float *xd,
-             int n, int asm_tokens, Carve &cv, size_t ws_limit, hipStream_t s) {
+// xf != nullptr: the kernel quantizes the fp32 activations itself (one launch per op).
+int run_gemv(int n_mats, float *const *out, const float *const *res, const uint8_t *const *w,
+             const int *rows, int cols, const float *xf, const int8_t *xq, const float *xd,
+             int n, int asm_tokens, hipStream_t s) {
   const int nb = cols / 32;
-  int slabs_total = 0;
-  long wg_est = 0;
-  for (int i = 0; i < n_mats; ++i) {
-    slabs_total += (rows[i] + 15) / 16;
-    wg_est += (long)((rows[i] + 15) / 16) * ((nb + 63) / 64);
-  }
-  const int ppl = wg_est >= 1024 ? 2 : 1;
-  const int bpw = 32 * ppl;
-  const int ks = (nb + bpw - 1) / bpw;
+  const int ppl = (!xf && nb > 32 * KQ4_GEMV_MAXW) ? 2 : 1;   // tile pairs per lane per chunk
+  const int chunks = (nb + 32 * ppl - 1) / (32 * ppl);
   KQ4GemvArgs a;
   memset(&a, 0, sizeof(a));
   a.nmat = n_mats;
+  a.xf = xf;
   a.xq = xq;
   a.xd = xd;
   a.asm_tokens = asm_tokens;
   a.cols = cols;
   a.nb = nb;
-  a.blocks_per_wg = bpw;
-  int rc = ensure(ds->cnt, (size_t)slabs_total * sizeof(unsigned), true);
-  if (rc) return rc;
-  unsigned *cnt = static_cast<unsigned *>(ds->cnt.p);
+  a.nwave = chunks < KQ4_GEMV_MAXW ? chunks : KQ4_GEMV_MAXW;
   int wg = 0;
   for (int i = 0; i < n_mats; ++i) {
-    const int slabs = (rows[i] + 15) / 16;
     KQ4GemvMat &m = a.mat[i];
     m.w = w[i];
     m.out = out[i];
     m.res = res ? res[i] : nullptr;
     m.rows = rows[i];
-    m.ks = ks;
     m.wg_begin = wg;
-    m.cnt = cnt;
-    cnt += slabs;
-    m.part = nullptr;
-    if (ks > 1) m.part = cv.take<float>((size_t)slabs * ks * n * 16);
-    wg += slabs * ks;
+    wg += (rows[i] + 15) / 16;
   }
-  if (cv.off > ws_limit) return fail(KQ4_EINVAL, "internal: workspace carve overflow");
   KQ4_HIP((hipError_t)kq4_launch_gemv(a, n, ppl, wg, s));
   return KQ4_OK;
-}
-
-size_t gemv_part_bytes(int n_mats, const int *rows, int cols, int n) {
-  const int nb = cols / 32;
-  size_t b = 0;
-  for (int i = 0; i < n_mats; ++i) {
-    const int slabs = (rows[i] + 15) / 16;
-    b += al256((size_t)slabs * ((nb + 31) / 32) * n * 16 * sizeof(float));
-  }
-  return b;
 }
 
 int matmul_impl(int n_mats, float *const *out, const float *const *res, const uint8_t *const *w,
@@ -178,31 +166,29 @@ int matmul_impl(int n_mats, float *const *out, const float *const *res, const ui
   const size_t qbytes = al256((size_t)n * cols) + al256((size_t)n * nb * sizeof(float));
 
   if (n <= KQ4_GEMV_MAX_M) {
-    const size_t need = qbytes + gemv_part_bytes(n_mats, rows, cols, n);
-    if ((rc = ensure(ds->ws, need))) return rc;
-    Carve cv{static_cast<char *>(ds->ws.p)};
+    if (x && n <= fused_quant_max_m())   // quantize inside the GEMV: one launch per op
+      return run_gemv(n_mats, out, res, w, rows, cols, x, nullptr, nullptr, n,
+                      asm_tokens_for(chain, n), s);
     const int8_t *xq = xq_in;
     const float *xd = xd_in;
     if (x) {
+      if ((rc = ensure(ds->ws, qbytes))) return rc;
+      Carve cv{static_cast<char *>(ds->ws.p)};
       int8_t *q = cv.take<int8_t>((size_t)n * cols);
       float *d = cv.take<float>((size_t)n * nb);
       KQ4_HIP((hipError_t)kq4_launch_quantize(x, q, d, nullptr, n, cols, 0, s, 0));
       xq = q;
       xd = d;
-    } else {
-      cv.off = qbytes;
     }
-    return run_gemv(ds, n_mats, out, res, w, rows, cols, xq, xd, n,
-                    asm_tokens_for(chain, n), cv, need, s);
+    return run_gemv(n_mats, out, res, w, rows, cols, nullptr, xq, xd, n,
+                    asm_tokens_for(chain, n), s);
   }
 
   // prefill: int8-MFMA GEMM on the main segment, GEMV on the 1..3-token CTILE tail (AUTO)
   const int main_n = chain == KQ4_CHAIN_AUTO ? (n & ~3) : n;
   const int tail = n - main_n;
   const int main_chain = chain == KQ4_CHAIN_AUTO ? KQ4_CHAIN_ASM : chain;
-  size_t need = qbytes;
-  if (tail) need += gemv_part_bytes(n_mats, rows, cols, tail);
-  if ((rc = ensure(ds->ws, need))) return rc;
+  if ((rc = ensure(ds->ws, qbytes))) return rc;
   Carve cv{static_cast<char *>(ds->ws.p)};
   KQ4GemmAct act;
   const int8_t *xq_t = nullptr;
@@ -237,7 +223,7 @@ int matmul_impl(int n_mats, float *const *out, const float *const *res, const ui
       o2[i] = out[i] + (size_t)main_n * rows[i];
       r2[i] = (res && res[i]) ? res[i] + (size_t)main_n * rows[i] : nullptr;
     }
-    return run_gemv(ds, n_mats, o2, r2, w, rows, cols, xq_t, xd_t, tail, 0, cv, need, s);
+    return run_gemv(n_mats, o2, r2, w, rows, cols, nullptr, xq_t, xd_t, tail, 0, s);
   }
   return KQ4_OK;
 }
@@ -274,12 +260,26 @@ int moe_impl(float *Y, const float *X, const int *sel, const float *pr, int T, i
 }
 
 // ---- host-pointer API helpers --------------------------------------------------------------
+
+// Cheap fingerprint of a host weight buffer (FNV-1a over 3 x 64 sampled bytes + size): a cache
+// entry whose key was reused for different bytes (e.g. a freed and reallocated host buffer) is
+// re-uploaded instead of served stale.
+uint64_t fingerprint(const uint8_t *w, size_t bytes) {
+  uint64_t h = 1469598103934665603ull ^ bytes;
+  const size_t span = bytes < 64 ? bytes : 64;
+  const size_t offs[3] = {0, bytes / 2 - (bytes / 2 >= span / 2 ? span / 2 : 0), bytes - span};
+  for (size_t o : offs)
+    for (size_t i = 0; i < span; ++i) h = (h ^ w[o + i]) * 1099511628211ull;
+  return h;
+}
+
 int dev_weights(DevState *ds, uint64_t wkey, const uint8_t *w, size_t bytes, Buf &tmp,
                 const uint8_t **dev) {
+  const uint64_t fp = wkey ? fingerprint(w, bytes) : 0;
   if (wkey) {
     std::lock_guard<std::mutex> lk(g_mu);
     auto it = ds->wcache.find(wkey);
-    if (it != ds->wcache.end() && it->second.bytes == bytes) {
+    if (it != ds->wcache.end() && it->second.bytes == bytes && it->second.fp == fp) {
       *dev = it->second.p;
       return KQ4_OK;
     }
@@ -294,8 +294,11 @@ int dev_weights(DevState *ds, uint64_t wkey, const uint8_t *w, size_t bytes, Buf
     }
     std::lock_guard<std::mutex> lk(g_mu);
     auto it = ds->wcache.find(wkey);
-    if (it != ds->wcache.end()) hipFree(it->second.p);
-    ds->wcache[wkey] = WEntry{static_cast<uint8_t *>(p), bytes};
+    if (it != ds->wcache.end()) {
+      (void)hipDeviceSynchronize();   // the stale copy may still be read by queued work
+      (void)hipFree(it->second.p);
+    }
+    ds->wcache[wkey] = WEntry{static_cast<uint8_t *>(p), bytes, fp};
     *dev = static_cast<uint8_t *>(p);
     return KQ4_OK;
   }
@@ -340,7 +343,7 @@ void kq4_shutdown(void) {
     if (!s.ready) continue;
     hipSetDevice(d);
     hipDeviceSynchronize();
-    Buf *bufs[] = {&s.ws, &s.cnt, &s.hx, &s.hres, &s.hout, &s.hw, &s.hsel, &s.hpr};
+    Buf *bufs[] = {&s.ws, &s.hx, &s.hres, &s.hout, &s.hw, &s.hsel, &s.hpr};
     for (Buf *b : bufs) {
       if (b->p) hipFree(b->p);
       *b = Buf();
@@ -459,10 +462,21 @@ int kq4_weights_evict(uint64_t wkey) {
   std::lock_guard<std::mutex> lk(g_mu);
   auto it = ds->wcache.find(wkey);
   if (it == ds->wcache.end()) return 0;
-  hipDeviceSynchronize();
-  hipFree(it->second.p);
+  (void)hipDeviceSynchronize();
+  (void)hipFree(it->second.p);
   ds->wcache.erase(it);
   return 1;
+}
+
+int kq4_weights_clear(void) {
+  DevState *ds = nullptr;
+  if (cur_dev(&ds)) return 0;
+  std::lock_guard<std::mutex> lk(g_mu);
+  const int n = (int)ds->wcache.size();
+  (void)hipDeviceSynchronize();
+  for (auto &kv : ds->wcache) (void)hipFree(kv.second.p);
+  ds->wcache.clear();
+  return n;
 }
 
 int kq4_matmul_multi(int n_mats, float *const *out, const float *const *residual,

@@ -6,35 +6,35 @@
 
 #define KQ4_GEMV_MAX_M 8
 #define KQ4_MAXMAT 4
+#define KQ4_GEMV_MAXW 8
+#define KQ4_GEMV_FQ_MAX_M 4   // largest token count the GEMV quantizes in-kernel
 
 // One weight matrix of a (possibly fused) GEMV launch. All matrices share the activation.
 struct KQ4GemvMat {
   const uint8_t *w;     // 4x4 tiles [rows/4][nb][72]
   float *out;           // [M][rows]
   const float *res;     // [M][rows] or nullptr
-  float *part;          // split-K partials [slabs][ks][M][16]
-  unsigned *cnt;        // split-K arrival counters [slabs] (zero between launches)
   int rows;
-  int ks;               // K chunks (workgroups) per 16-row slab
-  int wg_begin;         // first workgroup index of this matrix in the launch
+  int wg_begin;         // first workgroup (16-row slab) of this matrix in the launch
 };
 
 struct KQ4GemvArgs {
   KQ4GemvMat mat[KQ4_MAXMAT];
   int nmat;
-  const int8_t *xq;     // [M][cols]
-  const float *xd;      // [M][nb] activation scales
+  const float *xf;      // fp32 activations [M][cols] when the kernel quantizes them itself
+  const int8_t *xq;     // [M][cols] (pre-quantized path)
+  const float *xd;      // [M][nb] activation scales (pre-quantized path)
   int asm_tokens;       // tokens [0, asm_tokens) multiply by f32(f16_rne(xd)) (ASM chain)
   int cols;
   int nb;
-  int blocks_per_wg;    // 32 * pairs-per-lane
+  int nwave;            // waves per workgroup (K split), 1..KQ4_GEMV_MAXW
 };
 
 int kq4_launch_quantize(const float *x, int8_t *xq, float *xd, float *xde, int n_batch, int cols,
                         int asm_tokens, hipStream_t stream, int block_major = 0);
 
-// n_batch in [1, KQ4_GEMV_MAX_M]; ppl = tile pairs per lane (1 or 2); total_wg from the
-// matrices' wg_begin/ks.
+// n_batch in [1, KQ4_GEMV_MAX_M]; ppl = tile pairs per lane per K chunk (1 or 2);
+// total_wg = total 16-row slabs of all matrices.
 int kq4_launch_gemv(const KQ4GemvArgs &args, int n_batch, int ppl, int total_wg,
                     hipStream_t stream);
 

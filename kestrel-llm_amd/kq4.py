@@ -28,6 +28,7 @@ SIGNATURES = [
     ("kq4_version", ctypes.c_char_p, []),
     ("kq4_weights_upload", _I, [_U64, _P, _I, _I]),
     ("kq4_weights_evict", _I, [_U64]),
+    ("kq4_weights_clear", _I, []),
     ("kq4_matmul", _I, [_P, _P, _P, _P, _I, _I, _I, _I, _U64]),
     ("kq4_matmul_multi", _I, [_I, _P, _P, _P, _P, _I, _P, _I, _I, _P]),
     ("kq4_moe_ffn", _I, [_P, _P, _P, _P, _I, _I, _P, _P, _P, _I, _I, _I, _U64]),
@@ -75,6 +76,13 @@ def lib():
     """Loads libkq4.so (built in-tree by `make -C kestrel-llm_amd`); raises if absent."""
     global _lib
     if _lib is None:
+        # torch's wheel ships its own libamdhip64.so.7 (same soname as /opt/rocm's). Whichever
+        # loads first serves the whole process, and torch cannot use the system one; so when
+        # torch is installed, let it load first and libkq4 binds to the same runtime.
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         if not os.path.exists(LIB_PATH):
             raise KQ4Error(f"{LIB_PATH} is missing: build it with `make -C kestrel-llm_amd` "
                            "(or __graft_entry__.build())")

@@ -14,6 +14,25 @@ TOL = 1e-5
 P = lambda a: a.ctypes.data  # noqa: E731
 
 
+@pytest.fixture(autouse=True)
+def fresh_cache(kq4):
+    """The wrappers key cached weights by host pointer (the reference's weights are an mmap
+    that lives as long as the process); test arrays do not, so drop the cache per test."""
+    yield
+    kq4.lib().kq4_weights_clear()
+
+
+def test_reused_key_is_not_served_stale(kq4, orc):
+    rows, cols = 32, 256
+    w1 = synth.make_q4_weights(rows, cols, 61)
+    w2 = synth.make_q4_weights(rows, cols, 62)
+    x = synth.make_activations(1, cols, 63)
+    a = kq4.matmul(w1, x, rows, cols, wkey=77)
+    b = kq4.matmul(w2, x, rows, cols, wkey=77)     # same key, same size, different bytes
+    assert rel_err(a, orc.matmul(w1, x, rows, cols))[0] <= TOL
+    assert rel_err(b, orc.matmul(w2, x, rows, cols))[0] <= TOL
+
+
 def test_weight_cache_and_host_api(kq4, orc):
     rows, cols, n = 64, 512, 3
     w = synth.make_q4_weights(rows, cols, 1)
