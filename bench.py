@@ -2,19 +2,24 @@
 """Benchmark of the MI355X q4 x int8 matmul path (libkq4) on BASELINE.json's workload.
 
 Workload: the full decode-step linear set of a Qwen3-VL-2B-shaped
-decoder - QKV (2048 -> 16 q + 8 kv heads x 128), O (2048 -> 2048, + residual), gate/up
-(2048 -> 6144, one fused launch) and down (6144 -> 2048, + residual) - for all 28 layers, at
-M = 1 token (M = 4 reported alongside). One step = one token through the 28 layers' linear sets
-(quantize + matmul launches, 8 launches per layer). The 28 layers are distinct HBM copies
-(28 x 28.3 MB = 793 MB > the 256 MB Infinity Cache), so every step streams its weights from HBM.
-Inputs are resident in HBM before the timed region.
+decoder - QKV (2048 -> 16 q + 8 kv heads x 128, one fused launch), O (2048 -> 2048, + residual),
+gate/up (2048 -> 6144, one fused launch) and down (6144 -> 2048, + residual) - for all 28
+layers, at M = 1 token (--m 4 for the config's second batch). One step = one token through the
+28 layers' linear sets: 4 launches per layer (each quantizes its activations and multiplies),
+captured once as a HIP graph and replayed per step; the eager (host-launched) time is reported
+beside it. The 28 layers are distinct HBM copies (28 x 28.3 MB = 793 MB > the 256 MB Infinity
+Cache), so every step streams its weights from HBM. Inputs are resident in HBM before the timed
+region.
 
 value = algorithmic bytes per step (weights N*K*18/32 + activations M*K*4 + outputs M*N*4 +
-residuals M*N*4) / step time, in GB/s. roofline: the dominant kernel (the fused gate/up GEMV),
-timed on its own stream with HIP events, against MI355X HBM peak 8 TB/s. cpu_baseline: the
-reference's own x86-64 path (oracle/_ref, built from /root/reference) on a bounded sample.
+residuals M*N*4) / step time, in GB/s. roofline: the dominant kernel (the fused gate/up GEMV,
+launched exactly as in the step), each launch bracketed by HIP events on its stream, against
+MI355X HBM peak 8 TB/s. extras: BASELINE.json configs 3-5 (Qwen3-8B decode GEMVs, prefill GEMM,
+MoE FFN). cpu_baseline: the reference's own x86-64 path (oracle/_ref, built from
+/root/reference) on a bounded sample.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--m 1] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--m 1] [--no-cpu] [--no-extras]
+    python bench.py --calibrate-copy      (512 MiB copy for PMC byte-counter scaling)
 """
 import argparse
 import json
@@ -32,6 +37,24 @@ import synth  # noqa: E402
 METRIC = "q4 GEMV µs/call + HBM GB/s (% peak); prefill GEMM int8 TOPS (% peak)"
 HBM_PEAK_GBS = 8000.0
 CFG = synth.QWEN3VL_2B
+
+
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "pmc_hbm_traffic_gemv_qwen3vl2b_m1.md")
+
+
+def profiled_traffic(m):
+    """HBM bytes per launch of the dominant kernel at M = 1, from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE summary (copy-calibrated); None for other M or without it."""
+    if m != 1:
+        return None
+    try:
+        with open(TRAFFIC_PROFILE) as fh:
+            for line in fh:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
 
 
 def layer_mats():
@@ -69,7 +92,6 @@ def run_gpu(args):
 
     kq4.init(0)
     torch.cuda.set_device(0)
-    stream = torch.cuda.current_stream()
     m = args.m
     s = layer_mats()
     h, q, kv, f = CFG["hidden"], s["q"][0], s["k"][0], CFG["ffn"]
@@ -82,47 +104,76 @@ def run_gpu(args):
     oq, ok_, ov, oo, og, ou, od = dev((m, q)), dev((m, kv)), dev((m, kv)), dev((m, h)), \
         dev((m, f)), dev((m, f)), dev((m, h))
 
-    def step():
-        for L in layers:
-            kq4.matmul_multi_dev([oq, ok_, ov], x, [L["q"], L["k"], L["v"]], [q, kv, kv], h,
-                                 stream=stream)
-            kq4.matmul_dev(oo, attn, L["o"], h, q, residual=resid, stream=stream)
-            kq4.matmul_multi_dev([og, ou], x, [L["gate"], L["up"]], [f, f], h, stream=stream)
-            kq4.matmul_dev(od, act, L["down"], h, f, residual=resid, stream=stream)
+    def layer_ops(L, st):
+        kq4.matmul_multi_dev([oq, ok_, ov], x, [L["q"], L["k"], L["v"]], [q, kv, kv], h,
+                             stream=st)
+        kq4.matmul_dev(oo, attn, L["o"], h, q, residual=resid, stream=st)
+        kq4.matmul_multi_dev([og, ou], x, [L["gate"], L["up"]], [f, f], h, stream=st)
+        kq4.matmul_dev(od, act, L["down"], h, f, residual=resid, stream=st)
 
+    def step():
+        st = torch.cuda.current_stream()
+        for L in layers:
+            layer_ops(L, st)
+
+    def timed(fn, k):
+        torch.cuda.synchronize()
+        st = torch.cuda.current_stream()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(st)
+        for _ in range(k):
+            fn()
+        e1.record(st)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / k
+
+    # eager: one host launch per op (4 per layer)
     for _ in range(args.warmup):
         step()
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    for _ in range(args.steps):
-        step()
-    e1.record(stream)
-    torch.cuda.synchronize()
-    ms_step = e0.elapsed_time(e1) / args.steps
-    total_bytes = step_bytes(m) * CFG["layers"]
-    value = total_bytes / (ms_step * 1e-3) / 1e9
+    ms_eager = timed(step, args.steps)
 
-    # dominant kernel alone: fused gate/up GEMV from pre-quantized activations, rotating layers
-    xq = torch.empty((m, h), dtype=torch.int8, device="cuda")
-    xd = dev((m, h // 32))
-    kq4.quantize_dev(x, xq, xd, stream=stream)
-    reps = max(args.steps, 20)
-    for L in layers[:4]:
-        kq4.matmul_multi_q_dev([og, ou], xq, xd, [L["gate"], L["up"]], [f, f], h, m,
-                               stream=stream)
-    torch.cuda.synchronize()
-    e0.record(stream)
+    # the same step captured once as a HIP graph and replayed (how a decode loop runs it)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    for _ in range(args.warmup):
+        graph.replay()
+    ms_graph = timed(graph.replay, args.steps)
+    total_bytes = step_bytes(m) * CFG["layers"]
+
+    # dominant kernel: the fused gate/up GEMV launch exactly as the step issues it, each launch
+    # bracketed by HIP events on the stream it runs on, rotating over the 28 layers' weights
+    st = torch.cuda.current_stream()
+    reps = max(2 * CFG["layers"], args.steps)
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(reps)]
     for i in range(reps):
         L = layers[i % len(layers)]
-        kq4.matmul_multi_q_dev([og, ou], xq, xd, [L["gate"], L["up"]], [f, f], h, m,
-                               stream=stream)
-    e1.record(stream)
+        ev[i][0].record(st)
+        kq4.matmul_multi_dev([og, ou], x, [L["gate"], L["up"]], [f, f], h, stream=st)
+        ev[i][1].record(st)
     torch.cuda.synchronize()
-    us_launch = e0.elapsed_time(e1) * 1e3 / reps
+    us_launch = sum(a.elapsed_time(b) for a, b in ev) * 1e3 / reps
     achieved = gate_up_bytes(m) / (us_launch * 1e-6) / 1e9
-    return dict(ms_per_step=ms_step, value=value, us_gate_up=us_launch, achieved=achieved,
-                total_bytes=total_bytes)
+    return dict(ms_per_step=ms_graph, ms_eager=ms_eager,
+                value=total_bytes / (ms_graph * 1e-3) / 1e9,
+                value_eager=total_bytes / (ms_eager * 1e-3) / 1e9,
+                us_gate_up=us_launch, achieved=achieved, total_bytes=total_bytes)
+
+
+def copy_calibration(mib=512, reps=10):
+    """A plain device-to-device copy of known size, for scaling rocprofv3 FETCH_SIZE /
+    WRITE_SIZE counters to bytes (run under --pmc; its kernel reads and writes exactly
+    `mib` MiB per launch)."""
+    import torch
+
+    n = mib * (1 << 20) // 4
+    a = torch.ones(n, dtype=torch.float32, device="cuda")
+    b = torch.empty_like(a)
+    for _ in range(reps):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    return dict(copy_mib=mib, reps=reps)
 
 
 def _time_loop(torch, stream, fn, reps, warm=3):
@@ -287,12 +338,17 @@ def main():
     ap.add_argument("--no-extras", action="store_true",
                     help="skip the config 3-5 sub-results (8B decode, prefill GEMM, MoE)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run a 512 MiB device copy (PMC byte-counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
               "(the path would shard along weight rows / experts, see DESIGN.md)",
               file=sys.stderr)
         sys.exit(2)
+    if args.calibrate_copy:
+        print(json.dumps(copy_calibration()))
+        return
     g = run_gpu(args)
     line = {
         "metric": METRIC,
@@ -302,6 +358,7 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(g["ms_per_step"], 4),
+        "eager": {"ms_per_step": round(g["ms_eager"], 4), "value": round(g["value_eager"], 2)},
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -310,11 +367,12 @@ def main():
         "config": {"workload": f"qwen3-vl-2b decode-step linear set (QKV, O+res, gate/up, "
                                f"down+res) x {CFG['layers']} layers, M={args.m}",
                    "global_batch": args.m, "bytes_per_step": g["total_bytes"],
+                   "launch": "one HIP graph replay per step (4 launches per layer)",
                    "weights": "q4_0 4x4 tiles, int8 block-32 activations"},
         "gate_up_us_per_call": round(g["us_gate_up"], 3),
         "roofline": {"bound": "hbm", "achieved": round(g["achieved"], 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(g["achieved"] / HBM_PEAK_GBS, 4),
-                     "traffic": None,
+                     "traffic": profiled_traffic(args.m),
                      "kernel": "kq4_gemv_kernel (fused gate/up, 2 x 6144x2048)"},
     }
     if not args.no_extras:
