@@ -183,16 +183,27 @@ def _time_loop(torch, stream, fn, reps, warm=3):
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record(stream)
     for i in range(reps):
-        fn(i)
+        fn(warm + i)
     e1.record(stream)
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) * 1e3 / reps   # us per call
 
 
+ROTATE_BYTES = 640e6   # distinct weight bytes each measured op cycles through (> 256 MB MALL)
+
+
+def _copies(torch, arr):
+    """arr on the device, cloned until the copies exceed ROTATE_BYTES."""
+    t = torch.from_numpy(arr.reshape(-1)).cuda()
+    n = max(2, int(ROTATE_BYTES // t.numel()) + 1)
+    return [t] + [t.clone() for _ in range(n - 1)]
+
+
 def run_extras(reps=20):
     """BASELINE.json configs 3-5 (reported beside the headline line, each on its own):
     Qwen3-8B decode GEMVs at M in {1,2,4,8} (us/call, GB/s), prefill GEMM at M in {512, 2048}
-    (int8 TOPS vs 5.0 POPS dense), Qwen3-30B-A3B MoE FFN at T in {1, 64}."""
+    (int8 TOPS vs 5.0 POPS dense), Qwen3-30B-A3B MoE FFN at T in {1, 64}. Every measured op
+    cycles through > 640 MB of distinct weight copies, so its weights stream from HBM."""
     import torch
 
     import kq4
@@ -201,13 +212,10 @@ def run_extras(reps=20):
     cfg = synth.QWEN3_8B
     h, f = cfg["hidden"], cfg["ffn"]
     qkv = (cfg["q_heads"] + 2 * cfg["kv_heads"]) * cfg["head_dim"]
-    n_copies = 6                                       # 6 x 99 MB > 256 MB Infinity Cache
-    base = {"gate": synth.make_q4_weights(f, h, 11, **synth.SCALE_8B),
-            "up": synth.make_q4_weights(f, h, 12, **synth.SCALE_8B),
-            "down": synth.make_q4_weights(h, f, 13, **synth.SCALE_8B),
-            "qkv": synth.make_q4_weights(qkv, h, 14, **synth.SCALE_8B)}
-    d0 = {k: torch.from_numpy(v.reshape(-1)).cuda() for k, v in base.items()}
-    copies = [{k: v.clone() for k, v in d0.items()} for _ in range(n_copies)]
+    G = _copies(torch, synth.make_q4_weights(f, h, 11, **synth.SCALE_8B))
+    U = [g.clone() for g in G]
+    D = _copies(torch, synth.make_q4_weights(h, f, 13, **synth.SCALE_8B))
+    Q = _copies(torch, synth.make_q4_weights(qkv, h, 14, **synth.SCALE_8B))
     out = {}
     dec = {}
     for m in (1, 2, 4, 8):
@@ -216,12 +224,11 @@ def run_extras(reps=20):
         og, ou = torch.empty((m, f), device="cuda"), torch.empty((m, f), device="cuda")
         od, oq = torch.empty((m, h), device="cuda"), torch.empty((m, qkv), device="cuda")
         t_gu = _time_loop(torch, stream, lambda i: kq4.matmul_multi_dev(
-            [og, ou], x, [copies[i % n_copies]["gate"], copies[i % n_copies]["up"]], [f, f], h,
-            stream=stream), reps)
+            [og, ou], x, [G[i % len(G)], U[i % len(U)]], [f, f], h, stream=stream), reps)
         t_dn = _time_loop(torch, stream, lambda i: kq4.matmul_dev(
-            od, xf, copies[i % n_copies]["down"], h, f, stream=stream), reps)
+            od, xf, D[i % len(D)], h, f, stream=stream), reps)
         t_q = _time_loop(torch, stream, lambda i: kq4.matmul_dev(
-            oq, x, copies[i % n_copies]["qkv"], qkv, h, stream=stream), reps)
+            oq, x, Q[i % len(Q)], qkv, h, stream=stream), reps)
         b_gu = 2 * f * h * 18 // 32 + m * h * 4 + 2 * m * f * 4
         b_dn = h * f * 18 // 32 + m * f * 4 + m * h * 4
         b_q = qkv * h * 18 // 32 + m * h * 4 + m * qkv * 4
@@ -238,21 +245,19 @@ def run_extras(reps=20):
         od = torch.empty((m, h), device="cuda")
         r = max(3, reps // 4)
         t_g = _time_loop(torch, stream, lambda i: kq4.matmul_dev(
-            og, x, copies[i % 2]["gate"], f, h, stream=stream), r, warm=1)
+            og, x, G[i % len(G)], f, h, stream=stream), r, warm=1)
         t_d = _time_loop(torch, stream, lambda i: kq4.matmul_dev(
-            od, xf, copies[i % 2]["down"], h, f, stream=stream), r, warm=1)
+            od, xf, D[i % len(D)], h, f, stream=stream), r, warm=1)
         ops = 2.0 * m * f * h
         pre[f"M{m}"] = {"gate_us": round(t_g, 1), "gate_TOPS": round(ops / t_g / 1e6, 1),
                         "down_us": round(t_d, 1), "down_TOPS": round(ops / t_d / 1e6, 1),
                         "frac_int8_peak": round(ops / min(t_g, t_d) / 1e6 / 5000.0, 4)}
     out["qwen3_8b_prefill"] = pre
-    del copies, d0
+    del G, U, D, Q
     mcfg = synth.QWEN3_30B_A3B_MOE
     d, ne, tk, ef = mcfg["hidden"], mcfg["experts"], mcfg["top_k"], mcfg["ef"]
-    layers = []
-    for c in range(2):
-        G, U, D = synth.make_moe(mcfg, 50 + 3 * c)
-        layers.append([torch.from_numpy(a.reshape(-1)).cuda() for a in (G, U, D)])
+    Gm, Um, Dm = synth.make_moe(mcfg, 50)
+    layers = list(zip(_copies(torch, Gm), _copies(torch, Um), _copies(torch, Dm)))
     moe = {}
     for T in (1, 64):
         X = torch.from_numpy(synth.make_activations(T, d, 60)).cuda()
@@ -262,7 +267,7 @@ def run_extras(reps=20):
         Y = torch.empty((T, d), device="cuda")
         kq4.moe_route_dev(sel, pr, lg, tk, stream=stream)
         t = _time_loop(torch, stream, lambda i: kq4.moe_ffn_dev(
-            Y, X, sel, pr, *layers[i % 2], ne, d, ef, stream=stream), reps)
+            Y, X, sel, pr, *layers[i % len(layers)], ne, d, ef, stream=stream), reps)
         n_exp = len(set(sel.cpu().numpy().reshape(-1).tolist()))
         byts = n_exp * 3 * ef * d * 18 // 32 + T * d * 8
         moe[f"T{T}"] = {"us": round(t, 2), "experts": n_exp, "GBs": round(byts / t / 1e3, 1)}

@@ -44,7 +44,8 @@ const int kMaxDev = 16;
 
 struct DevState {
   bool ready = false;
-  Buf ws;    // quantized activations, split-K partials, MoE staging
+  int ncu = 256;        // compute units (sizes the GEMV grid)
+  Buf ws;    // quantized activations, MoE staging
   Buf hx, hres, hout, hw, hsel, hpr;   // staging for the host-pointer API
   std::unordered_map<uint64_t, WEntry> wcache;
 };
@@ -96,17 +97,9 @@ struct Carve {   // bump allocator over a workspace
 
 bool shape_ok(int rows, int cols) { return rows > 0 && rows % 4 == 0 && cols > 0 && cols % 32 == 0; }
 
-// Token counts up to this quantize their activations inside the GEMV (no separate launch).
-// KQ4_FUSED_QUANT_MAX_M (0..4) overrides it, e.g. to compare both paths.
-int fused_quant_max_m() {
-  static int v = -1;
-  if (v < 0) {
-    const char *e = getenv("KQ4_FUSED_QUANT_MAX_M");
-    v = e ? atoi(e) : KQ4_GEMV_FQ_MAX_M;
-    if (v < 0) v = 0;
-    if (v > KQ4_GEMV_FQ_MAX_M) v = KQ4_GEMV_FQ_MAX_M;
-  }
-  return v;
+int env_int(const char *name, int dflt) {
+  const char *e = getenv(name);
+  return e ? atoi(e) : dflt;
 }
 
 int asm_tokens_for(int chain, int n) {
@@ -115,24 +108,83 @@ int asm_tokens_for(int chain, int n) {
   return 0;
 }
 
-// GEMV over n_mats matrices for n tokens (n <= 8) from token-major xq/xd.
-// xf != nullptr: the kernel quantizes the fp32 activations itself (one launch per op).
-int run_gemv(int n_mats, float *const *out, const float *const *res, const uint8_t *const *w,
-             const int *rows, int cols, const float *xf, const int8_t *xq, const float *xd,
-             int n, int asm_tokens, hipStream_t s) {
+// Waves per GEMV workgroup (one workgroup per 32-row set, waves splitting K in 16-block
+// stages): enough waves in total to keep about 16 per CU streaming, balanced so that no wave
+// has more stages than another by more than one, within the LDS each wave's slab needs.
+// KQ4_GEMV_WAVES overrides it (for measurement).
+// Integer-dot kind of the GEMV: per-lane v_dot4 for few tokens (fewest instructions per byte),
+// v_mfma from the token count where the dot4 work (which grows with M) costs more; the dot4 kind
+// uses 16-row sets when 32-row sets would leave CUs without a workgroup.
+// KQ4_GEMV_KIND=0/1/2 forces one (for measurement).
+int gemv_kind(int n, int rows32, int ncu) {
+  static const int env = env_int("KQ4_GEMV_KIND", -1);
+  static const int mfma_from = env_int("KQ4_GEMV_MFMA_FROM", 3);
+  if (env >= 0) return env;
+  if (n >= mfma_from) return 1;
+  return rows32 < 2 * ncu ? 2 : 0;
+}
+
+// Waves per GEMV workgroup (one workgroup per row set, waves splitting K in stages of 128/G8
+// blocks): enough waves in total to keep about KQ4_GEMV_WPCU (16) per CU streaming, balanced so
+// that no wave has more stages than another by more than one, within the LDS each wave's slab
+// needs. KQ4_GEMV_WAVES overrides it (for measurement).
+int plan_gemv_waves(int rowsets, int nb, int n, int kind, int ncu) {
+  static const int force = env_int("KQ4_GEMV_WAVES", 0);
+  static const int per_cu = env_int("KQ4_GEMV_WPCU", 16);
+  const int cb = kind == 2 ? 32 : 16;
+  const int nst = (nb + cb - 1) / cb;
+  const int lds_max = (160 * 1024) / kq4_gemv_slab_bytes(n, kind);
+  int cap = nst < 8 ? nst : 8;
+  cap = cap < lds_max ? cap : lds_max;
+  int want = force > 0 ? force : (per_cu * ncu + rowsets - 1) / rowsets;
+  want = want < 1 ? 1 : (want > cap ? cap : want);
+  const int spw = (nst + want - 1) / want;   // stages per wave
+  return (nst + spw - 1) / spw;
+}
+
+// Whether the GEMV quantizes its fp32 activations itself (one launch per op) or reads them from
+// a separate quantize launch. Every wave quantizes its own stages, so the in-kernel path repeats
+// the work once per row set; it is used up to KQ4_GEMV_FQ_MAX_M tokens, where that costs less
+// than a second launch. KQ4_GEMV_FQ=0 turns it off (for measurement).
+bool gemv_fq(int n) {
+  static const int env = env_int("KQ4_GEMV_FQ", -1);
+  static const int max_m = env_int("KQ4_GEMV_FQ_M", KQ4_GEMV_FQ_MAX_M);
+  return env != 0 && n <= max_m && n <= KQ4_GEMV_FQ_MAX_M;
+}
+
+// GEMV over n_mats matrices for n tokens (n <= 8): from fp32 x (quantized in the kernel or by a
+// separate launch) or from token-major xq/xd.
+int run_gemv(DevState *ds, int n_mats, float *const *out, const float *const *res,
+             const uint8_t *const *w, const int *rows, int cols, const float *x,
+             const int8_t *xq, const float *xd, int n, int asm_tokens, hipStream_t s) {
   const int nb = cols / 32;
-  const int ppl = (!xf && nb > 32 * KQ4_GEMV_MAXW) ? 2 : 1;   // tile pairs per lane per chunk
-  const int chunks = (nb + 32 * ppl - 1) / (32 * ppl);
+  int rc;
   KQ4GemvArgs a;
   memset(&a, 0, sizeof(a));
+  if (x) {
+    if (gemv_fq(n)) {
+      a.xf = x;
+    } else {
+      if ((rc = ensure(ds->ws, al256((size_t)n * cols) + al256((size_t)n * nb * sizeof(float)))))
+        return rc;
+      Carve cv{static_cast<char *>(ds->ws.p)};
+      int8_t *q = cv.take<int8_t>((size_t)n * cols);
+      float *d = cv.take<float>((size_t)n * nb);
+      KQ4_HIP((hipError_t)kq4_launch_quantize(x, q, d, nullptr, n, cols, 0, s, 0));
+      xq = q;
+      xd = d;
+    }
+  }
   a.nmat = n_mats;
-  a.xf = xf;
   a.xq = xq;
   a.xd = xd;
   a.asm_tokens = asm_tokens;
   a.cols = cols;
   a.nb = nb;
-  a.nwave = chunks < KQ4_GEMV_MAXW ? chunks : KQ4_GEMV_MAXW;
+  int rows32 = 0;
+  for (int i = 0; i < n_mats; ++i) rows32 += (rows[i] + 31) / 32;
+  const int kind = gemv_kind(n, rows32, ds->ncu);
+  const int rsz = kq4_gemv_rowset(kind);
   int wg = 0;
   for (int i = 0; i < n_mats; ++i) {
     KQ4GemvMat &m = a.mat[i];
@@ -141,9 +193,13 @@ int run_gemv(int n_mats, float *const *out, const float *const *res, const uint8
     m.res = res ? res[i] : nullptr;
     m.rows = rows[i];
     m.wg_begin = wg;
-    wg += (rows[i] + 15) / 16;
+    wg += (rows[i] + rsz - 1) / rsz;
   }
-  KQ4_HIP((hipError_t)kq4_launch_gemv(a, n, ppl, wg, s));
+  const int nw = plan_gemv_waves(wg, nb, n, kind, ds->ncu);
+  static const int depth_env = env_int("KQ4_GEMV_DEPTH", 0);
+  const int nst = (nb + (kind == 2 ? 32 : 16) - 1) / (kind == 2 ? 32 : 16);
+  const int depth = depth_env ? depth_env : (nst > nw ? 2 : 1);   // two stages in flight if a wave has two
+  KQ4_HIP((hipError_t)kq4_launch_gemv(a, n, kind, nw, depth, wg, s));
   return KQ4_OK;
 }
 
@@ -165,24 +221,9 @@ int matmul_impl(int n_mats, float *const *out, const float *const *res, const ui
   const int nb = cols / 32;
   const size_t qbytes = al256((size_t)n * cols) + al256((size_t)n * nb * sizeof(float));
 
-  if (n <= KQ4_GEMV_MAX_M) {
-    if (x && n <= fused_quant_max_m())   // quantize inside the GEMV: one launch per op
-      return run_gemv(n_mats, out, res, w, rows, cols, x, nullptr, nullptr, n,
-                      asm_tokens_for(chain, n), s);
-    const int8_t *xq = xq_in;
-    const float *xd = xd_in;
-    if (x) {
-      if ((rc = ensure(ds->ws, qbytes))) return rc;
-      Carve cv{static_cast<char *>(ds->ws.p)};
-      int8_t *q = cv.take<int8_t>((size_t)n * cols);
-      float *d = cv.take<float>((size_t)n * nb);
-      KQ4_HIP((hipError_t)kq4_launch_quantize(x, q, d, nullptr, n, cols, 0, s, 0));
-      xq = q;
-      xd = d;
-    }
-    return run_gemv(n_mats, out, res, w, rows, cols, nullptr, xq, xd, n,
+  if (n <= KQ4_GEMV_MAX_M)
+    return run_gemv(ds, n_mats, out, res, w, rows, cols, x, xq_in, xd_in, n,
                     asm_tokens_for(chain, n), s);
-  }
 
   // prefill: int8-MFMA GEMM on the main segment, GEMV on the 1..3-token CTILE tail (AUTO)
   const int main_n = chain == KQ4_CHAIN_AUTO ? (n & ~3) : n;
@@ -223,7 +264,7 @@ int matmul_impl(int n_mats, float *const *out, const float *const *res, const ui
       o2[i] = out[i] + (size_t)main_n * rows[i];
       r2[i] = (res && res[i]) ? res[i] + (size_t)main_n * rows[i] : nullptr;
     }
-    return run_gemv(n_mats, o2, r2, w, rows, cols, nullptr, xq_t, xd_t, tail, 0, s);
+    return run_gemv(ds, n_mats, o2, r2, w, rows, cols, nullptr, xq_t, xd_t, tail, 0, s);
   }
   return KQ4_OK;
 }
@@ -331,7 +372,9 @@ int kq4_init(int device) {
     return fail(KQ4_ENODEV, "device %d is %s; libkq4 is built for gfx950", device,
                 prop.gcnArchName);
   std::lock_guard<std::mutex> lk(g_mu);
-  g_dev[device].ready = true;
+  DevState &ds = g_dev[device];
+  ds.ncu = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
+  ds.ready = true;
   return KQ4_OK;
 }
 

@@ -6,7 +6,6 @@
 
 #define KQ4_GEMV_MAX_M 8
 #define KQ4_MAXMAT 4
-#define KQ4_GEMV_MAXW 8
 #define KQ4_GEMV_FQ_MAX_M 4   // largest token count the GEMV quantizes in-kernel
 
 // One weight matrix of a (possibly fused) GEMV launch. All matrices share the activation.
@@ -15,7 +14,7 @@ struct KQ4GemvMat {
   float *out;           // [M][rows]
   const float *res;     // [M][rows] or nullptr
   int rows;
-  int wg_begin;         // first workgroup (16-row slab) of this matrix in the launch
+  int wg_begin;         // first workgroup (32-row set) of this matrix in the launch
 };
 
 struct KQ4GemvArgs {
@@ -27,16 +26,20 @@ struct KQ4GemvArgs {
   int asm_tokens;       // tokens [0, asm_tokens) multiply by f32(f16_rne(xd)) (ASM chain)
   int cols;
   int nb;
-  int nwave;            // waves per workgroup (K split), 1..KQ4_GEMV_MAXW
 };
 
 int kq4_launch_quantize(const float *x, int8_t *xq, float *xd, float *xde, int n_batch, int cols,
                         int asm_tokens, hipStream_t stream, int block_major = 0);
 
-// n_batch in [1, KQ4_GEMV_MAX_M]; ppl = tile pairs per lane per K chunk (1 or 2);
-// total_wg = total 16-row slabs of all matrices.
-int kq4_launch_gemv(const KQ4GemvArgs &args, int n_batch, int ppl, int total_wg,
-                    hipStream_t stream);
+// n_batch in [1, KQ4_GEMV_MAX_M]; one workgroup per row set of kq4_gemv_rowset(kind) rows
+// (total_wg over all matrices), nw waves (1..8) splitting K, each with `depth` (1 or 2) stages in
+// flight; kind 0 = per-lane v_dot4 dots on 32-row sets, 1 = v_mfma dots on 32-row sets, 2 =
+// v_dot4 on 16-row sets; nw * kq4_gemv_slab_bytes(n_batch, kind) must fit 160 KB of LDS.
+// args.xf (in-kernel quantization) requires n_batch <= KQ4_GEMV_FQ_MAX_M.
+int kq4_launch_gemv(const KQ4GemvArgs &args, int n_batch, int kind, int nw, int depth,
+                    int total_wg, hipStream_t stream);
+int kq4_gemv_slab_bytes(int n_batch, int kind);
+int kq4_gemv_rowset(int kind);
 
 int kq4_launch_block_sums(int32_t *s_lo, int32_t *s_hi, const int8_t *xq, const uint8_t *w,
                           int rows, int cols, int n_batch, hipStream_t stream);
