@@ -78,10 +78,14 @@ def gate_up_bytes(m):
 
 
 def make_model(torch, n_layers, seed=1):
-    """One layer of seeded weights, copied to n_layers distinct HBM buffers."""
+    """One layer of seeded weights (device copies in the stream layout), copied to n_layers
+    distinct HBM buffers."""
+    import kq4
+    mats = layer_mats()
     base = {name: synth.make_q4_weights(r, c, seed + i, **synth.SCALE_2B)
-            for i, (name, (r, c)) in enumerate(layer_mats().items())}
-    dev0 = {k: torch.from_numpy(v.reshape(-1)).cuda() for k, v in base.items()}
+            for i, (name, (r, c)) in enumerate(mats.items())}
+    dev0 = {k: kq4.prepare_dev(torch.from_numpy(v.reshape(-1)).cuda(), *mats[k])
+            for k, v in base.items()}
     return [{k: v.clone() for k, v in dev0.items()} for _ in range(n_layers)], base
 
 
@@ -176,7 +180,11 @@ def copy_calibration(mib=512, reps=10):
     return dict(copy_mib=mib, reps=reps)
 
 
-def _time_loop(torch, stream, fn, reps, warm=3):
+def _time_loop(torch, stream, fn, reps, warm=None, cycle=None):
+    """Average us per call of fn(i) over reps calls, after a warm-up that calls every rotated
+    copy (cycle = their number) at least once."""
+    if warm is None:
+        warm = max(3, cycle or 0)
     for i in range(warm):
         fn(i)
     torch.cuda.synchronize()
@@ -192,9 +200,11 @@ def _time_loop(torch, stream, fn, reps, warm=3):
 ROTATE_BYTES = 640e6   # distinct weight bytes each measured op cycles through (> 256 MB MALL)
 
 
-def _copies(torch, arr):
-    """arr on the device, cloned until the copies exceed ROTATE_BYTES."""
-    t = torch.from_numpy(arr.reshape(-1)).cuda()
+def _copies(torch, arr, rows, cols):
+    """The device (stream-layout) copy of the q4 matrix arr, cloned until the copies exceed
+    ROTATE_BYTES."""
+    import kq4
+    t = kq4.prepare_dev(torch.from_numpy(arr.reshape(-1)).cuda(), rows, cols)
     n = max(2, int(ROTATE_BYTES // t.numel()) + 1)
     return [t] + [t.clone() for _ in range(n - 1)]
 
@@ -212,10 +222,10 @@ def run_extras(reps=20):
     cfg = synth.QWEN3_8B
     h, f = cfg["hidden"], cfg["ffn"]
     qkv = (cfg["q_heads"] + 2 * cfg["kv_heads"]) * cfg["head_dim"]
-    G = _copies(torch, synth.make_q4_weights(f, h, 11, **synth.SCALE_8B))
+    G = _copies(torch, synth.make_q4_weights(f, h, 11, **synth.SCALE_8B), f, h)
     U = [g.clone() for g in G]
-    D = _copies(torch, synth.make_q4_weights(h, f, 13, **synth.SCALE_8B))
-    Q = _copies(torch, synth.make_q4_weights(qkv, h, 14, **synth.SCALE_8B))
+    D = _copies(torch, synth.make_q4_weights(h, f, 13, **synth.SCALE_8B), h, f)
+    Q = _copies(torch, synth.make_q4_weights(qkv, h, 14, **synth.SCALE_8B), qkv, h)
     out = {}
     dec = {}
     for m in (1, 2, 4, 8):
@@ -224,11 +234,12 @@ def run_extras(reps=20):
         og, ou = torch.empty((m, f), device="cuda"), torch.empty((m, f), device="cuda")
         od, oq = torch.empty((m, h), device="cuda"), torch.empty((m, qkv), device="cuda")
         t_gu = _time_loop(torch, stream, lambda i: kq4.matmul_multi_dev(
-            [og, ou], x, [G[i % len(G)], U[i % len(U)]], [f, f], h, stream=stream), reps)
+            [og, ou], x, [G[i % len(G)], U[i % len(U)]], [f, f], h, stream=stream), reps,
+            cycle=len(G))
         t_dn = _time_loop(torch, stream, lambda i: kq4.matmul_dev(
-            od, xf, D[i % len(D)], h, f, stream=stream), reps)
+            od, xf, D[i % len(D)], h, f, stream=stream), reps, cycle=len(D))
         t_q = _time_loop(torch, stream, lambda i: kq4.matmul_dev(
-            oq, x, Q[i % len(Q)], qkv, h, stream=stream), reps)
+            oq, x, Q[i % len(Q)], qkv, h, stream=stream), reps, cycle=len(Q))
         b_gu = 2 * f * h * 18 // 32 + m * h * 4 + 2 * m * f * 4
         b_dn = h * f * 18 // 32 + m * f * 4 + m * h * 4
         b_q = qkv * h * 18 // 32 + m * h * 4 + m * qkv * 4
@@ -257,7 +268,8 @@ def run_extras(reps=20):
     mcfg = synth.QWEN3_30B_A3B_MOE
     d, ne, tk, ef = mcfg["hidden"], mcfg["experts"], mcfg["top_k"], mcfg["ef"]
     Gm, Um, Dm = synth.make_moe(mcfg, 50)
-    layers = list(zip(_copies(torch, Gm), _copies(torch, Um), _copies(torch, Dm)))
+    layers = list(zip(_copies(torch, Gm, ne * ef, d), _copies(torch, Um, ne * ef, d),
+                      _copies(torch, Dm, d, ne * ef)))
     moe = {}
     for T in (1, 64):
         X = torch.from_numpy(synth.make_activations(T, d, 60)).cuda()

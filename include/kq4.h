@@ -14,7 +14,12 @@
  *   weights   VQF 4x4 tiles: [rows/4 groups][cols/32 blocks] x 72 B; a tile holds 4 f16 row
  *             scales then 64 nibble bytes, byte 8+16k+4r+i = legacy qs byte 4k+i of row r,
  *             XOR 0x88 (vqf_convert/src/qk_repack.c:19-46, VQF_FLAG_Q4_4X4
- *             include/model/vqf_format.h:32)
+ *             include/model/vqf_format.h:32). The host-pointer API takes them as stored. The
+ *             device-pointer API takes the device copy kq4_weights_prepare_dev makes of them
+ *             once (the "stream layout": the same tiles, regrouped so the GEMV reads each
+ *             kernel lane's tiles with full-width coalesced loads), as the reference's NPU path
+ *             converts weights once into its device cache (st_npu_gw_build
+ *             vllm_safetensors.c:2790-3040).
  *   x / out   fp32 token-major [n_batch][cols] / [n_batch][rows]
  *   residual  fp32 [n_batch][rows]; out = residual + W.x (fused O / down projections)
  * Preconditions (as the reference's 4x4 path): rows % 4 == 0, cols % 32 == 0.
@@ -100,6 +105,20 @@ int kq4_moe_ffn(float *Y, const float *X, const int *sel, const float *pr, int T
 
 /* ---- device-pointer API (stream-ordered, asynchronous) ----------------------------------- */
 
+/* Size in bytes of the stream-layout copy of a rows x cols q4 matrix (0 for a bad shape):
+ * 9216 B per (32-row set, 16-block stage), rows rounded up to 32, blocks up to 16. */
+size_t kq4_weights_stream_bytes(int rows, int cols);
+
+/* Writes the stream-layout copy of the VQF 4x4 matrix w4x4 (device memory, as stored) to dst
+ * (device memory, 16-byte aligned, kq4_weights_stream_bytes(rows, cols) bytes; w4x4 8-byte
+ * aligned). Stacked
+ * matrices of equal shape can be prepared as one matrix of their summed rows when rows % 32 == 0
+ * (MoE G/U: ne*ef rows). Replaces the upload/convert step of the NPU weight cache
+ * (st_npu_gw_build vllm_safetensors.c:2790-3040). Every `w` / `G` / `U` / `D` of the calls
+ * below is such a copy. */
+int kq4_weights_prepare_dev(uint8_t *dst, const uint8_t *w4x4, int rows, int cols,
+                            void *stream);
+
 /* Activation quantizer (quantize_row_q8_0_act vllm_safetensors.c:7893-7920) for n_batch rows:
  * xq int8 [n_batch][cols], xd f32 [n_batch][cols/32]. xde (may be NULL) receives the scale
  * each token's chain multiplies by: f32(f16_rne(xd)) for ASM-chain tokens, xd otherwise. */
@@ -137,7 +156,8 @@ int kq4_block_sums_dev(int32_t *s_lo, int32_t *s_hi, const int8_t *xq, const uin
 int kq4_moe_route_dev(int *sel, float *pr, const float *logits, int T, int ne, int tk,
                       void *stream);
 
-/* MoE FFN on device buffers (see kq4_moe_ffn). */
+/* MoE FFN on device buffers (see kq4_moe_ffn); G and U prepared as [ne*ef rows][d cols], D as
+ * [d rows][ne*ef cols]. */
 int kq4_moe_ffn_dev(float *Y, const float *X, const int *sel, const float *pr, int T, int tk,
                     const uint8_t *G, const uint8_t *U, const uint8_t *D, int ne, int d, int ef,
                     void *stream);

@@ -46,7 +46,7 @@ struct DevState {
   bool ready = false;
   int ncu = 256;        // compute units (sizes the GEMV grid)
   Buf ws;    // quantized activations, MoE staging
-  Buf hx, hres, hout, hw, hsel, hpr;   // staging for the host-pointer API
+  Buf hx, hres, hout, hw, hsel, hpr, hstage;   // staging for the host-pointer API
   std::unordered_map<uint64_t, WEntry> wcache;
 };
 
@@ -108,38 +108,35 @@ int asm_tokens_for(int chain, int n) {
   return 0;
 }
 
-// Waves per GEMV workgroup (one workgroup per 32-row set, waves splitting K in 16-block
-// stages): enough waves in total to keep about 16 per CU streaming, balanced so that no wave
-// has more stages than another by more than one, within the LDS each wave's slab needs.
-// KQ4_GEMV_WAVES overrides it (for measurement).
 // Integer-dot kind of the GEMV: per-lane v_dot4 for few tokens (fewest instructions per byte),
-// v_mfma from the token count where the dot4 work (which grows with M) costs more; the dot4 kind
-// uses 16-row sets when 32-row sets would leave CUs without a workgroup.
-// KQ4_GEMV_KIND=0/1/2 forces one (for measurement).
-int gemv_kind(int n, int rows32, int ncu) {
+// v_mfma from the token count where the dot4 work (which grows with M) costs more.
+// KQ4_GEMV_KIND=0/1 forces one (for measurement).
+int gemv_kind(int n) {
   static const int env = env_int("KQ4_GEMV_KIND", -1);
-  static const int mfma_from = env_int("KQ4_GEMV_MFMA_FROM", 3);
-  if (env >= 0) return env;
-  if (n >= mfma_from) return 1;
-  return rows32 < 2 * ncu ? 2 : 0;
+  static const int mfma_from = env_int("KQ4_GEMV_MFMA_FROM", 2);
+  if (env == 0 || env == 1) return env;
+  return n >= mfma_from ? 1 : 0;
 }
 
-// Waves per GEMV workgroup (one workgroup per row set, waves splitting K in stages of 128/G8
-// blocks): enough waves in total to keep about KQ4_GEMV_WPCU (16) per CU streaming, balanced so
-// that no wave has more stages than another by more than one, within the LDS each wave's slab
-// needs. KQ4_GEMV_WAVES overrides it (for measurement).
-int plan_gemv_waves(int rowsets, int nb, int n, int kind, int ncu) {
-  static const int force = env_int("KQ4_GEMV_WAVES", 0);
-  static const int per_cu = env_int("KQ4_GEMV_WPCU", 16);
-  const int cb = kind == 2 ? 32 : 16;
-  const int nst = (nb + cb - 1) / cb;
-  const int lds_max = (160 * 1024) / kq4_gemv_slab_bytes(n, kind);
-  int cap = nst < 8 ? nst : 8;
-  cap = cap < lds_max ? cap : lds_max;
-  int want = force > 0 ? force : (per_cu * ncu + rowsets - 1) / rowsets;
+// GEMV launch shape. Workgroups: one per 32-row set, or per 16-row half set when the launch
+// has fewer sets than the chip has CUs (so that every CU streams). Waves per workgroup (splitting
+// K in 16-block stages): about KQ4_GEMV_WPCU (32) per CU over the launch, at most one per stage
+// and 16 per workgroup, balanced so that no wave has more stages than another by more than one.
+// KQ4_GEMV_HS / KQ4_GEMV_WAVES / KQ4_GEMV_MAXW override (for measurement).
+void plan_gemv(int sets, int nb, int ncu, int *half_out, int *nw_out) {
+  static const int force_hs = env_int("KQ4_GEMV_HS", -1);
+  static const int force_w = env_int("KQ4_GEMV_WAVES", 0);
+  static const int per_cu = env_int("KQ4_GEMV_WPCU", 32);
+  const int hs = force_hs == 0 || force_hs == 1 ? force_hs : (sets < ncu ? 1 : 0);
+  const int wgs = sets << hs;
+  const int nst = (nb + 15) / 16;
+  int want = force_w > 0 ? force_w : (per_cu * ncu + wgs - 1) / wgs;
+  static const int max_w = env_int("KQ4_GEMV_MAXW", 16);
+  const int cap = nst < max_w ? nst : max_w;
   want = want < 1 ? 1 : (want > cap ? cap : want);
   const int spw = (nst + want - 1) / want;   // stages per wave
-  return (nst + spw - 1) / spw;
+  *half_out = hs;
+  *nw_out = (nst + spw - 1) / spw;
 }
 
 // Whether the GEMV quantizes its fp32 activations itself (one launch per op) or reads them from
@@ -181,10 +178,11 @@ int run_gemv(DevState *ds, int n_mats, float *const *out, const float *const *re
   a.asm_tokens = asm_tokens;
   a.cols = cols;
   a.nb = nb;
-  int rows32 = 0;
-  for (int i = 0; i < n_mats; ++i) rows32 += (rows[i] + 31) / 32;
-  const int kind = gemv_kind(n, rows32, ds->ncu);
-  const int rsz = kq4_gemv_rowset(kind);
+  const int kind = gemv_kind(n);
+  int sets = 0;
+  for (int i = 0; i < n_mats; ++i) sets += (rows[i] + 31) / 32;
+  int hs = 0, nw = 1;
+  plan_gemv(sets, nb, ds->ncu, &hs, &nw);
   int wg = 0;
   for (int i = 0; i < n_mats; ++i) {
     KQ4GemvMat &m = a.mat[i];
@@ -193,13 +191,9 @@ int run_gemv(DevState *ds, int n_mats, float *const *out, const float *const *re
     m.res = res ? res[i] : nullptr;
     m.rows = rows[i];
     m.wg_begin = wg;
-    wg += (rows[i] + rsz - 1) / rsz;
+    wg += ((rows[i] + 31) / 32) << hs;
   }
-  const int nw = plan_gemv_waves(wg, nb, n, kind, ds->ncu);
-  static const int depth_env = env_int("KQ4_GEMV_DEPTH", 0);
-  const int nst = (nb + (kind == 2 ? 32 : 16) - 1) / (kind == 2 ? 32 : 16);
-  const int depth = depth_env ? depth_env : (nst > nw ? 2 : 1);   // two stages in flight if a wave has two
-  KQ4_HIP((hipError_t)kq4_launch_gemv(a, n, kind, nw, depth, wg, s));
+  KQ4_HIP((hipError_t)kq4_launch_gemv(a, n, kind, hs, nw, wg, s));
   return KQ4_OK;
 }
 
@@ -213,6 +207,7 @@ int matmul_impl(int n_mats, float *const *out, const float *const *res, const ui
     if (!shape_ok(rows[i], cols))
       return fail(KQ4_EINVAL, "rows=%d cols=%d: need rows%%4==0, cols%%32==0", rows[i], cols);
     if (!w[i] || !out[i]) return fail(KQ4_EINVAL, "null weight/output pointer");
+    if ((uintptr_t)w[i] % 16) return fail(KQ4_EINVAL, "weights not 16-byte aligned");
   }
   if (n == 0) return KQ4_OK;
   DevState *ds = nullptr;
@@ -274,6 +269,8 @@ int moe_impl(float *Y, const float *X, const int *sel, const float *pr, int T, i
              float *g_out, float *u_out, float *av_out, const float *av_in, hipStream_t s) {
   if (T < 0 || tk < 1 || tk > 32 || ne < 1 || d <= 0 || d % 32 || ef <= 0 || ef % 32)
     return fail(KQ4_EINVAL, "moe: T=%d tk=%d ne=%d d=%d ef=%d", T, tk, ne, d, ef);
+  if (!G || !U || !D || (uintptr_t)G % 16 || (uintptr_t)U % 16 || (uintptr_t)D % 16)
+    return fail(KQ4_EINVAL, "moe: null or misaligned (16 B) weights");
   if (T == 0) return KQ4_OK;
   DevState *ds = nullptr;
   int rc = cur_dev(&ds);
@@ -302,6 +299,8 @@ int moe_impl(float *Y, const float *X, const int *sel, const float *pr, int T, i
 
 // ---- host-pointer API helpers --------------------------------------------------------------
 
+size_t wbytes(int rows, int cols) { return (size_t)(rows / 4) * (cols / 32) * 72; }
+
 // Cheap fingerprint of a host weight buffer (FNV-1a over 3 x 64 sampled bytes + size): a cache
 // entry whose key was reused for different bytes (e.g. a freed and reallocated host buffer) is
 // re-uploaded instead of served stale.
@@ -314,8 +313,13 @@ uint64_t fingerprint(const uint8_t *w, size_t bytes) {
   return h;
 }
 
-int dev_weights(DevState *ds, uint64_t wkey, const uint8_t *w, size_t bytes, Buf &tmp,
+// Device copy of host VQF weights in the stream layout: from the cache under wkey (uploaded and
+// repacked once), or for wkey == 0 repacked into `tmp` for this call only. The VQF bytes go
+// through the staging buffer hstage; everything runs on the null stream, so it is ordered before
+// the kernels that read the copy.
+int dev_weights(DevState *ds, uint64_t wkey, const uint8_t *w, int rows, int cols, Buf &tmp,
                 const uint8_t **dev) {
+  const size_t bytes = wbytes(rows, cols), sbytes = kq4_stream_bytes(rows, cols);
   const uint64_t fp = wkey ? fingerprint(w, bytes) : 0;
   if (wkey) {
     std::lock_guard<std::mutex> lk(g_mu);
@@ -325,32 +329,36 @@ int dev_weights(DevState *ds, uint64_t wkey, const uint8_t *w, size_t bytes, Buf
       return KQ4_OK;
     }
   }
+  int rc = ensure(ds->hstage, bytes);
+  if (rc) return rc;
+  KQ4_HIP(hipMemcpy(ds->hstage.p, w, bytes, hipMemcpyHostToDevice));
+  uint8_t *dst = nullptr;
   if (wkey) {
     void *p = nullptr;
-    if (hipMalloc(&p, bytes) != hipSuccess) return fail(KQ4_ENOMEM, "weights %zu B", bytes);
-    hipError_t e = hipMemcpy(p, w, bytes, hipMemcpyHostToDevice);
-    if (e != hipSuccess) {
-      hipFree(p);
-      return fail(KQ4_EHIP, "weight upload: %s", hipGetErrorString(e));
-    }
+    if (hipMalloc(&p, sbytes) != hipSuccess) return fail(KQ4_ENOMEM, "weights %zu B", sbytes);
+    dst = static_cast<uint8_t *>(p);
+  } else {
+    if ((rc = ensure(tmp, sbytes))) return rc;
+    dst = static_cast<uint8_t *>(tmp.p);
+  }
+  hipError_t e = (hipError_t)kq4_launch_repack(dst, static_cast<const uint8_t *>(ds->hstage.p),
+                                               rows, cols, nullptr);
+  if (e != hipSuccess) {
+    if (wkey) hipFree(dst);
+    return fail(KQ4_EHIP, "weight repack: %s", hipGetErrorString(e));
+  }
+  if (wkey) {
     std::lock_guard<std::mutex> lk(g_mu);
     auto it = ds->wcache.find(wkey);
     if (it != ds->wcache.end()) {
       (void)hipDeviceSynchronize();   // the stale copy may still be read by queued work
       (void)hipFree(it->second.p);
     }
-    ds->wcache[wkey] = WEntry{static_cast<uint8_t *>(p), bytes, fp};
-    *dev = static_cast<uint8_t *>(p);
-    return KQ4_OK;
+    ds->wcache[wkey] = WEntry{dst, bytes, fp};
   }
-  int rc = ensure(tmp, bytes);
-  if (rc) return rc;
-  KQ4_HIP(hipMemcpy(tmp.p, w, bytes, hipMemcpyHostToDevice));
-  *dev = static_cast<uint8_t *>(tmp.p);
+  *dev = dst;
   return KQ4_OK;
 }
-
-size_t wbytes(int rows, int cols) { return (size_t)(rows / 4) * (cols / 32) * 72; }
 
 }  // namespace
 
@@ -386,7 +394,7 @@ void kq4_shutdown(void) {
     if (!s.ready) continue;
     hipSetDevice(d);
     hipDeviceSynchronize();
-    Buf *bufs[] = {&s.ws, &s.hx, &s.hres, &s.hout, &s.hw, &s.hsel, &s.hpr};
+    Buf *bufs[] = {&s.ws, &s.hx, &s.hres, &s.hout, &s.hw, &s.hsel, &s.hpr, &s.hstage};
     for (Buf *b : bufs) {
       if (b->p) hipFree(b->p);
       *b = Buf();
@@ -405,6 +413,22 @@ int kq4_quantize_dev(int8_t *xq, float *xd, float *xde, const float *x, int n_ba
   KQ4_HIP((hipError_t)kq4_launch_quantize(x, xq, xd, xde, n_batch, cols,
                                           asm_tokens_for(chain, n_batch),
                                           (hipStream_t)stream, 0));
+  return KQ4_OK;
+}
+
+size_t kq4_weights_stream_bytes(int rows, int cols) {
+  return shape_ok(rows, cols) ? kq4_stream_bytes(rows, cols) : 0;
+}
+
+int kq4_weights_prepare_dev(uint8_t *dst, const uint8_t *w4x4, int rows, int cols,
+                            void *stream) {
+  if (!shape_ok(rows, cols)) return fail(KQ4_EINVAL, "prepare: rows=%d cols=%d", rows, cols);
+  if (!dst || !w4x4 || (uintptr_t)dst % 16 || (uintptr_t)w4x4 % 8)
+    return fail(KQ4_EINVAL, "prepare: null pointer, dst not 16-byte or w4x4 not 8-byte aligned");
+  DevState *ds = nullptr;
+  int rc = cur_dev(&ds);
+  if (rc) return rc;
+  KQ4_HIP((hipError_t)kq4_launch_repack(dst, w4x4, rows, cols, (hipStream_t)stream));
   return KQ4_OK;
 }
 
@@ -496,7 +520,7 @@ int kq4_weights_upload(uint64_t wkey, const uint8_t *w4x4, int rows, int cols) {
       ds->wcache.erase(it);
     }
   }
-  return dev_weights(ds, wkey, w4x4, wbytes(rows, cols), unused, &dev) == KQ4_OK ? 1 : 0;
+  return dev_weights(ds, wkey, w4x4, rows, cols, unused, &dev) == KQ4_OK ? 1 : 0;
 }
 
 int kq4_weights_evict(uint64_t wkey) {
@@ -547,7 +571,7 @@ int kq4_matmul_multi(int n_mats, float *const *out, const float *const *residual
   const uint8_t *dw[KQ4_MAX_MATS];
   int rc = KQ4_OK;
   for (int i = 0; i < n_mats && !rc; ++i)
-    rc = dev_weights(ds, wkeys ? wkeys[i] : 0, w4x4[i], wbytes(rows[i], cols),
+    rc = dev_weights(ds, wkeys ? wkeys[i] : 0, w4x4[i], rows[i], cols,
                      i == 0 ? ds->hw : tw[i], &dw[i]);
   int ok = 0;
   if (!rc && !ensure(ds->hx, xb) && !ensure(ds->hout, total_o) && !ensure(ds->hres, total_o)) {
@@ -599,12 +623,15 @@ int kq4_moe_ffn(float *Y, const float *X, const int *sel, const float *pr, int T
   }
   DevState *ds = nullptr;
   if (cur_dev(&ds)) return 0;
-  const size_t gb = wbytes(ne * ef, d), db = wbytes(d, ne * ef);
+  if (ne < 1 || d <= 0 || d % 32 || ef <= 0 || ef % 32) {
+    fail(KQ4_EINVAL, "moe_ffn: ne=%d d=%d ef=%d", ne, d, ef);
+    return 0;
+  }
   const uint8_t *dG, *dU, *dD;
   Buf tg, tu, td;
-  int rc = dev_weights(ds, wkey, G, gb, tg, &dG);
-  if (!rc) rc = dev_weights(ds, wkey ? wkey + 1 : 0, U, gb, tu, &dU);
-  if (!rc) rc = dev_weights(ds, wkey ? wkey + 2 : 0, D, db, td, &dD);
+  int rc = dev_weights(ds, wkey, G, ne * ef, d, tg, &dG);
+  if (!rc) rc = dev_weights(ds, wkey ? wkey + 1 : 0, U, ne * ef, d, tu, &dU);
+  if (!rc) rc = dev_weights(ds, wkey ? wkey + 2 : 0, D, d, ne * ef, td, &dD);
   int ok = 0;
   const size_t xb = (size_t)T * d * sizeof(float), sb = (size_t)T * tk * sizeof(int);
   if (!rc && !ensure(ds->hx, xb) && !ensure(ds->hout, xb) && !ensure(ds->hsel, sb) &&

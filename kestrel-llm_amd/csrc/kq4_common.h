@@ -28,15 +28,52 @@ KQ4_DEV int kq4_dot4(uint32_t a, uint32_t b, int c) {
   return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
 }
 
-// Butterfly all-reduce over the 16 lanes of a DPP row; every lane ends with the same bits.
-KQ4_DEV float kq4_row16_sum(float v) {
-  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, true));  // quad xor 1
-  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, true));  // quad xor 2
-  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, true)); // half-row mirror
-  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, true)); // row mirror
-  return v;
+// ---- stream layout of the device weights -------------------------------------------------
+// A q4 matrix lives in HBM as 9216-B chunks, one per (32-row set, 16-block stage), in
+// [set][stage] order. In a chunk, "lane" l = row + 32*h (row = row within the set, h = half of
+// the 32-element block: elements 16h .. 16h+15) holds
+//   * at 1024*i + 16*l, i = 0..7: 8 nibble bytes for block 2i, then 8 for block 2i+1 (of the
+//     stage); dword d, byte k carries the stored 4-bit codes of elements 16h+8d+k (low nibble)
+//     and 16h+8d+4+k (high nibble). The stored code is the VQF one (the legacy nibble n XOR 8,
+//     the 4-bit two's complement of n-8), so kq4_lo16 / kq4_hi16 of dword d are the 16*(n-8)
+//     int8 values of elements 16h+8d .. +3 and 16h+8d+4 .. +7: a lane's 8 bytes are one half
+//     of one row of one block, in element order - the B operand of v_mfma_i32_32x32x32_i8.
+//   * at 8192 + 16*l: the f16 row scales of blocks 8h .. 8h+7 (of the stage) of its row.
+// Rows past the matrix and blocks past its K are zero bytes (zero scale, zero codes).
+#define KQ4_STREAM_CB 16
+#define KQ4_STREAM_CHUNK 9216
+
+// Byte offset of the 8 nibble bytes of (row, block b, half h) in a matrix of nst stages.
+KQ4_DEV size_t kq4_stream_nib(int row, int b, int h, int nst) {
+  return ((size_t)(row >> 5) * nst + (b >> 4)) * KQ4_STREAM_CHUNK + 1024 * ((b & 15) >> 1) +
+         16 * ((row & 31) + 32 * h) + 8 * (b & 1);
 }
 
-struct KQ4Tile2 {   // two consecutive 72-byte tiles (144 B = 9 x 16 B)
-  uint32_t d[36];
-};
+// Byte offset of the f16 scale of (row, block b).
+KQ4_DEV size_t kq4_stream_scale(int row, int b, int nst) {
+  return ((size_t)(row >> 5) * nst + (b >> 4)) * KQ4_STREAM_CHUNK + 8192 +
+         16 * ((row & 31) + 32 * ((b & 15) >> 3)) + 2 * (b & 7);
+}
+
+// The 16*(n-8) int8 operand (4 dwords, element order) of 8 nibble bytes.
+KQ4_DEV void kq4_unpack_half(uint32_t d0, uint32_t d1, uint32_t *o) {
+  o[0] = kq4_lo16(d0);
+  o[1] = kq4_hi16(d0);
+  o[2] = kq4_lo16(d1);
+  o[3] = kq4_hi16(d1);
+}
+
+// Exact integer block sum S of (row, block b) against 32 int8 activations q (8 dwords).
+KQ4_DEV int kq4_stream_row_dot(const uint8_t *__restrict__ w, int row, int b, int nst,
+                               const uint32_t *q) {
+  int s = 0;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const uint2 v = *reinterpret_cast<const uint2 *>(w + kq4_stream_nib(row, b, h, nst));
+    uint32_t o[4];
+    kq4_unpack_half(v.x, v.y, o);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) s = kq4_dot4(o[k], q[4 * h + k], s);
+  }
+  return s >> 4;   // exact: 16*S
+}

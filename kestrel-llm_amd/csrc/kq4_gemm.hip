@@ -1,4 +1,5 @@
-// kq4_gemm.hip - prefill GEMM over VQF 4x4 q4 tiles x int8 activations with int8 MFMA (gfx950).
+// kq4_gemm.hip - prefill GEMM over q4 weights (stream layout of VQF 4x4 tiles) x int8
+// activations with int8 MFMA (gfx950).
 //
 // One v_mfma_i32_32x32x32_i8 covers exactly one 32-element quantization block, so its int32
 // result is the block sum 16*S for a 32-token x 32-row tile (weights enter the matrix core as
@@ -15,7 +16,8 @@
 // Per stage of KB = 4 blocks the workgroup stages into LDS (rows padded to 48 B so the 16-byte
 // fragment reads are bank-conflict free):
 //   A  block-major activations [block][token][32] (contiguous 4 KB per block)
-//   B  weights unpacked from the 72-byte tiles to 16*(n-8) int8 [block][row][32]
+//   B  weights (the stream layout's half-rows, 16 B per lane-load) unpacked to 16*(n-8) int8
+//      [block][row][32]
 //   sW per-row scale wd/16, sX per-token activation scale
 // The workgroup -> tile map keeps the tiles of one XCD (workgroup id mod 8) in one contiguous
 // range, token tiles fastest, so the weight tiles a workgroup streams are shared in its L2.
@@ -38,7 +40,7 @@ KQ4_DEV int kq4_mfma_tok(int v, int half) { return 8 * (v >> 2) + 4 * half + (v 
 template <int CHAIN>
 __global__ __launch_bounds__(256, 2) void kq4_gemm_kernel(
     float *__restrict__ out, const float *__restrict__ res, const uint8_t *__restrict__ w,
-    const KQ4GemmAct act, int rows, int n_tok, int nb, int mtiles, int ntiles) {
+    const KQ4GemmAct act, int rows, int n_tok, int nb, int nst, int mtiles, int ntiles) {
   __shared__ __align__(16) int8_t sA[KQ4_GEMM_KB][KQ4_GEMM_BM * KQ4_LDS_ROW];
   __shared__ __align__(16) int8_t sB[KQ4_GEMM_KB][KQ4_GEMM_BN * KQ4_LDS_ROW];
   __shared__ __align__(16) float sW[KQ4_GEMM_KB][KQ4_GEMM_BN];
@@ -87,36 +89,33 @@ __global__ __launch_bounds__(256, 2) void kq4_gemm_kernel(
                                              (long)b * act.q_bs + hh * 16);
       *reinterpret_cast<uint4 *>(&sA[u][tok * KQ4_LDS_ROW + hh * 16]) = v;
     }
-    // ---- stage B: 32 groups x KB tiles x 16 nibble dwords, unpacked to 16*(n-8)
+    // ---- stage B from the stream layout: blocks b0 .. b0+3 are nibble units (b0%16)/2 and +1 of
+    // the 4 row sets; load (set, unit, lane) = 16 B = the lane's half-row of 2 blocks, unpacked
+    // to 16*(n-8) bytes. Then the 128 rows' scales of the 4 blocks (8 B per row), as wd/16.
 #pragma unroll
-    for (int u = 0; u < 2 * KQ4_GEMM_KB; ++u) {
-      const int c = t + 256 * u;                 // (group, tile, dword) with dword fastest
-      const int kd = c & 15;
-      const int bl = (c >> 4) % KQ4_GEMM_KB;
-      const int gl = c / (16 * KQ4_GEMM_KB);
-      const int gg = (n0 >> 2) + gl;
-      const int b = b0 + bl;
-      uint32_t wv = 0;                           // padding rows: weight 0
-      if (b < nb && gg < groups)
-        wv = *reinterpret_cast<const uint32_t *>(w + ((size_t)gg * nb + b) * 72 + 8 + 4 * kd);
-      const int r = kd & 3, k = kd >> 2;
-      int8_t *rowp = &sB[bl][(4 * gl + r) * KQ4_LDS_ROW];
-      *reinterpret_cast<uint32_t *>(rowp + 4 * k) = kq4_lo16(wv);
-      *reinterpret_cast<uint32_t *>(rowp + 16 + 4 * k) = kq4_hi16(wv);
+    for (int u = 0; u < 2; ++u) {
+      const int idx = t + 256 * u;
+      const int ln = idx & 63, iu = (idx >> 6) & 1, sl = idx >> 7;
+      const int rl = 32 * sl + (ln & 31), h = ln >> 5;
+      uint4 v = make_uint4(0, 0, 0, 0);          // row sets past the matrix: weight 0
+      if (n0 + 32 * sl < rows)
+        v = *reinterpret_cast<const uint4 *>(w + kq4_stream_nib(n0 + rl, b0 + 2 * iu, h, nst));
+      uint32_t o[4];
+      kq4_unpack_half(v.x, v.y, o);
+      *reinterpret_cast<uint4 *>(&sB[2 * iu][rl * KQ4_LDS_ROW + 16 * h]) =
+          make_uint4(o[0], o[1], o[2], o[3]);
+      kq4_unpack_half(v.z, v.w, o);
+      *reinterpret_cast<uint4 *>(&sB[2 * iu + 1][rl * KQ4_LDS_ROW + 16 * h]) =
+          make_uint4(o[0], o[1], o[2], o[3]);
     }
-    // ---- row scales (2 per dword) and token scales
-    if (t < 32 * KQ4_GEMM_KB * 2) {
-      const int c = t;                           // (group, tile, word) : 32 x KB x 2
-      const int wd_i = c & 1;
-      const int bl = (c >> 1) % KQ4_GEMM_KB;
-      const int gl = c / (2 * KQ4_GEMM_KB);
-      const int gg = (n0 >> 2) + gl;
-      const int b = b0 + bl;
-      uint32_t sv = 0;
-      if (b < nb && gg < groups)
-        sv = *reinterpret_cast<const uint32_t *>(w + ((size_t)gg * nb + b) * 72 + 4 * wd_i);
-      sW[bl][4 * gl + 2 * wd_i] = kq4_h2f(sv) * 0.0625f;
-      sW[bl][4 * gl + 2 * wd_i + 1] = kq4_h2f(sv >> 16) * 0.0625f;
+    if (t < KQ4_GEMM_BN) {
+      uint2 sv = make_uint2(0, 0);
+      if (n0 + (t & ~31) < rows)
+        sv = *reinterpret_cast<const uint2 *>(w + kq4_stream_scale(n0 + t, b0, nst));
+      sW[0][t] = kq4_h2f(sv.x) * 0.0625f;
+      sW[1][t] = kq4_h2f(sv.x >> 16) * 0.0625f;
+      sW[2][t] = kq4_h2f(sv.y) * 0.0625f;
+      sW[3][t] = kq4_h2f(sv.y >> 16) * 0.0625f;
     }
 #pragma unroll
     for (int u = 0; u < KQ4_GEMM_KB * KQ4_GEMM_BM / 256; ++u) {
@@ -204,13 +203,14 @@ __global__ __launch_bounds__(256, 2) void kq4_gemm_kernel(
 int kq4_launch_gemm(float *out, const float *res, const uint8_t *w, const KQ4GemmAct &act,
                     int rows, int cols, int n_tok, int chain, hipStream_t s) {
   const int nb = cols / 32;
+  const int nst = (nb + KQ4_STREAM_CB - 1) / KQ4_STREAM_CB;
   const int mtiles = (n_tok + KQ4_GEMM_BM - 1) / KQ4_GEMM_BM;
   const int ntiles = (rows + KQ4_GEMM_BN - 1) / KQ4_GEMM_BN;
   const int grid = mtiles * ntiles;
   if (grid <= 0) return 0;
 #define KQ4_GEMM_LAUNCH(C)                                                                        \
   hipLaunchKernelGGL((kq4_gemm_kernel<C>), dim3(grid), dim3(256), 0, s, out, res, w, act, rows,   \
-                     n_tok, nb, mtiles, ntiles)
+                     n_tok, nb, nst, mtiles, ntiles)
   if (chain == KQ4_CHAIN_CTILE)
     KQ4_GEMM_LAUNCH(KQ4_CHAIN_CTILE);
   else if (chain == KQ4_CHAIN_GEMV32)

@@ -1,237 +1,184 @@
-// kq4_gemv.hip - decode GEMV (1..8 tokens) over VQF 4x4 q4 tiles x int8 activations, gfx950.
+// kq4_gemv.hip - decode GEMV (1..8 tokens) over q4 weights in the kq4 stream layout x int8
+// activations, gfx950; plus the repack from the VQF 4x4 layout into that stream layout.
 //
 // Computes out[m][n] = [res +] sum_b S[m,n,b] * fl(wd[n,b] * xs[m,b]), the op of
 // q4x4_gemm_batched / dyn_matvec_q4_q8 (kestrel-llm src/model/vllm_safetensors.c:4593-4631,
 // 6147-6174): S is the exact integer dot of row n's 32 nibble weights (n-8) with the token's
 // int8 block, xs the token's block scale (f16-rounded for ASM-chain tokens, as the reference's
 // asm path multiplies by the f16 scale it repacks, :4104-4105). Every per-block term is the
-// reference's; the blocks of one output are summed serially within a slice of K and the slices
-// are then added in a fixed order, so outputs agree with the reference's single serial chain to a
-// few ulp of the row magnitude.
+// reference's; the blocks of one output are summed serially within each wave's share of K and
+// the shares are then added in wave order, so outputs agree with the reference's single serial
+// chain to a few ulp of the row magnitude.
+//
+// The weights are in the stream layout (kq4_common.h): per (32-row set, 16-block stage) one
+// 9216-B chunk in which lane l of a wave finds, at 16-B units l, l+64, .. (1 KB apart), the
+// nibbles of its row (l%32) and K-half (l/32) for the stage's 16 blocks, and at 8192+16*l the
+// f16 scales. So a stage is 9 + 1 full-width coalesced loads per lane (the second scale load
+// reads the other half's 8 scales of the same row) and every lane then holds its own operands:
+// no weight bytes pass through LDS.
 //
 // Work decomposition (the weight stream is the whole cost):
-//   * a workgroup = one 32-row set (8 tile groups) over the whole K, W waves (1..8); wave w
-//     takes the 16-block stages w, w + W, ... . A stage is 8 x 16 x 72 B = 9216 B, loaded as
-//     9 x 16 B per lane so that every load instruction reads 1 KB of contiguous bytes (a
-//     group's 16 tiles are 1152 contiguous bytes), then laid out per group in the wave's own LDS
-//     slab. Up to two stages per wave are in flight, each issued as (activations, weights).
-//   * each wave also stages its own activations (int8 codes + per-block scales) in its slab,
-//     quantizing them from fp32 itself (FQ, M <= 2) or copying a pre-quantized buffer, so the
-//     stage loop has no workgroup barrier.
+//   * a workgroup = one 32-row set (or, when a launch has fewer sets than the chip has CUs, half
+//     of one: 16 rows, so twice the workgroups) over the whole K, W <= 16 waves; wave w takes the
+//     stages w, w + W, .., each issued as (activations, weights).
+//   * each wave stages its own activations (int8 codes + per-block scales) in a small LDS slab,
+//     quantizing them from fp32 itself (FQ) or copying a pre-quantized buffer, so the stage loop
+//     has no workgroup barrier.
 //   * the integer dot, two kinds:
-//       DOT4: lane (g, j) owns the tile pair (2j, 2j+1) of group g; v_dot4_i32_i8 on the
-//             nibbles shifted into the high half of each byte (16*(n-8)), the 8 lanes' partial
-//             rows all-reduced with DPP. Fewest instructions per byte at small M.
-//       MFMA: one v_mfma_i32_32x32x32_i8 per block: A = activations (32 token rows, M <= 8
-//             used), B = the 32 weight rows as 16*(n-8) bytes, K = the block's 32 elements; the
-//             result 16*S sits in lanes (row = lane%32, token = 4*(lane/32)+v). Its cost does not
-//             grow with M.
+//       DOT4: lane (row, half) dots its 16 weights of each block with v_dot4_i32_i8 against the
+//             token's 16 codes (an LDS broadcast read) and keeps one fp32 chain per token and
+//             half (the C-tile kernel's lo/hi split, :4180-4216); the halves are added at the
+//             end. Cost grows with M.
+//       MFMA: per block one v_mfma_i32_32x32x32_i8 with A = the tokens' codes (32 rows, M <= 8
+//             used) and B = the lanes' weight operands as they are; the result 16*S is at lane
+//             (row = lane%32, token = 4*(lane/32) + v). Cost independent of M.
 //   * at the end the waves' partial sums are added in wave order through LDS: deterministic,
 //     one launch, no cross-workgroup communication.
 #include "kq4_common.h"
 #include "kq4_internal.h"
 
-// A stage is G8 groups x CB blocks = 128 tiles = 9216 B: a 32-row set (G8 = 8, CB = 16) or a
-// 16-row set (G8 = 4, CB = 32, DOT4 only).
-template <int G8>
-constexpr int kq4_gv_cb() { return 128 / G8; }
-// LDS bytes per token row of a stage's int8 codes (block pairs at an 80-B pitch, see qpos).
-template <int G8>
-constexpr int kq4_gv_qts() { return G8 == 8 ? 672 : 1312; }
+#define KQ4_GV_CB KQ4_STREAM_CB       // blocks per stage
+#define KQ4_GV_CHUNK KQ4_STREAM_CHUNK // bytes per (32-row set, stage)
+#define KQ4_GV_QTS 672                // LDS bytes per token row of a stage's int8 codes
+#define KQ4_GV_XS (KQ4_GV_CB * 8 * 4) // LDS bytes of a stage's scales [16 blocks][8 tokens]
 
 typedef int kq4_v4i __attribute__((ext_vector_type(4)));
 typedef int kq4_v16i __attribute__((ext_vector_type(16)));
 
-// LDS pitch of one group's CB tiles: DOT4 reads 144-B tile pairs (the unpadded pitch is
-// conflict-free for them); MFMA reads one dword per lane of 8 groups at once, which needs a 16-B
-// pad to spread the groups over the banks.
-template <int KIND, int G8>
-constexpr int kq4_gv_pitch() { return kq4_gv_cb<G8>() * 72 + (KIND == 0 ? 0 : 16); }
-
-template <int M, int KIND, int G8>
+// LDS bytes of one wave's slab: [activation codes][scales]; it also holds the wave's partial
+// sums at the end (at most 2 x 8 x 32 floats).
+template <int M>
 constexpr int kq4_gv_slab() {
-  return G8 * kq4_gv_pitch<KIND, G8>() + M * kq4_gv_qts<G8>() + kq4_gv_cb<G8>() * 8 * 4;
+  return M * KQ4_GV_QTS + KQ4_GV_XS;
 }
 
 // Byte offset of block blk's 32 codes in a token row: block pairs at an 80-B pitch (16-B pad),
-// which spreads both readers' 16-B accesses over the banks.
+// which spreads the two halves' 16-B reads over the banks.
 KQ4_DEV int kq4_gv_qpos(int blk) { return (blk >> 1) * 80 + (blk & 1) * 32; }
-
-// B operand of one block for weight row (lane%32) from its tile's 4 nibble dwords: lanes
-// 0..31 carry elements 0..15 (low nibbles), lanes 32..63 elements 16..31 (high nibbles), each
-// as 16*(n-8) int8 lanes in element order.
-KQ4_DEV kq4_v4i kq4_gv_bop(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3, int sh) {
-  kq4_v4i b;
-  b.x = (int)((w0 << sh) & 0xF0F0F0F0u);
-  b.y = (int)((w1 << sh) & 0xF0F0F0F0u);
-  b.z = (int)((w2 << sh) & 0xF0F0F0F0u);
-  b.w = (int)((w3 << sh) & 0xF0F0F0F0u);
-  return b;
-}
 
 KQ4_DEV kq4_v16i kq4_gv_mfma(kq4_v4i a, kq4_v4i b) {
   const kq4_v16i z = {0};
   return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, z, 0, 0, 0);
 }
 
-// ---- weight stage: 9216 B = 36 dwords per lane ----------------------------------------------
+// ---- weights of one stage -------------------------------------------------------------------
+// Full-set mode (HS = 0): lane (r, h) = (lane%32, lane/32) holds row r's half h of all 16 blocks
+// (8 unit loads). Half-set mode (HS = 1, a workgroup takes rows 16*hs .. +15 of the set): lane
+// (r, p, h) = (lane%16, (lane/16)%2, lane/32) holds row 16*hs+r's half h of the 8 blocks
+// 4u+2p, 4u+2p+1 (u = 0..3; 4 unit loads, each instruction covering two 1-KB units at 256-B
+// runs). In both, the row's 16 scales (2 loads; lanes of one row share them).
 
-template <int UNIT>
+template <int HS>
 struct KQ4GvStage {
-  uint32_t d[36];
+  static constexpr int NU = HS ? 4 : 8;   // 16-B nibble loads per lane
+  uint32_t n[4 * NU];                     // lane block jb (0 .. 2*NU-1): n[2jb], n[2jb+1]
+  uint32_t sc[8];                         // stage block b: f16 at sc[b/2] >> 16*(b%2)
 };
 
-// Per-lane byte offsets of the lane's units within a stage, relative to the stage's first block
-// in group g0: unit u = 64 i + lane is group gi = u / UPG at byte (u % UPG)*UNIT of that group's
-// CB tiles (UPG = CB*72/UNIT units per group). Groups past the matrix end read group G-1 (in
-// bounds; unused).
-template <int UNIT, int G8>
-struct KQ4GvOff {
-  uint32_t o[9216 / UNIT / 64];
-};
-
-template <int UNIT, int G8>
-KQ4_DEV void kq4_gv_offsets(KQ4GvOff<UNIT, G8> &f, int g0, int G, int nb, int lane) {
-  constexpr int UPG = kq4_gv_cb<G8>() * 72 / UNIT;
-  constexpr int NL = 9216 / UNIT / 64;
+// Scales first: the loads complete in issue order, so the first block then waits only for the
+// scales and its own unit, and each later block for one more unit.
+template <int HS>
+KQ4_DEV void kq4_gv_load(KQ4GvStage<HS> &st, const uint8_t *__restrict__ chunk, int rr, int h,
+                         int p) {
+  const uint4 *sc = reinterpret_cast<const uint4 *>(chunk + 8192) + rr;
+  const uint4 a = sc[0], b = sc[32];
+  st.sc[0] = a.x; st.sc[1] = a.y; st.sc[2] = a.z; st.sc[3] = a.w;
+  st.sc[4] = b.x; st.sc[5] = b.y; st.sc[6] = b.z; st.sc[7] = b.w;
+  const uint4 *src = reinterpret_cast<const uint4 *>(chunk) + rr + 32 * h;
 #pragma unroll
-  for (int i = 0; i < NL; ++i) {
-    const int u = 64 * i + lane;
-    const int gi = u / UPG;
-    int g = g0 + gi;
-    g = g < G ? g : G - 1;
-    f.o[i] = (uint32_t)g * (uint32_t)nb * 72u + (uint32_t)((u - gi * UPG) * UNIT);
+  for (int u = 0; u < KQ4GvStage<HS>::NU; ++u) {
+    const int i = HS ? 2 * u + p : u;
+    const uint4 v = src[64 * i];
+    st.n[4 * u] = v.x; st.n[4 * u + 1] = v.y; st.n[4 * u + 2] = v.z; st.n[4 * u + 3] = v.w;
   }
 }
 
-// Loads stage st. In a partial last stage, bytes past the matrix's last block read the stage's
-// first block instead (in bounds; unused).
-template <int UNIT, int G8>
-KQ4_DEV void kq4_gv_load(KQ4GvStage<UNIT> &s, const uint8_t *__restrict__ w,
-                         const KQ4GvOff<UNIT, G8> &f, int nb, int st, int lane) {
-  constexpr int CB = kq4_gv_cb<G8>();
-  constexpr int UPG = CB * 72 / UNIT;
-  constexpr int NL = 9216 / UNIT / 64;
-  const int kb = st * CB;
-  const uint8_t *base = w + (size_t)kb * 72;
-  const bool partial = nb - kb < CB;
-  const uint32_t valid = (uint32_t)(nb - kb) * 72u;
-#pragma unroll
-  for (int i = 0; i < NL; ++i) {
-    uint32_t off = f.o[i];
-    if (partial) {
-      const int u = 64 * i + lane;
-      const uint32_t in = (uint32_t)((u - (u / UPG) * UPG) * UNIT);
-      off = in >= valid ? off - in : off;
-    }
-    const uint8_t *p = base + off;
-    if (UNIT == 16) {
-      const uint4 v = *reinterpret_cast<const uint4 *>(p);
-      s.d[4 * i] = v.x; s.d[4 * i + 1] = v.y; s.d[4 * i + 2] = v.z; s.d[4 * i + 3] = v.w;
-    } else {
-      const uint2 v = *reinterpret_cast<const uint2 *>(p);
-      s.d[2 * i] = v.x; s.d[2 * i + 1] = v.y;
-    }
-  }
+// Stage block of lane block jb (p = the lane's unit parity in half-set mode).
+template <int HS>
+KQ4_DEV int kq4_gv_blk(int jb, int p) { return HS ? 4 * (jb >> 1) + 2 * p + (jb & 1) : jb; }
+
+// a if p == 0, b if p == 1, by masks: a select between two elements of one register array
+// would be folded into a lane-dependent index, which puts the array in scratch memory.
+KQ4_DEV uint32_t kq4_gv_pick(uint32_t a, uint32_t b, int p) {
+  const uint32_t m = 0u - (uint32_t)p;
+  return (a & ~m) | (b & m);
 }
 
-template <int UNIT, int KIND, int G8>
-KQ4_DEV void kq4_gv_store(const KQ4GvStage<UNIT> &s, uint8_t *sw, int lane) {
-  constexpr int UPG = kq4_gv_cb<G8>() * 72 / UNIT;
-  constexpr int NL = 9216 / UNIT / 64;
-#pragma unroll
-  for (int i = 0; i < NL; ++i) {
-    const int u = 64 * i + lane;
-    uint8_t *p;
-    if (KIND == 0) {
-      p = sw + u * UNIT;                       // unpadded pitch: the stage bytes as loaded
-    } else {
-      const int gi = u / UPG;
-      p = sw + gi * kq4_gv_pitch<KIND, G8>() + (u - gi * UPG) * UNIT;
-    }
-    if (UNIT == 16)
-      *reinterpret_cast<uint4 *>(p) = make_uint4(s.d[4 * i], s.d[4 * i + 1], s.d[4 * i + 2], s.d[4 * i + 3]);
-    else
-      *reinterpret_cast<uint2 *>(p) = make_uint2(s.d[2 * i], s.d[2 * i + 1]);
-  }
+// Row scale (f32) of lane block jb; the register index is compile-time in both modes.
+template <int HS>
+KQ4_DEV float kq4_gv_wd(const KQ4GvStage<HS> &st, int jb, int p) {
+  const uint32_t w = HS ? kq4_gv_pick(st.sc[2 * (jb >> 1)], st.sc[2 * (jb >> 1) + 1], p)
+                        : st.sc[jb >> 1];
+  return kq4_h2f(w >> (16 * (jb & 1)));
 }
 
 // ---- activations of a stage -------------------------------------------------------------------
 // Loaded into registers together with (just before) the stage's weights, then written to the
-// wave's slab as int8 codes (token row m at m*qts, block at kq4_gv_qpos) and the effective
-// per-block scale sx[blk][m] = xs/16 (xs = f16-rounded xd for ASM-chain tokens; the /16 undoes the
-// 16*(n-8) weight scaling exactly). Issuing them before the weights keeps the in-order load
-// counter from making the quantization wait for the weights.
+// wave's slab as int8 codes (token row m at m*KQ4_GV_QTS, block at kq4_gv_qpos) and the
+// effective per-block scale sx[blk][m] = xs/16 (xs = f16-rounded xd for ASM-chain tokens; the /16
+// undoes the 16*(n-8) weight scaling exactly). Issuing them before the weights keeps the in-order
+// load counter from making the quantization wait for the weights.
 //
-// FQ (M <= KQ4_GEMV_FQ_MAX_M): lane quad (4q .. 4q+3) owns block q (+16 per pass) for one token
-// per pass, 8 fp32 each; the quantization restates quantize_row_q8_0_act
-// (vllm_safetensors.c:7893-7920): d = amax/127 is a true division, x/d the Markstein-corrected
-// quotient q = x*y, q += fma(-q, d, x)*y with y = RN(1/d), which is the correctly rounded x/d for
-// these normal operands, so the codes are the reference's bit for bit.
+// FQ (M <= KQ4_GEMV_FQ_MAX_M): lane quad (4q .. 4q+3) owns block q for one token per pass, 8
+// fp32 each; the quantization restates quantize_row_q8_0_act (vllm_safetensors.c:7893-7920):
+// d = amax/127 is a true division, x/d the Markstein-corrected quotient q = x*y,
+// q += fma(-q, d, x)*y with y = RN(1/d), which is the correctly rounded x/d for these normal
+// operands, so the codes are the reference's bit for bit.
 // Pre-quantized: lane i copies 16-B units i, i+64, .. of the stage's codes and scales i, i+64.
-template <int M, bool FQ, int G8>
+template <int M, bool FQ>
 struct KQ4GvAct {
-  static constexpr int CB = kq4_gv_cb<G8>();
-  static constexpr int NP = FQ ? M * CB / 16 : 1;              // quantization passes
-  static constexpr int NQ = FQ ? 1 : (2 * CB * M + 63) / 64;   // uint4 per lane
-  static constexpr int NX = FQ ? 1 : (CB * M + 63) / 64;       // scales per lane
-  float4 f[FQ ? 2 * NP : 1];
+  static constexpr int NQ = FQ ? 1 : (32 * M + 63) / 64;   // uint4 per lane
+  static constexpr int NX = FQ ? 1 : (16 * M + 63) / 64;   // scales per lane
+  float4 f[FQ ? 2 * M : 1];
   uint4 q[NQ];
   float x[NX];
 };
 
-template <int M, bool FQ, int G8>
-KQ4_DEV void kq4_gv_act_load(KQ4GvAct<M, FQ, G8> &r, const KQ4GemvArgs &a, int st, int lane) {
-  constexpr int CB = kq4_gv_cb<G8>();
+template <int M, bool FQ>
+KQ4_DEV void kq4_gv_act_load(KQ4GvAct<M, FQ> &r, const KQ4GemvArgs &a, int st, int lane) {
   const int nb = a.nb, cols = a.cols;
-  const int kb = st * CB;
+  const int kb = st * KQ4_GV_CB;
   if (FQ) {
-    const int qq = lane & 3;
+    const int b = kb + (lane >> 2), qq = lane & 3;
 #pragma unroll
-    for (int p = 0; p < KQ4GvAct<M, FQ, G8>::NP; ++p) {
-      const int item = (lane >> 2) + 16 * p;           // (token, block) = (item / CB, item % CB)
-      const int m = item / CB, b = kb + (item - m * CB);
+    for (int m = 0; m < M; ++m) {
       if (b < nb) {
         const float4 *src =
             reinterpret_cast<const float4 *>(a.xf + (size_t)m * cols + (size_t)b * 32 + 8 * qq);
-        r.f[2 * p] = src[0];
-        r.f[2 * p + 1] = src[1];
+        r.f[2 * m] = src[0];
+        r.f[2 * m + 1] = src[1];
       } else {
-        r.f[2 * p] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        r.f[2 * p + 1] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        r.f[2 * m] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        r.f[2 * m + 1] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
       }
     }
   } else {
 #pragma unroll
-    for (int c = 0; c < KQ4GvAct<M, FQ, G8>::NQ; ++c) {
+    for (int c = 0; c < KQ4GvAct<M, FQ>::NQ; ++c) {
       const int i = lane + 64 * c;
-      const int m = i / (2 * CB), u = i - m * 2 * CB, b = kb + (u >> 1), hh = u & 1;
+      const int m = i >> 5, u = i & 31, b = kb + (u >> 1), hh = u & 1;
       r.q[c] = make_uint4(0, 0, 0, 0);
       if (m < M && b < nb)
         r.q[c] = *reinterpret_cast<const uint4 *>(a.xq + (size_t)m * cols + (size_t)b * 32 + 16 * hh);
     }
 #pragma unroll
-    for (int c = 0; c < KQ4GvAct<M, FQ, G8>::NX; ++c) {
+    for (int c = 0; c < KQ4GvAct<M, FQ>::NX; ++c) {
       const int i = lane + 64 * c;
-      const int m = i / CB, b = kb + (i - m * CB);
+      const int m = i >> 4, b = kb + (i & 15);
       r.x[c] = (m < M && b < nb) ? a.xd[(size_t)m * nb + b] : 0.0f;
     }
   }
 }
 
-template <int M, bool FQ, int G8>
-KQ4_DEV void kq4_gv_act_put(const KQ4GvAct<M, FQ, G8> &r, const KQ4GemvArgs &a, int lane,
+template <int M, bool FQ>
+KQ4_DEV void kq4_gv_act_put(const KQ4GvAct<M, FQ> &r, const KQ4GemvArgs &a, int lane,
                             uint8_t *sq, float (*sx)[8]) {
-  constexpr int CB = kq4_gv_cb<G8>();
-  constexpr int QTS = kq4_gv_qts<G8>();
   if (FQ) {
-    const int qq = lane & 3;
+    const int blk = lane >> 2, qq = lane & 3;
 #pragma unroll
-    for (int p = 0; p < KQ4GvAct<M, FQ, G8>::NP; ++p) {
-      const int item = (lane >> 2) + 16 * p;
-      const int m = item / CB, blk = item - m * CB;
-      const float v[8] = {r.f[2 * p].x, r.f[2 * p].y, r.f[2 * p].z, r.f[2 * p].w,
-                          r.f[2 * p + 1].x, r.f[2 * p + 1].y, r.f[2 * p + 1].z, r.f[2 * p + 1].w};
+    for (int m = 0; m < M; ++m) {
+      const float v[8] = {r.f[2 * m].x, r.f[2 * m].y, r.f[2 * m].z, r.f[2 * m].w,
+                          r.f[2 * m + 1].x, r.f[2 * m + 1].y, r.f[2 * m + 1].z, r.f[2 * m + 1].w};
       float amax = 1e-10f;
 #pragma unroll
       for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
@@ -249,135 +196,98 @@ KQ4_DEV void kq4_gv_act_put(const KQ4GvAct<M, FQ, G8> &r, const KQ4GemvArgs &a, 
         c = c > 127 ? 127 : (c < -127 ? -127 : c);
         pk[i >> 2] |= ((uint32_t)c & 0xFFu) << (8 * (i & 3));
       }
-      *reinterpret_cast<uint2 *>(sq + m * QTS + kq4_gv_qpos(blk) + 8 * qq) = make_uint2(pk[0], pk[1]);
+      *reinterpret_cast<uint2 *>(sq + m * KQ4_GV_QTS + kq4_gv_qpos(blk) + 8 * qq) = make_uint2(pk[0], pk[1]);
       if (qq == 0) sx[blk][m] = ((m < a.asm_tokens) ? kq4_f16_round(d) : d) * 0.0625f;
     }
   } else {
 #pragma unroll
-    for (int c = 0; c < KQ4GvAct<M, FQ, G8>::NQ; ++c) {
+    for (int c = 0; c < KQ4GvAct<M, FQ>::NQ; ++c) {
       const int i = lane + 64 * c;
-      const int m = i / (2 * CB), u = i - m * 2 * CB;
+      const int m = i >> 5, u = i & 31;
       if (m < M)
-        *reinterpret_cast<uint4 *>(sq + m * QTS + kq4_gv_qpos(u >> 1) + 16 * (u & 1)) = r.q[c];
+        *reinterpret_cast<uint4 *>(sq + m * KQ4_GV_QTS + kq4_gv_qpos(u >> 1) + 16 * (u & 1)) = r.q[c];
     }
 #pragma unroll
-    for (int c = 0; c < KQ4GvAct<M, FQ, G8>::NX; ++c) {
+    for (int c = 0; c < KQ4GvAct<M, FQ>::NX; ++c) {
       const int i = lane + 64 * c;
-      const int m = i / CB, blk = i - m * CB;
+      const int m = i >> 4, blk = i & 15;
       if (m < M) sx[blk][m] = ((m < a.asm_tokens) ? kq4_f16_round(r.x[c]) : r.x[c]) * 0.0625f;
     }
   }
 }
 
-// ---- compute: the blocks of one stage for this wave's row set --------------------------------
+// ---- compute ---------------------------------------------------------------------------------
 
-// DOT4: lane (gl, j) = (lane / (CB/2), lane % (CB/2)) owns tiles (2j, 2j+1) of group gl;
-// acc[r*M + m] = row (4*gl + r), token m. The pair is read one tile at a time (18 dwords).
-template <int M, int G8>
-KQ4_DEV void kq4_gv_dot4(const uint8_t *sw, const uint8_t *sq, const float (*sx)[8], int nblk,
-                         int lane, float *acc) {
-  constexpr int CB = kq4_gv_cb<G8>();
-  constexpr int QTS = kq4_gv_qts<G8>();
-  const int gl = lane / (CB / 2), j = lane % (CB / 2);
-  const uint8_t *tp = sw + gl * (CB * 72) + j * 144;
+// Materialises x here: the unrolled block loops below would otherwise have every block's product
+// sunk to the end of the stage, keeping all blocks' operands live at once (far more registers
+// than a wave has).
+KQ4_DEV void kq4_gv_pin(float &x) { asm volatile("" : "+v"(x)); }
+
+// DOT4: acc[m] = token m's chain over this lane's blocks of its row and half.
+template <int M, int HS>
+KQ4_DEV void kq4_gv_dot4(const KQ4GvStage<HS> &st, const uint8_t *sq, const float (*sx)[8], int h,
+                         int p, float *acc) {
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    const int b = 2 * j + t;
-    if (b >= nblk) break;
-    uint32_t tile[18];
-    if (t == 0) {   // bytes 0..71 of the pair: 16-B aligned
-      const uint4 *p = reinterpret_cast<const uint4 *>(tp);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint4 v = p[i];
-        tile[4 * i] = v.x; tile[4 * i + 1] = v.y; tile[4 * i + 2] = v.z; tile[4 * i + 3] = v.w;
-      }
-      const uint2 v = *reinterpret_cast<const uint2 *>(tp + 64);
-      tile[16] = v.x; tile[17] = v.y;
-    } else {        // bytes 72..143: an 8-B piece, then 16-B aligned
-      const uint2 v = *reinterpret_cast<const uint2 *>(tp + 72);
-      tile[0] = v.x; tile[1] = v.y;
-      const uint4 *p = reinterpret_cast<const uint4 *>(tp + 80);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint4 u = p[i];
-        tile[2 + 4 * i] = u.x; tile[3 + 4 * i] = u.y; tile[4 + 4 * i] = u.z; tile[5 + 4 * i] = u.w;
-      }
-    }
-    float wd[4];
-    wd[0] = kq4_h2f(tile[0]);
-    wd[1] = kq4_h2f(tile[0] >> 16);
-    wd[2] = kq4_h2f(tile[1]);
-    wd[3] = kq4_h2f(tile[1] >> 16);
+  for (int jb = 0; jb < 4 * KQ4GvStage<HS>::NU / 2; ++jb) {
+    const int b = kq4_gv_blk<HS>(jb, p);
+    uint32_t o[4];
+    kq4_unpack_half(st.n[2 * jb], st.n[2 * jb + 1], o);
+    const float wd = kq4_gv_wd<HS>(st, jb, p);
 #pragma unroll
     for (int m = 0; m < M; ++m) {
-      const uint4 *qp = reinterpret_cast<const uint4 *>(sq + m * QTS + kq4_gv_qpos(b));
-      const uint4 q0 = qp[0], q1 = qp[1];
-      const uint32_t qa[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
-      const float xs = sx[b][m];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        int s = 0;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          const uint32_t wv = tile[2 + 4 * k + r];
-          s = kq4_dot4(kq4_lo16(wv), qa[k], s);
-          s = kq4_dot4(kq4_hi16(wv), qa[4 + k], s);
-        }
-        acc[r * M + m] = fmaf((float)s, wd[r] * xs, acc[r * M + m]);
-      }
+      const uint4 q = *reinterpret_cast<const uint4 *>(sq + m * KQ4_GV_QTS + kq4_gv_qpos(b) + 16 * h);
+      int s = kq4_dot4(o[0], q.x, 0);
+      s = kq4_dot4(o[1], q.y, s);
+      s = kq4_dot4(o[2], q.z, s);
+      s = kq4_dot4(o[3], q.w, s);
+      acc[m] = fmaf((float)s, wd * sx[b][m], acc[m]);
+      kq4_gv_pin(acc[m]);
     }
   }
 }
 
-// MFMA (32-row sets): acc[v] = row (lane%32), token 4*(lane/32)+v.
-template <int M>
-KQ4_DEV void kq4_gv_mfma_stage(const uint8_t *sw, const uint8_t *sq, const float (*sx)[8],
-                               int nblk, int lane, float *acc) {
+// MFMA: one v_mfma_i32_32x32x32_i8 per lane block. B column = lane%32 (full set: row; half set:
+// row + 16p, the two parities holding different blocks), k half = lane/32. A row = lane%32 holds
+// the codes of token min(lane%32 (%16 in half-set mode), M-1) for the lane's own block, so output
+// (token row T, column c) is valid where T's block matches c's: full set T = token 0..7, half set
+// T = token + 16p. acc[v] = token 4h+v of the lane's row (and parity).
+template <int M, int HS>
+KQ4_DEV void kq4_gv_mfma_stage(const KQ4GvStage<HS> &st, const uint8_t *sq, const float (*sx)[8],
+                               int lane, int p, float *acc) {
   constexpr int VT = M < 4 ? M : 4;
-  constexpr int P = kq4_gv_pitch<1, 8>();
-  constexpr int QTS = kq4_gv_qts<8>();
-  const int j = lane & 31, h = lane >> 5;
-  const int g = j >> 2, r = j & 3;
-  const int t = j < M ? j : M - 1;
-  const int sh = h ? 0 : 4;
-  const uint8_t *wb = sw + g * P + 8 + 4 * r;
-  const uint8_t *sb = sw + g * P + 2 * r;
-  const uint8_t *qb = sq + t * QTS + 16 * h;
-  for (int b = 0; b < nblk; ++b) {
-    const uint8_t *tb = wb + b * 72;
-    const kq4_v4i B = kq4_gv_bop(*reinterpret_cast<const uint32_t *>(tb),
-                                 *reinterpret_cast<const uint32_t *>(tb + 16),
-                                 *reinterpret_cast<const uint32_t *>(tb + 32),
-                                 *reinterpret_cast<const uint32_t *>(tb + 48), sh);
+  const int h = lane >> 5;
+  const int tr = HS ? (lane & 15) : (lane & 31);
+  const int t = tr < M ? tr : M - 1;
+  const uint8_t *qb = sq + t * KQ4_GV_QTS + 16 * h;
+#pragma unroll
+  for (int jb = 0; jb < 4 * KQ4GvStage<HS>::NU / 2; ++jb) {
+    const int b = kq4_gv_blk<HS>(jb, p);
+    uint32_t o[4];
+    kq4_unpack_half(st.n[2 * jb], st.n[2 * jb + 1], o);
+    const kq4_v4i B = {(int)o[0], (int)o[1], (int)o[2], (int)o[3]};
     const kq4_v4i A = *reinterpret_cast<const kq4_v4i *>(qb + kq4_gv_qpos(b));
     const kq4_v16i C = kq4_gv_mfma(A, B);
-    const float wd = kq4_h2f(*reinterpret_cast<const uint16_t *>(sb + b * 72));
+    const float wd = kq4_gv_wd<HS>(st, jb, p);
     const float4 xs = *reinterpret_cast<const float4 *>(&sx[b][4 * h]);
     const float xv[4] = {xs.x, xs.y, xs.z, xs.w};
 #pragma unroll
-    for (int v = 0; v < VT; ++v) acc[v] = fmaf((float)C[v], wd * xv[v], acc[v]);
+    for (int v = 0; v < VT; ++v) {
+      const int c = HS ? (int)kq4_gv_pick((uint32_t)C[v], (uint32_t)C[8 + v], p) : C[v];
+      acc[v] = fmaf((float)c, wd * xv[v], acc[v]);
+      kq4_gv_pin(acc[v]);
+    }
   }
 }
 
-// Sum over aligned runs of N (8 or 16) lanes of a DPP row; every lane ends with the same bits.
-template <int N>
-KQ4_DEV float kq4_rowN_sum(float v) {
-  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, true));  // quad xor 1
-  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, true));  // quad xor 2
-  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, true)); // half-row mirror
-  if (N == 16)
-    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, true)); // row mirror
-  return v;
-}
-
-template <int M, bool FQ, int UNIT, int D, int KIND, int G8>
-__global__ __launch_bounds__(512) void kq4_gemv_kernel(const KQ4GemvArgs a) {
+// One workgroup per 32-row set (HS = 0) or per half set (HS = 1), up to 16 waves splitting K
+// (every variant fits the 128 VGPRs that allows).
+template <int M, bool FQ, int KIND, int HS>
+__global__ __launch_bounds__(1024) void kq4_gemv_kernel(const KQ4GemvArgs a) {
   extern __shared__ __align__(16) uint8_t kq4_gv_lds[];
-  constexpr int CB = kq4_gv_cb<G8>();
-  constexpr int RSZ = 4 * G8;                     // rows per row set
-  constexpr int SLAB = kq4_gv_slab<M, KIND, G8>();
-  constexpr int NACC = KIND == 0 ? 4 * M : 4;
+  constexpr int SLAB = kq4_gv_slab<M>();
+  constexpr int NACC = KIND == 0 ? M : 4;
+  constexpr int NR = HS ? 16 : 32;                 // output rows of the workgroup
+  constexpr int NP = HS ? 2 : 1;                   // lane parities
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int nw = blockDim.x >> 6;
@@ -386,230 +296,244 @@ __global__ __launch_bounds__(512) void kq4_gemv_kernel(const KQ4GemvArgs a) {
 #pragma unroll
   for (int i = 1; i < KQ4_MAXMAT; ++i)
     if (i < a.nmat && wg >= a.mat[i].wg_begin) mi = i;
-  const uint8_t *__restrict__ w = a.mat[mi].w;
+  const int wl = wg - a.mat[mi].wg_begin;
+  const int rs = wl >> HS;                         // 32-row set within the matrix
+  const int hs = HS ? (wl & 1) : 0;
   const int rows = a.mat[mi].rows;
-  const int row0 = (wg - a.mat[mi].wg_begin) * RSZ;
+  const int row0 = rs * 32 + hs * 16;              // first output row of the workgroup
   const int nb = a.nb;
-  const int nst = (nb + CB - 1) / CB;
+  const int nst = (nb + KQ4_GV_CB - 1) / KQ4_GV_CB;
+  const uint8_t *__restrict__ wset = a.mat[mi].w + (size_t)rs * nst * KQ4_GV_CHUNK;
   uint8_t *slab = kq4_gv_lds + wave * SLAB;
-  uint8_t *sw = slab;
-  uint8_t *sq = slab + G8 * kq4_gv_pitch<KIND, G8>();
-  float (*sx)[8] = reinterpret_cast<float (*)[8]>(sq + M * kq4_gv_qts<G8>());
-
-  KQ4GvOff<UNIT, G8> off;
-  kq4_gv_offsets<UNIT, G8>(off, row0 >> 2, rows >> 2, nb, lane);
+  uint8_t *sq = slab;
+  float (*sx)[8] = reinterpret_cast<float (*)[8]>(sq + M * KQ4_GV_QTS);
+  const int h = lane >> 5;
+  const int p = HS ? (lane >> 4) & 1 : 0;
+  const int r = HS ? (lane & 15) : (lane & 31);    // row within the workgroup
+  const int rr = hs * 16 + r;                      // row within the set
 
   float acc[NACC];
 #pragma unroll
   for (int i = 0; i < NACC; ++i) acc[i] = 0.0f;
-  // D stages in flight per wave, each issued as (activations, weights) in stage order
-  KQ4GvAct<M, FQ, G8> ra[D];
-  KQ4GvStage<UNIT> rw[D];
-#pragma unroll
-  for (int d = 0; d < D; ++d) {
-    const int s0 = wave + d * nw;
-    if (s0 < nst) {
-      kq4_gv_act_load<M, FQ, G8>(ra[d], a, s0, lane);
-      kq4_gv_load<UNIT, G8>(rw[d], w, off, nb, s0, lane);
-    }
-  }
-  for (int base = wave; base < nst; base += D * nw) {
-#pragma unroll
-    for (int d = 0; d < D; ++d) {
-      const int st = base + d * nw;
-      if (st >= nst) break;
-      kq4_gv_act_put<M, FQ, G8>(ra[d], a, lane, sq, sx);
-      kq4_gv_store<UNIT, KIND, G8>(rw[d], sw, lane);
-      const int sn = st + D * nw;                  // next stage for this slot
-      if (sn < nst) {
-        kq4_gv_act_load<M, FQ, G8>(ra[d], a, sn, lane);
-        kq4_gv_load<UNIT, G8>(rw[d], w, off, nb, sn, lane);
-      }
-      const int nblk = nb - st * CB < CB ? nb - st * CB : CB;
-      if (KIND == 0)
-        kq4_gv_dot4<M, G8>(sw, sq, sx, nblk, lane, acc);
-      else
-        kq4_gv_mfma_stage<M>(sw, sq, sx, nblk, lane, acc);
-    }
+  for (int st = wave; st < nst; st += nw) {
+    // issued as (activations, weights), so quantizing the activations waits only for them
+    KQ4GvAct<M, FQ> ra;
+    KQ4GvStage<HS> rw;
+    kq4_gv_act_load<M, FQ>(ra, a, st, lane);
+    kq4_gv_load<HS>(rw, wset + (size_t)st * KQ4_GV_CHUNK, rr, h, p);
+    kq4_gv_act_put<M, FQ>(ra, a, lane, sq, sx);
+    if (KIND == 0) kq4_gv_dot4<M, HS>(rw, sq, sx, h, p, acc);
+    else kq4_gv_mfma_stage<M, HS>(rw, sq, sx, lane, p, acc);
   }
 
-  // this wave's partial sums as red[m*RSZ + row] in its slab
+  // this wave's partial sums in its slab: DOT4 red[((h*NP + p)*M + m)*NR + r], MFMA
+  // red[(p*M + token)*NR + r]
   float *__restrict__ out = a.mat[mi].out;
   const float *__restrict__ res = a.mat[mi].res;
   float *red = reinterpret_cast<float *>(slab);
+  if (nw > 1) __syncthreads();   // every wave is done with its slab
   if (KIND == 0) {
 #pragma unroll
-    for (int i = 0; i < NACC; ++i) acc[i] = kq4_rowN_sum<CB / 2>(acc[i]);
-  }
-  if (nw > 1) __syncthreads();   // every wave is done reading its slab's weights
-  if (KIND == 0) {
-    if (lane % (CB / 2) == 0) {
-      const int gl = lane / (CB / 2);
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-#pragma unroll
-        for (int m = 0; m < M; ++m) red[m * RSZ + 4 * gl + r] = acc[r * M + m];
-    }
+    for (int m = 0; m < M; ++m) red[((h * NP + p) * M + m) * NR + r] = acc[m];
   } else {
-    const int j = lane & 31, h = lane >> 5;
 #pragma unroll
     for (int v = 0; v < 4; ++v)
-      if (4 * h + v < M) red[(4 * h + v) * RSZ + j] = acc[v];
+      if (4 * h + v < M) red[(p * M + 4 * h + v) * NR + r] = acc[v];
   }
   __syncthreads();
-  // the waves' K partials of the row set, added in wave order
-  for (int i = threadIdx.x; i < RSZ * M; i += blockDim.x) {
-    const int m = i / RSZ, jj = i - m * RSZ;
-    const int row = row0 + jj;
+  // the partials of the workgroup's rows, added in a fixed order: waves, then parities (and for
+  // DOT4 each half's chain, then lo + hi as the C-tile kernel finishes)
+  for (int i = threadIdx.x; i < NR * M; i += blockDim.x) {
+    const int m = i / NR, rw = i - m * NR;
+    const int row = row0 + rw;
     if (row >= rows) continue;
-    float s = reinterpret_cast<const float *>(kq4_gv_lds)[i];
-    for (int v = 1; v < nw; ++v) s += reinterpret_cast<const float *>(kq4_gv_lds + v * SLAB)[i];
+    float s = 0.0f;
+#pragma unroll
+    for (int hh = 0; hh < (KIND == 0 ? 2 : 1); ++hh) {
+      float sh = 0.0f;
+      for (int v = 0; v < nw; ++v) {
+        const float *rv = reinterpret_cast<const float *>(kq4_gv_lds + v * SLAB);
+#pragma unroll
+        for (int pp = 0; pp < NP; ++pp) sh += rv[((hh * NP + pp) * M + m) * NR + rw];
+      }
+      s = hh == 0 ? sh : s + sh;
+    }
     const size_t o = (size_t)m * rows + row;
     out[o] = res ? res[o] + s : s;
   }
 }
 
-template <int M, bool FQ, int UNIT, int D, int KIND, int G8>
+template <int M, bool FQ, int KIND, int HS>
 static hipError_t gv_launch(const KQ4GemvArgs &a, int nw, int grid, hipStream_t s) {
-  const size_t lds = (size_t)nw * kq4_gv_slab<M, KIND, G8>();
-  static bool attr = false;   // raise the dynamic LDS limit once per variant
+  const size_t lds = (size_t)nw * kq4_gv_slab<M>();
+  static bool attr = false;   // allow more than 64 KB of dynamic LDS, once per variant
   if (!attr) {
     hipError_t e = hipFuncSetAttribute(
-        reinterpret_cast<const void *>(&kq4_gemv_kernel<M, FQ, UNIT, D, KIND, G8>),
+        reinterpret_cast<const void *>(&kq4_gemv_kernel<M, FQ, KIND, HS>),
         hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
     if (e != hipSuccess) return e;
     attr = true;
   }
-  hipLaunchKernelGGL((kq4_gemv_kernel<M, FQ, UNIT, D, KIND, G8>), dim3(grid), dim3(64 * nw), lds,
-                     s, a);
+  hipLaunchKernelGGL((kq4_gemv_kernel<M, FQ, KIND, HS>), dim3(grid), dim3(64 * nw), lds, s, a);
   return hipGetLastError();
 }
 
-// kind 0 = DOT4 on 32-row sets, 1 = MFMA on 32-row sets, 2 = DOT4 on 16-row sets
 template <int M, bool FQ>
-static hipError_t gv_launch_k(const KQ4GemvArgs &a, int kind, bool u16, int depth, int nw,
-                              int grid, hipStream_t s) {
-#define KQ4_GV_L(KIND, G8)                                                                   \
-  (depth == 2 ? (u16 ? gv_launch<M, FQ, 16, 2, KIND, G8>(a, nw, grid, s)                     \
-                     : gv_launch<M, FQ, 8, 2, KIND, G8>(a, nw, grid, s))                     \
-              : (u16 ? gv_launch<M, FQ, 16, 1, KIND, G8>(a, nw, grid, s)                     \
-                     : gv_launch<M, FQ, 8, 1, KIND, G8>(a, nw, grid, s)))
-  if (kind == 0) return KQ4_GV_L(0, 8);
-  if (kind == 1) return KQ4_GV_L(1, 8);
-  return KQ4_GV_L(0, 4);
-#undef KQ4_GV_L
+static hipError_t gv_launch_k(const KQ4GemvArgs &a, int kind, int hs, int nw, int grid,
+                              hipStream_t s) {
+  if (kind == 0)
+    return hs ? gv_launch<M, FQ, 0, 1>(a, nw, grid, s) : gv_launch<M, FQ, 0, 0>(a, nw, grid, s);
+  return hs ? gv_launch<M, FQ, 1, 1>(a, nw, grid, s) : gv_launch<M, FQ, 1, 0>(a, nw, grid, s);
 }
 
 // In-kernel quantization exists for M <= KQ4_GEMV_FQ_MAX_M.
 template <int M>
-static hipError_t gv_launch_m(const KQ4GemvArgs &a, int kind, bool fq, bool u16, int depth,
-                              int nw, int grid, hipStream_t s) {
+static hipError_t gv_launch_m(const KQ4GemvArgs &a, int kind, bool fq, int hs, int nw, int grid,
+                              hipStream_t s) {
   constexpr int MF = M <= KQ4_GEMV_FQ_MAX_M ? M : 1;
   if (fq) {
     if (M > KQ4_GEMV_FQ_MAX_M) return hipErrorInvalidValue;
-    return gv_launch_k<MF, true>(a, kind, u16, depth, nw, grid, s);
+    return gv_launch_k<MF, true>(a, kind, hs, nw, grid, s);
   }
-  return gv_launch_k<M, false>(a, kind, u16, depth, nw, grid, s);
+  return gv_launch_k<M, false>(a, kind, hs, nw, grid, s);
 }
 
-template <int KIND, int G8>
-static int slab_bytes(int n) {
-  switch (n) {
-    case 1: return kq4_gv_slab<1, KIND, G8>();
-    case 2: return kq4_gv_slab<2, KIND, G8>();
-    case 3: return kq4_gv_slab<3, KIND, G8>();
-    case 4: return kq4_gv_slab<4, KIND, G8>();
-    case 5: return kq4_gv_slab<5, KIND, G8>();
-    case 6: return kq4_gv_slab<6, KIND, G8>();
-    case 7: return kq4_gv_slab<7, KIND, G8>();
-    default: return kq4_gv_slab<8, KIND, G8>();
-  }
-}
+int kq4_gemv_slab_bytes(int n_batch) { return n_batch * KQ4_GV_QTS + KQ4_GV_XS; }
 
-int kq4_gemv_slab_bytes(int n_batch, int kind) {
-  return kind == 0 ? slab_bytes<0, 8>(n_batch)
-                   : (kind == 1 ? slab_bytes<1, 8>(n_batch) : slab_bytes<0, 4>(n_batch));
-}
-
-int kq4_gemv_rowset(int kind) { return kind == 2 ? 16 : 32; }
-
-int kq4_launch_gemv(const KQ4GemvArgs &a, int n_batch, int kind, int nw, int depth, int total_wg,
-                    hipStream_t s) {
-  if (n_batch < 1 || n_batch > KQ4_GEMV_MAX_M || total_wg <= 0 || nw < 1 || nw > 8 ||
-      kind < 0 || kind > 2 || (depth != 1 && depth != 2) ||
-      (size_t)nw * kq4_gemv_slab_bytes(n_batch, kind) > 160 * 1024)
+int kq4_launch_gemv(const KQ4GemvArgs &a, int n_batch, int kind, int half_sets, int nw,
+                    int total_wg, hipStream_t s) {
+  if (n_batch < 1 || n_batch > KQ4_GEMV_MAX_M || total_wg <= 0 || nw < 1 || nw > 16 ||
+      kind < 0 || kind > 1 || (half_sets != 0 && half_sets != 1) ||
+      (size_t)nw * kq4_gemv_slab_bytes(n_batch) > 160 * 1024)
     return (int)hipErrorInvalidValue;
-  // 16-byte units need every group and stage start 16-byte aligned: an even block count
-  bool u16 = (a.nb % 2) == 0;
-  for (int i = 0; i < a.nmat; ++i) {
-    u16 = u16 && ((uintptr_t)a.mat[i].w % 16) == 0;
-    if ((uintptr_t)a.mat[i].w % 8) return (int)hipErrorInvalidValue;
-    // per-lane offsets within a matrix are 32-bit
-    if ((size_t)(a.mat[i].rows / 4) * a.nb * 72 >= ((size_t)1 << 32)) return (int)hipErrorInvalidValue;
-  }
+  for (int i = 0; i < a.nmat; ++i)
+    if ((uintptr_t)a.mat[i].w % 16) return (int)hipErrorInvalidValue;
   const bool fq = a.xf != nullptr;
+  const int hs = half_sets;
   hipError_t e;
   switch (n_batch) {
-    case 1: e = gv_launch_m<1>(a, kind, fq, u16, depth, nw, total_wg, s); break;
-    case 2: e = gv_launch_m<2>(a, kind, fq, u16, depth, nw, total_wg, s); break;
-    case 3: e = gv_launch_m<3>(a, kind, fq, u16, depth, nw, total_wg, s); break;
-    case 4: e = gv_launch_m<4>(a, kind, fq, u16, depth, nw, total_wg, s); break;
-    case 5: e = gv_launch_m<5>(a, kind, fq, u16, depth, nw, total_wg, s); break;
-    case 6: e = gv_launch_m<6>(a, kind, fq, u16, depth, nw, total_wg, s); break;
-    case 7: e = gv_launch_m<7>(a, kind, fq, u16, depth, nw, total_wg, s); break;
-    default: e = gv_launch_m<8>(a, kind, fq, u16, depth, nw, total_wg, s); break;
+    case 1: e = gv_launch_m<1>(a, kind, fq, hs, nw, total_wg, s); break;
+    case 2: e = gv_launch_m<2>(a, kind, fq, hs, nw, total_wg, s); break;
+    case 3: e = gv_launch_m<3>(a, kind, fq, hs, nw, total_wg, s); break;
+    case 4: e = gv_launch_m<4>(a, kind, fq, hs, nw, total_wg, s); break;
+    case 5: e = gv_launch_m<5>(a, kind, fq, hs, nw, total_wg, s); break;
+    case 6: e = gv_launch_m<6>(a, kind, fq, hs, nw, total_wg, s); break;
+    case 7: e = gv_launch_m<7>(a, kind, fq, hs, nw, total_wg, s); break;
+    default: e = gv_launch_m<8>(a, kind, fq, hs, nw, total_wg, s); break;
   }
   return (int)e;
 }
 
+// ---- VQF 4x4 -> stream layout ------------------------------------------------------------------
+// One thread per 8-byte piece of the stream buffer. Piece o (byte offset in its chunk):
+//   o < 8192: unit i = o/1024, lane l = (o/16)%64, block 16*stage + 2i + (o/8)%2 of row
+//             32*set + l%32, half h = l/32. From the VQF tile the row's 16 code bytes are the
+//             dwords Q[k] at 8 + 16k + 4r (r = row%4; byte j of the row = element j in the low
+//             nibble, element j+16 in the high one), so half h's dword d is
+//             ((Q[2d] >> 4h) & 0x0F0F0F0F) | ((Q[2d+1] >> 4h) & 0x0F0F0F0F) << 4.
+//   o >= 8192: lane l = (o-8192)/16: the f16 scales of row 32*set + l%32, blocks
+//             16*stage + 8*(l/32) + 4*((o/8)%2) + 0..3 (tile byte 2r of each block's tile).
+// Rows or blocks past the matrix give zeros.
+__global__ __launch_bounds__(256) void kq4_repack_kernel(uint8_t *__restrict__ dst,
+                                                         const uint8_t *__restrict__ src,
+                                                         int rows, int nb, int nst, long total) {
+  const long k = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (k >= total) return;
+  const long chunk = k / (KQ4_GV_CHUNK / 8);
+  const int o = 8 * (int)(k - chunk * (KQ4_GV_CHUNK / 8));
+  const int set = (int)(chunk / nst), stage = (int)(chunk - (long)set * nst);
+  uint2 v = make_uint2(0, 0);
+  if (o < 8192) {
+    const int i = o >> 10, l = (o >> 4) & 63, hb = (o >> 3) & 1;
+    const int row = 32 * set + (l & 31), h = l >> 5;
+    const int b = 16 * stage + 2 * i + hb;
+    if (row < rows && b < nb) {
+      const uint8_t *tile = src + ((size_t)(row >> 2) * nb + b) * 72 + 8 + 4 * (row & 3);
+      uint32_t Q[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) Q[q] = *reinterpret_cast<const uint32_t *>(tile + 16 * q);
+      const int sh = 4 * h;
+      v.x = ((Q[0] >> sh) & 0x0F0F0F0Fu) | (((Q[1] >> sh) & 0x0F0F0F0Fu) << 4);
+      v.y = ((Q[2] >> sh) & 0x0F0F0F0Fu) | (((Q[3] >> sh) & 0x0F0F0F0Fu) << 4);
+    }
+  } else {
+    const int l = (o - 8192) >> 4, hb = (o >> 3) & 1;
+    const int row = 32 * set + (l & 31);
+    const int b0 = 16 * stage + 8 * (l >> 5) + 4 * hb;
+    uint32_t f[4] = {0, 0, 0, 0};
+    if (row < rows) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        if (b0 + u < nb)
+          f[u] = *reinterpret_cast<const uint16_t *>(
+              src + ((size_t)(row >> 2) * nb + b0 + u) * 72 + 2 * (row & 3));
+    }
+    v.x = f[0] | (f[1] << 16);
+    v.y = f[2] | (f[3] << 16);
+  }
+  *reinterpret_cast<uint2 *>(dst + chunk * KQ4_GV_CHUNK + o) = v;
+}
+
+size_t kq4_stream_bytes(int rows, int cols) {
+  const size_t sets = ((size_t)rows + 31) / 32;
+  const size_t nst = ((size_t)cols / 32 + KQ4_GV_CB - 1) / KQ4_GV_CB;
+  return sets * nst * KQ4_GV_CHUNK;
+}
+
+int kq4_launch_repack(uint8_t *dst, const uint8_t *src, int rows, int cols, hipStream_t s) {
+  const int nb = cols / 32;
+  const int nst = (nb + KQ4_GV_CB - 1) / KQ4_GV_CB;
+  const long total = (long)kq4_stream_bytes(rows, cols) / 8;
+  if (total <= 0) return 0;
+  hipLaunchKernelGGL(kq4_repack_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
+                     dst, src, rows, nb, nst, total);
+  return (int)hipGetLastError();
+}
+
 // ---- verification: exact per-block integer sums through the GEMV's integer dots --------------
-// One wave per (32-row set, block, 32-token set). S_lo / S_hi come from the MFMA kind's operand
-// builder and v_mfma (zeroing the B lanes of one K half), and are checked against the DOT4 kind's
-// kq4_dot4 sums of the same tile (the lane's row, first token of the set); a mismatch is written
-// as INT32_MIN so the test fails.
+// One wave per (32-row set, block, 32-token set), reading the weights in the stream layout.
+// S_lo / S_hi come from the MFMA kind's operands and v_mfma (zeroing the B lanes of one K half),
+// and are checked against the DOT4 kind's kq4_dot4 sums of the same half-rows (the lane's row,
+// first token of the set); a mismatch is written as INT32_MIN so the test fails.
 __global__ __launch_bounds__(64) void kq4_block_sums_kernel(int32_t *__restrict__ s_lo,
                                                             int32_t *__restrict__ s_hi,
                                                             const int8_t *__restrict__ xq,
                                                             const uint8_t *__restrict__ w,
                                                             int rows, int cols, int n_batch) {
   const int nb = cols / 32;
+  const int nst = (nb + KQ4_GV_CB - 1) / KQ4_GV_CB;
   const int lane = threadIdx.x;
   const int j = lane & 31, h = lane >> 5;
   const int row0 = blockIdx.x * 32, b = blockIdx.y, t0 = blockIdx.z * 32;
-  const int G = rows >> 2;
-  int g = (row0 + j) >> 2;
-  g = g < G ? g : G - 1;
-  const uint8_t *tile = w + ((size_t)g * nb + b) * 72;
-  const uint32_t *nib = reinterpret_cast<const uint32_t *>(tile + 8);
-  const int r = j & 3;
-  const uint32_t w0 = nib[r], w1 = nib[4 + r], w2 = nib[8 + r], w3 = nib[12 + r];
-  const kq4_v4i B = kq4_gv_bop(w0, w1, w2, w3, h ? 0 : 4);
+  const int rw = row0 + j < rows ? row0 + j : rows - 1;
+  const uint2 wv = *reinterpret_cast<const uint2 *>(w + kq4_stream_nib(rw, b, h, nst));
+  uint32_t o[4];
+  kq4_unpack_half(wv.x, wv.y, o);
+  const kq4_v4i B = {(int)o[0], (int)o[1], (int)o[2], (int)o[3]};
   const kq4_v4i Z = {0, 0, 0, 0};
   int t = t0 + j;
   t = t < n_batch ? t : n_batch - 1;
   const kq4_v4i A = *reinterpret_cast<const kq4_v4i *>(xq + (size_t)t * cols + (size_t)b * 32 + 16 * h);
   const kq4_v16i Clo = kq4_gv_mfma(A, h == 0 ? B : Z);
   const kq4_v16i Chi = kq4_gv_mfma(A, h == 1 ? B : Z);
-  // the DOT4 kind's sums for (row j, token t0): lanes 0..31 compute them for their row
+  // the DOT4 kind's sum of this lane's half-row against token t0, and the other half's
   const uint32_t *q = reinterpret_cast<const uint32_t *>(xq + (size_t)t0 * cols + (size_t)b * 32);
-  int dlo = 0, dhi = 0;
-  const uint32_t wk[4] = {w0, w1, w2, w3};
+  int dh = 0;
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    dlo = kq4_dot4(kq4_lo16(wk[k]), q[k], dlo);
-    dhi = kq4_dot4(kq4_hi16(wk[k]), q[4 + k], dhi);
-  }
+  for (int k = 0; k < 4; ++k) dh = kq4_dot4(o[k], q[4 * h + k], dh);
+  const int dx = __shfl_xor(dh, 32);
+  const int dlo = h == 0 ? dh : dx, dhi = h == 0 ? dx : dh;
   const int row = row0 + j;
   if (row >= rows) return;
 #pragma unroll
   for (int v = 0; v < 16; ++v) {
     const int m = t0 + 8 * (v >> 2) + 4 * h + (v & 3);
     if (m >= n_batch) continue;
-    const size_t o = ((size_t)m * rows + row) * nb + b;
+    const size_t oo = ((size_t)m * rows + row) * nb + b;
     int lo = Clo[v] >> 4, hi = Chi[v] >> 4;   // exact: multiples of 16
     if (m == t0 && (lo != (dlo >> 4) || hi != (dhi >> 4))) lo = hi = INT32_MIN;
-    s_lo[o] = lo;
-    s_hi[o] = hi;
+    s_lo[oo] = lo;
+    s_hi[oo] = hi;
   }
 }
 

@@ -8,13 +8,18 @@
 #define KQ4_MAXMAT 4
 #define KQ4_GEMV_FQ_MAX_M 4   // largest token count the GEMV quantizes in-kernel
 
+// Every kernel reads q4 weights in the stream layout (kq4_common.h): a VQF 4x4 matrix repacked
+// once by kq4_launch_repack into kq4_stream_bytes(rows, cols) bytes.
+size_t kq4_stream_bytes(int rows, int cols);
+int kq4_launch_repack(uint8_t *dst, const uint8_t *src, int rows, int cols, hipStream_t stream);
+
 // One weight matrix of a (possibly fused) GEMV launch. All matrices share the activation.
 struct KQ4GemvMat {
-  const uint8_t *w;     // 4x4 tiles [rows/4][nb][72]
+  const uint8_t *w;     // stream layout
   float *out;           // [M][rows]
   const float *res;     // [M][rows] or nullptr
   int rows;
-  int wg_begin;         // first workgroup (32-row set) of this matrix in the launch
+  int wg_begin;         // first workgroup (row set or half set) of this matrix in the launch
 };
 
 struct KQ4GemvArgs {
@@ -31,15 +36,13 @@ struct KQ4GemvArgs {
 int kq4_launch_quantize(const float *x, int8_t *xq, float *xd, float *xde, int n_batch, int cols,
                         int asm_tokens, hipStream_t stream, int block_major = 0);
 
-// n_batch in [1, KQ4_GEMV_MAX_M]; one workgroup per row set of kq4_gemv_rowset(kind) rows
-// (total_wg over all matrices), nw waves (1..8) splitting K, each with `depth` (1 or 2) stages in
-// flight; kind 0 = per-lane v_dot4 dots on 32-row sets, 1 = v_mfma dots on 32-row sets, 2 =
-// v_dot4 on 16-row sets; nw * kq4_gemv_slab_bytes(n_batch, kind) must fit 160 KB of LDS.
-// args.xf (in-kernel quantization) requires n_batch <= KQ4_GEMV_FQ_MAX_M.
-int kq4_launch_gemv(const KQ4GemvArgs &args, int n_batch, int kind, int nw, int depth,
+// n_batch in [1, KQ4_GEMV_MAX_M]; one workgroup per 32-row set, or per 16-row half set when
+// half_sets = 1 (total_wg over all matrices, each matrix's wg_begin counted in those units),
+// nw (1..16) waves splitting K in 16-block stages; kind 0 = per-lane v_dot4 dots, 1 = v_mfma
+// dots. args.xf (in-kernel quantization) requires n_batch <= KQ4_GEMV_FQ_MAX_M.
+int kq4_launch_gemv(const KQ4GemvArgs &args, int n_batch, int kind, int half_sets, int nw,
                     int total_wg, hipStream_t stream);
-int kq4_gemv_slab_bytes(int n_batch, int kind);
-int kq4_gemv_rowset(int kind);
+int kq4_gemv_slab_bytes(int n_batch);
 
 int kq4_launch_block_sums(int32_t *s_lo, int32_t *s_hi, const int8_t *xq, const uint8_t *w,
                           int rows, int cols, int n_batch, hipStream_t stream);

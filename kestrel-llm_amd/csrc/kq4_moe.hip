@@ -14,6 +14,8 @@
 // parallel (they are independent and exact to compute), staged in LDS, and each output then adds
 // its terms in block order in one lane. exp() is evaluated in double and rounded to float
 // (correctly rounded; the reference's libm expf agrees except in rare last-ulp cases).
+// G/U ([ne*ef rows][d cols]) and D ([d rows][ne*ef cols]) are in the stream layout; tiles are
+// addressed per (row, block) through kq4_stream_nib / kq4_stream_scale.
 #include "kq4_common.h"
 #include "kq4_internal.h"
 
@@ -84,26 +86,23 @@ __global__ __launch_bounds__(256) void kq4_moe_group_kernel(int *__restrict__ ex
   }
 }
 
-// ---- exact V4 terms of one tile row ------------------------------------------------------
-KQ4_DEV int kq4_row_dot(const uint32_t *tile, int r, const uint32_t *qa) {
-  int acc = 0;
+// ---- one weight row-block of the stream layout ---------------------------------------------
+// The 32 weights of (row, block b) as 16*(n-8) int8 (8 dwords, element order) and its scale.
+KQ4_DEV float kq4_load_rowblk(uint32_t *o, const uint8_t *__restrict__ w, int row, int b,
+                              int nst) {
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    const uint32_t w = tile[2 + 4 * k + r];
-    acc = kq4_dot4(kq4_lo16(w), qa[k], acc);
-    acc = kq4_dot4(kq4_hi16(w), qa[4 + k], acc);
+  for (int h = 0; h < 2; ++h) {
+    const uint2 v = *reinterpret_cast<const uint2 *>(w + kq4_stream_nib(row, b, h, nst));
+    kq4_unpack_half(v.x, v.y, o + 4 * h);
   }
-  return acc >> 4;   // exact: 16*S
+  return kq4_h2f(*reinterpret_cast<const uint16_t *>(w + kq4_stream_scale(row, b, nst)));
 }
 
-KQ4_DEV void kq4_load_tile(uint32_t *dst, const uint8_t *src) {
-  const uint2 *s = reinterpret_cast<const uint2 *>(src);
+KQ4_DEV int kq4_rowblk_dot(const uint32_t *o, const uint32_t *qa) {
+  int acc = 0;
 #pragma unroll
-  for (int i = 0; i < 9; ++i) {
-    const uint2 v = s[i];
-    dst[2 * i] = v.x;
-    dst[2 * i + 1] = v.y;
-  }
+  for (int k = 0; k < 8; ++k) acc = kq4_dot4(o[k], qa[k], acc);
+  return acc >> 4;   // exact: 16*S
 }
 
 KQ4_DEV void kq4_load_q(uint32_t *qa, const int8_t *src) {
@@ -127,32 +126,24 @@ __global__ __launch_bounds__(256) void kq4_moe_gu_kernel(
   const int o0 = ex_off[e], m = ex_off[e + 1] - o0;
   if (m <= 0) return;
   const int nbG = d / 32;
-  const size_t ggB = (size_t)nbG * 72;
-  const size_t grp0 = ((size_t)e * ef + (size_t)rb * 32) >> 2;   // first tile group
+  const int nstG = (nbG + KQ4_STREAM_CB - 1) / KQ4_STREAM_CB;
   const int t = threadIdx.x;
 
   for (int c0 = 0; c0 < m; c0 += pc) {
     const int np = (m - c0) < pc ? (m - c0) : pc;
-    // phase A: terms for 16 groups (8 gate, 8 up) x nbG tiles
-    for (int c = t; c < 16 * nbG; c += 256) {
+    // phase A: terms for 64 rows (32 gate, 32 up) x nbG blocks
+    for (int c = t; c < 64 * nbG; c += 256) {
       const int q = c / nbG, b = c - q * nbG;
-      const uint8_t *mat = q < 8 ? G : U;
-      const int gl = q & 7;
-      uint32_t tile[18];
-      kq4_load_tile(tile, mat + (grp0 + gl) * ggB + (size_t)b * 72);
-      float sc[4];
-      sc[0] = kq4_h2f(tile[0]); sc[1] = kq4_h2f(tile[0] >> 16);
-      sc[2] = kq4_h2f(tile[1]); sc[3] = kq4_h2f(tile[1] >> 16);
+      const uint8_t *mat = q < 32 ? G : U;
+      const int row = e * ef + rb * 32 + (q & 31);
+      uint32_t wv[8];
+      const float sc = kq4_load_rowblk(wv, mat, row, b, nstG);
       for (int p = 0; p < np; ++p) {
         const int tok = ex_pair[o0 + c0 + p] / tk;
         uint32_t qa[8];
         kq4_load_q(qa, xq + (size_t)tok * d + (size_t)b * 32);
         const float x = xd[(size_t)tok * nbG + b];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int S = kq4_row_dot(tile, r, qa);
-          s_term[((size_t)p * 64 + q * 4 + r) * nbG + b] = (sc[r] * x) * (float)S;
-        }
+        s_term[((size_t)p * 64 + q) * nbG + b] = (sc * x) * (float)kq4_rowblk_dot(wv, qa);
       }
     }
     __syncthreads();
@@ -212,28 +203,21 @@ __global__ __launch_bounds__(256) void kq4_moe_down_kernel(
   const int o0 = ex_off[e], m = ex_off[e + 1] - o0;
   if (m <= 0) return;
   const int cbe = ef / 32;
-  const size_t gdB = (size_t)(ne * ef / 32) * 72;
+  const int nstD = (ne * ef / 32 + KQ4_STREAM_CB - 1) / KQ4_STREAM_CB;
   const size_t cb0 = (size_t)e * ef / 32;
   const int t = threadIdx.x;
   for (int c0 = 0; c0 < m; c0 += pc) {
     const int np = (m - c0) < pc ? (m - c0) : pc;
-    for (int c = t; c < 8 * cbe; c += 256) {
-      const int gl = c / cbe, cb = c - gl * cbe;
-      uint32_t tile[18];
-      kq4_load_tile(tile, D + ((size_t)rb * 8 + gl) * gdB + (cb0 + cb) * 72);
-      float sc[4];
-      sc[0] = kq4_h2f(tile[0]); sc[1] = kq4_h2f(tile[0] >> 16);
-      sc[2] = kq4_h2f(tile[1]); sc[3] = kq4_h2f(tile[1] >> 16);
+    for (int c = t; c < 32 * cbe; c += 256) {
+      const int q = c / cbe, cb = c - q * cbe;
+      uint32_t wv[8];
+      const float sc = kq4_load_rowblk(wv, D, rb * 32 + q, (int)cb0 + cb, nstD);
       for (int p = 0; p < np; ++p) {
         const int pair = ex_pair[o0 + c0 + p];
         uint32_t qa[8];
         kq4_load_q(qa, avq + (size_t)pair * ef + (size_t)cb * 32);
         const float x = avd[(size_t)pair * cbe + cb];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int S = kq4_row_dot(tile, r, qa);
-          s_term[((size_t)p * 32 + gl * 4 + r) * cbe + cb] = (sc[r] * x) * (float)S;
-        }
+        s_term[((size_t)p * 32 + q) * cbe + cb] = (sc * x) * (float)kq4_rowblk_dot(wv, qa);
       }
     }
     __syncthreads();

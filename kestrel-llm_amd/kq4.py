@@ -32,6 +32,8 @@ SIGNATURES = [
     ("kq4_matmul", _I, [_P, _P, _P, _P, _I, _I, _I, _I, _U64]),
     ("kq4_matmul_multi", _I, [_I, _P, _P, _P, _P, _I, _P, _I, _I, _P]),
     ("kq4_moe_ffn", _I, [_P, _P, _P, _P, _I, _I, _P, _P, _P, _I, _I, _I, _U64]),
+    ("kq4_weights_stream_bytes", ctypes.c_size_t, [_I, _I]),
+    ("kq4_weights_prepare_dev", _I, [_P, _P, _I, _I, _P]),
     ("kq4_quantize_dev", _I, [_P, _P, _P, _P, _I, _I, _I, _P]),
     ("kq4_matmul_dev", _I, [_P, _P, _P, _P, _I, _I, _I, _I, _P]),
     ("kq4_matmul_multi_dev", _I, [_I, _P, _P, _P, _P, _I, _P, _I, _I, _P]),
@@ -177,6 +179,26 @@ def _tp(t):
 
 def _stream_ptr(stream):
     return None if stream is None else stream.cuda_stream
+
+
+def stream_bytes(rows, cols):
+    n = lib().kq4_weights_stream_bytes(rows, cols)
+    if n == 0:
+        raise KQ4Error(f"bad q4 matrix shape {rows}x{cols}")
+    return n
+
+
+def prepare_dev(w4x4, rows, cols, stream=None):
+    """Stream-layout device copy (a new uint8 tensor) of the VQF 4x4 matrix w4x4, a device
+    tensor or a host numpy array (copied to the device first); what every device-pointer call
+    takes as its weights."""
+    import torch
+    if isinstance(w4x4, np.ndarray):
+        w4x4 = torch.from_numpy(np.ascontiguousarray(w4x4, dtype=np.uint8)).cuda()
+    dst = torch.empty(stream_bytes(rows, cols), dtype=torch.uint8, device=w4x4.device)
+    check(lib().kq4_weights_prepare_dev(_tp(dst), _tp(w4x4), rows, cols, _stream_ptr(stream)),
+          "kq4_weights_prepare_dev")
+    return dst
 
 
 def quantize_dev(x, xq, xd, xde=None, chain=CHAIN_AUTO, stream=None):

@@ -42,6 +42,14 @@ def kq4():
 
 
 @pytest.fixture(scope="session")
+def kq4_cpu():
+    """libkq4 loaded without a device: only calls that touch no GPU (sizes, exports)."""
+    import kq4 as k
+    k.lib()
+    return k
+
+
+@pytest.fixture(scope="session")
 def torch_dev():
     import torch
     assert torch.cuda.is_available(), "GPU test needs a ROCm device"

@@ -84,7 +84,8 @@ def test_gpu_dense_fixture(kq4, torch_dev):
     g = load("dense.npz")
     rows, cols = int(g["rows"]), int(g["cols"])
     n = g["x"].shape[0]
-    w, x, res = _dev(torch, g["w"]), _dev(torch, g["x"]), _dev(torch, g["residual"])
+    w = kq4.prepare_dev(_dev(torch, g["w"]), rows, cols)
+    x, res = _dev(torch, g["x"]), _dev(torch, g["residual"])
     lo = torch.empty((n, rows, cols // 32), dtype=torch.int32, device="cuda")
     hi = torch.empty_like(lo)
     kq4.block_sums_dev(lo, hi, _dev(torch, g["xq"]), w, rows, cols, n)

@@ -17,14 +17,15 @@ def to_dev(torch, a):
 def test_graph_replays_match_eager(kq4, torch_dev):
     torch = torch_dev
     cols, rows, rows2 = 1024, 512, 256
-    w = to_dev(torch, synth.make_q4_weights(rows, cols, 1))
-    w2 = to_dev(torch, synth.make_q4_weights(rows2, cols, 2))
+    w = kq4.prepare_dev(to_dev(torch, synth.make_q4_weights(rows, cols, 1)), rows, cols)
+    w2 = kq4.prepare_dev(to_dev(torch, synth.make_q4_weights(rows2, cols, 2)), rows2, cols)
     x1 = to_dev(torch, synth.make_activations(1, cols, 3))
     x6 = to_dev(torch, synth.make_activations(6, cols, 4))
     x64 = to_dev(torch, synth.make_activations(64, cols, 5))
     res = to_dev(torch, synth.make_activations(6, rows, 6))
     cfg = dict(hidden=256, experts=16, top_k=4, ef=64)
-    G, U, D = (to_dev(torch, a) for a in synth.make_moe(cfg, 7))
+    G, U, D = (kq4.prepare_dev(to_dev(torch, a), r, c)
+               for a, r, c in zip(synth.make_moe(cfg, 7), (1024, 1024, 256), (256, 256, 1024)))
     X = to_dev(torch, synth.make_activations(3, 256, 8))
     lg = to_dev(torch, synth.make_logits(3, 16, 9))
     sel = torch.empty((3, 4), dtype=torch.int32, device="cuda")

@@ -20,6 +20,11 @@ def to_dev(torch, a):
     return torch.from_numpy(np.ascontiguousarray(a)).cuda()
 
 
+def wdev(kq4, torch, w, rows, cols):
+    """Device weights as the device API takes them: the stream-layout copy of the VQF tiles."""
+    return kq4.prepare_dev(to_dev(torch, w), rows, cols)
+
+
 def host(t):
     return t.cpu().numpy()
 
@@ -61,12 +66,13 @@ def test_block_sums_exact(kq4, torch_dev, orc, rows, cols, n):
     lo_o, hi_o = orc.block_sums(w, xq, rows, cols)
     lo = torch.empty((n, rows, cols // 32), dtype=torch.int32, device="cuda")
     hi = torch.empty_like(lo)
-    kq4.block_sums_dev(lo, hi, to_dev(torch, xq), to_dev(torch, w), rows, cols, n)
+    kq4.block_sums_dev(lo, hi, to_dev(torch, xq), wdev(kq4, torch, w, rows, cols), rows, cols, n)
     torch.cuda.synchronize()
     assert np.array_equal(host(lo), lo_o) and np.array_equal(host(hi), hi_o)
 
 
-GEMV_SHAPES = [(16, 256), (20, 160), (4, 32), (132, 4096), (6144, 2048), (2048, 6144)]
+GEMV_SHAPES = [(16, 256), (20, 160), (4, 32), (100, 2080), (132, 4096), (256, 12288),
+               (6144, 2048), (2048, 6144)]
 
 
 @pytest.mark.parametrize("n", [1, 2, 3, 4, 5, 8])
@@ -76,7 +82,7 @@ def test_gemv(kq4, torch_dev, orc, rows, cols, n):
     w, x = case(rows, cols, n, rows + cols + n)
     want = orc.matmul(w, x, rows, cols)
     out = torch.empty((n, rows), dtype=torch.float32, device="cuda")
-    kq4.matmul_dev(out, to_dev(torch, x), to_dev(torch, w), rows, cols)
+    kq4.matmul_dev(out, to_dev(torch, x), wdev(kq4, torch, w, rows, cols), rows, cols)
     torch.cuda.synchronize()
     r, a = rel_err(host(out), want)
     print(f"gemv rows={rows} cols={cols} n={n}: rel={r:.3e} maxabs={a:.3e}")
@@ -91,7 +97,7 @@ def test_gemv_chains_and_residual(kq4, torch_dev, orc, chain):
     res = np.random.default_rng(5).standard_normal((n, rows)).astype(np.float32)
     want = orc.matmul(w, x, rows, cols, residual=res, chain=chain)
     out = torch.empty((n, rows), dtype=torch.float32, device="cuda")
-    kq4.matmul_dev(out, to_dev(torch, x), to_dev(torch, w), rows, cols,
+    kq4.matmul_dev(out, to_dev(torch, x), wdev(kq4, torch, w, rows, cols), rows, cols,
                    residual=to_dev(torch, res), chain=chain)
     torch.cuda.synchronize()
     r, a = rel_err(host(out), want)
@@ -105,7 +111,8 @@ def test_gemv_multi_qkv(kq4, torch_dev, orc):
     ws = [synth.make_q4_weights(r, cols, 200 + i) for i, r in enumerate(rows)]
     x = synth.make_activations(n, cols, 300)
     outs = [torch.empty((n, r), dtype=torch.float32, device="cuda") for r in rows]
-    kq4.matmul_multi_dev(outs, to_dev(torch, x), [to_dev(torch, w) for w in ws], rows, cols)
+    kq4.matmul_multi_dev(outs, to_dev(torch, x),
+                         [wdev(kq4, torch, w, r, cols) for w, r in zip(ws, rows)], rows, cols)
     torch.cuda.synchronize()
     for o, w, r in zip(outs, ws, rows):
         rr, _ = rel_err(host(o), orc.matmul(w, x, r, cols))
@@ -121,7 +128,7 @@ def test_gemm_bit_exact(kq4, torch_dev, orc, n, chain):
     res = np.random.default_rng(n).standard_normal((n, rows)).astype(np.float32)
     want = orc.matmul(w, x, rows, cols, residual=res, chain=chain)
     out = torch.empty((n, rows), dtype=torch.float32, device="cuda")
-    kq4.matmul_dev(out, to_dev(torch, x), to_dev(torch, w), rows, cols,
+    kq4.matmul_dev(out, to_dev(torch, x), wdev(kq4, torch, w, rows, cols), rows, cols,
                    residual=to_dev(torch, res), chain=chain)
     torch.cuda.synchronize()
     got = host(out)
@@ -140,6 +147,7 @@ def test_gemm_from_prequantized(kq4, torch_dev, orc):
     xq, xd = orc.quantize(x, cols)
     want = orc.matmul_q(w, xq, xd, rows, cols)
     out = torch.empty((n, rows), dtype=torch.float32, device="cuda")
-    kq4.matmul_q_dev(out, to_dev(torch, xq), to_dev(torch, xd), to_dev(torch, w), rows, cols, n)
+    kq4.matmul_q_dev(out, to_dev(torch, xq), to_dev(torch, xd), wdev(kq4, torch, w, rows, cols),
+                     rows, cols, n)
     torch.cuda.synchronize()
     assert np.array_equal(host(out), want)

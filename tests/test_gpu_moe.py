@@ -57,7 +57,8 @@ def test_moe_stages(kq4, torch_dev, orc, shape, T):
     sel, pr = orc.moe_route(synth.make_logits(T, ne, 60 + T), tk)
     Y_o, st = orc.moe_ffn(X, sel, pr, G, U, D, ne, d, ef, stages=True)
 
-    dG, dU, dD = (to_dev(torch, a) for a in (G, U, D))
+    dG, dU = (kq4.prepare_dev(to_dev(torch, a), ne * ef, d) for a in (G, U))
+    dD = kq4.prepare_dev(to_dev(torch, D), d, ne * ef)
     dX, dsel, dpr = to_dev(torch, X), to_dev(torch, sel), to_dev(torch, pr)
     Y = torch.empty((T, d), dtype=torch.float32, device="cuda")
     gate = torch.zeros((T * tk, ef), dtype=torch.float32, device="cuda")
