@@ -13,8 +13,8 @@ region.
 
 value = algorithmic bytes per step (weights N*K*18/32 + activations M*K*4 + outputs M*N*4 +
 residuals M*N*4) / step time, in GB/s. roofline: the dominant kernel (the fused gate/up GEMV,
-launched exactly as in the step), each launch bracketed by HIP events on its stream, against
-MI355X HBM peak 8 TB/s. extras: BASELINE.json configs 3-5 (Qwen3-8B decode GEMVs, prefill GEMM,
+launched exactly as in the step, once per layer's weights), its launches captured back to back
+as a graph and replayed between HIP events on their stream, against MI355X HBM peak 8 TB/s. extras: BASELINE.json configs 3-5 (Qwen3-8B decode GEMVs, prefill GEMM,
 MoE FFN). cpu_baseline: the reference's own x86-64 path (oracle/_ref, built from
 /root/reference) on a bounded sample.
 
@@ -145,19 +145,25 @@ def run_gpu(args):
     ms_graph = timed(graph.replay, args.steps)
     total_bytes = step_bytes(m) * CFG["layers"]
 
-    # dominant kernel: the fused gate/up GEMV launch exactly as the step issues it, each launch
-    # bracketed by HIP events on the stream it runs on, rotating over the 28 layers' weights
+    # dominant kernel: the fused gate/up GEMV launch exactly as the step issues it, one per
+    # layer's weights, captured as a graph of back-to-back launches and replayed between HIP
+    # events recorded on the stream the launches run on
     st = torch.cuda.current_stream()
-    reps = max(2 * CFG["layers"], args.steps)
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-          for _ in range(reps)]
-    for i in range(reps):
-        L = layers[i % len(layers)]
-        ev[i][0].record(st)
-        kq4.matmul_multi_dev([og, ou], x, [L["gate"], L["up"]], [f, f], h, stream=st)
-        ev[i][1].record(st)
+    gu = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gu):
+        for L in layers:
+            kq4.matmul_multi_dev([og, ou], x, [L["gate"], L["up"]], [f, f], h,
+                                 stream=torch.cuda.current_stream())
+    gu.replay()
+    reps = max(4, args.steps // 4)
     torch.cuda.synchronize()
-    us_launch = sum(a.elapsed_time(b) for a, b in ev) * 1e3 / reps
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    for _ in range(reps):
+        gu.replay()
+    e1.record(st)
+    torch.cuda.synchronize()
+    us_launch = e0.elapsed_time(e1) * 1e3 / (reps * len(layers))
     achieved = gate_up_bytes(m) / (us_launch * 1e-6) / 1e9
     return dict(ms_per_step=ms_graph, ms_eager=ms_eager,
                 value=total_bytes / (ms_graph * 1e-3) / 1e9,
@@ -180,21 +186,30 @@ def copy_calibration(mib=512, reps=10):
     return dict(copy_mib=mib, reps=reps)
 
 
-def _time_loop(torch, stream, fn, reps, warm=None, cycle=None):
-    """Average us per call of fn(i) over reps calls, after a warm-up that calls every rotated
-    copy (cycle = their number) at least once."""
-    if warm is None:
-        warm = max(3, cycle or 0)
-    for i in range(warm):
-        fn(i)
+def _time_graph(torch, fn, n, reps=5):
+    """Average us per call of fn(0..n-1) (one call per rotated weight copy): the n calls are
+    captured as one HIP graph and replayed reps times between events on the capture stream, so
+    no host launch cost is in the timed region. An eager pass first sizes the library's
+    workspaces and touches every copy."""
+    st = torch.cuda.Stream()
+    with torch.cuda.stream(st):
+        for i in range(n):
+            fn(i, st)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=st):
+        for i in range(n):
+            fn(i, st)
+    g.replay()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    for i in range(reps):
-        fn(warm + i)
-    e1.record(stream)
+    e0.record(st)
+    for _ in range(reps):
+        with torch.cuda.stream(st):
+            g.replay()
+    e1.record(st)
     torch.cuda.synchronize()
-    return e0.elapsed_time(e1) * 1e3 / reps   # us per call
+    return e0.elapsed_time(e1) * 1e3 / (reps * n)
 
 
 ROTATE_BYTES = 640e6   # distinct weight bytes each measured op cycles through (> 256 MB MALL)
@@ -209,16 +224,16 @@ def _copies(torch, arr, rows, cols):
     return [t] + [t.clone() for _ in range(n - 1)]
 
 
-def run_extras(reps=20):
+def run_extras():
     """BASELINE.json configs 3-5 (reported beside the headline line, each on its own):
     Qwen3-8B decode GEMVs at M in {1,2,4,8} (us/call, GB/s), prefill GEMM at M in {512, 2048}
     (int8 TOPS vs 5.0 POPS dense), Qwen3-30B-A3B MoE FFN at T in {1, 64}. Every measured op
-    cycles through > 640 MB of distinct weight copies, so its weights stream from HBM."""
+    cycles through > 640 MB of distinct weight copies, so its weights stream from HBM; each is
+    timed as a graph replay (_time_graph)."""
     import torch
 
     import kq4
 
-    stream = torch.cuda.current_stream()
     cfg = synth.QWEN3_8B
     h, f = cfg["hidden"], cfg["ffn"]
     qkv = (cfg["q_heads"] + 2 * cfg["kv_heads"]) * cfg["head_dim"]
@@ -233,13 +248,12 @@ def run_extras(reps=20):
         xf = torch.from_numpy(synth.make_activations(m, f, 30 + m)).cuda()
         og, ou = torch.empty((m, f), device="cuda"), torch.empty((m, f), device="cuda")
         od, oq = torch.empty((m, h), device="cuda"), torch.empty((m, qkv), device="cuda")
-        t_gu = _time_loop(torch, stream, lambda i: kq4.matmul_multi_dev(
-            [og, ou], x, [G[i % len(G)], U[i % len(U)]], [f, f], h, stream=stream), reps,
-            cycle=len(G))
-        t_dn = _time_loop(torch, stream, lambda i: kq4.matmul_dev(
-            od, xf, D[i % len(D)], h, f, stream=stream), reps, cycle=len(D))
-        t_q = _time_loop(torch, stream, lambda i: kq4.matmul_dev(
-            oq, x, Q[i % len(Q)], qkv, h, stream=stream), reps, cycle=len(Q))
+        t_gu = _time_graph(torch, lambda i, st: kq4.matmul_multi_dev(
+            [og, ou], x, [G[i], U[i]], [f, f], h, stream=st), len(G))
+        t_dn = _time_graph(torch, lambda i, st: kq4.matmul_dev(
+            od, xf, D[i], h, f, stream=st), len(D))
+        t_q = _time_graph(torch, lambda i, st: kq4.matmul_dev(
+            oq, x, Q[i], qkv, h, stream=st), len(Q))
         b_gu = 2 * f * h * 18 // 32 + m * h * 4 + 2 * m * f * 4
         b_dn = h * f * 18 // 32 + m * f * 4 + m * h * 4
         b_q = qkv * h * 18 // 32 + m * h * 4 + m * qkv * 4
@@ -254,17 +268,18 @@ def run_extras(reps=20):
         xf = torch.from_numpy(synth.make_activations(m, f, 41)).cuda()
         og = torch.empty((m, f), device="cuda")
         od = torch.empty((m, h), device="cuda")
-        r = max(3, reps // 4)
-        t_g = _time_loop(torch, stream, lambda i: kq4.matmul_dev(
-            og, x, G[i % len(G)], f, h, stream=stream), r, warm=1)
-        t_d = _time_loop(torch, stream, lambda i: kq4.matmul_dev(
-            od, xf, D[i % len(D)], h, f, stream=stream), r, warm=1)
+        n = 4
+        t_g = _time_graph(torch, lambda i, st: kq4.matmul_dev(
+            og, x, G[i], f, h, stream=st), n, reps=2)
+        t_d = _time_graph(torch, lambda i, st: kq4.matmul_dev(
+            od, xf, D[i], h, f, stream=st), n, reps=2)
         ops = 2.0 * m * f * h
         pre[f"M{m}"] = {"gate_us": round(t_g, 1), "gate_TOPS": round(ops / t_g / 1e6, 1),
                         "down_us": round(t_d, 1), "down_TOPS": round(ops / t_d / 1e6, 1),
                         "frac_int8_peak": round(ops / min(t_g, t_d) / 1e6 / 5000.0, 4)}
     out["qwen3_8b_prefill"] = pre
     del G, U, D, Q
+    torch.cuda.empty_cache()
     mcfg = synth.QWEN3_30B_A3B_MOE
     d, ne, tk, ef = mcfg["hidden"], mcfg["experts"], mcfg["top_k"], mcfg["ef"]
     Gm, Um, Dm = synth.make_moe(mcfg, 50)
@@ -277,9 +292,10 @@ def run_extras(reps=20):
         sel = torch.empty((T, tk), dtype=torch.int32, device="cuda")
         pr = torch.empty((T, tk), device="cuda")
         Y = torch.empty((T, d), device="cuda")
-        kq4.moe_route_dev(sel, pr, lg, tk, stream=stream)
-        t = _time_loop(torch, stream, lambda i: kq4.moe_ffn_dev(
-            Y, X, sel, pr, *layers[i % len(layers)], ne, d, ef, stream=stream), reps)
+        kq4.moe_route_dev(sel, pr, lg, tk)
+        torch.cuda.synchronize()
+        t = _time_graph(torch, lambda i, st: kq4.moe_ffn_dev(
+            Y, X, sel, pr, *layers[i], ne, d, ef, stream=st), len(layers))
         n_exp = len(set(sel.cpu().numpy().reshape(-1).tolist()))
         byts = n_exp * 3 * ef * d * 18 // 32 + T * d * 8
         moe[f"T{T}"] = {"us": round(t, 2), "experts": n_exp, "GBs": round(byts / t / 1e3, 1)}
@@ -385,7 +401,8 @@ def main():
                                f"down+res) x {CFG['layers']} layers, M={args.m}",
                    "global_batch": args.m, "bytes_per_step": g["total_bytes"],
                    "launch": "one HIP graph replay per step (4 launches per layer)",
-                   "weights": "q4_0 4x4 tiles, int8 block-32 activations"},
+                   "weights": "q4_0 4x4 tiles (repacked once into the kq4 stream layout), "
+                              "int8 block-32 activations"},
         "gate_up_us_per_call": round(g["us_gate_up"], 3),
         "roofline": {"bound": "hbm", "achieved": round(g["achieved"], 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(g["achieved"] / HBM_PEAK_GBS, 4),

@@ -108,8 +108,8 @@ int asm_tokens_for(int chain, int n) {
   return 0;
 }
 
-// Integer-dot kind of the GEMV: per-lane v_dot4 for few tokens (fewest instructions per byte),
-// v_mfma from the token count where the dot4 work (which grows with M) costs more.
+// Integer-dot kind of the GEMV: per-lane v_dot4 for one token, v_mfma from two tokens on (the
+// dot4 work grows with M, the MFMA's does not; at one token both measure the same).
 // KQ4_GEMV_KIND=0/1 forces one (for measurement).
 int gemv_kind(int n) {
   static const int env = env_int("KQ4_GEMV_KIND", -1);
@@ -119,7 +119,7 @@ int gemv_kind(int n) {
 }
 
 // GEMV launch shape. Workgroups: one per 32-row set, or per 16-row half set when the launch
-// has fewer sets than the chip has CUs (so that every CU streams). Waves per workgroup (splitting
+// has fewer than two sets per CU (so that every CU streams, with a second workgroup to overlap). Waves per workgroup (splitting
 // K in 16-block stages): about KQ4_GEMV_WPCU (32) per CU over the launch, at most one per stage
 // and 16 per workgroup, balanced so that no wave has more stages than another by more than one.
 // KQ4_GEMV_HS / KQ4_GEMV_WAVES / KQ4_GEMV_MAXW override (for measurement).
@@ -127,7 +127,7 @@ void plan_gemv(int sets, int nb, int ncu, int *half_out, int *nw_out) {
   static const int force_hs = env_int("KQ4_GEMV_HS", -1);
   static const int force_w = env_int("KQ4_GEMV_WAVES", 0);
   static const int per_cu = env_int("KQ4_GEMV_WPCU", 32);
-  const int hs = force_hs == 0 || force_hs == 1 ? force_hs : (sets < ncu ? 1 : 0);
+  const int hs = force_hs == 0 || force_hs == 1 ? force_hs : (sets < 2 * ncu ? 1 : 0);
   const int wgs = sets << hs;
   const int nst = (nb + 15) / 16;
   int want = force_w > 0 ? force_w : (per_cu * ncu + wgs - 1) / wgs;
@@ -344,7 +344,7 @@ int dev_weights(DevState *ds, uint64_t wkey, const uint8_t *w, int rows, int col
   hipError_t e = (hipError_t)kq4_launch_repack(dst, static_cast<const uint8_t *>(ds->hstage.p),
                                                rows, cols, nullptr);
   if (e != hipSuccess) {
-    if (wkey) hipFree(dst);
+    if (wkey) (void)hipFree(dst);
     return fail(KQ4_EHIP, "weight repack: %s", hipGetErrorString(e));
   }
   if (wkey) {
@@ -388,22 +388,22 @@ int kq4_init(int device) {
 
 void kq4_shutdown(void) {
   int cur = 0;
-  hipGetDevice(&cur);
+  (void)hipGetDevice(&cur);
   for (int d = 0; d < kMaxDev; ++d) {
     DevState &s = g_dev[d];
     if (!s.ready) continue;
-    hipSetDevice(d);
-    hipDeviceSynchronize();
+    (void)hipSetDevice(d);
+    (void)hipDeviceSynchronize();
     Buf *bufs[] = {&s.ws, &s.hx, &s.hres, &s.hout, &s.hw, &s.hsel, &s.hpr, &s.hstage};
     for (Buf *b : bufs) {
-      if (b->p) hipFree(b->p);
+      if (b->p) (void)hipFree(b->p);
       *b = Buf();
     }
-    for (auto &kv : s.wcache) hipFree(kv.second.p);
+    for (auto &kv : s.wcache) (void)hipFree(kv.second.p);
     s.wcache.clear();
     s.ready = false;
   }
-  hipSetDevice(cur);
+  (void)hipSetDevice(cur);
 }
 
 int kq4_quantize_dev(int8_t *xq, float *xd, float *xde, const float *x, int n_batch, int cols,
@@ -516,7 +516,7 @@ int kq4_weights_upload(uint64_t wkey, const uint8_t *w4x4, int rows, int cols) {
     std::lock_guard<std::mutex> lk(g_mu);
     auto it = ds->wcache.find(wkey);
     if (it != ds->wcache.end()) {
-      hipFree(it->second.p);
+      (void)hipFree(it->second.p);
       ds->wcache.erase(it);
     }
   }
@@ -602,9 +602,9 @@ int kq4_matmul_multi(int n_mats, float *const *out, const float *const *residual
   }
   bool any_tmp = false;
   for (int i = 1; i < n_mats; ++i) any_tmp = any_tmp || tw[i].p;
-  if (any_tmp) hipDeviceSynchronize();
+  if (any_tmp) (void)hipDeviceSynchronize();
   for (int i = 1; i < n_mats; ++i)
-    if (tw[i].p) hipFree(tw[i].p);
+    if (tw[i].p) (void)hipFree(tw[i].p);
   return ok;
 }
 
@@ -644,10 +644,10 @@ int kq4_moe_ffn(float *Y, const float *X, const int *sel, const float *pr, int T
                       T, tk, dG, dU, dD, ne, d, ef, nullptr) == KQ4_OK &&
       hipMemcpy(Y, ds->hout.p, xb, hipMemcpyDeviceToHost) == hipSuccess)
     ok = 1;
-  if (tg.p || tu.p || td.p) hipDeviceSynchronize();
-  if (tg.p) hipFree(tg.p);
-  if (tu.p) hipFree(tu.p);
-  if (td.p) hipFree(td.p);
+  if (tg.p || tu.p || td.p) (void)hipDeviceSynchronize();
+  if (tg.p) (void)hipFree(tg.p);
+  if (tu.p) (void)hipFree(tu.p);
+  if (td.p) (void)hipFree(td.p);
   return ok;
 }
 

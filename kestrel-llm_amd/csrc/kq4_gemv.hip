@@ -330,8 +330,7 @@ __global__ __launch_bounds__(1024) void kq4_gemv_kernel(const KQ4GemvArgs a) {
   // red[(p*M + token)*NR + r]
   float *__restrict__ out = a.mat[mi].out;
   const float *__restrict__ res = a.mat[mi].res;
-  float *red = reinterpret_cast<float *>(slab);
-  if (nw > 1) __syncthreads();   // every wave is done with its slab
+  float *red = reinterpret_cast<float *>(slab);   // only this wave used its slab so far
   if (KIND == 0) {
 #pragma unroll
     for (int m = 0; m < M; ++m) red[((h * NP + p) * M + m) * NR + r] = acc[m];
