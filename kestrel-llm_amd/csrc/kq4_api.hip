@@ -267,8 +267,9 @@ int matmul_impl(int n_mats, float *const *out, const float *const *res, const ui
 int moe_impl(float *Y, const float *X, const int *sel, const float *pr, int T, int tk,
              const uint8_t *G, const uint8_t *U, const uint8_t *D, int ne, int d, int ef,
              float *g_out, float *u_out, float *av_out, const float *av_in, hipStream_t s) {
-  if (T < 0 || tk < 1 || tk > 32 || ne < 1 || d <= 0 || d % 32 || ef <= 0 || ef % 32)
-    return fail(KQ4_EINVAL, "moe: T=%d tk=%d ne=%d d=%d ef=%d", T, tk, ne, d, ef);
+  if (T < 0 || tk < 1 || tk > 32 || ne < 1 || !kq4_moe_shape_ok(d, ef))
+    return fail(KQ4_EINVAL, "moe: T=%d tk=%d ne=%d d=%d ef=%d (need d, ef %% 32 == 0, "
+                "d <= 4096, ef <= 3840)", T, tk, ne, d, ef);
   if (!G || !U || !D || (uintptr_t)G % 16 || (uintptr_t)U % 16 || (uintptr_t)D % 16)
     return fail(KQ4_EINVAL, "moe: null or misaligned (16 B) weights");
   if (T == 0) return KQ4_OK;
@@ -277,23 +278,23 @@ int moe_impl(float *Y, const float *X, const int *sel, const float *pr, int T, i
   if (rc) return rc;
   const size_t np = (size_t)T * tk;
   const size_t need = al256((ne + 1) * sizeof(int)) + al256(np * sizeof(int)) +
-                      al256((size_t)T * d) + al256((size_t)T * (d / 32) * sizeof(float)) +
-                      al256(np * ef * sizeof(float)) + al256(np * ef) +
+                      al256(ne * sizeof(int)) + al256((size_t)T * d) +
+                      al256((size_t)T * (d / 32) * sizeof(float)) + al256(np * ef) +
                       al256(np * (ef / 32) * sizeof(float)) + al256(np * d * sizeof(float));
   if ((rc = ensure(ds->ws, need))) return rc;
   Carve cv{static_cast<char *>(ds->ws.p)};
   KQ4MoeWs ws;
   ws.ex_off = cv.take<int>(ne + 1);
   ws.ex_pair = cv.take<int>(np);
+  ws.act = cv.take<int>(ne);
   ws.xq = cv.take<int8_t>((size_t)T * d);
   ws.xd = cv.take<float>((size_t)T * (d / 32));
-  ws.av = av_out ? av_out : cv.take<float>(np * ef);
-  if (av_out) cv.take<float>(np * ef);
   ws.avq = cv.take<int8_t>(np * ef);
   ws.avd = cv.take<float>(np * (ef / 32));
   ws.P = cv.take<float>(np * d);
+  ws.ncu = ds->ncu;
   KQ4_HIP((hipError_t)kq4_launch_moe_dbg(Y, X, sel, pr, T, tk, G, U, D, ne, d, ef, ws, g_out,
-                                         u_out, av_in, s));
+                                         u_out, av_out, av_in, s));
   return KQ4_OK;
 }
 
@@ -476,7 +477,7 @@ int kq4_block_sums_dev(int32_t *s_lo, int32_t *s_hi, const int8_t *xq, const uin
 
 int kq4_moe_route_dev(int *sel, float *pr, const float *logits, int T, int ne, int tk,
                       void *stream) {
-  if (T < 0 || ne < 1 || tk < 1 || tk > 32 || tk > ne)
+  if (T < 0 || ne < 1 || ne > 2048 || tk < 1 || tk > 32 || tk > ne)
     return fail(KQ4_EINVAL, "route: T=%d ne=%d tk=%d", T, ne, tk);
   if (T == 0) return KQ4_OK;
   KQ4_HIP((hipError_t)kq4_launch_moe_route(sel, pr, logits, T, ne, tk, (hipStream_t)stream));
@@ -623,7 +624,7 @@ int kq4_moe_ffn(float *Y, const float *X, const int *sel, const float *pr, int T
   }
   DevState *ds = nullptr;
   if (cur_dev(&ds)) return 0;
-  if (ne < 1 || d <= 0 || d % 32 || ef <= 0 || ef % 32) {
+  if (ne < 1 || !kq4_moe_shape_ok(d, ef)) {
     fail(KQ4_EINVAL, "moe_ffn: ne=%d d=%d ef=%d", ne, d, ef);
     return 0;
   }

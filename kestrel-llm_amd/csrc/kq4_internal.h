@@ -65,16 +65,19 @@ int kq4_launch_moe_route(int *sel, float *pr, const float *logits, int T, int ne
 struct KQ4MoeWs {
   int *ex_off;   // [ne+1]
   int *ex_pair;  // [T*tk] (t*tk+j) grouped by expert
+  int *act;      // [ne] active experts in id order, -1 past them
   int8_t *xq;    // [T][d]
   float *xd;     // [T][d/32]
-  float *av;     // [T*tk][ef]
   int8_t *avq;   // [T*tk][ef]
   float *avd;    // [T*tk][ef/32]
   float *P;      // [T*tk][d]
+  int ncu;       // compute units of the device (sizes the down projection's workgroups)
 };
+// Shapes the MoE kernels take: d, ef multiples of 32, d <= 4096, ef <= 3840.
+int kq4_moe_shape_ok(int d, int ef);
 int kq4_launch_moe_dbg(float *Y, const float *X, const int *sel, const float *pr, int T, int tk,
                        const uint8_t *G, const uint8_t *U, const uint8_t *D, int ne, int d,
-                       int ef, const KQ4MoeWs &ws, float *g_out, float *u_out,
+                       int ef, const KQ4MoeWs &ws, float *g_out, float *u_out, float *av_out,
                        const float *av_in, hipStream_t s);
 int kq4_launch_moe(float *Y, const float *X, const int *sel, const float *pr, int T, int tk,
                    const uint8_t *G, const uint8_t *U, const uint8_t *D, int ne, int d, int ef,

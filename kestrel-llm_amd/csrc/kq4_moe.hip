@@ -4,171 +4,345 @@
 // src/model/vllm_safetensors.c:12921-13398 and its batched twin st_moe_ffn_sparse_q4_batch_arm
 // :14894-15064, int8 track VLLM_ACTQ=1):
 //   route   top-k by insertion (ties -> smaller id), p = fl(exp(l - max) * fl(1/sum))
-//   group   expert -> (token, rank) table in (token, rank) order          (:15004-15018)
+//   group   expert -> (token, rank) table                                  (:15004-15018)
 //   gu      per (t,j), expert e: g/u rows [e*ef, e*ef+ef), V4 chain
 //           acc = fl(acc + fl(fl(sc*xd) * S)) over blocks ascending        (:11861-11924)
 //           av = fl(fl(g / fl(1 + exp(-g))) * u), re-quantized per 32 rows  (:12671-12675)
 //   down    unweighted P[(t,j)][n] over the column band of expert e, V4 chain (:14799-14840)
 //   combine y = fl(y + fl(p * P)) for j ascending from 0                    (:14875-14886)
-// Every fp32 chain is the reference's: the per-block terms fl(fl(sc*xd)*S) are computed in
-// parallel (they are independent and exact to compute), staged in LDS, and each output then adds
-// its terms in block order in one lane. exp() is evaluated in double and rounded to float
-// (correctly rounded; the reference's libm expf agrees except in rare last-ulp cases).
-// G/U ([ne*ef rows][d cols]) and D ([d rows][ne*ef cols]) are in the stream layout; tiles are
-// addressed per (row, block) through kq4_stream_nib / kq4_stream_scale.
+// Every fp32 chain is the reference's, bit for bit. exp() is evaluated in double and rounded to
+// float (correctly rounded; the reference's libm expf agrees except in rare last-ulp cases).
+//
+// Four launches: prep (grouping + activation quantizer), gate/up, down, combine. The weights are
+// in the stream layout (kq4_common.h): G/U as [ne*ef rows][d cols], D as [d rows][ne*ef cols].
+// The gate/up and down kernels stream them the way the decode GEMV does: one workgroup per
+// (active expert, 32-row set), its waves splitting K, each wave holding its chunk's weights in
+// registers as loaded (full-width coalesced loads), the integer dots on
+// v_mfma_i32_32x32x32_i8 with A = the expert's (token, rank) pairs' codes (4 or 8 per pass)
+// and B = the lanes' weight registers. The reference's serial chain over the blocks is kept
+// exactly: each wave computes its blocks' terms fl(fl(sc*xd)*S) in registers, then the waves
+// add them to the running sum one after another in block order, handing the sum on through LDS
+// (one barrier per wave). SiLU, the product and the av re-quantization are fused into the gate/up
+// kernel's end (a 32-row set is exactly one quantization block of av).
 #include "kq4_common.h"
 #include "kq4_internal.h"
 
 #define KQ4_MOE_MAXTK 32
+#define KQ4_MOE_MAXNE 2048  // routing: a lane's experts fit one 32-bit mask
+#define KQ4_MOE_PCG 4       // gate/up pairs per pass: MFMA token rows 4*(lane/32)+v, v < 2
+#define KQ4_MOE_PCD 8       // down pairs per pass: token rows 4*(lane/32)+v, v < 4
+#define KQ4_MOE_QTS 672     // LDS bytes per pair row of a 16-block stage's codes
+#define KQ4_MOE_QTS8 320    // the same for an 8-block half stage
+
+typedef int kq4_v4i __attribute__((ext_vector_type(4)));
+typedef int kq4_v16i __attribute__((ext_vector_type(16)));
+
+// LDS slab of one stage's activations for pc pairs: codes [pair][qpos(block)] then scales
+// [block][pair].
+constexpr int kq4_moe_slab(int blocks, int pc) {
+  return pc * (blocks == 16 ? KQ4_MOE_QTS : KQ4_MOE_QTS8) + blocks * pc * 4;
+}
 
 KQ4_DEV float kq4_expf(float x) { return (float)exp((double)x); }
 
-// ---- routing + expert grouping (one workgroup) -------------------------------------------
+// Block pairs at an 80-B pitch: the two K halves' 16-B reads spread over the banks.
+KQ4_DEV int kq4_moe_qpos(int blk) { return (blk >> 1) * 80 + (blk & 1) * 32; }
+
+KQ4_DEV kq4_v16i kq4_moe_mfma(kq4_v4i a, kq4_v4i b) {
+  const kq4_v16i z = {0};
+  return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, z, 0, 0, 0);
+}
+
+// Materialises x here (keeps the unrolled block loop from sinking every term to its end).
+KQ4_DEV void kq4_moe_pin(float &x) { asm volatile("" : "+v"(x)); }
+
+// Marks the packed weights as changed here, so the per-pass unpacking is not hoisted out of the
+// pass loop (the unpacked operands take twice the registers).
+template <int N>
+KQ4_DEV void kq4_moe_touch(uint32_t (&a)[N]) {
+#pragma unroll
+  for (int i = 0; i < N; ++i) asm volatile("" : "+v"(a[i]));
+}
+
+// ---- routing (one wave per token) -----------------------------------------------------------
+// The k largest logits, ties to the smaller id, in order: the reference's insertion top-k
+// (:12968-12984) gives the same list (a NaN logit is never inserted; -inf is, into an empty
+// slot). Then p = fl(exp(l - max)) summed in rank order, scaled by fl(1/sum).
 __global__ __launch_bounds__(256) void kq4_moe_route_kernel(int *__restrict__ sel,
                                                             float *__restrict__ pr,
                                                             const float *__restrict__ logits,
                                                             int T, int ne, int tk) {
-  for (int t = threadIdx.x; t < T; t += blockDim.x) {
-    const float *lg = logits + (size_t)t * ne;
-    int sl[KQ4_MOE_MAXTK];
-    float sv[KQ4_MOE_MAXTK];
-    for (int k = 0; k < tk; ++k) { sl[k] = -1; sv[k] = -INFINITY; }
-    for (int e = 0; e < ne; ++e) {
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (t >= T) return;   // whole waves
+  const float *lg = logits + (size_t)t * ne;
+  uint32_t taken = 0;   // bit i: this lane's expert lane + 64*i is already selected
+  for (int k = 0; k < tk; ++k) {
+    float bv = -INFINITY;
+    int be = -1;
+    for (int i = 0, e = lane; e < ne; ++i, e += 64) {
       const float v = lg[e];
-      for (int k = 0; k < tk; ++k) {
-        if (v > sv[k] || (v == sv[k] && (sl[k] < 0 || e < sl[k]))) {
-          for (int q = tk - 1; q > k; --q) { sl[q] = sl[q - 1]; sv[q] = sv[q - 1]; }
-          sl[k] = e;
-          sv[k] = v;
-          break;
-        }
-      }
+      if (!((taken >> i) & 1u) && v == v && (be < 0 || v > bv)) { bv = v; be = e; }
     }
+    // wave arg-max, ties to the smaller id (-1 = no candidate)
+#pragma unroll
+    for (int s = 32; s > 0; s >>= 1) {
+      const float ov = __shfl_xor(bv, s);
+      const int oe = __shfl_xor(be, s);
+      if (oe >= 0 && (be < 0 || ov > bv || (ov == bv && oe < be))) { bv = ov; be = oe; }
+    }
+    if (be >= 0 && (be & 63) == lane) taken |= 1u << (be >> 6);
+    if (lane == 0) {
+      sel[(size_t)t * tk + k] = be;
+      pr[(size_t)t * tk + k] = be >= 0 ? bv : -INFINITY;   // the logit, until the pass below
+    }
+  }
+  if (lane == 0) {
+    float *pt = pr + (size_t)t * tk;
     float mx = -INFINITY;
-    for (int k = 0; k < tk; ++k) mx = sv[k] > mx ? sv[k] : mx;
-    float p[KQ4_MOE_MAXTK];
+    for (int k = 0; k < tk; ++k) mx = pt[k] > mx ? pt[k] : mx;
     float sum = 0.0f;
-    for (int k = 0; k < tk; ++k) { p[k] = kq4_expf(sv[k] - mx); sum += p[k]; }
+    for (int k = 0; k < tk; ++k) sum += kq4_expf(pt[k] - mx);
     const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
-    for (int k = 0; k < tk; ++k) {
-      sel[(size_t)t * tk + k] = sl[k];
-      pr[(size_t)t * tk + k] = p[k] * inv;
-    }
+    for (int k = 0; k < tk; ++k) pt[k] = kq4_expf(pt[k] - mx) * inv;
   }
 }
 
-__global__ __launch_bounds__(256) void kq4_moe_group_kernel(int *__restrict__ ex_off,
-                                                            int *__restrict__ ex_pair,
-                                                            const int *__restrict__ sel,
-                                                            int n_pairs, int ne) {
-  extern __shared__ int s_cnt[];   // ne + 1
-  for (int e = threadIdx.x; e < ne; e += blockDim.x) {
-    int c = 0;
-    for (int i = 0; i < n_pairs; ++i) c += (sel[i] == e);
-    s_cnt[e] = c;
-  }
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    int acc = 0;
-    for (int e = 0; e < ne; ++e) {
-      const int c = s_cnt[e];
-      s_cnt[e] = acc;
+// ---- prep: grouping + activation quantizer ---------------------------------------------------
+// Workgroup 0 builds the expert -> (token, rank) table: counts by LDS atomics, an exclusive scan,
+// then each pair takes a slot by an atomic cursor. The order of an expert's pairs is whatever the
+// atomics give: every pair is computed on its own (its own MFMA token row, its own fp32 chain), so
+// no output depends on it. It also lists the active experts in id order (act[s], -1 past them).
+// Workgroups 1..: the activation quantizer of kq4_quant.hip (one half-wave per 32-block).
+__global__ __launch_bounds__(256) void kq4_moe_prep_kernel(
+    int *__restrict__ ex_off, int *__restrict__ ex_pair, int *__restrict__ act,
+    const int *__restrict__ sel, int n_pairs, int ne, const float *__restrict__ X,
+    int8_t *__restrict__ xq, float *__restrict__ xd, int T, int d) {
+  if (blockIdx.x == 0) {
+    // LDS: cnt[ne], cursor[ne], per-thread partial sums [2][blockDim]
+    extern __shared__ int kq4_moe_cnt[];
+    int *cnt = kq4_moe_cnt, *cur = kq4_moe_cnt + ne, *part = kq4_moe_cnt + 2 * ne;
+    const int nt = blockDim.x, tid = threadIdx.x;
+    // the first 4 * blockDim pairs' expert ids stay in registers for the scatter below
+    int ev[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) ev[j] = tid + nt * j < n_pairs ? sel[tid + nt * j] : -1;
+    for (int e = tid; e < ne; e += nt) cnt[e] = 0;
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (ev[j] >= 0 && ev[j] < ne) atomicAdd(&cnt[ev[j]], 1);
+    for (int i = tid + 4 * nt; i < n_pairs; i += nt) {
+      const int e = sel[i];
+      if (e >= 0 && e < ne) atomicAdd(&cnt[e], 1);
+    }
+    __syncthreads();
+    // exclusive scans of the counts and of the active flags: thread tid owns experts
+    // [tid*per, tid*per + per); its totals are scanned across the block (Hillis-Steele)
+    const int per = (ne + nt - 1) / nt, e0 = tid * per;
+    int sc = 0, sa = 0;
+    for (int e = e0; e < e0 + per && e < ne; ++e) { sc += cnt[e]; sa += cnt[e] > 0; }
+    part[tid] = sc;
+    part[nt + tid] = sa;
+    __syncthreads();
+    for (int o = 1; o < nt; o <<= 1) {
+      const int vc = tid >= o ? part[tid - o] : 0, va = tid >= o ? part[nt + tid - o] : 0;
+      __syncthreads();
+      part[tid] += vc;
+      part[nt + tid] += va;
+      __syncthreads();
+    }
+    int acc = part[tid] - sc, na = part[nt + tid] - sa;   // exclusive prefixes
+    for (int e = e0; e < e0 + per && e < ne; ++e) {
+      const int c = cnt[e];
+      cur[e] = acc;
       ex_off[e] = acc;
+      if (c) act[na++] = e;
       acc += c;
     }
-    ex_off[ne] = acc;
-  }
-  __syncthreads();
-  for (int e = threadIdx.x; e < ne; e += blockDim.x) {
-    int pos = s_cnt[e];
-    for (int i = 0; i < n_pairs; ++i)
-      if (sel[i] == e) ex_pair[pos++] = i;
-  }
-}
-
-// ---- one weight row-block of the stream layout ---------------------------------------------
-// The 32 weights of (row, block b) as 16*(n-8) int8 (8 dwords, element order) and its scale.
-KQ4_DEV float kq4_load_rowblk(uint32_t *o, const uint8_t *__restrict__ w, int row, int b,
-                              int nst) {
+    if (tid == nt - 1) {
+      ex_off[ne] = part[nt - 1];
+      for (int s = part[2 * nt - 1]; s < ne; ++s) act[s] = -1;
+    }
+    __syncthreads();
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const uint2 v = *reinterpret_cast<const uint2 *>(w + kq4_stream_nib(row, b, h, nst));
-    kq4_unpack_half(v.x, v.y, o + 4 * h);
+    for (int j = 0; j < 4; ++j)
+      if (ev[j] >= 0 && ev[j] < ne) ex_pair[atomicAdd(&cur[ev[j]], 1)] = tid + nt * j;
+    for (int i = tid + 4 * nt; i < n_pairs; i += nt) {
+      const int e = sel[i];
+      if (e >= 0 && e < ne) ex_pair[atomicAdd(&cur[e], 1)] = i;
+    }
+    return;
   }
-  return kq4_h2f(*reinterpret_cast<const uint16_t *>(w + kq4_stream_scale(row, b, nst)));
-}
-
-KQ4_DEV int kq4_rowblk_dot(const uint32_t *o, const uint32_t *qa) {
-  int acc = 0;
+  const int nb = d / 32;
+  const int lane = threadIdx.x & 31;
+  const long blk = (long)(blockIdx.x - 1) * (blockDim.x >> 5) + (threadIdx.x >> 5);
+  if (blk >= (long)T * nb) return;   // whole 32-lane halves exit together
+  const float v = X[blk * 32 + lane];
+  float a = fmaxf(fabsf(v), 1e-10f);
 #pragma unroll
-  for (int k = 0; k < 8; ++k) acc = kq4_dot4(o[k], qa[k], acc);
-  return acc >> 4;   // exact: 16*S
+  for (int s = 16; s > 0; s >>= 1) a = fmaxf(a, __shfl_xor(a, s, 32));
+  const float dq = a / 127.0f;
+  int q = (int)(v / dq + 0.5f);
+  q = q > 127 ? 127 : (q < -127 ? -127 : q);
+  xq[blk * 32 + lane] = (int8_t)q;
+  if (lane == 0) xd[blk] = dq;
 }
 
-KQ4_DEV void kq4_load_q(uint32_t *qa, const int8_t *src) {
-  const uint4 *p = reinterpret_cast<const uint4 *>(src);
-  const uint4 a = p[0], b = p[1];
-  qa[0] = a.x; qa[1] = a.y; qa[2] = a.z; qa[3] = a.w;
-  qa[4] = b.x; qa[5] = b.y; qa[6] = b.z; qa[7] = b.w;
+// ---- shared pieces of the expert kernels ----------------------------------------------------
+
+// This lane's weights of one (row set, stage) chunk of the stream layout: units u0 .. u0+NU-1
+// (2 blocks each) of its (row, half), and the f16 scales of its row's blocks 8*sh .. 8*sh+7
+// (NS = 1) or 0 .. 15 (NS = 2). Scales first: loads complete in issue order.
+template <int NU, int NS>
+struct KQ4MoeW {
+  uint32_t n[4 * NU];
+  uint32_t sc[4 * NS];
+};
+
+template <int NU, int NS>
+KQ4_DEV void kq4_moe_wload(KQ4MoeW<NU, NS> &w, const uint8_t *__restrict__ chunk, int lane, int u0,
+                           int sh) {
+  const uint4 *sc = reinterpret_cast<const uint4 *>(chunk + 8192) + (lane & 31);
+#pragma unroll
+  for (int i = 0; i < NS; ++i) {
+    const uint4 v = sc[32 * (NS == 2 ? i : sh)];
+    w.sc[4 * i] = v.x; w.sc[4 * i + 1] = v.y; w.sc[4 * i + 2] = v.z; w.sc[4 * i + 3] = v.w;
+  }
+  const uint4 *src = reinterpret_cast<const uint4 *>(chunk) + lane;
+#pragma unroll
+  for (int u = 0; u < NU; ++u) {
+    const uint4 v = src[64 * (u0 + u)];
+    w.n[4 * u] = v.x; w.n[4 * u + 1] = v.y; w.n[4 * u + 2] = v.z; w.n[4 * u + 3] = v.w;
+  }
 }
 
-// ---- gate/up + SiLU + av quantization ----------------------------------------------------
-// grid: ne * (ef/32) workgroups; workgroup (e, rb) owns expert e's rows rb*32 .. +32 of G and
-// U (8 tile groups each) and every (token, rank) routed to e, in chunks of `pc` pairs.
-__global__ __launch_bounds__(256) void kq4_moe_gu_kernel(
+// Terms t[b][v] = fl(fl(sc*xd) * S) of the chunk's 2*NU blocks for this lane's row (lane%32) and
+// pair VT*(lane/32)+v (VT = 2 or 4; 2*VT pairs): the pair's codes sit in MFMA token row
+// 4*(lane/32)+v, i.e. A row rho = 4*i+v holds pair VT*i+v (i < 2, v < VT; other rows: any codes).
+// The activation codes are at slab[pair*qts + qpos(b)], scales sx[b*2*VT + pair].
+template <int NU, int NS, int VT>
+KQ4_DEV void kq4_moe_terms(const KQ4MoeW<NU, NS> &w, const uint8_t *slab, int qts,
+                           const float *sx, int lane, float (*t)[VT]) {
+  const int h = lane >> 5, r = lane & 31;
+  const int pr = (r < 8 && (r & 3) < VT) ? VT * (r >> 2) + (r & 3) : 0;
+  const uint8_t *qb = slab + pr * qts + 16 * h;
+#pragma unroll
+  for (int b = 0; b < 2 * NU; ++b) {
+    uint32_t o[4];
+    kq4_unpack_half(w.n[2 * b], w.n[2 * b + 1], o);
+    const kq4_v4i B = {(int)o[0], (int)o[1], (int)o[2], (int)o[3]};
+    const kq4_v4i A = *reinterpret_cast<const kq4_v4i *>(qb + kq4_moe_qpos(b));
+    const kq4_v16i C = kq4_moe_mfma(A, B);
+    const float sc = kq4_h2f(w.sc[b >> 1] >> (16 * (b & 1)));
+    const float *xs = sx + b * 2 * VT + VT * h;
+#pragma unroll
+    for (int v = 0; v < VT; ++v) {
+      t[b][v] = (sc * xs[v]) * (float)(C[v] >> 4);   // C = 16*S exactly
+      kq4_moe_pin(t[b][v]);
+    }
+    // one block's MFMA in flight at a time: each holds 16 result registers
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+// ---- gate/up + SiLU + av quantization ----------------------------------------------------------
+// grid: min(ne, pairs) expert slots x (ef/32) row sets; block: 2*nst waves, wave k < nst streams
+// stage k of G, wave nst + k stage k of U (the same rows). Per pass of up to 4 pairs: the gate
+// wave of stage k stages the pairs' codes of stage k in slab k; every wave computes its terms;
+// then nst phases add them to the gate and up chains in block order; then one lane per (pair,
+// row) forms av, and the 32 rows of the set (one av block) are quantized together.
+__global__ __launch_bounds__(1024) void kq4_moe_gu_kernel(
     const uint8_t *__restrict__ G, const uint8_t *__restrict__ U, const int8_t *__restrict__ xq,
     const float *__restrict__ xd, const int *__restrict__ ex_off, const int *__restrict__ ex_pair,
-    float *__restrict__ av, int8_t *__restrict__ avq, float *__restrict__ avd,
-    float *__restrict__ g_out, float *__restrict__ u_out, int ne, int d, int ef, int tk, int pc) {
-  extern __shared__ float s_term[];   // [pc][64 rows][nbG]
+    const int *__restrict__ act, int8_t *__restrict__ avq, float *__restrict__ avd,
+    float *__restrict__ g_out, float *__restrict__ u_out, float *__restrict__ av_out, int d,
+    int ef, int tk) {
+  extern __shared__ __align__(16) uint8_t kq4_moe_lds[];
+  constexpr int PC = KQ4_MOE_PCG, VT = PC / 2;
+  constexpr int SLAB = kq4_moe_slab(16, PC);
   const int rbs = ef / 32;
-  const int e = blockIdx.x / rbs, rb = blockIdx.x % rbs;
-  const int o0 = ex_off[e], m = ex_off[e + 1] - o0;
-  if (m <= 0) return;
-  const int nbG = d / 32;
-  const int nstG = (nbG + KQ4_STREAM_CB - 1) / KQ4_STREAM_CB;
-  const int t = threadIdx.x;
+  const int slot = blockIdx.x / rbs, rs = blockIdx.x - slot * rbs;
+  const int e = act[slot];
+  if (e < 0) return;                                  // no expert in this slot (whole workgroup)
+  const int o0 = ex_off[e], cnt = ex_off[e + 1] - o0;
+  const int nb = d / 32, nst = (nb + 15) / 16;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int m = wave >= nst ? 1 : 0;                  // 0 = gate, 1 = up
+  const int k = wave - m * nst;                       // stage
+  const int h = lane >> 5, r = lane & 31;
+  uint8_t *slab = kq4_moe_lds + k * SLAB;
+  float *sx = reinterpret_cast<float *>(slab + PC * KQ4_MOE_QTS);     // [16][PC]
+  float *accb = reinterpret_cast<float *>(kq4_moe_lds + nst * SLAB);   // [2][PC][32]
+  KQ4MoeW<8, 2> w;
+  kq4_moe_wload<8, 2>(w, (m ? U : G) + ((size_t)((e * ef) / 32 + rs) * nst + k) * KQ4_STREAM_CHUNK,
+                      lane, 0, 0);
+  const int nblk = nb - 16 * k < 16 ? nb - 16 * k : 16;
 
-  for (int c0 = 0; c0 < m; c0 += pc) {
-    const int np = (m - c0) < pc ? (m - c0) : pc;
-    // phase A: terms for 64 rows (32 gate, 32 up) x nbG blocks
-    for (int c = t; c < 64 * nbG; c += 256) {
-      const int q = c / nbG, b = c - q * nbG;
-      const uint8_t *mat = q < 32 ? G : U;
-      const int row = e * ef + rb * 32 + (q & 31);
-      uint32_t wv[8];
-      const float sc = kq4_load_rowblk(wv, mat, row, b, nstG);
-      for (int p = 0; p < np; ++p) {
-        const int tok = ex_pair[o0 + c0 + p] / tk;
-        uint32_t qa[8];
-        kq4_load_q(qa, xq + (size_t)tok * d + (size_t)b * 32);
-        const float x = xd[(size_t)tok * nbG + b];
-        s_term[((size_t)p * 64 + q) * nbG + b] = (sc * x) * (float)kq4_rowblk_dot(wv, qa);
+  for (int c0 = 0; c0 < cnt; c0 += PC) {
+    const int np = cnt - c0 < PC ? cnt - c0 : PC;
+    if (m == 0) {   // stage k's codes and scales of the pass's pairs (zeros past them and past K)
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {   // 4 pairs x 16 blocks x 2 halves = 128 units of 16 B
+        const int i = lane + 64 * u;
+        const int p = i >> 5, bb = (i >> 1) & 15, hh = i & 1;
+        uint4 v = make_uint4(0, 0, 0, 0);
+        if (p < np && bb < nblk) {
+          const int tok = ex_pair[o0 + c0 + p] / tk;
+          v = *reinterpret_cast<const uint4 *>(xq + (size_t)tok * d + (size_t)(16 * k + bb) * 32 +
+                                               16 * hh);
+        }
+        *reinterpret_cast<uint4 *>(slab + p * KQ4_MOE_QTS + kq4_moe_qpos(bb) + 16 * hh) = v;
+      }
+      {
+        const int p = lane >> 4, bb = lane & 15;      // 64 scales
+        float x = 0.0f;
+        if (p < np && bb < nblk) x = xd[(size_t)(ex_pair[o0 + c0 + p] / tk) * nb + 16 * k + bb];
+        sx[bb * PC + p] = x;
       }
     }
     __syncthreads();
-    // phase B: block-ordered sums, SiLU, quantize each pair's 32 av values (one half-wave)
-    if (t < 32 * np) {
-      const int p = t >> 5, r = t & 31;
-      const float *tg = s_term + ((size_t)p * 64 + r) * nbG;
-      const float *tu = s_term + ((size_t)p * 64 + 32 + r) * nbG;
-      float g = 0.0f, u = 0.0f;
-      for (int b = 0; b < nbG; ++b) { g = g + tg[b]; u = u + tu[b]; }
+    float t[16][VT];
+    kq4_moe_touch(w.n);
+    kq4_moe_terms<8, 2, VT>(w, slab, KQ4_MOE_QTS, sx, lane, t);
+    // the chains: stage kk's waves add their blocks' terms in order, then hand the sums on
+    for (int kk = 0; kk < nst; ++kk) {
+      if (k == kk) {
+        float acc[VT];
+#pragma unroll
+        for (int v = 0; v < VT; ++v) acc[v] = kk ? accb[(m * PC + VT * h + v) * 32 + r] : 0.0f;
+#pragma unroll
+        for (int b = 0; b < 16; ++b)
+          if (b < nblk)
+#pragma unroll
+            for (int v = 0; v < VT; ++v) acc[v] = acc[v] + t[b][v];
+#pragma unroll
+        for (int v = 0; v < VT; ++v) accb[(m * PC + VT * h + v) * 32 + r] = acc[v];
+      }
+      __syncthreads();
+    }
+    // av = fl(fl(g / fl(1 + exp(-g))) * u), quantized over the set's 32 rows (one av block)
+    for (int i = threadIdx.x; i < PC * 32; i += blockDim.x) {
+      const int p = i >> 5, rw = i & 31;
+      const float g = accb[p * 32 + rw], u = accb[(PC + p) * 32 + rw];
       const float a = (g / (1.0f + kq4_expf(-g))) * u;
-      const int pair = ex_pair[o0 + c0 + p];
-      const size_t o = (size_t)pair * ef + (size_t)rb * 32 + r;
-      av[o] = a;
-      if (g_out) { g_out[o] = g; u_out[o] = u; }
       float amax = fmaxf(fabsf(a), 1e-10f);
 #pragma unroll
       for (int s = 16; s > 0; s >>= 1) amax = fmaxf(amax, __shfl_xor(amax, s, 32));
       const float dq = amax / 127.0f;
       int qv = (int)(a / dq + 0.5f);
       qv = qv > 127 ? 127 : (qv < -127 ? -127 : qv);
-      avq[o] = (int8_t)qv;
-      if (r == 0) avd[(size_t)pair * rbs + rb] = dq;
+      if (p < np) {
+        const int pair = ex_pair[o0 + c0 + p];
+        const size_t o = (size_t)pair * ef + (size_t)rs * 32 + rw;
+        avq[o] = (int8_t)qv;
+        if (rw == 0) avd[(size_t)pair * rbs + rs] = dq;
+        if (g_out) { g_out[o] = g; u_out[o] = u; }
+        if (av_out) av_out[o] = a;
+      }
     }
-    __syncthreads();
+    __syncthreads();   // before the next pass overwrites the slabs and sums
   }
 }
 
@@ -190,49 +364,115 @@ __global__ __launch_bounds__(256) void kq4_moe_avq_kernel(const float *__restric
   if (lane == 0) avd[blk] = dq;
 }
 
-// ---- down projection: unweighted partials ------------------------------------------------
-// grid: ne * (d/32); workgroup (e, rb) owns output rows rb*32 .. +32 (8 tile groups of D) over
-// expert e's column band (tiles e*ef/32 .. +ef/32) for every (token, rank) routed to e.
-__global__ __launch_bounds__(256) void kq4_moe_down_kernel(
+// ---- down projection: unweighted partials -------------------------------------------------------
+// grid: expert slots x groups of RSG row sets of D; block: RSG x NH waves. Wave (g, w) takes row
+// set g of the group and half stage qa + w of D's blocks (8 blocks; qa = the first half stage that
+// meets the expert's column band [e*ef/32, e*ef/32 + ef/32)); blocks outside the band are
+// skipped, waves past the band only join the barriers. Per pass of up to 8 pairs the workgroup
+// stages the band's av codes once (shared by its row sets), each wave computes its terms, and for
+// every row set the waves add them in block order.
+__global__ __launch_bounds__(1024) void kq4_moe_down_kernel(
     const uint8_t *__restrict__ D, const int8_t *__restrict__ avq, const float *__restrict__ avd,
-    const int *__restrict__ ex_off, const int *__restrict__ ex_pair, float *__restrict__ P,
-    int ne, int d, int ef, int pc) {
-  extern __shared__ float s_term[];   // [pc][32 rows][cbe]
-  const int rbs = d / 32;
-  const int e = blockIdx.x / rbs, rb = blockIdx.x % rbs;
-  const int o0 = ex_off[e], m = ex_off[e + 1] - o0;
-  if (m <= 0) return;
-  const int cbe = ef / 32;
-  const int nstD = (ne * ef / 32 + KQ4_STREAM_CB - 1) / KQ4_STREAM_CB;
-  const size_t cb0 = (size_t)e * ef / 32;
-  const int t = threadIdx.x;
-  for (int c0 = 0; c0 < m; c0 += pc) {
-    const int np = (m - c0) < pc ? (m - c0) : pc;
-    for (int c = t; c < 32 * cbe; c += 256) {
-      const int q = c / cbe, cb = c - q * cbe;
-      uint32_t wv[8];
-      const float sc = kq4_load_rowblk(wv, D, rb * 32 + q, (int)cb0 + cb, nstD);
-      for (int p = 0; p < np; ++p) {
-        const int pair = ex_pair[o0 + c0 + p];
-        uint32_t qa[8];
-        kq4_load_q(qa, avq + (size_t)pair * ef + (size_t)cb * 32);
-        const float x = avd[(size_t)pair * cbe + cb];
-        s_term[((size_t)p * 32 + q) * cbe + cb] = (sc * x) * (float)kq4_rowblk_dot(wv, qa);
+    const int *__restrict__ ex_off, const int *__restrict__ ex_pair, const int *__restrict__ act,
+    float *__restrict__ P, int ne, int d, int ef, int rsg, int nhl) {
+  extern __shared__ __align__(16) uint8_t kq4_moe_lds[];
+  constexpr int PC = KQ4_MOE_PCD, VT = PC / 2;
+  const int nrs = d / 32, ngrp = (nrs + rsg - 1) / rsg;
+  const int slot = blockIdx.x / ngrp, grp = blockIdx.x - slot * ngrp;
+  const int e = act[slot];
+  if (e < 0) return;
+  const int o0 = ex_off[e], cnt = ex_off[e + 1] - o0;
+  const int cbe = ef / 32, nbD = ne * cbe, nstD = (nbD + 15) / 16;
+  const int b0 = e * cbe;                              // first block of the band
+  const int qa = b0 >> 3, nh = ((b0 + cbe - 1) >> 3) - qa + 1;
+  const int qts = ((cbe + 1) >> 1) * 80;               // pair pitch of the staged band codes
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g = wave / nhl, w = wave - g * nhl;        // row set in the group, half stage
+  const int rs = grp * rsg + g;
+  const int h = lane >> 5, r = lane & 31;
+  const int hq = qa + w;
+  const bool live = w < nh && rs < nrs;
+  uint8_t *codes = kq4_moe_lds;                                         // [PC][qts]
+  float *sxb = reinterpret_cast<float *>(kq4_moe_lds + PC * qts);       // [cbe][PC]
+  float *accb = sxb + cbe * PC + g * PC * 32;                           // per row set [PC][32]
+  KQ4MoeW<4, 1> wt;
+  if (live)
+    kq4_moe_wload<4, 1>(wt, D + ((size_t)rs * nstD + (hq >> 1)) * KQ4_STREAM_CHUNK, lane,
+                        4 * (hq & 1), hq & 1);
+  // band-relative block of local block j, or -1 outside the band
+  auto cbof = [&](int j) {
+    const int gb = 8 * hq + j;
+    return (gb >= b0 && gb < b0 + cbe) ? gb - b0 : -1;
+  };
+  const int pr = (r < 8 && (r & 3) < VT) ? VT * (r >> 2) + (r & 3) : 0;   // A row -> pair
+
+  for (int c0 = 0; c0 < cnt; c0 += PC) {
+    const int np = cnt - c0 < PC ? cnt - c0 : PC;
+    // the band's codes and scales of the pass's pairs, once for all row sets
+    for (int i = threadIdx.x; i < PC * cbe * 2; i += blockDim.x) {
+      const int p = i / (2 * cbe), rem = i - p * 2 * cbe, cb = rem >> 1, hh = rem & 1;
+      uint4 v = make_uint4(0, 0, 0, 0);
+      if (p < np)
+        v = *reinterpret_cast<const uint4 *>(avq + (size_t)ex_pair[o0 + c0 + p] * ef +
+                                             (size_t)cb * 32 + 16 * hh);
+      *reinterpret_cast<uint4 *>(codes + p * qts + kq4_moe_qpos(cb) + 16 * hh) = v;
+    }
+    for (int i = threadIdx.x; i < PC * cbe; i += blockDim.x) {
+      const int cb = i / PC, p = i - cb * PC;
+      sxb[i] = p < np ? avd[(size_t)ex_pair[o0 + c0 + p] * cbe + cb] : 0.0f;
+    }
+    __syncthreads();
+    float t[8][VT];
+    if (live) {
+      kq4_moe_touch(wt.n);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int cb = cbof(j);
+        const int cbs = cb < 0 ? 0 : cb;
+        uint32_t o[4];
+        kq4_unpack_half(wt.n[2 * j], wt.n[2 * j + 1], o);
+        const kq4_v4i B = {(int)o[0], (int)o[1], (int)o[2], (int)o[3]};
+        const kq4_v4i A =
+            *reinterpret_cast<const kq4_v4i *>(codes + pr * qts + kq4_moe_qpos(cbs) + 16 * h);
+        const kq4_v16i C = kq4_moe_mfma(A, B);
+        const float sc = kq4_h2f(wt.sc[j >> 1] >> (16 * (j & 1)));
+        const float *xs = sxb + cbs * PC + VT * h;
+#pragma unroll
+        for (int v = 0; v < VT; ++v) {
+          t[j][v] = (sc * xs[v]) * (float)(C[v] >> 4);   // C = 16*S exactly
+          kq4_moe_pin(t[j][v]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
-    __syncthreads();
-    if (t < 32 * np) {
-      const int p = t >> 5, r = t & 31;
-      const float *tp = s_term + ((size_t)p * 32 + r) * cbe;
-      float acc = 0.0f;
-      for (int cb = 0; cb < cbe; ++cb) acc = acc + tp[cb];
-      const int pair = ex_pair[o0 + c0 + p];
-      P[(size_t)pair * d + (size_t)rb * 32 + r] = acc;
+    // the chains over the band's blocks, one per row set: wave by wave, block by block
+    for (int ww = 0; ww < nh; ++ww) {
+      if (w == ww && rs < nrs) {
+        float acc[VT];
+#pragma unroll
+        for (int v = 0; v < VT; ++v) acc[v] = ww ? accb[(VT * h + v) * 32 + r] : 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          if (cbof(j) >= 0)
+#pragma unroll
+            for (int v = 0; v < VT; ++v) acc[v] = acc[v] + t[j][v];
+#pragma unroll
+        for (int v = 0; v < VT; ++v) {
+          if (ww + 1 < nh) {
+            accb[(VT * h + v) * 32 + r] = acc[v];
+          } else if (VT * h + v < np) {
+            P[(size_t)ex_pair[o0 + c0 + VT * h + v] * d + (size_t)rs * 32 + r] = acc[v];
+          }
+        }
+      }
+      __syncthreads();
     }
-    __syncthreads();
   }
 }
 
+// y = fl(y + fl(p * P)) over the ranks in order, skipping invalid expert ids. The loads of all
+// ranks are issued before the chain (P rows of skipped ranks are read but not used).
 __global__ __launch_bounds__(256) void kq4_moe_combine_kernel(float *__restrict__ Y,
                                                               const float *__restrict__ P,
                                                               const int *__restrict__ sel,
@@ -242,53 +482,79 @@ __global__ __launch_bounds__(256) void kq4_moe_combine_kernel(float *__restrict_
   if (i >= (long)T * d) return;
   const int t = (int)(i / d), n = (int)(i - (long)t * d);
   float y = 0.0f;
-  for (int j = 0; j < tk; ++j) {
-    const int s = t * tk + j;
-    const int e = sel[s];
-    if (e < 0 || e >= ne) continue;
-    y = y + pr[s] * P[(size_t)s * d + n];
+  for (int j0 = 0; j0 < tk; j0 += 8) {
+    float pv[8], wv[8];
+    int ev[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int s = t * tk + j0 + j;
+      const bool in = j0 + j < tk;
+      ev[j] = in ? sel[s] : -1;
+      wv[j] = in ? pr[s] : 0.0f;
+      pv[j] = in ? P[(size_t)s * d + n] : 0.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (ev[j] >= 0 && ev[j] < ne) y = y + wv[j] * pv[j];
   }
   Y[i] = y;
 }
 
 int kq4_launch_moe_route(int *sel, float *pr, const float *logits, int T, int ne, int tk,
                          hipStream_t s) {
-  if (tk > KQ4_MOE_MAXTK) return (int)hipErrorInvalidValue;
-  hipLaunchKernelGGL(kq4_moe_route_kernel, dim3(1), dim3(256), 0, s, sel, pr, logits, T, ne, tk);
+  if (tk > KQ4_MOE_MAXTK || ne > KQ4_MOE_MAXNE) return (int)hipErrorInvalidValue;
+  hipLaunchKernelGGL(kq4_moe_route_kernel, dim3((unsigned)((T + 3) / 4)), dim3(256), 0, s, sel,
+                     pr, logits, T, ne, tk);
   return (int)hipGetLastError();
 }
 
-static int moe_pc(int per_pair_floats) {
-  const int budget = 48 * 1024 / 4;   // floats of LDS for staged terms
-  int pc = budget / per_pair_floats;
-  if (pc > 8) pc = 8;
-  if (pc < 1) pc = 1;
-  return pc;
+int kq4_moe_shape_ok(int d, int ef) {
+  if (d <= 0 || ef <= 0 || d % 32 || ef % 32) return 0;
+  const int nst = (d / 32 + 15) / 16;
+  return nst <= 8 && (ef / 32) / 8 + 2 <= 16 && ef <= 4096;   // 2*nst and <= 16 waves; LDS
 }
 
 int kq4_launch_moe_dbg(float *Y, const float *X, const int *sel, const float *pr, int T, int tk,
                        const uint8_t *G, const uint8_t *U, const uint8_t *D, int ne, int d,
-                       int ef, const KQ4MoeWs &ws, float *g_out, float *u_out,
+                       int ef, const KQ4MoeWs &ws, float *g_out, float *u_out, float *av_out,
                        const float *av_in, hipStream_t s) {
+  if (!kq4_moe_shape_ok(d, ef) || T <= 0 || tk <= 0) return (int)hipErrorInvalidValue;
   const int n_pairs = T * tk;
-  hipLaunchKernelGGL(kq4_moe_group_kernel, dim3(1), dim3(256), (ne + 1) * sizeof(int), s,
-                     ws.ex_off, ws.ex_pair, sel, n_pairs, ne);
-  int rc = kq4_launch_quantize(X, ws.xq, ws.xd, nullptr, T, d, 0, s);
-  if (rc) return rc;
-  const int nbG = d / 32, cbe = ef / 32;
-  const int pcg = moe_pc(64 * nbG) > 4 ? 4 : moe_pc(64 * nbG);   // phase B: 32*pc <= 256 lanes
-  hipLaunchKernelGGL(kq4_moe_gu_kernel, dim3(ne * (ef / 32)), dim3(256),
-                     (size_t)pcg * 64 * nbG * sizeof(float), s, G, U, ws.xq, ws.xd, ws.ex_off,
-                     ws.ex_pair, ws.av, ws.avq, ws.avd, g_out, u_out, ne, d, ef, tk, pcg);
+  const int nb = d / 32, nst = (nb + 15) / 16, cbe = ef / 32;
+  const long qblk = (long)T * nb;
+  hipLaunchKernelGGL(kq4_moe_prep_kernel, dim3((unsigned)(1 + (qblk + 7) / 8)), dim3(256),
+                     (2 * ne + 2 * 256) * sizeof(int), s, ws.ex_off, ws.ex_pair, ws.act, sel, n_pairs, ne, X,
+                     ws.xq, ws.xd, T, d);
+  const int slots = ne < n_pairs ? ne : n_pairs;
+  const size_t lds_gu = (size_t)nst * kq4_moe_slab(16, KQ4_MOE_PCG) +
+                        2 * KQ4_MOE_PCG * 32 * sizeof(float);
+  hipLaunchKernelGGL(kq4_moe_gu_kernel, dim3((unsigned)(slots * cbe)), dim3(128 * nst), lds_gu, s,
+                     G, U, ws.xq, ws.xd, ws.ex_off, ws.ex_pair, ws.act, ws.avq, ws.avd, g_out,
+                     u_out, av_out, d, ef, tk);
   if (av_in) {
     const long nblk = (long)n_pairs * cbe;
     hipLaunchKernelGGL(kq4_moe_avq_kernel, dim3((unsigned)((nblk + 7) / 8)), dim3(256), 0, s,
                        av_in, ws.avq, ws.avd, nblk);
   }
-  const int pcd = moe_pc(32 * cbe) > 8 ? 8 : moe_pc(32 * cbe);
-  hipLaunchKernelGGL(kq4_moe_down_kernel, dim3(ne * (d / 32)), dim3(256),
-                     (size_t)pcd * 32 * cbe * sizeof(float), s, D, ws.avq, ws.avd, ws.ex_off,
-                     ws.ex_pair, ws.P, ne, d, ef, pcd);
+  // half stages a band can meet (the most over the experts), and row sets per workgroup
+  int nhl = 1;
+  for (int e = 0; e < ne; ++e) {
+    const int b0 = e * cbe, nh = ((b0 + cbe - 1) >> 3) - (b0 >> 3) + 1;
+    nhl = nh > nhl ? nh : nhl;
+  }
+  // row sets per workgroup: as many as fit 16 waves, but keep about two workgroups per CU
+  const int nrs = d / 32;
+  int rsg = 16 / nhl;
+  const int spread = (slots * nrs) / (2 * (ws.ncu > 0 ? ws.ncu : 256));
+  rsg = rsg < spread ? rsg : spread;
+  rsg = rsg < 1 ? 1 : (rsg > nrs ? nrs : rsg);
+  const int ngrp = (nrs + rsg - 1) / rsg;
+  const size_t lds_dn = (size_t)KQ4_MOE_PCD * (((cbe + 1) / 2) * 80) +
+                        (size_t)cbe * KQ4_MOE_PCD * sizeof(float) +
+                        (size_t)rsg * KQ4_MOE_PCD * 32 * sizeof(float);
+  hipLaunchKernelGGL(kq4_moe_down_kernel, dim3((unsigned)(slots * ngrp)), dim3(64 * rsg * nhl),
+                     lds_dn, s, D, ws.avq, ws.avd, ws.ex_off, ws.ex_pair, ws.act, ws.P, ne, d,
+                     ef, rsg, nhl);
   const long n = (long)T * d;
   hipLaunchKernelGGL(kq4_moe_combine_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
                      Y, ws.P, sel, pr, T, tk, d, ne);
@@ -299,5 +565,5 @@ int kq4_launch_moe(float *Y, const float *X, const int *sel, const float *pr, in
                    const uint8_t *G, const uint8_t *U, const uint8_t *D, int ne, int d, int ef,
                    const KQ4MoeWs &ws, hipStream_t s) {
   return kq4_launch_moe_dbg(Y, X, sel, pr, T, tk, G, U, D, ne, d, ef, ws, nullptr, nullptr,
-                            nullptr, s);
+                            nullptr, nullptr, s);
 }
