@@ -251,7 +251,7 @@ int matmul_impl(int n_mats, float *const *out, const float *const *res, const ui
   }
   for (int i = 0; i < n_mats; ++i)
     KQ4_HIP((hipError_t)kq4_launch_gemm(out[i], res ? res[i] : nullptr, w[i], act, rows[i], cols,
-                                        main_n, main_chain, s));
+                                        main_n, main_chain, ds->ncu, s));
   if (tail) {
     float *o2[KQ4_MAX_MATS];
     const float *r2[KQ4_MAX_MATS];

@@ -10,7 +10,7 @@
 //   GEMV32 the same with the f32 xd (q4x4_dot1_group16_gemv :4229-4251)
 //   CTILE  lo/hi accumulators fed by two half-K MFMAs, out = fl(lo + hi) (:4180-4216)
 // and out = fl(residual + acc) when fused. The epilogue (convert, scale, fma per output per
-// block) runs on the VALU; it, not the matrix core, bounds this kernel.
+// block) runs on the VALU.
 //
 // Tiling: workgroup = 4 waves = 128 tokens x 128 rows, each wave 64 x 64 (2 x 2 MFMA tiles).
 // Per stage of KB = 4 blocks the workgroup stages into LDS (rows padded to 48 B so the 16-byte
@@ -25,11 +25,11 @@
 #include "kq4_internal.h"
 #include "../../include/kq4.h"
 
+#include <stdlib.h>
+
 typedef int kq4_v4i __attribute__((ext_vector_type(4)));
 typedef int kq4_v16i __attribute__((ext_vector_type(16)));
 
-#define KQ4_GEMM_BM 128
-#define KQ4_GEMM_BN 128
 #define KQ4_GEMM_KB 4
 #define KQ4_LDS_ROW 48
 
@@ -37,10 +37,13 @@ typedef int kq4_v16i __attribute__((ext_vector_type(16)));
 // row = 8*(v/4) + 4*(lane/32) + v%4 (token).
 KQ4_DEV int kq4_mfma_tok(int v, int half) { return 8 * (v >> 2) + 4 * half + (v & 3); }
 
-template <int CHAIN>
+// TM / TN = MFMA token / row tiles per wave: a workgroup covers BM = 64*TM tokens x BN = 64*TN
+// rows (128 x 128, or smaller when the launch would otherwise have fewer than two tiles per CU).
+template <int CHAIN, int TM, int TN>
 __global__ __launch_bounds__(256, 2) void kq4_gemm_kernel(
     float *__restrict__ out, const float *__restrict__ res, const uint8_t *__restrict__ w,
     const KQ4GemmAct act, int rows, int n_tok, int nb, int nst, int mtiles, int ntiles) {
+  constexpr int KQ4_GEMM_BM = 64 * TM, KQ4_GEMM_BN = 64 * TN;
   __shared__ __align__(16) int8_t sA[KQ4_GEMM_KB][KQ4_GEMM_BM * KQ4_LDS_ROW];
   __shared__ __align__(16) int8_t sB[KQ4_GEMM_KB][KQ4_GEMM_BN * KQ4_LDS_ROW];
   __shared__ __align__(16) float sW[KQ4_GEMM_KB][KQ4_GEMM_BN];
@@ -64,100 +67,136 @@ __global__ __launch_bounds__(256, 2) void kq4_gemm_kernel(
   const int l32 = lane & 31, half = lane >> 5;
   const int groups = rows >> 2;
 
-  float acc[2][2][16];
-  float acc_hi[2][2][16];
+  float acc[TM][TN][16];
+  float acc_hi[TM][TN][16];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < TM; ++i)
 #pragma unroll
-    for (int jn = 0; jn < 2; ++jn)
+    for (int jn = 0; jn < TN; ++jn)
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         acc[i][jn][v] = 0.0f;
         acc_hi[i][jn][v] = 0.0f;
       }
 
-  for (int b0 = 0; b0 < nb; b0 += KQ4_GEMM_KB) {
-    __syncthreads();
-    // ---- stage A: KB blocks x 128 tokens x 32 B, 16 B per thread per block
+  // Global -> registers for one stage (issued a whole compute phase ahead), then registers ->
+  // LDS. Activations: KB blocks x 128 tokens x 32 B, 16 B per thread per block. Weights from the
+  // stream layout: blocks b0 .. b0+3 are nibble units (b0%16)/2 and +1 of the 4 row sets; load
+  // (set, unit, lane) = 16 B = the lane's half-row of 2 blocks, unpacked to 16*(n-8) bytes when
+  // stored. Row scales (8 B per row, as wd/16) and token scales.
+  struct Regs {
+    uint4 a[KQ4_GEMM_KB];
+    uint4 b[TN];
+    uint2 sw;
+    float x[KQ4_GEMM_KB * KQ4_GEMM_BM / 256];
+  };
+  auto load = [&](Regs &rg, int b0) {
 #pragma unroll
     for (int u = 0; u < KQ4_GEMM_KB; ++u) {
       const int tok = t >> 1, hh = t & 1;
       const int b = b0 + u;
-      uint4 v = make_uint4(0, 0, 0, 0);
-      if (b < nb && m0 + tok < n_tok)
-        v = *reinterpret_cast<const uint4 *>(act.xq + (long)(m0 + tok) * act.q_ts +
-                                             (long)b * act.q_bs + hh * 16);
-      *reinterpret_cast<uint4 *>(&sA[u][tok * KQ4_LDS_ROW + hh * 16]) = v;
+      rg.a[u] = make_uint4(0, 0, 0, 0);
+      if (tok < KQ4_GEMM_BM && b < nb && m0 + tok < n_tok)
+        rg.a[u] = *reinterpret_cast<const uint4 *>(act.xq + (long)(m0 + tok) * act.q_ts +
+                                                   (long)b * act.q_bs + hh * 16);
     }
-    // ---- stage B from the stream layout: blocks b0 .. b0+3 are nibble units (b0%16)/2 and +1 of
-    // the 4 row sets; load (set, unit, lane) = 16 B = the lane's half-row of 2 blocks, unpacked
-    // to 16*(n-8) bytes. Then the 128 rows' scales of the 4 blocks (8 B per row), as wd/16.
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
+    for (int u = 0; u < TN; ++u) {
       const int idx = t + 256 * u;
       const int ln = idx & 63, iu = (idx >> 6) & 1, sl = idx >> 7;
       const int rl = 32 * sl + (ln & 31), h = ln >> 5;
-      uint4 v = make_uint4(0, 0, 0, 0);          // row sets past the matrix: weight 0
+      rg.b[u] = make_uint4(0, 0, 0, 0);          // row sets past the matrix: weight 0
       if (n0 + 32 * sl < rows)
-        v = *reinterpret_cast<const uint4 *>(w + kq4_stream_nib(n0 + rl, b0 + 2 * iu, h, nst));
-      uint32_t o[4];
-      kq4_unpack_half(v.x, v.y, o);
-      *reinterpret_cast<uint4 *>(&sB[2 * iu][rl * KQ4_LDS_ROW + 16 * h]) =
-          make_uint4(o[0], o[1], o[2], o[3]);
-      kq4_unpack_half(v.z, v.w, o);
-      *reinterpret_cast<uint4 *>(&sB[2 * iu + 1][rl * KQ4_LDS_ROW + 16 * h]) =
-          make_uint4(o[0], o[1], o[2], o[3]);
+        rg.b[u] = *reinterpret_cast<const uint4 *>(w + kq4_stream_nib(n0 + rl, b0 + 2 * iu, h, nst));
     }
-    if (t < KQ4_GEMM_BN) {
-      uint2 sv = make_uint2(0, 0);
-      if (n0 + (t & ~31) < rows)
-        sv = *reinterpret_cast<const uint2 *>(w + kq4_stream_scale(n0 + t, b0, nst));
-      sW[0][t] = kq4_h2f(sv.x) * 0.0625f;
-      sW[1][t] = kq4_h2f(sv.x >> 16) * 0.0625f;
-      sW[2][t] = kq4_h2f(sv.y) * 0.0625f;
-      sW[3][t] = kq4_h2f(sv.y >> 16) * 0.0625f;
-    }
+    rg.sw = make_uint2(0, 0);
+    if (t < KQ4_GEMM_BN && n0 + (t & ~31) < rows)
+      rg.sw = *reinterpret_cast<const uint2 *>(w + kq4_stream_scale(n0 + t, b0, nst));
 #pragma unroll
     for (int u = 0; u < KQ4_GEMM_KB * KQ4_GEMM_BM / 256; ++u) {
       const int c = t + 256 * u;
       const int bl = c / KQ4_GEMM_BM, tok = c % KQ4_GEMM_BM;
       const int b = b0 + bl;
-      float xv = 0.0f;
-      if (b < nb && m0 + tok < n_tok) xv = act.xd[(long)(m0 + tok) * act.d_ts + (long)b * act.d_bs];
-      // ASM chain: the reference's asm GEMM multiplies by the f16-rounded activation scale
-      sX[bl][tok] = (CHAIN == KQ4_CHAIN_ASM) ? kq4_f16_round(xv) : xv;
+      rg.x[u] = 0.0f;
+      if (b < nb && m0 + tok < n_tok) rg.x[u] = act.xd[(long)(m0 + tok) * act.d_ts + (long)b * act.d_bs];
     }
+  };
+  auto store = [&](const Regs &rg) {
+#pragma unroll
+    for (int u = 0; u < KQ4_GEMM_KB; ++u)
+      if ((t >> 1) < KQ4_GEMM_BM)
+        *reinterpret_cast<uint4 *>(&sA[u][(t >> 1) * KQ4_LDS_ROW + (t & 1) * 16]) = rg.a[u];
+#pragma unroll
+    for (int u = 0; u < TN; ++u) {
+      const int idx = t + 256 * u;
+      const int ln = idx & 63, iu = (idx >> 6) & 1, sl = idx >> 7;
+      const int rl = 32 * sl + (ln & 31), h = ln >> 5;
+      uint32_t o[4];
+      kq4_unpack_half(rg.b[u].x, rg.b[u].y, o);
+      *reinterpret_cast<uint4 *>(&sB[2 * iu][rl * KQ4_LDS_ROW + 16 * h]) =
+          make_uint4(o[0], o[1], o[2], o[3]);
+      kq4_unpack_half(rg.b[u].z, rg.b[u].w, o);
+      *reinterpret_cast<uint4 *>(&sB[2 * iu + 1][rl * KQ4_LDS_ROW + 16 * h]) =
+          make_uint4(o[0], o[1], o[2], o[3]);
+    }
+    if (t < KQ4_GEMM_BN) {
+      sW[0][t] = kq4_h2f(rg.sw.x) * 0.0625f;
+      sW[1][t] = kq4_h2f(rg.sw.x >> 16) * 0.0625f;
+      sW[2][t] = kq4_h2f(rg.sw.y) * 0.0625f;
+      sW[3][t] = kq4_h2f(rg.sw.y >> 16) * 0.0625f;
+    }
+#pragma unroll
+    for (int u = 0; u < KQ4_GEMM_KB * KQ4_GEMM_BM / 256; ++u) {
+      const int c = t + 256 * u;
+      // ASM chain: the reference's asm GEMM multiplies by the f16-rounded activation scale
+      sX[c / KQ4_GEMM_BM][c % KQ4_GEMM_BM] = (CHAIN == KQ4_CHAIN_ASM) ? kq4_f16_round(rg.x[u]) : rg.x[u];
+    }
+  };
+
+  // The C-tile chain keeps two accumulator sets; it has no registers left for the prefetch and
+  // loads each stage just before storing it.
+  constexpr bool PREFETCH = CHAIN != KQ4_CHAIN_CTILE;
+  Regs rg;
+  if (PREFETCH) load(rg, 0);
+  for (int b0 = 0; b0 < nb; b0 += KQ4_GEMM_KB) {
+    __syncthreads();              // the previous stage's compute is done with the LDS tiles
+    if (!PREFETCH) load(rg, b0);
+    store(rg);
     __syncthreads();
+    if (PREFETCH && b0 + KQ4_GEMM_KB < nb) load(rg, b0 + KQ4_GEMM_KB);   // during the compute
 
     // ---- compute: per block, 2 x 2 MFMA tiles per wave + exact per-block epilogue
 #pragma unroll
     for (int bl = 0; bl < KQ4_GEMM_KB; ++bl) {
       if (b0 + bl >= nb) break;
-      kq4_v4i af[2], bf[2];
-      float wdv[2];
-      float xsv[2][16];
+      kq4_v4i af[TM], bf[TN];
+      float wdv[TN];
+      float xsv[TM][16];
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
+      for (int i = 0; i < TM; ++i) {
         af[i] = *reinterpret_cast<const kq4_v4i *>(
-            &sA[bl][(64 * wm + 32 * i + l32) * KQ4_LDS_ROW + 16 * half]);
-        bf[i] = *reinterpret_cast<const kq4_v4i *>(
-            &sB[bl][(64 * wn + 32 * i + l32) * KQ4_LDS_ROW + 16 * half]);
-        wdv[i] = sW[bl][64 * wn + 32 * i + l32];
+            &sA[bl][(32 * TM * wm + 32 * i + l32) * KQ4_LDS_ROW + 16 * half]);
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          const float4 x4 =
-              *reinterpret_cast<const float4 *>(&sX[bl][64 * wm + 32 * i + 8 * q + 4 * half]);
+          const float4 x4 = *reinterpret_cast<const float4 *>(
+              &sX[bl][32 * TM * wm + 32 * i + 8 * q + 4 * half]);
           xsv[i][4 * q + 0] = x4.x;
           xsv[i][4 * q + 1] = x4.y;
           xsv[i][4 * q + 2] = x4.z;
           xsv[i][4 * q + 3] = x4.w;
         }
       }
+#pragma unroll
+      for (int jn = 0; jn < TN; ++jn) {
+        bf[jn] = *reinterpret_cast<const kq4_v4i *>(
+            &sB[bl][(32 * TN * wn + 32 * jn + l32) * KQ4_LDS_ROW + 16 * half]);
+        wdv[jn] = sW[bl][32 * TN * wn + 32 * jn + l32];
+      }
       const kq4_v16i zero = {0};
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+      for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int jn = 0; jn < 2; ++jn) {
+        for (int jn = 0; jn < TN; ++jn) {
           if (CHAIN == KQ4_CHAIN_CTILE) {
             // lane half 0 carries elements 0..15 (low nibbles), half 1 elements 16..31
             const kq4_v4i z = {0, 0, 0, 0};
@@ -167,9 +206,9 @@ __global__ __launch_bounds__(256, 2) void kq4_gemm_kernel(
             const kq4_v16i chi = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bhi, zero, 0, 0, 0);
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
-              const float s = wdv[jn] * xsv[i][v];
-              acc[i][jn][v] = fmaf((float)clo[v], s, acc[i][jn][v]);
-              acc_hi[i][jn][v] = fmaf((float)chi[v], s, acc_hi[i][jn][v]);
+              const float sc = wdv[jn] * xsv[i][v];
+              acc[i][jn][v] = fmaf((float)clo[v], sc, acc[i][jn][v]);
+              acc_hi[i][jn][v] = fmaf((float)chi[v], sc, acc_hi[i][jn][v]);
             }
           } else {
             const kq4_v16i c = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[jn], zero, 0, 0, 0);
@@ -183,14 +222,14 @@ __global__ __launch_bounds__(256, 2) void kq4_gemm_kernel(
 
   // ---- epilogue: out = [res +] acc (CTILE: fl(lo + hi) first)
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < TM; ++i)
 #pragma unroll
-    for (int jn = 0; jn < 2; ++jn) {
-      const int row = n0 + 64 * wn + 32 * jn + l32;
+    for (int jn = 0; jn < TN; ++jn) {
+      const int row = n0 + 32 * TN * wn + 32 * jn + l32;
       if (row >= rows) continue;
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
-        const int tok = m0 + 64 * wm + 32 * i + kq4_mfma_tok(v, half);
+        const int tok = m0 + 32 * TM * wm + 32 * i + kq4_mfma_tok(v, half);
         if (tok >= n_tok) continue;
         float r = acc[i][jn][v];
         if (CHAIN == KQ4_CHAIN_CTILE) r = acc[i][jn][v] + acc_hi[i][jn][v];
@@ -200,23 +239,41 @@ __global__ __launch_bounds__(256, 2) void kq4_gemm_kernel(
     }
 }
 
+template <int TM, int TN>
+static hipError_t gemm_launch(float *out, const float *res, const uint8_t *w,
+                              const KQ4GemmAct &act, int rows, int n_tok, int nb, int nst,
+                              int chain, hipStream_t s) {
+  const int mtiles = (n_tok + 64 * TM - 1) / (64 * TM);
+  const int ntiles = (rows + 64 * TN - 1) / (64 * TN);
+  const dim3 grid((unsigned)(mtiles * ntiles));
+  if (chain == KQ4_CHAIN_CTILE)
+    hipLaunchKernelGGL((kq4_gemm_kernel<KQ4_CHAIN_CTILE, TM, TN>), grid, dim3(256), 0, s, out,
+                       res, w, act, rows, n_tok, nb, nst, mtiles, ntiles);
+  else if (chain == KQ4_CHAIN_GEMV32)
+    hipLaunchKernelGGL((kq4_gemm_kernel<KQ4_CHAIN_GEMV32, TM, TN>), grid, dim3(256), 0, s, out,
+                       res, w, act, rows, n_tok, nb, nst, mtiles, ntiles);
+  else
+    hipLaunchKernelGGL((kq4_gemm_kernel<KQ4_CHAIN_ASM, TM, TN>), grid, dim3(256), 0, s, out, res,
+                       w, act, rows, n_tok, nb, nst, mtiles, ntiles);
+  return hipGetLastError();
+}
+
+// The largest of the 128x128, 64x128 and 64x64 (tokens x rows) tiles that gives at least two
+// tiles per CU (else 64x64). KQ4_GEMM_TILE = 1/2/3 forces one (for measurement).
 int kq4_launch_gemm(float *out, const float *res, const uint8_t *w, const KQ4GemmAct &act,
-                    int rows, int cols, int n_tok, int chain, hipStream_t s) {
+                    int rows, int cols, int n_tok, int chain, int ncu, hipStream_t s) {
   const int nb = cols / 32;
   const int nst = (nb + KQ4_STREAM_CB - 1) / KQ4_STREAM_CB;
-  const int mtiles = (n_tok + KQ4_GEMM_BM - 1) / KQ4_GEMM_BM;
-  const int ntiles = (rows + KQ4_GEMM_BN - 1) / KQ4_GEMM_BN;
-  const int grid = mtiles * ntiles;
-  if (grid <= 0) return 0;
-#define KQ4_GEMM_LAUNCH(C)                                                                        \
-  hipLaunchKernelGGL((kq4_gemm_kernel<C>), dim3(grid), dim3(256), 0, s, out, res, w, act, rows,   \
-                     n_tok, nb, nst, mtiles, ntiles)
-  if (chain == KQ4_CHAIN_CTILE)
-    KQ4_GEMM_LAUNCH(KQ4_CHAIN_CTILE);
-  else if (chain == KQ4_CHAIN_GEMV32)
-    KQ4_GEMM_LAUNCH(KQ4_CHAIN_GEMV32);
-  else
-    KQ4_GEMM_LAUNCH(KQ4_CHAIN_ASM);
-#undef KQ4_GEMM_LAUNCH
-  return (int)hipGetLastError();
+  if (n_tok <= 0 || rows <= 0) return 0;
+  auto tiles = [&](int bm, int bn) {
+    return (long)((n_tok + bm - 1) / bm) * ((rows + bn - 1) / bn);
+  };
+  static const int force = [] { const char *e = getenv("KQ4_GEMM_TILE"); return e ? atoi(e) : 0; }();
+  int pick = force >= 1 && force <= 3 ? force
+             : tiles(128, 128) >= 2L * ncu ? 1 : (tiles(64, 128) >= 2L * ncu ? 2 : 3);
+  hipError_t e;
+  if (pick == 1) e = gemm_launch<2, 2>(out, res, w, act, rows, n_tok, nb, nst, chain, s);
+  else if (pick == 2) e = gemm_launch<1, 2>(out, res, w, act, rows, n_tok, nb, nst, chain, s);
+  else e = gemm_launch<1, 1>(out, res, w, act, rows, n_tok, nb, nst, chain, s);
+  return (int)e;
 }

@@ -57,7 +57,7 @@ struct KQ4GemmAct {
   long d_ts, d_bs;
 };
 int kq4_launch_gemm(float *out, const float *res, const uint8_t *w, const KQ4GemmAct &act,
-                    int rows, int cols, int n_tok, int chain, hipStream_t stream);
+                    int rows, int cols, int n_tok, int chain, int ncu, hipStream_t stream);
 
 // MoE
 int kq4_launch_moe_route(int *sel, float *pr, const float *logits, int T, int ne, int tk,
