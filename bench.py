@@ -20,6 +20,7 @@ MoE FFN). cpu_baseline: the reference's own x86-64 path (oracle/_ref, built from
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--m 1] [--no-cpu] [--no-extras]
     python bench.py --calibrate-copy      (512 MiB copy for PMC byte-counter scaling)
+    python bench.py --profile-op OP --m M --reps R   (one op repeated, for rocprofv3 runs)
 """
 import argparse
 import json
@@ -361,6 +362,48 @@ def cpu_baseline(m, budget_s=12.0):
                        f"distinct weight copies, {dt * 1e3:.2f} ms per layer")
 
 
+PROFILE_OPS = ("gemv_gate_up_2b", "gemv_gate_up_8b", "gemv_down_8b", "gemm_gate_8b",
+               "gemm_down_8b", "moe_30b_a3b")
+
+
+def profile_op(op, m, reps):
+    """Launches one op `reps` times back to back (eager) for rocprofv3 runs: the 2B / 8B decode
+    GEMVs, the 8B prefill GEMMs (m tokens) or the Qwen3-30B-A3B MoE FFN (m tokens)."""
+    import torch
+
+    import kq4
+
+    kq4.init(0)
+    st = torch.cuda.current_stream()
+    if op.startswith("moe"):
+        cfg = synth.QWEN3_30B_A3B_MOE
+        d, ne, tk, ef = cfg["hidden"], cfg["experts"], cfg["top_k"], cfg["ef"]
+        G, U, D = synth.make_moe(cfg, 50)
+        Gd, Ud = (kq4.prepare_dev(torch.from_numpy(a).cuda(), ne * ef, d) for a in (G, U))
+        Dd = kq4.prepare_dev(torch.from_numpy(D).cuda(), d, ne * ef)
+        X = torch.from_numpy(synth.make_activations(m, d, 60)).cuda()
+        lg = torch.from_numpy(synth.make_logits(m, ne, 61)).cuda()
+        sel = torch.empty((m, tk), dtype=torch.int32, device="cuda")
+        pr = torch.empty((m, tk), device="cuda")
+        Y = torch.empty((m, d), device="cuda")
+        kq4.moe_route_dev(sel, pr, lg, tk, stream=st)
+        for _ in range(reps):
+            kq4.moe_ffn_dev(Y, X, sel, pr, Gd, Ud, Dd, ne, d, ef, stream=st)
+    else:
+        cfg = CFG if op.endswith("2b") else synth.QWEN3_8B
+        h, f = cfg["hidden"], cfg["ffn"]
+        rows, cols = (h, f) if "down" in op else (f, h)
+        nmat = 2 if "gate_up" in op else 1
+        ws = [kq4.prepare_dev(torch.from_numpy(synth.make_q4_weights(rows, cols, 11 + i)).cuda(),
+                              rows, cols) for i in range(nmat)]
+        x = torch.from_numpy(synth.make_activations(m, cols, 20)).cuda()
+        outs = [torch.empty((m, rows), device="cuda") for _ in range(nmat)]
+        for _ in range(reps):
+            kq4.matmul_multi_dev(outs, x, ws, [rows] * nmat, cols, stream=st)
+    torch.cuda.synchronize()
+    return dict(op=op, m=m, reps=reps)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -373,6 +416,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a 512 MiB device copy (PMC byte-counter calibration)")
+    ap.add_argument("--profile-op", choices=PROFILE_OPS,
+                    help="only launch this op --reps times (for rocprofv3 runs); --m = tokens")
+    ap.add_argument("--reps", type=int, default=5)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
@@ -381,6 +427,9 @@ def main():
         sys.exit(2)
     if args.calibrate_copy:
         print(json.dumps(copy_calibration()))
+        return
+    if args.profile_op:
+        print(json.dumps(profile_op(args.profile_op, args.m, args.reps)))
         return
     g = run_gpu(args)
     line = {

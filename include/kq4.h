@@ -121,7 +121,8 @@ int kq4_weights_prepare_dev(uint8_t *dst, const uint8_t *w4x4, int rows, int col
 
 /* Activation quantizer (quantize_row_q8_0_act vllm_safetensors.c:7893-7920) for n_batch rows:
  * xq int8 [n_batch][cols], xd f32 [n_batch][cols/32]. xde (may be NULL) receives the scale
- * each token's chain multiplies by: f32(f16_rne(xd)) for ASM-chain tokens, xd otherwise. */
+ * each token's chain multiplies by: f32(f16_rne(xd)) for ASM-chain tokens, xd otherwise.
+ * Device buffers of this API: x and xq 16-byte aligned (xq 8-byte here), scales 4-byte. */
 int kq4_quantize_dev(int8_t *xq, float *xd, float *xde, const float *x, int n_batch, int cols,
                      int chain, void *stream);
 

@@ -210,6 +210,8 @@ int matmul_impl(int n_mats, float *const *out, const float *const *res, const ui
     if ((uintptr_t)w[i] % 16) return fail(KQ4_EINVAL, "weights not 16-byte aligned");
   }
   if (n == 0) return KQ4_OK;
+  if ((x && (uintptr_t)x % 16) || (xq_in && (uintptr_t)xq_in % 16) || (xd_in && (uintptr_t)xd_in % 4))
+    return fail(KQ4_EINVAL, "activations not aligned (x, xq: 16 B; xd: 4 B)");
   DevState *ds = nullptr;
   int rc = cur_dev(&ds);
   if (rc) return rc;
@@ -230,19 +232,14 @@ int matmul_impl(int n_mats, float *const *out, const float *const *res, const ui
   const int8_t *xq_t = nullptr;
   const float *xd_t = nullptr;
   if (x) {
+    // every token at once, token-major (contiguous stores; the GEMM's staging reads 32-byte
+    // token rows per block at a stride, and the tail GEMV reads its rows as they are)
     int8_t *q = cv.take<int8_t>((size_t)n * cols);
     float *d = cv.take<float>((size_t)n * nb);
-    // main tokens block-major (contiguous 32-byte token rows per block for the MFMA staging)
-    KQ4_HIP((hipError_t)kq4_launch_quantize(x, q, d, nullptr, main_n, cols, 0, s, 1));
-    act = KQ4GemmAct{q, 32, (long)main_n * 32, d, 1, main_n};
-    if (tail) {
-      int8_t *qt = q + (size_t)main_n * cols;
-      float *dt = d + (size_t)main_n * nb;
-      KQ4_HIP((hipError_t)kq4_launch_quantize(x + (size_t)main_n * cols, qt, dt, nullptr, tail,
-                                              cols, 0, s, 0));
-      xq_t = qt;
-      xd_t = dt;
-    }
+    KQ4_HIP((hipError_t)kq4_launch_quantize(x, q, d, nullptr, n, cols, 0, s, 0));
+    act = KQ4GemmAct{q, cols, 32, d, nb, 1};
+    xq_t = q + (size_t)main_n * cols;
+    xd_t = d + (size_t)main_n * nb;
   } else {
     cv.off = qbytes;
     act = KQ4GemmAct{xq_in, cols, 32, xd_in, nb, 1};
@@ -411,6 +408,8 @@ int kq4_quantize_dev(int8_t *xq, float *xd, float *xde, const float *x, int n_ba
                      int chain, void *stream) {
   if (n_batch < 0 || cols <= 0 || cols % 32 || !xq || !xd || (!x && n_batch))
     return fail(KQ4_EINVAL, "quantize: n_batch=%d cols=%d", n_batch, cols);
+  if ((uintptr_t)x % 16 || (uintptr_t)xq % 8 || (uintptr_t)xd % 4 || (uintptr_t)xde % 4)
+    return fail(KQ4_EINVAL, "quantize: x must be 16-byte, xq 8-byte aligned");
   KQ4_HIP((hipError_t)kq4_launch_quantize(x, xq, xd, xde, n_batch, cols,
                                           asm_tokens_for(chain, n_batch),
                                           (hipStream_t)stream, 0));
