@@ -255,13 +255,28 @@ def run_extras():
             od, xf, D[i], h, f, stream=st), len(D))
         t_q = _time_graph(torch, lambda i, st: kq4.matmul_dev(
             oq, x, Q[i], qkv, h, stream=st), len(Q))
+        # the FFN's second half: SiLU-multiply fused into the down projection, and the same as
+        # two launches (the in-place product, then the down projection); |up| < 1 keeps the
+        # repeatedly multiplied gate bounded
+        xu = torch.rand((m, f), device="cuda") * 2 - 1
+        xs = xf.clone()
+        t_sd = _time_graph(torch, lambda i, st: kq4.matmul_silu_dev(
+            od, xf, xu, D[i], h, f, stream=st), len(D))
+
+        def unfused(i, st):
+            kq4.silu_mul_dev(xs, xu, stream=st)
+            kq4.matmul_dev(od, xs, D[i], h, f, stream=st)
+        t_su = _time_graph(torch, unfused, len(D))
         b_gu = 2 * f * h * 18 // 32 + m * h * 4 + 2 * m * f * 4
         b_dn = h * f * 18 // 32 + m * f * 4 + m * h * 4
         b_q = qkv * h * 18 // 32 + m * h * 4 + m * qkv * 4
         dec[f"M{m}"] = {
             "gate_up_us": round(t_gu, 2), "gate_up_GBs": round(b_gu / t_gu / 1e3, 1),
             "down_us": round(t_dn, 2), "down_GBs": round(b_dn / t_dn / 1e3, 1),
-            "qkv_us": round(t_q, 2), "qkv_GBs": round(b_q / t_q / 1e3, 1)}
+            "qkv_us": round(t_q, 2), "qkv_GBs": round(b_q / t_q / 1e3, 1),
+            "silu_down_us": round(t_sd, 2),
+            "silu_down_GBs": round((b_dn + m * f * 4) / t_sd / 1e3, 1),
+            "silu_then_down_us": round(t_su, 2)}
     out["qwen3_8b_decode"] = dec
     pre = {}
     for m in (512, 2048):

@@ -89,6 +89,16 @@ int kq4_weights_clear(void);
 int kq4_matmul(float *out, const float *x, const float *residual, const uint8_t *w4x4, int rows,
                int cols, int n_batch, int chain, uint64_t wkey);
 
+/* The dense FFN's SiLU-multiply and down projection in one call:
+ * out = [residual +] W.silu_mul(gate, up), gate/up [n_batch][cols]. silu_mul is the reference's
+ * AArch64 vllm_silu_mul_worker element rule (vllm_safetensors.c:10932-10958: exp_neon4 :4041,
+ * FRECPE and two FRECPS Newton steps), bit for bit; it replaces the worker's parfor plus
+ * dyn_matvec_q4_q8_fused_down_residual[_batched] (:8663, :8762; dense decode :16756-16767,
+ * batched :17232-17247). The product is quantized without being written to memory. */
+int kq4_matmul_silu(float *out, const float *gate, const float *up, const float *residual,
+                    const uint8_t *w4x4, int rows, int cols, int n_batch, int chain,
+                    uint64_t wkey);
+
 /* Up to KQ4_MAX_MATS matrices sharing one activation (fused QKV / gate+up wrappers); wkeys may
  * be NULL (no caching) or hold one key per matrix (0 = no caching for that matrix). */
 int kq4_matmul_multi(int n_mats, float *const *out, const float *const *residual,
@@ -129,6 +139,19 @@ int kq4_quantize_dev(int8_t *xq, float *xd, float *xde, const float *x, int n_ba
 /* Quantize x once, then out = [residual +] W.x. */
 int kq4_matmul_dev(float *out, const float *x, const float *residual, const uint8_t *w,
                    int rows, int cols, int n_batch, int chain, void *stream);
+
+/* kq4_matmul_silu on device buffers (gate, up 16-byte aligned): up to 4 tokens in one launch
+ * (the GEMV forms the product while quantizing), else the quantizer forms it. */
+int kq4_matmul_silu_dev(float *out, const float *gate, const float *up, const float *residual,
+                        const uint8_t *w, int rows, int cols, int n_batch, int chain,
+                        void *stream);
+
+/* vllm_silu_mul_worker over n elements in place (vllm_safetensors.c:10932-10958):
+ * gate[i] = silu_mul(gate[i], up[i]) in the NEON form for i < (n & ~3), bit for bit; the last
+ * n % 4 elements take the worker's scalar tail fast_silu(g) * u (:3685-3696), here with a
+ * correctly rounded exp (the reference's libm expf may differ in the last bit). gate and up
+ * 16-byte aligned. */
+int kq4_silu_mul_dev(float *gate, const float *up, long n, void *stream);
 
 /* Up to KQ4_MAX_MATS weight matrices sharing one activation (one quantization, one launch):
  * fused QKV (dyn_matvec_q4_q8_fused_qkv_batched :8684) and gate/up (:8738). residual[i] may

@@ -44,6 +44,11 @@ int kq4_dyn_matvec_q4_q8_fused_down_residual(float *x, const float *residual,
                                              const uint8_t *q4_down, const float *activated,
                                              int hidden_dim, int ffn_dim);
 
+/* vllm_silu_mul_worker's parfor (:10932-10958, called over ffn_dim elements at :16735) followed
+ * by dyn_matvec_q4_q8_fused_down_residual (:8663): x = residual + down.silu_mul(gate, up). */
+int kq4_silu_mul_down_residual(float *x, const float *residual, const uint8_t *q4_down,
+                               const float *gate, const float *up, int hidden_dim, int ffn_dim);
+
 /* dyn_matvec_q4_q8_fused_qkv_batched (:8684) */
 int kq4_dyn_matvec_q4_q8_fused_qkv_batched(float *q_out, float *k_out, float *v_out,
                                            const uint8_t *q4_q, const uint8_t *q4_k,
@@ -71,6 +76,13 @@ int kq4_dyn_matvec_q4_q8_fused_down_residual_batched(float *x_batch, const float
                                                      const float *activated_batch, int hidden_dim,
                                                      int ffn_dim, int n_batch,
                                                      const uint8_t *x8_down);
+
+/* The batched twin: the parfor over n_batch * ffn_dim elements (:17232-17233) followed by
+ * dyn_matvec_q4_q8_fused_down_residual_batched (:8762). */
+int kq4_silu_mul_down_residual_batched(float *x_batch, const float *residual_batch,
+                                       const uint8_t *q4_down, const float *gate_batch,
+                                       const float *up_batch, int hidden_dim, int ffn_dim,
+                                       int n_batch);
 
 /* One MoE layer as st_moe_ffn_sparse_q4 reads it from STModelWeights (:12937-12952): fp32 router
  * [ne][d], q4 4x4 G/U [ne*ef][d] and D [d][ne*ef]. */

@@ -46,7 +46,7 @@ struct DevState {
   bool ready = false;
   int ncu = 256;        // compute units (sizes the GEMV grid)
   Buf ws;    // quantized activations, MoE staging
-  Buf hx, hres, hout, hw, hsel, hpr, hstage;   // staging for the host-pointer API
+  Buf hx, hu, hres, hout, hw, hsel, hpr, hstage;   // staging for the host-pointer API
   std::unordered_map<uint64_t, WEntry> wcache;
 };
 
@@ -140,34 +140,45 @@ void plan_gemv(int sets, int nb, int ncu, int *half_out, int *nw_out) {
 }
 
 // Whether the GEMV quantizes its fp32 activations itself (one launch per op) or reads them from
-// a separate quantize launch. Every wave quantizes its own stages, so the in-kernel path repeats
-// the work once per row set; it is used up to KQ4_GEMV_FQ_MAX_M tokens, where that costs less
-// than a second launch. KQ4_GEMV_FQ=0 turns it off (for measurement).
-bool gemv_fq(int n) {
+// a separate quantize launch (about 2 us more per op in a graph). Every workgroup quantizes the
+// whole activation for itself, so a CU spends VALU time on cols * n elements per workgroup it
+// runs: work = cols * n * ceil(workgroups / CUs). Measured on MI355X (Qwen3-8B and Qwen3-VL-2B
+// decode shapes, M = 1..4) the in-kernel path is faster up to about 45K such elements, and with
+// the SiLU product (about 30 more instructions per element) up to about 15K (the 8B down
+// projection at one token, 12288, still gains 1 us; at two tokens it loses 2 us).
+// KQ4_GEMV_FQ=0 turns it off; KQ4_GEMV_FQ_WORK and KQ4_GEMV_SILU_FQ_WORK set the two limits.
+bool gemv_fq(long work, int n, bool silu) {
   static const int env = env_int("KQ4_GEMV_FQ", -1);
-  static const int max_m = env_int("KQ4_GEMV_FQ_M", KQ4_GEMV_FQ_MAX_M);
-  return env != 0 && n <= max_m && n <= KQ4_GEMV_FQ_MAX_M;
+  static const long max_work = env_int("KQ4_GEMV_FQ_WORK", 45000);
+  static const long max_silu = env_int("KQ4_GEMV_SILU_FQ_WORK", 15000);
+  return env != 0 && n <= KQ4_GEMV_FQ_MAX_M && work <= (silu ? max_silu : max_work);
 }
 
 // GEMV over n_mats matrices for n tokens (n <= 8): from fp32 x (quantized in the kernel or by a
-// separate launch) or from token-major xq/xd.
+// separate launch; with xu the activation is silu_mul(x, xu)) or from token-major xq/xd.
 int run_gemv(DevState *ds, int n_mats, float *const *out, const float *const *res,
-             const uint8_t *const *w, const int *rows, int cols, const float *x,
+             const uint8_t *const *w, const int *rows, int cols, const float *x, const float *xu,
              const int8_t *xq, const float *xd, int n, int asm_tokens, hipStream_t s) {
   const int nb = cols / 32;
   int rc;
   KQ4GemvArgs a;
   memset(&a, 0, sizeof(a));
+  int sets = 0;
+  for (int i = 0; i < n_mats; ++i) sets += (rows[i] + 31) / 32;
+  int hs = 0, nw = 1;
+  plan_gemv(sets, nb, ds->ncu, &hs, &nw);
   if (x) {
-    if (gemv_fq(n)) {
+    const long per_cu = ((long)(sets << hs) + ds->ncu - 1) / ds->ncu;
+    if (gemv_fq(per_cu * cols * n, n, xu != nullptr)) {
       a.xf = x;
+      a.xu = xu;
     } else {
       if ((rc = ensure(ds->ws, al256((size_t)n * cols) + al256((size_t)n * nb * sizeof(float)))))
         return rc;
       Carve cv{static_cast<char *>(ds->ws.p)};
       int8_t *q = cv.take<int8_t>((size_t)n * cols);
       float *d = cv.take<float>((size_t)n * nb);
-      KQ4_HIP((hipError_t)kq4_launch_quantize(x, q, d, nullptr, n, cols, 0, s, 0));
+      KQ4_HIP((hipError_t)kq4_launch_quantize(x, q, d, nullptr, n, cols, 0, s, 0, xu));
       xq = q;
       xd = d;
     }
@@ -179,10 +190,6 @@ int run_gemv(DevState *ds, int n_mats, float *const *out, const float *const *re
   a.cols = cols;
   a.nb = nb;
   const int kind = gemv_kind(n);
-  int sets = 0;
-  for (int i = 0; i < n_mats; ++i) sets += (rows[i] + 31) / 32;
-  int hs = 0, nw = 1;
-  plan_gemv(sets, nb, ds->ncu, &hs, &nw);
   int wg = 0;
   for (int i = 0; i < n_mats; ++i) {
     KQ4GemvMat &m = a.mat[i];
@@ -197,9 +204,10 @@ int run_gemv(DevState *ds, int n_mats, float *const *out, const float *const *re
   return KQ4_OK;
 }
 
+// x (fp32; with xu the activation is silu_mul(x, xu)) or xq_in/xd_in (pre-quantized).
 int matmul_impl(int n_mats, float *const *out, const float *const *res, const uint8_t *const *w,
                 const int *rows, int cols, const float *x, const int8_t *xq_in,
-                const float *xd_in, int n, int chain, hipStream_t s) {
+                const float *xd_in, int n, int chain, hipStream_t s, const float *xu = nullptr) {
   if (n_mats < 1 || n_mats > KQ4_MAX_MATS) return fail(KQ4_EINVAL, "n_mats=%d", n_mats);
   if (chain < KQ4_CHAIN_AUTO || chain > KQ4_CHAIN_ASM) return fail(KQ4_EINVAL, "chain=%d", chain);
   if (n < 0) return fail(KQ4_EINVAL, "n_batch=%d", n);
@@ -210,8 +218,10 @@ int matmul_impl(int n_mats, float *const *out, const float *const *res, const ui
     if ((uintptr_t)w[i] % 16) return fail(KQ4_EINVAL, "weights not 16-byte aligned");
   }
   if (n == 0) return KQ4_OK;
-  if ((x && (uintptr_t)x % 16) || (xq_in && (uintptr_t)xq_in % 16) || (xd_in && (uintptr_t)xd_in % 4))
-    return fail(KQ4_EINVAL, "activations not aligned (x, xq: 16 B; xd: 4 B)");
+  if ((x && (uintptr_t)x % 16) || (xu && (uintptr_t)xu % 16) || (xq_in && (uintptr_t)xq_in % 16) ||
+      (xd_in && (uintptr_t)xd_in % 4))
+    return fail(KQ4_EINVAL, "activations not aligned (x, up, xq: 16 B; xd: 4 B)");
+  if (xu && !x) return fail(KQ4_EINVAL, "up without gate");
   DevState *ds = nullptr;
   int rc = cur_dev(&ds);
   if (rc) return rc;
@@ -219,7 +229,7 @@ int matmul_impl(int n_mats, float *const *out, const float *const *res, const ui
   const size_t qbytes = al256((size_t)n * cols) + al256((size_t)n * nb * sizeof(float));
 
   if (n <= KQ4_GEMV_MAX_M)
-    return run_gemv(ds, n_mats, out, res, w, rows, cols, x, xq_in, xd_in, n,
+    return run_gemv(ds, n_mats, out, res, w, rows, cols, x, xu, xq_in, xd_in, n,
                     asm_tokens_for(chain, n), s);
 
   // prefill: int8-MFMA GEMM on the main segment, GEMV on the 1..3-token CTILE tail (AUTO)
@@ -236,7 +246,7 @@ int matmul_impl(int n_mats, float *const *out, const float *const *res, const ui
     // token rows per block at a stride, and the tail GEMV reads its rows as they are)
     int8_t *q = cv.take<int8_t>((size_t)n * cols);
     float *d = cv.take<float>((size_t)n * nb);
-    KQ4_HIP((hipError_t)kq4_launch_quantize(x, q, d, nullptr, n, cols, 0, s, 0));
+    KQ4_HIP((hipError_t)kq4_launch_quantize(x, q, d, nullptr, n, cols, 0, s, 0, xu));
     act = KQ4GemmAct{q, cols, 32, d, nb, 1};
     xq_t = q + (size_t)main_n * cols;
     xd_t = d + (size_t)main_n * nb;
@@ -256,7 +266,7 @@ int matmul_impl(int n_mats, float *const *out, const float *const *res, const ui
       o2[i] = out[i] + (size_t)main_n * rows[i];
       r2[i] = (res && res[i]) ? res[i] + (size_t)main_n * rows[i] : nullptr;
     }
-    return run_gemv(ds, n_mats, o2, r2, w, rows, cols, nullptr, xq_t, xd_t, tail, 0, s);
+    return run_gemv(ds, n_mats, o2, r2, w, rows, cols, nullptr, nullptr, xq_t, xd_t, tail, 0, s);
   }
   return KQ4_OK;
 }
@@ -440,6 +450,23 @@ int kq4_matmul_dev(float *out, const float *x, const float *residual, const uint
                      (hipStream_t)stream);
 }
 
+int kq4_matmul_silu_dev(float *out, const float *gate, const float *up, const float *residual,
+                        const uint8_t *w, int rows, int cols, int n_batch, int chain,
+                        void *stream) {
+  if ((!gate || !up) && n_batch) return fail(KQ4_EINVAL, "null gate/up");
+  const float *res[1] = {residual};
+  return matmul_impl(1, &out, res, &w, &rows, cols, gate, nullptr, nullptr, n_batch, chain,
+                     (hipStream_t)stream, up);
+}
+
+int kq4_silu_mul_dev(float *gate, const float *up, long n, void *stream) {
+  if (n < 0 || (n && (!gate || !up))) return fail(KQ4_EINVAL, "silu_mul: n=%ld", n);
+  if ((uintptr_t)gate % 16 || (uintptr_t)up % 16)
+    return fail(KQ4_EINVAL, "silu_mul: gate and up must be 16-byte aligned");
+  KQ4_HIP((hipError_t)kq4_launch_silu_mul(gate, up, n, (hipStream_t)stream));
+  return KQ4_OK;
+}
+
 int kq4_matmul_multi_dev(int n_mats, float *const *out, const float *const *residual,
                          const uint8_t *const *w, const int *rows, int cols, const float *x,
                          int n_batch, int chain, void *stream) {
@@ -546,9 +573,14 @@ int kq4_weights_clear(void) {
   return n;
 }
 
-int kq4_matmul_multi(int n_mats, float *const *out, const float *const *residual,
-                     const uint8_t *const *w4x4, const int *rows, int cols, const float *x,
-                     int n_batch, int chain, const uint64_t *wkeys) {
+}  // extern "C"
+
+namespace {
+
+// The host-pointer matmul: stage x (and up) and the residuals, run on the device, read back.
+int host_matmul(int n_mats, float *const *out, const float *const *residual,
+                const uint8_t *const *w4x4, const int *rows, int cols, const float *x,
+                const float *xu, int n_batch, int chain, const uint64_t *wkeys) {
   if (n_mats < 1 || n_mats > KQ4_MAX_MATS || !out || !w4x4 || !rows || !x || n_batch < 1) {
     fail(KQ4_EINVAL, "matmul: n_mats=%d n_batch=%d", n_mats, n_batch);
     return 0;
@@ -574,11 +606,13 @@ int kq4_matmul_multi(int n_mats, float *const *out, const float *const *residual
     rc = dev_weights(ds, wkeys ? wkeys[i] : 0, w4x4[i], rows[i], cols,
                      i == 0 ? ds->hw : tw[i], &dw[i]);
   int ok = 0;
-  if (!rc && !ensure(ds->hx, xb) && !ensure(ds->hout, total_o) && !ensure(ds->hres, total_o)) {
+  if (!rc && !ensure(ds->hx, xb) && !ensure(ds->hout, total_o) && !ensure(ds->hres, total_o) &&
+      (!xu || !ensure(ds->hu, xb))) {
     float *dout[KQ4_MAX_MATS];
     const float *dres[KQ4_MAX_MATS];
     char *po = static_cast<char *>(ds->hout.p), *pr = static_cast<char *>(ds->hres.p);
-    bool good = hipMemcpy(ds->hx.p, x, xb, hipMemcpyHostToDevice) == hipSuccess;
+    bool good = hipMemcpy(ds->hx.p, x, xb, hipMemcpyHostToDevice) == hipSuccess &&
+                (!xu || hipMemcpy(ds->hu.p, xu, xb, hipMemcpyHostToDevice) == hipSuccess);
     for (int i = 0; i < n_mats && good; ++i) {
       dout[i] = reinterpret_cast<float *>(po);
       dres[i] = nullptr;
@@ -591,7 +625,8 @@ int kq4_matmul_multi(int n_mats, float *const *out, const float *const *residual
     }
     if (good &&
         matmul_impl(n_mats, dout, dres, dw, rows, cols, static_cast<const float *>(ds->hx.p),
-                    nullptr, nullptr, n_batch, chain, nullptr) == KQ4_OK) {
+                    nullptr, nullptr, n_batch, chain, nullptr,
+                    xu ? static_cast<const float *>(ds->hu.p) : nullptr) == KQ4_OK) {
       ok = 1;
       for (int i = 0; i < n_mats && ok; ++i)
         if (hipMemcpy(out[i], dout[i], ob[i], hipMemcpyDeviceToHost) != hipSuccess) {
@@ -608,10 +643,31 @@ int kq4_matmul_multi(int n_mats, float *const *out, const float *const *residual
   return ok;
 }
 
+}  // namespace
+
+extern "C" {
+
+int kq4_matmul_multi(int n_mats, float *const *out, const float *const *residual,
+                     const uint8_t *const *w4x4, const int *rows, int cols, const float *x,
+                     int n_batch, int chain, const uint64_t *wkeys) {
+  return host_matmul(n_mats, out, residual, w4x4, rows, cols, x, nullptr, n_batch, chain, wkeys);
+}
+
 int kq4_matmul(float *out, const float *x, const float *residual, const uint8_t *w4x4, int rows,
                int cols, int n_batch, int chain, uint64_t wkey) {
   const float *res[1] = {residual};
-  return kq4_matmul_multi(1, &out, res, &w4x4, &rows, cols, x, n_batch, chain, &wkey);
+  return host_matmul(1, &out, res, &w4x4, &rows, cols, x, nullptr, n_batch, chain, &wkey);
+}
+
+int kq4_matmul_silu(float *out, const float *gate, const float *up, const float *residual,
+                    const uint8_t *w4x4, int rows, int cols, int n_batch, int chain,
+                    uint64_t wkey) {
+  if (!up) {
+    fail(KQ4_EINVAL, "matmul_silu: null up");
+    return 0;
+  }
+  const float *res[1] = {residual};
+  return host_matmul(1, &out, res, &w4x4, &rows, cols, gate, up, n_batch, chain, &wkey);
 }
 
 int kq4_moe_ffn(float *Y, const float *X, const int *sel, const float *pr, int T, int tk,

@@ -23,6 +23,55 @@ KQ4_DEV float kq4_f16_round(float x) { return __half2float(__float2half_rn(x)); 
 KQ4_DEV uint32_t kq4_lo16(uint32_t w) { return (w << 4) & 0xF0F0F0F0u; }
 KQ4_DEV uint32_t kq4_hi16(uint32_t w) { return w & 0xF0F0F0F0u; }
 
+// ---- SiLU(g) * u of the dense FFN ---------------------------------------------------------
+// The reference's dense path runs its SiLU-multiply on AArch64 as vllm_silu_mul_worker
+// (vllm_safetensors.c:10932-10958): 4-wide, every element of n & ~3, with exp_neon4 (:4041-4068),
+// the FRECPE reciprocal estimate and two FRECPS Newton steps. Each step below is the same IEEE
+// binary32 operation as the NEON instruction it stands for (vfmaq/vfmsq = one fused rounding,
+// vrndnq = round to nearest even, vcvtq_s32 = truncation), so the result is that path's, bit for
+// bit, for finite inputs.
+
+// exp_neon4: clamp to [-87, 87], n = rne(x * log2e), r = x - n*ln2 (fused), degree-7 Taylor
+// polynomial in Horner form (fused steps), 2^n added to the exponent field.
+KQ4_DEV float kq4_exp_neon(float x) {
+  x = fminf(fmaxf(x, -87.0f), 87.0f);
+  const float n = rintf(x * 1.4426950408889634f);
+  const float r = fmaf(-n, 0.6931471805599453f, x);
+  float p = 0.001388888888888889f;
+  p = fmaf(p, r, 0.008333333333333333f);
+  p = fmaf(p, r, 0.041666666666666664f);
+  p = fmaf(p, r, 0.16666666666666666f);
+  p = fmaf(p, r, 0.5f);
+  p = fmaf(p, r, 1.0f);
+  p = fmaf(p, r, 1.0f);
+  return __int_as_float(__float_as_int(p) + ((int)n << 23));
+}
+
+// FRECPE (ARMv8 FPRecipEstimate, single precision, no FEAT_RPRES) for positive normal x below
+// 2^126, the range of 1 + exp_neon4(-g): the 8 fraction bits f below the leading one select
+// a = 2*(256 + f) + 1, the estimate mantissa is r = (floor(2^19 / a) + 1) / 2 in [256, 511] and
+// the exponent 253 - e. floor(2^19 / a) is taken from a float reciprocal: a is odd, so the exact
+// quotient is at least 1/a >= 1/1023 away from an integer, far more than the reciprocal's
+// error (< 2^-22 relative, < 3e-4 absolute here).
+KQ4_DEV float kq4_frecpe(float x) {
+  const uint32_t b = __float_as_uint(x);
+  const uint32_t e = (b >> 23) & 0xFFu;
+  const int a = 2 * (256 + (int)((b >> 15) & 0xFFu)) + 1;
+  const int q = (int)(524288.0f * __builtin_amdgcn_rcpf((float)a));
+  const uint32_t r = (uint32_t)((q + 1) >> 1);
+  return __uint_as_float((b & 0x80000000u) | ((253u - e) << 23) | ((r & 0xFFu) << 15));
+}
+
+// fl(fl(g * rec) * u) with rec = 1 / (1 + e^-g) from FRECPE and two FRECPS steps
+// (FRECPS = 2 - d*r with one rounding).
+KQ4_DEV float kq4_silu_mul(float g, float u) {
+  const float den = kq4_exp_neon(-g) + 1.0f;
+  float rec = kq4_frecpe(den);
+  rec = rec * fmaf(-den, rec, 2.0f);
+  rec = rec * fmaf(-den, rec, 2.0f);
+  return (g * rec) * u;
+}
+
 // 4 x int8 dot product accumulated into c (v_dot4_i32_i8).
 KQ4_DEV int kq4_dot4(uint32_t a, uint32_t b, int c) {
   return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);

@@ -65,7 +65,6 @@ __global__ __launch_bounds__(256, 2) void kq4_gemm_kernel(
   const int wave = t >> 6;
   const int wm = wave >> 1, wn = wave & 1;
   const int l32 = lane & 31, half = lane >> 5;
-  const int groups = rows >> 2;
 
   float acc[TM][TN][16];
   float acc_hi[TM][TN][16];

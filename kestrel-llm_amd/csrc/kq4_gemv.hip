@@ -119,22 +119,25 @@ KQ4_DEV float kq4_gv_wd(const KQ4GvStage<HS> &st, int jb, int p) {
 // undoes the 16*(n-8) weight scaling exactly). Issuing them before the weights keeps the in-order
 // load counter from making the quantization wait for the weights.
 //
-// FQ (M <= KQ4_GEMV_FQ_MAX_M): lane quad (4q .. 4q+3) owns block q for one token per pass, 8
+// FQ = 0: pre-quantized; 1: fp32 activations; 2: fp32 gate and up, activation = silu_mul(g, u)
+// (kq4_silu_mul, the dense FFN's down input, vllm_safetensors.c:10932-10958).
+// FQ 1, 2 (M <= KQ4_GEMV_FQ_MAX_M): lane quad (4q .. 4q+3) owns block q for one token per pass, 8
 // fp32 each; the quantization restates quantize_row_q8_0_act (vllm_safetensors.c:7893-7920):
 // d = amax/127 is a true division, x/d the Markstein-corrected quotient q = x*y,
 // q += fma(-q, d, x)*y with y = RN(1/d), which is the correctly rounded x/d for these normal
 // operands, so the codes are the reference's bit for bit.
 // Pre-quantized: lane i copies 16-B units i, i+64, .. of the stage's codes and scales i, i+64.
-template <int M, bool FQ>
+template <int M, int FQ>
 struct KQ4GvAct {
   static constexpr int NQ = FQ ? 1 : (32 * M + 63) / 64;   // uint4 per lane
   static constexpr int NX = FQ ? 1 : (16 * M + 63) / 64;   // scales per lane
   float4 f[FQ ? 2 * M : 1];
+  float4 u[FQ == 2 ? 2 * M : 1];
   uint4 q[NQ];
   float x[NX];
 };
 
-template <int M, bool FQ>
+template <int M, int FQ>
 KQ4_DEV void kq4_gv_act_load(KQ4GvAct<M, FQ> &r, const KQ4GemvArgs &a, int st, int lane) {
   const int nb = a.nb, cols = a.cols;
   const int kb = st * KQ4_GV_CB;
@@ -147,9 +150,19 @@ KQ4_DEV void kq4_gv_act_load(KQ4GvAct<M, FQ> &r, const KQ4GemvArgs &a, int st, i
             reinterpret_cast<const float4 *>(a.xf + (size_t)m * cols + (size_t)b * 32 + 8 * qq);
         r.f[2 * m] = src[0];
         r.f[2 * m + 1] = src[1];
+        if (FQ == 2) {
+          const float4 *su = reinterpret_cast<const float4 *>(a.xu + (size_t)m * cols +
+                                                              (size_t)b * 32 + 8 * qq);
+          r.u[2 * m] = su[0];
+          r.u[2 * m + 1] = su[1];
+        }
       } else {
         r.f[2 * m] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         r.f[2 * m + 1] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (FQ == 2) {
+          r.u[2 * m] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+          r.u[2 * m + 1] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
       }
     }
   } else {
@@ -170,15 +183,21 @@ KQ4_DEV void kq4_gv_act_load(KQ4GvAct<M, FQ> &r, const KQ4GemvArgs &a, int st, i
   }
 }
 
-template <int M, bool FQ>
+template <int M, int FQ>
 KQ4_DEV void kq4_gv_act_put(const KQ4GvAct<M, FQ> &r, const KQ4GemvArgs &a, int lane,
                             uint8_t *sq, float (*sx)[8]) {
   if (FQ) {
     const int blk = lane >> 2, qq = lane & 3;
 #pragma unroll
     for (int m = 0; m < M; ++m) {
-      const float v[8] = {r.f[2 * m].x, r.f[2 * m].y, r.f[2 * m].z, r.f[2 * m].w,
-                          r.f[2 * m + 1].x, r.f[2 * m + 1].y, r.f[2 * m + 1].z, r.f[2 * m + 1].w};
+      float v[8] = {r.f[2 * m].x, r.f[2 * m].y, r.f[2 * m].z, r.f[2 * m].w,
+                    r.f[2 * m + 1].x, r.f[2 * m + 1].y, r.f[2 * m + 1].z, r.f[2 * m + 1].w};
+      if (FQ == 2) {
+        const float u[8] = {r.u[2 * m].x, r.u[2 * m].y, r.u[2 * m].z, r.u[2 * m].w,
+                            r.u[2 * m + 1].x, r.u[2 * m + 1].y, r.u[2 * m + 1].z, r.u[2 * m + 1].w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = kq4_silu_mul(v[i], u[i]);
+      }
       float amax = 1e-10f;
 #pragma unroll
       for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
@@ -281,7 +300,7 @@ KQ4_DEV void kq4_gv_mfma_stage(const KQ4GvStage<HS> &st, const uint8_t *sq, cons
 
 // One workgroup per 32-row set (HS = 0) or per half set (HS = 1), up to 16 waves splitting K
 // (every variant fits the 128 VGPRs that allows).
-template <int M, bool FQ, int KIND, int HS>
+template <int M, int FQ, int KIND, int HS>
 __global__ __launch_bounds__(1024) void kq4_gemv_kernel(const KQ4GemvArgs a) {
   extern __shared__ __align__(16) uint8_t kq4_gv_lds[];
   constexpr int SLAB = kq4_gv_slab<M>();
@@ -362,7 +381,7 @@ __global__ __launch_bounds__(1024) void kq4_gemv_kernel(const KQ4GemvArgs a) {
   }
 }
 
-template <int M, bool FQ, int KIND, int HS>
+template <int M, int FQ, int KIND, int HS>
 static hipError_t gv_launch(const KQ4GemvArgs &a, int nw, int grid, hipStream_t s) {
   const size_t lds = (size_t)nw * kq4_gv_slab<M>();
   static bool attr = false;   // allow more than 64 KB of dynamic LDS, once per variant
@@ -377,7 +396,7 @@ static hipError_t gv_launch(const KQ4GemvArgs &a, int nw, int grid, hipStream_t 
   return hipGetLastError();
 }
 
-template <int M, bool FQ>
+template <int M, int FQ>
 static hipError_t gv_launch_k(const KQ4GemvArgs &a, int kind, int hs, int nw, int grid,
                               hipStream_t s) {
   if (kind == 0)
@@ -387,14 +406,15 @@ static hipError_t gv_launch_k(const KQ4GemvArgs &a, int kind, int hs, int nw, in
 
 // In-kernel quantization exists for M <= KQ4_GEMV_FQ_MAX_M.
 template <int M>
-static hipError_t gv_launch_m(const KQ4GemvArgs &a, int kind, bool fq, int hs, int nw, int grid,
+static hipError_t gv_launch_m(const KQ4GemvArgs &a, int kind, int fq, int hs, int nw, int grid,
                               hipStream_t s) {
   constexpr int MF = M <= KQ4_GEMV_FQ_MAX_M ? M : 1;
   if (fq) {
     if (M > KQ4_GEMV_FQ_MAX_M) return hipErrorInvalidValue;
-    return gv_launch_k<MF, true>(a, kind, hs, nw, grid, s);
+    return fq == 2 ? gv_launch_k<MF, 2>(a, kind, hs, nw, grid, s)
+                   : gv_launch_k<MF, 1>(a, kind, hs, nw, grid, s);
   }
-  return gv_launch_k<M, false>(a, kind, hs, nw, grid, s);
+  return gv_launch_k<M, 0>(a, kind, hs, nw, grid, s);
 }
 
 int kq4_gemv_slab_bytes(int n_batch) { return n_batch * KQ4_GV_QTS + KQ4_GV_XS; }
@@ -407,7 +427,8 @@ int kq4_launch_gemv(const KQ4GemvArgs &a, int n_batch, int kind, int half_sets, 
     return (int)hipErrorInvalidValue;
   for (int i = 0; i < a.nmat; ++i)
     if ((uintptr_t)a.mat[i].w % 16) return (int)hipErrorInvalidValue;
-  const bool fq = a.xf != nullptr;
+  if (a.xu && !a.xf) return (int)hipErrorInvalidValue;
+  const int fq = a.xf ? (a.xu ? 2 : 1) : 0;
   const int hs = half_sets;
   hipError_t e;
   switch (n_batch) {

@@ -26,6 +26,7 @@ struct KQ4GemvArgs {
   KQ4GemvMat mat[KQ4_MAXMAT];
   int nmat;
   const float *xf;      // fp32 activations [M][cols] when the kernel quantizes them itself
+  const float *xu;      // with xf: the dense FFN's up output; the activation is silu_mul(xf, xu)
   const int8_t *xq;     // [M][cols] (pre-quantized path)
   const float *xd;      // [M][nb] activation scales (pre-quantized path)
   int asm_tokens;       // tokens [0, asm_tokens) multiply by f32(f16_rne(xd)) (ASM chain)
@@ -33,8 +34,12 @@ struct KQ4GemvArgs {
   int nb;
 };
 
+// up != nullptr: quantizes silu_mul(x, up) instead of x (the dense FFN's down input).
 int kq4_launch_quantize(const float *x, int8_t *xq, float *xd, float *xde, int n_batch, int cols,
-                        int asm_tokens, hipStream_t stream, int block_major = 0);
+                        int asm_tokens, hipStream_t stream, int block_major = 0,
+                        const float *up = nullptr);
+// g[i] = silu_mul(g[i], u[i]) in place, the reference worker's element rule (g, u 16-B aligned).
+int kq4_launch_silu_mul(float *g, const float *u, long n, hipStream_t stream);
 
 // n_batch in [1, KQ4_GEMV_MAX_M]; one workgroup per 32-row set, or per 16-row half set when
 // half_sets = 1 (total_wg over all matrices, each matrix's wg_begin counted in those units),

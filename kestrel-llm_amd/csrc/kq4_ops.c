@@ -44,6 +44,22 @@ int kq4_dyn_matvec_q4_q8_fused_down_residual(float *x, const float *residual,
                       key_of(q4_down));
 }
 
+int kq4_silu_mul_down_residual(float *x, const float *residual, const uint8_t *q4_down,
+                               const float *gate, const float *up, int hidden_dim, int ffn_dim) {
+    /* the dense decode path follows the worker with the batched down wrapper at n_batch = 1
+     * (:16761), whose dispatch gives the C-tile chain */
+    return kq4_matmul_silu(x, gate, up, residual, q4_down, hidden_dim, ffn_dim, 1,
+                           KQ4_CHAIN_AUTO, key_of(q4_down));
+}
+
+int kq4_silu_mul_down_residual_batched(float *x_batch, const float *residual_batch,
+                                       const uint8_t *q4_down, const float *gate_batch,
+                                       const float *up_batch, int hidden_dim, int ffn_dim,
+                                       int n_batch) {
+    return kq4_matmul_silu(x_batch, gate_batch, up_batch, residual_batch, q4_down, hidden_dim,
+                           ffn_dim, n_batch, KQ4_CHAIN_AUTO, key_of(q4_down));
+}
+
 int kq4_dyn_matvec_q4_q8_fused_qkv_batched(float *q_out, float *k_out, float *v_out,
                                            const uint8_t *q4_q, const uint8_t *q4_k,
                                            const uint8_t *q4_v, const float *x_batch, int q_rows,

@@ -31,12 +31,15 @@ SIGNATURES = [
     ("kq4_weights_clear", _I, []),
     ("kq4_matmul", _I, [_P, _P, _P, _P, _I, _I, _I, _I, _U64]),
     ("kq4_matmul_multi", _I, [_I, _P, _P, _P, _P, _I, _P, _I, _I, _P]),
+    ("kq4_matmul_silu", _I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _U64]),
     ("kq4_moe_ffn", _I, [_P, _P, _P, _P, _I, _I, _P, _P, _P, _I, _I, _I, _U64]),
     ("kq4_weights_stream_bytes", ctypes.c_size_t, [_I, _I]),
     ("kq4_weights_prepare_dev", _I, [_P, _P, _I, _I, _P]),
     ("kq4_quantize_dev", _I, [_P, _P, _P, _P, _I, _I, _I, _P]),
     ("kq4_matmul_dev", _I, [_P, _P, _P, _P, _I, _I, _I, _I, _P]),
     ("kq4_matmul_multi_dev", _I, [_I, _P, _P, _P, _P, _I, _P, _I, _I, _P]),
+    ("kq4_matmul_silu_dev", _I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _P]),
+    ("kq4_silu_mul_dev", _I, [_P, _P, ctypes.c_long, _P]),
     ("kq4_matmul_q_dev", _I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _P]),
     ("kq4_matmul_multi_q_dev", _I, [_I, _P, _P, _P, _P, _I, _P, _P, _I, _I, _P]),
     ("kq4_block_sums_dev", _I, [_P, _P, _P, _P, _I, _I, _I, _P]),
@@ -50,6 +53,8 @@ SIGNATURES = [
     ("kq4_dyn_matvec_q4_q8_fused_qkv", _I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I]),
     ("kq4_dyn_matvec_q4_q8_fused_o_residual", _I, [_P, _P, _P, _P, _I, _I]),
     ("kq4_dyn_matvec_q4_q8_fused_down_residual", _I, [_P, _P, _P, _P, _I, _I]),
+    ("kq4_silu_mul_down_residual", _I, [_P, _P, _P, _P, _P, _I, _I]),
+    ("kq4_silu_mul_down_residual_batched", _I, [_P, _P, _P, _P, _P, _I, _I, _I]),
     ("kq4_dyn_matvec_q4_q8_fused_qkv_batched", _I,
      [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _P]),
     ("kq4_dyn_matvec_q4_q8_fused_o_residual_batched", _I, [_P, _P, _P, _P, _I, _I, _I, _P]),
@@ -142,6 +147,18 @@ def matmul(w, x, rows, cols, residual=None, chain=CHAIN_AUTO, wkey=0):
     return out
 
 
+def matmul_silu(w, gate, up, rows, cols, residual=None, chain=CHAIN_AUTO, wkey=0):
+    """out = [residual +] W.silu_mul(gate, up) through kq4_matmul_silu (host pointers)."""
+    gate = _c(gate, np.float32).reshape(-1, cols)
+    up = _c(up, np.float32).reshape(gate.shape)
+    out = np.empty((gate.shape[0], rows), np.float32)
+    res = None if residual is None else _c(residual, np.float32).reshape(gate.shape[0], rows)
+    check_done(lib().kq4_matmul_silu(_np_ptr(out), _np_ptr(gate), _np_ptr(up), _np_ptr(res),
+                                     _np_ptr(_c(w, np.uint8)), rows, cols, gate.shape[0], chain,
+                                     wkey), "kq4_matmul_silu")
+    return out
+
+
 def matmul_multi(ws, rows, x, cols, residuals=None, chain=CHAIN_AUTO, wkeys=None):
     x = _c(x, np.float32).reshape(-1, cols)
     n = x.shape[0]
@@ -211,6 +228,19 @@ def matmul_dev(out, x, w, rows, cols, residual=None, chain=CHAIN_AUTO, stream=No
     n = x.shape[0]
     check(lib().kq4_matmul_dev(_tp(out), _tp(x), _tp(residual), _tp(w), rows, cols, n, chain,
                                _stream_ptr(stream)), "kq4_matmul_dev")
+
+
+def matmul_silu_dev(out, gate, up, w, rows, cols, residual=None, chain=CHAIN_AUTO, stream=None):
+    n = gate.shape[0]
+    check(lib().kq4_matmul_silu_dev(_tp(out), _tp(gate), _tp(up), _tp(residual), _tp(w), rows,
+                                    cols, n, chain, _stream_ptr(stream)), "kq4_matmul_silu_dev")
+
+
+def silu_mul_dev(gate, up, stream=None):
+    """gate <- silu_mul(gate, up) in place (the reference worker's element rule)."""
+    assert gate.numel() == up.numel()
+    check(lib().kq4_silu_mul_dev(_tp(gate), _tp(up), gate.numel(), _stream_ptr(stream)),
+          "kq4_silu_mul_dev")
 
 
 def matmul_multi_dev(outs, x, ws, rows, cols, residuals=None, chain=CHAIN_AUTO, stream=None):

@@ -316,6 +316,98 @@ int kqo_matmul(float *out, const float *x, const float *residual, const uint8_t 
     return rc;
 }
 
+/* ---------------------------------------------------------------- dense SiLU * up */
+
+static float f32_from_bits(uint32_t b) { float f; memcpy(&f, &b, 4); return f; }
+static uint32_t f32_bits(float f) { uint32_t b; memcpy(&b, &f, 4); return b; }
+
+/* exp_neon4 (vllm_safetensors.c:4041-4068), one lane: clamp to [-87, 87]; n = vrndnq(x*log2e)
+ * (round to nearest even); r = vfmsq(x, n, ln2) = x - n*ln2 fused; p = Horner over the Taylor
+ * coefficients 1/6!, 1/5!, .., 1/2, 1, 1 with vfmaq(c, p, r) = c + p*r fused; result bits =
+ * bits(p) + (int(n) << 23). Pinned: exp(0) = 1 exactly, relative error against libm exp below
+ * 2.5e-7 over [-87, 87] (a dropped or mis-ordered coefficient is far outside it), and an
+ * independent float64 emulation of the instruction sequence (tests/test_oracle_silu.py). */
+float kqo_exp_neon(float x) {
+    x = fmaxf(x, -87.0f);
+    x = fminf(x, 87.0f);
+    float n = rintf(x * 1.4426950408889634f);
+    float r = fmaf(-n, 0.6931471805599453f, x);
+    float p = 0.001388888888888889f;
+    p = fmaf(p, r, 0.008333333333333333f);
+    p = fmaf(p, r, 0.041666666666666664f);
+    p = fmaf(p, r, 0.16666666666666666f);
+    p = fmaf(p, r, 0.5f);
+    p = fmaf(p, r, 1.0f);
+    p = fmaf(p, r, 1.0f);
+    return f32_from_bits(f32_bits(p) + ((uint32_t)(int32_t)n << 23));
+}
+
+/* vrecpeq_f32 / FRECPE, single precision, as the ARMv8 Architecture Reference Manual's
+ * FPRecipEstimate and RecipEstimate pseudocode define it (no FEAT_RPRES; the RK3588's
+ * Cortex-A76/A55 have none), for positive normal inputs below 2^126 - the range of the SiLU
+ * denominator 1 + exp_neon4(-g), which lies in [1, 6.1e37]: scaled = 256 + the top 8 fraction
+ * bits; a = 2*scaled + 1; b = 2^19 DIV a; r = (b + 1) DIV 2; result = 2^(253 - e - 127) *
+ * (1 + (r - 256)/256). Pinned: FRECPE(1.0) = 0.998046875 (the documented value), every
+ * estimate within 2^-8 relative of 1/x, monotone in x, exponent symmetry. Returns NaN outside
+ * the domain. */
+float kqo_frecpe(float x) {
+    uint32_t b = f32_bits(x);
+    uint32_t e = (b >> 23) & 0xFFu;
+    if ((b >> 31) || e == 0 || e >= 253) return NAN;
+    int a = 2 * (256 + (int)((b >> 15) & 0xFFu)) + 1;
+    int q = (1 << 19) / a;
+    uint32_t r = (uint32_t)((q + 1) / 2);
+    return f32_from_bits(((253u - e) << 23) | ((r & 0xFFu) << 15));
+}
+
+/* One element of vllm_silu_mul_worker's NEON loop (vllm_safetensors.c:10941-10950):
+ * ex = exp_neon4(-g); den = ex + 1; rec = FRECPE(den); twice rec = rec * FRECPS(den, rec) with
+ * FRECPS(d, r) = 2 - d*r fused (FPRecipStepFused); out = fl(fl(g * rec) * u). */
+float kqo_silu_mul_neon(float g, float u) {
+    float den = kqo_exp_neon(-g) + 1.0f;
+    float rec = kqo_frecpe(den);
+    rec = rec * fmaf(-den, rec, 2.0f);
+    rec = rec * fmaf(-den, rec, 2.0f);
+    return (g * rec) * u;
+}
+
+/* fast_silu (vllm_safetensors.c:3685-3696), the worker's scalar tail and its non-NEON body. */
+float kqo_fast_silu(float x) {
+    if (x <= 0.0f) {
+        if (x < -20.0f) return 0.0f;
+        float ex = expf(x);
+        return x * ex / (1.0f + ex);
+    }
+    if (x > 20.0f) return x;
+    return x / (1.0f + expf(-x));
+}
+
+/* vllm_silu_mul_worker over a flat array of n elements, in place, as the parfor of 16-element
+ * tasks covers it (:10932-10958, callers :16735, :17233): within every task the first
+ * (count & ~3) elements take the NEON form, the rest fast_silu(g) * u. Since tasks start at
+ * multiples of 16, that is: element i < (n & ~3) NEON, the last n % 4 elements scalar. */
+void kqo_silu_mul_rows(float *g, const float *u, long n) {
+    long nv = n & ~3L;
+    for (long i = 0; i < nv; i++) g[i] = kqo_silu_mul_neon(g[i], u[i]);
+    for (long i = nv; i < n; i++) g[i] = kqo_fast_silu(g[i]) * u[i];
+}
+
+/* The dense FFN's second half: av = silu_mul(gate, up) over [n_batch][cols], then
+ * out = [residual +] down . av with the chain `chain` (dyn_matvec_q4_q8_fused_down_residual*
+ * :8663, :8762 after vllm_silu_mul_worker; dense decode :16756-16767). */
+int kqo_matmul_silu(float *out, const float *gate, const float *up, const float *residual,
+                    const uint8_t *w, int rows, int cols, int n_batch, int chain) {
+    if (rows <= 0 || rows % 4 || cols <= 0 || cols % 32 || n_batch < 0) return -1;
+    size_t n = (size_t)n_batch * cols;
+    float *av = (float *)malloc((n + 1) * sizeof(float));
+    if (!av) return -1;
+    memcpy(av, gate, n * sizeof(float));
+    kqo_silu_mul_rows(av, up, (long)n);
+    int rc = kqo_matmul(out, av, residual, w, rows, cols, n_batch, chain);
+    free(av);
+    return rc;
+}
+
 void kqo_matmul_f64(double *out, const int8_t *xq, const float *xd, const uint8_t *w, int rows,
                     int cols, int n_batch) {
     int nb = cols / 32;

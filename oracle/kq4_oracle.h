@@ -62,6 +62,16 @@ int kqo_matmul_q_sample(float *out, const int8_t *xq, const float *xd, const flo
                         const uint8_t *w, int rows, int cols, int n_batch, int chain,
                         const int *tok, const int *row, int n_sample);
 
+/* ---- dense SiLU * up (AArch64 NEON form of vllm_silu_mul_worker) ---- */
+float kqo_exp_neon(float x);
+float kqo_frecpe(float x);                     /* positive normal x < 2^126, else NaN */
+float kqo_silu_mul_neon(float g, float u);
+float kqo_fast_silu(float x);
+void kqo_silu_mul_rows(float *g, const float *u, long n);   /* in place, n elements */
+/* out = [residual +] W . silu_mul(gate, up), both [n_batch][cols]. */
+int kqo_matmul_silu(float *out, const float *gate, const float *up, const float *residual,
+                    const uint8_t *w, int rows, int cols, int n_batch, int chain);
+
 /* float64 brute-force sum_b wd*xd*S (error-budget reference, not a chain). */
 void kqo_matmul_f64(double *out, const int8_t *xq, const float *xd, const uint8_t *w,
                     int rows, int cols, int n_batch);

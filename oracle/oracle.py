@@ -35,6 +35,12 @@ _ORACLE_SIGS = [
     ("kqo_moe_route", None, [_P, _I, _I, _P, _P]),
     ("kqo_router_logits", None, [_P, _P, _I, _I, _P]),
     ("kqo_silu_mul", ctypes.c_float, [ctypes.c_float, ctypes.c_float]),
+    ("kqo_exp_neon", ctypes.c_float, [ctypes.c_float]),
+    ("kqo_frecpe", ctypes.c_float, [ctypes.c_float]),
+    ("kqo_silu_mul_neon", ctypes.c_float, [ctypes.c_float, ctypes.c_float]),
+    ("kqo_fast_silu", ctypes.c_float, [ctypes.c_float]),
+    ("kqo_silu_mul_rows", None, [_P, _P, ctypes.c_long]),
+    ("kqo_matmul_silu", _I, [_P, _P, _P, _P, _P, _I, _I, _I, _I]),
     ("kqo_moe_ffn", _I, [_P, _P, _P, _P, _I, _I, _P, _P, _P, _I, _I, _I,
                          _P, _P, _P, _P, _P, _P, _P]),
 ]
@@ -53,6 +59,7 @@ _REF_SIGS = [
     ("kref_o_residual_batched", None, [_P, _P, _P, _P, _I, _I, _I]),
     ("kref_down_residual_batched", None, [_P, _P, _P, _P, _I, _I, _I]),
     ("kref_matvec", None, [_P, _P, _P, _I, _I]),
+    ("kref_silu_mul", None, [_P, _P, _I]),
 ]
 
 _oracle = None
@@ -152,6 +159,27 @@ def matmul_q_sample(w, xq, xd, rows, cols, n_batch, tok, row, residual=None, cha
     rc = lib().kqo_matmul_q_sample(_p(out), _p(_c(xq, np.int8)), _p(_c(xd, np.float32)), _p(res),
                                    _p(_c(w, np.uint8)), rows, cols, n_batch, chain, _p(tok),
                                    _p(row), tok.shape[0])
+    assert rc == 0
+    return out
+
+
+def silu_mul(g, u):
+    """vllm_silu_mul_worker over the flattened arrays (NEON form; last n % 4 scalar)."""
+    g = _c(g, np.float32).copy()
+    u = _c(u, np.float32)
+    assert g.size == u.size
+    lib().kqo_silu_mul_rows(_p(g), _p(u), g.size)
+    return g
+
+
+def matmul_silu(w, gate, up, rows, cols, residual=None, chain=CHAIN_AUTO):
+    gate = _c(gate, np.float32).reshape(-1, cols)
+    up = _c(up, np.float32).reshape(-1, cols)
+    n = gate.shape[0]
+    out = np.empty((n, rows), np.float32)
+    res = None if residual is None else _c(residual, np.float32)
+    rc = lib().kqo_matmul_silu(_p(out), _p(gate), _p(up), _p(res), _p(_c(w, np.uint8)), rows,
+                               cols, n, chain)
     assert rc == 0
     return out
 

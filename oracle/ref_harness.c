@@ -88,3 +88,11 @@ void kref_down_residual_batched(float *x, const float *res, const uint8_t *wd, c
 void kref_matvec(float *out, const uint8_t *w, const float *x, int rows, int cols) {
     dyn_matvec_q4_q8(out, w, x, rows, cols);
 }
+
+/* The reference's SiLU-multiply over n elements in place, run as its callers run it
+ * (vllm_tp_parfor over 16-element tasks, :16735 / :17233). On x86-64 the worker takes its
+ * non-NEON body, fast_silu(g) * u with this host's expf (:10955-10957). */
+void kref_silu_mul(float *g, const float *u, int n) {
+    vllm_silu_mul_ctx c = {g, (float *)u, n};
+    vllm_tp_parfor(0, (n + 15) / 16, vllm_silu_mul_worker, &c);
+}
