@@ -267,6 +267,17 @@ def run_extras():
             kq4.silu_mul_dev(xs, xu, stream=st)
             kq4.matmul_dev(od, xs, D[i], h, f, stream=st)
         t_su = _time_graph(torch, unfused, len(D))
+        # the attention block's input: RMSNorm + quantize in one pass feeding the QKV GEMV, and
+        # the same as an RMSNorm launch followed by the QKV op
+        nw = torch.rand(h, device="cuda") + 0.5
+        xn = torch.empty_like(x)
+        t_nq = _time_graph(torch, lambda i, st: kq4.rmsnorm_matmul_multi_dev(
+            [oq], x, nw, 1e-6, [Q[i]], [qkv], h, stream=st), len(Q))
+
+        def norm_then_qkv(i, st):
+            kq4.rms_norm_dev(xn, x, nw, 1e-6, stream=st)
+            kq4.matmul_dev(oq, xn, Q[i], qkv, h, stream=st)
+        t_nu = _time_graph(torch, norm_then_qkv, len(Q))
         b_gu = 2 * f * h * 18 // 32 + m * h * 4 + 2 * m * f * 4
         b_dn = h * f * 18 // 32 + m * f * 4 + m * h * 4
         b_q = qkv * h * 18 // 32 + m * h * 4 + m * qkv * 4
@@ -276,7 +287,8 @@ def run_extras():
             "qkv_us": round(t_q, 2), "qkv_GBs": round(b_q / t_q / 1e3, 1),
             "silu_down_us": round(t_sd, 2),
             "silu_down_GBs": round((b_dn + m * f * 4) / t_sd / 1e3, 1),
-            "silu_then_down_us": round(t_su, 2)}
+            "silu_then_down_us": round(t_su, 2),
+            "rmsnorm_qkv_us": round(t_nq, 2), "rmsnorm_then_qkv_us": round(t_nu, 2)}
     out["qwen3_8b_decode"] = dec
     pre = {}
     for m in (512, 2048):

@@ -57,6 +57,14 @@ extern "C" {
 #define KQ4_CHAIN_GEMV32 2  /* q4x4_dot1_group16_gemv (M4f), :4229-4251 */
 #define KQ4_CHAIN_ASM 3     /* llama 4x4 asm GEMM, f16-rounded activation scale, :4328-4368 */
 
+/* Summation order of an RMSNorm's sum of squares (both are the reference's, one binary32
+ * rounding per step): CHUNKED = dyn_rms_norm (vllm_safetensors.c:8811-8827, decode; also the
+ * batch worker under VLLM_SPEC_VNORM=1): 8-element chunks, each reduced as
+ * ((q0+q4)+(q1+q5))+((q2+q6)+(q3+q7)), summed in order; SERIAL = dyn_rms_norm_batch's default
+ * worker (:8849-8867, prefill): the squares summed in order. */
+#define KQ4_RMS_CHUNKED 0
+#define KQ4_RMS_SERIAL 1
+
 /* Most weight matrices one fused call may take (QKV = 3, gate/up = 2). */
 #define KQ4_MAX_MATS 4
 
@@ -145,6 +153,24 @@ int kq4_matmul_dev(float *out, const float *x, const float *residual, const uint
 int kq4_matmul_silu_dev(float *out, const float *gate, const float *up, const float *residual,
                         const uint8_t *w, int rows, int cols, int n_batch, int chain,
                         void *stream);
+
+/* RMSNorm of n_batch rows of d floats, bit for bit the reference's: out = fl(fl(x*rms)*w),
+ * rms = 1/sqrtf(ss/d + eps) with ss in `order` (KQ4_RMS_*). Replaces dyn_rms_norm (:8811) and
+ * dyn_rms_norm_batch (:8869). d % 8 == 0, d <= 16384; out, x, w 16-byte aligned; out may be
+ * x. */
+int kq4_rms_norm_dev(float *out, const float *x, const float *w, int n_batch, int d, float eps,
+                     int order, void *stream);
+
+/* RMSNorm and the matmuls it feeds in one call: the layer input x [n_batch][cols] is normalised
+ * (norm_w [cols], eps, order as kq4_rms_norm_dev) and quantized in the same pass, then
+ * out[i] = [residual[i] +] W[i].normed as kq4_matmul_multi_dev. It replaces the reference's
+ * dyn_rms_norm / dyn_rms_norm_batch followed by the QKV or gate/up wrapper (decode
+ * :16413-16436 and :16705-16753; prefill :17096-17120 and :17191-17224). normed (may be NULL,
+ * 16-byte aligned) receives the fp32 normalised input. */
+int kq4_rmsnorm_matmul_multi_dev(int n_mats, float *const *out, const float *const *residual,
+                                 const uint8_t *const *w, const int *rows, int cols,
+                                 const float *x, const float *norm_w, float eps, int order,
+                                 float *normed, int n_batch, int chain, void *stream);
 
 /* vllm_silu_mul_worker over n elements in place (vllm_safetensors.c:10932-10958):
  * gate[i] = silu_mul(gate[i], up[i]) in the NEON form for i < (n & ~3), bit for bit; the last

@@ -459,6 +459,54 @@ int kq4_matmul_silu_dev(float *out, const float *gate, const float *up, const fl
                      (hipStream_t)stream, up);
 }
 
+int kq4_rms_norm_dev(float *out, const float *x, const float *w, int n_batch, int d, float eps,
+                     int order, void *stream) {
+  if (n_batch < 0 || d <= 0 || d % 8 || d > 16384 ||
+      (order != KQ4_RMS_CHUNKED && order != KQ4_RMS_SERIAL) || (n_batch && (!out || !x || !w)))
+    return fail(KQ4_EINVAL, "rms_norm: n_batch=%d d=%d order=%d (d %% 8 == 0, d <= 16384)",
+                n_batch, d, order);
+  if ((uintptr_t)out % 16 || (uintptr_t)x % 16 || (uintptr_t)w % 16)
+    return fail(KQ4_EINVAL, "rms_norm: out, x and w must be 16-byte aligned");
+  DevState *ds = nullptr;
+  int rc = cur_dev(&ds);
+  if (rc) return rc;
+  KQ4_HIP((hipError_t)kq4_launch_rms_norm(x, w, out, nullptr, nullptr, n_batch, d, eps,
+                                          order == KQ4_RMS_SERIAL, (hipStream_t)stream));
+  return KQ4_OK;
+}
+
+int kq4_rmsnorm_matmul_multi_dev(int n_mats, float *const *out, const float *const *residual,
+                                 const uint8_t *const *w, const int *rows, int cols,
+                                 const float *x, const float *norm_w, float eps, int order,
+                                 float *normed, int n_batch, int chain, void *stream) {
+  if (n_batch < 0 || cols > 16384 || (order != KQ4_RMS_CHUNKED && order != KQ4_RMS_SERIAL) ||
+      (n_batch && (!x || !norm_w)))
+    return fail(KQ4_EINVAL, "rmsnorm_matmul: n_batch=%d cols=%d order=%d", n_batch, cols, order);
+  if (!out || !w || !rows) return fail(KQ4_EINVAL, "null array argument");
+  if ((uintptr_t)x % 16 || (uintptr_t)norm_w % 16 || (uintptr_t)normed % 16)
+    return fail(KQ4_EINVAL, "rmsnorm_matmul: x, norm_w and normed must be 16-byte aligned");
+  if (n_mats < 1 || n_mats > KQ4_MAX_MATS) return fail(KQ4_EINVAL, "n_mats=%d", n_mats);
+  for (int i = 0; i < n_mats; ++i)
+    if (!shape_ok(rows[i], cols))
+      return fail(KQ4_EINVAL, "rows=%d cols=%d: need rows%%4==0, cols%%32==0", rows[i], cols);
+  if (n_batch == 0) return KQ4_OK;
+  DevState *ds = nullptr;
+  int rc = cur_dev(&ds);
+  if (rc) return rc;
+  // the normalised activations are quantized where they are formed; the matmul then reads the
+  // codes (the same workspace carve matmul_impl makes for its own quantization, so it stays)
+  const int nb = cols / 32;
+  const size_t qbytes = al256((size_t)n_batch * cols) + al256((size_t)n_batch * nb * sizeof(float));
+  if ((rc = ensure(ds->ws, qbytes))) return rc;
+  Carve cv{static_cast<char *>(ds->ws.p)};
+  int8_t *q = cv.take<int8_t>((size_t)n_batch * cols);
+  float *dq = cv.take<float>((size_t)n_batch * nb);
+  hipStream_t s = (hipStream_t)stream;
+  KQ4_HIP((hipError_t)kq4_launch_rms_norm(x, norm_w, normed, q, dq, n_batch, cols, eps,
+                                          order == KQ4_RMS_SERIAL, s));
+  return matmul_impl(n_mats, out, residual, w, rows, cols, nullptr, q, dq, n_batch, chain, s);
+}
+
 int kq4_silu_mul_dev(float *gate, const float *up, long n, void *stream) {
   if (n < 0 || (n && (!gate || !up))) return fail(KQ4_EINVAL, "silu_mul: n=%ld", n);
   if ((uintptr_t)gate % 16 || (uintptr_t)up % 16)

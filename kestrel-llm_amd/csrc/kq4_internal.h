@@ -40,6 +40,12 @@ int kq4_launch_quantize(const float *x, int8_t *xq, float *xd, float *xde, int n
                         const float *up = nullptr);
 // g[i] = silu_mul(g[i], u[i]) in place, the reference worker's element rule (g, u 16-B aligned).
 int kq4_launch_silu_mul(float *g, const float *u, long n, hipStream_t stream);
+// RMSNorm of n_batch rows of d (d % 8 == 0, d <= 16384; 16-B aligned rows), serial = 0 the chunked order of
+// dyn_rms_norm, 1 the serial order of dyn_rms_norm_batch; out (may be null) the fp32 result,
+// xq/xd (may be null; d % 32 == 0) its int8 quantization, token-major. LDS: kq4_rms_norm_lds.
+size_t kq4_rms_norm_lds(int d, int serial);
+int kq4_launch_rms_norm(const float *x, const float *w, float *out, int8_t *xq, float *xd,
+                        int n_batch, int d, float eps, int serial, hipStream_t stream);
 
 // n_batch in [1, KQ4_GEMV_MAX_M]; one workgroup per 32-row set, or per 16-row half set when
 // half_sets = 1 (total_wg over all matrices, each matrix's wg_begin counted in those units),

@@ -106,3 +106,155 @@ int kq4_launch_silu_mul(float *g, const float *u, long n, hipStream_t stream) {
   hipLaunchKernelGGL(kq4_silu_mul_kernel, dim3((unsigned)grid), dim3(256), 0, stream, g, u, n);
   return (int)hipGetLastError();
 }
+
+// ---- RMSNorm, optionally quantized in the same pass -------------------------------------------
+// dyn_rms_norm (vllm_safetensors.c:8811-8827) and dyn_rms_norm_batch's worker (:8849-8867), one
+// workgroup per token: out = fl(fl(x * rms) * w), rms = fl(1 / fl(sqrt(fl(fl(ss / d) + eps)))).
+// The sum of squares ss is the reference's serial chain, in one of its two orders:
+//   chunked (dyn_rms_norm; the batch worker under VLLM_SPEC_VNORM=1): the workgroup's threads
+//     form every 8-element chunk's hsum8 of squares, ((q0+q4)+(q1+q5)) + ((q2+q6)+(q3+q7)), into
+//     LDS, then one lane adds the d/8 chunk sums in order;
+//   serial (dyn_rms_norm_batch's default): the threads square every element into LDS, one lane
+//     adds the d squares in order.
+// Thread i holds chunks i, i+256, .. (CPT of them) of x and w in registers from the start, so the
+// only global-memory wait is the first. Then each thread normalises its chunks and, when xq is
+// given, quantizes them as kq4_quantize_kernel does (a lane quad per 32-block,
+// quantize_row_q8_0_act :7893-7920).
+// d % 8 == 0 (d % 32 == 0 to quantize), d <= 2048 * CPT; rows 16-byte aligned. out may be x (in
+// place, as the reference calls it at :19607): all of x is read before anything is written.
+#define KQ4_RMS_THREADS 256
+#define KQ4_RMS_BATCH 64   // terms the serial lane reads from LDS at once
+
+template <int CPT>
+__global__ __launch_bounds__(KQ4_RMS_THREADS) void kq4_rms_norm_kernel(
+    const float *x, const float *__restrict__ w, float *out, int8_t *__restrict__ xq,
+    float *__restrict__ xd, int d, float eps, int serial) {
+  extern __shared__ __align__(16) float kq4_rms_lds[];   // d/8 chunk sums, or d squares
+  __shared__ float rms_s;
+  const int t = blockIdx.x;
+  const float *xr = x + (size_t)t * d;
+  const int nc = d >> 3;
+  float v[CPT][8], wv[CPT][8];
+#pragma unroll
+  for (int j = 0; j < CPT; ++j) {
+    const int c = threadIdx.x + KQ4_RMS_THREADS * j;
+    float4 a = make_float4(0, 0, 0, 0), b = a, wa = a, wb = a;
+    if (c < nc) {
+      a = *reinterpret_cast<const float4 *>(xr + 8 * c);
+      b = *reinterpret_cast<const float4 *>(xr + 8 * c + 4);
+      wa = *reinterpret_cast<const float4 *>(w + 8 * c);
+      wb = *reinterpret_cast<const float4 *>(w + 8 * c + 4);
+    }
+    v[j][0] = a.x; v[j][1] = a.y; v[j][2] = a.z; v[j][3] = a.w;
+    v[j][4] = b.x; v[j][5] = b.y; v[j][6] = b.z; v[j][7] = b.w;
+    wv[j][0] = wa.x; wv[j][1] = wa.y; wv[j][2] = wa.z; wv[j][3] = wa.w;
+    wv[j][4] = wb.x; wv[j][5] = wb.y; wv[j][6] = wb.z; wv[j][7] = wb.w;
+  }
+#pragma unroll
+  for (int j = 0; j < CPT; ++j) {
+    const int c = threadIdx.x + KQ4_RMS_THREADS * j;
+    if (c < nc) {
+      float q[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) q[k] = v[j][k] * v[j][k];
+      if (serial) {
+        *reinterpret_cast<float4 *>(kq4_rms_lds + 8 * c) = make_float4(q[0], q[1], q[2], q[3]);
+        *reinterpret_cast<float4 *>(kq4_rms_lds + 8 * c + 4) = make_float4(q[4], q[5], q[6], q[7]);
+      } else {
+        kq4_rms_lds[c] = ((q[0] + q[4]) + (q[1] + q[5])) + ((q[2] + q[6]) + (q[3] + q[7]));
+      }
+    }
+  }
+  // zero padding to whole batches: adding +0 to the non-negative sum is exact
+  const int n = serial ? d : nc;
+  const int npad = (n + KQ4_RMS_BATCH - 1) & ~(KQ4_RMS_BATCH - 1);
+  for (int i = n + threadIdx.x; i < npad; i += KQ4_RMS_THREADS) kq4_rms_lds[i] = 0.0f;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    // one dependent add per term, KQ4_RMS_BATCH terms read at a time
+    float ss = 0.0f;
+    for (int i = 0; i < npad; i += KQ4_RMS_BATCH) {
+      float4 b[KQ4_RMS_BATCH / 4];
+#pragma unroll
+      for (int k = 0; k < KQ4_RMS_BATCH / 4; ++k)
+        b[k] = *reinterpret_cast<const float4 *>(kq4_rms_lds + i + 4 * k);
+#pragma unroll
+      for (int k = 0; k < KQ4_RMS_BATCH / 4; ++k) {
+        ss += b[k].x;
+        ss += b[k].y;
+        ss += b[k].z;
+        ss += b[k].w;
+      }
+    }
+    rms_s = 1.0f / sqrtf(ss / (float)d + eps);
+  }
+  __syncthreads();
+  const float rms = rms_s;
+  float *orow = out ? out + (size_t)t * d : nullptr;
+  const int nb = d >> 5;
+#pragma unroll
+  for (int j = 0; j < CPT; ++j) {
+    const int c = threadIdx.x + KQ4_RMS_THREADS * j;
+    const bool live = c < nc;
+    float o[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) o[k] = v[j][k] * rms * wv[j][k];
+    if (live && orow) {
+      *reinterpret_cast<float4 *>(orow + 8 * c) = make_float4(o[0], o[1], o[2], o[3]);
+      *reinterpret_cast<float4 *>(orow + 8 * c + 4) = make_float4(o[4], o[5], o[6], o[7]);
+    }
+    if (xq) {   // uniform; nc % 4 == 0 here, so a lane quad is live or dead as a whole
+      float a = 1e-10f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) a = fmaxf(a, fabsf(o[i]));
+      a = fmaxf(a, __shfl_xor(a, 1));
+      a = fmaxf(a, __shfl_xor(a, 2));
+      const float dq = a / 127.0f;
+      uint32_t pk[2] = {0, 0};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        int q = (int)(o[i] / dq + 0.5f);
+        q = q > 127 ? 127 : (q < -127 ? -127 : q);
+        pk[i >> 2] |= ((uint32_t)q & 0xFFu) << (8 * (i & 3));
+      }
+      if (live) {
+        *reinterpret_cast<uint2 *>(xq + (size_t)t * d + 8 * c) = make_uint2(pk[0], pk[1]);
+        if ((c & 3) == 0) xd[(size_t)t * nb + (c >> 2)] = dq;
+      }
+    }
+  }
+}
+
+size_t kq4_rms_norm_lds(int d, int serial) {
+  const int n = serial ? d : d / 8;
+  return (size_t)((n + KQ4_RMS_BATCH - 1) & ~(KQ4_RMS_BATCH - 1)) * sizeof(float);
+}
+
+template <int CPT>
+static hipError_t rms_launch(const float *x, const float *w, float *out, int8_t *xq, float *xd,
+                             int n_batch, int d, float eps, int serial, hipStream_t s) {
+  // the serial order keeps d squares in LDS (64 KB at d = 16384); the kernel's static LDS (the
+  // broadcast rms) comes off the 160 KB a workgroup may hold
+  static bool attr = false;
+  if (!attr) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&kq4_rms_norm_kernel<CPT>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       160 * 1024 - 1024);
+    if (e != hipSuccess) return e;
+    attr = true;
+  }
+  hipLaunchKernelGGL((kq4_rms_norm_kernel<CPT>), dim3(n_batch), dim3(KQ4_RMS_THREADS),
+                     kq4_rms_norm_lds(d, serial), s, x, w, out, xq, xd, d, eps, serial);
+  return hipGetLastError();
+}
+
+int kq4_launch_rms_norm(const float *x, const float *w, float *out, int8_t *xq, float *xd,
+                        int n_batch, int d, float eps, int serial, hipStream_t stream) {
+  if (n_batch <= 0) return 0;
+  const int cpt = (d / 8 + KQ4_RMS_THREADS - 1) / KQ4_RMS_THREADS;
+  if (d % 8 || cpt > 8 || (xq && d % 32)) return (int)hipErrorInvalidValue;
+  if (cpt <= 1) return (int)rms_launch<1>(x, w, out, xq, xd, n_batch, d, eps, serial, stream);
+  if (cpt <= 2) return (int)rms_launch<2>(x, w, out, xq, xd, n_batch, d, eps, serial, stream);
+  if (cpt <= 4) return (int)rms_launch<4>(x, w, out, xq, xd, n_batch, d, eps, serial, stream);
+  return (int)rms_launch<8>(x, w, out, xq, xd, n_batch, d, eps, serial, stream);
+}

@@ -40,6 +40,9 @@ SIGNATURES = [
     ("kq4_matmul_multi_dev", _I, [_I, _P, _P, _P, _P, _I, _P, _I, _I, _P]),
     ("kq4_matmul_silu_dev", _I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _P]),
     ("kq4_silu_mul_dev", _I, [_P, _P, ctypes.c_long, _P]),
+    ("kq4_rms_norm_dev", _I, [_P, _P, _P, _I, _I, ctypes.c_float, _I, _P]),
+    ("kq4_rmsnorm_matmul_multi_dev", _I, [_I, _P, _P, _P, _P, _I, _P, _P, ctypes.c_float, _I,
+                                          _P, _I, _I, _P]),
     ("kq4_matmul_q_dev", _I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _P]),
     ("kq4_matmul_multi_q_dev", _I, [_I, _P, _P, _P, _P, _I, _P, _P, _I, _I, _P]),
     ("kq4_block_sums_dev", _I, [_P, _P, _P, _P, _I, _I, _I, _P]),
@@ -234,6 +237,26 @@ def matmul_silu_dev(out, gate, up, w, rows, cols, residual=None, chain=CHAIN_AUT
     n = gate.shape[0]
     check(lib().kq4_matmul_silu_dev(_tp(out), _tp(gate), _tp(up), _tp(residual), _tp(w), rows,
                                     cols, n, chain, _stream_ptr(stream)), "kq4_matmul_silu_dev")
+
+
+RMS_CHUNKED, RMS_SERIAL = 0, 1
+
+
+def rms_norm_dev(out, x, w, eps, order=RMS_CHUNKED, stream=None):
+    n, d = x.shape
+    check(lib().kq4_rms_norm_dev(_tp(out), _tp(x), _tp(w), n, d, eps, order,
+                                 _stream_ptr(stream)), "kq4_rms_norm_dev")
+
+
+def rmsnorm_matmul_multi_dev(outs, x, norm_w, eps, ws, rows, cols, residuals=None,
+                             order=RMS_CHUNKED, normed=None, chain=CHAIN_AUTO, stream=None):
+    n = x.shape[0]
+    res = [None] * len(ws) if residuals is None else residuals
+    check(lib().kq4_rmsnorm_matmul_multi_dev(
+        len(ws), _ptr_array([_tp(o) for o in outs]), _ptr_array([_tp(r) for r in res]),
+        _ptr_array([_tp(w) for w in ws]), (ctypes.c_int * len(rows))(*rows), cols, _tp(x),
+        _tp(norm_w), eps, order, _tp(normed), n, chain, _stream_ptr(stream)),
+        "kq4_rmsnorm_matmul_multi_dev")
 
 
 def silu_mul_dev(gate, up, stream=None):

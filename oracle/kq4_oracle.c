@@ -408,6 +408,50 @@ int kqo_matmul_silu(float *out, const float *gate, const float *up, const float 
     return rc;
 }
 
+/* ---------------------------------------------------------------- RMSNorm */
+
+/* hsum8_f32 (vllm_safetensors.c:8803-8809): ((v0+v4) + (v1+v5)) + ((v2+v6) + (v3+v7)). */
+static float hsum8(const float *v) {
+    float lo[4];
+    for (int i = 0; i < 4; i++) lo[i] = v[i] + v[4 + i];
+    return (lo[0] + lo[1]) + (lo[2] + lo[3]);
+}
+
+/* Sum of squares of one row in the reference's two orders:
+ *   chunked (dyn_rms_norm :8811-8822, and the batch worker under VLLM_SPEC_VNORM=1 :8854-8861):
+ *     ss = serial sum over 8-element chunks of hsum8(x^2), then the d % 8 tail serially;
+ *   serial (the batch worker's default, :8862-8863): ss = serial sum of x[i]^2.
+ * Every square and every sum is one binary32 rounding (the reference builds with
+ * -ffp-contract=off). */
+static float rms_ss(const float *x, int d, int chunked) {
+    float ss = 0.0f;
+    int i = 0;
+    if (chunked) {
+        int d8 = d & ~7;
+        for (; i < d8; i += 8) {
+            float v[8];
+            for (int k = 0; k < 8; k++) v[k] = x[i + k] * x[i + k];
+            ss += hsum8(v);
+        }
+    }
+    for (; i < d; i++) ss += x[i] * x[i];
+    return ss;
+}
+
+/* out[t] = fl(fl(x[t][i] * rms) * w[i]), rms = fl(1 / fl(sqrt(fl(fl(ss / d) + eps)))), for
+ * n_batch rows of d: dyn_rms_norm (:8811-8827, chunked = 1) and dyn_rms_norm_batch's worker
+ * (:8849-8867, chunked = 0, or 1 under VLLM_SPEC_VNORM=1). Pinned bit for bit against both
+ * reference functions built in oracle/_ref, and by exact cases (tests/test_oracle_rmsnorm.py). */
+void kqo_rms_norm(float *out, const float *x, const float *w, int n_batch, int d, float eps,
+                  int chunked) {
+    for (int t = 0; t < n_batch; t++) {
+        const float *xr = x + (size_t)t * d;
+        float *orow = out + (size_t)t * d;
+        float rms = 1.0f / sqrtf(rms_ss(xr, d, chunked) / (float)d + eps);
+        for (int i = 0; i < d; i++) orow[i] = xr[i] * rms * w[i];
+    }
+}
+
 void kqo_matmul_f64(double *out, const int8_t *xq, const float *xd, const uint8_t *w, int rows,
                     int cols, int n_batch) {
     int nb = cols / 32;

@@ -72,6 +72,10 @@ void kqo_silu_mul_rows(float *g, const float *u, long n);   /* in place, n eleme
 int kqo_matmul_silu(float *out, const float *gate, const float *up, const float *residual,
                     const uint8_t *w, int rows, int cols, int n_batch, int chain);
 
+/* ---- RMSNorm (dyn_rms_norm chunked order / dyn_rms_norm_batch serial order) ---- */
+void kqo_rms_norm(float *out, const float *x, const float *w, int n_batch, int d, float eps,
+                  int chunked);
+
 /* float64 brute-force sum_b wd*xd*S (error-budget reference, not a chain). */
 void kqo_matmul_f64(double *out, const int8_t *xq, const float *xd, const uint8_t *w,
                     int rows, int cols, int n_batch);

@@ -41,6 +41,7 @@ _ORACLE_SIGS = [
     ("kqo_fast_silu", ctypes.c_float, [ctypes.c_float]),
     ("kqo_silu_mul_rows", None, [_P, _P, ctypes.c_long]),
     ("kqo_matmul_silu", _I, [_P, _P, _P, _P, _P, _I, _I, _I, _I]),
+    ("kqo_rms_norm", None, [_P, _P, _P, _I, _I, ctypes.c_float, _I]),
     ("kqo_moe_ffn", _I, [_P, _P, _P, _P, _I, _I, _P, _P, _P, _I, _I, _I,
                          _P, _P, _P, _P, _P, _P, _P]),
 ]
@@ -60,6 +61,8 @@ _REF_SIGS = [
     ("kref_down_residual_batched", None, [_P, _P, _P, _P, _I, _I, _I]),
     ("kref_matvec", None, [_P, _P, _P, _I, _I]),
     ("kref_silu_mul", None, [_P, _P, _I]),
+    ("kref_rms_norm", None, [_P, _P, _P, _I, ctypes.c_float]),
+    ("kref_rms_norm_batch", None, [_P, _P, _P, _I, _I, ctypes.c_float]),
 ]
 
 _oracle = None
@@ -181,6 +184,13 @@ def matmul_silu(w, gate, up, rows, cols, residual=None, chain=CHAIN_AUTO):
     rc = lib().kqo_matmul_silu(_p(out), _p(gate), _p(up), _p(res), _p(_c(w, np.uint8)), rows,
                                cols, n, chain)
     assert rc == 0
+    return out
+
+
+def rms_norm(x, w, d, eps, chunked=True):
+    x = _c(x, np.float32).reshape(-1, d)
+    out = np.empty_like(x)
+    lib().kqo_rms_norm(_p(out), _p(x), _p(_c(w, np.float32)), x.shape[0], d, eps, int(chunked))
     return out
 
 

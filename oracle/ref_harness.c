@@ -96,3 +96,13 @@ void kref_silu_mul(float *g, const float *u, int n) {
     vllm_silu_mul_ctx c = {g, (float *)u, n};
     vllm_tp_parfor(0, (n + 15) / 16, vllm_silu_mul_worker, &c);
 }
+
+/* The reference's RMSNorms: single-token dyn_rms_norm (chunked sum of squares, :8811-8827)
+ * and the batched dyn_rms_norm_batch (per-token worker, serial sum unless VLLM_SPEC_VNORM=1,
+ * :8849-8873). */
+void kref_rms_norm(float *out, const float *x, const float *w, int d, float eps) {
+    dyn_rms_norm(out, x, w, d, eps);
+}
+void kref_rms_norm_batch(float *out, const float *x, const float *w, int nb, int d, float eps) {
+    dyn_rms_norm_batch(out, x, w, nb, d, eps);
+}
