@@ -326,7 +326,15 @@ def run_extras():
             Y, X, sel, pr, *layers[i], ne, d, ef, stream=st), len(layers))
         n_exp = len(set(sel.cpu().numpy().reshape(-1).tolist()))
         byts = n_exp * 3 * ef * d * 18 // 32 + T * d * 8
-        moe[f"T{T}"] = {"us": round(t, 2), "experts": n_exp, "GBs": round(byts / t / 1e3, 1)}
+        # the whole layer on the device: fp32 router logits (serial chains), top-k, expert FFN
+        R = torch.randn((ne, d), device="cuda") * 0.02
+        lgr = torch.empty((T, ne), device="cuda")
+        t_lg = _time_graph(torch, lambda i, st: kq4.moe_router_logits_dev(lgr, R, X, stream=st),
+                           len(layers))
+        t_l = _time_graph(torch, lambda i, st: kq4.moe_layer_dev(
+            Y, X, R, *layers[i], ne, tk, d, ef, stream=st), len(layers))
+        moe[f"T{T}"] = {"us": round(t, 2), "experts": n_exp, "GBs": round(byts / t / 1e3, 1),
+                        "router_logits_us": round(t_lg, 2), "layer_us": round(t_l, 2)}
     out["qwen3_30b_a3b_moe"] = moe
     return out
 

@@ -206,6 +206,21 @@ int kq4_block_sums_dev(int32_t *s_lo, int32_t *s_hi, const int8_t *xq, const uin
 int kq4_moe_route_dev(int *sel, float *pr, const float *logits, int T, int ne, int tk,
                       void *stream);
 
+/* MoE router logits on the device: logits [T][ne] = router [ne][d] . X [T][d] in fp32, each
+ * (token, expert) the reference's serial chain s += rw[i] * x[i], i ascending
+ * (st_moe_ffn_sparse_q4 vllm_safetensors.c:12961-12966, batched :14937-14962), bit for bit.
+ * d % 32 == 0; router and X 16-byte aligned. */
+int kq4_moe_router_logits_dev(float *logits, const float *router, const float *X, int T, int ne,
+                              int d, void *stream);
+
+/* A whole MoE FFN layer on the device, as st_moe_ffn_sparse_q4 / _batch_arm run it
+ * (:12921-13398, :14894-15064): router logits, top-k + softmax (kq4_moe_route_dev), and the
+ * expert FFN (kq4_moe_ffn_dev). sel_out [T][tk] / pr_out [T][tk] receive the routing when not
+ * NULL. */
+int kq4_moe_layer_dev(float *Y, const float *X, const float *router, const uint8_t *G,
+                      const uint8_t *U, const uint8_t *D, int T, int ne, int tk, int d, int ef,
+                      int *sel_out, float *pr_out, void *stream);
+
 /* MoE FFN on device buffers (see kq4_moe_ffn); G and U prepared as [ne*ef rows][d cols], D as
  * [d rows][ne*ef cols]. */
 int kq4_moe_ffn_dev(float *Y, const float *X, const int *sel, const float *pr, int T, int tk,

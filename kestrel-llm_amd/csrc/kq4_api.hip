@@ -47,6 +47,7 @@ struct DevState {
   int ncu = 256;        // compute units (sizes the GEMV grid)
   Buf ws;    // quantized activations, MoE staging
   Buf hx, hu, hres, hout, hw, hsel, hpr, hstage;   // staging for the host-pointer API
+  Buf rt;    // MoE routing of the fused layer call: logits, sel, pr
   std::unordered_map<uint64_t, WEntry> wcache;
 };
 
@@ -556,6 +557,45 @@ int kq4_moe_route_dev(int *sel, float *pr, const float *logits, int T, int ne, i
   if (T == 0) return KQ4_OK;
   KQ4_HIP((hipError_t)kq4_launch_moe_route(sel, pr, logits, T, ne, tk, (hipStream_t)stream));
   return KQ4_OK;
+}
+
+int kq4_moe_router_logits_dev(float *logits, const float *router, const float *X, int T, int ne,
+                              int d, void *stream) {
+  if (T < 0 || ne < 1 || d <= 0 || d % 32 || (T && (!logits || !router || !X)))
+    return fail(KQ4_EINVAL, "router_logits: T=%d ne=%d d=%d (d %% 32 == 0)", T, ne, d);
+  if ((uintptr_t)router % 16 || (uintptr_t)X % 16)
+    return fail(KQ4_EINVAL, "router_logits: router and X must be 16-byte aligned");
+  DevState *ds = nullptr;
+  int rc = cur_dev(&ds);
+  if (rc) return rc;
+  KQ4_HIP((hipError_t)kq4_launch_moe_logits(logits, router, X, T, ne, d, (hipStream_t)stream));
+  return KQ4_OK;
+}
+
+int kq4_moe_layer_dev(float *Y, const float *X, const float *router, const uint8_t *G,
+                      const uint8_t *U, const uint8_t *D, int T, int ne, int tk, int d, int ef,
+                      int *sel_out, float *pr_out, void *stream) {
+  if (T < 0 || ne < 1 || ne > 2048 || tk < 1 || tk > 32 || tk > ne || d <= 0 || d % 32 ||
+      (T && (!Y || !X || !router)))
+    return fail(KQ4_EINVAL, "moe_layer: T=%d ne=%d tk=%d d=%d", T, ne, tk, d);
+  if ((uintptr_t)router % 16 || (uintptr_t)X % 16)
+    return fail(KQ4_EINVAL, "moe_layer: router and X must be 16-byte aligned");
+  if (T == 0) return KQ4_OK;
+  DevState *ds = nullptr;
+  int rc = cur_dev(&ds);
+  if (rc) return rc;
+  hipStream_t s = (hipStream_t)stream;
+  const size_t np = (size_t)T * tk;
+  if ((rc = ensure(ds->rt, al256((size_t)T * ne * sizeof(float)) + al256(np * sizeof(int)) +
+                               al256(np * sizeof(float)))))
+    return rc;
+  Carve cv{static_cast<char *>(ds->rt.p)};
+  float *lg = cv.take<float>((size_t)T * ne);
+  int *sel = sel_out ? sel_out : cv.take<int>(np);
+  float *pr = pr_out ? pr_out : cv.take<float>(np);
+  KQ4_HIP((hipError_t)kq4_launch_moe_logits(lg, router, X, T, ne, d, s));
+  KQ4_HIP((hipError_t)kq4_launch_moe_route(sel, pr, lg, T, ne, tk, s));
+  return moe_impl(Y, X, sel, pr, T, tk, G, U, D, ne, d, ef, nullptr, nullptr, nullptr, nullptr, s);
 }
 
 int kq4_moe_ffn_dev(float *Y, const float *X, const int *sel, const float *pr, int T, int tk,

@@ -73,6 +73,10 @@ int kq4_launch_gemm(float *out, const float *res, const uint8_t *w, const KQ4Gem
 // MoE
 int kq4_launch_moe_route(int *sel, float *pr, const float *logits, int T, int ne, int tk,
                          hipStream_t stream);
+// fp32 router logits [T][ne] = router [ne][d] . X [T][d], the reference's serial chain per
+// (token, expert); d % 32 == 0, rows 16-byte aligned.
+int kq4_launch_moe_logits(float *logits, const float *router, const float *X, int T, int ne,
+                          int d, hipStream_t stream);
 struct KQ4MoeWs {
   int *ex_off;   // [ne+1]
   int *ex_pair;  // [T*tk] (t*tk+j) grouped by expert

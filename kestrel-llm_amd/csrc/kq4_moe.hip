@@ -108,6 +108,101 @@ __global__ __launch_bounds__(256) void kq4_moe_route_kernel(int *__restrict__ se
   }
 }
 
+// ---- router logits ----------------------------------------------------------------------------
+// logits[t][e] = the reference's serial fp32 chain s = fl(s + fl(rw[e][i] * x[t][i])), i ascending
+// (st_moe_ffn_sparse_q4 :12961-12966; the batched router :14937-14962 keeps the same chain per
+// (token, expert)). A chain cannot be split without changing its roundings, so one lane runs one
+// (token, expert) chain and does nothing else: a workgroup takes one token and 16 experts; lanes
+// 0-15 of wave 0 add, waves 1-4 form the products. Per 512-column tile each producer thread
+// loads a 128-B segment of one row and the matching x (issued a tile ahead, so the loads are in
+// flight during a whole tile's 512 dependent adds, ~1.6 us), multiplies and stores the products
+// to LDS (double-buffered; row pitch 516 floats, so the adders' 16-B reads hit distinct banks);
+// each adder then adds its row's products in order.
+#define KQ4_RT_E 16        // experts (chains) per workgroup
+#define KQ4_RT_C 512       // columns per tile
+#define KQ4_RT_P 516       // LDS row pitch (floats)
+
+__global__ __launch_bounds__(320) void kq4_moe_logits_kernel(float *__restrict__ logits,
+                                                             const float *__restrict__ router,
+                                                             const float *__restrict__ X, int ne,
+                                                             int d) {
+  extern __shared__ __align__(16) float kq4_rt_lds[];   // [2][KQ4_RT_E][KQ4_RT_P]
+  const int t = blockIdx.y;
+  const int e0 = blockIdx.x * KQ4_RT_E;
+  const int wave = threadIdx.x >> 6;
+  const float *__restrict__ xt = X + (size_t)t * d;
+  const int ntile = (d + KQ4_RT_C - 1) / KQ4_RT_C;
+  // producer thread p: row p/16 of the tile, columns 32*(p%16) .. +32
+  const int p = threadIdx.x - 64;
+  const int pr = p >> 4, pc = 32 * (p & 15);
+  const bool prow = wave > 0 && e0 + pr < ne;
+  const float *__restrict__ rw = router + (size_t)(e0 + pr) * d;
+  float4 cur[8], xv[8];   // the next tile's weights and x, loaded a tile ahead
+  auto load = [&](int k) {
+    const int c = k * KQ4_RT_C + pc;
+    const bool live = prow && c < d;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      cur[j] = live ? *reinterpret_cast<const float4 *>(rw + c + 4 * j) : make_float4(0, 0, 0, 0);
+      xv[j] = live ? *reinterpret_cast<const float4 *>(xt + c + 4 * j) : make_float4(0, 0, 0, 0);
+    }
+  };
+  auto store = [&](int k) {
+    const int c = k * KQ4_RT_C + pc;
+    if (!(prow && c < d)) return;
+    float *dst = kq4_rt_lds + ((k & 1) * KQ4_RT_E + pr) * KQ4_RT_P + pc;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      *reinterpret_cast<float4 *>(dst + 4 * j) = make_float4(
+          cur[j].x * xv[j].x, cur[j].y * xv[j].y, cur[j].z * xv[j].z, cur[j].w * xv[j].w);
+  };
+  if (wave > 0) load(0);
+  float s = 0.0f;
+  const bool adder = wave == 0 && threadIdx.x < KQ4_RT_E;
+  for (int k = 0; k < ntile; ++k) {
+    if (wave > 0) {
+      store(k);
+      if (k + 1 < ntile) load(k + 1);
+    }
+    __syncthreads();   // tile k's products are in LDS; the adders are done with buffer k-1
+    if (adder) {
+      const int n = min(KQ4_RT_C, d - k * KQ4_RT_C);   // a multiple of 32
+      const float *src = kq4_rt_lds + ((k & 1) * KQ4_RT_E + threadIdx.x) * KQ4_RT_P;
+      for (int i = 0; i < n; i += 32) {
+        float4 v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = *reinterpret_cast<const float4 *>(src + i + 4 * j);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          s += v[j].x;
+          s += v[j].y;
+          s += v[j].z;
+          s += v[j].w;
+        }
+      }
+    }
+  }
+  if (adder && e0 + threadIdx.x < ne) logits[(size_t)t * ne + e0 + threadIdx.x] = s;
+}
+
+int kq4_launch_moe_logits(float *logits, const float *router, const float *X, int T, int ne,
+                          int d, hipStream_t s) {
+  if (T <= 0) return 0;
+  if (d % 32) return (int)hipErrorInvalidValue;
+  const size_t lds = 2 * KQ4_RT_E * KQ4_RT_P * sizeof(float);
+  static bool attr = false;   // 66 KB of LDS
+  if (!attr) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&kq4_moe_logits_kernel),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return (int)e;
+    attr = true;
+  }
+  hipLaunchKernelGGL(kq4_moe_logits_kernel,
+                     dim3((unsigned)((ne + KQ4_RT_E - 1) / KQ4_RT_E), (unsigned)T), dim3(320),
+                     lds, s, logits, router, X, ne, d);
+  return (int)hipGetLastError();
+}
+
 // ---- prep: grouping + activation quantizer ---------------------------------------------------
 // Workgroup 0 builds the expert -> (token, rank) table: counts by LDS atomics, an exclusive scan,
 // then each pair takes a slot by an atomic cursor. The order of an expert's pairs is whatever the

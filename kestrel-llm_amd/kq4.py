@@ -48,6 +48,8 @@ SIGNATURES = [
     ("kq4_block_sums_dev", _I, [_P, _P, _P, _P, _I, _I, _I, _P]),
     ("kq4_moe_route_dev", _I, [_P, _P, _P, _I, _I, _I, _P]),
     ("kq4_moe_ffn_dev", _I, [_P, _P, _P, _P, _I, _I, _P, _P, _P, _I, _I, _I, _P]),
+    ("kq4_moe_router_logits_dev", _I, [_P, _P, _P, _I, _I, _I, _P]),
+    ("kq4_moe_layer_dev", _I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _P, _P]),
     ("kq4_moe_ffn_stages_dev", _I,
      [_P, _P, _P, _P, _I, _I, _P, _P, _P, _I, _I, _I, _P, _P, _P, _P, _P]),
     # C11 op wrappers (include/kq4_ops.h)
@@ -300,6 +302,20 @@ def moe_route_dev(sel, pr, logits, tk, stream=None):
     T, ne = logits.shape
     check(lib().kq4_moe_route_dev(_tp(sel), _tp(pr), _tp(logits), T, ne, tk,
                                   _stream_ptr(stream)), "kq4_moe_route_dev")
+
+
+def moe_router_logits_dev(logits, router, X, stream=None):
+    T, d = X.shape
+    ne = router.shape[0]
+    check(lib().kq4_moe_router_logits_dev(_tp(logits), _tp(router), _tp(X), T, ne, d,
+                                          _stream_ptr(stream)), "kq4_moe_router_logits_dev")
+
+
+def moe_layer_dev(Y, X, router, G, U, D, ne, tk, d, ef, sel=None, pr=None, stream=None):
+    T = X.shape[0]
+    check(lib().kq4_moe_layer_dev(_tp(Y), _tp(X), _tp(router), _tp(G), _tp(U), _tp(D), T, ne, tk,
+                                  d, ef, _tp(sel), _tp(pr), _stream_ptr(stream)),
+          "kq4_moe_layer_dev")
 
 
 def moe_ffn_dev(Y, X, sel, pr, G, U, D, ne, d, ef, stream=None):

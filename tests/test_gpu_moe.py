@@ -1,5 +1,6 @@
 """GPU parity of the MoE FFN (int8 track) against the oracle (which is pinned bit-exact to the
 reference's own MoE in tests/test_oracle_moe.py), stage by stage:
+  router logits (fp32 serial chains)      bit-exact
   routing (device top-k/softmax)          sel exact, pr within 2 ulp (expf bits)
   gate / up (V4 chains)                   bit-exact
   SiLU product av                          within 4 ulp (exp evaluated on the device)
@@ -96,4 +97,50 @@ def test_moe_invalid_expert_ids_skipped(kq4, torch_dev, orc):
     Y_o = orc.moe_ffn(X, sel, pr, G, U, D, ne, d, ef)
     Y = kq4.moe_ffn(X, sel, pr, G, U, D, ne, d, ef)
     r, _ = rel_err(Y, Y_o)
+    assert r <= 1e-5
+
+
+def make_router(ne, d, seed):
+    return (np.random.default_rng(seed).standard_normal((ne, d)) * 0.02).astype(np.float32)
+
+
+@pytest.mark.parametrize("T,ne,d", [(1, 128, 2048), (7, 60, 96), (64, 128, 2048), (3, 300, 64)])
+def test_router_logits_bit_exact(kq4, torch_dev, orc, T, ne, d):
+    """fp32 router logits: the reference's serial chain per (token, expert), bit for bit."""
+    torch = torch_dev
+    R = make_router(ne, d, T + ne)
+    X = synth.make_activations(T, d, d + T)
+    want = orc.router_logits(R, X, ne, d)
+    lg = torch.empty((T, ne), dtype=torch.float32, device="cuda")
+    kq4.moe_router_logits_dev(lg, to_dev(torch, R), to_dev(torch, X))
+    torch.cuda.synchronize()
+    assert np.array_equal(host(lg).view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("T", [1, 64])
+@pytest.mark.parametrize("shape", ["small", "qwen3_30b_a3b"])
+def test_moe_layer_dev(kq4, torch_dev, orc, shape, T):
+    """Router logits + routing + expert FFN in one call against the oracle's layer (its router
+    and FFN are each pinned to the reference's own MoE)."""
+    torch = torch_dev
+    cfg = SHAPES[shape]
+    d, ne, tk, ef = cfg["hidden"], cfg["experts"], cfg["top_k"], cfg["ef"]
+    G, U, D = synth.make_moe(cfg, 70 + T)
+    R = make_router(ne, d, 71 + T)
+    X = synth.make_activations(T, d, 72 + T)
+    sel_o, pr_o = orc.moe_route(orc.router_logits(R, X, ne, d), tk)
+    Y_o = orc.moe_ffn(X, sel_o, pr_o, G, U, D, ne, d, ef)
+
+    dG, dU = (kq4.prepare_dev(to_dev(torch, a), ne * ef, d) for a in (G, U))
+    dD = kq4.prepare_dev(to_dev(torch, D), d, ne * ef)
+    Y = torch.empty((T, d), dtype=torch.float32, device="cuda")
+    sel = torch.empty((T, tk), dtype=torch.int32, device="cuda")
+    pr = torch.empty((T, tk), dtype=torch.float32, device="cuda")
+    kq4.moe_layer_dev(Y, to_dev(torch, X), to_dev(torch, R), dG, dU, dD, ne, tk, d, ef,
+                      sel=sel, pr=pr)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(sel), sel_o)
+    assert ulps(host(pr), pr_o) <= 2
+    r, a = rel_err(host(Y), Y_o)
+    print(f"moe layer {shape} T={T}: Y rel={r:.3e} maxabs={a:.3e}")
     assert r <= 1e-5

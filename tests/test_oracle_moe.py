@@ -83,3 +83,14 @@ def test_moe_stages_consistent(orc):
     g_dense = orc.matmul_q(G.reshape(-1, d // 32, 72)[e0 * ef // 4:(e0 + 1) * ef // 4], xq[:1],
                            xd[:1], ef, d, chain=2)
     assert np.allclose(st["gate"][0], g_dense[0], rtol=0, atol=1e-5 * np.abs(g_dense).max())
+
+
+def test_router_logits_closed_form(orc):
+    """Integer router weights and activations: every product and partial sum is exact, so the
+    serial chain equals the integer dot product (a transposed router or a wrong row fails)."""
+    rng = np.random.default_rng(4)
+    ne, d = 12, 96
+    R = rng.integers(-4, 5, (ne, d)).astype(np.float32)
+    X = rng.integers(-3, 4, (2, d)).astype(np.float32)
+    lg = orc.router_logits(R, X, ne, d)
+    assert np.array_equal(lg, (X.astype(np.int64) @ R.astype(np.int64).T).astype(np.float32))
