@@ -47,6 +47,7 @@ extern "C" {
 #define KQ4_EHIP (-2)     /* HIP runtime error */
 #define KQ4_ENOMEM (-3)   /* device allocation failed */
 #define KQ4_ENODEV (-4)   /* no usable gfx950 device */
+#define KQ4_EIO (-5)      /* file cannot be read or fails validation (kq4_vqf.h) */
 
 /* fp32 accumulation chain (how per-block products are summed; integer block sums are the
  * same in all of them). AUTO is the reference's dispatch (q4x4_gemm_batched
@@ -136,6 +137,12 @@ size_t kq4_weights_stream_bytes(int rows, int cols);
  * below is such a copy. */
 int kq4_weights_prepare_dev(uint8_t *dst, const uint8_t *w4x4, int rows, int cols,
                             void *stream);
+
+/* kq4_weights_prepare_dev from VQF 4x4 tiles in host memory (e.g. the mmap'd VQF file): the
+ * tiles are copied to the device and repacked into dst; returns once the host bytes have been
+ * read. */
+int kq4_weights_prepare_host(uint8_t *dst, const uint8_t *w4x4_host, int rows, int cols,
+                             void *stream);
 
 /* Activation quantizer (quantize_row_q8_0_act vllm_safetensors.c:7893-7920) for n_batch rows:
  * xq int8 [n_batch][cols], xd f32 [n_batch][cols/32]. xde (may be NULL) receives the scale

@@ -23,6 +23,19 @@ int fail(int code, const char *fmt, ...) {
   return code;
 }
 
+}  // namespace
+
+// Error reporting for the library's C host files (kq4_err.h).
+extern "C" __attribute__((visibility("hidden"))) int kq4_fail(int code, const char *fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+namespace {
+
 #define KQ4_HIP(call)                                                                   \
   do {                                                                                  \
     hipError_t e_ = (call);                                                             \
@@ -440,6 +453,24 @@ int kq4_weights_prepare_dev(uint8_t *dst, const uint8_t *w4x4, int rows, int col
   int rc = cur_dev(&ds);
   if (rc) return rc;
   KQ4_HIP((hipError_t)kq4_launch_repack(dst, w4x4, rows, cols, (hipStream_t)stream));
+  return KQ4_OK;
+}
+
+int kq4_weights_prepare_host(uint8_t *dst, const uint8_t *w4x4_host, int rows, int cols,
+                             void *stream) {
+  if (!shape_ok(rows, cols)) return fail(KQ4_EINVAL, "prepare: rows=%d cols=%d", rows, cols);
+  if (!dst || !w4x4_host || (uintptr_t)dst % 16)
+    return fail(KQ4_EINVAL, "prepare: null pointer or dst not 16-byte aligned");
+  DevState *ds = nullptr;
+  int rc = cur_dev(&ds);
+  if (rc) return rc;
+  const size_t n = wbytes(rows, cols);
+  if ((rc = ensure(ds->hstage, n))) return rc;
+  hipStream_t s = (hipStream_t)stream;
+  KQ4_HIP(hipMemcpyAsync(ds->hstage.p, w4x4_host, n, hipMemcpyHostToDevice, s));
+  KQ4_HIP((hipError_t)kq4_launch_repack(dst, static_cast<const uint8_t *>(ds->hstage.p), rows,
+                                        cols, s));
+  KQ4_HIP(hipStreamSynchronize(s));   // the staging buffer is reused by the next call
   return KQ4_OK;
 }
 

@@ -68,7 +68,33 @@ SIGNATURES = [
     ("kq4_dyn_matvec_q4_q8_fused_down_residual_batched", _I, [_P, _P, _P, _P, _I, _I, _I, _P]),
     ("kq4_st_moe_ffn_sparse_q4", _I, [_P, _P, _P]),
     ("kq4_st_moe_ffn_sparse_q4_batch", _I, [_P, _I, _P, _P]),
+    # include/kq4_vqf.h
+    ("kq4_weights_prepare_host", _I, [_P, _P, _I, _I, _P]),
+    ("kq4_vqf_parse_header", _I, [_P, ctypes.c_size_t, _U64, _P]),
+    ("kq4_vqf_open", _I, [ctypes.c_char_p, _I, ctypes.POINTER(_P)]),
+    ("kq4_vqf_close", None, [_P]),
+    ("kq4_vqf_get_info", _P, [_P]),
+    ("kq4_vqf_entry", _I, [_P, _I, ctypes.c_char_p, ctypes.POINTER(ctypes.c_uint32),
+                           ctypes.POINTER(ctypes.c_uint32), ctypes.POINTER(ctypes.c_uint32),
+                           ctypes.POINTER(_P), ctypes.POINTER(_U64)]),
+    ("kq4_vqf_find", _I, [_P, ctypes.c_char_p, ctypes.POINTER(_P), ctypes.POINTER(_U64)]),
+    ("kq4_vqf_q4_matrix", _I, [_P, _I, _I, ctypes.POINTER(_P), ctypes.POINTER(_I),
+                               ctypes.POINTER(_I)]),
+    ("kq4_vqf_prepare_dev", _I, [_P, _I, _I, _P, _P]),
+    ("kq4_vqf_upload", _I, [_P, _I, _I, ctypes.POINTER(_U64)]),
 ]
+
+PROJ_Q, PROJ_K, PROJ_V, PROJ_O, PROJ_GATE, PROJ_UP, PROJ_DOWN, PROJ_LM = range(8)
+
+
+class VqfInfo(ctypes.Structure):
+    """kq4_vqf_info (include/kq4_vqf.h)."""
+    _fields_ = [(n, ctypes.c_uint32) for n in (
+        "version", "flags", "n_tensors", "dim", "n_layers", "n_heads", "n_kv_heads",
+        "head_dim", "ffn_dim", "vocab_size")] + [
+        ("rope_theta", ctypes.c_float), ("norm_eps", ctypes.c_float)] + [
+        (n, ctypes.c_uint32) for n in ("n_experts", "moe_ffn", "top_k")] + [
+        ("data_offset", _U64), ("file_len", _U64), ("legacy_header", _I)]
 
 
 class KQ4Error(RuntimeError):
@@ -331,3 +357,71 @@ def moe_ffn_stages_dev(Y, X, sel, pr, G, U, D, ne, d, ef, gate=None, up=None, av
                                        _tp(D), ne, d, ef, _tp(gate), _tp(up), _tp(av),
                                        _tp(av_in), _stream_ptr(stream)),
           "kq4_moe_ffn_stages_dev")
+
+
+# ---- VQF files (include/kq4_vqf.h) -------------------------------------------------------------
+
+def vqf_parse_header(buf, file_size):
+    """Validates a header + directory held in buf (bytes) for a file of file_size bytes."""
+    b = np.frombuffer(buf, np.uint8)
+    info = VqfInfo()
+    check(lib().kq4_vqf_parse_header(b.ctypes.data, b.size, file_size, ctypes.byref(info)),
+          "kq4_vqf_parse_header")
+    return info
+
+
+class Vqf:
+    """A mmap'd VQF file (kq4_vqf_open); close() or use as a context manager."""
+
+    def __init__(self, path, verify_checksum=False):
+        self._h = _P()
+        check(lib().kq4_vqf_open(os.fsencode(path), int(verify_checksum), ctypes.byref(self._h)),
+              "kq4_vqf_open")
+        self.info = VqfInfo.from_address(lib().kq4_vqf_get_info(self._h))
+
+    def close(self):
+        if self._h:
+            lib().kq4_vqf_close(self._h)
+            self._h = _P()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    def entries(self):
+        out = []
+        for i in range(self.info.n_tensors):
+            name = ctypes.create_string_buffer(32)
+            qt, r, c = ctypes.c_uint32(), ctypes.c_uint32(), ctypes.c_uint32()
+            data, nbytes = _P(), _U64()
+            check(lib().kq4_vqf_entry(self._h, i, name, ctypes.byref(qt), ctypes.byref(r),
+                                      ctypes.byref(c), ctypes.byref(data), ctypes.byref(nbytes)),
+                  "kq4_vqf_entry")
+            out.append((name.value.decode(), qt.value, r.value, c.value, nbytes.value))
+        return out
+
+    def q4_matrix(self, proj, layer):
+        """(numpy view of the layer's VQF 4x4 tile bytes, rows, cols)."""
+        data, r, c = _P(), _I(), _I()
+        check(lib().kq4_vqf_q4_matrix(self._h, proj, layer, ctypes.byref(data), ctypes.byref(r),
+                                      ctypes.byref(c)), "kq4_vqf_q4_matrix")
+        n = r.value // 4 * (c.value // 32) * 72
+        arr = np.ctypeslib.as_array(ctypes.cast(data, ctypes.POINTER(ctypes.c_uint8)), (n,))
+        return arr, r.value, c.value
+
+    def prepare_dev(self, proj, layer, stream=None):
+        """The layer's stream-layout device copy (a new uint8 tensor)."""
+        import torch
+        _, r, c = self.q4_matrix(proj, layer)
+        dst = torch.empty(stream_bytes(r, c), dtype=torch.uint8, device="cuda")
+        check(lib().kq4_vqf_prepare_dev(self._h, proj, layer, _tp(dst), _stream_ptr(stream)),
+              "kq4_vqf_prepare_dev")
+        return dst, r, c
+
+    def upload(self, proj, layer):
+        """Uploads into the host-pointer API's cache; returns the key (layer << 32 | proj)."""
+        key = _U64()
+        check(lib().kq4_vqf_upload(self._h, proj, layer, ctypes.byref(key)), "kq4_vqf_upload")
+        return key.value

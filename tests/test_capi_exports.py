@@ -1,5 +1,5 @@
-"""libkq4.so loads without a GPU and exports every entry point include/kq4.h and
-include/kq4_ops.h declare (no compute calls here)."""
+"""libkq4.so loads without a GPU and exports every entry point include/kq4.h, include/kq4_ops.h
+and include/kq4_vqf.h declare (no compute calls here)."""
 import ctypes
 import os
 import re
@@ -7,7 +7,7 @@ import re
 import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADERS = [os.path.join(ROOT, "include", h) for h in ("kq4.h", "kq4_ops.h")]
+HEADERS = [os.path.join(ROOT, "include", h) for h in ("kq4.h", "kq4_ops.h", "kq4_vqf.h")]
 
 
 def declared(path):
