@@ -408,6 +408,126 @@ int kqo_matmul_silu(float *out, const float *gate, const float *up, const float 
     return rc;
 }
 
+/* ---------------------------------------------------------------- Q8_0 weights */
+
+/* Legacy Q8_0 encoder, 34-B blocks {f16 d; int8 qs[32]} (vqf_convert/src/quant_kernels.c:64-107):
+ * scale = max(1e-10f, max|x|) / 127 (true division), stored as f16 (RNE); qs = round half away
+ * from zero of fl(x * fl(1/scale)) (the f32 scale), clamped to [-127, 127]. Pinned byte for byte
+ * against the reference's f32_to_q8_0 built in oracle/_ref. */
+void kqo_f32_to_q8_0(uint8_t *q8_out, const float *f32_in, int n_elements) {
+    int n_blocks = n_elements / 32;
+    for (int b = 0; b < n_blocks; b++) {
+        const float *xb = f32_in + (size_t)b * 32;
+        float amax = 1e-10f;
+        for (int i = 0; i < 32; i++) {
+            float av = fabsf(xb[i]);
+            if (av > amax) amax = av;
+        }
+        volatile float c127 = 127.0f;
+        float scale = amax / c127;
+        if (scale < 1e-10f) scale = 1e-10f;
+        uint16_t h = kqo_f32_to_f16_bits(scale);
+        memcpy(q8_out + (size_t)b * 34, &h, 2);
+        int8_t *qs = (int8_t *)(q8_out + (size_t)b * 34 + 2);
+        float rscale = 1.0f / scale;
+        for (int i = 0; i < 32; i++) {
+            volatile float qv = xb[i] * rscale;
+            int q = (int)(qv < 0.0f ? qv - 0.5f : qv + 0.5f);
+            qs[i] = (int8_t)(q > 127 ? 127 : (q < -127 ? -127 : q));
+        }
+    }
+}
+
+/* Legacy -> tiled Q8_0 (vqf_convert/src/qk_repack.c:51-103): per group of g rows (g = 8: the
+ * 272-B block_q8_0x8, VQF_FLAG_Q8_8X8; g = 4: the 136-B block_q8_0x4) and block b: the g row
+ * scales (f16, row order), then qs[k*4g + m*4 + i] = row m's element 4k+i (k = 0..7). Pinned byte
+ * for byte against the reference's repack_q8_0_8x8_inplace / repack_q8_0_4x4_inplace. */
+int kqo_repack_q8_0_tiled(const uint8_t *legacy, uint8_t *tiles, int g, int rows, int cols) {
+    if ((g != 8 && g != 4) || rows % g != 0 || cols % 32 != 0) return -1;
+    int nb = cols / 32;
+    size_t row_stride = (size_t)nb * 34, tb = (size_t)34 * g;
+    for (int r0 = 0; r0 < rows; r0 += g) {
+        const uint8_t *src = legacy + (size_t)r0 * row_stride;
+        for (int b = 0; b < nb; b++) {
+            uint8_t *out = tiles + ((size_t)(r0 / g) * nb + b) * tb;
+            for (int m = 0; m < g; m++) memcpy(out + 2 * m, src + m * row_stride + (size_t)b * 34, 2);
+            for (int k = 0; k < 8; k++)
+                for (int m = 0; m < g; m++)
+                    memcpy(out + 2 * g + (size_t)k * 4 * g + 4 * m,
+                           src + m * row_stride + (size_t)b * 34 + 2 + 4 * k, 4);
+        }
+    }
+    return 0;
+}
+
+/* Code of element e (0..31) of (row, block b) in a tiled matrix, and its row scale (f32). */
+static int q8_code(const uint8_t *w, int g, int nb, int row, int b, int e) {
+    const uint8_t *t = w + ((size_t)(row / g) * nb + b) * (size_t)(34 * g);
+    return (int8_t)t[2 * g + (e >> 2) * 4 * g + (row % g) * 4 + (e & 3)];
+}
+static float q8_scale(const uint8_t *w, int g, int nb, int row, int b) {
+    const uint8_t *t = w + ((size_t)(row / g) * nb + b) * (size_t)(34 * g);
+    uint16_t h;
+    memcpy(&h, t + 2 * (row % g), 2);
+    return kqo_f16_to_f32(h);
+}
+
+/* Q8_0 matmul from quantized activations, per token the reference's chain (AArch64, weights
+ * repacked):
+ *   VDOT (KQO_CHAIN_GEMV32; q8x8_dot_rows vllm_safetensors.c:5178-5225, single-token decode
+ *     :5410-5421): acc = fma(f32(S), fl(wd * xd), acc), S = the exact int32 block dot;
+ *   GEMM (KQO_CHAIN_Q8GEMM; gemm_q8_0_8x8_neon :4973-5050 and its 8x4 tail, batched
+ *     n_batch >= 2 :5323-5331, activation scales through repack_q8_0_8x8_act :4937-4965):
+ *     acc = fl(acc + fl(fl(wd * f32(f16_rne(xd))) * f32(S))) (vmlaq_f32 is an unfused
+ *     multiply-add under the reference's -ffp-contract=off);
+ *   AUTO: n_batch == 1 -> VDOT, n_batch >= 2 -> GEMM for every token
+ *     (dyn_matvec_q8_*_batched_neon :5977-6001, :6071-6091).
+ * out = fl(residual + acc) when fused (:5219-5224, vllm_q8x4_res_worker :4806-4814). g = 8 or 4
+ * (tile rows). Pinned by exact cases and planted differences (tests/test_oracle_q8.py). */
+int kqo_q8_matmul_q(float *out, const int8_t *xq, const float *xd, const float *residual,
+                    const uint8_t *w, int g, int rows, int cols, int n_batch, int chain) {
+    if ((g != 8 && g != 4) || rows <= 0 || rows % g || cols <= 0 || cols % 32 || n_batch < 0)
+        return -1;
+    int nb = cols / 32;
+    int gemm = chain == KQO_CHAIN_Q8GEMM || (chain == KQO_CHAIN_AUTO && n_batch >= 2);
+    if (!gemm && chain != KQO_CHAIN_GEMV32 && chain != KQO_CHAIN_AUTO) return -1;
+    for (int t = 0; t < n_batch; t++) {
+        const int8_t *q = xq + (size_t)t * cols;
+        for (int n = 0; n < rows; n++) {
+            float acc = 0.0f;
+            for (int b = 0; b < nb; b++) {
+                int32_t s = 0;
+                for (int e = 0; e < 32; e++) s += q8_code(w, g, nb, n, b, e) * (int32_t)q[b * 32 + e];
+                float wd = q8_scale(w, g, nb, n, b);
+                float xs = xd[(size_t)t * nb + b];
+                if (gemm) {
+                    float sc = wd * kqo_f16_to_f32(kqo_f32_to_f16_bits(xs));
+                    acc = acc + sc * (float)s;
+                } else {
+                    acc = fmaf((float)s, wd * xs, acc);
+                }
+            }
+            float r = residual ? residual[(size_t)t * rows + n] + acc : acc;
+            out[(size_t)t * rows + n] = r;
+        }
+    }
+    return 0;
+}
+
+int kqo_q8_matmul(float *out, const float *x, const float *residual, const uint8_t *w, int g,
+                  int rows, int cols, int n_batch, int chain) {
+    if (cols <= 0 || cols % 32 || n_batch < 0) return -1;
+    int nb = cols / 32;
+    int8_t *xq = (int8_t *)malloc((size_t)n_batch * cols + 1);
+    float *xd = (float *)malloc(((size_t)n_batch * nb + 1) * sizeof(float));
+    if (!xq || !xd) { free(xq); free(xd); return -1; }
+    kqo_quantize_rows(x, xq, xd, n_batch, cols);
+    int rc = kqo_q8_matmul_q(out, xq, xd, residual, w, g, rows, cols, n_batch, chain);
+    free(xq);
+    free(xd);
+    return rc;
+}
+
 /* ---------------------------------------------------------------- RMSNorm */
 
 /* hsum8_f32 (vllm_safetensors.c:8803-8809): ((v0+v4) + (v1+v5)) + ((v2+v6) + (v3+v7)). */

@@ -29,7 +29,8 @@ enum {
     KQO_CHAIN_AUTO = 0,   /* reference dispatch: M<=3 -> CTILE; M>=4 -> ASM on 4*floor(M/4) + CTILE tail */
     KQO_CHAIN_CTILE = 1,  /* V1: lo/hi accumulators, f32 activation scale */
     KQO_CHAIN_GEMV32 = 2, /* V2: single accumulator, f32 activation scale */
-    KQO_CHAIN_ASM = 3     /* V3: single accumulator, activation scale rounded to f16 (RNE) */
+    KQO_CHAIN_ASM = 3,    /* V3: single accumulator, activation scale rounded to f16 (RNE) */
+    KQO_CHAIN_Q8GEMM = 4  /* Q8_0 batched GEMM: fl(acc + fl(fl(wd * f16r(xd)) * S)) */
 };
 
 uint32_t kqo_f16_to_f32_bits(uint16_t h);
@@ -71,6 +72,16 @@ void kqo_silu_mul_rows(float *g, const float *u, long n);   /* in place, n eleme
 /* out = [residual +] W . silu_mul(gate, up), both [n_batch][cols]. */
 int kqo_matmul_silu(float *out, const float *gate, const float *up, const float *residual,
                     const uint8_t *w, int rows, int cols, int n_batch, int chain);
+
+/* ---- Q8_0 weights: legacy 34-B blocks, tiled 8x8 (272 B) / 4x4 (136 B), matmul chains ---- */
+void kqo_f32_to_q8_0(uint8_t *q8_out, const float *f32_in, int n_elements);
+int kqo_repack_q8_0_tiled(const uint8_t *legacy, uint8_t *tiles, int g, int rows, int cols);
+/* chain: KQO_CHAIN_AUTO (n_batch 1 -> VDOT, >= 2 -> GEMM), KQO_CHAIN_GEMV32 (VDOT),
+ * KQO_CHAIN_Q8GEMM (GEMM); g = tile rows (8 or 4) */
+int kqo_q8_matmul_q(float *out, const int8_t *xq, const float *xd, const float *residual,
+                    const uint8_t *w, int g, int rows, int cols, int n_batch, int chain);
+int kqo_q8_matmul(float *out, const float *x, const float *residual, const uint8_t *w, int g,
+                  int rows, int cols, int n_batch, int chain);
 
 /* ---- RMSNorm (dyn_rms_norm chunked order / dyn_rms_norm_batch serial order) ---- */
 void kqo_rms_norm(float *out, const float *x, const float *w, int n_batch, int d, float eps,

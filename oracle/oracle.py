@@ -14,7 +14,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ORACLE_SO = os.path.join(HERE, "libkq4_oracle.so")
 REF_SO = os.path.join(HERE, "_ref", "libkref.so")
 
-CHAIN_AUTO, CHAIN_CTILE, CHAIN_GEMV32, CHAIN_ASM = 0, 1, 2, 3
+CHAIN_AUTO, CHAIN_CTILE, CHAIN_GEMV32, CHAIN_ASM, CHAIN_Q8GEMM = 0, 1, 2, 3, 4
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -42,6 +42,10 @@ _ORACLE_SIGS = [
     ("kqo_silu_mul_rows", None, [_P, _P, ctypes.c_long]),
     ("kqo_matmul_silu", _I, [_P, _P, _P, _P, _P, _I, _I, _I, _I]),
     ("kqo_rms_norm", None, [_P, _P, _P, _I, _I, ctypes.c_float, _I]),
+    ("kqo_f32_to_q8_0", None, [_P, _P, _I]),
+    ("kqo_repack_q8_0_tiled", _I, [_P, _P, _I, _I, _I]),
+    ("kqo_q8_matmul_q", _I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I]),
+    ("kqo_q8_matmul", _I, [_P, _P, _P, _P, _I, _I, _I, _I, _I]),
     ("kqo_moe_ffn", _I, [_P, _P, _P, _P, _I, _I, _P, _P, _P, _I, _I, _I,
                          _P, _P, _P, _P, _P, _P, _P]),
 ]
@@ -62,6 +66,9 @@ _REF_SIGS = [
     ("kref_matvec", None, [_P, _P, _P, _I, _I]),
     ("kref_silu_mul", None, [_P, _P, _I]),
     ("kref_rms_norm", None, [_P, _P, _P, _I, ctypes.c_float]),
+    ("kref_f32_to_q8_0", None, [_P, _P, _I]),
+    ("kref_repack_q8_0_8x8", _I, [_P, _I, _I]),
+    ("kref_repack_q8_0_4x4", _I, [_P, _I, _I]),
     ("kref_rms_norm_batch", None, [_P, _P, _P, _I, _I, ctypes.c_float]),
 ]
 
@@ -183,6 +190,38 @@ def matmul_silu(w, gate, up, rows, cols, residual=None, chain=CHAIN_AUTO):
     res = None if residual is None else _c(residual, np.float32)
     rc = lib().kqo_matmul_silu(_p(out), _p(gate), _p(up), _p(res), _p(_c(w, np.uint8)), rows,
                                cols, n, chain)
+    assert rc == 0
+    return out
+
+
+def q8_tiles(wf, rows, cols, g=8):
+    """Q8_0 tiles (g = 8: block_q8_0x8, VQF_FLAG_Q8_8X8; g = 4: block_q8_0x4) of fp32 weights."""
+    wf = _c(wf, np.float32).reshape(rows, cols)
+    legacy = np.empty(rows * cols // 32 * 34, np.uint8)
+    lib().kqo_f32_to_q8_0(_p(legacy), _p(wf), rows * cols)
+    tiles = np.empty_like(legacy)
+    assert lib().kqo_repack_q8_0_tiled(_p(legacy), _p(tiles), g, rows, cols) == 0
+    return tiles
+
+
+def q8_matmul(w, x, rows, cols, residual=None, chain=CHAIN_AUTO, g=8):
+    x = _c(x, np.float32).reshape(-1, cols)
+    n = x.shape[0]
+    out = np.empty((n, rows), np.float32)
+    res = None if residual is None else _c(residual, np.float32)
+    rc = lib().kqo_q8_matmul(_p(out), _p(x), _p(res), _p(_c(w, np.uint8)), g, rows, cols, n,
+                             chain)
+    assert rc == 0
+    return out
+
+
+def q8_matmul_q(w, xq, xd, rows, cols, residual=None, chain=CHAIN_AUTO, g=8):
+    xq = _c(xq, np.int8).reshape(-1, cols)
+    n = xq.shape[0]
+    out = np.empty((n, rows), np.float32)
+    res = None if residual is None else _c(residual, np.float32)
+    rc = lib().kqo_q8_matmul_q(_p(out), _p(xq), _p(_c(xd, np.float32)), _p(res),
+                               _p(_c(w, np.uint8)), g, rows, cols, n, chain)
     assert rc == 0
     return out
 

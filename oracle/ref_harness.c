@@ -106,3 +106,16 @@ void kref_rms_norm(float *out, const float *x, const float *w, int d, float eps)
 void kref_rms_norm_batch(float *out, const float *x, const float *w, int nb, int d, float eps) {
     dyn_rms_norm_batch(out, x, w, nb, d, eps);
 }
+
+/* The reference converter's Q8_0 encoder and tile repacks (vqf_convert/src/quant_kernels.c:64,
+ * qk_repack.c:51, :78; linked from their own objects). */
+void f32_to_q8_0(uint8_t *q8_out, const float *f32_in, int n_elements);
+int repack_q8_0_8x8_inplace(uint8_t *buf, int rows, int cols);
+int repack_q8_0_4x4_inplace(uint8_t *buf, int rows, int cols);
+void kref_f32_to_q8_0(uint8_t *out, const float *in, int n) { f32_to_q8_0(out, in, n); }
+int kref_repack_q8_0_8x8(uint8_t *buf, int rows, int cols) {
+    return repack_q8_0_8x8_inplace(buf, rows, cols);
+}
+int kref_repack_q8_0_4x4(uint8_t *buf, int rows, int cols) {
+    return repack_q8_0_4x4_inplace(buf, rows, cols);
+}
