@@ -57,6 +57,10 @@ extern "C" {
 #define KQ4_CHAIN_CTILE 1   /* q4x4_dot1_group16, vllm_safetensors.c:4180-4216 */
 #define KQ4_CHAIN_GEMV32 2  /* q4x4_dot1_group16_gemv (M4f), :4229-4251 */
 #define KQ4_CHAIN_ASM 3     /* llama 4x4 asm GEMM, f16-rounded activation scale, :4328-4368 */
+/* Q8_0 weights (kq4_q8_*): AUTO = 1 token -> GEMV32 (the VDOT chain of q8x8_dot_rows
+ * :5178-5225), >= 2 tokens -> Q8GEMM for every token (gemm_q8_0_8x8_neon :4973-5050:
+ * acc = fl(acc + fl(fl(wd * f16r(xd)) * S)), unfused). */
+#define KQ4_CHAIN_Q8GEMM 4
 
 /* Summation order of an RMSNorm's sum of squares (both are the reference's, one binary32
  * rounding per step): CHUNKED = dyn_rms_norm (vllm_safetensors.c:8811-8827, decode; also the
@@ -114,6 +118,18 @@ int kq4_matmul_multi(int n_mats, float *const *out, const float *const *residual
                      const uint8_t *const *w4x4, const int *rows, int cols, const float *x,
                      int n_batch, int chain, const uint64_t *wkeys);
 
+/* Q8_0 weights (the reference's prefill format of dual VQF files, vllm_safetensors.c:2453-2460,
+ * and its q8 mode): tiles of g = 8 rows (block_q8_0x8, 272 B per 8 rows x 32 cols,
+ * VQF_FLAG_Q8_8X8, the reference's default) or g = 4 rows (block_q8_0x4, 136 B): g f16 row
+ * scales, then qs[k*4g + m*4 + i] = row m's element 4k+i (vqf_convert/src/qk_repack.c:51-103).
+ * out = [residual +] W.x with the reference's Q8 chains (KQ4_CHAIN_AUTO / GEMV32 / Q8GEMM).
+ * wkey as kq4_matmul (the q8 copy of a key is kept apart from its q4 copy). */
+int kq4_q8_matmul(float *out, const float *x, const float *residual, const uint8_t *w_tiles,
+                  int g, int rows, int cols, int n_batch, int chain, uint64_t wkey);
+int kq4_q8_matmul_multi(int n_mats, float *const *out, const float *const *residual,
+                        const uint8_t *const *w_tiles, int g, const int *rows, int cols,
+                        const float *x, int n_batch, int chain, const uint64_t *wkeys);
+
 /* MoE FFN of T tokens with top-k routing given as expert ids `sel` [T][tk] and weights `pr`
  * [T][tk]; int8 activation track (VLLM_ACTQ=1) of st_moe_ffn_sparse_q4 / _batch_arm
  * (vllm_safetensors.c:12921-13398, 14894-15064). G/U: [ne*ef rows][d cols], D: [d rows]
@@ -143,6 +159,20 @@ int kq4_weights_prepare_dev(uint8_t *dst, const uint8_t *w4x4, int rows, int col
  * read. */
 int kq4_weights_prepare_host(uint8_t *dst, const uint8_t *w4x4_host, int rows, int cols,
                              void *stream);
+
+/* Q8_0 weights on the device: the q8 stream layout (8704 B per 32-row set and 8-block stage)
+ * made once from the reference's tiles (device or host memory), and the matmuls over it
+ * (decode GEMV up to 8 tokens, int8-MFMA GEMM beyond). g = 8 or 4 tile rows, rows % g == 0. */
+size_t kq4_q8_weights_stream_bytes(int rows, int cols);
+int kq4_q8_weights_prepare_dev(uint8_t *dst, const uint8_t *w_tiles, int g, int rows, int cols,
+                               void *stream);
+int kq4_q8_weights_prepare_host(uint8_t *dst, const uint8_t *w_tiles_host, int g, int rows,
+                                int cols, void *stream);
+int kq4_q8_matmul_dev(float *out, const float *x, const float *residual, const uint8_t *w,
+                      int rows, int cols, int n_batch, int chain, void *stream);
+int kq4_q8_matmul_multi_dev(int n_mats, float *const *out, const float *const *residual,
+                            const uint8_t *const *w, const int *rows, int cols, const float *x,
+                            int n_batch, int chain, void *stream);
 
 /* Activation quantizer (quantize_row_q8_0_act vllm_safetensors.c:7893-7920) for n_batch rows:
  * xq int8 [n_batch][cols], xd f32 [n_batch][cols/32]. xde (may be NULL) receives the scale

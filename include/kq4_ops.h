@@ -84,6 +84,43 @@ int kq4_silu_mul_down_residual_batched(float *x_batch, const float *residual_bat
                                        const float *up_batch, int hidden_dim, int ffn_dim,
                                        int n_batch);
 
+/* ---- Q8_0 op family (dyn_matvec_q8_* vllm_safetensors.c:8509-8610): weights in the tiled
+ * Q8_0 layout the reference repacks to - 8x8 (block_q8_0x8) unless VLLM_Q8_8X8=0 or rows % 8 != 0,
+ * then 4x4 - as q8x8_enabled / q8_vdot_dispatch choose it (:3971-3979, :5283-5290). */
+
+/* dyn_matvec_q8 (single-token matvec, :1236 / :5400-5440) */
+int kq4_dyn_matvec_q8(float *out, const uint8_t *q8_w, const float *x, int rows, int cols);
+
+/* dyn_matvec_q8_fused_qkv_batched (:8509) */
+int kq4_dyn_matvec_q8_fused_qkv_batched(float *q_out, float *k_out, float *v_out,
+                                        const uint8_t *q8_q, const uint8_t *q8_k,
+                                        const uint8_t *q8_v, const float *x_batch, int q_rows,
+                                        int kv_rows, int cols, int n_batch);
+
+/* dyn_matvec_q8_fused_o_residual_batched (:8529) */
+int kq4_dyn_matvec_q8_fused_o_residual_batched(float *x_batch, const float *residual_batch,
+                                               const uint8_t *q8_o, const float *attn_batch,
+                                               int rows, int cols, int n_batch);
+
+/* dyn_matvec_q8_fused_gate_up_batched (:8547) */
+int kq4_dyn_matvec_q8_fused_gate_up_batched(float *gate_out, float *up_out,
+                                            const uint8_t *q8_gate, const uint8_t *q8_up,
+                                            const float *x_batch, int rows, int cols,
+                                            int n_batch);
+
+/* dyn_matvec_q8_fused_down_residual_batched (:8563) */
+int kq4_dyn_matvec_q8_fused_down_residual_batched(float *x_batch, const float *residual_batch,
+                                                  const uint8_t *q8_down,
+                                                  const float *activated_batch, int hidden_dim,
+                                                  int ffn_dim, int n_batch);
+
+/* dyn_matvec_q8_fused_o_residual (:8583) and _down_residual (:8595), single token */
+int kq4_dyn_matvec_q8_fused_o_residual(float *x, const float *residual, const uint8_t *q8_o,
+                                       const float *attn_in, int rows, int cols);
+int kq4_dyn_matvec_q8_fused_down_residual(float *x, const float *residual,
+                                          const uint8_t *q8_down, const float *activated,
+                                          int hidden_dim, int ffn_dim);
+
 /* One MoE layer as st_moe_ffn_sparse_q4 reads it from STModelWeights (:12937-12952): fp32 router
  * [ne][d], q4 4x4 G/U [ne*ef][d] and D [d][ne*ef]. */
 typedef struct {

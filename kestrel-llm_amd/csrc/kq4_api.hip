@@ -172,7 +172,8 @@ bool gemv_fq(long work, int n, bool silu) {
 // separate launch; with xu the activation is silu_mul(x, xu)) or from token-major xq/xd.
 int run_gemv(DevState *ds, int n_mats, float *const *out, const float *const *res,
              const uint8_t *const *w, const int *rows, int cols, const float *x, const float *xu,
-             const int8_t *xq, const float *xd, int n, int asm_tokens, hipStream_t s) {
+             const int8_t *xq, const float *xd, int n, int asm_tokens, hipStream_t s,
+             int wf = 0) {
   const int nb = cols / 32;
   int rc;
   KQ4GemvArgs a;
@@ -180,7 +181,7 @@ int run_gemv(DevState *ds, int n_mats, float *const *out, const float *const *re
   int sets = 0;
   for (int i = 0; i < n_mats; ++i) sets += (rows[i] + 31) / 32;
   int hs = 0, nw = 1;
-  plan_gemv(sets, nb, ds->ncu, &hs, &nw);
+  plan_gemv(sets, wf ? 2 * nb : nb, ds->ncu, &hs, &nw);   // q8 stages hold 8 blocks
   if (x) {
     const long per_cu = ((long)(sets << hs) + ds->ncu - 1) / ds->ncu;
     if (gemv_fq(per_cu * cols * n, n, xu != nullptr)) {
@@ -203,7 +204,8 @@ int run_gemv(DevState *ds, int n_mats, float *const *out, const float *const *re
   a.asm_tokens = asm_tokens;
   a.cols = cols;
   a.nb = nb;
-  const int kind = gemv_kind(n);
+  a.wf = wf;
+  const int kind = wf ? 1 : gemv_kind(n);
   int wg = 0;
   for (int i = 0; i < n_mats; ++i) {
     KQ4GemvMat &m = a.mat[i];
@@ -221,9 +223,13 @@ int run_gemv(DevState *ds, int n_mats, float *const *out, const float *const *re
 // x (fp32; with xu the activation is silu_mul(x, xu)) or xq_in/xd_in (pre-quantized).
 int matmul_impl(int n_mats, float *const *out, const float *const *res, const uint8_t *const *w,
                 const int *rows, int cols, const float *x, const int8_t *xq_in,
-                const float *xd_in, int n, int chain, hipStream_t s, const float *xu = nullptr) {
+                const float *xd_in, int n, int chain, hipStream_t s, const float *xu = nullptr,
+                int wf = 0) {
   if (n_mats < 1 || n_mats > KQ4_MAX_MATS) return fail(KQ4_EINVAL, "n_mats=%d", n_mats);
-  if (chain < KQ4_CHAIN_AUTO || chain > KQ4_CHAIN_ASM) return fail(KQ4_EINVAL, "chain=%d", chain);
+  if (wf ? (chain != KQ4_CHAIN_AUTO && chain != KQ4_CHAIN_GEMV32 && chain != KQ4_CHAIN_Q8GEMM)
+         : (chain < KQ4_CHAIN_AUTO || chain > KQ4_CHAIN_ASM))
+    return fail(KQ4_EINVAL, "chain=%d", chain);
+  if (wf && xu) return fail(KQ4_EINVAL, "the SiLU form takes q4 weights");
   if (n < 0) return fail(KQ4_EINVAL, "n_batch=%d", n);
   for (int i = 0; i < n_mats; ++i) {
     if (!shape_ok(rows[i], cols))
@@ -241,6 +247,30 @@ int matmul_impl(int n_mats, float *const *out, const float *const *res, const ui
   if (rc) return rc;
   const int nb = cols / 32;
   const size_t qbytes = al256((size_t)n * cols) + al256((size_t)n * nb * sizeof(float));
+
+  if (wf) {
+    // Q8_0: the VDOT chain (f32 activation scale, fused) or the GEMM chain (f16-rounded scale,
+    // unfused) for every token; AUTO takes VDOT for one token and GEMM from two on, as the
+    // reference's q8 wrappers dispatch (vllm_safetensors.c:5977-6001, :6071-6091)
+    const bool gchain = chain == KQ4_CHAIN_Q8GEMM || (chain == KQ4_CHAIN_AUTO && n >= 2);
+    if (n <= KQ4_GEMV_MAX_M)
+      return run_gemv(ds, n_mats, out, res, w, rows, cols, x, nullptr, xq_in, xd_in, n,
+                      gchain ? n : 0, s, gchain ? 2 : 1);
+    if ((rc = ensure(ds->ws, qbytes))) return rc;
+    Carve cv{static_cast<char *>(ds->ws.p)};
+    KQ4GemmAct act{xq_in, cols, 32, xd_in, nb, 1};
+    if (x) {
+      int8_t *q = cv.take<int8_t>((size_t)n * cols);
+      float *d = cv.take<float>((size_t)n * nb);
+      KQ4_HIP((hipError_t)kq4_launch_quantize(x, q, d, nullptr, n, cols, 0, s, 0));
+      act = KQ4GemmAct{q, cols, 32, d, nb, 1};
+    }
+    for (int i = 0; i < n_mats; ++i)
+      KQ4_HIP((hipError_t)kq4_launch_gemm(out[i], res ? res[i] : nullptr, w[i], act, rows[i],
+                                          cols, n, gchain ? KQ4_CHAIN_Q8GEMM : KQ4_CHAIN_GEMV32,
+                                          ds->ncu, s, 1));
+    return KQ4_OK;
+  }
 
   if (n <= KQ4_GEMV_MAX_M)
     return run_gemv(ds, n_mats, out, res, w, rows, cols, x, xu, xq_in, xd_in, n,
@@ -339,9 +369,13 @@ uint64_t fingerprint(const uint8_t *w, size_t bytes) {
 // repacked once), or for wkey == 0 repacked into `tmp` for this call only. The VQF bytes go
 // through the staging buffer hstage; everything runs on the null stream, so it is ordered before
 // the kernels that read the copy.
+// g = 0: q4 VQF 4x4 tiles; g = 8 / 4: Q8_0 tiles of g rows (kept under wkey with bit 63 set, so
+// a layer's q4 and q8 copies of one projection do not collide).
 int dev_weights(DevState *ds, uint64_t wkey, const uint8_t *w, int rows, int cols, Buf &tmp,
-                const uint8_t **dev) {
-  const size_t bytes = wbytes(rows, cols), sbytes = kq4_stream_bytes(rows, cols);
+                const uint8_t **dev, int g = 0) {
+  const size_t bytes = g ? (size_t)rows * (cols / 32) * 34 : wbytes(rows, cols);
+  const size_t sbytes = g ? kq8_stream_bytes(rows, cols) : kq4_stream_bytes(rows, cols);
+  if (wkey && g) wkey |= 1ull << 63;
   const uint64_t fp = wkey ? fingerprint(w, bytes) : 0;
   if (wkey) {
     std::lock_guard<std::mutex> lk(g_mu);
@@ -363,8 +397,9 @@ int dev_weights(DevState *ds, uint64_t wkey, const uint8_t *w, int rows, int col
     if ((rc = ensure(tmp, sbytes))) return rc;
     dst = static_cast<uint8_t *>(tmp.p);
   }
-  hipError_t e = (hipError_t)kq4_launch_repack(dst, static_cast<const uint8_t *>(ds->hstage.p),
-                                               rows, cols, nullptr);
+  const uint8_t *src = static_cast<const uint8_t *>(ds->hstage.p);
+  hipError_t e = (hipError_t)(g ? kq8_launch_repack(dst, src, g, rows, cols, nullptr)
+                                : kq4_launch_repack(dst, src, rows, cols, nullptr));
   if (e != hipSuccess) {
     if (wkey) (void)hipFree(dst);
     return fail(KQ4_EHIP, "weight repack: %s", hipGetErrorString(e));
@@ -454,6 +489,59 @@ int kq4_weights_prepare_dev(uint8_t *dst, const uint8_t *w4x4, int rows, int col
   if (rc) return rc;
   KQ4_HIP((hipError_t)kq4_launch_repack(dst, w4x4, rows, cols, (hipStream_t)stream));
   return KQ4_OK;
+}
+
+size_t kq4_q8_weights_stream_bytes(int rows, int cols) {
+  return shape_ok(rows, cols) ? kq8_stream_bytes(rows, cols) : 0;
+}
+
+int kq4_q8_weights_prepare_dev(uint8_t *dst, const uint8_t *w_tiles, int g, int rows, int cols,
+                               void *stream) {
+  if ((g != 8 && g != 4) || !shape_ok(rows, cols) || rows % g)
+    return fail(KQ4_EINVAL, "q8 prepare: g=%d rows=%d cols=%d", g, rows, cols);
+  if (!dst || !w_tiles || (uintptr_t)dst % 16 || (uintptr_t)w_tiles % 4)
+    return fail(KQ4_EINVAL, "q8 prepare: null pointer, dst not 16-byte or tiles not 4-byte aligned");
+  DevState *ds = nullptr;
+  int rc = cur_dev(&ds);
+  if (rc) return rc;
+  KQ4_HIP((hipError_t)kq8_launch_repack(dst, w_tiles, g, rows, cols, (hipStream_t)stream));
+  return KQ4_OK;
+}
+
+int kq4_q8_weights_prepare_host(uint8_t *dst, const uint8_t *w_tiles_host, int g, int rows,
+                                int cols, void *stream) {
+  if ((g != 8 && g != 4) || !shape_ok(rows, cols) || rows % g)
+    return fail(KQ4_EINVAL, "q8 prepare: g=%d rows=%d cols=%d", g, rows, cols);
+  if (!dst || !w_tiles_host || (uintptr_t)dst % 16)
+    return fail(KQ4_EINVAL, "q8 prepare: null pointer or dst not 16-byte aligned");
+  DevState *ds = nullptr;
+  int rc = cur_dev(&ds);
+  if (rc) return rc;
+  const size_t n = (size_t)rows * (cols / 32) * 34;
+  if ((rc = ensure(ds->hstage, n))) return rc;
+  hipStream_t s = (hipStream_t)stream;
+  KQ4_HIP(hipMemcpyAsync(ds->hstage.p, w_tiles_host, n, hipMemcpyHostToDevice, s));
+  KQ4_HIP((hipError_t)kq8_launch_repack(dst, static_cast<const uint8_t *>(ds->hstage.p), g, rows,
+                                        cols, s));
+  KQ4_HIP(hipStreamSynchronize(s));   // the staging buffer is reused by the next call
+  return KQ4_OK;
+}
+
+int kq4_q8_matmul_dev(float *out, const float *x, const float *residual, const uint8_t *w,
+                      int rows, int cols, int n_batch, int chain, void *stream) {
+  if (!x && n_batch) return fail(KQ4_EINVAL, "null x");
+  const float *res[1] = {residual};
+  return matmul_impl(1, &out, res, &w, &rows, cols, x, nullptr, nullptr, n_batch, chain,
+                     (hipStream_t)stream, nullptr, 1);
+}
+
+int kq4_q8_matmul_multi_dev(int n_mats, float *const *out, const float *const *residual,
+                            const uint8_t *const *w, const int *rows, int cols, const float *x,
+                            int n_batch, int chain, void *stream) {
+  if (!x && n_batch) return fail(KQ4_EINVAL, "null x");
+  if (!out || !w || !rows) return fail(KQ4_EINVAL, "null array argument");
+  return matmul_impl(n_mats, out, residual, w, rows, cols, x, nullptr, nullptr, n_batch, chain,
+                     (hipStream_t)stream, nullptr, 1);
 }
 
 int kq4_weights_prepare_host(uint8_t *dst, const uint8_t *w4x4_host, int rows, int cols,
@@ -699,13 +787,13 @@ namespace {
 // The host-pointer matmul: stage x (and up) and the residuals, run on the device, read back.
 int host_matmul(int n_mats, float *const *out, const float *const *residual,
                 const uint8_t *const *w4x4, const int *rows, int cols, const float *x,
-                const float *xu, int n_batch, int chain, const uint64_t *wkeys) {
+                const float *xu, int n_batch, int chain, const uint64_t *wkeys, int g = 0) {
   if (n_mats < 1 || n_mats > KQ4_MAX_MATS || !out || !w4x4 || !rows || !x || n_batch < 1) {
     fail(KQ4_EINVAL, "matmul: n_mats=%d n_batch=%d", n_mats, n_batch);
     return 0;
   }
   for (int i = 0; i < n_mats; ++i)
-    if (!out[i] || !w4x4[i] || !shape_ok(rows[i], cols)) {
+    if (!out[i] || !w4x4[i] || !shape_ok(rows[i], cols) || (g && rows[i] % g)) {
       fail(KQ4_EINVAL, "matmul: rows=%d cols=%d", rows[i], cols);
       return 0;
     }
@@ -723,7 +811,7 @@ int host_matmul(int n_mats, float *const *out, const float *const *residual,
   int rc = KQ4_OK;
   for (int i = 0; i < n_mats && !rc; ++i)
     rc = dev_weights(ds, wkeys ? wkeys[i] : 0, w4x4[i], rows[i], cols,
-                     i == 0 ? ds->hw : tw[i], &dw[i]);
+                     i == 0 ? ds->hw : tw[i], &dw[i], g);
   int ok = 0;
   if (!rc && !ensure(ds->hx, xb) && !ensure(ds->hout, total_o) && !ensure(ds->hres, total_o) &&
       (!xu || !ensure(ds->hu, xb))) {
@@ -745,7 +833,7 @@ int host_matmul(int n_mats, float *const *out, const float *const *residual,
     if (good &&
         matmul_impl(n_mats, dout, dres, dw, rows, cols, static_cast<const float *>(ds->hx.p),
                     nullptr, nullptr, n_batch, chain, nullptr,
-                    xu ? static_cast<const float *>(ds->hu.p) : nullptr) == KQ4_OK) {
+                    xu ? static_cast<const float *>(ds->hu.p) : nullptr, g ? 1 : 0) == KQ4_OK) {
       ok = 1;
       for (int i = 0; i < n_mats && ok; ++i)
         if (hipMemcpy(out[i], dout[i], ob[i], hipMemcpyDeviceToHost) != hipSuccess) {
@@ -776,6 +864,23 @@ int kq4_matmul(float *out, const float *x, const float *residual, const uint8_t 
                int cols, int n_batch, int chain, uint64_t wkey) {
   const float *res[1] = {residual};
   return host_matmul(1, &out, res, &w4x4, &rows, cols, x, nullptr, n_batch, chain, &wkey);
+}
+
+int kq4_q8_matmul_multi(int n_mats, float *const *out, const float *const *residual,
+                        const uint8_t *const *w_tiles, int g, const int *rows, int cols,
+                        const float *x, int n_batch, int chain, const uint64_t *wkeys) {
+  if (g != 8 && g != 4) {
+    fail(KQ4_EINVAL, "q8 matmul: tile rows %d (8 or 4)", g);
+    return 0;
+  }
+  return host_matmul(n_mats, out, residual, w_tiles, rows, cols, x, nullptr, n_batch, chain,
+                     wkeys, g);
+}
+
+int kq4_q8_matmul(float *out, const float *x, const float *residual, const uint8_t *w_tiles,
+                  int g, int rows, int cols, int n_batch, int chain, uint64_t wkey) {
+  const float *res[1] = {residual};
+  return kq4_q8_matmul_multi(1, &out, res, &w_tiles, g, &rows, cols, x, n_batch, chain, &wkey);
 }
 
 int kq4_matmul_silu(float *out, const float *gate, const float *up, const float *residual,

@@ -31,7 +31,7 @@ KQ4_DEV uint32_t kq4_hi16(uint32_t w) { return w & 0xF0F0F0F0u; }
 // vrndnq = round to nearest even, vcvtq_s32 = truncation), so the result is that path's, bit for
 // bit, for finite inputs.
 
-// exp_neon4: clamp to [-87, 87], n = rne(x * log2e), r = x - n*ln2 (fused), degree-7 Taylor
+// exp_neon4: clamp to [-87, 87], n = rne(x * log2e), r = x - n*ln2 (fused), degree-6 Taylor
 // polynomial in Horner form (fused steps), 2^n added to the exponent field.
 KQ4_DEV float kq4_exp_neon(float x) {
   x = fminf(fmaxf(x, -87.0f), 87.0f);
@@ -102,6 +102,25 @@ KQ4_DEV size_t kq4_stream_nib(int row, int b, int h, int nst) {
 KQ4_DEV size_t kq4_stream_scale(int row, int b, int nst) {
   return ((size_t)(row >> 5) * nst + (b >> 4)) * KQ4_STREAM_CHUNK + 8192 +
          16 * ((row & 31) + 32 * ((b & 15) >> 3)) + 2 * (b & 7);
+}
+
+// ---- q8 stream layout (device copy of Q8_0 tiles) -----------------------------------------
+// One 8704-B chunk per (32-row set, 8-block stage), in [set][stage] order; lane l = row + 32*h
+//   * at 1024*i + 16*l, i = 0..7: the 16 int8 codes of elements 16h .. 16h+15 of block i of the
+//     stage, row `row` - in element order, the B operand of v_mfma_i32_32x32x32_i8 as loaded;
+//   * at 8192 + 16*row: the row's 8 f16 scales (blocks 0..7 of the stage).
+// Rows past the matrix and blocks past its K are zero bytes.
+#define KQ8_STREAM_CB 8
+#define KQ8_STREAM_CHUNK 8704
+
+KQ4_DEV size_t kq8_stream_code(int row, int b, int h, int nst) {
+  return ((size_t)(row >> 5) * nst + (b >> 3)) * KQ8_STREAM_CHUNK + 1024 * (b & 7) +
+         16 * ((row & 31) + 32 * h);
+}
+
+KQ4_DEV size_t kq8_stream_scale(int row, int b, int nst) {
+  return ((size_t)(row >> 5) * nst + (b >> 3)) * KQ8_STREAM_CHUNK + 8192 + 16 * (row & 31) +
+         2 * (b & 7);
 }
 
 // The 16*(n-8) int8 operand (4 dwords, element order) of 8 nibble bytes.

@@ -11,6 +11,9 @@
 //   CTILE  lo/hi accumulators fed by two half-K MFMAs, out = fl(lo + hi) (:4180-4216)
 // and out = fl(residual + acc) when fused. The epilogue (convert, scale, fma per output per
 // block) runs on the VALU.
+// With Q8_0 weights (WF = 1, the q8 stream layout) the MFMA result is S itself and the chain is
+//   Q8GEMM acc = fl(acc + fl(fl(wd * f16r(xd)) * S))  (gemm_q8_0_8x8_neon :4973-5050, unfused
+//          vmlaq_f32) or GEMV32 as above (q8x8_dot_rows :5178-5225).
 //
 // Tiling: workgroup = 4 waves = 128 tokens x 128 rows, each wave 64 x 64 (2 x 2 MFMA tiles).
 // Per stage of KB = 4 blocks the workgroup stages into LDS (rows padded to 48 B so the 16-byte
@@ -39,7 +42,7 @@ KQ4_DEV int kq4_mfma_tok(int v, int half) { return 8 * (v >> 2) + 4 * half + (v 
 
 // TM / TN = MFMA token / row tiles per wave: a workgroup covers BM = 64*TM tokens x BN = 64*TN
 // rows (128 x 128, or smaller when the launch would otherwise have fewer than two tiles per CU).
-template <int CHAIN, int TM, int TN>
+template <int CHAIN, int TM, int TN, int WF>
 __global__ __launch_bounds__(256, 2) void kq4_gemm_kernel(
     float *__restrict__ out, const float *__restrict__ res, const uint8_t *__restrict__ w,
     const KQ4GemmAct act, int rows, int n_tok, int nb, int nst, int mtiles, int ntiles) {
@@ -83,9 +86,11 @@ __global__ __launch_bounds__(256, 2) void kq4_gemm_kernel(
   // stream layout: blocks b0 .. b0+3 are nibble units (b0%16)/2 and +1 of the 4 row sets; load
   // (set, unit, lane) = 16 B = the lane's half-row of 2 blocks, unpacked to 16*(n-8) bytes when
   // stored. Row scales (8 B per row, as wd/16) and token scales.
+  // q8: per stage 4 blocks x BN rows x 2 halves of 16 B, 2*TN loads per thread
+  constexpr int NB = WF ? 2 * TN : TN;
   struct Regs {
     uint4 a[KQ4_GEMM_KB];
-    uint4 b[TN];
+    uint4 b[NB];
     uint2 sw;
     float x[KQ4_GEMM_KB * KQ4_GEMM_BM / 256];
   };
@@ -100,17 +105,26 @@ __global__ __launch_bounds__(256, 2) void kq4_gemm_kernel(
                                                    (long)b * act.q_bs + hh * 16);
     }
 #pragma unroll
-    for (int u = 0; u < TN; ++u) {
+    for (int u = 0; u < NB; ++u) {
       const int idx = t + 256 * u;
-      const int ln = idx & 63, iu = (idx >> 6) & 1, sl = idx >> 7;
-      const int rl = 32 * sl + (ln & 31), h = ln >> 5;
-      rg.b[u] = make_uint4(0, 0, 0, 0);          // row sets past the matrix: weight 0
-      if (n0 + 32 * sl < rows)
-        rg.b[u] = *reinterpret_cast<const uint4 *>(w + kq4_stream_nib(n0 + rl, b0 + 2 * iu, h, nst));
+      if (WF) {   // (set sl, block iu of the stage, lane ln): 16 int8 codes
+        const int ln = idx & 63, iu = (idx >> 6) & 3, sl = idx >> 8;
+        const int rl = 32 * sl + (ln & 31), h = ln >> 5;
+        rg.b[u] = make_uint4(0, 0, 0, 0);
+        if (n0 + 32 * sl < rows)
+          rg.b[u] = *reinterpret_cast<const uint4 *>(w + kq8_stream_code(n0 + rl, b0 + iu, h, nst));
+      } else {    // (set sl, nibble unit iu = 2 blocks, lane ln)
+        const int ln = idx & 63, iu = (idx >> 6) & 1, sl = idx >> 7;
+        const int rl = 32 * sl + (ln & 31), h = ln >> 5;
+        rg.b[u] = make_uint4(0, 0, 0, 0);          // row sets past the matrix: weight 0
+        if (n0 + 32 * sl < rows)
+          rg.b[u] = *reinterpret_cast<const uint4 *>(w + kq4_stream_nib(n0 + rl, b0 + 2 * iu, h, nst));
+      }
     }
     rg.sw = make_uint2(0, 0);
     if (t < KQ4_GEMM_BN && n0 + (t & ~31) < rows)
-      rg.sw = *reinterpret_cast<const uint2 *>(w + kq4_stream_scale(n0 + t, b0, nst));
+      rg.sw = *reinterpret_cast<const uint2 *>(
+          w + (WF ? kq8_stream_scale(n0 + t, b0, nst) : kq4_stream_scale(n0 + t, b0, nst)));
 #pragma unroll
     for (int u = 0; u < KQ4_GEMM_KB * KQ4_GEMM_BM / 256; ++u) {
       const int c = t + 256 * u;
@@ -126,29 +140,37 @@ __global__ __launch_bounds__(256, 2) void kq4_gemm_kernel(
       if ((t >> 1) < KQ4_GEMM_BM)
         *reinterpret_cast<uint4 *>(&sA[u][(t >> 1) * KQ4_LDS_ROW + (t & 1) * 16]) = rg.a[u];
 #pragma unroll
-    for (int u = 0; u < TN; ++u) {
+    for (int u = 0; u < NB; ++u) {
       const int idx = t + 256 * u;
-      const int ln = idx & 63, iu = (idx >> 6) & 1, sl = idx >> 7;
-      const int rl = 32 * sl + (ln & 31), h = ln >> 5;
-      uint32_t o[4];
-      kq4_unpack_half(rg.b[u].x, rg.b[u].y, o);
-      *reinterpret_cast<uint4 *>(&sB[2 * iu][rl * KQ4_LDS_ROW + 16 * h]) =
-          make_uint4(o[0], o[1], o[2], o[3]);
-      kq4_unpack_half(rg.b[u].z, rg.b[u].w, o);
-      *reinterpret_cast<uint4 *>(&sB[2 * iu + 1][rl * KQ4_LDS_ROW + 16 * h]) =
-          make_uint4(o[0], o[1], o[2], o[3]);
+      if (WF) {
+        const int ln = idx & 63, iu = (idx >> 6) & 3, sl = idx >> 8;
+        const int rl = 32 * sl + (ln & 31), h = ln >> 5;
+        *reinterpret_cast<uint4 *>(&sB[iu][rl * KQ4_LDS_ROW + 16 * h]) = rg.b[u];
+      } else {
+        const int ln = idx & 63, iu = (idx >> 6) & 1, sl = idx >> 7;
+        const int rl = 32 * sl + (ln & 31), h = ln >> 5;
+        uint32_t o[4];
+        kq4_unpack_half(rg.b[u].x, rg.b[u].y, o);
+        *reinterpret_cast<uint4 *>(&sB[2 * iu][rl * KQ4_LDS_ROW + 16 * h]) =
+            make_uint4(o[0], o[1], o[2], o[3]);
+        kq4_unpack_half(rg.b[u].z, rg.b[u].w, o);
+        *reinterpret_cast<uint4 *>(&sB[2 * iu + 1][rl * KQ4_LDS_ROW + 16 * h]) =
+            make_uint4(o[0], o[1], o[2], o[3]);
+      }
     }
     if (t < KQ4_GEMM_BN) {
-      sW[0][t] = kq4_h2f(rg.sw.x) * 0.0625f;
-      sW[1][t] = kq4_h2f(rg.sw.x >> 16) * 0.0625f;
-      sW[2][t] = kq4_h2f(rg.sw.y) * 0.0625f;
-      sW[3][t] = kq4_h2f(rg.sw.y >> 16) * 0.0625f;
+      constexpr float WS = WF ? 1.0f : 0.0625f;   // q4 enters the MFMA as 16*(n-8)
+      sW[0][t] = kq4_h2f(rg.sw.x) * WS;
+      sW[1][t] = kq4_h2f(rg.sw.x >> 16) * WS;
+      sW[2][t] = kq4_h2f(rg.sw.y) * WS;
+      sW[3][t] = kq4_h2f(rg.sw.y >> 16) * WS;
     }
 #pragma unroll
     for (int u = 0; u < KQ4_GEMM_KB * KQ4_GEMM_BM / 256; ++u) {
       const int c = t + 256 * u;
-      // ASM chain: the reference's asm GEMM multiplies by the f16-rounded activation scale
-      sX[c / KQ4_GEMM_BM][c % KQ4_GEMM_BM] = (CHAIN == KQ4_CHAIN_ASM) ? kq4_f16_round(rg.x[u]) : rg.x[u];
+      // ASM and Q8GEMM chains: the reference multiplies by the f16-rounded activation scale
+      sX[c / KQ4_GEMM_BM][c % KQ4_GEMM_BM] =
+          (CHAIN == KQ4_CHAIN_ASM || CHAIN == KQ4_CHAIN_Q8GEMM) ? kq4_f16_round(rg.x[u]) : rg.x[u];
     }
   };
 
@@ -212,8 +234,12 @@ __global__ __launch_bounds__(256, 2) void kq4_gemm_kernel(
           } else {
             const kq4_v16i c = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[jn], zero, 0, 0, 0);
 #pragma unroll
-            for (int v = 0; v < 16; ++v)
-              acc[i][jn][v] = fmaf((float)c[v], wdv[jn] * xsv[i][v], acc[i][jn][v]);
+            for (int v = 0; v < 16; ++v) {
+              if (CHAIN == KQ4_CHAIN_Q8GEMM)
+                acc[i][jn][v] = acc[i][jn][v] + (wdv[jn] * xsv[i][v]) * (float)c[v];
+              else
+                acc[i][jn][v] = fmaf((float)c[v], wdv[jn] * xsv[i][v], acc[i][jn][v]);
+            }
           }
         }
     }
@@ -241,28 +267,41 @@ __global__ __launch_bounds__(256, 2) void kq4_gemm_kernel(
 template <int TM, int TN>
 static hipError_t gemm_launch(float *out, const float *res, const uint8_t *w,
                               const KQ4GemmAct &act, int rows, int n_tok, int nb, int nst,
-                              int chain, hipStream_t s) {
+                              int chain, int wf, hipStream_t s) {
   const int mtiles = (n_tok + 64 * TM - 1) / (64 * TM);
   const int ntiles = (rows + 64 * TN - 1) / (64 * TN);
   const dim3 grid((unsigned)(mtiles * ntiles));
-  if (chain == KQ4_CHAIN_CTILE)
-    hipLaunchKernelGGL((kq4_gemm_kernel<KQ4_CHAIN_CTILE, TM, TN>), grid, dim3(256), 0, s, out,
+  if (wf) {
+    if (chain == KQ4_CHAIN_GEMV32)
+      hipLaunchKernelGGL((kq4_gemm_kernel<KQ4_CHAIN_GEMV32, TM, TN, 1>), grid, dim3(256), 0, s,
+                         out, res, w, act, rows, n_tok, nb, nst, mtiles, ntiles);
+    else if (chain == KQ4_CHAIN_Q8GEMM)
+      hipLaunchKernelGGL((kq4_gemm_kernel<KQ4_CHAIN_Q8GEMM, TM, TN, 1>), grid, dim3(256), 0, s,
+                         out, res, w, act, rows, n_tok, nb, nst, mtiles, ntiles);
+    else
+      return hipErrorInvalidValue;
+  } else if (chain == KQ4_CHAIN_CTILE) {
+    hipLaunchKernelGGL((kq4_gemm_kernel<KQ4_CHAIN_CTILE, TM, TN, 0>), grid, dim3(256), 0, s, out,
                        res, w, act, rows, n_tok, nb, nst, mtiles, ntiles);
-  else if (chain == KQ4_CHAIN_GEMV32)
-    hipLaunchKernelGGL((kq4_gemm_kernel<KQ4_CHAIN_GEMV32, TM, TN>), grid, dim3(256), 0, s, out,
+  } else if (chain == KQ4_CHAIN_GEMV32) {
+    hipLaunchKernelGGL((kq4_gemm_kernel<KQ4_CHAIN_GEMV32, TM, TN, 0>), grid, dim3(256), 0, s, out,
                        res, w, act, rows, n_tok, nb, nst, mtiles, ntiles);
-  else
-    hipLaunchKernelGGL((kq4_gemm_kernel<KQ4_CHAIN_ASM, TM, TN>), grid, dim3(256), 0, s, out, res,
-                       w, act, rows, n_tok, nb, nst, mtiles, ntiles);
+  } else if (chain == KQ4_CHAIN_ASM) {
+    hipLaunchKernelGGL((kq4_gemm_kernel<KQ4_CHAIN_ASM, TM, TN, 0>), grid, dim3(256), 0, s, out,
+                       res, w, act, rows, n_tok, nb, nst, mtiles, ntiles);
+  } else {
+    return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 
 // The largest of the 128x128, 64x128 and 64x64 (tokens x rows) tiles that gives at least two
 // tiles per CU (else 64x64). KQ4_GEMM_TILE = 1/2/3 forces one (for measurement).
 int kq4_launch_gemm(float *out, const float *res, const uint8_t *w, const KQ4GemmAct &act,
-                    int rows, int cols, int n_tok, int chain, int ncu, hipStream_t s) {
+                    int rows, int cols, int n_tok, int chain, int ncu, hipStream_t s, int wf) {
   const int nb = cols / 32;
-  const int nst = (nb + KQ4_STREAM_CB - 1) / KQ4_STREAM_CB;
+  const int cb = wf ? KQ8_STREAM_CB : KQ4_STREAM_CB;
+  const int nst = (nb + cb - 1) / cb;
   if (n_tok <= 0 || rows <= 0) return 0;
   auto tiles = [&](int bm, int bn) {
     return (long)((n_tok + bm - 1) / bm) * ((rows + bn - 1) / bn);
@@ -271,8 +310,8 @@ int kq4_launch_gemm(float *out, const float *res, const uint8_t *w, const KQ4Gem
   int pick = force >= 1 && force <= 3 ? force
              : tiles(128, 128) >= 2L * ncu ? 1 : (tiles(64, 128) >= 2L * ncu ? 2 : 3);
   hipError_t e;
-  if (pick == 1) e = gemm_launch<2, 2>(out, res, w, act, rows, n_tok, nb, nst, chain, s);
-  else if (pick == 2) e = gemm_launch<1, 2>(out, res, w, act, rows, n_tok, nb, nst, chain, s);
-  else e = gemm_launch<1, 1>(out, res, w, act, rows, n_tok, nb, nst, chain, s);
+  if (pick == 1) e = gemm_launch<2, 2>(out, res, w, act, rows, n_tok, nb, nst, chain, wf, s);
+  else if (pick == 2) e = gemm_launch<1, 2>(out, res, w, act, rows, n_tok, nb, nst, chain, wf, s);
+  else e = gemm_launch<1, 1>(out, res, w, act, rows, n_tok, nb, nst, chain, wf, s);
   return (int)e;
 }

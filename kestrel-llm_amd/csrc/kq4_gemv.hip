@@ -42,6 +42,17 @@
 #define KQ4_GV_QTS 672                // LDS bytes per token row of a stage's int8 codes
 #define KQ4_GV_XS (KQ4_GV_CB * 8 * 4) // LDS bytes of a stage's scales [16 blocks][8 tokens]
 
+// Weight formats: 0 = q4 (kq4 stream layout); 1 = q8 (q8 stream layout) with the fused VDOT
+// chain acc = fma(S, fl(wd*xs), acc); 2 = q8 with the unfused GEMM chain
+// acc = fl(acc + fl(fl(wd*xs) * S)) (xs f16-rounded through asm_tokens).
+template <int WF>
+struct KQ4Wf {
+  static constexpr int CB = WF ? KQ8_STREAM_CB : KQ4_STREAM_CB;          // blocks per stage
+  static constexpr int CHUNK = WF ? KQ8_STREAM_CHUNK : KQ4_STREAM_CHUNK;
+  static constexpr int BPU = WF ? 1 : 2;                                  // blocks per 16-B unit
+  static constexpr float XS = WF ? 1.0f : 0.0625f;  // q4 enters the MFMA as 16*(n-8): undo it
+};
+
 typedef int kq4_v4i __attribute__((ext_vector_type(4)));
 typedef int kq4_v16i __attribute__((ext_vector_type(16)));
 
@@ -77,13 +88,17 @@ struct KQ4GvStage {
 
 // Scales first: the loads complete in issue order, so the first block then waits only for the
 // scales and its own unit, and each later block for one more unit.
-template <int HS>
+// q8 (WF > 0): the same unit loads, one block per unit, and the row's 8 scales in one load.
+template <int HS, int WF>
 KQ4_DEV void kq4_gv_load(KQ4GvStage<HS> &st, const uint8_t *__restrict__ chunk, int rr, int h,
                          int p) {
   const uint4 *sc = reinterpret_cast<const uint4 *>(chunk + 8192) + rr;
-  const uint4 a = sc[0], b = sc[32];
+  const uint4 a = sc[0];
   st.sc[0] = a.x; st.sc[1] = a.y; st.sc[2] = a.z; st.sc[3] = a.w;
-  st.sc[4] = b.x; st.sc[5] = b.y; st.sc[6] = b.z; st.sc[7] = b.w;
+  if (WF == 0) {
+    const uint4 b = sc[32];
+    st.sc[4] = b.x; st.sc[5] = b.y; st.sc[6] = b.z; st.sc[7] = b.w;
+  }
   const uint4 *src = reinterpret_cast<const uint4 *>(chunk) + rr + 32 * h;
 #pragma unroll
   for (int u = 0; u < KQ4GvStage<HS>::NU; ++u) {
@@ -94,8 +109,11 @@ KQ4_DEV void kq4_gv_load(KQ4GvStage<HS> &st, const uint8_t *__restrict__ chunk, 
 }
 
 // Stage block of lane block jb (p = the lane's unit parity in half-set mode).
-template <int HS>
-KQ4_DEV int kq4_gv_blk(int jb, int p) { return HS ? 4 * (jb >> 1) + 2 * p + (jb & 1) : jb; }
+template <int HS, int WF>
+KQ4_DEV int kq4_gv_blk(int jb, int p) {
+  if (WF) return HS ? 2 * jb + p : jb;
+  return HS ? 4 * (jb >> 1) + 2 * p + (jb & 1) : jb;
+}
 
 // a if p == 0, b if p == 1, by masks: a select between two elements of one register array
 // would be folded into a lane-dependent index, which puts the array in scratch memory.
@@ -104,20 +122,33 @@ KQ4_DEV uint32_t kq4_gv_pick(uint32_t a, uint32_t b, int p) {
   return (a & ~m) | (b & m);
 }
 
-// Row scale (f32) of lane block jb; the register index is compile-time in both modes.
-template <int HS>
+// Row scale (f32) of lane block jb; the register index is compile-time in all modes.
+template <int HS, int WF>
 KQ4_DEV float kq4_gv_wd(const KQ4GvStage<HS> &st, int jb, int p) {
+  if (WF) return HS ? kq4_h2f(st.sc[jb] >> (16 * p)) : kq4_h2f(st.sc[jb >> 1] >> (16 * (jb & 1)));
   const uint32_t w = HS ? kq4_gv_pick(st.sc[2 * (jb >> 1)], st.sc[2 * (jb >> 1) + 1], p)
                         : st.sc[jb >> 1];
   return kq4_h2f(w >> (16 * (jb & 1)));
 }
 
+// The MFMA B operand of lane block jb: q4 unpacks its 8 nibble bytes to 16*(n-8); q8 is the
+// 16-B unit as loaded.
+template <int WF>
+KQ4_DEV void kq4_gv_bop(const uint32_t *n, int jb, uint32_t *o) {
+  if (WF) {
+    o[0] = n[4 * jb]; o[1] = n[4 * jb + 1]; o[2] = n[4 * jb + 2]; o[3] = n[4 * jb + 3];
+  } else {
+    kq4_unpack_half(n[2 * jb], n[2 * jb + 1], o);
+  }
+}
+
 // ---- activations of a stage -------------------------------------------------------------------
 // Loaded into registers together with (just before) the stage's weights, then written to the
 // wave's slab as int8 codes (token row m at m*KQ4_GV_QTS, block at kq4_gv_qpos) and the
-// effective per-block scale sx[blk][m] = xs/16 (xs = f16-rounded xd for ASM-chain tokens; the /16
-// undoes the 16*(n-8) weight scaling exactly). Issuing them before the weights keeps the in-order
-// load counter from making the quantization wait for the weights.
+// effective per-block scale sx[blk][m] = xs/16 for q4 (xs = f16-rounded xd for ASM-chain tokens;
+// the /16 undoes the 16*(n-8) weight scaling exactly), xs for q8. A stage is 16 blocks of q4 or 8
+// of q8. Issuing them before the weights keeps the in-order load counter from making the
+// quantization wait for the weights.
 //
 // FQ = 0: pre-quantized; 1: fp32 activations; 2: fp32 gate and up, activation = silu_mul(g, u)
 // (kq4_silu_mul, the dense FFN's down input, vllm_safetensors.c:10932-10958).
@@ -127,25 +158,28 @@ KQ4_DEV float kq4_gv_wd(const KQ4GvStage<HS> &st, int jb, int p) {
 // q += fma(-q, d, x)*y with y = RN(1/d), which is the correctly rounded x/d for these normal
 // operands, so the codes are the reference's bit for bit.
 // Pre-quantized: lane i copies 16-B units i, i+64, .. of the stage's codes and scales i, i+64.
-template <int M, int FQ>
+template <int M, int FQ, int WF>
 struct KQ4GvAct {
-  static constexpr int NQ = FQ ? 1 : (32 * M + 63) / 64;   // uint4 per lane
-  static constexpr int NX = FQ ? 1 : (16 * M + 63) / 64;   // scales per lane
+  static constexpr int CB = KQ4Wf<WF>::CB;
+  static constexpr int NQ = FQ ? 1 : (2 * CB * M + 63) / 64;   // uint4 per lane
+  static constexpr int NX = FQ ? 1 : (CB * M + 63) / 64;       // scales per lane
   float4 f[FQ ? 2 * M : 1];
   float4 u[FQ == 2 ? 2 * M : 1];
   uint4 q[NQ];
   float x[NX];
 };
 
-template <int M, int FQ>
-KQ4_DEV void kq4_gv_act_load(KQ4GvAct<M, FQ> &r, const KQ4GemvArgs &a, int st, int lane) {
+template <int M, int FQ, int WF>
+KQ4_DEV void kq4_gv_act_load(KQ4GvAct<M, FQ, WF> &r, const KQ4GemvArgs &a, int st, int lane) {
+  constexpr int CB = KQ4Wf<WF>::CB;
   const int nb = a.nb, cols = a.cols;
-  const int kb = st * KQ4_GV_CB;
+  const int kb = st * CB;
   if (FQ) {
     const int b = kb + (lane >> 2), qq = lane & 3;
+    const bool live = (lane >> 2) < CB && b < nb;
 #pragma unroll
     for (int m = 0; m < M; ++m) {
-      if (b < nb) {
+      if (live) {
         const float4 *src =
             reinterpret_cast<const float4 *>(a.xf + (size_t)m * cols + (size_t)b * 32 + 8 * qq);
         r.f[2 * m] = src[0];
@@ -167,25 +201,27 @@ KQ4_DEV void kq4_gv_act_load(KQ4GvAct<M, FQ> &r, const KQ4GemvArgs &a, int st, i
     }
   } else {
 #pragma unroll
-    for (int c = 0; c < KQ4GvAct<M, FQ>::NQ; ++c) {
+    for (int c = 0; c < KQ4GvAct<M, FQ, WF>::NQ; ++c) {
       const int i = lane + 64 * c;
-      const int m = i >> 5, u = i & 31, b = kb + (u >> 1), hh = u & 1;
+      const int m = i / (2 * CB), u = i % (2 * CB), b = kb + (u >> 1), hh = u & 1;
       r.q[c] = make_uint4(0, 0, 0, 0);
       if (m < M && b < nb)
         r.q[c] = *reinterpret_cast<const uint4 *>(a.xq + (size_t)m * cols + (size_t)b * 32 + 16 * hh);
     }
 #pragma unroll
-    for (int c = 0; c < KQ4GvAct<M, FQ>::NX; ++c) {
+    for (int c = 0; c < KQ4GvAct<M, FQ, WF>::NX; ++c) {
       const int i = lane + 64 * c;
-      const int m = i >> 4, b = kb + (i & 15);
+      const int m = i / CB, b = kb + i % CB;
       r.x[c] = (m < M && b < nb) ? a.xd[(size_t)m * nb + b] : 0.0f;
     }
   }
 }
 
-template <int M, int FQ>
-KQ4_DEV void kq4_gv_act_put(const KQ4GvAct<M, FQ> &r, const KQ4GemvArgs &a, int lane,
+template <int M, int FQ, int WF>
+KQ4_DEV void kq4_gv_act_put(const KQ4GvAct<M, FQ, WF> &r, const KQ4GemvArgs &a, int lane,
                             uint8_t *sq, float (*sx)[8]) {
+  constexpr int CB = KQ4Wf<WF>::CB;
+  constexpr float XS = KQ4Wf<WF>::XS;
   if (FQ) {
     const int blk = lane >> 2, qq = lane & 3;
 #pragma unroll
@@ -215,22 +251,25 @@ KQ4_DEV void kq4_gv_act_put(const KQ4GvAct<M, FQ> &r, const KQ4GemvArgs &a, int 
         c = c > 127 ? 127 : (c < -127 ? -127 : c);
         pk[i >> 2] |= ((uint32_t)c & 0xFFu) << (8 * (i & 3));
       }
-      *reinterpret_cast<uint2 *>(sq + m * KQ4_GV_QTS + kq4_gv_qpos(blk) + 8 * qq) = make_uint2(pk[0], pk[1]);
-      if (qq == 0) sx[blk][m] = ((m < a.asm_tokens) ? kq4_f16_round(d) : d) * 0.0625f;
+      if (blk < CB) {   // q8 stages have 8 blocks: lanes 32-63 hold nothing
+        *reinterpret_cast<uint2 *>(sq + m * KQ4_GV_QTS + kq4_gv_qpos(blk) + 8 * qq) =
+            make_uint2(pk[0], pk[1]);
+        if (qq == 0) sx[blk][m] = ((m < a.asm_tokens) ? kq4_f16_round(d) : d) * XS;
+      }
     }
   } else {
 #pragma unroll
-    for (int c = 0; c < KQ4GvAct<M, FQ>::NQ; ++c) {
+    for (int c = 0; c < KQ4GvAct<M, FQ, WF>::NQ; ++c) {
       const int i = lane + 64 * c;
-      const int m = i >> 5, u = i & 31;
+      const int m = i / (2 * CB), u = i % (2 * CB);
       if (m < M)
         *reinterpret_cast<uint4 *>(sq + m * KQ4_GV_QTS + kq4_gv_qpos(u >> 1) + 16 * (u & 1)) = r.q[c];
     }
 #pragma unroll
-    for (int c = 0; c < KQ4GvAct<M, FQ>::NX; ++c) {
+    for (int c = 0; c < KQ4GvAct<M, FQ, WF>::NX; ++c) {
       const int i = lane + 64 * c;
-      const int m = i >> 4, blk = i & 15;
-      if (m < M) sx[blk][m] = ((m < a.asm_tokens) ? kq4_f16_round(r.x[c]) : r.x[c]) * 0.0625f;
+      const int m = i / CB, blk = i % CB;
+      if (m < M) sx[blk][m] = ((m < a.asm_tokens) ? kq4_f16_round(r.x[c]) : r.x[c]) * XS;
     }
   }
 }
@@ -248,10 +287,10 @@ KQ4_DEV void kq4_gv_dot4(const KQ4GvStage<HS> &st, const uint8_t *sq, const floa
                          int p, float *acc) {
 #pragma unroll
   for (int jb = 0; jb < 4 * KQ4GvStage<HS>::NU / 2; ++jb) {
-    const int b = kq4_gv_blk<HS>(jb, p);
+    const int b = kq4_gv_blk<HS, 0>(jb, p);
     uint32_t o[4];
     kq4_unpack_half(st.n[2 * jb], st.n[2 * jb + 1], o);
-    const float wd = kq4_gv_wd<HS>(st, jb, p);
+    const float wd = kq4_gv_wd<HS, 0>(st, jb, p);
 #pragma unroll
     for (int m = 0; m < M; ++m) {
       const uint4 q = *reinterpret_cast<const uint4 *>(sq + m * KQ4_GV_QTS + kq4_gv_qpos(b) + 16 * h);
@@ -270,7 +309,7 @@ KQ4_DEV void kq4_gv_dot4(const KQ4GvStage<HS> &st, const uint8_t *sq, const floa
 // the codes of token min(lane%32 (%16 in half-set mode), M-1) for the lane's own block, so output
 // (token row T, column c) is valid where T's block matches c's: full set T = token 0..7, half set
 // T = token + 16p. acc[v] = token 4h+v of the lane's row (and parity).
-template <int M, int HS>
+template <int M, int HS, int WF>
 KQ4_DEV void kq4_gv_mfma_stage(const KQ4GvStage<HS> &st, const uint8_t *sq, const float (*sx)[8],
                                int lane, int p, float *acc) {
   constexpr int VT = M < 4 ? M : 4;
@@ -279,20 +318,21 @@ KQ4_DEV void kq4_gv_mfma_stage(const KQ4GvStage<HS> &st, const uint8_t *sq, cons
   const int t = tr < M ? tr : M - 1;
   const uint8_t *qb = sq + t * KQ4_GV_QTS + 16 * h;
 #pragma unroll
-  for (int jb = 0; jb < 4 * KQ4GvStage<HS>::NU / 2; ++jb) {
-    const int b = kq4_gv_blk<HS>(jb, p);
+  for (int jb = 0; jb < KQ4GvStage<HS>::NU * KQ4Wf<WF>::BPU; ++jb) {
+    const int b = kq4_gv_blk<HS, WF>(jb, p);
     uint32_t o[4];
-    kq4_unpack_half(st.n[2 * jb], st.n[2 * jb + 1], o);
+    kq4_gv_bop<WF>(st.n, jb, o);
     const kq4_v4i B = {(int)o[0], (int)o[1], (int)o[2], (int)o[3]};
     const kq4_v4i A = *reinterpret_cast<const kq4_v4i *>(qb + kq4_gv_qpos(b));
     const kq4_v16i C = kq4_gv_mfma(A, B);
-    const float wd = kq4_gv_wd<HS>(st, jb, p);
+    const float wd = kq4_gv_wd<HS, WF>(st, jb, p);
     const float4 xs = *reinterpret_cast<const float4 *>(&sx[b][4 * h]);
     const float xv[4] = {xs.x, xs.y, xs.z, xs.w};
 #pragma unroll
     for (int v = 0; v < VT; ++v) {
       const int c = HS ? (int)kq4_gv_pick((uint32_t)C[v], (uint32_t)C[8 + v], p) : C[v];
-      acc[v] = fmaf((float)c, wd * xv[v], acc[v]);
+      if (WF == 2) acc[v] = acc[v] + (wd * xv[v]) * (float)c;   // the q8 GEMM chain, unfused
+      else acc[v] = fmaf((float)c, wd * xv[v], acc[v]);
       kq4_gv_pin(acc[v]);
     }
   }
@@ -300,7 +340,7 @@ KQ4_DEV void kq4_gv_mfma_stage(const KQ4GvStage<HS> &st, const uint8_t *sq, cons
 
 // One workgroup per 32-row set (HS = 0) or per half set (HS = 1), up to 16 waves splitting K
 // (every variant fits the 128 VGPRs that allows).
-template <int M, int FQ, int KIND, int HS>
+template <int M, int FQ, int KIND, int HS, int WF>
 __global__ __launch_bounds__(1024) void kq4_gemv_kernel(const KQ4GemvArgs a) {
   extern __shared__ __align__(16) uint8_t kq4_gv_lds[];
   constexpr int SLAB = kq4_gv_slab<M>();
@@ -321,8 +361,9 @@ __global__ __launch_bounds__(1024) void kq4_gemv_kernel(const KQ4GemvArgs a) {
   const int rows = a.mat[mi].rows;
   const int row0 = rs * 32 + hs * 16;              // first output row of the workgroup
   const int nb = a.nb;
-  const int nst = (nb + KQ4_GV_CB - 1) / KQ4_GV_CB;
-  const uint8_t *__restrict__ wset = a.mat[mi].w + (size_t)rs * nst * KQ4_GV_CHUNK;
+  constexpr int CB = KQ4Wf<WF>::CB, CHUNK = KQ4Wf<WF>::CHUNK;
+  const int nst = (nb + CB - 1) / CB;
+  const uint8_t *__restrict__ wset = a.mat[mi].w + (size_t)rs * nst * CHUNK;
   uint8_t *slab = kq4_gv_lds + wave * SLAB;
   uint8_t *sq = slab;
   float (*sx)[8] = reinterpret_cast<float (*)[8]>(sq + M * KQ4_GV_QTS);
@@ -336,13 +377,13 @@ __global__ __launch_bounds__(1024) void kq4_gemv_kernel(const KQ4GemvArgs a) {
   for (int i = 0; i < NACC; ++i) acc[i] = 0.0f;
   for (int st = wave; st < nst; st += nw) {
     // issued as (activations, weights), so quantizing the activations waits only for them
-    KQ4GvAct<M, FQ> ra;
+    KQ4GvAct<M, FQ, WF> ra;
     KQ4GvStage<HS> rw;
-    kq4_gv_act_load<M, FQ>(ra, a, st, lane);
-    kq4_gv_load<HS>(rw, wset + (size_t)st * KQ4_GV_CHUNK, rr, h, p);
-    kq4_gv_act_put<M, FQ>(ra, a, lane, sq, sx);
+    kq4_gv_act_load<M, FQ, WF>(ra, a, st, lane);
+    kq4_gv_load<HS, WF>(rw, wset + (size_t)st * CHUNK, rr, h, p);
+    kq4_gv_act_put<M, FQ, WF>(ra, a, lane, sq, sx);
     if (KIND == 0) kq4_gv_dot4<M, HS>(rw, sq, sx, h, p, acc);
-    else kq4_gv_mfma_stage<M, HS>(rw, sq, sx, lane, p, acc);
+    else kq4_gv_mfma_stage<M, HS, WF>(rw, sq, sx, lane, p, acc);
   }
 
   // this wave's partial sums in its slab: DOT4 red[((h*NP + p)*M + m)*NR + r], MFMA
@@ -381,38 +422,48 @@ __global__ __launch_bounds__(1024) void kq4_gemv_kernel(const KQ4GemvArgs a) {
   }
 }
 
-template <int M, int FQ, int KIND, int HS>
+template <int M, int FQ, int KIND, int HS, int WF>
 static hipError_t gv_launch(const KQ4GemvArgs &a, int nw, int grid, hipStream_t s) {
   const size_t lds = (size_t)nw * kq4_gv_slab<M>();
   static bool attr = false;   // allow more than 64 KB of dynamic LDS, once per variant
   if (!attr) {
     hipError_t e = hipFuncSetAttribute(
-        reinterpret_cast<const void *>(&kq4_gemv_kernel<M, FQ, KIND, HS>),
+        reinterpret_cast<const void *>(&kq4_gemv_kernel<M, FQ, KIND, HS, WF>),
         hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
     if (e != hipSuccess) return e;
     attr = true;
   }
-  hipLaunchKernelGGL((kq4_gemv_kernel<M, FQ, KIND, HS>), dim3(grid), dim3(64 * nw), lds, s, a);
+  hipLaunchKernelGGL((kq4_gemv_kernel<M, FQ, KIND, HS, WF>), dim3(grid), dim3(64 * nw), lds, s,
+                     a);
   return hipGetLastError();
 }
 
 template <int M, int FQ>
 static hipError_t gv_launch_k(const KQ4GemvArgs &a, int kind, int hs, int nw, int grid,
                               hipStream_t s) {
+  if (a.wf == 1)   // q8: the MFMA kind only (its block sums span both K halves)
+    return hs ? gv_launch<M, FQ, 1, 1, 1>(a, nw, grid, s) : gv_launch<M, FQ, 1, 0, 1>(a, nw, grid, s);
+  if (a.wf == 2)
+    return hs ? gv_launch<M, FQ, 1, 1, 2>(a, nw, grid, s) : gv_launch<M, FQ, 1, 0, 2>(a, nw, grid, s);
   if (kind == 0)
-    return hs ? gv_launch<M, FQ, 0, 1>(a, nw, grid, s) : gv_launch<M, FQ, 0, 0>(a, nw, grid, s);
-  return hs ? gv_launch<M, FQ, 1, 1>(a, nw, grid, s) : gv_launch<M, FQ, 1, 0>(a, nw, grid, s);
+    return hs ? gv_launch<M, FQ, 0, 1, 0>(a, nw, grid, s) : gv_launch<M, FQ, 0, 0, 0>(a, nw, grid, s);
+  return hs ? gv_launch<M, FQ, 1, 1, 0>(a, nw, grid, s) : gv_launch<M, FQ, 1, 0, 0>(a, nw, grid, s);
 }
 
-// In-kernel quantization exists for M <= KQ4_GEMV_FQ_MAX_M.
+// In-kernel quantization exists for M <= KQ4_GEMV_FQ_MAX_M (the SiLU form for q4 only).
 template <int M>
 static hipError_t gv_launch_m(const KQ4GemvArgs &a, int kind, int fq, int hs, int nw, int grid,
                               hipStream_t s) {
   constexpr int MF = M <= KQ4_GEMV_FQ_MAX_M ? M : 1;
   if (fq) {
     if (M > KQ4_GEMV_FQ_MAX_M) return hipErrorInvalidValue;
-    return fq == 2 ? gv_launch_k<MF, 2>(a, kind, hs, nw, grid, s)
-                   : gv_launch_k<MF, 1>(a, kind, hs, nw, grid, s);
+    if (fq == 2) {
+      if (a.wf) return hipErrorInvalidValue;
+      if (kind == 0)
+        return hs ? gv_launch<MF, 2, 0, 1, 0>(a, nw, grid, s) : gv_launch<MF, 2, 0, 0, 0>(a, nw, grid, s);
+      return hs ? gv_launch<MF, 2, 1, 1, 0>(a, nw, grid, s) : gv_launch<MF, 2, 1, 0, 0>(a, nw, grid, s);
+    }
+    return gv_launch_k<MF, 1>(a, kind, hs, nw, grid, s);
   }
   return gv_launch_k<M, 0>(a, kind, hs, nw, grid, s);
 }
@@ -507,6 +558,71 @@ int kq4_launch_repack(uint8_t *dst, const uint8_t *src, int rows, int cols, hipS
   if (total <= 0) return 0;
   hipLaunchKernelGGL(kq4_repack_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
                      dst, src, rows, nb, nst, total);
+  return (int)hipGetLastError();
+}
+
+// ---- tiled Q8_0 -> q8 stream layout ---------------------------------------------------------------
+// One thread per 16-byte piece of the stream buffer. The source is the reference's tiled Q8_0
+// (g = 8: block_q8_0x8, 272 B per 8 rows x 32 cols; g = 4: block_q8_0x4, 136 B): g f16 row scales,
+// then qs[k*4g + m*4 + i] = row m's element 4k+i. Piece o (byte offset in its chunk):
+//   o < 8192: block i = o/1024 of the stage, lane l = (o/16)%64: row 32*set + l%32, half h = l/32,
+//             i.e. the 4 dwords k = 4h .. 4h+3 of that row in the tile;
+//   o >= 8192: row 32*set + (o-8192)/16: its 8 scales (blocks 8*stage + 0..7).
+// Rows or blocks past the matrix give zeros.
+__global__ __launch_bounds__(256) void kq8_repack_kernel(uint8_t *__restrict__ dst,
+                                                         const uint8_t *__restrict__ src, int g,
+                                                         int rows, int nb, int nst, long total) {
+  const long k = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (k >= total) return;
+  const long chunk = k / (KQ8_STREAM_CHUNK / 16);
+  const int o = 16 * (int)(k - chunk * (KQ8_STREAM_CHUNK / 16));
+  const int set = (int)(chunk / nst), stage = (int)(chunk - (long)set * nst);
+  const size_t tb = (size_t)34 * g;   // bytes per tile
+  uint4 v = make_uint4(0, 0, 0, 0);
+  if (o < 8192) {
+    const int i = o >> 10, l = (o >> 4) & 63;
+    const int row = 32 * set + (l & 31), h = l >> 5;
+    const int b = KQ8_STREAM_CB * stage + i;
+    if (row < rows && b < nb) {
+      const uint8_t *q = src + ((size_t)(row / g) * nb + b) * tb + 2 * g + 4 * (row % g);
+      v.x = *reinterpret_cast<const uint32_t *>(q + (4 * h + 0) * 4 * g);
+      v.y = *reinterpret_cast<const uint32_t *>(q + (4 * h + 1) * 4 * g);
+      v.z = *reinterpret_cast<const uint32_t *>(q + (4 * h + 2) * 4 * g);
+      v.w = *reinterpret_cast<const uint32_t *>(q + (4 * h + 3) * 4 * g);
+    }
+  } else {
+    const int row = 32 * set + ((o - 8192) >> 4);
+    uint32_t f[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    if (row < rows) {
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int b = KQ8_STREAM_CB * stage + u;
+        if (b < nb)
+          f[u] = *reinterpret_cast<const uint16_t *>(src + ((size_t)(row / g) * nb + b) * tb +
+                                                     2 * (row % g));
+      }
+    }
+    v = make_uint4(f[0] | (f[1] << 16), f[2] | (f[3] << 16), f[4] | (f[5] << 16),
+                   f[6] | (f[7] << 16));
+  }
+  *reinterpret_cast<uint4 *>(dst + chunk * KQ8_STREAM_CHUNK + o) = v;
+}
+
+size_t kq8_stream_bytes(int rows, int cols) {
+  const size_t sets = ((size_t)rows + 31) / 32;
+  const size_t nst = ((size_t)cols / 32 + KQ8_STREAM_CB - 1) / KQ8_STREAM_CB;
+  return sets * nst * KQ8_STREAM_CHUNK;
+}
+
+int kq8_launch_repack(uint8_t *dst, const uint8_t *src, int g, int rows, int cols,
+                      hipStream_t s) {
+  const int nb = cols / 32;
+  const int nst = (nb + KQ8_STREAM_CB - 1) / KQ8_STREAM_CB;
+  const long total = (long)kq8_stream_bytes(rows, cols) / 16;
+  if (total <= 0) return 0;
+  if (g != 8 && g != 4) return (int)hipErrorInvalidValue;
+  hipLaunchKernelGGL(kq8_repack_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
+                     dst, src, g, rows, nb, nst, total);
   return (int)hipGetLastError();
 }
 

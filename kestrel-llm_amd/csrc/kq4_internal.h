@@ -12,6 +12,11 @@
 // once by kq4_launch_repack into kq4_stream_bytes(rows, cols) bytes.
 size_t kq4_stream_bytes(int rows, int cols);
 int kq4_launch_repack(uint8_t *dst, const uint8_t *src, int rows, int cols, hipStream_t stream);
+// Q8_0 weights: the reference's tiles (g = 8 rows: block_q8_0x8, 4: block_q8_0x4) repacked into
+// the q8 stream layout (kq4_common.h), kq8_stream_bytes(rows, cols) bytes.
+size_t kq8_stream_bytes(int rows, int cols);
+int kq8_launch_repack(uint8_t *dst, const uint8_t *src, int g, int rows, int cols,
+                      hipStream_t stream);
 
 // One weight matrix of a (possibly fused) GEMV launch. All matrices share the activation.
 struct KQ4GemvMat {
@@ -30,6 +35,8 @@ struct KQ4GemvArgs {
   const int8_t *xq;     // [M][cols] (pre-quantized path)
   const float *xd;      // [M][nb] activation scales (pre-quantized path)
   int asm_tokens;       // tokens [0, asm_tokens) multiply by f32(f16_rne(xd)) (ASM chain)
+  int wf;               // weights: 0 q4 (kq4 stream layout); q8 (q8 stream layout) with the
+                        // 1 fused VDOT or 2 unfused GEMM chain
   int cols;
   int nb;
 };
@@ -67,8 +74,10 @@ struct KQ4GemmAct {
   const float *xd;
   long d_ts, d_bs;
 };
+// wf = 1: Q8_0 weights in the q8 stream layout, chain KQ4_CHAIN_Q8GEMM or KQ4_CHAIN_GEMV32.
 int kq4_launch_gemm(float *out, const float *res, const uint8_t *w, const KQ4GemmAct &act,
-                    int rows, int cols, int n_tok, int chain, int ncu, hipStream_t stream);
+                    int rows, int cols, int n_tok, int chain, int ncu, hipStream_t stream,
+                    int wf = 0);
 
 // MoE
 int kq4_launch_moe_route(int *sel, float *pr, const float *logits, int T, int ne, int tk,

@@ -4,6 +4,7 @@
 
 #include <math.h>
 #include <stdlib.h>
+#include <string.h>
 
 #include "kq4.h"
 
@@ -58,6 +59,72 @@ int kq4_silu_mul_down_residual_batched(float *x_batch, const float *residual_bat
                                        int n_batch) {
     return kq4_matmul_silu(x_batch, gate_batch, up_batch, residual_batch, q4_down, hidden_dim,
                            ffn_dim, n_batch, KQ4_CHAIN_AUTO, key_of(q4_down));
+}
+
+/* Tile rows of the reference's Q8_0 repack for a matrix of `rows` rows (q8_8x8_enabled
+ * vllm_safetensors.c:3971-3979 and the rows % 8 gate of q8_vdot_dispatch :5283-5290). */
+static int q8_tile_rows(int rows) {
+    const char *e = getenv("VLLM_Q8_8X8");
+    const int on = !(e && e[0] == '0');
+    return (on && rows % 8 == 0) ? 8 : 4;
+}
+
+int kq4_dyn_matvec_q8(float *out, const uint8_t *q8_w, const float *x, int rows, int cols) {
+    return kq4_q8_matmul(out, x, NULL, q8_w, q8_tile_rows(rows), rows, cols, 1, KQ4_CHAIN_AUTO,
+                         key_of(q8_w));
+}
+
+int kq4_dyn_matvec_q8_fused_qkv_batched(float *q_out, float *k_out, float *v_out,
+                                        const uint8_t *q8_q, const uint8_t *q8_k,
+                                        const uint8_t *q8_v, const float *x_batch, int q_rows,
+                                        int kv_rows, int cols, int n_batch) {
+    /* one tile layout per call: the q and kv matrices share it when both row counts allow */
+    const int g = (q8_tile_rows(q_rows) == 8 && q8_tile_rows(kv_rows) == 8) ? 8 : 4;
+    float *out[3] = {q_out, k_out, v_out};
+    const uint8_t *w[3] = {q8_q, q8_k, q8_v};
+    const int r[3] = {q_rows, kv_rows, kv_rows};
+    const uint64_t k[3] = {key_of(q8_q), key_of(q8_k), key_of(q8_v)};
+    return kq4_q8_matmul_multi(3, out, NULL, w, g, r, cols, x_batch, n_batch, KQ4_CHAIN_AUTO, k);
+}
+
+int kq4_dyn_matvec_q8_fused_o_residual_batched(float *x_batch, const float *residual_batch,
+                                               const uint8_t *q8_o, const float *attn_batch,
+                                               int rows, int cols, int n_batch) {
+    return kq4_q8_matmul(x_batch, attn_batch, residual_batch, q8_o, q8_tile_rows(rows), rows,
+                         cols, n_batch, KQ4_CHAIN_AUTO, key_of(q8_o));
+}
+
+int kq4_dyn_matvec_q8_fused_gate_up_batched(float *gate_out, float *up_out,
+                                            const uint8_t *q8_gate, const uint8_t *q8_up,
+                                            const float *x_batch, int rows, int cols,
+                                            int n_batch) {
+    float *out[2] = {gate_out, up_out};
+    const uint8_t *w[2] = {q8_gate, q8_up};
+    const int r[2] = {rows, rows};
+    const uint64_t k[2] = {key_of(q8_gate), key_of(q8_up)};
+    return kq4_q8_matmul_multi(2, out, NULL, w, q8_tile_rows(rows), r, cols, x_batch, n_batch,
+                               KQ4_CHAIN_AUTO, k);
+}
+
+int kq4_dyn_matvec_q8_fused_down_residual_batched(float *x_batch, const float *residual_batch,
+                                                  const uint8_t *q8_down,
+                                                  const float *activated_batch, int hidden_dim,
+                                                  int ffn_dim, int n_batch) {
+    return kq4_q8_matmul(x_batch, activated_batch, residual_batch, q8_down,
+                         q8_tile_rows(hidden_dim), hidden_dim, ffn_dim, n_batch, KQ4_CHAIN_AUTO,
+                         key_of(q8_down));
+}
+
+int kq4_dyn_matvec_q8_fused_o_residual(float *x, const float *residual, const uint8_t *q8_o,
+                                       const float *attn_in, int rows, int cols) {
+    return kq4_dyn_matvec_q8_fused_o_residual_batched(x, residual, q8_o, attn_in, rows, cols, 1);
+}
+
+int kq4_dyn_matvec_q8_fused_down_residual(float *x, const float *residual,
+                                          const uint8_t *q8_down, const float *activated,
+                                          int hidden_dim, int ffn_dim) {
+    return kq4_dyn_matvec_q8_fused_down_residual_batched(x, residual, q8_down, activated,
+                                                         hidden_dim, ffn_dim, 1);
 }
 
 int kq4_dyn_matvec_q4_q8_fused_qkv_batched(float *q_out, float *k_out, float *v_out,

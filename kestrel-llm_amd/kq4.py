@@ -13,7 +13,7 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libkq4.so")
 
-CHAIN_AUTO, CHAIN_CTILE, CHAIN_GEMV32, CHAIN_ASM = 0, 1, 2, 3
+CHAIN_AUTO, CHAIN_CTILE, CHAIN_GEMV32, CHAIN_ASM, CHAIN_Q8GEMM = 0, 1, 2, 3, 4
 MAX_MATS = 4
 
 _P = ctypes.c_void_p
@@ -32,6 +32,13 @@ SIGNATURES = [
     ("kq4_matmul", _I, [_P, _P, _P, _P, _I, _I, _I, _I, _U64]),
     ("kq4_matmul_multi", _I, [_I, _P, _P, _P, _P, _I, _P, _I, _I, _P]),
     ("kq4_matmul_silu", _I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _U64]),
+    ("kq4_q8_matmul", _I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _U64]),
+    ("kq4_q8_matmul_multi", _I, [_I, _P, _P, _P, _I, _P, _I, _P, _I, _I, _P]),
+    ("kq4_q8_weights_stream_bytes", ctypes.c_size_t, [_I, _I]),
+    ("kq4_q8_weights_prepare_dev", _I, [_P, _P, _I, _I, _I, _P]),
+    ("kq4_q8_weights_prepare_host", _I, [_P, _P, _I, _I, _I, _P]),
+    ("kq4_q8_matmul_dev", _I, [_P, _P, _P, _P, _I, _I, _I, _I, _P]),
+    ("kq4_q8_matmul_multi_dev", _I, [_I, _P, _P, _P, _P, _I, _P, _I, _I, _P]),
     ("kq4_moe_ffn", _I, [_P, _P, _P, _P, _I, _I, _P, _P, _P, _I, _I, _I, _U64]),
     ("kq4_weights_stream_bytes", ctypes.c_size_t, [_I, _I]),
     ("kq4_weights_prepare_dev", _I, [_P, _P, _I, _I, _P]),
@@ -66,6 +73,13 @@ SIGNATURES = [
     ("kq4_dyn_matvec_q4_q8_fused_gate_up_batched", _I,
      [_P, _P, _P, _P, _P, _I, _I, _I, _P, _P]),
     ("kq4_dyn_matvec_q4_q8_fused_down_residual_batched", _I, [_P, _P, _P, _P, _I, _I, _I, _P]),
+    ("kq4_dyn_matvec_q8", _I, [_P, _P, _P, _I, _I]),
+    ("kq4_dyn_matvec_q8_fused_qkv_batched", _I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I]),
+    ("kq4_dyn_matvec_q8_fused_o_residual_batched", _I, [_P, _P, _P, _P, _I, _I, _I]),
+    ("kq4_dyn_matvec_q8_fused_gate_up_batched", _I, [_P, _P, _P, _P, _P, _I, _I, _I]),
+    ("kq4_dyn_matvec_q8_fused_down_residual_batched", _I, [_P, _P, _P, _P, _I, _I, _I]),
+    ("kq4_dyn_matvec_q8_fused_o_residual", _I, [_P, _P, _P, _P, _I, _I]),
+    ("kq4_dyn_matvec_q8_fused_down_residual", _I, [_P, _P, _P, _P, _I, _I]),
     ("kq4_st_moe_ffn_sparse_q4", _I, [_P, _P, _P]),
     ("kq4_st_moe_ffn_sparse_q4_batch", _I, [_P, _I, _P, _P]),
     # include/kq4_vqf.h
@@ -190,6 +204,17 @@ def matmul_silu(w, gate, up, rows, cols, residual=None, chain=CHAIN_AUTO, wkey=0
     return out
 
 
+def q8_matmul(w, x, rows, cols, residual=None, chain=CHAIN_AUTO, wkey=0, g=8):
+    """out = [residual +] W.x for Q8_0 tiles of g rows through kq4_q8_matmul (host pointers)."""
+    x = _c(x, np.float32).reshape(-1, cols)
+    out = np.empty((x.shape[0], rows), np.float32)
+    res = None if residual is None else _c(residual, np.float32).reshape(x.shape[0], rows)
+    check_done(lib().kq4_q8_matmul(_np_ptr(out), _np_ptr(x), _np_ptr(res),
+                                   _np_ptr(_c(w, np.uint8)), g, rows, cols, x.shape[0], chain,
+                                   wkey), "kq4_q8_matmul")
+    return out
+
+
 def matmul_multi(ws, rows, x, cols, residuals=None, chain=CHAIN_AUTO, wkeys=None):
     x = _c(x, np.float32).reshape(-1, cols)
     n = x.shape[0]
@@ -247,6 +272,44 @@ def prepare_dev(w4x4, rows, cols, stream=None):
     check(lib().kq4_weights_prepare_dev(_tp(dst), _tp(w4x4), rows, cols, _stream_ptr(stream)),
           "kq4_weights_prepare_dev")
     return dst
+
+
+def q8_stream_bytes(rows, cols):
+    n = lib().kq4_q8_weights_stream_bytes(rows, cols)
+    if n == 0:
+        raise KQ4Error(f"bad q8 matrix shape {rows}x{cols}")
+    return n
+
+
+def q8_prepare_dev(tiles, rows, cols, g=8, stream=None):
+    """q8 stream-layout device copy (a new uint8 tensor) of Q8_0 tiles of g rows (a device
+    tensor, or a host numpy array)."""
+    import torch
+    dst = torch.empty(q8_stream_bytes(rows, cols), dtype=torch.uint8, device="cuda")
+    if isinstance(tiles, np.ndarray):
+        t = np.ascontiguousarray(tiles, dtype=np.uint8)
+        check(lib().kq4_q8_weights_prepare_host(_tp(dst), t.ctypes.data, g, rows, cols,
+                                                _stream_ptr(stream)), "kq4_q8_weights_prepare_host")
+    else:
+        check(lib().kq4_q8_weights_prepare_dev(_tp(dst), _tp(tiles), g, rows, cols,
+                                               _stream_ptr(stream)), "kq4_q8_weights_prepare_dev")
+    return dst
+
+
+def q8_matmul_dev(out, x, w, rows, cols, residual=None, chain=CHAIN_AUTO, stream=None):
+    n = x.shape[0]
+    check(lib().kq4_q8_matmul_dev(_tp(out), _tp(x), _tp(residual), _tp(w), rows, cols, n, chain,
+                                  _stream_ptr(stream)), "kq4_q8_matmul_dev")
+
+
+def q8_matmul_multi_dev(outs, x, ws, rows, cols, residuals=None, chain=CHAIN_AUTO, stream=None):
+    n = x.shape[0]
+    res = [None] * len(ws) if residuals is None else residuals
+    check(lib().kq4_q8_matmul_multi_dev(len(ws), _ptr_array([_tp(o) for o in outs]),
+                                        _ptr_array([_tp(r) for r in res]),
+                                        _ptr_array([_tp(w) for w in ws]),
+                                        (ctypes.c_int * len(rows))(*rows), cols, _tp(x), n,
+                                        chain, _stream_ptr(stream)), "kq4_q8_matmul_multi_dev")
 
 
 def quantize_dev(x, xq, xd, xde=None, chain=CHAIN_AUTO, stream=None):
