@@ -308,6 +308,38 @@ def run_extras():
     out["qwen3_8b_prefill"] = pre
     del G, U, D, Q
     torch.cuda.empty_cache()
+    # the same shapes with Q8_0 weights (8x8 tiles), the reference's prefill format of dual VQF
+    # files: prefill GEMM and the decode GEMV
+    def q8_copies(rows, cols, seed):
+        t = kq4.q8_prepare_dev(synth.make_q8_weights(rows, cols, seed), rows, cols)
+        n = max(2, int(ROTATE_BYTES // t.numel()) + 1)
+        return [t] + [t.clone() for _ in range(n - 1)]
+    G8, D8 = q8_copies(f, h, 15), q8_copies(h, f, 16)
+    q8 = {}
+    for m in (1, 4, 512, 2048):
+        x = torch.from_numpy(synth.make_activations(m, h, 70 + m)).cuda()
+        xf = torch.from_numpy(synth.make_activations(m, f, 71 + m)).cuda()
+        og = torch.empty((m, f), device="cuda")
+        od = torch.empty((m, h), device="cuda")
+        n, reps = (len(G8), 5) if m <= 8 else (4, 2)
+        t_g = _time_graph(torch, lambda i, st: kq4.q8_matmul_dev(og, x, G8[i], f, h, stream=st),
+                          n, reps=reps)
+        t_d = _time_graph(torch, lambda i, st: kq4.q8_matmul_dev(od, xf, D8[i], h, f, stream=st),
+                          n, reps=reps)
+        if m <= 8:
+            b_w = f * h * 34 // 32
+            q8[f"M{m}"] = {"gate_us": round(t_g, 2),
+                           "gate_GBs": round((b_w + m * h * 4 + m * f * 4) / t_g / 1e3, 1),
+                           "down_us": round(t_d, 2),
+                           "down_GBs": round((b_w + m * f * 4 + m * h * 4) / t_d / 1e3, 1)}
+        else:
+            ops = 2.0 * m * f * h
+            q8[f"M{m}"] = {"gate_us": round(t_g, 1), "gate_TOPS": round(ops / t_g / 1e6, 1),
+                           "down_us": round(t_d, 1), "down_TOPS": round(ops / t_d / 1e6, 1),
+                           "frac_int8_peak": round(ops / min(t_g, t_d) / 1e6 / 5000.0, 4)}
+    out["qwen3_8b_q8_0"] = q8
+    del G8, D8
+    torch.cuda.empty_cache()
     mcfg = synth.QWEN3_30B_A3B_MOE
     d, ne, tk, ef = mcfg["hidden"], mcfg["experts"], mcfg["top_k"], mcfg["ef"]
     Gm, Um, Dm = synth.make_moe(mcfg, 50)

@@ -1,13 +1,14 @@
 /* kq4_vqf.h - VQF model files as libkq4 reads them: mmap, header and directory validation, and
- * each layer's q4 weight matrix uploaded to HBM (in the stream layout the kernels read).
+ * each layer's q4 / q8 weight matrix uploaded to HBM (in the stream layouts the kernels read).
  *
- * Restates the part of kestrel-llm's VQF loader the q4 matmul needs (src/model/vqf.c vqf_load
+ * Restates the part of kestrel-llm's VQF loader the matmul needs (src/model/vqf.c vqf_load
  * :222-560, format include/model/vqf_format.h): the 448-byte header (or the legacy 432-byte one,
  * told apart by which (data_offset, file_len) pair is consistent with the file size,
  * vqf_header_normalize :160-220), the 64-byte directory entries after it, the FNV-1a checksum
- * trailer of plaintext files (:470-490), and the layout flag VQF_FLAG_Q4_4X4 the q4 tensors must
- * carry. Per-layer matrices are stacked as the reference stacks them: layer l of a tensor starts
- * at Q4_BYTES(l * N * K) (vllm_safetensors.c:2338, :16426). Encrypted files (VQF_FLAG_ENC,
+ * trailer of plaintext files (:470-490), and the layout flags VQF_FLAG_Q4_4X4 (q4 tensors) and
+ * VQF_FLAG_Q8_8X8 (q8 tensors). Per-layer matrices are stacked as the reference stacks them:
+ * layer l of a tensor starts at Q4_BYTES(l * N * K) / Q8_BYTES(l * N * K)
+ * (vllm_safetensors.c:2338, :16426). Encrypted files (VQF_FLAG_ENC,
  * SM4-CTR) are refused; signatures (VQF_FLAG_SIGNED) are not verified - both belong to the
  * reference's supply-chain layer, not to the matmul.
  *
@@ -77,15 +78,26 @@ int kq4_vqf_find(const kq4_vqf *v, const char *name, const uint8_t **data, uint6
 int kq4_vqf_q4_matrix(const kq4_vqf *v, int proj, int layer, const uint8_t **w4x4, int *rows,
                       int *cols);
 
-/* That matrix's stream-layout copy written to dst (device memory,
+/* The q4 matrix's stream-layout copy written to dst (device memory,
  * kq4_weights_stream_bytes(rows, cols) bytes, 16-byte aligned): what every kq4_*_dev call
  * takes as weights. Synchronous with respect to the host bytes. */
 int kq4_vqf_prepare_dev(const kq4_vqf *v, int proj, int layer, uint8_t *dst, void *stream);
 
-/* Uploads that matrix into the host-pointer API's weight cache under the reference's key
+/* Uploads the q4 matrix into the host-pointer API's weight cache under the reference's key
  * wkey = layer << 32 | proj (st_npu_gw_get vllm_safetensors.c:2780-2800); returns 0 or
  * KQ4_E*. */
 int kq4_vqf_upload(const kq4_vqf *v, int proj, int layer, uint64_t *wkey_out);
+
+/* Layer `layer` of the Q8_0 matrix of projection proj (tensors q8_q .. q8_lm of dual / q8 VQF
+ * files, stacked at Q8_BYTES(l * N * K), vqf.c:930): its tiles and shape as above, and g, the
+ * tile rows: 8 (block_q8_0x8) when the file carries VQF_FLAG_Q8_8X8, else 4 (block_q8_0x4, the
+ * reference's other repacked layout). */
+int kq4_vqf_q8_matrix(const kq4_vqf *v, int proj, int layer, const uint8_t **w_tiles, int *rows,
+                      int *cols, int *g);
+
+/* The q8 matrix's stream-layout copy written to dst (kq4_q8_weights_stream_bytes(rows, cols)
+ * bytes, 16-byte aligned): what the kq4_q8_*_dev calls take as weights. */
+int kq4_vqf_prepare_q8_dev(const kq4_vqf *v, int proj, int layer, uint8_t *dst, void *stream);
 
 #ifdef __cplusplus
 }

@@ -216,17 +216,18 @@ int kq4_vqf_find(const kq4_vqf *v, const char *name, const uint8_t **data, uint6
 
 static const char *const q4_names[8] = {"q4_q", "q4_k", "q4_v", "q4_o",
                                         "q4_gate", "q4_up", "q4_down", "q4_lm"};
+static const char *const q8_names[8] = {"q8_q", "q8_k", "q8_v", "q8_o",
+                                        "q8_gate", "q8_up", "q8_down", "q8_lm"};
 
-int kq4_vqf_q4_matrix(const kq4_vqf *v, int proj, int layer, const uint8_t **w4x4, int *rows,
-                      int *cols) {
+/* Layer `layer` of projection proj: N x K from the arch, the tensor's bytes at
+ * layer * N*K/32*bpb (bpb = 18 for Q4_0, 34 for Q8_0). */
+static int layer_matrix(const kq4_vqf *v, const char *const *names, uint64_t bpb, int proj,
+                        int layer, const uint8_t **w, int *rows, int *cols) {
     if (!v || proj < KQ4_PROJ_Q || proj > KQ4_PROJ_LM)
         return kq4_fail(KQ4_EINVAL, "vqf: projection %d", proj);
     const kq4_vqf_info *a = &v->info;
     if (layer < 0 || (proj == KQ4_PROJ_LM ? layer != 0 : (uint32_t)layer >= a->n_layers))
         return kq4_fail(KQ4_EINVAL, "vqf: layer %d of %u", layer, a->n_layers);
-    if (!(a->flags & KQ4_VQF_FLAG_Q4_4X4))
-        return kq4_fail(KQ4_EIO, "vqf: q4 tensors not in the 4x4 tile layout (flags 0x%x)",
-                        a->flags);
     const uint64_t q_out = (uint64_t)a->n_heads * a->head_dim;
     const uint64_t kv_out = (uint64_t)a->n_kv_heads * a->head_dim;
     uint64_t n = 0, k = 0;
@@ -240,20 +241,51 @@ int kq4_vqf_q4_matrix(const kq4_vqf *v, int proj, int layer, const uint8_t **w4x
     }
     if (n == 0 || n % 4 || k == 0 || k % 32 || n > 0x7fffffff || k > 0x7fffffff)
         return kq4_fail(KQ4_EIO, "vqf: %s is %llux%llu (need rows %% 4 == 0, cols %% 32 == 0)",
-                        q4_names[proj], (unsigned long long)n, (unsigned long long)k);
+                        names[proj], (unsigned long long)n, (unsigned long long)k);
     const uint8_t *data;
     uint64_t bytes;
-    int rc = kq4_vqf_find(v, q4_names[proj], &data, &bytes);
+    int rc = kq4_vqf_find(v, names[proj], &data, &bytes);
     if (rc) return rc;
-    const uint64_t per = n * k / 32 * 18;   /* Q4_BYTES(N*K): layer l at l * per */
+    const uint64_t per = n * k / 32 * bpb;   /* Q4_BYTES / Q8_BYTES (N*K): layer l at l * per */
     if ((uint64_t)(layer + 1) * per > bytes)
         return kq4_fail(KQ4_EIO, "vqf: %s holds %llu bytes, layer %d needs %llu",
-                        q4_names[proj], (unsigned long long)bytes, layer,
+                        names[proj], (unsigned long long)bytes, layer,
                         (unsigned long long)((uint64_t)(layer + 1) * per));
-    if (w4x4) *w4x4 = data + (uint64_t)layer * per;
+    if (w) *w = data + (uint64_t)layer * per;
     if (rows) *rows = (int)n;
     if (cols) *cols = (int)k;
     return KQ4_OK;
+}
+
+int kq4_vqf_q4_matrix(const kq4_vqf *v, int proj, int layer, const uint8_t **w4x4, int *rows,
+                      int *cols) {
+    if (v && !(v->info.flags & KQ4_VQF_FLAG_Q4_4X4))
+        return kq4_fail(KQ4_EIO, "vqf: q4 tensors not in the 4x4 tile layout (flags 0x%x)",
+                        v->info.flags);
+    return layer_matrix(v, q4_names, 18, proj, layer, w4x4, rows, cols);
+}
+
+int kq4_vqf_q8_matrix(const kq4_vqf *v, int proj, int layer, const uint8_t **w_tiles, int *rows,
+                      int *cols, int *g) {
+    int r = 0, c = 0;
+    int rc = layer_matrix(v, q8_names, 34, proj, layer, w_tiles, &r, &c);
+    if (rc) return rc;
+    const int gg = (v->info.flags & KQ4_VQF_FLAG_Q8_8X8) ? 8 : 4;
+    if (r % gg)
+        return kq4_fail(KQ4_EIO, "vqf: %s has %d rows, not whole %d-row tiles", q8_names[proj], r,
+                        gg);
+    if (rows) *rows = r;
+    if (cols) *cols = c;
+    if (g) *g = gg;
+    return KQ4_OK;
+}
+
+int kq4_vqf_prepare_q8_dev(const kq4_vqf *v, int proj, int layer, uint8_t *dst, void *stream) {
+    const uint8_t *w;
+    int rows, cols, g;
+    int rc = kq4_vqf_q8_matrix(v, proj, layer, &w, &rows, &cols, &g);
+    if (rc) return rc;
+    return kq4_q8_weights_prepare_host(dst, w, g, rows, cols, stream);
 }
 
 int kq4_vqf_prepare_dev(const kq4_vqf *v, int proj, int layer, uint8_t *dst, void *stream) {

@@ -95,6 +95,9 @@ SIGNATURES = [
     ("kq4_vqf_q4_matrix", _I, [_P, _I, _I, ctypes.POINTER(_P), ctypes.POINTER(_I),
                                ctypes.POINTER(_I)]),
     ("kq4_vqf_prepare_dev", _I, [_P, _I, _I, _P, _P]),
+    ("kq4_vqf_q8_matrix", _I, [_P, _I, _I, ctypes.POINTER(_P), ctypes.POINTER(_I),
+                               ctypes.POINTER(_I), ctypes.POINTER(_I)]),
+    ("kq4_vqf_prepare_q8_dev", _I, [_P, _I, _I, _P, _P]),
     ("kq4_vqf_upload", _I, [_P, _I, _I, ctypes.POINTER(_U64)]),
 ]
 
@@ -473,6 +476,24 @@ class Vqf:
         n = r.value // 4 * (c.value // 32) * 72
         arr = np.ctypeslib.as_array(ctypes.cast(data, ctypes.POINTER(ctypes.c_uint8)), (n,))
         return arr, r.value, c.value
+
+    def q8_matrix(self, proj, layer):
+        """(numpy view of the layer's Q8_0 tile bytes, rows, cols, tile rows g)."""
+        data, r, c, g = _P(), _I(), _I(), _I()
+        check(lib().kq4_vqf_q8_matrix(self._h, proj, layer, ctypes.byref(data), ctypes.byref(r),
+                                      ctypes.byref(c), ctypes.byref(g)), "kq4_vqf_q8_matrix")
+        n = r.value * (c.value // 32) * 34
+        arr = np.ctypeslib.as_array(ctypes.cast(data, ctypes.POINTER(ctypes.c_uint8)), (n,))
+        return arr, r.value, c.value, g.value
+
+    def prepare_q8_dev(self, proj, layer, stream=None):
+        """The layer's q8 stream-layout device copy (a new uint8 tensor), rows, cols."""
+        import torch
+        _, r, c, _g = self.q8_matrix(proj, layer)
+        dst = torch.empty(q8_stream_bytes(r, c), dtype=torch.uint8, device="cuda")
+        check(lib().kq4_vqf_prepare_q8_dev(self._h, proj, layer, _tp(dst), _stream_ptr(stream)),
+              "kq4_vqf_prepare_q8_dev")
+        return dst, r, c
 
     def prepare_dev(self, proj, layer, stream=None):
         """The layer's stream-layout device copy (a new uint8 tensor)."""

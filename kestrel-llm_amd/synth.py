@@ -37,6 +37,20 @@ def make_q4_weights(rows, cols, seed, sigma=0.02, floor=1e-4):
     return tiles
 
 
+def make_q8_weights(rows, cols, seed, sigma=0.015, g=8):
+    """uint8 Q8_0 tiles of g rows (block_q8_0x8 for g = 8): codes uniform in [-127, 127], f16
+    |N(0, sigma)| row scales (the q8 counterpart of the config-3 q4 weights)."""
+    assert rows % g == 0 and cols % 32 == 0
+    rng = np.random.default_rng(seed)
+    G, nb = rows // g, cols // 32
+    tiles = np.empty((G, nb, 34 * g), np.uint8)
+    sc = (np.abs(rng.standard_normal((G, nb, g), dtype=np.float32)) * np.float32(sigma)).astype(
+        np.float16)
+    tiles[:, :, :2 * g] = sc.view(np.uint8).reshape(G, nb, 2 * g)
+    tiles[:, :, 2 * g:] = rng.integers(-127, 128, size=(G, nb, 32 * g), dtype=np.int8).view(np.uint8)
+    return tiles
+
+
 def make_activations(n, cols, seed):
     return np.random.default_rng(seed).standard_normal((n, cols), dtype=np.float32)
 

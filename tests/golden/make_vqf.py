@@ -1,7 +1,8 @@
-"""Writes tests/golden/synth_q4.vqf: a genuine VQF file made by the reference's own converter
-(vqf_convert, built from /root/reference by `make -C oracle conv` into oracle/_ref/vqf_conv) from
-a tiny synthetic Qwen3-shaped model defined here (bf16 safetensors + config.json, seeded). The
-VQF loader tests read it back and check every layer's q4 matrix against the oracle's own
+"""Writes tests/golden/synth_dual.vqf: a genuine VQF file made by the reference's own converter
+(vqf_convert, built from /root/reference by `make -C oracle conv` into oracle/_ref/vqf_conv, in
+its default "dual" mode: Q4_0 4x4 decode weights and Q8_0 8x8 prefill weights) from a tiny
+synthetic Qwen3-shaped model defined here (bf16 safetensors + config.json, seeded). The VQF
+loader tests read it back and check every layer's q4 and q8 matrix against the oracle's own
 quantization of the same weights (model_tensors() regenerates them).
 
     python tests/golden/make_vqf.py
@@ -17,7 +18,7 @@ import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(os.path.dirname(HERE))
-OUT = os.path.join(HERE, "synth_q4.vqf")
+OUT = os.path.join(HERE, "synth_dual.vqf")
 
 CONFIG = dict(model_type="qwen3", hidden_size=128, num_hidden_layers=2, num_attention_heads=2,
               num_key_value_heads=1, head_dim=64, intermediate_size=256, vocab_size=64,
@@ -81,7 +82,7 @@ def main():
     conv = os.path.join(ROOT, "oracle", "_ref", "vqf_conv")
     with tempfile.TemporaryDirectory() as d:
         write_model(d)
-        subprocess.run([conv, "--model", d, "--convert-vqf", OUT, "--wmode", "q4"], check=True)
+        subprocess.run([conv, "--model", d, "--convert-vqf", OUT, "--wmode", "dual"], check=True)
     print("wrote", OUT, os.path.getsize(OUT), "bytes")
 
 

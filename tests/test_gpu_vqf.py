@@ -1,5 +1,5 @@
 """GPU side of the VQF loader: a layer's q4 matrix goes from the mmap'd file
-(tests/golden/synth_q4.vqf, written by the reference's own converter) to HBM in the stream layout
+(tests/golden/synth_dual.vqf, written by the reference's own converter) to HBM in the stream layout
 (kq4_vqf_prepare_dev: byte-equal to the layout's definition) and into the host-pointer API's
 weight cache under the reference's key layer << 32 | proj (kq4_vqf_upload); the matmul over either
 agrees with the oracle on the file's tiles (GEMV bar, max|got-ref| / max|ref| <= 1e-5)."""
@@ -15,7 +15,7 @@ from conftest import rel_err
 pytestmark = pytest.mark.gpu
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-SYNTH = os.path.join(HERE, "golden", "synth_q4.vqf")
+SYNTH = os.path.join(HERE, "golden", "synth_dual.vqf")
 sys.path.insert(0, HERE)
 from test_stream_layout import stream_layout  # noqa: E402
 
@@ -48,3 +48,22 @@ def test_upload_under_reference_key(kq4, orc):
     x = synth.make_activations(2, cols, 5)
     got = kq4.matmul(tiles, x, rows, cols, wkey=key)       # served from the cache entry
     assert rel_err(got, orc.matmul(tiles, x, rows, cols))[0] <= 1e-5
+
+
+@pytest.mark.parametrize("proj,layer", [(0, 1), (4, 0), (6, 1)])
+def test_q8_prepare_and_gemm_from_vqf(kq4, torch_dev, orc, proj, layer):
+    """The dual file's Q8_0 prefill weights to HBM and through the q8 GEMM (bit-exact chain)."""
+    from test_stream_layout import q8_stream_layout
+    torch = torch_dev
+    with kq4.Vqf(SYNTH) as v:
+        tiles, rows, cols, g = v.q8_matrix(proj, layer)
+        tiles = tiles.copy()
+        W, _, _ = v.prepare_q8_dev(proj, layer)
+    torch.cuda.synchronize()
+    assert np.array_equal(W.cpu().numpy(), q8_stream_layout(tiles, g, rows, cols))
+    x = synth.make_activations(16, cols, proj + 3 * layer)
+    want = orc.q8_matmul(tiles, x, rows, cols, g=g)
+    out = torch.empty((16, rows), dtype=torch.float32, device="cuda")
+    kq4.q8_matmul_dev(out, torch.from_numpy(x).cuda(), W, rows, cols)
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy().view(np.uint32), want.view(np.uint32))

@@ -1,6 +1,6 @@
 """The VQF loader (include/kq4_vqf.h) on the CPU - header and directory validation, per-layer q4
 matrices - against two files the reference made itself:
-  * tests/golden/synth_q4.vqf: the reference's own converter (vqf_convert, tests/golden/
+  * tests/golden/synth_dual.vqf: the reference's own converter (vqf_convert, tests/golden/
     make_vqf.py) on a seeded synthetic model; every layer's q4 matrix read through the loader
     must equal the oracle's quantization + 4x4 repack of the same bf16 weights (those two
     oracle functions are pinned byte for byte to the reference's converter code in
@@ -17,7 +17,7 @@ import pytest
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 GOLD = os.path.join(HERE, "golden")
-SYNTH = os.path.join(GOLD, "synth_q4.vqf")
+SYNTH = os.path.join(GOLD, "synth_dual.vqf")
 LEGACY = os.path.join(GOLD, "vqf_header_legacy_qwen3vl8b.bin")
 
 import sys  # noqa: E402
@@ -83,6 +83,23 @@ def test_every_layer_matrix_matches_the_oracle(kq4_cpu, orc):
                 assert np.array_equal(tiles, q4_tiles(orc, src, rows, cols)), (layer, name)
         tiles, rows, cols = v.q4_matrix(kq4_cpu.PROJ_LM, 0)
         assert np.array_equal(tiles, q4_tiles(orc, T["lm_head.weight"], rows, cols))
+
+
+def test_every_layer_q8_matrix_matches_the_oracle(kq4_cpu, orc):
+    """The dual file's Q8_0 8x8 prefill weights: the oracle's f32_to_q8_0 + 8x8 repack (both
+    pinned byte for byte to the reference's converter code in tests/test_oracle_q8.py)."""
+    T = make_vqf.model_tensors()
+    with kq4_cpu.Vqf(SYNTH) as v:
+        assert v.info.flags & 0x1                                  # VQF_FLAG_Q8_8X8
+        for layer in range(make_vqf.CONFIG["num_hidden_layers"]):
+            for proj, name in PROJ.items():
+                tiles, rows, cols, g = v.q8_matrix(proj, layer)
+                assert g == 8
+                f = make_vqf.bf16_to_f32(T[f"model.layers.{layer}.{name}.weight"])
+                assert np.array_equal(tiles, orc.q8_tiles(f, rows, cols, 8)), (layer, name)
+        tiles, rows, cols, g = v.q8_matrix(kq4_cpu.PROJ_LM, 0)
+        assert np.array_equal(tiles, orc.q8_tiles(make_vqf.bf16_to_f32(T["lm_head.weight"]),
+                                                  rows, cols, 8))
 
 
 def test_rejects_bad_files(kq4_cpu, tmp_path):
