@@ -430,12 +430,15 @@ def cpu_baseline(m, budget_s=12.0):
 
 
 PROFILE_OPS = ("gemv_gate_up_2b", "gemv_gate_up_8b", "gemv_down_8b", "gemm_gate_8b",
-               "gemm_down_8b", "moe_30b_a3b")
+               "gemm_down_8b", "moe_30b_a3b", "moe_layer_30b_a3b", "silu_down_8b",
+               "rmsnorm_qkv_8b", "q8_gate_8b", "q8_down_8b")
 
 
 def profile_op(op, m, reps):
     """Launches one op `reps` times back to back (eager) for rocprofv3 runs: the 2B / 8B decode
-    GEMVs, the 8B prefill GEMMs (m tokens) or the Qwen3-30B-A3B MoE FFN (m tokens)."""
+    GEMVs, the 8B prefill GEMMs (m tokens), the Qwen3-30B-A3B MoE FFN or whole layer (router
+    included; m tokens), the 8B SiLU-multiply + down and RMSNorm + QKV ops, or the 8B gate / down
+    with Q8_0 weights (m tokens: GEMV up to 8, GEMM beyond)."""
     import torch
 
     import kq4
@@ -454,8 +457,38 @@ def profile_op(op, m, reps):
         pr = torch.empty((m, tk), device="cuda")
         Y = torch.empty((m, d), device="cuda")
         kq4.moe_route_dev(sel, pr, lg, tk, stream=st)
+        R = torch.randn((ne, d), device="cuda") * 0.02
         for _ in range(reps):
-            kq4.moe_ffn_dev(Y, X, sel, pr, Gd, Ud, Dd, ne, d, ef, stream=st)
+            if op == "moe_layer_30b_a3b":
+                kq4.moe_layer_dev(Y, X, R, Gd, Ud, Dd, ne, tk, d, ef, stream=st)
+            else:
+                kq4.moe_ffn_dev(Y, X, sel, pr, Gd, Ud, Dd, ne, d, ef, stream=st)
+    elif op.startswith("q8"):
+        h, f = synth.QWEN3_8B["hidden"], synth.QWEN3_8B["ffn"]
+        rows, cols = (h, f) if "down" in op else (f, h)
+        w = kq4.q8_prepare_dev(synth.make_q8_weights(rows, cols, 15), rows, cols)
+        x = torch.from_numpy(synth.make_activations(m, cols, 20)).cuda()
+        out = torch.empty((m, rows), device="cuda")
+        for _ in range(reps):
+            kq4.q8_matmul_dev(out, x, w, rows, cols, stream=st)
+    elif op in ("silu_down_8b", "rmsnorm_qkv_8b"):
+        cfg = synth.QWEN3_8B
+        h, f = cfg["hidden"], cfg["ffn"]
+        if op == "silu_down_8b":
+            w = kq4.prepare_dev(torch.from_numpy(synth.make_q4_weights(h, f, 13)).cuda(), h, f)
+            g = torch.from_numpy(synth.make_activations(m, f, 21)).cuda()
+            u = torch.rand((m, f), device="cuda") * 2 - 1
+            out = torch.empty((m, h), device="cuda")
+            for _ in range(reps):
+                kq4.matmul_silu_dev(out, g, u, w, h, f, stream=st)
+        else:
+            qkv = (cfg["q_heads"] + 2 * cfg["kv_heads"]) * cfg["head_dim"]
+            w = kq4.prepare_dev(torch.from_numpy(synth.make_q4_weights(qkv, h, 14)).cuda(), qkv, h)
+            x = torch.from_numpy(synth.make_activations(m, h, 22)).cuda()
+            nw = torch.rand(h, device="cuda") + 0.5
+            out = torch.empty((m, qkv), device="cuda")
+            for _ in range(reps):
+                kq4.rmsnorm_matmul_multi_dev([out], x, nw, 1e-6, [w], [qkv], h, stream=st)
     else:
         cfg = CFG if op.endswith("2b") else synth.QWEN3_8B
         h, f = cfg["hidden"], cfg["ffn"]
