@@ -282,23 +282,40 @@ KQ4_DEV void kq4_gv_act_put(const KQ4GvAct<M, FQ, WF> &r, const KQ4GemvArgs &a, 
 KQ4_DEV void kq4_gv_pin(float &x) { asm volatile("" : "+v"(x)); }
 
 // DOT4: acc[m] = token m's chain over this lane's blocks of its row and half.
+// One token in half-set mode (the decode shapes with few row sets): all 8 blocks' codes and
+// scales are read from LDS first (40 registers), so the blocks do not wait for LDS one by one
+// once the weights are in.
 template <int M, int HS>
 KQ4_DEV void kq4_gv_dot4(const KQ4GvStage<HS> &st, const uint8_t *sq, const float (*sx)[8], int h,
                          int p, float *acc) {
+  constexpr int NJB = 2 * KQ4GvStage<HS>::NU;
+  constexpr bool PRE = M == 1 && HS == 1;
+  uint4 qv[PRE ? NJB : 1];
+  float xv[PRE ? NJB : 1];
+  if (PRE) {
 #pragma unroll
-  for (int jb = 0; jb < 4 * KQ4GvStage<HS>::NU / 2; ++jb) {
+    for (int jb = 0; jb < NJB; ++jb) {
+      const int b = kq4_gv_blk<HS, 0>(jb, p);
+      qv[jb] = *reinterpret_cast<const uint4 *>(sq + kq4_gv_qpos(b) + 16 * h);
+      xv[jb] = sx[b][0];
+    }
+  }
+#pragma unroll
+  for (int jb = 0; jb < NJB; ++jb) {
     const int b = kq4_gv_blk<HS, 0>(jb, p);
     uint32_t o[4];
     kq4_unpack_half(st.n[2 * jb], st.n[2 * jb + 1], o);
     const float wd = kq4_gv_wd<HS, 0>(st, jb, p);
 #pragma unroll
     for (int m = 0; m < M; ++m) {
-      const uint4 q = *reinterpret_cast<const uint4 *>(sq + m * KQ4_GV_QTS + kq4_gv_qpos(b) + 16 * h);
+      const uint4 q = PRE ? qv[jb]
+                          : *reinterpret_cast<const uint4 *>(sq + m * KQ4_GV_QTS + kq4_gv_qpos(b) +
+                                                             16 * h);
       int s = kq4_dot4(o[0], q.x, 0);
       s = kq4_dot4(o[1], q.y, s);
       s = kq4_dot4(o[2], q.z, s);
       s = kq4_dot4(o[3], q.w, s);
-      acc[m] = fmaf((float)s, wd * sx[b][m], acc[m]);
+      acc[m] = fmaf((float)s, wd * (PRE ? xv[jb] : sx[b][m]), acc[m]);
       kq4_gv_pin(acc[m]);
     }
   }
@@ -338,6 +355,43 @@ KQ4_DEV void kq4_gv_mfma_stage(const KQ4GvStage<HS> &st, const uint8_t *sq, cons
   }
 }
 
+// The matrix of workgroup wg (a launch covers up to KQ4_MAXMAT matrices, each a contiguous range
+// of workgroups). Every entry's fields are read first and then chosen by compares: indexing the
+// argument array by the chosen entry would be a second scalar load that waits for the first, and
+// the weight loads wait for both (the empty asm keeps the compiler from turning the selects back
+// into an indexed load).
+// The pointers are kept in the global address space (kernel arguments are global memory; a
+// generic pointer out of the asm would make every weight load a flat load, which also counts
+// against the LDS wait counter).
+typedef const __attribute__((address_space(1))) uint8_t *kq4_gw_t;
+typedef __attribute__((address_space(1))) float *kq4_go_t;
+typedef const __attribute__((address_space(1))) float *kq4_gr_t;
+
+struct KQ4GvMatSel {
+  kq4_gw_t w;
+  kq4_go_t out;
+  kq4_gr_t res;
+  int rows, wg_begin;
+};
+
+KQ4_DEV KQ4GvMatSel kq4_gv_select(const KQ4GemvArgs &a, int wg) {
+  static_assert(KQ4_MAXMAT == 4, "kq4_gv_select reads 4 entries");
+  kq4_gw_t w1 = (kq4_gw_t)a.mat[1].w, w2 = (kq4_gw_t)a.mat[2].w, w3 = (kq4_gw_t)a.mat[3].w;
+  kq4_go_t o1 = (kq4_go_t)a.mat[1].out, o2 = (kq4_go_t)a.mat[2].out, o3 = (kq4_go_t)a.mat[3].out;
+  kq4_gr_t r1 = (kq4_gr_t)a.mat[1].res, r2 = (kq4_gr_t)a.mat[2].res, r3 = (kq4_gr_t)a.mat[3].res;
+  int n1 = a.mat[1].rows, n2 = a.mat[2].rows, n3 = a.mat[3].rows;
+  int b1 = a.mat[1].wg_begin, b2 = a.mat[2].wg_begin, b3 = a.mat[3].wg_begin;
+  asm volatile("" : "+s"(w1), "+s"(w2), "+s"(w3), "+s"(o1), "+s"(o2), "+s"(o3), "+s"(r1),
+               "+s"(r2), "+s"(r3), "+s"(n1), "+s"(n2), "+s"(n3), "+s"(b1), "+s"(b2), "+s"(b3));
+  KQ4GvMatSel s{(kq4_gw_t)a.mat[0].w, (kq4_go_t)a.mat[0].out, (kq4_gr_t)a.mat[0].res,
+                a.mat[0].rows, 0};
+  const int nm = a.nmat;
+  if (nm > 1 && wg >= b1) s = KQ4GvMatSel{w1, o1, r1, n1, b1};
+  if (nm > 2 && wg >= b2) s = KQ4GvMatSel{w2, o2, r2, n2, b2};
+  if (nm > 3 && wg >= b3) s = KQ4GvMatSel{w3, o3, r3, n3, b3};
+  return s;
+}
+
 // One workgroup per 32-row set (HS = 0) or per half set (HS = 1), up to 16 waves splitting K
 // (every variant fits the 128 VGPRs that allows).
 template <int M, int FQ, int KIND, int HS, int WF>
@@ -349,21 +403,18 @@ __global__ __launch_bounds__(1024) void kq4_gemv_kernel(const KQ4GemvArgs a) {
   constexpr int NP = HS ? 2 : 1;                   // lane parities
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int nw = blockDim.x >> 6;
+  const int nw = a.nw;   // = blockDim.x / 64 (an argument: the dispatch's own field sits on another line)
   const int wg = blockIdx.x;
-  int mi = 0;
-#pragma unroll
-  for (int i = 1; i < KQ4_MAXMAT; ++i)
-    if (i < a.nmat && wg >= a.mat[i].wg_begin) mi = i;
-  const int wl = wg - a.mat[mi].wg_begin;
+  const KQ4GvMatSel ms = kq4_gv_select(a, wg);
+  const int wl = wg - ms.wg_begin;
   const int rs = wl >> HS;                         // 32-row set within the matrix
   const int hs = HS ? (wl & 1) : 0;
-  const int rows = a.mat[mi].rows;
+  const int rows = ms.rows;
   const int row0 = rs * 32 + hs * 16;              // first output row of the workgroup
   const int nb = a.nb;
   constexpr int CB = KQ4Wf<WF>::CB, CHUNK = KQ4Wf<WF>::CHUNK;
   const int nst = (nb + CB - 1) / CB;
-  const uint8_t *__restrict__ wset = a.mat[mi].w + (size_t)rs * nst * CHUNK;
+  const uint8_t *__restrict__ wset = (const uint8_t *)ms.w + (size_t)rs * nst * CHUNK;
   uint8_t *slab = kq4_gv_lds + wave * SLAB;
   uint8_t *sq = slab;
   float (*sx)[8] = reinterpret_cast<float (*)[8]>(sq + M * KQ4_GV_QTS);
@@ -381,6 +432,12 @@ __global__ __launch_bounds__(1024) void kq4_gemv_kernel(const KQ4GemvArgs a) {
     KQ4GvStage<HS> rw;
     kq4_gv_act_load<M, FQ, WF>(ra, a, st, lane);
     kq4_gv_load<HS, WF>(rw, wset + (size_t)st * CHUNK, rr, h, p);
+    // One token, fp32 activations: every load is issued before the quantization waits for the
+    // activations (the compiler otherwise sinks the weight loads below it, and the two memory
+    // latencies add up). Measured: the Qwen3-VL-2B decode GEMVs 0.1-0.3 us faster each, the
+    // Qwen3-8B down 0.5 us; with more tokens or the SiLU form it measured slower, so there the
+    // compiler's order stays.
+    if constexpr (M == 1 && FQ == 1) __builtin_amdgcn_sched_barrier(0);
     kq4_gv_act_put<M, FQ, WF>(ra, a, lane, sq, sx);
     if (KIND == 0) kq4_gv_dot4<M, HS>(rw, sq, sx, h, p, acc);
     else kq4_gv_mfma_stage<M, HS, WF>(rw, sq, sx, lane, p, acc);
@@ -388,8 +445,8 @@ __global__ __launch_bounds__(1024) void kq4_gemv_kernel(const KQ4GemvArgs a) {
 
   // this wave's partial sums in its slab: DOT4 red[((h*NP + p)*M + m)*NR + r], MFMA
   // red[(p*M + token)*NR + r]
-  float *__restrict__ out = a.mat[mi].out;
-  const float *__restrict__ res = a.mat[mi].res;
+  float *__restrict__ out = (float *)ms.out;
+  const float *__restrict__ res = (const float *)ms.res;
   float *red = reinterpret_cast<float *>(slab);   // only this wave used its slab so far
   if (KIND == 0) {
 #pragma unroll
@@ -402,7 +459,7 @@ __global__ __launch_bounds__(1024) void kq4_gemv_kernel(const KQ4GemvArgs a) {
   __syncthreads();
   // the partials of the workgroup's rows, added in a fixed order: waves, then parities (and for
   // DOT4 each half's chain, then lo + hi as the C-tile kernel finishes)
-  for (int i = threadIdx.x; i < NR * M; i += blockDim.x) {
+  for (int i = threadIdx.x; i < NR * M; i += 64 * nw) {
     const int m = i / NR, rw = i - m * NR;
     const int row = row0 + rw;
     if (row >= rows) continue;
@@ -433,8 +490,10 @@ static hipError_t gv_launch(const KQ4GemvArgs &a, int nw, int grid, hipStream_t 
     if (e != hipSuccess) return e;
     attr = true;
   }
+  KQ4GemvArgs b = a;
+  b.nw = nw;
   hipLaunchKernelGGL((kq4_gemv_kernel<M, FQ, KIND, HS, WF>), dim3(grid), dim3(64 * nw), lds, s,
-                     a);
+                     b);
   return hipGetLastError();
 }
 
@@ -450,18 +509,20 @@ static hipError_t gv_launch_k(const KQ4GemvArgs &a, int kind, int hs, int nw, in
   return hs ? gv_launch<M, FQ, 1, 1, 0>(a, nw, grid, s) : gv_launch<M, FQ, 1, 0, 0>(a, nw, grid, s);
 }
 
-// In-kernel quantization exists for M <= KQ4_GEMV_FQ_MAX_M (the SiLU form for q4 only).
+// In-kernel quantization exists for M <= KQ4_GEMV_FQ_MAX_M, the SiLU form for q4 and
+// M <= KQ4_GEMV_SILU_FQ_MAX_M (its fp32 gate and up registers would spill beyond).
 template <int M>
 static hipError_t gv_launch_m(const KQ4GemvArgs &a, int kind, int fq, int hs, int nw, int grid,
                               hipStream_t s) {
   constexpr int MF = M <= KQ4_GEMV_FQ_MAX_M ? M : 1;
+  constexpr int MS = M <= KQ4_GEMV_SILU_FQ_MAX_M ? M : 1;
   if (fq) {
     if (M > KQ4_GEMV_FQ_MAX_M) return hipErrorInvalidValue;
     if (fq == 2) {
-      if (a.wf) return hipErrorInvalidValue;
+      if (a.wf || M > KQ4_GEMV_SILU_FQ_MAX_M) return hipErrorInvalidValue;
       if (kind == 0)
-        return hs ? gv_launch<MF, 2, 0, 1, 0>(a, nw, grid, s) : gv_launch<MF, 2, 0, 0, 0>(a, nw, grid, s);
-      return hs ? gv_launch<MF, 2, 1, 1, 0>(a, nw, grid, s) : gv_launch<MF, 2, 1, 0, 0>(a, nw, grid, s);
+        return hs ? gv_launch<MS, 2, 0, 1, 0>(a, nw, grid, s) : gv_launch<MS, 2, 0, 0, 0>(a, nw, grid, s);
+      return hs ? gv_launch<MS, 2, 1, 1, 0>(a, nw, grid, s) : gv_launch<MS, 2, 1, 0, 0>(a, nw, grid, s);
     }
     return gv_launch_k<MF, 1>(a, kind, hs, nw, grid, s);
   }

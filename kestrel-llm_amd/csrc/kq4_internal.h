@@ -7,6 +7,7 @@
 #define KQ4_GEMV_MAX_M 8
 #define KQ4_MAXMAT 4
 #define KQ4_GEMV_FQ_MAX_M 4   // largest token count the GEMV quantizes in-kernel
+#define KQ4_GEMV_SILU_FQ_MAX_M 3   // .. and forms the SiLU product in-kernel (registers)
 
 // Every kernel reads q4 weights in the stream layout (kq4_common.h): a VQF 4x4 matrix repacked
 // once by kq4_launch_repack into kq4_stream_bytes(rows, cols) bytes.
@@ -39,6 +40,7 @@ struct KQ4GemvArgs {
                         // 1 fused VDOT or 2 unfused GEMM chain
   int cols;
   int nb;
+  int nw;               // waves per workgroup (set by kq4_launch_gemv)
 };
 
 // up != nullptr: quantizes silu_mul(x, up) instead of x (the dense FFN's down input).
