@@ -132,8 +132,11 @@ int gemv_kind(int n) {
   return n >= mfma_from ? 1 : 0;
 }
 
-// GEMV launch shape. Workgroups: one per 32-row set, or per 16-row half set when the launch
-// has fewer than two sets per CU (so that every CU streams, with a second workgroup to overlap).
+// GEMV launch shape. Workgroups: one per 32-row set; per 16-row half set when the launch has
+// fewer than two sets per CU (so that every CU streams, with a second workgroup to overlap); per
+// 8-row quarter set when even that would be at most one workgroup per CU. Measured on MI355X
+// (M = 1 .. 8): quarter sets make the Qwen3-VL-2B down (64 sets) 0.2-0.45 us faster and O up to
+// 0.2 us, but the 128-set shapes (Qwen3-8B down and O, 2B QKV) 0.1-0.7 us slower than halves.
 // Waves per workgroup (splitting K in 16-block stages): about KQ4_GEMV_WPCU (32) per CU over
 // the launch, at most one per stage and 16 per workgroup, balanced so that no wave has more
 // stages than another by more than one. (Issuing a wave's second stage before computing its first
@@ -143,7 +146,10 @@ void plan_gemv(int sets, int nb, int ncu, int *half_out, int *nw_out) {
   static const int force_hs = env_int("KQ4_GEMV_HS", -1);
   static const int force_w = env_int("KQ4_GEMV_WAVES", 0);
   static const int per_cu = env_int("KQ4_GEMV_WPCU", 32);
-  const int hs = force_hs == 0 || force_hs == 1 ? force_hs : (sets < 2 * ncu ? 1 : 0);
+  const int hs = force_hs >= 0 && force_hs <= 2 ? force_hs
+                 : 4 * sets <= ncu                ? 2
+                 : sets < 2 * ncu                 ? 1
+                                                  : 0;
   const int wgs = sets << hs;
   const int nst = (nb + 15) / 16;
   int want = force_w > 0 ? force_w : (per_cu * ncu + wgs - 1) / wgs;

@@ -73,15 +73,16 @@ KQ4_DEV kq4_v16i kq4_gv_mfma(kq4_v4i a, kq4_v4i b) {
 }
 
 // ---- weights of one stage -------------------------------------------------------------------
-// Full-set mode (HS = 0): lane (r, h) = (lane%32, lane/32) holds row r's half h of all 16 blocks
-// (8 unit loads). Half-set mode (HS = 1, a workgroup takes rows 16*hs .. +15 of the set): lane
-// (r, p, h) = (lane%16, (lane/16)%2, lane/32) holds row 16*hs+r's half h of the 8 blocks
-// 4u+2p, 4u+2p+1 (u = 0..3; 4 unit loads, each instruction covering two 1-KB units at 256-B
-// runs). In both, the row's 16 scales (2 loads; lanes of one row share them).
+// A workgroup takes NR = 32 >> HS rows of a set (rows NR*hs .. +NR-1): HS = 0 the full set, 1 a
+// half, 2 a quarter. Lane (r, p, h) = (lane % NR, (lane / NR) % NP, lane / 32) with NP = 1 << HS
+// parities holds row NR*hs + r's half h of the units i = NP*u + p (u = 0 .. NU-1, NU = 8 >> HS
+// unit loads; a q4 unit is 2 blocks, a q8 unit 1), so one load instruction covers NP units at
+// 16*NR-byte runs. In every mode the row's scales (2 loads for q4, 1 for q8; the lanes of one
+// row share them).
 
 template <int HS>
 struct KQ4GvStage {
-  static constexpr int NU = HS ? 4 : 8;   // 16-B nibble loads per lane
+  static constexpr int NU = 8 >> HS;      // 16-B nibble loads per lane
   uint32_t n[4 * NU];                     // lane block jb (0 .. 2*NU-1): n[2jb], n[2jb+1]
   uint32_t sc[8];                         // stage block b: f16 at sc[b/2] >> 16*(b%2)
 };
@@ -102,32 +103,45 @@ KQ4_DEV void kq4_gv_load(KQ4GvStage<HS> &st, const uint8_t *__restrict__ chunk, 
   const uint4 *src = reinterpret_cast<const uint4 *>(chunk) + rr + 32 * h;
 #pragma unroll
   for (int u = 0; u < KQ4GvStage<HS>::NU; ++u) {
-    const int i = HS ? 2 * u + p : u;
+    const int i = (u << HS) + p;
     const uint4 v = src[64 * i];
     st.n[4 * u] = v.x; st.n[4 * u + 1] = v.y; st.n[4 * u + 2] = v.z; st.n[4 * u + 3] = v.w;
   }
 }
 
-// Stage block of lane block jb (p = the lane's unit parity in half-set mode).
+// Stage block of lane block jb (p = the lane's unit parity).
 template <int HS, int WF>
 KQ4_DEV int kq4_gv_blk(int jb, int p) {
-  if (WF) return HS ? 2 * jb + p : jb;
-  return HS ? 4 * (jb >> 1) + 2 * p + (jb & 1) : jb;
+  if (WF) return (jb << HS) + p;
+  return 2 * (((jb >> 1) << HS) + p) + (jb & 1);
 }
 
-// a if p == 0, b if p == 1, by masks: a select between two elements of one register array
-// would be folded into a lane-dependent index, which puts the array in scratch memory.
+// a if p == 0, b if p == 1 (p in {0, 1}), by masks: a select between two elements of one register
+// array would be folded into a lane-dependent index, which puts the array in scratch memory.
 KQ4_DEV uint32_t kq4_gv_pick(uint32_t a, uint32_t b, int p) {
   const uint32_t m = 0u - (uint32_t)p;
   return (a & ~m) | (b & m);
 }
 
+// v[p] of the NP = 1 << HS registers v[0 .. NP-1] (p < NP), by masks.
+template <int HS>
+KQ4_DEV uint32_t kq4_gv_pickn(const uint32_t *v, int p) {
+  if (HS == 0) return v[0];
+  if (HS == 1) return kq4_gv_pick(v[0], v[1], p);
+  return kq4_gv_pick(kq4_gv_pick(v[0], v[1], p & 1), kq4_gv_pick(v[2], v[3], p & 1), p >> 1);
+}
+
 // Row scale (f32) of lane block jb; the register index is compile-time in all modes.
+// q8: block b = NP*jb + p, its scale at sc[b/2] >> 16*(b%2); q4: block 2*(NP*(jb/2) + p) + jb%2,
+// at sc[NP*(jb/2) + p] >> 16*(jb%2).
 template <int HS, int WF>
 KQ4_DEV float kq4_gv_wd(const KQ4GvStage<HS> &st, int jb, int p) {
-  if (WF) return HS ? kq4_h2f(st.sc[jb] >> (16 * p)) : kq4_h2f(st.sc[jb >> 1] >> (16 * (jb & 1)));
-  const uint32_t w = HS ? kq4_gv_pick(st.sc[2 * (jb >> 1)], st.sc[2 * (jb >> 1) + 1], p)
-                        : st.sc[jb >> 1];
+  if (WF) {
+    if (HS == 0) return kq4_h2f(st.sc[jb >> 1] >> (16 * (jb & 1)));
+    if (HS == 1) return kq4_h2f(st.sc[jb] >> (16 * p));
+    return kq4_h2f(kq4_gv_pick(st.sc[2 * jb], st.sc[2 * jb + 1], p >> 1) >> (16 * (p & 1)));
+  }
+  const uint32_t w = kq4_gv_pickn<HS>(&st.sc[(jb >> 1) << HS], p);
   return kq4_h2f(w >> (16 * (jb & 1)));
 }
 
@@ -282,14 +296,14 @@ KQ4_DEV void kq4_gv_act_put(const KQ4GvAct<M, FQ, WF> &r, const KQ4GemvArgs &a, 
 KQ4_DEV void kq4_gv_pin(float &x) { asm volatile("" : "+v"(x)); }
 
 // DOT4: acc[m] = token m's chain over this lane's blocks of its row and half.
-// One token in half-set mode (the decode shapes with few row sets): all 8 blocks' codes and
-// scales are read from LDS first (40 registers), so the blocks do not wait for LDS one by one
-// once the weights are in.
+// One token in half- or quarter-set mode (the decode shapes with few row sets): all the lane's
+// blocks' codes and scales are read from LDS first (40 or 20 registers), so the blocks do not wait
+// for LDS one by one once the weights are in.
 template <int M, int HS>
 KQ4_DEV void kq4_gv_dot4(const KQ4GvStage<HS> &st, const uint8_t *sq, const float (*sx)[8], int h,
                          int p, float *acc) {
   constexpr int NJB = 2 * KQ4GvStage<HS>::NU;
-  constexpr bool PRE = M == 1 && HS == 1;
+  constexpr bool PRE = M == 1 && HS >= 1;
   uint4 qv[PRE ? NJB : 1];
   float xv[PRE ? NJB : 1];
   if (PRE) {
@@ -321,17 +335,18 @@ KQ4_DEV void kq4_gv_dot4(const KQ4GvStage<HS> &st, const uint8_t *sq, const floa
   }
 }
 
-// MFMA: one v_mfma_i32_32x32x32_i8 per lane block. B column = lane%32 (full set: row; half set:
-// row + 16p, the two parities holding different blocks), k half = lane/32. A row = lane%32 holds
-// the codes of token min(lane%32 (%16 in half-set mode), M-1) for the lane's own block, so output
-// (token row T, column c) is valid where T's block matches c's: full set T = token 0..7, half set
-// T = token + 16p. acc[v] = token 4h+v of the lane's row (and parity).
+// MFMA: one v_mfma_i32_32x32x32_i8 per lane block. B column = lane%32 = row + NR*p (the NP
+// parities hold different blocks), k half = lane/32. A row = lane%32 holds the codes of token
+// min(lane % NR, M-1) for the lane's own block, so output (token row T, column c) is valid where
+// T's block matches c's: T = token + NR*p, which the 32x32 output layout puts in result register
+// (NR/2)*p + v for token 4h+v. acc[v] = token 4h+v of the lane's row (and parity).
 template <int M, int HS, int WF>
 KQ4_DEV void kq4_gv_mfma_stage(const KQ4GvStage<HS> &st, const uint8_t *sq, const float (*sx)[8],
                                int lane, int p, float *acc) {
   constexpr int VT = M < 4 ? M : 4;
   const int h = lane >> 5;
-  const int tr = HS ? (lane & 15) : (lane & 31);
+  constexpr int NR = 32 >> HS;
+  const int tr = lane & (NR - 1);
   const int t = tr < M ? tr : M - 1;
   const uint8_t *qb = sq + t * KQ4_GV_QTS + 16 * h;
 #pragma unroll
@@ -347,7 +362,10 @@ KQ4_DEV void kq4_gv_mfma_stage(const KQ4GvStage<HS> &st, const uint8_t *sq, cons
     const float xv[4] = {xs.x, xs.y, xs.z, xs.w};
 #pragma unroll
     for (int v = 0; v < VT; ++v) {
-      const int c = HS ? (int)kq4_gv_pick((uint32_t)C[v], (uint32_t)C[8 + v], p) : C[v];
+      uint32_t cv[1 << HS];
+#pragma unroll
+      for (int pp = 0; pp < (1 << HS); ++pp) cv[pp] = (uint32_t)C[(NR / 2) * pp + v];
+      const int c = (int)kq4_gv_pickn<HS>(cv, p);
       if (WF == 2) acc[v] = acc[v] + (wd * xv[v]) * (float)c;   // the q8 GEMM chain, unfused
       else acc[v] = fmaf((float)c, wd * xv[v], acc[v]);
       kq4_gv_pin(acc[v]);
@@ -392,15 +410,15 @@ KQ4_DEV KQ4GvMatSel kq4_gv_select(const KQ4GemvArgs &a, int wg) {
   return s;
 }
 
-// One workgroup per 32-row set (HS = 0) or per half set (HS = 1), up to 16 waves splitting K
-// (every variant fits the 128 VGPRs that allows).
+// One workgroup per 32-row set (HS = 0), half set (HS = 1) or quarter set (HS = 2), up to 16
+// waves splitting K (every variant fits the 128 VGPRs that allows).
 template <int M, int FQ, int KIND, int HS, int WF>
 __global__ __launch_bounds__(1024) void kq4_gemv_kernel(const KQ4GemvArgs a) {
   extern __shared__ __align__(16) uint8_t kq4_gv_lds[];
   constexpr int SLAB = kq4_gv_slab<M>();
   constexpr int NACC = KIND == 0 ? M : 4;
-  constexpr int NR = HS ? 16 : 32;                 // output rows of the workgroup
-  constexpr int NP = HS ? 2 : 1;                   // lane parities
+  constexpr int NR = 32 >> HS;                     // output rows of the workgroup
+  constexpr int NP = 1 << HS;                      // lane parities
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int nw = a.nw;   // = blockDim.x / 64 (an argument: the dispatch's own field sits on another line)
@@ -408,9 +426,9 @@ __global__ __launch_bounds__(1024) void kq4_gemv_kernel(const KQ4GemvArgs a) {
   const KQ4GvMatSel ms = kq4_gv_select(a, wg);
   const int wl = wg - ms.wg_begin;
   const int rs = wl >> HS;                         // 32-row set within the matrix
-  const int hs = HS ? (wl & 1) : 0;
+  const int hs = wl & (NP - 1);                    // the workgroup's part of the set
   const int rows = ms.rows;
-  const int row0 = rs * 32 + hs * 16;              // first output row of the workgroup
+  const int row0 = rs * 32 + hs * NR;              // first output row of the workgroup
   const int nb = a.nb;
   constexpr int CB = KQ4Wf<WF>::CB, CHUNK = KQ4Wf<WF>::CHUNK;
   const int nst = (nb + CB - 1) / CB;
@@ -419,9 +437,9 @@ __global__ __launch_bounds__(1024) void kq4_gemv_kernel(const KQ4GemvArgs a) {
   uint8_t *sq = slab;
   float (*sx)[8] = reinterpret_cast<float (*)[8]>(sq + M * KQ4_GV_QTS);
   const int h = lane >> 5;
-  const int p = HS ? (lane >> 4) & 1 : 0;
-  const int r = HS ? (lane & 15) : (lane & 31);    // row within the workgroup
-  const int rr = hs * 16 + r;                      // row within the set
+  const int p = (lane >> (5 - HS)) & (NP - 1);
+  const int r = lane & (NR - 1);                   // row within the workgroup
+  const int rr = hs * NR + r;                      // row within the set
 
   float acc[NACC];
 #pragma unroll
@@ -497,16 +515,23 @@ static hipError_t gv_launch(const KQ4GemvArgs &a, int nw, int grid, hipStream_t 
   return hipGetLastError();
 }
 
+template <int M, int FQ, int KIND, int WF>
+static hipError_t gv_launch_hs(const KQ4GemvArgs &a, int hs, int nw, int grid, hipStream_t s) {
+  if (hs == 2) return gv_launch<M, FQ, KIND, 2, WF>(a, nw, grid, s);
+  if (hs == 1) return gv_launch<M, FQ, KIND, 1, WF>(a, nw, grid, s);
+  return gv_launch<M, FQ, KIND, 0, WF>(a, nw, grid, s);
+}
+
 template <int M, int FQ>
 static hipError_t gv_launch_k(const KQ4GemvArgs &a, int kind, int hs, int nw, int grid,
                               hipStream_t s) {
   if (a.wf == 1)   // q8: the MFMA kind only (its block sums span both K halves)
-    return hs ? gv_launch<M, FQ, 1, 1, 1>(a, nw, grid, s) : gv_launch<M, FQ, 1, 0, 1>(a, nw, grid, s);
+    return gv_launch_hs<M, FQ, 1, 1>(a, hs, nw, grid, s);
   if (a.wf == 2)
-    return hs ? gv_launch<M, FQ, 1, 1, 2>(a, nw, grid, s) : gv_launch<M, FQ, 1, 0, 2>(a, nw, grid, s);
+    return gv_launch_hs<M, FQ, 1, 2>(a, hs, nw, grid, s);
   if (kind == 0)
-    return hs ? gv_launch<M, FQ, 0, 1, 0>(a, nw, grid, s) : gv_launch<M, FQ, 0, 0, 0>(a, nw, grid, s);
-  return hs ? gv_launch<M, FQ, 1, 1, 0>(a, nw, grid, s) : gv_launch<M, FQ, 1, 0, 0>(a, nw, grid, s);
+    return gv_launch_hs<M, FQ, 0, 0>(a, hs, nw, grid, s);
+  return gv_launch_hs<M, FQ, 1, 0>(a, hs, nw, grid, s);
 }
 
 // In-kernel quantization exists for M <= KQ4_GEMV_FQ_MAX_M, the SiLU form for q4 and
@@ -521,8 +546,8 @@ static hipError_t gv_launch_m(const KQ4GemvArgs &a, int kind, int fq, int hs, in
     if (fq == 2) {
       if (a.wf || M > KQ4_GEMV_SILU_FQ_MAX_M) return hipErrorInvalidValue;
       if (kind == 0)
-        return hs ? gv_launch<MS, 2, 0, 1, 0>(a, nw, grid, s) : gv_launch<MS, 2, 0, 0, 0>(a, nw, grid, s);
-      return hs ? gv_launch<MS, 2, 1, 1, 0>(a, nw, grid, s) : gv_launch<MS, 2, 1, 0, 0>(a, nw, grid, s);
+        return gv_launch_hs<MS, 2, 0, 0>(a, hs, nw, grid, s);
+      return gv_launch_hs<MS, 2, 1, 0>(a, hs, nw, grid, s);
     }
     return gv_launch_k<MF, 1>(a, kind, hs, nw, grid, s);
   }
@@ -534,7 +559,7 @@ int kq4_gemv_slab_bytes(int n_batch) { return n_batch * KQ4_GV_QTS + KQ4_GV_XS; 
 int kq4_launch_gemv(const KQ4GemvArgs &a, int n_batch, int kind, int half_sets, int nw,
                     int total_wg, hipStream_t s) {
   if (n_batch < 1 || n_batch > KQ4_GEMV_MAX_M || total_wg <= 0 || nw < 1 || nw > 16 ||
-      kind < 0 || kind > 1 || (half_sets != 0 && half_sets != 1) ||
+      kind < 0 || kind > 1 || half_sets < 0 || half_sets > 2 ||
       (size_t)nw * kq4_gemv_slab_bytes(n_batch) > 160 * 1024)
     return (int)hipErrorInvalidValue;
   for (int i = 0; i < a.nmat; ++i)

@@ -57,7 +57,8 @@ int kq4_launch_rms_norm(const float *x, const float *w, float *out, int8_t *xq, 
                         int n_batch, int d, float eps, int serial, hipStream_t stream);
 
 // n_batch in [1, KQ4_GEMV_MAX_M]; one workgroup per 32-row set, or per 16-row half set when
-// half_sets = 1 (total_wg over all matrices, each matrix's wg_begin counted in those units),
+// half_sets = 1, per 8-row quarter set when 2 (total_wg over all matrices, each matrix's wg_begin
+// counted in those units),
 // nw (1..16) waves splitting K in 16-block stages; kind 0 = per-lane v_dot4 dots, 1 = v_mfma
 // dots. args.xf (in-kernel quantization) requires n_batch <= KQ4_GEMV_FQ_MAX_M.
 int kq4_launch_gemv(const KQ4GemvArgs &args, int n_batch, int kind, int half_sets, int nw,

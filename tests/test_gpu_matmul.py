@@ -71,9 +71,9 @@ def test_block_sums_exact(kq4, torch_dev, orc, rows, cols, n):
     assert np.array_equal(host(lo), lo_o) and np.array_equal(host(hi), hi_o)
 
 
-# (256, 12288) and (64, 24576): more 16-block stages than waves (2 and 4 per wave), half-set
-# workgroups; (88000, 2048): the same with full-set workgroups (so many row sets that each
-# workgroup gets two waves for four stages)
+# Workgroup modes: up to 64 row sets (2048 rows) quarter sets, (6144, 2048) half sets, (88000,
+# 2048) full sets with two waves for four stages; (256, 12288) and (64, 24576) have more 16-block
+# stages than waves (2 and 4 per wave).
 GEMV_SHAPES = [(16, 256), (20, 160), (4, 32), (100, 2080), (132, 4096), (256, 12288),
                (64, 24576), (6144, 2048), (2048, 6144), (88000, 2048)]
 
