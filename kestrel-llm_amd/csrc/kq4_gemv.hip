@@ -27,13 +27,14 @@
 //   * the integer dot, two kinds:
 //       DOT4: lane (row, half) dots its 16 weights of each block with v_dot4_i32_i8 against the
 //             token's 16 codes (an LDS broadcast read) and keeps one fp32 chain per token and
-//             half (the C-tile kernel's lo/hi split, :4180-4216); the halves are added at the
-//             end. Cost grows with M.
+//             half (the C-tile kernel's lo/hi split, :4180-4216); each wave adds its halves
+//             before the waves' sums are added. Cost grows with M.
 //       MFMA: per block one v_mfma_i32_32x32x32_i8 with A = the tokens' codes (32 rows, M <= 8
 //             used) and B = the lanes' weight operands as they are; the result 16*S is at lane
 //             (row = lane%32, token = 4*(lane/32) + v). Cost independent of M.
-//   * at the end the waves' partial sums are added in wave order through LDS: deterministic,
-//     one launch, no cross-workgroup communication.
+//   * at the end the partials of an output are added in a fixed order (DOT4: each wave's lanes
+//     by shuffles, then the waves' sums through LDS; MFMA: the lanes' partials through LDS, over
+//     waves then parities): deterministic, one launch, no cross-workgroup communication.
 #include "kq4_common.h"
 #include "kq4_internal.h"
 
@@ -57,7 +58,7 @@ typedef int kq4_v4i __attribute__((ext_vector_type(4)));
 typedef int kq4_v16i __attribute__((ext_vector_type(16)));
 
 // LDS bytes of one wave's slab: [activation codes][scales]; it also holds the wave's partial
-// sums at the end (at most 2 x 8 x 32 floats).
+// sums at the end (at most 8 tokens x 32 floats).
 template <int M>
 constexpr int kq4_gv_slab() {
   return M * KQ4_GV_QTS + KQ4_GV_XS;
@@ -461,38 +462,43 @@ __global__ __launch_bounds__(1024) void kq4_gemv_kernel(const KQ4GemvArgs a) {
     else kq4_gv_mfma_stage<M, HS, WF>(rw, sq, sx, lane, p, acc);
   }
 
-  // this wave's partial sums in its slab: DOT4 red[((h*NP + p)*M + m)*NR + r], MFMA
-  // red[(p*M + token)*NR + r]
+  // DOT4: each output's lane partials are first added inside the wave (a fixed tree: the two K
+  // halves' chains, then the parities) and the wave's sum goes to its slab at red[m*NR + r]; one
+  // thread per output then adds the waves' sums in wave order. MFMA (whose in-wave shuffles
+  // measured slower): the lanes store red[(p*M + token)*NR + r] and the thread adds them over
+  // waves, then parities. Either order is fixed, so results are deterministic.
   float *__restrict__ out = (float *)ms.out;
   const float *__restrict__ res = (const float *)ms.res;
   float *red = reinterpret_cast<float *>(slab);   // only this wave used its slab so far
   if (KIND == 0) {
 #pragma unroll
-    for (int m = 0; m < M; ++m) red[((h * NP + p) * M + m) * NR + r] = acc[m];
+    for (int m = 0; m < M; ++m) {
+      float v = acc[m];
+      v += __shfl_xor(v, 32);
+#pragma unroll
+      for (int k = 0; k < HS; ++k) v += __shfl_xor(v, NR << k);
+      if (lane < NR) red[m * NR + r] = v;
+    }
   } else {
 #pragma unroll
     for (int v = 0; v < 4; ++v)
       if (4 * h + v < M) red[(p * M + 4 * h + v) * NR + r] = acc[v];
   }
   __syncthreads();
-  // the partials of the workgroup's rows, added in a fixed order: waves, then parities (and for
-  // DOT4 each half's chain, then lo + hi as the C-tile kernel finishes)
   for (int i = threadIdx.x; i < NR * M; i += 64 * nw) {
-    const int m = i / NR, rw = i - m * NR;
-    const int row = row0 + rw;
+    const int row = row0 + (i & (NR - 1));
     if (row >= rows) continue;
     float s = 0.0f;
+    for (int w = 0; w < nw; ++w) {
+      const float *rv = reinterpret_cast<const float *>(kq4_gv_lds + w * SLAB);
+      if (KIND == 0) {
+        s += rv[i];
+      } else {
 #pragma unroll
-    for (int hh = 0; hh < (KIND == 0 ? 2 : 1); ++hh) {
-      float sh = 0.0f;
-      for (int v = 0; v < nw; ++v) {
-        const float *rv = reinterpret_cast<const float *>(kq4_gv_lds + v * SLAB);
-#pragma unroll
-        for (int pp = 0; pp < NP; ++pp) sh += rv[((hh * NP + pp) * M + m) * NR + rw];
+        for (int pp = 0; pp < NP; ++pp) s += rv[pp * M * NR + i];
       }
-      s = hh == 0 ? sh : s + sh;
     }
-    const size_t o = (size_t)m * rows + row;
+    const size_t o = (size_t)(i / NR) * rows + row;
     out[o] = res ? res[o] + s : s;
   }
 }
