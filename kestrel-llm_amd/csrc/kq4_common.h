@@ -72,6 +72,24 @@ KQ4_DEV float kq4_silu_mul(float g, float u) {
   return (g * rec) * u;
 }
 
+// v + v(lane ^ MASK) for MASK = 8, 16, 32 in VALU instructions, no LDS: a DPP row rotate by 8
+// (xor 8 within a 16-lane row), v_permlane16_swap (rows 0<->1, 2<->3) and v_permlane32_swap
+// (lanes 0-31 <-> 32-63). Both lanes of a pair get the same (commutative) sum.
+template <int MASK>
+KQ4_DEV float kq4_xor_add(float v) {
+  static_assert(MASK == 8 || MASK == 16 || MASK == 32, "kq4_xor_add: mask 8, 16 or 32");
+  const uint32_t u = __float_as_uint(v);
+  if constexpr (MASK == 32) {
+    const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  } else if constexpr (MASK == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  } else {
+    return v + __int_as_float(__builtin_amdgcn_update_dpp(0, (int)u, 0x128, 0xf, 0xf, false));
+  }
+}
+
 // 4 x int8 dot product accumulated into c (v_dot4_i32_i8).
 KQ4_DEV int kq4_dot4(uint32_t a, uint32_t b, int c) {
   return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);

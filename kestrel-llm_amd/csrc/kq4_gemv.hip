@@ -32,9 +32,9 @@
 //       MFMA: per block one v_mfma_i32_32x32x32_i8 with A = the tokens' codes (32 rows, M <= 8
 //             used) and B = the lanes' weight operands as they are; the result 16*S is at lane
 //             (row = lane%32, token = 4*(lane/32) + v). Cost independent of M.
-//   * at the end the partials of an output are added in a fixed order (DOT4: each wave's lanes
-//     by shuffles, then the waves' sums through LDS; MFMA: the lanes' partials through LDS, over
-//     waves then parities): deterministic, one launch, no cross-workgroup communication.
+//   * at the end the partials of an output are added in a fixed order, each wave's lanes by lane
+//     swaps, then the waves' sums through LDS: deterministic, one launch, no cross-workgroup
+//     communication.
 #include "kq4_common.h"
 #include "kq4_internal.h"
 
@@ -462,27 +462,30 @@ __global__ __launch_bounds__(1024) void kq4_gemv_kernel(const KQ4GemvArgs a) {
     else kq4_gv_mfma_stage<M, HS, WF>(rw, sq, sx, lane, p, acc);
   }
 
-  // DOT4: each output's lane partials are first added inside the wave (a fixed tree: the two K
-  // halves' chains, then the parities) and the wave's sum goes to its slab at red[m*NR + r]; one
-  // thread per output then adds the waves' sums in wave order. MFMA (whose in-wave shuffles
-  // measured slower): the lanes store red[(p*M + token)*NR + r] and the thread adds them over
-  // waves, then parities. Either order is fixed, so results are deterministic.
+  // Each output's lane partials are first added inside the wave by a fixed tree of lane swaps
+  // (DOT4: the two K halves' chains, then the parities; MFMA: the parities; lane bits 3 and 4 of
+  // quarter sets, bit 4 of half sets), and the wave's sum goes to its slab at red[m*NR + r]; one
+  // thread per output then adds the waves' sums in wave order. The order is fixed, so results
+  // are deterministic.
   float *__restrict__ out = (float *)ms.out;
   const float *__restrict__ res = (const float *)ms.res;
   float *red = reinterpret_cast<float *>(slab);   // only this wave used its slab so far
   if (KIND == 0) {
 #pragma unroll
     for (int m = 0; m < M; ++m) {
-      float v = acc[m];
-      v += __shfl_xor(v, 32);
-#pragma unroll
-      for (int k = 0; k < HS; ++k) v += __shfl_xor(v, NR << k);
+      float v = kq4_xor_add<32>(acc[m]);
+      if (HS == 2) v = kq4_xor_add<8>(v);
+      if (HS >= 1) v = kq4_xor_add<16>(v);
       if (lane < NR) red[m * NR + r] = v;
     }
   } else {
 #pragma unroll
-    for (int v = 0; v < 4; ++v)
-      if (4 * h + v < M) red[(p * M + 4 * h + v) * NR + r] = acc[v];
+    for (int v = 0; v < 4; ++v) {
+      float t = acc[v];
+      if (HS == 2) t = kq4_xor_add<8>(t);
+      if (HS >= 1) t = kq4_xor_add<16>(t);
+      if (p == 0 && 4 * h + v < M) red[(4 * h + v) * NR + r] = t;
+    }
   }
   __syncthreads();
   for (int i = threadIdx.x; i < NR * M; i += 64 * nw) {
@@ -494,8 +497,7 @@ __global__ __launch_bounds__(1024) void kq4_gemv_kernel(const KQ4GemvArgs a) {
       if (KIND == 0) {
         s += rv[i];
       } else {
-#pragma unroll
-        for (int pp = 0; pp < NP; ++pp) s += rv[pp * M * NR + i];
+        s += rv[i];
       }
     }
     const size_t o = (size_t)(i / NR) * rows + row;
