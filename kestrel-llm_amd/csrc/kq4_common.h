@@ -90,6 +90,16 @@ KQ4_DEV float kq4_xor_add(float v) {
   }
 }
 
+// max of v over the lane quad (lanes 4q .. 4q+3) by two DPP quad permutes (xor 1, xor 2): VALU
+// only, no LDS round trip. For non-NaN values every lane of the quad gets the same maximum.
+KQ4_DEV float kq4_quad_max(float v) {
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xf, 0xf,
+                                                          false)));   // quad_perm [1,0,3,2]
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xf, 0xf,
+                                                          false)));   // quad_perm [2,3,0,1]
+  return v;
+}
+
 // 4 x int8 dot product accumulated into c (v_dot4_i32_i8).
 KQ4_DEV int kq4_dot4(uint32_t a, uint32_t b, int c) {
   return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);

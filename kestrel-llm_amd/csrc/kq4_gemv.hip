@@ -252,8 +252,7 @@ KQ4_DEV void kq4_gv_act_put(const KQ4GvAct<M, FQ, WF> &r, const KQ4GemvArgs &a, 
       float amax = 1e-10f;
 #pragma unroll
       for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
-      amax = fmaxf(amax, __shfl_xor(amax, 1));
-      amax = fmaxf(amax, __shfl_xor(amax, 2));
+      amax = kq4_quad_max(amax);
       const float d = amax / 127.0f;
       const float y = 1.0f / d;
       uint32_t pk[2] = {0, 0};

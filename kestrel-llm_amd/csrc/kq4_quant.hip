@@ -9,8 +9,8 @@
 #include "kq4_internal.h"
 
 // A lane quad per block: each lane reads 8 consecutive floats (two 16-B loads; a wave's load
-// instruction covers 16 blocks = 1 KB), the quad's max takes two shuffles, and each lane writes its
-// 8 codes as one 8-byte store.
+// instruction covers 16 blocks = 1 KB), the quad's max takes two DPP quad permutes, and each lane
+// writes its 8 codes as one 8-byte store.
 __global__ __launch_bounds__(256) void kq4_quantize_kernel(const float *__restrict__ x,
                                                            const float *__restrict__ up,
                                                            int8_t *__restrict__ xq,
@@ -37,8 +37,7 @@ __global__ __launch_bounds__(256) void kq4_quantize_kernel(const float *__restri
   float a = 1e-10f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) a = fmaxf(a, fabsf(v[i]));
-  a = fmaxf(a, __shfl_xor(a, 1));
-  a = fmaxf(a, __shfl_xor(a, 2));
+  a = kq4_quad_max(a);
   const float d = a / 127.0f;
   uint32_t pk[2] = {0, 0};
 #pragma unroll
@@ -207,8 +206,7 @@ __global__ __launch_bounds__(KQ4_RMS_THREADS) void kq4_rms_norm_kernel(
       float a = 1e-10f;
 #pragma unroll
       for (int i = 0; i < 8; ++i) a = fmaxf(a, fabsf(o[i]));
-      a = fmaxf(a, __shfl_xor(a, 1));
-      a = fmaxf(a, __shfl_xor(a, 2));
+      a = kq4_quad_max(a);
       const float dq = a / 127.0f;
       uint32_t pk[2] = {0, 0};
 #pragma unroll
