@@ -68,43 +68,116 @@ KQ4_DEV void kq4_moe_touch(uint32_t (&a)[N]) {
 // The k largest logits, ties to the smaller id, in order: the reference's insertion top-k
 // (:12968-12984) gives the same list (a NaN logit is never inserted; -inf is, into an empty
 // slot). Then p = fl(exp(l - max)) summed in rank order, scaled by fl(1/sum).
+//
+// Lane l holds the logits of experts l, l+64, .. in registers (read once). A candidate is the
+// 64-bit key (order-preserving bits of the logit, ~id), so the wave maximum of the keys is the
+// largest logit with ties to the smaller id; -0 is keyed as +0 (the reference compares values),
+// NaN is never a candidate, and 0 means none. The maximum takes DPP quad permutes and row
+// rotates and the two permlane swaps: VALU only. Each round only the winner's lane rescans.
+template <int CTRL>
+KQ4_DEV uint64_t kq4_dpp64(uint64_t v) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)v, CTRL, 0xf, 0xf, false);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(v >> 32), CTRL, 0xf, 0xf, false);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+KQ4_DEV uint64_t kq4_max_u64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+
+KQ4_DEV uint64_t kq4_wave_max_u64(uint64_t k) {
+  k = kq4_max_u64(k, kq4_dpp64<0xB1>(k));    // quad_perm [1,0,3,2]
+  k = kq4_max_u64(k, kq4_dpp64<0x4E>(k));    // quad_perm [2,3,0,1]
+  k = kq4_max_u64(k, kq4_dpp64<0x124>(k));   // row_ror:4 (the quads of a 16-lane row)
+  k = kq4_max_u64(k, kq4_dpp64<0x128>(k));   // row_ror:8
+  {
+    const uint32_t lo = (uint32_t)k, hi = (uint32_t)(k >> 32);
+    const auto a = __builtin_amdgcn_permlane16_swap(lo, lo, false, false);
+    const auto b = __builtin_amdgcn_permlane16_swap(hi, hi, false, false);
+    k = kq4_max_u64(((uint64_t)b[0] << 32) | a[0], ((uint64_t)b[1] << 32) | a[1]);
+  }
+  {
+    const uint32_t lo = (uint32_t)k, hi = (uint32_t)(k >> 32);
+    const auto a = __builtin_amdgcn_permlane32_swap(lo, lo, false, false);
+    const auto b = __builtin_amdgcn_permlane32_swap(hi, hi, false, false);
+    k = kq4_max_u64(((uint64_t)b[0] << 32) | a[0], ((uint64_t)b[1] << 32) | a[1]);
+  }
+  return k;
+}
+
+KQ4_DEV uint64_t kq4_route_key(float v, int e) {
+  const uint32_t u = __float_as_uint(v + 0.0f);   // -0 -> +0
+  const uint32_t o = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return ((uint64_t)o << 32) | (0xFFFFFFFFu - (uint32_t)e);
+}
+
+KQ4_DEV float kq4_route_val(uint64_t key) {
+  const uint32_t o = (uint32_t)(key >> 32);
+  return __uint_as_float((o & 0x80000000u) ? (o & 0x7FFFFFFFu) : ~o);
+}
+
 __global__ __launch_bounds__(256) void kq4_moe_route_kernel(int *__restrict__ sel,
                                                             float *__restrict__ pr,
                                                             const float *__restrict__ logits,
                                                             int T, int ne, int tk) {
+  constexpr int NV = KQ4_MOE_MAXNE / 64;   // logits per lane at most
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
   if (t >= T) return;   // whole waves
   const float *lg = logits + (size_t)t * ne;
-  uint32_t taken = 0;   // bit i: this lane's expert lane + 64*i is already selected
-  for (int k = 0; k < tk; ++k) {
-    float bv = -INFINITY;
-    int be = -1;
-    for (int i = 0, e = lane; e < ne; ++i, e += 64) {
-      const float v = lg[e];
-      if (!((taken >> i) & 1u) && v == v && (be < 0 || v > bv)) { bv = v; be = e; }
-    }
-    // wave arg-max, ties to the smaller id (-1 = no candidate)
+  const int nv = (ne + 63) >> 6;   // uniform
+  float vals[NV];
 #pragma unroll
-    for (int s = 32; s > 0; s >>= 1) {
-      const float ov = __shfl_xor(bv, s);
-      const int oe = __shfl_xor(be, s);
-      if (oe >= 0 && (be < 0 || ov > bv || (ov == bv && oe < be))) { bv = ov; be = oe; }
+  for (int i = 0; i < NV; ++i) {
+    if (i >= nv) break;
+    const int e = lane + 64 * i;
+    vals[i] = e < ne ? lg[e] : __builtin_nanf("");
+  }
+  uint32_t taken = 0;   // bit i: this lane's expert lane + 64*i is already selected
+  auto local_best = [&]() {
+    uint64_t best = 0;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      if (i >= nv) break;
+      const float v = vals[i];
+      if (!((taken >> i) & 1u) && v == v) best = kq4_max_u64(best, kq4_route_key(v, lane + 64 * i));
     }
-    if (be >= 0 && (be & 63) == lane) taken |= 1u << (be >> 6);
-    if (lane == 0) {
-      sel[(size_t)t * tk + k] = be;
-      pr[(size_t)t * tk + k] = be >= 0 ? bv : -INFINITY;   // the logit, until the pass below
+    return best;
+  };
+  uint64_t mine = local_best();
+  int sk[KQ4_MOE_MAXTK];
+  float vk[KQ4_MOE_MAXTK];
+#pragma unroll
+  for (int k = 0; k < KQ4_MOE_MAXTK; ++k) {
+    if (k >= tk) break;
+    const uint64_t key = kq4_wave_max_u64(mine);
+    const int be = key ? (int)(0xFFFFFFFFu - (uint32_t)key) : -1;
+    sk[k] = be;
+    vk[k] = be >= 0 ? kq4_route_val(key) : -INFINITY;   // the logit, until the pass below
+    if (be >= 0 && (be & 63) == lane) {
+      taken |= 1u << (be >> 6);
+      mine = local_best();
     }
   }
-  if (lane == 0) {
-    float *pt = pr + (size_t)t * tk;
-    float mx = -INFINITY;
-    for (int k = 0; k < tk; ++k) mx = pt[k] > mx ? pt[k] : mx;
-    float sum = 0.0f;
-    for (int k = 0; k < tk; ++k) sum += kq4_expf(pt[k] - mx);
-    const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
-    for (int k = 0; k < tk; ++k) pt[k] = kq4_expf(pt[k] - mx) * inv;
+  // softmax over the k picks: lane k forms p_k = fl(exp(l_k - max)) (the picks are the same in
+  // every lane), the p_k are summed in rank order (lane reads), lane k writes fl(p_k * fl(1/sum))
+  float mx = -INFINITY, lk = -INFINITY;
+  int sid = -1;
+#pragma unroll
+  for (int k = 0; k < KQ4_MOE_MAXTK; ++k) {
+    if (k >= tk) break;
+    mx = vk[k] > mx ? vk[k] : mx;
+    if (lane == k) { lk = vk[k]; sid = sk[k]; }
+  }
+  const float pk = lane < tk ? kq4_expf(lk - mx) : 0.0f;
+  float sum = 0.0f;
+#pragma unroll
+  for (int k = 0; k < KQ4_MOE_MAXTK; ++k) {
+    if (k >= tk) break;
+    sum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pk), k));
+  }
+  const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
+  if (lane < tk) {
+    sel[(size_t)t * tk + lane] = sid;
+    pr[(size_t)t * tk + lane] = pk * inv;
   }
 }
 

@@ -47,6 +47,33 @@ def test_route(kq4, torch_dev, orc):
     assert ulps(host(pr), pr_o) <= 2
 
 
+@pytest.mark.parametrize("ne,tk", [(100, 8), (2048, 32), (64, 1)])
+def test_route_edge_cases(kq4, torch_dev, orc, ne, tk):
+    """Ragged expert counts, the largest ne and top-k, NaN / -inf / signed-zero logits, ties,
+    and tokens with fewer than k candidates (their tail ids are -1, probabilities 0)."""
+    torch = torch_dev
+    T = 6
+    lg = synth.make_logits(T, ne, 17 + ne)
+    lg[1, ::3] = np.nan
+    lg[1, 1::7] = -np.inf
+    lg[2, :] = 0.5                                   # all tied: ids 0 .. tk-1 in order
+    lg[3, :] = 0.0
+    lg[3, ::2] = -0.0                                # +0 and -0 compare equal: ties by id
+    lg[4, :] = np.nan
+    lg[4, [ne - 1, ne // 2, 0][:min(3, ne)]] = [1.0, -np.inf, 2.0][:min(3, ne)]
+    lg[5, :] = -np.inf                               # only -inf candidates
+    lg[5, ne // 3] = 3.0
+    sel_o, pr_o = orc.moe_route(lg, tk)
+    sel = torch.empty((T, tk), dtype=torch.int32, device="cuda")
+    pr = torch.empty((T, tk), dtype=torch.float32, device="cuda")
+    kq4.moe_route_dev(sel, pr, to_dev(torch, lg), tk)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(sel), sel_o)
+    assert np.array_equal(np.isnan(host(pr)), np.isnan(pr_o))
+    fin = ~np.isnan(pr_o)
+    assert ulps(host(pr)[fin], pr_o[fin]) <= 2
+
+
 @pytest.mark.parametrize("T", [1, 7, 64])
 @pytest.mark.parametrize("shape", ["small", "qwen3_30b_a3b"])
 def test_moe_stages(kq4, torch_dev, orc, shape, T):
