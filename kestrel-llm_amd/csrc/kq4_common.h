@@ -100,6 +100,15 @@ KQ4_DEV float kq4_quad_max(float v) {
   return v;
 }
 
+// 16-byte load with the non-temporal hint (global_load_dwordx4 ... nt), for data read once per
+// launch (weight streams): measured on MI355X, plain streaming reads of 7-56 MB run 9-14 %
+// faster with it than without.
+typedef unsigned int kq4_v4u __attribute__((ext_vector_type(4)));
+KQ4_DEV uint4 kq4_ld_nt(const void *p) {
+  const kq4_v4u v = __builtin_nontemporal_load(reinterpret_cast<const kq4_v4u *>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 // 4 x int8 dot product accumulated into c (v_dot4_i32_i8).
 KQ4_DEV int kq4_dot4(uint32_t a, uint32_t b, int c) {
   return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);

@@ -94,18 +94,19 @@ struct KQ4GvStage {
 template <int HS, int WF>
 KQ4_DEV void kq4_gv_load(KQ4GvStage<HS> &st, const uint8_t *__restrict__ chunk, int rr, int h,
                          int p) {
+  // the weights are read once per launch: non-temporal loads
   const uint4 *sc = reinterpret_cast<const uint4 *>(chunk + 8192) + rr;
-  const uint4 a = sc[0];
+  const uint4 a = kq4_ld_nt(sc);
   st.sc[0] = a.x; st.sc[1] = a.y; st.sc[2] = a.z; st.sc[3] = a.w;
   if (WF == 0) {
-    const uint4 b = sc[32];
+    const uint4 b = kq4_ld_nt(sc + 32);
     st.sc[4] = b.x; st.sc[5] = b.y; st.sc[6] = b.z; st.sc[7] = b.w;
   }
   const uint4 *src = reinterpret_cast<const uint4 *>(chunk) + rr + 32 * h;
 #pragma unroll
   for (int u = 0; u < KQ4GvStage<HS>::NU; ++u) {
     const int i = (u << HS) + p;
-    const uint4 v = src[64 * i];
+    const uint4 v = kq4_ld_nt(src + 64 * i);
     st.n[4 * u] = v.x; st.n[4 * u + 1] = v.y; st.n[4 * u + 2] = v.z; st.n[4 * u + 3] = v.w;
   }
 }
