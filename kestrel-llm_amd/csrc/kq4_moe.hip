@@ -371,16 +371,17 @@ struct KQ4MoeW {
 template <int NU, int NS>
 KQ4_DEV void kq4_moe_wload(KQ4MoeW<NU, NS> &w, const uint8_t *__restrict__ chunk, int lane, int u0,
                            int sh) {
+  // each chunk is read once per launch: non-temporal loads
   const uint4 *sc = reinterpret_cast<const uint4 *>(chunk + 8192) + (lane & 31);
 #pragma unroll
   for (int i = 0; i < NS; ++i) {
-    const uint4 v = sc[32 * (NS == 2 ? i : sh)];
+    const uint4 v = kq4_ld_nt(sc + 32 * (NS == 2 ? i : sh));
     w.sc[4 * i] = v.x; w.sc[4 * i + 1] = v.y; w.sc[4 * i + 2] = v.z; w.sc[4 * i + 3] = v.w;
   }
   const uint4 *src = reinterpret_cast<const uint4 *>(chunk) + lane;
 #pragma unroll
   for (int u = 0; u < NU; ++u) {
-    const uint4 v = src[64 * (u0 + u)];
+    const uint4 v = kq4_ld_nt(src + 64 * (u0 + u));
     w.n[4 * u] = v.x; w.n[4 * u + 1] = v.y; w.n[4 * u + 2] = v.z; w.n[4 * u + 3] = v.w;
   }
 }
