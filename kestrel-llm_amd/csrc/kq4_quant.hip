@@ -8,6 +8,8 @@
 #include "kq4_common.h"
 #include "kq4_internal.h"
 
+#include <stdlib.h>
+
 // A lane quad per block: each lane reads 8 consecutive floats (two 16-B loads; a wave's load
 // instruction covers 16 blocks = 1 KB), the quad's max takes two DPP quad permutes, and each lane
 // writes its 8 codes as one 8-byte store.
@@ -115,16 +117,21 @@ int kq4_launch_silu_mul(float *g, const float *u, long n, hipStream_t stream) {
 //     LDS, then one lane adds the d/8 chunk sums in order;
 //   serial (dyn_rms_norm_batch's default): the threads square every element into LDS, one lane
 //     adds the d squares in order.
-// Thread i holds chunks i, i+256, .. (CPT of them) of x and w in registers from the start, so the
-// only global-memory wait is the first. Then each thread normalises its chunks and, when xq is
-// given, quantizes them as kq4_quantize_kernel does (a lane quad per 32-block,
-// quantize_row_q8_0_act :7893-7920).
+// Thread i takes chunks i, i+256, .. (CPT of them). HOLD = 1 (a few tokens: the latency of one
+// token is what counts) keeps them and w's in registers from the start, so the only global-memory
+// wait is the first; HOLD = 0 (many tokens: the workgroups resident at once are what count) reads
+// them again after the sum, so a wave needs about 40 registers and a CU holds 8 workgroups.
+// The serial lane reads its terms from LDS 32 at a time. Then each thread normalises its
+// chunks and, when xq is given, quantizes them as kq4_quantize_kernel does (a lane quad per
+// 32-block, quantize_row_q8_0_act :7893-7920).
 // d % 8 == 0 (d % 32 == 0 to quantize), d <= 2048 * CPT; rows 16-byte aligned. out may be x (in
-// place, as the reference calls it at :19607): all of x is read before anything is written.
+// place, as the reference calls it at :19607): every workgroup reads its own row before the
+// barrier that precedes its writes, and re-reads (HOLD = 0) only that row.
 #define KQ4_RMS_THREADS 256
-#define KQ4_RMS_BATCH 64   // terms the serial lane reads from LDS at once
+#define KQ4_RMS_HOLD_MAX 256   // tokens up to which x and w stay in registers
+#define KQ4_RMS_BATCH 32   // terms the serial lane reads from LDS at once
 
-template <int CPT>
+template <int CPT, int HOLD>
 __global__ __launch_bounds__(KQ4_RMS_THREADS) void kq4_rms_norm_kernel(
     const float *x, const float *__restrict__ w, float *out, int8_t *__restrict__ xq,
     float *__restrict__ xd, int d, float eps, int serial) {
@@ -133,29 +140,38 @@ __global__ __launch_bounds__(KQ4_RMS_THREADS) void kq4_rms_norm_kernel(
   const int t = blockIdx.x;
   const float *xr = x + (size_t)t * d;
   const int nc = d >> 3;
-  float v[CPT][8], wv[CPT][8];
-#pragma unroll
-  for (int j = 0; j < CPT; ++j) {
-    const int c = threadIdx.x + KQ4_RMS_THREADS * j;
-    float4 a = make_float4(0, 0, 0, 0), b = a, wa = a, wb = a;
+  auto load8 = [&](const float *p, int c, float *o) {
+    float4 a = make_float4(0, 0, 0, 0), b = a;
     if (c < nc) {
-      a = *reinterpret_cast<const float4 *>(xr + 8 * c);
-      b = *reinterpret_cast<const float4 *>(xr + 8 * c + 4);
-      wa = *reinterpret_cast<const float4 *>(w + 8 * c);
-      wb = *reinterpret_cast<const float4 *>(w + 8 * c + 4);
+      a = *reinterpret_cast<const float4 *>(p + 8 * c);
+      b = *reinterpret_cast<const float4 *>(p + 8 * c + 4);
     }
-    v[j][0] = a.x; v[j][1] = a.y; v[j][2] = a.z; v[j][3] = a.w;
-    v[j][4] = b.x; v[j][5] = b.y; v[j][6] = b.z; v[j][7] = b.w;
-    wv[j][0] = wa.x; wv[j][1] = wa.y; wv[j][2] = wa.z; wv[j][3] = wa.w;
-    wv[j][4] = wb.x; wv[j][5] = wb.y; wv[j][6] = wb.z; wv[j][7] = wb.w;
+    o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w;
+    o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
+  };
+  float v[HOLD ? CPT : 1][8], wv[HOLD ? CPT : 1][8];
+  if (HOLD) {
+#pragma unroll
+    for (int j = 0; j < CPT; ++j) {
+      const int c = threadIdx.x + KQ4_RMS_THREADS * j;
+      load8(xr, c, v[HOLD ? j : 0]);
+      load8(w, c, wv[HOLD ? j : 0]);
+    }
   }
 #pragma unroll
   for (int j = 0; j < CPT; ++j) {
     const int c = threadIdx.x + KQ4_RMS_THREADS * j;
+    float vj[8];
+    if (HOLD) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) vj[k] = v[HOLD ? j : 0][k];
+    } else {
+      load8(xr, c, vj);
+    }
     if (c < nc) {
       float q[8];
 #pragma unroll
-      for (int k = 0; k < 8; ++k) q[k] = v[j][k] * v[j][k];
+      for (int k = 0; k < 8; ++k) q[k] = vj[k] * vj[k];
       if (serial) {
         *reinterpret_cast<float4 *>(kq4_rms_lds + 8 * c) = make_float4(q[0], q[1], q[2], q[3]);
         *reinterpret_cast<float4 *>(kq4_rms_lds + 8 * c + 4) = make_float4(q[4], q[5], q[6], q[7]);
@@ -169,8 +185,10 @@ __global__ __launch_bounds__(KQ4_RMS_THREADS) void kq4_rms_norm_kernel(
   const int npad = (n + KQ4_RMS_BATCH - 1) & ~(KQ4_RMS_BATCH - 1);
   for (int i = n + threadIdx.x; i < npad; i += KQ4_RMS_THREADS) kq4_rms_lds[i] = 0.0f;
   __syncthreads();
-  if (threadIdx.x == 0) {
-    // one dependent add per term, KQ4_RMS_BATCH terms read at a time
+  // the chain lane: lane 0 of wave (t % 4), so that the chains of a CU's workgroups spread over
+  // its four SIMDs
+  if (threadIdx.x == 64 * (t & 3)) {
+    // one dependent add per term, KQ4_RMS_BATCH terms read at a time (each consumed as it lands)
     float ss = 0.0f;
     for (int i = 0; i < npad; i += KQ4_RMS_BATCH) {
       float4 b[KQ4_RMS_BATCH / 4];
@@ -195,9 +213,20 @@ __global__ __launch_bounds__(KQ4_RMS_THREADS) void kq4_rms_norm_kernel(
   for (int j = 0; j < CPT; ++j) {
     const int c = threadIdx.x + KQ4_RMS_THREADS * j;
     const bool live = c < nc;
+    float vj[8], wj[8];
+    if (HOLD) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        vj[k] = v[HOLD ? j : 0][k];
+        wj[k] = wv[HOLD ? j : 0][k];
+      }
+    } else {
+      load8(xr, c, vj);
+      load8(w, c, wj);
+    }
     float o[8];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) o[k] = v[j][k] * rms * wv[j][k];
+    for (int k = 0; k < 8; ++k) o[k] = vj[k] * rms * wj[k];
     if (live && orow) {
       *reinterpret_cast<float4 *>(orow + 8 * c) = make_float4(o[0], o[1], o[2], o[3]);
       *reinterpret_cast<float4 *>(orow + 8 * c + 4) = make_float4(o[4], o[5], o[6], o[7]);
@@ -228,22 +257,36 @@ size_t kq4_rms_norm_lds(int d, int serial) {
   return (size_t)((n + KQ4_RMS_BATCH - 1) & ~(KQ4_RMS_BATCH - 1)) * sizeof(float);
 }
 
-template <int CPT>
-static hipError_t rms_launch(const float *x, const float *w, float *out, int8_t *xq, float *xd,
-                             int n_batch, int d, float eps, int serial, hipStream_t s) {
+template <int CPT, int HOLD>
+static hipError_t rms_launch_h(const float *x, const float *w, float *out, int8_t *xq, float *xd,
+                               int n_batch, int d, float eps, int serial, hipStream_t s) {
   // the serial order keeps d squares in LDS (64 KB at d = 16384); the kernel's static LDS (the
   // broadcast rms) comes off the 160 KB a workgroup may hold
   static bool attr = false;
   if (!attr) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&kq4_rms_norm_kernel<CPT>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       160 * 1024 - 1024);
+    hipError_t e = hipFuncSetAttribute(
+        reinterpret_cast<const void *>(&kq4_rms_norm_kernel<CPT, HOLD>),
+        hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024 - 1024);
     if (e != hipSuccess) return e;
     attr = true;
   }
-  hipLaunchKernelGGL((kq4_rms_norm_kernel<CPT>), dim3(n_batch), dim3(KQ4_RMS_THREADS),
+  hipLaunchKernelGGL((kq4_rms_norm_kernel<CPT, HOLD>), dim3(n_batch), dim3(KQ4_RMS_THREADS),
                      kq4_rms_norm_lds(d, serial), s, x, w, out, xq, xd, d, eps, serial);
   return hipGetLastError();
+}
+
+// Registers held (HOLD = 1) up to KQ4_RMS_HOLD_MAX tokens, re-read beyond (KQ4_RMS_HOLD_MAX in the
+// environment overrides it, for measurement).
+template <int CPT>
+static hipError_t rms_launch(const float *x, const float *w, float *out, int8_t *xq, float *xd,
+                             int n_batch, int d, float eps, int serial, hipStream_t s) {
+  static const int hold_max = [] {
+    const char *e = getenv("KQ4_RMS_HOLD_MAX");
+    return e ? atoi(e) : KQ4_RMS_HOLD_MAX;
+  }();
+  if (n_batch <= hold_max)
+    return rms_launch_h<CPT, 1>(x, w, out, xq, xd, n_batch, d, eps, serial, s);
+  return rms_launch_h<CPT, 0>(x, w, out, xq, xd, n_batch, d, eps, serial, s);
 }
 
 int kq4_launch_rms_norm(const float *x, const float *w, float *out, int8_t *xq, float *xd,

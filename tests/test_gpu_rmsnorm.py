@@ -32,9 +32,11 @@ def rows(n, d, seed):
     return x, w
 
 
+# (300, 1032) and (513, 4096): the serial order's many-token path (one chain per lane, then the
+# normalisation), with a ragged last wave of tokens
 @pytest.mark.parametrize("order", [0, 1])
 @pytest.mark.parametrize("n,d", [(1, 8), (3, 64), (1, 2048), (5, 4096), (64, 2048), (2, 8200),
-                                 (1, 16384)])
+                                 (1, 16384), (300, 1032), (513, 4096)])
 def test_rms_norm_bit_exact(kq4, torch_dev, orc, n, d, order):
     torch = torch_dev
     x, w = rows(n, d, d + n)
@@ -49,7 +51,7 @@ CASES = [([20, 8, 8], 160), ([2048, 512, 512], 2048), ([6144, 6144], 2048),
          ([4096, 1024, 1024], 4096)]
 
 
-@pytest.mark.parametrize("n", [1, 2, 4, 8, 16, 33])
+@pytest.mark.parametrize("n", [1, 2, 4, 8, 16, 33, 300])
 @pytest.mark.parametrize("mats,cols", CASES)
 def test_rmsnorm_matmul_multi(kq4, torch_dev, orc, mats, cols, n):
     torch = torch_dev
