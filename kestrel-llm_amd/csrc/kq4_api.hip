@@ -338,7 +338,7 @@ int moe_impl(float *Y, const float *X, const int *sel, const float *pr, int T, i
   if (rc) return rc;
   const size_t np = (size_t)T * tk;
   const size_t need = al256((ne + 1) * sizeof(int)) + al256(np * sizeof(int)) +
-                      al256(ne * sizeof(int)) + al256((size_t)T * d) +
+                      al256((size_t)ne * KQ4_MOE_REC * sizeof(int)) + al256((size_t)T * d) +
                       al256((size_t)T * (d / 32) * sizeof(float)) + al256(np * ef) +
                       al256(np * (ef / 32) * sizeof(float)) + al256(np * d * sizeof(float));
   if ((rc = ensure(ds->ws, need))) return rc;
@@ -346,7 +346,7 @@ int moe_impl(float *Y, const float *X, const int *sel, const float *pr, int T, i
   KQ4MoeWs ws;
   ws.ex_off = cv.take<int>(ne + 1);
   ws.ex_pair = cv.take<int>(np);
-  ws.act = cv.take<int>(ne);
+  ws.rec = cv.take<int>((size_t)ne * KQ4_MOE_REC);
   ws.xq = cv.take<int8_t>((size_t)T * d);
   ws.xd = cv.take<float>((size_t)T * (d / 32));
   ws.avq = cv.take<int8_t>(np * ef);

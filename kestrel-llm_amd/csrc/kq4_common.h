@@ -109,6 +109,19 @@ KQ4_DEV uint4 kq4_ld_nt(const void *p) {
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// max of v over each 32-lane half of the wave (lanes 0-31, 32-63): the quad max, DPP row rotates
+// by 4 and 8 (the 16-lane row), then v_permlane16_swap (rows 0<->1, 2<->3). VALU only.
+KQ4_DEV float kq4_max32(float v) {
+  v = kq4_quad_max(v);
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x124, 0xf, 0xf,
+                                                          false)));   // row_ror:4
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xf, 0xf,
+                                                          false)));   // row_ror:8
+  const uint32_t u = __float_as_uint(v);
+  const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
 // 4 x int8 dot product accumulated into c (v_dot4_i32_i8).
 KQ4_DEV int kq4_dot4(uint32_t a, uint32_t b, int c) {
   return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);

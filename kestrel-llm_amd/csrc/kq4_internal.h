@@ -89,10 +89,13 @@ int kq4_launch_moe_route(int *sel, float *pr, const float *logits, int T, int ne
 // (token, expert); d % 32 == 0, rows 16-byte aligned.
 int kq4_launch_moe_logits(float *logits, const float *router, const float *X, int T, int ne,
                           int d, hipStream_t stream);
+#define KQ4_MOE_REC 16     // ints per slot record (3 header + 12 pair ids + 1 spare)
+#define KQ4_MOE_RECP 12    // pair ids a slot record holds
 struct KQ4MoeWs {
   int *ex_off;   // [ne+1]
   int *ex_pair;  // [T*tk] (t*tk+j) grouped by expert
-  int *act;      // [ne] active experts in id order, -1 past them
+  int *rec;      // [ne][KQ4_MOE_REC] slot records (active experts in id order): expert (-1 past
+                 // them), offset of its pairs in ex_pair, pair count, its first pair ids
   int8_t *xq;    // [T][d]
   float *xd;     // [T][d/32]
   int8_t *avq;   // [T*tk][ef]

@@ -280,16 +280,20 @@ int kq4_launch_moe_logits(float *logits, const float *router, const float *X, in
 // Workgroup 0 builds the expert -> (token, rank) table: counts by LDS atomics, an exclusive scan,
 // then each pair takes a slot by an atomic cursor. The order of an expert's pairs is whatever the
 // atomics give: every pair is computed on its own (its own MFMA token row, its own fp32 chain), so
-// no output depends on it. It also lists the active experts in id order (act[s], -1 past them).
+// no output depends on it. It also writes one record per slot (the active experts in id order):
+// rec[16s] = expert (-1 for slots [active, nslot)), rec[16s+1] = the offset of its pairs in
+// ex_pair, rec[16s+2] = their count, rec[16s+4 ..] = its first KQ4_MOE_RECP pair ids, so an
+// expert workgroup finds its expert and pairs with one load instead of a chain of three.
 // Workgroups 1..: the activation quantizer of kq4_quant.hip (one half-wave per 32-block).
 __global__ __launch_bounds__(256) void kq4_moe_prep_kernel(
-    int *__restrict__ ex_off, int *__restrict__ ex_pair, int *__restrict__ act,
+    int *__restrict__ ex_off, int *__restrict__ ex_pair, int *__restrict__ rec, int nslot,
     const int *__restrict__ sel, int n_pairs, int ne, const float *__restrict__ X,
     int8_t *__restrict__ xq, float *__restrict__ xd, int T, int d) {
   if (blockIdx.x == 0) {
-    // LDS: cnt[ne], cursor[ne], per-thread partial sums [2][blockDim]
+    // LDS: cnt[ne] (then each expert's offset), cursor[ne], slot[ne], partial sums [2][blockDim]
     extern __shared__ int kq4_moe_cnt[];
-    int *cnt = kq4_moe_cnt, *cur = kq4_moe_cnt + ne, *part = kq4_moe_cnt + 2 * ne;
+    int *cnt = kq4_moe_cnt, *cur = kq4_moe_cnt + ne, *slt = kq4_moe_cnt + 2 * ne,
+        *part = kq4_moe_cnt + 3 * ne;
     const int nt = blockDim.x, tid = threadIdx.x;
     // the first 4 * blockDim pairs' expert ids stay in registers for the scatter below
     int ev[4];
@@ -324,21 +328,30 @@ __global__ __launch_bounds__(256) void kq4_moe_prep_kernel(
     for (int e = e0; e < e0 + per && e < ne; ++e) {
       const int c = cnt[e];
       cur[e] = acc;
+      cnt[e] = acc;
       ex_off[e] = acc;
-      if (c) act[na++] = e;
+      if (c) {
+        rec[KQ4_MOE_REC * na] = e;
+        rec[KQ4_MOE_REC * na + 1] = acc;
+        rec[KQ4_MOE_REC * na + 2] = c;
+        slt[e] = na++;
+      }
       acc += c;
     }
-    if (tid == nt - 1) {
-      ex_off[ne] = part[nt - 1];
-      for (int s = part[2 * nt - 1]; s < ne; ++s) act[s] = -1;
-    }
+    if (tid == nt - 1) ex_off[ne] = part[nt - 1];
     __syncthreads();
+    for (int s = part[2 * nt - 1] + tid; s < nslot; s += nt) rec[KQ4_MOE_REC * s] = -1;
+    auto place = [&](int e, int i) {   // pair i of expert e
+      const int pos = atomicAdd(&cur[e], 1);
+      ex_pair[pos] = i;
+      if (pos - cnt[e] < KQ4_MOE_RECP) rec[KQ4_MOE_REC * slt[e] + 4 + pos - cnt[e]] = i;
+    };
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-      if (ev[j] >= 0 && ev[j] < ne) ex_pair[atomicAdd(&cur[ev[j]], 1)] = tid + nt * j;
+      if (ev[j] >= 0 && ev[j] < ne) place(ev[j], tid + nt * j);
     for (int i = tid + 4 * nt; i < n_pairs; i += nt) {
       const int e = sel[i];
-      if (e >= 0 && e < ne) ex_pair[atomicAdd(&cur[e], 1)] = i;
+      if (e >= 0 && e < ne) place(e, i);
     }
     return;
   }
@@ -347,9 +360,7 @@ __global__ __launch_bounds__(256) void kq4_moe_prep_kernel(
   const long blk = (long)(blockIdx.x - 1) * (blockDim.x >> 5) + (threadIdx.x >> 5);
   if (blk >= (long)T * nb) return;   // whole 32-lane halves exit together
   const float v = X[blk * 32 + lane];
-  float a = fmaxf(fabsf(v), 1e-10f);
-#pragma unroll
-  for (int s = 16; s > 0; s >>= 1) a = fmaxf(a, __shfl_xor(a, s, 32));
+  const float a = kq4_max32(fmaxf(fabsf(v), 1e-10f));
   const float dq = a / 127.0f;
   int q = (int)(v / dq + 0.5f);
   q = q > 127 ? 127 : (q < -127 ? -127 : q);
@@ -358,6 +369,39 @@ __global__ __launch_bounds__(256) void kq4_moe_prep_kernel(
 }
 
 // ---- shared pieces of the expert kernels ----------------------------------------------------
+
+// Slot s's record (written by the prep kernel), the header and the first NI pair ids: uniform
+// loads kept in scalar registers.
+template <int NI>
+struct KQ4MoeSlot {
+  int r[4 + NI];
+};
+
+template <int NI>
+KQ4_DEV KQ4MoeSlot<NI> kq4_moe_slot(const int *__restrict__ rec, int slot) {
+  static_assert(NI % 4 == 0 && NI <= KQ4_MOE_RECP, "kq4_moe_slot: 0, 4, 8 or 12 pair ids");
+  KQ4MoeSlot<NI> s;
+  const int4 *p = reinterpret_cast<const int4 *>(rec + KQ4_MOE_REC * slot);
+#pragma unroll
+  for (int k = 0; k < 1 + NI / 4; ++k) {
+    const int4 v = p[k];
+    s.r[4 * k] = __builtin_amdgcn_readfirstlane(v.x);
+    s.r[4 * k + 1] = __builtin_amdgcn_readfirstlane(v.y);
+    s.r[4 * k + 2] = __builtin_amdgcn_readfirstlane(v.z);
+    s.r[4 * k + 3] = __builtin_amdgcn_readfirstlane(v.w);
+  }
+  return s;
+}
+
+template <int NI>
+KQ4_DEV int kq4_moe_pair(const KQ4MoeSlot<NI> &s, const int *__restrict__ ex_pair, int j) {
+  static_assert(NI <= KQ4_MOE_RECP, "kq4_moe_pair: the record holds KQ4_MOE_RECP pair ids");
+  if (j >= NI) return ex_pair[s.r[1] + j];
+  uint32_t v = 0;
+#pragma unroll
+  for (int k = 0; k < NI; ++k) v |= (uint32_t)s.r[4 + k] & (0u - (uint32_t)(j == k));
+  return (int)v;
+}
 
 // This lane's weights of one (row set, stage) chunk of the stream layout: units u0 .. u0+NU-1
 // (2 blocks each) of its (row, half), and the f16 scales of its row's blocks 8*sh .. 8*sh+7
@@ -423,8 +467,8 @@ KQ4_DEV void kq4_moe_terms(const KQ4MoeW<NU, NS> &w, const uint8_t *slab, int qt
 // row) forms av, and the 32 rows of the set (one av block) are quantized together.
 __global__ __launch_bounds__(1024) void kq4_moe_gu_kernel(
     const uint8_t *__restrict__ G, const uint8_t *__restrict__ U, const int8_t *__restrict__ xq,
-    const float *__restrict__ xd, const int *__restrict__ ex_off, const int *__restrict__ ex_pair,
-    const int *__restrict__ act, int8_t *__restrict__ avq, float *__restrict__ avd,
+    const float *__restrict__ xd, const int *__restrict__ rec, const int *__restrict__ ex_pair,
+    int8_t *__restrict__ avq, float *__restrict__ avd,
     float *__restrict__ g_out, float *__restrict__ u_out, float *__restrict__ av_out, int d,
     int ef, int tk) {
   extern __shared__ __align__(16) uint8_t kq4_moe_lds[];
@@ -432,9 +476,10 @@ __global__ __launch_bounds__(1024) void kq4_moe_gu_kernel(
   constexpr int SLAB = kq4_moe_slab(16, PC);
   const int rbs = ef / 32;
   const int slot = blockIdx.x / rbs, rs = blockIdx.x - slot * rbs;
-  const int e = act[slot];
+  const KQ4MoeSlot<0> sr = kq4_moe_slot<0>(rec, slot);   // header only: inline ids spill here
+  const int e = sr.r[0];
   if (e < 0) return;                                  // no expert in this slot (whole workgroup)
-  const int o0 = ex_off[e], cnt = ex_off[e + 1] - o0;
+  const int cnt = sr.r[2];
   const int nb = d / 32, nst = (nb + 15) / 16;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -458,7 +503,7 @@ __global__ __launch_bounds__(1024) void kq4_moe_gu_kernel(
         const int p = i >> 5, bb = (i >> 1) & 15, hh = i & 1;
         uint4 v = make_uint4(0, 0, 0, 0);
         if (p < np && bb < nblk) {
-          const int tok = ex_pair[o0 + c0 + p] / tk;
+          const int tok = kq4_moe_pair<0>(sr, ex_pair, c0 + p) / tk;
           v = *reinterpret_cast<const uint4 *>(xq + (size_t)tok * d + (size_t)(16 * k + bb) * 32 +
                                                16 * hh);
         }
@@ -467,7 +512,7 @@ __global__ __launch_bounds__(1024) void kq4_moe_gu_kernel(
       {
         const int p = lane >> 4, bb = lane & 15;      // 64 scales
         float x = 0.0f;
-        if (p < np && bb < nblk) x = xd[(size_t)(ex_pair[o0 + c0 + p] / tk) * nb + 16 * k + bb];
+        if (p < np && bb < nblk) x = xd[(size_t)(kq4_moe_pair<0>(sr, ex_pair, c0 + p) / tk) * nb + 16 * k + bb];
         sx[bb * PC + p] = x;
       }
     }
@@ -496,14 +541,12 @@ __global__ __launch_bounds__(1024) void kq4_moe_gu_kernel(
       const int p = i >> 5, rw = i & 31;
       const float g = accb[p * 32 + rw], u = accb[(PC + p) * 32 + rw];
       const float a = (g / (1.0f + kq4_expf(-g))) * u;
-      float amax = fmaxf(fabsf(a), 1e-10f);
-#pragma unroll
-      for (int s = 16; s > 0; s >>= 1) amax = fmaxf(amax, __shfl_xor(amax, s, 32));
+      const float amax = kq4_max32(fmaxf(fabsf(a), 1e-10f));
       const float dq = amax / 127.0f;
       int qv = (int)(a / dq + 0.5f);
       qv = qv > 127 ? 127 : (qv < -127 ? -127 : qv);
       if (p < np) {
-        const int pair = ex_pair[o0 + c0 + p];
+        const int pair = kq4_moe_pair<0>(sr, ex_pair, c0 + p);
         const size_t o = (size_t)pair * ef + (size_t)rs * 32 + rw;
         avq[o] = (int8_t)qv;
         if (rw == 0) avd[(size_t)pair * rbs + rs] = dq;
@@ -542,15 +585,16 @@ __global__ __launch_bounds__(256) void kq4_moe_avq_kernel(const float *__restric
 // every row set the waves add them in block order.
 __global__ __launch_bounds__(1024) void kq4_moe_down_kernel(
     const uint8_t *__restrict__ D, const int8_t *__restrict__ avq, const float *__restrict__ avd,
-    const int *__restrict__ ex_off, const int *__restrict__ ex_pair, const int *__restrict__ act,
-    float *__restrict__ P, int ne, int d, int ef, int rsg, int nhl) {
+    const int *__restrict__ rec, const int *__restrict__ ex_pair, float *__restrict__ P, int ne,
+    int d, int ef, int rsg, int nhl) {
   extern __shared__ __align__(16) uint8_t kq4_moe_lds[];
   constexpr int PC = KQ4_MOE_PCD, VT = PC / 2;
   const int nrs = d / 32, ngrp = (nrs + rsg - 1) / rsg;
   const int slot = blockIdx.x / ngrp, grp = blockIdx.x - slot * ngrp;
-  const int e = act[slot];
+  const KQ4MoeSlot<PC> sr = kq4_moe_slot<PC>(rec, slot);
+  const int e = sr.r[0];
   if (e < 0) return;
-  const int o0 = ex_off[e], cnt = ex_off[e + 1] - o0;
+  const int cnt = sr.r[2];
   const int cbe = ef / 32, nbD = ne * cbe, nstD = (nbD + 15) / 16;
   const int b0 = e * cbe;                              // first block of the band
   const int qa = b0 >> 3, nh = ((b0 + cbe - 1) >> 3) - qa + 1;
@@ -583,13 +627,13 @@ __global__ __launch_bounds__(1024) void kq4_moe_down_kernel(
       const int p = i / (2 * cbe), rem = i - p * 2 * cbe, cb = rem >> 1, hh = rem & 1;
       uint4 v = make_uint4(0, 0, 0, 0);
       if (p < np)
-        v = *reinterpret_cast<const uint4 *>(avq + (size_t)ex_pair[o0 + c0 + p] * ef +
+        v = *reinterpret_cast<const uint4 *>(avq + (size_t)kq4_moe_pair<PC>(sr, ex_pair, c0 + p) * ef +
                                              (size_t)cb * 32 + 16 * hh);
       *reinterpret_cast<uint4 *>(codes + p * qts + kq4_moe_qpos(cb) + 16 * hh) = v;
     }
     for (int i = threadIdx.x; i < PC * cbe; i += blockDim.x) {
       const int cb = i / PC, p = i - cb * PC;
-      sxb[i] = p < np ? avd[(size_t)ex_pair[o0 + c0 + p] * cbe + cb] : 0.0f;
+      sxb[i] = p < np ? avd[(size_t)kq4_moe_pair<PC>(sr, ex_pair, c0 + p) * cbe + cb] : 0.0f;
     }
     __syncthreads();
     float t[8][VT];
@@ -631,7 +675,7 @@ __global__ __launch_bounds__(1024) void kq4_moe_down_kernel(
           if (ww + 1 < nh) {
             accb[(VT * h + v) * 32 + r] = acc[v];
           } else if (VT * h + v < np) {
-            P[(size_t)ex_pair[o0 + c0 + VT * h + v] * d + (size_t)rs * 32 + r] = acc[v];
+            P[(size_t)kq4_moe_pair<PC>(sr, ex_pair, c0 + VT * h + v) * d + (size_t)rs * 32 + r] = acc[v];
           }
         }
       }
@@ -691,14 +735,14 @@ int kq4_launch_moe_dbg(float *Y, const float *X, const int *sel, const float *pr
   const int n_pairs = T * tk;
   const int nb = d / 32, nst = (nb + 15) / 16, cbe = ef / 32;
   const long qblk = (long)T * nb;
-  hipLaunchKernelGGL(kq4_moe_prep_kernel, dim3((unsigned)(1 + (qblk + 7) / 8)), dim3(256),
-                     (2 * ne + 2 * 256) * sizeof(int), s, ws.ex_off, ws.ex_pair, ws.act, sel, n_pairs, ne, X,
-                     ws.xq, ws.xd, T, d);
   const int slots = ne < n_pairs ? ne : n_pairs;
+  hipLaunchKernelGGL(kq4_moe_prep_kernel, dim3((unsigned)(1 + (qblk + 7) / 8)), dim3(256),
+                     (3 * ne + 2 * 256) * sizeof(int), s, ws.ex_off, ws.ex_pair, ws.rec, slots, sel,
+                     n_pairs, ne, X, ws.xq, ws.xd, T, d);
   const size_t lds_gu = (size_t)nst * kq4_moe_slab(16, KQ4_MOE_PCG) +
                         2 * KQ4_MOE_PCG * 32 * sizeof(float);
   hipLaunchKernelGGL(kq4_moe_gu_kernel, dim3((unsigned)(slots * cbe)), dim3(128 * nst), lds_gu, s,
-                     G, U, ws.xq, ws.xd, ws.ex_off, ws.ex_pair, ws.act, ws.avq, ws.avd, g_out,
+                     G, U, ws.xq, ws.xd, ws.rec, ws.ex_pair, ws.avq, ws.avd, g_out,
                      u_out, av_out, d, ef, tk);
   if (av_in) {
     const long nblk = (long)n_pairs * cbe;
@@ -722,7 +766,7 @@ int kq4_launch_moe_dbg(float *Y, const float *X, const int *sel, const float *pr
                         (size_t)cbe * KQ4_MOE_PCD * sizeof(float) +
                         (size_t)rsg * KQ4_MOE_PCD * 32 * sizeof(float);
   hipLaunchKernelGGL(kq4_moe_down_kernel, dim3((unsigned)(slots * ngrp)), dim3(64 * rsg * nhl),
-                     lds_dn, s, D, ws.avq, ws.avd, ws.ex_off, ws.ex_pair, ws.act, ws.P, ne, d,
+                     lds_dn, s, D, ws.avq, ws.avd, ws.rec, ws.ex_pair, ws.P, ne, d,
                      ef, rsg, nhl);
   const long n = (long)T * d;
   hipLaunchKernelGGL(kq4_moe_combine_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
