@@ -187,8 +187,8 @@ __global__ __launch_bounds__(256) void kq4_moe_route_kernel(int *__restrict__ se
 // (token, expert)). A chain cannot be split without changing its roundings, so one lane runs one
 // (token, expert) chain and does nothing else: a workgroup takes one token and 16 experts; lanes
 // 0-15 of wave 0 add, waves 1-4 form the products. Per 512-column tile each producer thread
-// loads a 128-B segment of one row and the matching x (issued a tile ahead, so the loads are in
-// flight during a whole tile's 512 dependent adds, ~1.6 us), multiplies and stores the products
+// loads 8 float4s of one row (256 B apart) and the matching x (issued a tile ahead, so the loads
+// are in flight during a whole tile's 512 dependent adds, ~1.6 us), multiplies and stores the products
 // to LDS (double-buffered; row pitch 516 floats, so the adders' 16-B reads hit distinct banks);
 // each adder then adds its row's products in order.
 #define KQ4_RT_E 16        // experts (chains) per workgroup
@@ -199,35 +199,42 @@ __global__ __launch_bounds__(320) void kq4_moe_logits_kernel(float *__restrict__
                                                              const float *__restrict__ router,
                                                              const float *__restrict__ X, int ne,
                                                              int d) {
-  extern __shared__ __align__(16) float kq4_rt_lds[];   // [2][KQ4_RT_E][KQ4_RT_P]
+  extern __shared__ __align__(16) float kq4_rt_lds[];   // [2][KQ4_RT_E][KQ4_RT_P] + 32 pad
   const int t = blockIdx.y;
   const int e0 = blockIdx.x * KQ4_RT_E;
   const int wave = threadIdx.x >> 6;
   const float *__restrict__ xt = X + (size_t)t * d;
   const int ntile = (d + KQ4_RT_C - 1) / KQ4_RT_C;
-  // producer thread p: row p/16 of the tile, columns 32*(p%16) .. +32
+  // producer thread p: row p/16 of the tile, the float4s q, q+16, .. (q = p%16) of its 512
+  // columns, so the 16 threads of a row store 256 contiguous bytes per instruction (a thread
+  // owning 32 consecutive columns put all 16 on the same LDS banks, and those stores delayed the
+  // adders' reads)
   const int p = threadIdx.x - 64;
-  const int pr = p >> 4, pc = 32 * (p & 15);
+  const int pr = p >> 4, pc = 4 * (p & 15);
   const bool prow = wave > 0 && e0 + pr < ne;
   const float *__restrict__ rw = router + (size_t)(e0 + pr) * d;
-  float4 cur[8], xv[8];   // the next tile's weights and x, loaded a tile ahead
+  // One register array for both roles (no wave has both; as separate arrays the kernel took 138
+  // VGPRs, and two 5-wave workgroups did not fit a CU): a producer's next-tile weights rb[0..7]
+  // and x rb[8..15], loaded a tile ahead; the adder's two chunks of products.
+  float4 rb[16];
+  float4 *cur = rb, *xv = rb + 8;
   auto load = [&](int k) {
-    const int c = k * KQ4_RT_C + pc;
-    const bool live = prow && c < d;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      cur[j] = live ? *reinterpret_cast<const float4 *>(rw + c + 4 * j) : make_float4(0, 0, 0, 0);
-      xv[j] = live ? *reinterpret_cast<const float4 *>(xt + c + 4 * j) : make_float4(0, 0, 0, 0);
+      const int c = k * KQ4_RT_C + pc + 64 * j;
+      const bool live = prow && c < d;   // d % 32 == 0: a float4 is wholly in or out
+      cur[j] = live ? *reinterpret_cast<const float4 *>(rw + c) : make_float4(0, 0, 0, 0);
+      xv[j] = live ? *reinterpret_cast<const float4 *>(xt + c) : make_float4(0, 0, 0, 0);
     }
   };
   auto store = [&](int k) {
-    const int c = k * KQ4_RT_C + pc;
-    if (!(prow && c < d)) return;
+    if (!prow) return;
     float *dst = kq4_rt_lds + ((k & 1) * KQ4_RT_E + pr) * KQ4_RT_P + pc;
 #pragma unroll
     for (int j = 0; j < 8; ++j)
-      *reinterpret_cast<float4 *>(dst + 4 * j) = make_float4(
-          cur[j].x * xv[j].x, cur[j].y * xv[j].y, cur[j].z * xv[j].z, cur[j].w * xv[j].w);
+      if (k * KQ4_RT_C + pc + 64 * j < d)
+        *reinterpret_cast<float4 *>(dst + 64 * j) = make_float4(
+            cur[j].x * xv[j].x, cur[j].y * xv[j].y, cur[j].z * xv[j].z, cur[j].w * xv[j].w);
   };
   if (wave > 0) load(0);
   float s = 0.0f;
@@ -239,12 +246,19 @@ __global__ __launch_bounds__(320) void kq4_moe_logits_kernel(float *__restrict__
     }
     __syncthreads();   // tile k's products are in LDS; the adders are done with buffer k-1
     if (adder) {
+      // 32-column chunks, each read before the previous one is added (two register sets), so
+      // the LDS latency stays off the add chain. The loop body is straight-line (one chunk past
+      // n may be read and not added; the LDS has a 32-float pad after the last row), so every
+      // add waits for exactly its own read.
       const int n = min(KQ4_RT_C, d - k * KQ4_RT_C);   // a multiple of 32
       const float *src = kq4_rt_lds + ((k & 1) * KQ4_RT_E + threadIdx.x) * KQ4_RT_P;
-      for (int i = 0; i < n; i += 32) {
-        float4 v[8];
+      float4 *va = rb, *vb = rb + 8;
+      auto rd = [&](float4 *v, int i) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) v[j] = *reinterpret_cast<const float4 *>(src + i + 4 * j);
+        __builtin_amdgcn_sched_barrier(0);   // issued here, not sunk below the adds
+      };
+      auto add = [&](const float4 *v) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
           s += v[j].x;
@@ -252,7 +266,16 @@ __global__ __launch_bounds__(320) void kq4_moe_logits_kernel(float *__restrict__
           s += v[j].z;
           s += v[j].w;
         }
+      };
+      rd(va, 0);
+      int i = 0;
+      for (; i + 64 <= n; i += 64) {
+        rd(vb, i + 32);
+        add(va);
+        rd(va, i + 64);
+        add(vb);
       }
+      if (i < n) add(va);   // n % 64 == 32: the last chunk, already read
     }
   }
   if (adder && e0 + threadIdx.x < ne) logits[(size_t)t * ne + e0 + threadIdx.x] = s;
@@ -262,7 +285,7 @@ int kq4_launch_moe_logits(float *logits, const float *router, const float *X, in
                           int d, hipStream_t s) {
   if (T <= 0) return 0;
   if (d % 32) return (int)hipErrorInvalidValue;
-  const size_t lds = 2 * KQ4_RT_E * KQ4_RT_P * sizeof(float);
+  const size_t lds = (2 * KQ4_RT_E * KQ4_RT_P + 32) * sizeof(float);
   static bool attr = false;   // 66 KB of LDS
   if (!attr) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&kq4_moe_logits_kernel),
