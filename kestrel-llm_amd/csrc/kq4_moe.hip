@@ -313,7 +313,8 @@ __global__ __launch_bounds__(256) void kq4_moe_prep_kernel(
     const int *__restrict__ sel, int n_pairs, int ne, const float *__restrict__ X,
     int8_t *__restrict__ xq, float *__restrict__ xd, int T, int d) {
   if (blockIdx.x == 0) {
-    // LDS: cnt[ne] (then each expert's offset), cursor[ne], slot[ne], partial sums [2][blockDim]
+    // LDS: cnt[ne] (then each expert's offset), cursor[ne], slot[ne], the waves' totals part[w] and
+    // part[blockDim + w]
     extern __shared__ int kq4_moe_cnt[];
     int *cnt = kq4_moe_cnt, *cur = kq4_moe_cnt + ne, *slt = kq4_moe_cnt + 2 * ne,
         *part = kq4_moe_cnt + 3 * ne;
@@ -333,21 +334,26 @@ __global__ __launch_bounds__(256) void kq4_moe_prep_kernel(
     }
     __syncthreads();
     // exclusive scans of the counts and of the active flags: thread tid owns experts
-    // [tid*per, tid*per + per); its totals are scanned across the block (Hillis-Steele)
+    // [tid*per, tid*per + per); its totals are scanned inside each wave by lane shifts, and the
+    // waves' totals (through LDS, one barrier) give each wave its offset and every thread the
+    // block totals tc (pairs) and ta (active experts).
     const int per = (ne + nt - 1) / nt, e0 = tid * per;
     int sc = 0, sa = 0;
     for (int e = e0; e < e0 + per && e < ne; ++e) { sc += cnt[e]; sa += cnt[e] > 0; }
-    part[tid] = sc;
-    part[nt + tid] = sa;
-    __syncthreads();
-    for (int o = 1; o < nt; o <<= 1) {
-      const int vc = tid >= o ? part[tid - o] : 0, va = tid >= o ? part[nt + tid - o] : 0;
-      __syncthreads();
-      part[tid] += vc;
-      part[nt + tid] += va;
-      __syncthreads();
+    const int lane = tid & 63, wv = tid >> 6, nwv = nt >> 6;
+    int ic = sc, ia = sa;   // inclusive scans within the wave
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int vc = __shfl_up(ic, o, 64), va = __shfl_up(ia, o, 64);
+      if (lane >= o) { ic += vc; ia += va; }
     }
-    int acc = part[tid] - sc, na = part[nt + tid] - sa;   // exclusive prefixes
+    if (lane == 63) { part[wv] = ic; part[nt + wv] = ia; }
+    __syncthreads();
+    int oc = 0, oa = 0;   // the earlier waves' totals
+    for (int w = 0; w < wv; ++w) { oc += part[w]; oa += part[nt + w]; }
+    int tc = 0, ta = 0;
+    for (int w = 0; w < nwv; ++w) { tc += part[w]; ta += part[nt + w]; }
+    int acc = oc + ic - sc, na = oa + ia - sa;   // exclusive prefixes
     for (int e = e0; e < e0 + per && e < ne; ++e) {
       const int c = cnt[e];
       cur[e] = acc;
@@ -361,9 +367,9 @@ __global__ __launch_bounds__(256) void kq4_moe_prep_kernel(
       }
       acc += c;
     }
-    if (tid == nt - 1) ex_off[ne] = part[nt - 1];
+    if (tid == nt - 1) ex_off[ne] = tc;
     __syncthreads();
-    for (int s = part[2 * nt - 1] + tid; s < nslot; s += nt) rec[KQ4_MOE_REC * s] = -1;
+    for (int s = ta + tid; s < nslot; s += nt) rec[KQ4_MOE_REC * s] = -1;
     auto place = [&](int e, int i) {   // pair i of expert e
       const int pos = atomicAdd(&cur[e], 1);
       ex_pair[pos] = i;
@@ -488,21 +494,33 @@ KQ4_DEV void kq4_moe_terms(const KQ4MoeW<NU, NS> &w, const uint8_t *slab, int qt
 // wave of stage k stages the pairs' codes of stage k in slab k; every wave computes its terms;
 // then nst phases add them to the gate and up chains in block order; then one lane per (pair,
 // row) forms av, and the 32 rows of the set (one av block) are quantized together.
+// T1 (one token): slot j is rank j, expert sel[j] with the single pair j, and the gate waves
+// quantize X themselves, so the launch needs no prep kernel (the grouping is trivial).
+template <bool T1>
 __global__ __launch_bounds__(1024) void kq4_moe_gu_kernel(
     const uint8_t *__restrict__ G, const uint8_t *__restrict__ U, const int8_t *__restrict__ xq,
     const float *__restrict__ xd, const int *__restrict__ rec, const int *__restrict__ ex_pair,
     int8_t *__restrict__ avq, float *__restrict__ avd,
     float *__restrict__ g_out, float *__restrict__ u_out, float *__restrict__ av_out, int d,
-    int ef, int tk) {
+    int ef, int tk, const int *__restrict__ sel, const float *__restrict__ X, int ne) {
   extern __shared__ __align__(16) uint8_t kq4_moe_lds[];
   constexpr int PC = KQ4_MOE_PCG, VT = PC / 2;
   constexpr int SLAB = kq4_moe_slab(16, PC);
   const int rbs = ef / 32;
   const int slot = blockIdx.x / rbs, rs = blockIdx.x - slot * rbs;
-  const KQ4MoeSlot<0> sr = kq4_moe_slot<0>(rec, slot);   // header only: inline ids spill here
-  const int e = sr.r[0];
-  if (e < 0) return;                                  // no expert in this slot (whole workgroup)
-  const int cnt = sr.r[2];
+  KQ4MoeSlot<0> sr{};   // header only: inline ids spill here
+  int e, cnt;
+  if (T1) {
+    e = __builtin_amdgcn_readfirstlane(sel[slot]);
+    if (e < 0 || e >= ne) return;                     // no expert at this rank
+    cnt = 1;
+  } else {
+    sr = kq4_moe_slot<0>(rec, slot);
+    e = sr.r[0];
+    if (e < 0) return;                                // no expert in this slot (whole workgroup)
+    cnt = sr.r[2];
+  }
+  auto pair = [&](int j) { return T1 ? slot : kq4_moe_pair<0>(sr, ex_pair, j); };
   const int nb = d / 32, nst = (nb + 15) / 16;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -519,14 +537,50 @@ __global__ __launch_bounds__(1024) void kq4_moe_gu_kernel(
 
   for (int c0 = 0; c0 < cnt; c0 += PC) {
     const int np = cnt - c0 < PC ? cnt - c0 : PC;
-    if (m == 0) {   // stage k's codes and scales of the pass's pairs (zeros past them and past K)
+    if (m == 0 && T1) {
+      // token 0's stage k quantized here, a lane quad per block (8 values per lane), as the prep
+      // kernel's quantizer does it: amax floored at 1e-10, dq = amax/127, q = (int)(x/dq + 0.5)
+      // clamped to +-127; pairs 1-3 and blocks past K get zero codes and scales
+      const int bb = lane >> 2, qq = lane & 3;
+      const bool live = bb < nblk;
+      float4 x0 = make_float4(0, 0, 0, 0), x1 = x0;
+      if (live) {
+        const float4 *src = reinterpret_cast<const float4 *>(X + (size_t)(16 * k + bb) * 32 + 8 * qq);
+        x0 = src[0];
+        x1 = src[1];
+      }
+      const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+      float am = 1e-10f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) am = fmaxf(am, fabsf(xv[i]));
+      am = kq4_quad_max(am);
+      const float dq = am / 127.0f;
+      uint32_t pk[2] = {0, 0};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        int q = (int)(xv[i] / dq + 0.5f);
+        q = q > 127 ? 127 : (q < -127 ? -127 : q);
+        pk[i >> 2] |= ((uint32_t)q & 0xFFu) << (8 * (i & 3));
+      }
+      *reinterpret_cast<uint2 *>(slab + kq4_moe_qpos(bb) + 8 * qq) = make_uint2(pk[0], pk[1]);
+      if (qq == 0) sx[bb * PC] = live ? dq : 0.0f;
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {   // pairs 1-3: 96 units of 16 B
+        const int i = lane + 64 * u;
+        const int p = i >> 5, b2 = (i >> 1) & 15, hh = i & 1;
+        if (p >= 1)
+          *reinterpret_cast<uint4 *>(slab + p * KQ4_MOE_QTS + kq4_moe_qpos(b2) + 16 * hh) =
+              make_uint4(0, 0, 0, 0);
+      }
+      if (lane >= 16) sx[(lane & 15) * PC + (lane >> 4)] = 0.0f;
+    } else if (m == 0) {   // stage k's codes and scales of the pass's pairs (zeros past them and past K)
 #pragma unroll
       for (int u = 0; u < 2; ++u) {   // 4 pairs x 16 blocks x 2 halves = 128 units of 16 B
         const int i = lane + 64 * u;
         const int p = i >> 5, bb = (i >> 1) & 15, hh = i & 1;
         uint4 v = make_uint4(0, 0, 0, 0);
         if (p < np && bb < nblk) {
-          const int tok = kq4_moe_pair<0>(sr, ex_pair, c0 + p) / tk;
+          const int tok = pair(c0 + p) / tk;
           v = *reinterpret_cast<const uint4 *>(xq + (size_t)tok * d + (size_t)(16 * k + bb) * 32 +
                                                16 * hh);
         }
@@ -535,7 +589,7 @@ __global__ __launch_bounds__(1024) void kq4_moe_gu_kernel(
       {
         const int p = lane >> 4, bb = lane & 15;      // 64 scales
         float x = 0.0f;
-        if (p < np && bb < nblk) x = xd[(size_t)(kq4_moe_pair<0>(sr, ex_pair, c0 + p) / tk) * nb + 16 * k + bb];
+        if (p < np && bb < nblk) x = xd[(size_t)(pair(c0 + p) / tk) * nb + 16 * k + bb];
         sx[bb * PC + p] = x;
       }
     }
@@ -569,10 +623,10 @@ __global__ __launch_bounds__(1024) void kq4_moe_gu_kernel(
       int qv = (int)(a / dq + 0.5f);
       qv = qv > 127 ? 127 : (qv < -127 ? -127 : qv);
       if (p < np) {
-        const int pair = kq4_moe_pair<0>(sr, ex_pair, c0 + p);
-        const size_t o = (size_t)pair * ef + (size_t)rs * 32 + rw;
+        const int pi = pair(c0 + p);
+        const size_t o = (size_t)pi * ef + (size_t)rs * 32 + rw;
         avq[o] = (int8_t)qv;
-        if (rw == 0) avd[(size_t)pair * rbs + rs] = dq;
+        if (rw == 0) avd[(size_t)pi * rbs + rs] = dq;
         if (g_out) { g_out[o] = g; u_out[o] = u; }
         if (av_out) av_out[o] = a;
       }
@@ -606,18 +660,29 @@ __global__ __launch_bounds__(256) void kq4_moe_avq_kernel(const float *__restric
 // skipped, waves past the band only join the barriers. Per pass of up to 8 pairs the workgroup
 // stages the band's av codes once (shared by its row sets), each wave computes its terms, and for
 // every row set the waves add them in block order.
+// T1 (one token): slot j is rank j, expert sel[j], its single pair j.
+template <bool T1>
 __global__ __launch_bounds__(1024) void kq4_moe_down_kernel(
     const uint8_t *__restrict__ D, const int8_t *__restrict__ avq, const float *__restrict__ avd,
     const int *__restrict__ rec, const int *__restrict__ ex_pair, float *__restrict__ P, int ne,
-    int d, int ef, int rsg, int nhl) {
+    int d, int ef, int rsg, int nhl, const int *__restrict__ sel) {
   extern __shared__ __align__(16) uint8_t kq4_moe_lds[];
   constexpr int PC = KQ4_MOE_PCD, VT = PC / 2;
   const int nrs = d / 32, ngrp = (nrs + rsg - 1) / rsg;
   const int slot = blockIdx.x / ngrp, grp = blockIdx.x - slot * ngrp;
-  const KQ4MoeSlot<PC> sr = kq4_moe_slot<PC>(rec, slot);
-  const int e = sr.r[0];
-  if (e < 0) return;
-  const int cnt = sr.r[2];
+  KQ4MoeSlot<PC> sr{};
+  int e, cnt;
+  if (T1) {
+    e = __builtin_amdgcn_readfirstlane(sel[slot]);
+    if (e < 0 || e >= ne) return;
+    cnt = 1;
+  } else {
+    sr = kq4_moe_slot<PC>(rec, slot);
+    e = sr.r[0];
+    if (e < 0) return;
+    cnt = sr.r[2];
+  }
+  auto pair = [&](int j) { return T1 ? slot : kq4_moe_pair<PC>(sr, ex_pair, j); };
   const int cbe = ef / 32, nbD = ne * cbe, nstD = (nbD + 15) / 16;
   const int b0 = e * cbe;                              // first block of the band
   const int qa = b0 >> 3, nh = ((b0 + cbe - 1) >> 3) - qa + 1;
@@ -650,13 +715,13 @@ __global__ __launch_bounds__(1024) void kq4_moe_down_kernel(
       const int p = i / (2 * cbe), rem = i - p * 2 * cbe, cb = rem >> 1, hh = rem & 1;
       uint4 v = make_uint4(0, 0, 0, 0);
       if (p < np)
-        v = *reinterpret_cast<const uint4 *>(avq + (size_t)kq4_moe_pair<PC>(sr, ex_pair, c0 + p) * ef +
+        v = *reinterpret_cast<const uint4 *>(avq + (size_t)pair(c0 + p) * ef +
                                              (size_t)cb * 32 + 16 * hh);
       *reinterpret_cast<uint4 *>(codes + p * qts + kq4_moe_qpos(cb) + 16 * hh) = v;
     }
     for (int i = threadIdx.x; i < PC * cbe; i += blockDim.x) {
       const int cb = i / PC, p = i - cb * PC;
-      sxb[i] = p < np ? avd[(size_t)kq4_moe_pair<PC>(sr, ex_pair, c0 + p) * cbe + cb] : 0.0f;
+      sxb[i] = p < np ? avd[(size_t)pair(c0 + p) * cbe + cb] : 0.0f;
     }
     __syncthreads();
     float t[8][VT];
@@ -698,7 +763,7 @@ __global__ __launch_bounds__(1024) void kq4_moe_down_kernel(
           if (ww + 1 < nh) {
             accb[(VT * h + v) * 32 + r] = acc[v];
           } else if (VT * h + v < np) {
-            P[(size_t)kq4_moe_pair<PC>(sr, ex_pair, c0 + VT * h + v) * d + (size_t)rs * 32 + r] = acc[v];
+            P[(size_t)pair(c0 + VT * h + v) * d + (size_t)rs * 32 + r] = acc[v];
           }
         }
       }
@@ -758,15 +823,18 @@ int kq4_launch_moe_dbg(float *Y, const float *X, const int *sel, const float *pr
   const int n_pairs = T * tk;
   const int nb = d / 32, nst = (nb + 15) / 16, cbe = ef / 32;
   const long qblk = (long)T * nb;
-  const int slots = ne < n_pairs ? ne : n_pairs;
-  hipLaunchKernelGGL(kq4_moe_prep_kernel, dim3((unsigned)(1 + (qblk + 7) / 8)), dim3(256),
-                     (3 * ne + 2 * 256) * sizeof(int), s, ws.ex_off, ws.ex_pair, ws.rec, slots, sel,
-                     n_pairs, ne, X, ws.xq, ws.xd, T, d);
+  // one token: every slot is a rank with one pair, the kernels take sel directly (no prep)
+  const bool t1 = T == 1;
+  const int slots = t1 ? tk : (ne < n_pairs ? ne : n_pairs);
+  if (!t1)
+    hipLaunchKernelGGL(kq4_moe_prep_kernel, dim3((unsigned)(1 + (qblk + 7) / 8)), dim3(256),
+                       (3 * ne + 2 * 256) * sizeof(int), s, ws.ex_off, ws.ex_pair, ws.rec, slots,
+                       sel, n_pairs, ne, X, ws.xq, ws.xd, T, d);
   const size_t lds_gu = (size_t)nst * kq4_moe_slab(16, KQ4_MOE_PCG) +
                         2 * KQ4_MOE_PCG * 32 * sizeof(float);
-  hipLaunchKernelGGL(kq4_moe_gu_kernel, dim3((unsigned)(slots * cbe)), dim3(128 * nst), lds_gu, s,
-                     G, U, ws.xq, ws.xd, ws.rec, ws.ex_pair, ws.avq, ws.avd, g_out,
-                     u_out, av_out, d, ef, tk);
+  hipLaunchKernelGGL(t1 ? kq4_moe_gu_kernel<true> : kq4_moe_gu_kernel<false>,
+                     dim3((unsigned)(slots * cbe)), dim3(128 * nst), lds_gu, s, G, U, ws.xq, ws.xd,
+                     ws.rec, ws.ex_pair, ws.avq, ws.avd, g_out, u_out, av_out, d, ef, tk, sel, X, ne);
   if (av_in) {
     const long nblk = (long)n_pairs * cbe;
     hipLaunchKernelGGL(kq4_moe_avq_kernel, dim3((unsigned)((nblk + 7) / 8)), dim3(256), 0, s,
@@ -788,9 +856,9 @@ int kq4_launch_moe_dbg(float *Y, const float *X, const int *sel, const float *pr
   const size_t lds_dn = (size_t)KQ4_MOE_PCD * (((cbe + 1) / 2) * 80) +
                         (size_t)cbe * KQ4_MOE_PCD * sizeof(float) +
                         (size_t)rsg * KQ4_MOE_PCD * 32 * sizeof(float);
-  hipLaunchKernelGGL(kq4_moe_down_kernel, dim3((unsigned)(slots * ngrp)), dim3(64 * rsg * nhl),
-                     lds_dn, s, D, ws.avq, ws.avd, ws.rec, ws.ex_pair, ws.P, ne, d,
-                     ef, rsg, nhl);
+  hipLaunchKernelGGL(t1 ? kq4_moe_down_kernel<true> : kq4_moe_down_kernel<false>,
+                     dim3((unsigned)(slots * ngrp)), dim3(64 * rsg * nhl), lds_dn, s, D, ws.avq,
+                     ws.avd, ws.rec, ws.ex_pair, ws.P, ne, d, ef, rsg, nhl, sel);
   const long n = (long)T * d;
   hipLaunchKernelGGL(kq4_moe_combine_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
                      Y, ws.P, sel, pr, T, tk, d, ne);

@@ -112,15 +112,16 @@ def test_moe_stages(kq4, torch_dev, orc, shape, T):
     assert np.array_equal(host(Y2).view(np.uint32), Y_o.view(np.uint32))
 
 
-def test_moe_invalid_expert_ids_skipped(kq4, torch_dev, orc):
+@pytest.mark.parametrize("T", [1, 3])   # T = 1 takes the kernels' one-token mode (no grouping)
+def test_moe_invalid_expert_ids_skipped(kq4, torch_dev, orc, T):
     torch = torch_dev
     cfg = SHAPES["small"]
     d, ne, tk, ef = cfg["hidden"], cfg["experts"], cfg["top_k"], cfg["ef"]
     G, U, D = synth.make_moe(cfg, 90)
-    X = synth.make_activations(3, d, 91)
-    sel, pr = orc.moe_route(synth.make_logits(3, ne, 92), tk)
-    sel[1, 2] = -1
-    sel[2, 0] = ne + 5
+    X = synth.make_activations(T, d, 91)
+    sel, pr = orc.moe_route(synth.make_logits(T, ne, 92), tk)
+    sel[T - 1, 1] = -1
+    sel[T // 2, 0] = ne + 5
     Y_o = orc.moe_ffn(X, sel, pr, G, U, D, ne, d, ef)
     Y = kq4.moe_ffn(X, sel, pr, G, U, D, ne, d, ef)
     r, _ = rel_err(Y, Y_o)
