@@ -463,12 +463,52 @@ KQ4_DEV void kq4_moe_wload(KQ4MoeW<NU, NS> &w, const uint8_t *__restrict__ chunk
 // pair VT*(lane/32)+v (VT = 2 or 4; 2*VT pairs): the pair's codes sit in MFMA token row
 // 4*(lane/32)+v, i.e. A row rho = 4*i+v holds pair VT*i+v (i < 2, v < VT; other rows: any codes).
 // The activation codes are at slab[pair*qts + qpos(b)], scales sx[b*2*VT + pair].
-template <int NU, int NS, int VT>
+// PIPE: every block's activation scales are read first, the A fragments two blocks ahead, and
+// two MFMAs are in flight, so LDS and MFMA latencies are not paid block by block (the scale read
+// of each block used to wait for all outstanding LDS reads); for kernels with the registers to
+// spare. VTC: the pairs computed (1 in one-token launches; t[b][v] = 0 for the others).
+template <int NU, int NS, int VT, bool PIPE = false, int VTC = VT>
 KQ4_DEV void kq4_moe_terms(const KQ4MoeW<NU, NS> &w, const uint8_t *slab, int qts,
                            const float *sx, int lane, float (*t)[VT]) {
   const int h = lane >> 5, r = lane & 31;
   const int pr = (r < 8 && (r & 3) < VT) ? VT * (r >> 2) + (r & 3) : 0;
   const uint8_t *qb = slab + pr * qts + 16 * h;
+  if constexpr (PIPE) {
+    constexpr int NB = 2 * NU;
+    float xsv[NB][VTC];
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+      for (int v = 0; v < VTC; ++v) xsv[b][v] = sx[b * 2 * VT + VT * h + v];
+    auto rd = [&](int b) { return *reinterpret_cast<const kq4_v4i *>(qb + kq4_moe_qpos(b)); };
+    auto mf = [&](int b, kq4_v4i A) {
+      uint32_t o[4];
+      kq4_unpack_half(w.n[2 * b], w.n[2 * b + 1], o);
+      const kq4_v4i B = {(int)o[0], (int)o[1], (int)o[2], (int)o[3]};
+      return kq4_moe_mfma(A, B);
+    };
+    kq4_v4i Aq[3];
+    Aq[0] = rd(0);
+    if (NB > 1) Aq[1] = rd(1);
+    kq4_v16i C = mf(0, Aq[0]);
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      if (b + 2 < NB) Aq[(b + 2) % 3] = rd(b + 2);
+      kq4_v16i Cn = C;
+      if (b + 1 < NB) Cn = mf(b + 1, Aq[(b + 1) % 3]);
+      // block b+1's MFMA is issued before block b's result is read (two result sets live)
+      __builtin_amdgcn_sched_barrier(0);
+      const float sc = kq4_h2f(w.sc[b >> 1] >> (16 * (b & 1)));
+#pragma unroll
+      for (int v = 0; v < VT; ++v) {
+        t[b][v] = v < VTC ? (sc * xsv[b][v < VTC ? v : 0]) * (float)(C[v] >> 4) : 0.0f;
+        kq4_moe_pin(t[b][v]);
+      }
+      C = Cn;
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    return;
+  }
 #pragma unroll
   for (int b = 0; b < 2 * NU; ++b) {
     uint32_t o[4];
@@ -596,7 +636,33 @@ __global__ __launch_bounds__(1024) void kq4_moe_gu_kernel(
     __syncthreads();
     float t[16][VT];
     kq4_moe_touch(w.n);
-    kq4_moe_terms<8, 2, VT>(w, slab, KQ4_MOE_QTS, sx, lane, t);
+    kq4_moe_terms<8, 2, VT, T1, T1 ? 1 : VT>(w, slab, KQ4_MOE_QTS, sx, lane, t);
+    if (T1) {
+      // one pair: every wave puts its blocks' terms (pair 0: lanes 0-31, v = 0) in LDS, then one
+      // lane per (gate/up, row) adds all of them in block order, the same chain in one pass
+      float *tb = reinterpret_cast<float *>(kq4_moe_lds + nst * SLAB) + 2 * PC * 32;   // [2][32][pitch]
+      const int pitch = 16 * nst + 1;
+      if (h == 0) {
+#pragma unroll
+        for (int b = 0; b < 16; ++b) tb[(m * 32 + r) * pitch + 16 * k + b] = t[b][0];
+      }
+      __syncthreads();
+      if (threadIdx.x < 64) {
+        const int mm = threadIdx.x >> 5, rr = threadIdx.x & 31;
+        const float *src = tb + (mm * 32 + rr) * pitch;
+        float acc = 0.0f;
+        for (int b0 = 0; b0 < nb; b0 += 16) {   // 16 reads, then 16 adds (every stage's 16 are set)
+          float v[16];
+#pragma unroll
+          for (int j = 0; j < 16; ++j) v[j] = src[b0 + j];
+#pragma unroll
+          for (int j = 0; j < 16; ++j)
+            if (b0 + j < nb) acc = acc + v[j];
+        }
+        accb[(mm * PC) * 32 + rr] = acc;
+      }
+      __syncthreads();
+    } else
     // the chains: stage kk's waves add their blocks' terms in order, then hand the sums on
     for (int kk = 0; kk < nst; ++kk) {
       if (k == kk) {
@@ -725,7 +791,46 @@ __global__ __launch_bounds__(1024) void kq4_moe_down_kernel(
     }
     __syncthreads();
     float t[8][VT];
-    if (live) {
+    if (live && T1) {
+      // one pair: the pipelined form of the loop below (scales first, A fragments two blocks
+      // ahead, two MFMAs in flight), pair 0's terms only
+      kq4_moe_touch(wt.n);
+      float xs0[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int cb = cbof(j);
+        xs0[j] = sxb[(cb < 0 ? 0 : cb) * PC + VT * h];
+      }
+      auto rd = [&](int j) {
+        const int cb = cbof(j);
+        return *reinterpret_cast<const kq4_v4i *>(codes + pr * qts + kq4_moe_qpos(cb < 0 ? 0 : cb) +
+                                                  16 * h);
+      };
+      auto mf = [&](int j, kq4_v4i A) {
+        uint32_t o[4];
+        kq4_unpack_half(wt.n[2 * j], wt.n[2 * j + 1], o);
+        const kq4_v4i B = {(int)o[0], (int)o[1], (int)o[2], (int)o[3]};
+        return kq4_moe_mfma(A, B);
+      };
+      kq4_v4i Aq[3];
+      Aq[0] = rd(0);
+      Aq[1] = rd(1);
+      kq4_v16i C = mf(0, Aq[0]);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        if (j + 2 < 8) Aq[(j + 2) % 3] = rd(j + 2);
+        kq4_v16i Cn = C;
+        if (j + 1 < 8) Cn = mf(j + 1, Aq[(j + 1) % 3]);
+        __builtin_amdgcn_sched_barrier(0);
+        const float sc = kq4_h2f(wt.sc[j >> 1] >> (16 * (j & 1)));
+        t[j][0] = (sc * xs0[j]) * (float)(C[0] >> 4);   // C = 16*S exactly
+        kq4_moe_pin(t[j][0]);
+#pragma unroll
+        for (int v = 1; v < VT; ++v) t[j][v] = 0.0f;
+        C = Cn;
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    } else if (live) {
       kq4_moe_touch(wt.n);
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
@@ -831,7 +936,8 @@ int kq4_launch_moe_dbg(float *Y, const float *X, const int *sel, const float *pr
                        (3 * ne + 2 * 256) * sizeof(int), s, ws.ex_off, ws.ex_pair, ws.rec, slots,
                        sel, n_pairs, ne, X, ws.xq, ws.xd, T, d);
   const size_t lds_gu = (size_t)nst * kq4_moe_slab(16, KQ4_MOE_PCG) +
-                        2 * KQ4_MOE_PCG * 32 * sizeof(float);
+                        2 * KQ4_MOE_PCG * 32 * sizeof(float) +
+                        (t1 ? (size_t)2 * 32 * (16 * nst + 1) * sizeof(float) : 0);   // T1 terms
   hipLaunchKernelGGL(t1 ? kq4_moe_gu_kernel<true> : kq4_moe_gu_kernel<false>,
                      dim3((unsigned)(slots * cbe)), dim3(128 * nst), lds_gu, s, G, U, ws.xq, ws.xd,
                      ws.rec, ws.ex_pair, ws.avq, ws.avd, g_out, u_out, av_out, d, ef, tk, sel, X, ne);
