@@ -27,6 +27,8 @@
 #include "kq4_common.h"
 #include "kq4_internal.h"
 
+#include <stdlib.h>
+
 #define KQ4_MOE_MAXTK 32
 #define KQ4_MOE_MAXNE 2048  // routing: a lane's experts fit one 32-bit mask
 #define KQ4_MOE_PCG 4       // gate/up pairs per pass: MFMA token rows 4*(lane/32)+v, v < 2
@@ -952,11 +954,20 @@ int kq4_launch_moe_dbg(float *Y, const float *X, const int *sel, const float *pr
     const int b0 = e * cbe, nh = ((b0 + cbe - 1) >> 3) - (b0 >> 3) + 1;
     nhl = nh > nhl ? nh : nhl;
   }
-  // row sets per workgroup: as many as fit 16 waves, but keep about two workgroups per CU
+  // row sets per workgroup: as many as fit 16 waves, keeping about two workgroups per CU
   const int nrs = d / 32;
   int rsg = 16 / nhl;
   const int spread = (slots * nrs) / (2 * (ws.ncu > 0 ? ws.ncu : 256));
   rsg = rsg < spread ? rsg : spread;
+  // Capped at 1 by default: one row set per workgroup (nhl waves) measured fastest at every T
+  // (Qwen3-30B-A3B T = 64: 114.5 us at up to 4 row sets per workgroup, 16 waves, against 108.1 us;
+  // small workgroups let a CU overlap one's loads with another's chain), although each then
+  // stages the band's codes for itself. KQ4_MOE_RSG sets the cap (for measurement).
+  static const int rsg_max = [] {
+    const char *v = getenv("KQ4_MOE_RSG");
+    return v ? atoi(v) : 1;
+  }();
+  rsg = rsg < rsg_max ? rsg : rsg_max;
   rsg = rsg < 1 ? 1 : (rsg > nrs ? nrs : rsg);
   const int ngrp = (nrs + rsg - 1) / rsg;
   const size_t lds_dn = (size_t)KQ4_MOE_PCD * (((cbe + 1) / 2) * 80) +
