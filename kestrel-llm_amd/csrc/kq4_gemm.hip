@@ -281,8 +281,10 @@ static hipError_t gemm_launch(float *out, const float *res, const uint8_t *w,
     else
       return hipErrorInvalidValue;
   } else if (chain == KQ4_CHAIN_CTILE) {
-    hipLaunchKernelGGL((kq4_gemm_kernel<KQ4_CHAIN_CTILE, TM, TN, 0>), grid, dim3(256), 0, s, out,
-                       res, w, act, rows, n_tok, nb, nst, mtiles, ntiles);
+    if constexpr (TM == 2 && TN == 2) return hipErrorInvalidValue;   // capped by the planner
+    else
+      hipLaunchKernelGGL((kq4_gemm_kernel<KQ4_CHAIN_CTILE, TM, TN, 0>), grid, dim3(256), 0, s,
+                         out, res, w, act, rows, n_tok, nb, nst, mtiles, ntiles);
   } else if (chain == KQ4_CHAIN_GEMV32) {
     hipLaunchKernelGGL((kq4_gemm_kernel<KQ4_CHAIN_GEMV32, TM, TN, 0>), grid, dim3(256), 0, s, out,
                        res, w, act, rows, n_tok, nb, nst, mtiles, ntiles);
@@ -296,7 +298,9 @@ static hipError_t gemm_launch(float *out, const float *res, const uint8_t *w,
 }
 
 // The largest of the 128x128, 64x128 and 64x64 (tokens x rows) tiles that gives at least two
-// tiles per CU (else 64x64). KQ4_GEMM_TILE = 1/2/3 forces one (for measurement).
+// tiles per CU (else 64x64). The C-tile chain (two accumulator sets) takes 64x128 at most: at
+// 128x128 it needs more than 256 registers and spills. KQ4_GEMM_TILE = 1/2/3 forces one (for
+// measurement; the C-tile chain still caps it).
 int kq4_launch_gemm(float *out, const float *res, const uint8_t *w, const KQ4GemmAct &act,
                     int rows, int cols, int n_tok, int chain, int ncu, hipStream_t s, int wf) {
   const int nb = cols / 32;
@@ -309,6 +313,7 @@ int kq4_launch_gemm(float *out, const float *res, const uint8_t *w, const KQ4Gem
   static const int force = [] { const char *e = getenv("KQ4_GEMM_TILE"); return e ? atoi(e) : 0; }();
   int pick = force >= 1 && force <= 3 ? force
              : tiles(128, 128) >= 2L * ncu ? 1 : (tiles(64, 128) >= 2L * ncu ? 2 : 3);
+  if (chain == KQ4_CHAIN_CTILE && pick == 1) pick = 2;
   hipError_t e;
   if (pick == 1) e = gemm_launch<2, 2>(out, res, w, act, rows, n_tok, nb, nst, chain, wf, s);
   else if (pick == 2) e = gemm_launch<1, 2>(out, res, w, act, rows, n_tok, nb, nst, chain, wf, s);

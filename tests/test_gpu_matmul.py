@@ -143,6 +143,26 @@ def test_gemm_bit_exact(kq4, torch_dev, orc, n, chain):
     assert r <= TOL
 
 
+# The tile planner takes 128x128 tiles from 2 per CU (n = 2048, 4096 rows: 512 tiles), 64x128
+# below that (2048 rows); the C-tile chain is capped at 64x128. Short K keeps the oracle quick.
+@pytest.mark.parametrize("n,rows,chain", [(2048, 4096, 0), (2048, 4096, 1), (2048, 4096, 3),
+                                          (2048, 2048, 2), (2048, 2048, 3)])
+def test_gemm_large_tiles_bit_exact(kq4, torch_dev, orc, n, rows, chain):
+    torch = torch_dev
+    cols = 128
+    w, x = case(rows, cols, n, 700 + rows + chain)
+    want = orc.matmul(w, x, rows, cols, chain=chain)
+    out = torch.empty((n, rows), dtype=torch.float32, device="cuda")
+    kq4.matmul_dev(out, to_dev(torch, x), wdev(kq4, torch, w, rows, cols), rows, cols,
+                   chain=chain)
+    torch.cuda.synchronize()
+    got = host(out)
+    main = (n & ~3) if chain == 0 else n
+    assert np.array_equal(got[:main].view(np.uint32), want[:main].view(np.uint32))
+    r, _ = rel_err(got, want)
+    assert r <= TOL
+
+
 def test_gemm_from_prequantized(kq4, torch_dev, orc):
     torch = torch_dev
     rows, cols, n = 128, 1024, 40
