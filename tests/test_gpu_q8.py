@@ -59,6 +59,22 @@ def test_q8_gemm_bit_exact(kq4, torch_dev, orc, rows, cols, g, n, chain):
     assert np.array_equal(out.cpu().numpy().view(np.uint32), want.view(np.uint32))
 
 
+# 128x128 tiles (2048 tokens x 4096 rows: 512 tiles) and 64x128 (2048 rows); short K keeps the
+# oracle quick
+@pytest.mark.parametrize("n,rows,chain", [(2048, 4096, 0), (2048, 4096, 4), (2048, 2048, 2)])
+def test_q8_gemm_large_tiles_bit_exact(kq4, torch_dev, orc, n, rows, chain):
+    torch = torch_dev
+    cols = 256
+    w = q8_tiles_synth(rows, cols, 8, rows + chain)
+    x = synth.make_activations(n, cols, 5 + chain)
+    want = orc.q8_matmul(w, x, rows, cols, chain=chain, g=8)
+    W = kq4.q8_prepare_dev(w, rows, cols, g=8)
+    out = torch.empty((n, rows), dtype=torch.float32, device="cuda")
+    kq4.q8_matmul_dev(out, to_dev(torch, x), W, rows, cols, chain=chain)
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy().view(np.uint32), want.view(np.uint32))
+
+
 @pytest.mark.parametrize("n", [1, 6])
 def test_q8_gemv_explicit_chains(kq4, torch_dev, orc, n):
     """GEMV32 (fused, f32 scale) and Q8GEMM (unfused, f16 scale) forced at decode sizes."""
