@@ -626,6 +626,21 @@ int kq4_rmsnorm_matmul_multi_dev(int n_mats, float *const *out, const float *con
   // codes (the same workspace carve matmul_impl makes for its own quantization, so it stays)
   const int nb = cols / 32;
   const size_t qbytes = al256((size_t)n_batch * cols) + al256((size_t)n_batch * nb * sizeof(float));
+  if (n_batch == 1) {
+    // One token: the norm is written in fp32 and the matmul quantizes it in its own kernel (the
+    // same codes), the cheaper GEMV form at one token (measured 0.2-0.3 us per call, Qwen3-8B and
+    // Qwen3-VL-2B QKV). Without a caller buffer the fp32 row sits above the carve matmul_impl
+    // makes for its own quantization, reserved first so that matmul_impl does not reallocate.
+    float *nx = normed;
+    if (!nx) {
+      if ((rc = ensure(ds->ws, qbytes + al256((size_t)cols * sizeof(float))))) return rc;
+      nx = reinterpret_cast<float *>(static_cast<char *>(ds->ws.p) + qbytes);
+    }
+    KQ4_HIP((hipError_t)kq4_launch_rms_norm(x, norm_w, nx, nullptr, nullptr, 1, cols, eps,
+                                            order == KQ4_RMS_SERIAL, (hipStream_t)stream));
+    return matmul_impl(n_mats, out, residual, w, rows, cols, nx, nullptr, nullptr, 1, chain,
+                       (hipStream_t)stream);
+  }
   if ((rc = ensure(ds->ws, qbytes))) return rc;
   Carve cv{static_cast<char *>(ds->ws.p)};
   int8_t *q = cv.take<int8_t>((size_t)n_batch * cols);

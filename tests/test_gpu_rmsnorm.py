@@ -77,6 +77,23 @@ def test_rmsnorm_matmul_multi(kq4, torch_dev, orc, mats, cols, n):
         assert rel <= TOL, (rel, mx)
 
 
+@pytest.mark.parametrize("n", [1, 2])   # one token keeps the fp32 norm in the workspace
+def test_rmsnorm_matmul_without_normed_buffer(kq4, torch_dev, orc, n):
+    torch = torch_dev
+    mats, cols = [6144, 6144], 2048
+    x, nw = rows(n, cols, 11 + n)
+    ws = [synth.make_q4_weights(r, cols, 200 + i) for i, r in enumerate(mats)]
+    normed = orc.rms_norm(x, nw, cols, 1e-6, chunked=True)
+    W = [kq4.prepare_dev(to_dev(torch, w), r, cols) for w, r in zip(ws, mats)]
+    outs = [torch.empty((n, r), dtype=torch.float32, device="cuda") for r in mats]
+    kq4.rmsnorm_matmul_multi_dev(outs, to_dev(torch, x), to_dev(torch, nw), 1e-6, W, mats, cols)
+    refs = [torch.empty_like(o) for o in outs]
+    kq4.matmul_multi_dev(refs, to_dev(torch, normed), W, mats, cols)
+    torch.cuda.synchronize()
+    for o, r in zip(outs, refs):
+        assert np.array_equal(o.cpu().numpy().view(np.uint32), r.cpu().numpy().view(np.uint32))
+
+
 def test_rms_norm_rejects_bad_shapes(kq4, torch_dev):
     torch = torch_dev
     x = torch.zeros((1, 12), dtype=torch.float32, device="cuda")
