@@ -31,7 +31,9 @@ def ulps(a, b):
 
 
 SHAPES = {"small": dict(hidden=256, experts=16, top_k=4, ef=64),
-          "qwen3_30b_a3b": synth.QWEN3_30B_A3B_MOE}
+          "qwen3_30b_a3b": synth.QWEN3_30B_A3B_MOE,
+          # the largest hidden size the kernels take (8 stages of 16 blocks)
+          "wide": dict(hidden=4096, experts=12, top_k=3, ef=96)}
 
 
 def test_route(kq4, torch_dev, orc):
@@ -75,7 +77,7 @@ def test_route_edge_cases(kq4, torch_dev, orc, ne, tk):
 
 
 @pytest.mark.parametrize("T", [1, 7, 64])
-@pytest.mark.parametrize("shape", ["small", "qwen3_30b_a3b"])
+@pytest.mark.parametrize("shape", ["small", "qwen3_30b_a3b", "wide"])
 def test_moe_stages(kq4, torch_dev, orc, shape, T):
     torch = torch_dev
     cfg = SHAPES[shape]
