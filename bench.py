@@ -522,7 +522,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
-              "(the path would shard along weight rows / experts, see DESIGN.md)",
+              "(the path would shard along weight rows for the dense matmuls and along experts "
+              "for the MoE, each GPU running these kernels on its share)",
               file=sys.stderr)
         sys.exit(2)
     if args.calibrate_copy:
