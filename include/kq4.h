@@ -28,6 +28,14 @@
  * vllm_safetensors.c:4670-4672), the library keeps one workspace per device; calls that
  * overlap on one device (different host threads or different streams) race on it.
  *
+ * HIP graphs: the device-pointer calls may be captured. A captured call keeps the workspace it
+ * was recorded with; the library never frees a workspace before kq4_shutdown (growing it
+ * allocates a new one and keeps the old one for the graphs that use it), so a graph stays valid
+ * whatever calls run after its capture. The workspace cannot grow while a stream is being
+ * captured (that needs hipMalloc): such a call returns KQ4_EINVAL and launches nothing. Size it
+ * before capturing with kq4_workspace_reserve (kq4_matmul_workspace_bytes,
+ * kq4_moe_workspace_bytes), or by running the same calls once eagerly.
+ *
  * Error convention: device-pointer calls return KQ4_OK (0) or a negative KQ4_E* code;
  * host-pointer drop-in calls return 1 (done on the GPU) or 0 (not done: the caller runs its
  * CPU path). kq4_last_error() describes the last failure of the calling thread.
@@ -52,7 +60,14 @@ extern "C" {
 /* fp32 accumulation chain (how per-block products are summed; integer block sums are the
  * same in all of them). AUTO is the reference's dispatch (q4x4_gemm_batched
  * vllm_safetensors.c:4593-4631): n_batch <= 3 -> CTILE; n_batch > 3 -> ASM on the first
- * n_batch & ~3 tokens and CTILE on the rest. */
+ * n_batch & ~3 tokens and CTILE on the rest.
+ * The prefill GEMM (n_batch > 8) replays the selected chain per output bit for bit. The decode
+ * GEMV (n_batch <= 8, and the 1..3-token AUTO tail) takes from the chain only its activation
+ * scale (f16-rounded for ASM tokens, f32 otherwise): it splits K over waves and sums each
+ * wave's terms in block order (one token: a lo and a hi chain per half block, as CTILE; two or
+ * more: one term per block, as GEMV32), then adds the waves' sums in a fixed order. So CTILE and
+ * GEMV32 run the same GEMV, whose outputs match either reference chain within 1e-5 of the
+ * output's magnitude, not bit for bit. */
 #define KQ4_CHAIN_AUTO 0
 #define KQ4_CHAIN_CTILE 1   /* q4x4_dot1_group16, vllm_safetensors.c:4180-4216 */
 #define KQ4_CHAIN_GEMV32 2  /* q4x4_dot1_group16_gemv (M4f), :4229-4251 */
@@ -139,6 +154,18 @@ int kq4_moe_ffn(float *Y, const float *X, const int *sel, const float *pr, int T
                 uint64_t wkey);
 
 /* ---- device-pointer API (stream-ordered, asynchronous) ----------------------------------- */
+
+/* Workspace bytes the device-pointer matmuls (kq4_matmul_dev, _multi_dev, _silu_dev,
+ * kq4_rmsnorm_matmul_multi_dev and the q8 twins) need for n_batch tokens of cols columns, and
+ * the MoE calls (kq4_moe_ffn_dev, kq4_moe_ffn_stages_dev, kq4_moe_layer_dev) for T tokens; 0 for
+ * a bad shape. The workspace is shared: reserve the largest any call will need. No counterpart
+ * in the reference (its scratch grows inside the op, xq_scratch_ensure
+ * vllm_safetensors.c:4670-4695); for callers that capture HIP graphs. */
+size_t kq4_matmul_workspace_bytes(int n_batch, int cols);
+size_t kq4_moe_workspace_bytes(int T, int tk, int ne, int d, int ef);
+/* Grows the current device's workspace to at least `bytes` now (not while the calling thread's
+ * stream is being captured). */
+int kq4_workspace_reserve(size_t bytes);
 
 /* Size in bytes of the stream-layout copy of a rows x cols q4 matrix (0 for a bad shape):
  * 9216 B per (32-row set, 16-block stage), rows rounded up to 32, blocks up to 16. */

@@ -10,6 +10,7 @@
 
 #include <mutex>
 #include <unordered_map>
+#include <vector>
 
 namespace {
 
@@ -58,9 +59,9 @@ const int kMaxDev = 16;
 struct DevState {
   bool ready = false;
   int ncu = 256;        // compute units (sizes the GEMV grid)
-  Buf ws;    // quantized activations, MoE staging
+  Buf ws;    // device-API workspace: quantized activations, MoE routing and staging
+  std::vector<void *> retired;   // outgrown device-API workspaces, freed by kq4_shutdown
   Buf hx, hu, hres, hout, hw, hsel, hpr, hstage;   // staging for the host-pointer API
-  Buf rt;    // MoE routing of the fused layer call: logits, sel, pr
   std::unordered_map<uint64_t, WEntry> wcache;
 };
 
@@ -81,9 +82,13 @@ int cur_dev(DevState **out) {
   return KQ4_OK;
 }
 
+size_t grow_size(size_t bytes) { return al256(bytes > 4096 ? bytes + bytes / 4 : 4096); }
+
+// Staging buffers of the host-pointer API, whose calls are synchronous and cannot be captured
+// (they copy from and to host memory): grown by freeing the old buffer once the device is idle.
 int ensure(Buf &b, size_t bytes) {
   if (b.cap >= bytes) return KQ4_OK;
-  size_t n = al256(bytes > 4096 ? bytes + bytes / 4 : 4096);
+  const size_t n = grow_size(bytes);
   if (b.p) {
     KQ4_HIP(hipDeviceSynchronize());   // in-flight kernels may still read the old buffer
     KQ4_HIP(hipFree(b.p));
@@ -98,6 +103,38 @@ int ensure(Buf &b, size_t bytes) {
   return KQ4_OK;
 }
 
+// A device-API call's workspace: the device's growable one, or a fixed buffer it must fit in.
+struct Ws {
+  Buf *b;
+  DevState *ds;   // nullptr: fixed (never grows)
+};
+
+// Makes ws hold at least `bytes`. A HIP graph captured around a device-API call keeps the
+// workspace address it was recorded with, so a workspace is never freed while the library runs:
+// growth allocates a larger one and retires the old one (freed by kq4_shutdown), which graphs
+// captured before the growth go on using. Growth needs hipMalloc, which stream capture does not
+// allow, so a call on a capturing stream that would grow the workspace fails with KQ4_EINVAL
+// before it launches anything (kq4_workspace_reserve sizes it beforehand).
+int ensure_ws(const Ws &ws, size_t bytes, hipStream_t s) {
+  Buf &b = *ws.b;
+  if (b.cap >= bytes) return KQ4_OK;
+  if (!ws.ds)
+    return fail(KQ4_EINVAL, "the call needs %zu B of workspace; its fixed buffer holds %zu B",
+                bytes, b.cap);
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  KQ4_HIP(hipStreamIsCapturing(s, &cs));
+  if (cs != hipStreamCaptureStatusNone)
+    return fail(KQ4_EINVAL, "the workspace must grow to %zu B (it holds %zu B) while the stream "
+                "is being captured; call kq4_workspace_reserve before capturing", bytes, b.cap);
+  const size_t n = grow_size(bytes);
+  void *p = nullptr;
+  if (hipMalloc(&p, n) != hipSuccess) return fail(KQ4_ENOMEM, "hipMalloc(%zu) failed", n);
+  if (b.p) ws.ds->retired.push_back(b.p);
+  b.p = p;
+  b.cap = n;
+  return KQ4_OK;
+}
+
 struct Carve {   // bump allocator over a workspace
   char *base;
   size_t off = 0;
@@ -108,6 +145,12 @@ struct Carve {   // bump allocator over a workspace
     return p;
   }
 };
+
+// Bytes of a matmul's quantized activations (int8 codes + f32 scales, token-major) in the
+// workspace.
+size_t qa_bytes(int n, int cols) {
+  return al256((size_t)n * cols) + al256((size_t)n * (cols / 32) * sizeof(float));
+}
 
 bool shape_ok(int rows, int cols) { return rows > 0 && rows % 4 == 0 && cols > 0 && cols % 32 == 0; }
 
@@ -179,7 +222,7 @@ bool gemv_fq(long work, int n, bool silu) {
 
 // GEMV over n_mats matrices for n tokens (n <= 8): from fp32 x (quantized in the kernel or by a
 // separate launch; with xu the activation is silu_mul(x, xu)) or from token-major xq/xd.
-int run_gemv(DevState *ds, int n_mats, float *const *out, const float *const *res,
+int run_gemv(DevState *ds, const Ws &wsp, int n_mats, float *const *out, const float *const *res,
              const uint8_t *const *w, const int *rows, int cols, const float *x, const float *xu,
              const int8_t *xq, const float *xd, int n, int asm_tokens, hipStream_t s,
              int wf = 0) {
@@ -197,9 +240,8 @@ int run_gemv(DevState *ds, int n_mats, float *const *out, const float *const *re
       a.xf = x;
       a.xu = xu;
     } else {
-      if ((rc = ensure(ds->ws, al256((size_t)n * cols) + al256((size_t)n * nb * sizeof(float)))))
-        return rc;
-      Carve cv{static_cast<char *>(ds->ws.p)};
+      if ((rc = ensure_ws(wsp, qa_bytes(n, cols), s))) return rc;
+      Carve cv{static_cast<char *>(wsp.b->p)};
       int8_t *q = cv.take<int8_t>((size_t)n * cols);
       float *d = cv.take<float>((size_t)n * nb);
       KQ4_HIP((hipError_t)kq4_launch_quantize(x, q, d, nullptr, n, cols, 0, s, 0, xu));
@@ -230,10 +272,11 @@ int run_gemv(DevState *ds, int n_mats, float *const *out, const float *const *re
 }
 
 // x (fp32; with xu the activation is silu_mul(x, xu)) or xq_in/xd_in (pre-quantized).
+// wsp (may be null): the workspace to carve instead of the device's growable one.
 int matmul_impl(int n_mats, float *const *out, const float *const *res, const uint8_t *const *w,
                 const int *rows, int cols, const float *x, const int8_t *xq_in,
                 const float *xd_in, int n, int chain, hipStream_t s, const float *xu = nullptr,
-                int wf = 0) {
+                int wf = 0, const Ws *wsp = nullptr) {
   if (n_mats < 1 || n_mats > KQ4_MAX_MATS) return fail(KQ4_EINVAL, "n_mats=%d", n_mats);
   if (wf ? (chain != KQ4_CHAIN_AUTO && chain != KQ4_CHAIN_GEMV32 && chain != KQ4_CHAIN_Q8GEMM)
          : (chain < KQ4_CHAIN_AUTO || chain > KQ4_CHAIN_ASM))
@@ -254,8 +297,9 @@ int matmul_impl(int n_mats, float *const *out, const float *const *res, const ui
   DevState *ds = nullptr;
   int rc = cur_dev(&ds);
   if (rc) return rc;
+  const Ws ws = wsp ? *wsp : Ws{&ds->ws, ds};
   const int nb = cols / 32;
-  const size_t qbytes = al256((size_t)n * cols) + al256((size_t)n * nb * sizeof(float));
+  const size_t qbytes = qa_bytes(n, cols);
 
   if (wf) {
     // Q8_0: the VDOT chain (f32 activation scale, fused) or the GEMM chain (f16-rounded scale,
@@ -263,10 +307,10 @@ int matmul_impl(int n_mats, float *const *out, const float *const *res, const ui
     // reference's q8 wrappers dispatch (vllm_safetensors.c:5977-6001, :6071-6091)
     const bool gchain = chain == KQ4_CHAIN_Q8GEMM || (chain == KQ4_CHAIN_AUTO && n >= 2);
     if (n <= KQ4_GEMV_MAX_M)
-      return run_gemv(ds, n_mats, out, res, w, rows, cols, x, nullptr, xq_in, xd_in, n,
+      return run_gemv(ds, ws, n_mats, out, res, w, rows, cols, x, nullptr, xq_in, xd_in, n,
                       gchain ? n : 0, s, gchain ? 2 : 1);
-    if ((rc = ensure(ds->ws, qbytes))) return rc;
-    Carve cv{static_cast<char *>(ds->ws.p)};
+    if ((rc = ensure_ws(ws, qbytes, s))) return rc;
+    Carve cv{static_cast<char *>(ws.b->p)};
     KQ4GemmAct act{xq_in, cols, 32, xd_in, nb, 1};
     if (x) {
       int8_t *q = cv.take<int8_t>((size_t)n * cols);
@@ -282,15 +326,15 @@ int matmul_impl(int n_mats, float *const *out, const float *const *res, const ui
   }
 
   if (n <= KQ4_GEMV_MAX_M)
-    return run_gemv(ds, n_mats, out, res, w, rows, cols, x, xu, xq_in, xd_in, n,
+    return run_gemv(ds, ws, n_mats, out, res, w, rows, cols, x, xu, xq_in, xd_in, n,
                     asm_tokens_for(chain, n), s);
 
   // prefill: int8-MFMA GEMM on the main segment, GEMV on the 1..3-token CTILE tail (AUTO)
   const int main_n = chain == KQ4_CHAIN_AUTO ? (n & ~3) : n;
   const int tail = n - main_n;
   const int main_chain = chain == KQ4_CHAIN_AUTO ? KQ4_CHAIN_ASM : chain;
-  if ((rc = ensure(ds->ws, qbytes))) return rc;
-  Carve cv{static_cast<char *>(ds->ws.p)};
+  if ((rc = ensure_ws(ws, qbytes, s))) return rc;
+  Carve cv{static_cast<char *>(ws.b->p)};
   KQ4GemmAct act;
   const int8_t *xq_t = nullptr;
   const float *xd_t = nullptr;
@@ -319,14 +363,34 @@ int matmul_impl(int n_mats, float *const *out, const float *const *res, const ui
       o2[i] = out[i] + (size_t)main_n * rows[i];
       r2[i] = (res && res[i]) ? res[i] + (size_t)main_n * rows[i] : nullptr;
     }
-    return run_gemv(ds, n_mats, o2, r2, w, rows, cols, nullptr, nullptr, xq_t, xd_t, tail, 0, s);
+    return run_gemv(ds, ws, n_mats, o2, r2, w, rows, cols, nullptr, nullptr, xq_t, xd_t, tail, 0,
+                    s);
   }
   return KQ4_OK;
 }
 
+// Workspace bytes of the expert FFN's staging (expert CSR, slot records, quantized X and av,
+// unweighted partials) and of the fused layer's routing (logits, sel, pr) carved before it.
+size_t moe_stage_bytes(int T, int tk, int ne, int d, int ef) {
+  const size_t np = (size_t)T * tk;
+  return al256((ne + 1) * sizeof(int)) + al256(np * sizeof(int)) +
+         al256((size_t)ne * KQ4_MOE_REC * sizeof(int)) + al256((size_t)T * d) +
+         al256((size_t)T * (d / 32) * sizeof(float)) + al256(np * ef) +
+         al256(np * (ef / 32) * sizeof(float)) + al256(np * d * sizeof(float));
+}
+
+size_t moe_route_bytes(int T, int tk, int ne) {
+  const size_t np = (size_t)T * tk;
+  return al256((size_t)T * ne * sizeof(float)) + al256(np * sizeof(int)) +
+         al256(np * sizeof(float));
+}
+
+// The expert FFN; its staging is carved from the workspace at byte offset `off` (the fused
+// layer call keeps its routing below it).
 int moe_impl(float *Y, const float *X, const int *sel, const float *pr, int T, int tk,
              const uint8_t *G, const uint8_t *U, const uint8_t *D, int ne, int d, int ef,
-             float *g_out, float *u_out, float *av_out, const float *av_in, hipStream_t s) {
+             float *g_out, float *u_out, float *av_out, const float *av_in, hipStream_t s,
+             size_t off = 0) {
   if (T < 0 || tk < 1 || tk > 32 || ne < 1 || !kq4_moe_shape_ok(d, ef))
     return fail(KQ4_EINVAL, "moe: T=%d tk=%d ne=%d d=%d ef=%d (need d, ef %% 32 == 0, "
                 "d <= 4096, ef <= 3840)", T, tk, ne, d, ef);
@@ -337,12 +401,8 @@ int moe_impl(float *Y, const float *X, const int *sel, const float *pr, int T, i
   int rc = cur_dev(&ds);
   if (rc) return rc;
   const size_t np = (size_t)T * tk;
-  const size_t need = al256((ne + 1) * sizeof(int)) + al256(np * sizeof(int)) +
-                      al256((size_t)ne * KQ4_MOE_REC * sizeof(int)) + al256((size_t)T * d) +
-                      al256((size_t)T * (d / 32) * sizeof(float)) + al256(np * ef) +
-                      al256(np * (ef / 32) * sizeof(float)) + al256(np * d * sizeof(float));
-  if ((rc = ensure(ds->ws, need))) return rc;
-  Carve cv{static_cast<char *>(ds->ws.p)};
+  if ((rc = ensure_ws(Ws{&ds->ws, ds}, off + moe_stage_bytes(T, tk, ne, d, ef), s))) return rc;
+  Carve cv{static_cast<char *>(ds->ws.p), off};
   KQ4MoeWs ws;
   ws.ex_off = cv.take<int>(ne + 1);
   ws.ex_pair = cv.take<int>(np);
@@ -460,16 +520,35 @@ void kq4_shutdown(void) {
     if (!s.ready) continue;
     (void)hipSetDevice(d);
     (void)hipDeviceSynchronize();
-    Buf *bufs[] = {&s.ws, &s.hx, &s.hres, &s.hout, &s.hw, &s.hsel, &s.hpr, &s.hstage};
+    Buf *bufs[] = {&s.ws, &s.hx, &s.hu, &s.hres, &s.hout, &s.hw, &s.hsel, &s.hpr, &s.hstage};
     for (Buf *b : bufs) {
       if (b->p) (void)hipFree(b->p);
       *b = Buf();
     }
+    for (void *p : s.retired) (void)hipFree(p);
+    s.retired.clear();
     for (auto &kv : s.wcache) (void)hipFree(kv.second.p);
     s.wcache.clear();
     s.ready = false;
   }
   (void)hipSetDevice(cur);
+}
+
+size_t kq4_matmul_workspace_bytes(int n_batch, int cols) {
+  if (n_batch < 0 || cols <= 0 || cols % 32) return 0;
+  return qa_bytes(n_batch, cols) + al256((size_t)cols * sizeof(float));
+}
+
+size_t kq4_moe_workspace_bytes(int T, int tk, int ne, int d, int ef) {
+  if (T < 0 || tk < 1 || tk > 32 || ne < 1 || !kq4_moe_shape_ok(d, ef)) return 0;
+  return moe_route_bytes(T, tk, ne) + moe_stage_bytes(T, tk, ne, d, ef);
+}
+
+int kq4_workspace_reserve(size_t bytes) {
+  DevState *ds = nullptr;
+  int rc = cur_dev(&ds);
+  if (rc) return rc;
+  return ensure_ws(Ws{&ds->ws, ds}, bytes, nullptr);
 }
 
 int kq4_quantize_dev(int8_t *xq, float *xd, float *xde, const float *x, int n_batch, int cols,
@@ -624,8 +703,7 @@ int kq4_rmsnorm_matmul_multi_dev(int n_mats, float *const *out, const float *con
   if (rc) return rc;
   // the normalised activations are quantized where they are formed; the matmul then reads the
   // codes (the same workspace carve matmul_impl makes for its own quantization, so it stays)
-  const int nb = cols / 32;
-  const size_t qbytes = al256((size_t)n_batch * cols) + al256((size_t)n_batch * nb * sizeof(float));
+  const size_t qbytes = qa_bytes(n_batch, cols);
   if (n_batch == 1) {
     // One token: the norm is written in fp32 and the matmul quantizes it in its own kernel (the
     // same codes), the cheaper GEMV form at one token (measured 0.2-0.3 us per call, Qwen3-8B and
@@ -633,7 +711,9 @@ int kq4_rmsnorm_matmul_multi_dev(int n_mats, float *const *out, const float *con
     // makes for its own quantization, reserved first so that matmul_impl does not reallocate.
     float *nx = normed;
     if (!nx) {
-      if ((rc = ensure(ds->ws, qbytes + al256((size_t)cols * sizeof(float))))) return rc;
+      if ((rc = ensure_ws(Ws{&ds->ws, ds}, qbytes + al256((size_t)cols * sizeof(float)),
+                          (hipStream_t)stream)))
+        return rc;
       nx = reinterpret_cast<float *>(static_cast<char *>(ds->ws.p) + qbytes);
     }
     KQ4_HIP((hipError_t)kq4_launch_rms_norm(x, norm_w, nx, nullptr, nullptr, 1, cols, eps,
@@ -641,10 +721,10 @@ int kq4_rmsnorm_matmul_multi_dev(int n_mats, float *const *out, const float *con
     return matmul_impl(n_mats, out, residual, w, rows, cols, nx, nullptr, nullptr, 1, chain,
                        (hipStream_t)stream);
   }
-  if ((rc = ensure(ds->ws, qbytes))) return rc;
+  if ((rc = ensure_ws(Ws{&ds->ws, ds}, qbytes, (hipStream_t)stream))) return rc;
   Carve cv{static_cast<char *>(ds->ws.p)};
   int8_t *q = cv.take<int8_t>((size_t)n_batch * cols);
-  float *dq = cv.take<float>((size_t)n_batch * nb);
+  float *dq = cv.take<float>((size_t)n_batch * (cols / 32));
   hipStream_t s = (hipStream_t)stream;
   KQ4_HIP((hipError_t)kq4_launch_rms_norm(x, norm_w, normed, q, dq, n_batch, cols, eps,
                                           order == KQ4_RMS_SERIAL, s));
@@ -718,9 +798,9 @@ int kq4_moe_router_logits_dev(float *logits, const float *router, const float *X
 int kq4_moe_layer_dev(float *Y, const float *X, const float *router, const uint8_t *G,
                       const uint8_t *U, const uint8_t *D, int T, int ne, int tk, int d, int ef,
                       int *sel_out, float *pr_out, void *stream) {
-  if (T < 0 || ne < 1 || ne > 2048 || tk < 1 || tk > 32 || tk > ne || d <= 0 || d % 32 ||
+  if (T < 0 || ne < 1 || ne > 2048 || tk < 1 || tk > 32 || tk > ne || !kq4_moe_shape_ok(d, ef) ||
       (T && (!Y || !X || !router)))
-    return fail(KQ4_EINVAL, "moe_layer: T=%d ne=%d tk=%d d=%d", T, ne, tk, d);
+    return fail(KQ4_EINVAL, "moe_layer: T=%d ne=%d tk=%d d=%d ef=%d", T, ne, tk, d, ef);
   if ((uintptr_t)router % 16 || (uintptr_t)X % 16)
     return fail(KQ4_EINVAL, "moe_layer: router and X must be 16-byte aligned");
   if (T == 0) return KQ4_OK;
@@ -729,16 +809,17 @@ int kq4_moe_layer_dev(float *Y, const float *X, const float *router, const uint8
   if (rc) return rc;
   hipStream_t s = (hipStream_t)stream;
   const size_t np = (size_t)T * tk;
-  if ((rc = ensure(ds->rt, al256((size_t)T * ne * sizeof(float)) + al256(np * sizeof(int)) +
-                               al256(np * sizeof(float)))))
-    return rc;
-  Carve cv{static_cast<char *>(ds->rt.p)};
+  const size_t rbytes = moe_route_bytes(T, tk, ne);
+  // the routing sits below the expert FFN's staging, so the FFN does not overwrite it
+  if ((rc = ensure_ws(Ws{&ds->ws, ds}, rbytes + moe_stage_bytes(T, tk, ne, d, ef), s))) return rc;
+  Carve cv{static_cast<char *>(ds->ws.p)};
   float *lg = cv.take<float>((size_t)T * ne);
   int *sel = sel_out ? sel_out : cv.take<int>(np);
   float *pr = pr_out ? pr_out : cv.take<float>(np);
   KQ4_HIP((hipError_t)kq4_launch_moe_logits(lg, router, X, T, ne, d, s));
   KQ4_HIP((hipError_t)kq4_launch_moe_route(sel, pr, lg, T, ne, tk, s));
-  return moe_impl(Y, X, sel, pr, T, tk, G, U, D, ne, d, ef, nullptr, nullptr, nullptr, nullptr, s);
+  return moe_impl(Y, X, sel, pr, T, tk, G, U, D, ne, d, ef, nullptr, nullptr, nullptr, nullptr, s,
+                  rbytes);
 }
 
 int kq4_moe_ffn_dev(float *Y, const float *X, const int *sel, const float *pr, int T, int tk,

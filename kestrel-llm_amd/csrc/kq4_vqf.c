@@ -246,11 +246,12 @@ static int layer_matrix(const kq4_vqf *v, const char *const *names, uint64_t bpb
     uint64_t bytes;
     int rc = kq4_vqf_find(v, names[proj], &data, &bytes);
     if (rc) return rc;
-    const uint64_t per = n * k / 32 * bpb;   /* Q4_BYTES / Q8_BYTES (N*K): layer l at l * per */
-    if ((uint64_t)(layer + 1) * per > bytes)
-        return kq4_fail(KQ4_EIO, "vqf: %s holds %llu bytes, layer %d needs %llu",
-                        names[proj], (unsigned long long)bytes, layer,
-                        (unsigned long long)((uint64_t)(layer + 1) * per));
+    /* Q4_BYTES / Q8_BYTES (N*K): layer l at l * per. n, k < 2^31, so per < 2^63; the bound is
+     * checked by division, as (layer + 1) * per can wrap past 2^64 for a crafted header. */
+    const uint64_t per = n * k / 32 * bpb;
+    if ((uint64_t)layer >= bytes / per)
+        return kq4_fail(KQ4_EIO, "vqf: %s holds %llu bytes, too few for layer %d of %llu bytes",
+                        names[proj], (unsigned long long)bytes, layer, (unsigned long long)per);
     if (w) *w = data + (uint64_t)layer * per;
     if (rows) *rows = (int)n;
     if (cols) *cols = (int)k;

@@ -41,6 +41,9 @@ SIGNATURES = [
     ("kq4_q8_matmul_multi_dev", _I, [_I, _P, _P, _P, _P, _I, _P, _I, _I, _P]),
     ("kq4_moe_ffn", _I, [_P, _P, _P, _P, _I, _I, _P, _P, _P, _I, _I, _I, _U64]),
     ("kq4_weights_stream_bytes", ctypes.c_size_t, [_I, _I]),
+    ("kq4_matmul_workspace_bytes", ctypes.c_size_t, [_I, _I]),
+    ("kq4_moe_workspace_bytes", ctypes.c_size_t, [_I, _I, _I, _I, _I]),
+    ("kq4_workspace_reserve", _I, [ctypes.c_size_t]),
     ("kq4_weights_prepare_dev", _I, [_P, _P, _I, _I, _P]),
     ("kq4_quantize_dev", _I, [_P, _P, _P, _P, _I, _I, _I, _P]),
     ("kq4_matmul_dev", _I, [_P, _P, _P, _P, _I, _I, _I, _I, _P]),
@@ -253,8 +256,64 @@ def _tp(t):
     return None if t is None else t.data_ptr()
 
 
+def _need(t, name, dtype, numel, optional=False):
+    """Raises unless t is a contiguous device tensor of `dtype` with at least `numel` elements
+    (the library reads and writes raw pointers: a wrong view would be read out of bounds)."""
+    import torch
+    if t is None:
+        if optional:
+            return
+        raise KQ4Error(f"{name}: missing")
+    if not isinstance(t, torch.Tensor) or not t.is_cuda:
+        raise KQ4Error(f"{name}: not a device tensor")
+    if t.dtype != dtype:
+        raise KQ4Error(f"{name}: dtype {t.dtype}, expected {dtype}")
+    if not t.is_contiguous():
+        raise KQ4Error(f"{name}: not contiguous")
+    if t.numel() < numel:
+        raise KQ4Error(f"{name}: {t.numel()} elements, needs {numel}")
+
+
+def _act(x, cols, name="x"):
+    """Token count of a [n][cols] fp32 activation tensor, checked."""
+    import torch
+    if x is None or x.dim() != 2 or x.shape[1] != cols:
+        raise KQ4Error(f"{name}: expected shape [n, {cols}], got "
+                       f"{None if x is None else tuple(x.shape)}")
+    _need(x, name, torch.float32, x.shape[0] * cols)
+    return x.shape[0]
+
+
+def _mat(w, rows, cols, q8=False):
+    import torch
+    _need(w, "weights", torch.uint8, (q8_stream_bytes if q8 else stream_bytes)(rows, cols))
+
+
+def _outs(outs, residuals, rows, n):
+    import torch
+    if len(outs) != len(rows) or (residuals is not None and len(residuals) != len(rows)):
+        raise KQ4Error("one output (and residual) per matrix")
+    for i, (o, r) in enumerate(zip(outs, rows)):
+        _need(o, f"out[{i}]", torch.float32, n * r)
+        if residuals is not None:
+            _need(residuals[i], f"residual[{i}]", torch.float32, n * r, optional=True)
+
+
 def _stream_ptr(stream):
     return None if stream is None else stream.cuda_stream
+
+
+def matmul_workspace_bytes(n_batch, cols):
+    return lib().kq4_matmul_workspace_bytes(n_batch, cols)
+
+
+def moe_workspace_bytes(T, tk, ne, d, ef):
+    return lib().kq4_moe_workspace_bytes(T, tk, ne, d, ef)
+
+
+def workspace_reserve(nbytes):
+    """Grows the device workspace before a HIP graph capture (see include/kq4.h)."""
+    check(lib().kq4_workspace_reserve(nbytes), "kq4_workspace_reserve")
 
 
 def stream_bytes(rows, cols):
@@ -300,13 +359,18 @@ def q8_prepare_dev(tiles, rows, cols, g=8, stream=None):
 
 
 def q8_matmul_dev(out, x, w, rows, cols, residual=None, chain=CHAIN_AUTO, stream=None):
-    n = x.shape[0]
+    n = _act(x, cols)
+    _mat(w, rows, cols, q8=True)
+    _outs([out], [residual], [rows], n)
     check(lib().kq4_q8_matmul_dev(_tp(out), _tp(x), _tp(residual), _tp(w), rows, cols, n, chain,
                                   _stream_ptr(stream)), "kq4_q8_matmul_dev")
 
 
 def q8_matmul_multi_dev(outs, x, ws, rows, cols, residuals=None, chain=CHAIN_AUTO, stream=None):
-    n = x.shape[0]
+    n = _act(x, cols)
+    for w, r in zip(ws, rows):
+        _mat(w, r, cols, q8=True)
+    _outs(outs, residuals, rows, n)
     res = [None] * len(ws) if residuals is None else residuals
     check(lib().kq4_q8_matmul_multi_dev(len(ws), _ptr_array([_tp(o) for o in outs]),
                                         _ptr_array([_tp(r) for r in res]),
@@ -316,19 +380,30 @@ def q8_matmul_multi_dev(outs, x, ws, rows, cols, residuals=None, chain=CHAIN_AUT
 
 
 def quantize_dev(x, xq, xd, xde=None, chain=CHAIN_AUTO, stream=None):
+    import torch
     n, cols = x.shape
+    _act(x, cols)
+    _need(xq, "xq", torch.int8, n * cols)
+    _need(xd, "xd", torch.float32, n * (cols // 32))
+    _need(xde, "xde", torch.float32, n * (cols // 32), optional=True)
     check(lib().kq4_quantize_dev(_tp(xq), _tp(xd), _tp(xde), _tp(x), n, cols, chain,
                                  _stream_ptr(stream)), "kq4_quantize_dev")
 
 
 def matmul_dev(out, x, w, rows, cols, residual=None, chain=CHAIN_AUTO, stream=None):
-    n = x.shape[0]
+    n = _act(x, cols)
+    _mat(w, rows, cols)
+    _outs([out], [residual], [rows], n)
     check(lib().kq4_matmul_dev(_tp(out), _tp(x), _tp(residual), _tp(w), rows, cols, n, chain,
                                _stream_ptr(stream)), "kq4_matmul_dev")
 
 
 def matmul_silu_dev(out, gate, up, w, rows, cols, residual=None, chain=CHAIN_AUTO, stream=None):
-    n = gate.shape[0]
+    n = _act(gate, cols, "gate")
+    if _act(up, cols, "up") != n:
+        raise KQ4Error("gate and up differ in tokens")
+    _mat(w, rows, cols)
+    _outs([out], [residual], [rows], n)
     check(lib().kq4_matmul_silu_dev(_tp(out), _tp(gate), _tp(up), _tp(residual), _tp(w), rows,
                                     cols, n, chain, _stream_ptr(stream)), "kq4_matmul_silu_dev")
 
@@ -337,14 +412,24 @@ RMS_CHUNKED, RMS_SERIAL = 0, 1
 
 
 def rms_norm_dev(out, x, w, eps, order=RMS_CHUNKED, stream=None):
+    import torch
     n, d = x.shape
+    _act(x, d)
+    _need(out, "out", torch.float32, n * d)
+    _need(w, "w", torch.float32, d)
     check(lib().kq4_rms_norm_dev(_tp(out), _tp(x), _tp(w), n, d, eps, order,
                                  _stream_ptr(stream)), "kq4_rms_norm_dev")
 
 
 def rmsnorm_matmul_multi_dev(outs, x, norm_w, eps, ws, rows, cols, residuals=None,
                              order=RMS_CHUNKED, normed=None, chain=CHAIN_AUTO, stream=None):
-    n = x.shape[0]
+    import torch
+    n = _act(x, cols)
+    _need(norm_w, "norm_w", torch.float32, cols)
+    _need(normed, "normed", torch.float32, n * cols, optional=True)
+    for w, r in zip(ws, rows):
+        _mat(w, r, cols)
+    _outs(outs, residuals, rows, n)
     res = [None] * len(ws) if residuals is None else residuals
     check(lib().kq4_rmsnorm_matmul_multi_dev(
         len(ws), _ptr_array([_tp(o) for o in outs]), _ptr_array([_tp(r) for r in res]),
@@ -355,13 +440,18 @@ def rmsnorm_matmul_multi_dev(outs, x, norm_w, eps, ws, rows, cols, residuals=Non
 
 def silu_mul_dev(gate, up, stream=None):
     """gate <- silu_mul(gate, up) in place (the reference worker's element rule)."""
-    assert gate.numel() == up.numel()
+    import torch
+    _need(gate, "gate", torch.float32, up.numel())
+    _need(up, "up", torch.float32, gate.numel())
     check(lib().kq4_silu_mul_dev(_tp(gate), _tp(up), gate.numel(), _stream_ptr(stream)),
           "kq4_silu_mul_dev")
 
 
 def matmul_multi_dev(outs, x, ws, rows, cols, residuals=None, chain=CHAIN_AUTO, stream=None):
-    n = x.shape[0]
+    n = _act(x, cols)
+    for w, r in zip(ws, rows):
+        _mat(w, r, cols)
+    _outs(outs, residuals, rows, n)
     res = [None] * len(ws) if residuals is None else residuals
     check(lib().kq4_matmul_multi_dev(len(ws), _ptr_array([_tp(o) for o in outs]),
                                      _ptr_array([_tp(r) for r in res]),
@@ -370,13 +460,26 @@ def matmul_multi_dev(outs, x, ws, rows, cols, residuals=None, chain=CHAIN_AUTO, 
                                      _stream_ptr(stream)), "kq4_matmul_multi_dev")
 
 
+def _qact(xq, xd, cols, n):
+    import torch
+    _need(xq, "xq", torch.int8, n * cols)
+    _need(xd, "xd", torch.float32, n * (cols // 32))
+
+
 def matmul_q_dev(out, xq, xd, w, rows, cols, n, residual=None, chain=CHAIN_AUTO, stream=None):
+    _qact(xq, xd, cols, n)
+    _mat(w, rows, cols)
+    _outs([out], [residual], [rows], n)
     check(lib().kq4_matmul_q_dev(_tp(out), _tp(xq), _tp(xd), _tp(residual), _tp(w), rows, cols,
                                  n, chain, _stream_ptr(stream)), "kq4_matmul_q_dev")
 
 
 def matmul_multi_q_dev(outs, xq, xd, ws, rows, cols, n, residuals=None, chain=CHAIN_AUTO,
                        stream=None):
+    _qact(xq, xd, cols, n)
+    for w, r in zip(ws, rows):
+        _mat(w, r, cols)
+    _outs(outs, residuals, rows, n)
     res = [None] * len(ws) if residuals is None else residuals
     check(lib().kq4_matmul_multi_q_dev(len(ws), _ptr_array([_tp(o) for o in outs]),
                                        _ptr_array([_tp(r) for r in res]),
@@ -386,39 +489,78 @@ def matmul_multi_q_dev(outs, xq, xd, ws, rows, cols, n, residuals=None, chain=CH
 
 
 def block_sums_dev(s_lo, s_hi, xq, w, rows, cols, n, stream=None):
+    import torch
+    _need(xq, "xq", torch.int8, n * cols)
+    _mat(w, rows, cols)
+    _need(s_lo, "s_lo", torch.int32, n * rows * (cols // 32))
+    _need(s_hi, "s_hi", torch.int32, n * rows * (cols // 32))
     check(lib().kq4_block_sums_dev(_tp(s_lo), _tp(s_hi), _tp(xq), _tp(w), rows, cols, n,
                                    _stream_ptr(stream)), "kq4_block_sums_dev")
 
 
 def moe_route_dev(sel, pr, logits, tk, stream=None):
+    import torch
     T, ne = logits.shape
+    _need(logits, "logits", torch.float32, T * ne)
+    _need(sel, "sel", torch.int32, T * tk)
+    _need(pr, "pr", torch.float32, T * tk)
     check(lib().kq4_moe_route_dev(_tp(sel), _tp(pr), _tp(logits), T, ne, tk,
                                   _stream_ptr(stream)), "kq4_moe_route_dev")
 
 
 def moe_router_logits_dev(logits, router, X, stream=None):
+    import torch
     T, d = X.shape
     ne = router.shape[0]
+    _act(X, d, "X")
+    _need(router, "router", torch.float32, ne * d)
+    _need(logits, "logits", torch.float32, T * ne)
     check(lib().kq4_moe_router_logits_dev(_tp(logits), _tp(router), _tp(X), T, ne, d,
                                           _stream_ptr(stream)), "kq4_moe_router_logits_dev")
 
 
+def _moe_args(Y, X, G, U, D, ne, d, ef):
+    import torch
+    T = _act(X, d, "X")
+    _need(Y, "Y", torch.float32, T * d)
+    _mat(G, ne * ef, d)
+    _mat(U, ne * ef, d)
+    _mat(D, d, ne * ef)
+    return T
+
+
 def moe_layer_dev(Y, X, router, G, U, D, ne, tk, d, ef, sel=None, pr=None, stream=None):
-    T = X.shape[0]
+    import torch
+    T = _moe_args(Y, X, G, U, D, ne, d, ef)
+    _need(router, "router", torch.float32, ne * d)
+    _need(sel, "sel", torch.int32, T * tk, optional=True)
+    _need(pr, "pr", torch.float32, T * tk, optional=True)
     check(lib().kq4_moe_layer_dev(_tp(Y), _tp(X), _tp(router), _tp(G), _tp(U), _tp(D), T, ne, tk,
                                   d, ef, _tp(sel), _tp(pr), _stream_ptr(stream)),
           "kq4_moe_layer_dev")
 
 
 def moe_ffn_dev(Y, X, sel, pr, G, U, D, ne, d, ef, stream=None):
+    import torch
     T, tk = sel.shape
+    if _moe_args(Y, X, G, U, D, ne, d, ef) != T:
+        raise KQ4Error("X and sel differ in tokens")
+    _need(sel, "sel", torch.int32, T * tk)
+    _need(pr, "pr", torch.float32, T * tk)
     check(lib().kq4_moe_ffn_dev(_tp(Y), _tp(X), _tp(sel), _tp(pr), T, tk, _tp(G), _tp(U),
                                 _tp(D), ne, d, ef, _stream_ptr(stream)), "kq4_moe_ffn_dev")
 
 
 def moe_ffn_stages_dev(Y, X, sel, pr, G, U, D, ne, d, ef, gate=None, up=None, av=None,
                        av_in=None, stream=None):
+    import torch
     T, tk = sel.shape
+    if _moe_args(Y, X, G, U, D, ne, d, ef) != T:
+        raise KQ4Error("X and sel differ in tokens")
+    _need(sel, "sel", torch.int32, T * tk)
+    _need(pr, "pr", torch.float32, T * tk)
+    for name, t in (("gate", gate), ("up", up), ("av", av), ("av_in", av_in)):
+        _need(t, name, torch.float32, T * tk * ef, optional=True)
     check(lib().kq4_moe_ffn_stages_dev(_tp(Y), _tp(X), _tp(sel), _tp(pr), T, tk, _tp(G), _tp(U),
                                        _tp(D), ne, d, ef, _tp(gate), _tp(up), _tp(av),
                                        _tp(av_in), _stream_ptr(stream)),

@@ -60,3 +60,66 @@ def test_graph_replays_match_eager(kq4, torch_dev):
             assert np.array_equal(got.view(np.uint32), exp.view(np.uint32)), (rep, k)
         work()                                 # eager work between replays
         torch.cuda.synchronize()
+
+
+def test_graph_survives_workspace_growth(kq4, torch_dev):
+    """A graph captured around calls that use the library's workspace (the separate quantizer
+    launch of a 6-token GEMV, a 64-token GEMM) stays valid after the workspace grows: growth
+    keeps the old buffer for the graph, and the eager calls after it use the new one. Every
+    replay reproduces the eager result bit for bit."""
+    torch = torch_dev
+    rows, cols = 512, 1024
+    w = kq4.prepare_dev(to_dev(torch, synth.make_q4_weights(rows, cols, 21)), rows, cols)
+    x6 = to_dev(torch, synth.make_activations(6, cols, 22))
+    x64 = to_dev(torch, synth.make_activations(64, cols, 23))
+    o6, o64 = torch.empty((6, rows), device="cuda"), torch.empty((64, rows), device="cuda")
+
+    def work():
+        st = torch.cuda.current_stream()
+        kq4.matmul_dev(o6, x6, w, rows, cols, stream=st)
+        kq4.matmul_dev(o64, x64, w, rows, cols, stream=st)
+
+    work()
+    torch.cuda.synchronize()
+    want = [o6.clone(), o64.clone()]
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        work()
+    # grow the workspace well past anything used so far, then overwrite the new one eagerly
+    kq4.workspace_reserve(512 << 20)
+    big_n, big_cols = 1024, 8192
+    wb = kq4.prepare_dev(to_dev(torch, synth.make_q4_weights(64, big_cols, 24)), 64, big_cols)
+    xb = to_dev(torch, synth.make_activations(big_n, big_cols, 25))
+    ob = torch.empty((big_n, 64), device="cuda")
+    for rep in range(3):
+        o6.fill_(float("nan"))
+        o64.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        for got, exp in zip((o6, o64), want):
+            assert np.array_equal(got.cpu().numpy().view(np.uint32),
+                                  exp.cpu().numpy().view(np.uint32)), rep
+        kq4.matmul_dev(ob, xb, wb, 64, big_cols)   # eager, in the grown workspace
+        torch.cuda.synchronize()
+
+
+def test_growth_during_capture_is_refused(kq4, torch_dev):
+    """A call that would have to grow the workspace while its stream is captured fails with
+    KQ4_EINVAL before launching anything, and the capture stays usable. Its inputs are never
+    read (the call returns first), so they are left uninitialised."""
+    torch = torch_dev
+    rows, cols, n = 4, 32 * 5120, 4096            # 755 MB of quantized activations
+    assert kq4.matmul_workspace_bytes(n, cols) > (640 << 20)
+    w = torch.zeros(kq4.stream_bytes(rows, cols), dtype=torch.uint8, device="cuda")
+    x = torch.empty((n, cols), dtype=torch.float32, device="cuda")
+    out = torch.empty((n, rows), device="cuda")
+    marker = torch.empty(16, device="cuda")
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        marker.fill_(7.0)
+        with pytest.raises(kq4.KQ4Error, match="captured"):
+            kq4.matmul_dev(out, x, w, rows, cols, stream=torch.cuda.current_stream())
+    marker.zero_()
+    graph.replay()
+    torch.cuda.synchronize()
+    assert float(marker.sum()) == 7.0 * 16

@@ -86,7 +86,10 @@ def test_batched_wrappers(kq4, orc, n):
     assert rel_err(dn, orc.matmul(wd, act, h, ffn, residual=res))[0] <= TOL
 
 
-def test_single_token_wrappers_use_m4f_chain(kq4, orc):
+def test_single_token_wrappers_within_tolerance_of_m4f_chain(kq4, orc):
+    """The single-token wrappers request the M4f chain (their NEON bodies call
+    q4x4_dot1_group16_gemv, vllm_safetensors.c:6182-6560); the GEMV takes from it only the f32
+    activation scale and sums in its own K split, so the bar is 1e-5, not bit identity."""
     lib = kq4.lib()
     rows, cols = 128, 1024
     w = synth.make_q4_weights(rows, cols, 40)

@@ -141,3 +141,19 @@ def test_rejects_bad_files(kq4_cpu, tmp_path):
             v.q4_matrix(4, make_vqf.CONFIG["num_hidden_layers"])
         with pytest.raises(kq4_cpu.KQ4Error, match="projection"):
             v.q4_matrix(9, 0)
+
+
+def test_layer_bound_does_not_wrap(kq4_cpu, tmp_path):
+    """A crafted arch (dim = ffn_dim = 2^30, 256 layers) makes a gate layer 9 * 2^56 bytes, so
+    layer 255 ends at 9 * 2^64: a product-based bound wraps to 0 and would hand out a wild
+    pointer. The loader bounds layers by division and refuses it."""
+    data = bytearray(open(SYNTH, "rb").read())
+    struct.pack_into("<I", data, 16, 1 << 30)                     # VQFArch.dim
+    struct.pack_into("<I", data, 20, 256)                         # n_layers
+    struct.pack_into("<I", data, 36, 1 << 30)                     # ffn_dim
+    p = tmp_path / "wrap.vqf"
+    p.write_bytes(bytes(data))
+    with kq4_cpu.Vqf(str(p)) as v:
+        for layer in (0, 255):
+            with pytest.raises(kq4_cpu.KQ4Error, match="too few"):
+                v.q4_matrix(kq4_cpu.PROJ_GATE, layer)
