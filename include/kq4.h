@@ -212,6 +212,17 @@ int kq4_quantize_dev(int8_t *xq, float *xd, float *xde, const float *x, int n_ba
 int kq4_matmul_dev(float *out, const float *x, const float *residual, const uint8_t *w,
                    int rows, int cols, int n_batch, int chain, void *stream);
 
+/* kq4_matmul_dev that allocates nothing, for callers that cannot call hipMalloc (code under HIP
+ * graph capture, serving loops and harnesses that forbid allocation). No counterpart in the
+ * reference. Same arguments, kernels and results as kq4_matmul_dev; the quantized activations go
+ * to a fixed per-device scratch array of KQ4_NOALLOC_SCRATCH_BYTES (held by each GPU the library
+ * runs on until the process ends) instead of the growable workspace. n_batch * cols * 33/32
+ * bytes (rounded up to 256-byte pieces) must fit in it, else KQ4_EINVAL. Every call on a GPU
+ * shares that GPU's scratch: calls that overlap on one GPU (other streams or threads) race. */
+#define KQ4_NOALLOC_SCRATCH_BYTES (32u << 20)
+int kq4_matmul_noalloc_dev(float *out, const float *x, const float *residual, const uint8_t *w,
+                           int rows, int cols, int n_batch, int chain, void *stream);
+
 /* kq4_matmul_silu on device buffers (gate, up 16-byte aligned): up to 4 tokens in one launch
  * (the GEMV forms the product while quantizing), else the quantizer forms it. */
 int kq4_matmul_silu_dev(float *out, const float *gate, const float *up, const float *residual,

@@ -63,9 +63,17 @@ struct DevState {
   std::vector<void *> retired;   // outgrown device-API workspaces, freed by kq4_shutdown
   Buf hx, hu, hres, hout, hw, hsel, hpr, hstage;   // staging for the host-pointer API
   std::unordered_map<uint64_t, WEntry> wcache;
+  uint8_t *scratch = nullptr;   // this device's address of kq4_scratch (set by kq4_init)
 };
 
 DevState g_dev[kMaxDev];
+
+// Scratch of kq4_matmul_noalloc_dev, the entry point that allocates nothing: a file-scope device
+// array, one copy per GPU at its own address, held until the process ends. Host code never
+// passes `kq4_scratch` itself to a kernel (on the host that name is a stand-in, not a device
+// address): kq4_init looks up each device's address with hipGetSymbolAddress and the entry point
+// carves its buffers from DevState::scratch.
+__device__ __align__(256) uint8_t kq4_scratch[KQ4_NOALLOC_SCRATCH_BYTES];
 std::mutex g_mu;   // guards lazy init / cache maps (the op itself is single-caller)
 
 inline size_t al256(size_t n) { return (n + 255) & ~(size_t)255; }
@@ -508,6 +516,12 @@ int kq4_init(int device) {
   std::lock_guard<std::mutex> lk(g_mu);
   DevState &ds = g_dev[device];
   ds.ncu = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
+  if (!ds.scratch) {   // once per device, with that device current
+    void *p = nullptr;
+    KQ4_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(kq4_scratch)));
+    if (!p) return fail(KQ4_EHIP, "device %d: no address for the no-allocation scratch", device);
+    ds.scratch = static_cast<uint8_t *>(p);
+  }
   ds.ready = true;
   return KQ4_OK;
 }
@@ -656,6 +670,26 @@ int kq4_matmul_dev(float *out, const float *x, const float *residual, const uint
   const float *res[1] = {residual};
   return matmul_impl(1, &out, res, &w, &rows, cols, x, nullptr, nullptr, n_batch, chain,
                      (hipStream_t)stream);
+}
+
+int kq4_matmul_noalloc_dev(float *out, const float *x, const float *residual, const uint8_t *w,
+                           int rows, int cols, int n_batch, int chain, void *stream) {
+  if (!x && n_batch) return fail(KQ4_EINVAL, "null x");
+  if (n_batch > 0 && cols > 0 && cols % 32 == 0 &&
+      qa_bytes(n_batch, cols) > (size_t)KQ4_NOALLOC_SCRATCH_BYTES)
+    return fail(KQ4_EINVAL, "matmul_noalloc: %d tokens x %d columns need %zu B of scratch; the "
+                "maximum is %u B", n_batch, cols, qa_bytes(n_batch, cols),
+                (unsigned)KQ4_NOALLOC_SCRATCH_BYTES);
+  DevState *ds = nullptr;
+  int rc = cur_dev(&ds);
+  if (rc) return rc;
+  Buf b;   // the device's copy of kq4_scratch, fixed: matmul_impl carves it and never grows it
+  b.p = ds->scratch;
+  b.cap = KQ4_NOALLOC_SCRATCH_BYTES;
+  const Ws ws{&b, nullptr};
+  const float *res[1] = {residual};
+  return matmul_impl(1, &out, res, &w, &rows, cols, x, nullptr, nullptr, n_batch, chain,
+                     (hipStream_t)stream, nullptr, 0, &ws);
 }
 
 int kq4_matmul_silu_dev(float *out, const float *gate, const float *up, const float *residual,

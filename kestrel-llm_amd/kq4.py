@@ -47,6 +47,7 @@ SIGNATURES = [
     ("kq4_weights_prepare_dev", _I, [_P, _P, _I, _I, _P]),
     ("kq4_quantize_dev", _I, [_P, _P, _P, _P, _I, _I, _I, _P]),
     ("kq4_matmul_dev", _I, [_P, _P, _P, _P, _I, _I, _I, _I, _P]),
+    ("kq4_matmul_noalloc_dev", _I, [_P, _P, _P, _P, _I, _I, _I, _I, _P]),
     ("kq4_matmul_multi_dev", _I, [_I, _P, _P, _P, _P, _I, _P, _I, _I, _P]),
     ("kq4_matmul_silu_dev", _I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _P]),
     ("kq4_silu_mul_dev", _I, [_P, _P, ctypes.c_long, _P]),
@@ -396,6 +397,18 @@ def matmul_dev(out, x, w, rows, cols, residual=None, chain=CHAIN_AUTO, stream=No
     _outs([out], [residual], [rows], n)
     check(lib().kq4_matmul_dev(_tp(out), _tp(x), _tp(residual), _tp(w), rows, cols, n, chain,
                                _stream_ptr(stream)), "kq4_matmul_dev")
+
+
+NOALLOC_SCRATCH_BYTES = 32 << 20
+
+
+def matmul_noalloc_dev(out, x, w, rows, cols, residual=None, chain=CHAIN_AUTO, stream=None):
+    """kq4_matmul_dev without any device allocation (fixed per-device scratch)."""
+    n = _act(x, cols)
+    _mat(w, rows, cols)
+    _outs([out], [residual], [rows], n)
+    check(lib().kq4_matmul_noalloc_dev(_tp(out), _tp(x), _tp(residual), _tp(w), rows, cols, n,
+                                       chain, _stream_ptr(stream)), "kq4_matmul_noalloc_dev")
 
 
 def matmul_silu_dev(out, gate, up, w, rows, cols, residual=None, chain=CHAIN_AUTO, stream=None):
