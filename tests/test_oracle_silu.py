@@ -162,3 +162,42 @@ def test_matmul_silu_composition(orc, n):
     got = orc.matmul_silu(w, g, u, rows, cols, residual=res)
     want = orc.matmul(w, orc.silu_mul(g, u).reshape(n, cols), rows, cols, residual=res)
     assert np.array_equal(got, want)
+
+
+def recip_estimate_midpoint(a):
+    """FRECPE's 9-bit estimate for the 8-bit mantissa bucket a (256..511) stated independently
+    of the pseudocode's integer steps: the reciprocal of the bucket's midpoint (a + 1/2)/256,
+    scaled to 9 bits and rounded half up, in exact rational arithmetic. (The pseudocode's
+    b = 2^19 DIV (2a+1), r = (b+1) DIV 2 is floor(v/2 + 1/2) of v = 2^19/(2a+1), the same
+    number.)"""
+    from fractions import Fraction
+    from math import floor
+    return floor(Fraction(1 << 17) / (Fraction(a) + Fraction(1, 2)) + Fraction(1, 2))
+
+
+def test_frecpe_every_bucket_matches_independent_statement(orc):
+    L = orc.lib()
+    rng = np.random.default_rng(8)
+    table = {a: recip_estimate_midpoint(a) for a in range(256, 512)}
+    assert all(256 <= r <= 511 for r in table.values())
+    assert table[256] == 511 and table[511] == 256          # 1.0 -> 0.998046875
+    for a, r in table.items():
+        for e in (1, 64, 127, 128, 200, 252):
+            low = int(rng.integers(0, 1 << 15))
+            x = np.uint32((e << 23) | ((a - 256) << 15) | low).view(F32)
+            want = np.uint32(((253 - e) << 23) | ((r - 256) << 15)).view(F32)
+            got = F32(L.kqo_frecpe(float(x)))
+            assert got.view(np.uint32) == want.view(np.uint32), (a, e)
+
+
+def test_frecpe_check_catches_planted_rounding_mistakes():
+    """The per-bucket check above separates the pseudocode's rounding from plausible
+    transcription slips: r = b DIV 2 (no +1) keeps FRECPE(1.0) = 0.998046875, so the documented
+    value alone would miss it, and a = 2*scaled (no +1) also changes buckets; both differ from
+    the statement above in many buckets."""
+    good = {a: recip_estimate_midpoint(a) for a in range(256, 512)}
+    no_round = {a: ((1 << 19) // (2 * a + 1)) // 2 for a in range(256, 512)}
+    no_half = {a: ((1 << 19) // (2 * a) + 1) // 2 for a in range(256, 512)}
+    assert no_round[256] == good[256] == 511
+    for bad in (no_round, no_half):
+        assert sum(bad[a] != good[a] for a in good) >= 32
