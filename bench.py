@@ -431,7 +431,36 @@ def cpu_baseline(m, budget_s=12.0):
 
 PROFILE_OPS = ("gemv_gate_up_2b", "gemv_gate_up_8b", "gemv_down_8b", "gemm_gate_8b",
                "gemm_down_8b", "moe_30b_a3b", "moe_layer_30b_a3b", "silu_down_8b",
-               "rmsnorm_qkv_8b", "q8_gate_8b", "q8_down_8b")
+               "rmsnorm_qkv_8b", "q8_gate_8b", "q8_down_8b", "gemv_8b_sweep")
+
+
+def profile_gemv_sweep(reps):
+    """The Qwen3-8B decode GEMVs as the extras time them - the fused gate/up pair and down, from
+    fp32 activations, at M = 1, 2, 4, 8 - each launched `reps` times over rotating weight copies
+    (> 640 MB, so the weights stream from HBM). In a kernel trace the GEMV's template arguments
+    name M, and the grid (gate/up 768 row sets, down 128) names the op."""
+    import torch
+
+    import kq4
+
+    kq4.init(0)
+    st = torch.cuda.current_stream()
+    cfg = synth.QWEN3_8B
+    h, f = cfg["hidden"], cfg["ffn"]
+    G = _copies(torch, synth.make_q4_weights(f, h, 11, **synth.SCALE_8B), f, h)
+    U = [g.clone() for g in G]
+    D = _copies(torch, synth.make_q4_weights(h, f, 13, **synth.SCALE_8B), h, f)
+    for m in (1, 2, 4, 8):
+        x = torch.from_numpy(synth.make_activations(m, h, 20 + m)).cuda()
+        xf = torch.from_numpy(synth.make_activations(m, f, 30 + m)).cuda()
+        og, ou = torch.empty((m, f), device="cuda"), torch.empty((m, f), device="cuda")
+        od = torch.empty((m, h), device="cuda")
+        for r in range(reps):
+            kq4.matmul_multi_dev([og, ou], x, [G[r % len(G)], U[r % len(G)]], [f, f], h, stream=st)
+        for r in range(reps):
+            kq4.matmul_dev(od, xf, D[r % len(D)], h, f, stream=st)
+        torch.cuda.synchronize()
+    return dict(op="gemv_8b_sweep", reps=reps)
 
 
 def profile_op(op, m, reps):
@@ -528,6 +557,9 @@ def main():
         sys.exit(2)
     if args.calibrate_copy:
         print(json.dumps(copy_calibration()))
+        return
+    if args.profile_op == "gemv_8b_sweep":
+        print(json.dumps(profile_gemv_sweep(args.reps)))
         return
     if args.profile_op:
         print(json.dumps(profile_op(args.profile_op, args.m, args.reps)))

@@ -99,6 +99,15 @@ const char *kq4_last_error(void);
 /* Library version string. */
 const char *kq4_version(void);
 
+/* Sets one of the launch planner's options, for measurement and tests (no counterpart in the
+ * reference): gemv_kind (0 v_dot4 / 1 MFMA dots), gemv_mfma_from, gemv_hs (0 whole 32-row sets,
+ * 1 halves, 2 quarters per workgroup), gemv_rps (row sets per workgroup, 1..3), gemv_ksl (K
+ * slices), gemv_waves, gemv_wpcu, gemv_maxw, gemv_fq (0 / 1: activations quantized by a separate
+ * launch / in the GEMV), gemv_fq_work, gemv_silu_fq_work. value < 0 restores the default (for
+ * most, the planner's own choice). The initial values come from the environment variables KQ4_
+ * + the upper-case name. Takes effect for launches planned after it returns. */
+int kq4_set_option(const char *name, int value);
+
 /* ---- host-pointer drop-in API (synchronous; 1 = done, 0 = caller falls back) -------------- */
 
 /* Uploads 4x4 q4 weights once and keeps them under `wkey` (layer<<32 | proj), as the NPU
@@ -217,7 +226,8 @@ int kq4_matmul_dev(float *out, const float *x, const float *residual, const uint
  * reference. Same arguments, kernels and results as kq4_matmul_dev; the quantized activations go
  * to a fixed per-device scratch array of KQ4_NOALLOC_SCRATCH_BYTES (held by each GPU the library
  * runs on until the process ends) instead of the growable workspace. n_batch * cols * 33/32
- * bytes (rounded up to 256-byte pieces) must fit in it, else KQ4_EINVAL. Every call on a GPU
+ * bytes (rounded up to 256-byte pieces) and 64 KiB of counters must fit in it (and 4 MiB of
+ * split-K partial sums for n_batch <= 8), else KQ4_EINVAL. Every call on a GPU
  * shares that GPU's scratch: calls that overlap on one GPU (other streams or threads) race. */
 #define KQ4_NOALLOC_SCRATCH_BYTES (32u << 20)
 int kq4_matmul_noalloc_dev(float *out, const float *x, const float *residual, const uint8_t *w,

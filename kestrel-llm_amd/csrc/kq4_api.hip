@@ -1,6 +1,7 @@
 // kq4_api.hip - C ABI of libkq4.so (declared in include/kq4.h): argument checks, per-device
 // workspaces, the weight cache of the host-pointer drop-in API, and kernel dispatch.
 #include "../../include/kq4.h"
+#include "kq4_common.h"
 #include "kq4_internal.h"
 
 #include <stdarg.h>
@@ -8,6 +9,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <atomic>
 #include <mutex>
 #include <unordered_map>
 #include <vector>
@@ -90,6 +92,11 @@ int cur_dev(DevState **out) {
   return KQ4_OK;
 }
 
+// Every workspace starts with kCntBytes of counters (the split-K GEMV's per-group arrival
+// counters), zero when it is allocated and zero again after every launch that uses them; the
+// carves of a call start after it.
+const size_t kCntBytes = 64 * 1024;
+
 size_t grow_size(size_t bytes) { return al256(bytes > 4096 ? bytes + bytes / 4 : 4096); }
 
 // Staging buffers of the host-pointer API, whose calls are synchronous and cannot be captured
@@ -123,8 +130,9 @@ struct Ws {
 // captured before the growth go on using. Growth needs hipMalloc, which stream capture does not
 // allow, so a call on a capturing stream that would grow the workspace fails with KQ4_EINVAL
 // before it launches anything (kq4_workspace_reserve sizes it beforehand).
-int ensure_ws(const Ws &ws, size_t bytes, hipStream_t s) {
+int ensure_ws(const Ws &ws, size_t payload, hipStream_t s) {
   Buf &b = *ws.b;
+  const size_t bytes = kCntBytes + payload;
   if (b.cap >= bytes) return KQ4_OK;
   if (!ws.ds)
     return fail(KQ4_EINVAL, "the call needs %zu B of workspace; its fixed buffer holds %zu B",
@@ -137,15 +145,19 @@ int ensure_ws(const Ws &ws, size_t bytes, hipStream_t s) {
   const size_t n = grow_size(bytes);
   void *p = nullptr;
   if (hipMalloc(&p, n) != hipSuccess) return fail(KQ4_ENOMEM, "hipMalloc(%zu) failed", n);
+  if (hipMemsetAsync(p, 0, kCntBytes, s) != hipSuccess) {   // the counters start at zero
+    (void)hipFree(p);
+    return fail(KQ4_EHIP, "clearing a new workspace failed");
+  }
   if (b.p) ws.ds->retired.push_back(b.p);
   b.p = p;
   b.cap = n;
   return KQ4_OK;
 }
 
-struct Carve {   // bump allocator over a workspace
+struct Carve {   // bump allocator over a workspace, above its counter area
   char *base;
-  size_t off = 0;
+  size_t off = kCntBytes;
   template <class T>
   T *take(size_t count) {
     T *p = reinterpret_cast<T *>(base + off);
@@ -167,6 +179,35 @@ int env_int(const char *name, int dflt) {
   return e ? atoi(e) : dflt;
 }
 
+// Tuning options (measurement and tests): initial values from the environment variable of each
+// (KQ4_ + the name in upper case), changed at run time by kq4_set_option. -1 = the planner's
+// choice where a planner chooses.
+enum OptId {
+  kGemvKind, kGemvMfmaFrom, kGemvHs, kGemvRps, kGemvKsl, kGemvWaves, kGemvWpcu, kGemvMaxw,
+  kGemvFq, kGemvFqWork, kGemvSiluFqWork, kOptCount
+};
+struct OptDef {
+  const char *name, *env;
+  int dflt;
+};
+const OptDef kOpts[kOptCount] = {
+    {"gemv_kind", "KQ4_GEMV_KIND", -1},          {"gemv_mfma_from", "KQ4_GEMV_MFMA_FROM", 2},
+    {"gemv_hs", "KQ4_GEMV_HS", -1},              {"gemv_rps", "KQ4_GEMV_RPS", -1},
+    {"gemv_ksl", "KQ4_GEMV_KSL", -1},            {"gemv_waves", "KQ4_GEMV_WAVES", -1},
+    {"gemv_wpcu", "KQ4_GEMV_WPCU", 32},          {"gemv_maxw", "KQ4_GEMV_MAXW", 16},
+    {"gemv_fq", "KQ4_GEMV_FQ", -1},              {"gemv_fq_work", "KQ4_GEMV_FQ_WORK", 45000},
+    {"gemv_silu_fq_work", "KQ4_GEMV_SILU_FQ_WORK", 15000},
+};
+std::atomic<int> g_opt[kOptCount];
+std::once_flag g_opt_once;
+
+int opt(OptId i) {
+  std::call_once(g_opt_once, [] {
+    for (int k = 0; k < kOptCount; ++k) g_opt[k] = env_int(kOpts[k].env, kOpts[k].dflt);
+  });
+  return g_opt[i].load(std::memory_order_relaxed);
+}
+
 int asm_tokens_for(int chain, int n) {
   if (chain == KQ4_CHAIN_ASM) return n;
   if (chain == KQ4_CHAIN_AUTO) return n > 3 ? (n & ~3) : 0;
@@ -175,57 +216,84 @@ int asm_tokens_for(int chain, int n) {
 
 // Integer-dot kind of the GEMV: per-lane v_dot4 for one token, v_mfma from two tokens on (the
 // dot4 work grows with M, the MFMA's does not; at one token both measure the same).
-// KQ4_GEMV_KIND=0/1 forces one (for measurement).
+// Option gemv_kind = 0/1 forces one (for measurement).
 int gemv_kind(int n) {
-  static const int env = env_int("KQ4_GEMV_KIND", -1);
-  static const int mfma_from = env_int("KQ4_GEMV_MFMA_FROM", 2);
-  if (env == 0 || env == 1) return env;
-  return n >= mfma_from ? 1 : 0;
+  const int force = opt(kGemvKind);
+  if (force == 1 || (force == 0 && n <= KQ4_GEMV_DOT4_MAX_M)) return force;
+  return n >= opt(kGemvMfmaFrom) || n > KQ4_GEMV_DOT4_MAX_M ? 1 : 0;
 }
 
-// GEMV launch shape. Workgroups: one per 32-row set; per 16-row half set when the launch has
-// fewer than two sets per CU (so that every CU streams, with a second workgroup to overlap); per
-// 8-row quarter set when even that would be at most one workgroup per CU. Measured on MI355X
-// (M = 1 .. 8): quarter sets make the Qwen3-VL-2B down (64 sets) 0.2-0.45 us faster and O up to
-// 0.2 us, but the 128-set shapes (Qwen3-8B down and O, 2B QKV) 0.1-0.7 us slower than halves.
-// Waves per workgroup (splitting K in 16-block stages): about KQ4_GEMV_WPCU (32) per CU over
-// the launch, at most one per stage and 16 per workgroup, balanced so that no wave has more
-// stages than another by more than one. (Issuing a wave's second stage before computing its first
-// was measured slower at the Qwen3-8B down shape, 10.2 against 9.0 us.)
-// KQ4_GEMV_HS / KQ4_GEMV_WAVES / KQ4_GEMV_MAXW override (for measurement).
-void plan_gemv(int sets, int nb, int ncu, int *half_out, int *nw_out) {
-  static const int force_hs = env_int("KQ4_GEMV_HS", -1);
-  static const int force_w = env_int("KQ4_GEMV_WAVES", 0);
-  static const int per_cu = env_int("KQ4_GEMV_WPCU", 32);
-  const int hs = force_hs >= 0 && force_hs <= 2 ? force_hs
-                 : 4 * sets <= ncu                ? 2
-                 : sets < 2 * ncu                 ? 1
-                                                  : 0;
-  const int wgs = sets << hs;
-  const int nst = (nb + 15) / 16;
+// Largest partial-sum buffer a split-K GEMV takes (else it runs unsplit).
+const size_t kPartMax = 4u << 20;
+
+size_t gemv_part_bound(int, int) { return kPartMax; }
+
+// GEMV launch shape (kq4_gemv_impl.h). A group of output rows is R whole 32-row sets (rps), or
+// half (hs = 1) or a quarter (hs = 2) of one set; each group is split into ksl K slices, one
+// workgroup each, of nw waves that take the slice's 16-block stages in turn. Chosen from a
+// sweep of every combination over the Qwen3-8B and Qwen3-VL-2B decode shapes at M = 1, 2, 4, 8
+// on MI355X (graph replay, weights streamed from HBM):
+//   * hs: quarter sets when the launch has at most one set per 4 CUs, half sets below two sets
+//     per CU, whole sets beyond - and whole sets from two tokens on when K has at least 8
+//     stages and there are at least 3 sets per 4 CUs (Qwen3-8B QKV, 192 sets: 6.97 against
+//     7.85 us at M = 4);
+//   * rps: 3 sets per workgroup from 4 tokens on when whole sets fill the chip, with the
+//     activations quantized in the kernel, once for the 3 sets (Qwen3-8B gate/up pair at M = 4:
+//     14.7 against 16.0 us); 1 otherwise (at fewer tokens the lower wave count costs more);
+//   * ksl: 1. Splitting K across workgroups (each slice's sums combined by the last slice to
+//     arrive, with device-scope fences) measured 2-4x slower at every shape; it stays available
+//     as an option;
+//   * waves: about gemv_wpcu (32) per CU over the launch, at most one per stage and 16 per
+//     workgroup (8 with rps > 1), balanced so that no wave has more stages than another by more
+//     than one.
+// Options gemv_hs / _rps / _ksl / _waves / _maxw / _wpcu override it (measurement, tests).
+struct GemvPlan {
+  int hs, rps, ksl, spk, nw, groups;
+};
+
+GemvPlan plan_gemv(int n_mats, const int *rows, int nst, int ncu, int n) {
+  const int force_hs = opt(kGemvHs), force_r = opt(kGemvRps), force_k = opt(kGemvKsl);
+  const int force_w = opt(kGemvWaves), per_cu = opt(kGemvWpcu);
+  const int max_w = opt(kGemvMaxw) >= 1 && opt(kGemvMaxw) <= 16 ? opt(kGemvMaxw) : 16;
+  int sets = 0;
+  for (int i = 0; i < n_mats; ++i) sets += (rows[i] + 31) / 32;
+  GemvPlan p;
+  p.hs = force_hs >= 0 && force_hs <= 2                  ? force_hs
+         : 4 * sets <= ncu                                   ? 2
+         : sets >= 2 * ncu || (n >= 2 && nst >= 8 && 4 * sets >= 3 * ncu) ? 0
+                                                             : 1;
+  p.rps = force_r >= 1 && force_r <= KQ4_GEMV_MAX_RPS ? force_r
+          : n >= 4 && sets >= 2 * ncu                 ? 3
+                                                      : 1;
+  if (p.hs) p.rps = 1;
+  p.ksl = force_k >= 1 ? (force_k < nst ? force_k : nst) : 1;
+  p.spk = (nst + p.ksl - 1) / p.ksl;
+  p.ksl = (nst + p.spk - 1) / p.spk;   // no empty slice
+  p.groups = 0;
+  for (int i = 0; i < n_mats; ++i) p.groups += ((rows[i] + 31) / 32 + p.rps - 1) / p.rps << p.hs;
+  const int wgs = p.groups * p.ksl;
   int want = force_w > 0 ? force_w : (per_cu * ncu + wgs - 1) / wgs;
-  static const int max_w = env_int("KQ4_GEMV_MAXW", 16);
-  const int cap = nst < max_w ? nst : max_w;
+  const int mw = p.rps > 1 && max_w > KQ4_GEMV_RPS_MAX_WAVES ? KQ4_GEMV_RPS_MAX_WAVES : max_w;
+  const int cap = p.spk < mw ? p.spk : mw;
   want = want < 1 ? 1 : (want > cap ? cap : want);
-  const int spw = (nst + want - 1) / want;   // stages per wave
-  *half_out = hs;
-  *nw_out = (nst + spw - 1) / spw;
+  const int spw = (p.spk + want - 1) / want;   // stages per wave
+  p.nw = (p.spk + spw - 1) / spw;
+  return p;
 }
 
 // Whether the GEMV quantizes its fp32 activations itself (one launch per op) or reads them from
-// a separate quantize launch (about 2 us more per op in a graph). Every workgroup quantizes the
-// whole activation for itself, so a CU spends VALU time on cols * n elements per workgroup it
-// runs: work = cols * n * ceil(workgroups / CUs). Measured on MI355X (Qwen3-8B and Qwen3-VL-2B
-// decode shapes, M = 1..4) the in-kernel path is faster up to about 45K such elements, and with
-// the SiLU product (about 30 more instructions per element) up to about 15K (the 8B down
-// projection at one token, 12288, still gains 1 us; at two tokens it loses 2 us).
-// KQ4_GEMV_FQ=0 turns it off; KQ4_GEMV_FQ_WORK and KQ4_GEMV_SILU_FQ_WORK set the two limits.
-bool gemv_fq(long work, int n, bool silu) {
-  static const int env = env_int("KQ4_GEMV_FQ", -1);
-  static const long max_work = env_int("KQ4_GEMV_FQ_WORK", 45000);
-  static const long max_silu = env_int("KQ4_GEMV_SILU_FQ_WORK", 15000);
-  return env != 0 && n <= (silu ? KQ4_GEMV_SILU_FQ_MAX_M : KQ4_GEMV_FQ_MAX_M) &&
-         work <= (silu ? max_silu : max_work);
+// a separate quantize launch (about 2 us more per op in a graph). Every workgroup quantizes its
+// K slice of the activation for itself, so a CU spends VALU time on that many elements per
+// workgroup it runs: work = n * (K slice) * ceil(workgroups / CUs). From the sweep above, the
+// in-kernel path is faster up to about 45K such elements at 1-4 tokens and 20K at 5-8 (two
+// quantization passes), always with several sets per workgroup, and with the SiLU product
+// (about 30 more instructions per element) up to about 15K. Option gemv_fq = 0 / 1 forces it
+// off / on; gemv_fq_work and gemv_silu_fq_work set the 1-4-token limits.
+bool gemv_fq(long work, int n, int rps, bool silu) {
+  const int force = opt(kGemvFq);
+  if (force == 0 || force == 1) return force;
+  if (silu) return work <= opt(kGemvSiluFqWork);
+  return rps > 1 || work <= (n <= 4 ? opt(kGemvFqWork) : opt(kGemvFqWork) * 4 / 9);
 }
 
 // GEMV over n_mats matrices for n tokens (n <= 8): from fp32 x (quantized in the kernel or by a
@@ -235,21 +303,41 @@ int run_gemv(DevState *ds, const Ws &wsp, int n_mats, float *const *out, const f
              const int8_t *xq, const float *xd, int n, int asm_tokens, hipStream_t s,
              int wf = 0) {
   const int nb = cols / 32;
+  const int cb = wf ? KQ8_STREAM_CB : KQ4_STREAM_CB;   // q8 stages hold 8 blocks
+  const int nst = (nb + cb - 1) / cb;
   int rc;
   KQ4GemvArgs a;
   memset(&a, 0, sizeof(a));
-  int sets = 0;
-  for (int i = 0; i < n_mats; ++i) sets += (rows[i] + 31) / 32;
-  int hs = 0, nw = 1;
-  plan_gemv(sets, wf ? 2 * nb : nb, ds->ncu, &hs, &nw);   // q8 stages hold 8 blocks
+  GemvPlan pl = plan_gemv(n_mats, rows, nst, ds->ncu, n);
+  const int kind = wf ? 1 : gemv_kind(n);
+  // the split-K partial sums and the quantized activations (when quantized apart) in the
+  // workspace; the per-group counters in its fixed counter area
+  const size_t nout = (size_t)pl.rps * n * (32 >> pl.hs);
+  size_t pbytes = al256((size_t)pl.groups * pl.ksl * nout * sizeof(float));
+  if (pl.ksl > 1 && (pl.groups > (int)(kCntBytes / sizeof(unsigned)) || pbytes > kPartMax)) {
+    pl.ksl = 1;   // too many groups or partial sums for the split: whole K per workgroup
+    pl.spk = nst;
+  }
+  if (pl.ksl == 1) pbytes = 0;
+  const int wgs = pl.groups * pl.ksl;
+  bool fq = false;
   if (x) {
-    const long per_cu = ((long)(sets << hs) + ds->ncu - 1) / ds->ncu;
-    if (gemv_fq(per_cu * cols * n, n, xu != nullptr)) {
+    const long per_cu = ((long)wgs + ds->ncu - 1) / ds->ncu;
+    fq = gemv_fq(per_cu * n * ((long)pl.spk * cb * 32 < cols ? (long)pl.spk * cb * 32 : cols), n,
+                 pl.rps, xu != nullptr);
+  }
+  const size_t qbytes = x && !fq ? qa_bytes(n, cols) : 0;
+  if (pbytes + qbytes && (rc = ensure_ws(wsp, pbytes + qbytes, s))) return rc;
+  Carve cv{static_cast<char *>(wsp.b->p)};
+  if (pl.ksl > 1) {
+    a.part = cv.take<float>((size_t)pl.groups * pl.ksl * nout);
+    a.cnt = reinterpret_cast<unsigned *>(wsp.b->p);
+  }
+  if (x) {
+    if (fq) {
       a.xf = x;
       a.xu = xu;
     } else {
-      if ((rc = ensure_ws(wsp, qa_bytes(n, cols), s))) return rc;
-      Carve cv{static_cast<char *>(wsp.b->p)};
       int8_t *q = cv.take<int8_t>((size_t)n * cols);
       float *d = cv.take<float>((size_t)n * nb);
       KQ4_HIP((hipError_t)kq4_launch_quantize(x, q, d, nullptr, n, cols, 0, s, 0, xu));
@@ -264,18 +352,20 @@ int run_gemv(DevState *ds, const Ws &wsp, int n_mats, float *const *out, const f
   a.cols = cols;
   a.nb = nb;
   a.wf = wf;
-  const int kind = wf ? 1 : gemv_kind(n);
-  int wg = 0;
+  a.nw = pl.nw;
+  a.ksl = pl.ksl;
+  a.spk = pl.spk;
+  int g = 0;
   for (int i = 0; i < n_mats; ++i) {
     KQ4GemvMat &m = a.mat[i];
     m.w = w[i];
     m.out = out[i];
     m.res = res ? res[i] : nullptr;
     m.rows = rows[i];
-    m.wg_begin = wg;
-    wg += ((rows[i] + 31) / 32) << hs;
+    m.wg_begin = g;
+    g += ((rows[i] + 31) / 32 + pl.rps - 1) / pl.rps << pl.hs;
   }
-  KQ4_HIP((hipError_t)kq4_launch_gemv(a, n, kind, hs, nw, wg, s));
+  KQ4_HIP((hipError_t)kq4_launch_gemv(a, n, kind, pl.hs, pl.rps, wgs, s));
   return KQ4_OK;
 }
 
@@ -410,7 +500,7 @@ int moe_impl(float *Y, const float *X, const int *sel, const float *pr, int T, i
   if (rc) return rc;
   const size_t np = (size_t)T * tk;
   if ((rc = ensure_ws(Ws{&ds->ws, ds}, off + moe_stage_bytes(T, tk, ne, d, ef), s))) return rc;
-  Carve cv{static_cast<char *>(ds->ws.p), off};
+  Carve cv{static_cast<char *>(ds->ws.p), kCntBytes + off};
   KQ4MoeWs ws;
   ws.ex_off = cv.take<int>(ne + 1);
   ws.ex_pair = cv.take<int>(np);
@@ -550,19 +640,33 @@ void kq4_shutdown(void) {
 
 size_t kq4_matmul_workspace_bytes(int n_batch, int cols) {
   if (n_batch < 0 || cols <= 0 || cols % 32) return 0;
-  return qa_bytes(n_batch, cols) + al256((size_t)cols * sizeof(float));
+  // quantized activations, the one-token RMSNorm row, the split-K GEMV's partial sums (at most
+  // one float per output row, token and K stage)
+  return kCntBytes + qa_bytes(n_batch, cols) + al256((size_t)cols * sizeof(float)) +
+         (n_batch <= KQ4_GEMV_MAX_M ? gemv_part_bound(n_batch, cols) : 0);
 }
 
 size_t kq4_moe_workspace_bytes(int T, int tk, int ne, int d, int ef) {
   if (T < 0 || tk < 1 || tk > 32 || ne < 1 || !kq4_moe_shape_ok(d, ef)) return 0;
-  return moe_route_bytes(T, tk, ne) + moe_stage_bytes(T, tk, ne, d, ef);
+  return kCntBytes + moe_route_bytes(T, tk, ne) + moe_stage_bytes(T, tk, ne, d, ef);
 }
 
 int kq4_workspace_reserve(size_t bytes) {
   DevState *ds = nullptr;
   int rc = cur_dev(&ds);
   if (rc) return rc;
-  return ensure_ws(Ws{&ds->ws, ds}, bytes, nullptr);
+  return ensure_ws(Ws{&ds->ws, ds}, bytes > kCntBytes ? bytes - kCntBytes : 0, nullptr);
+}
+
+int kq4_set_option(const char *name, int value) {
+  if (!name) return fail(KQ4_EINVAL, "set_option: null name");
+  (void)opt(kGemvKind);   // the environment's values first
+  for (int k = 0; k < kOptCount; ++k)
+    if (strcmp(name, kOpts[k].name) == 0) {
+      g_opt[k] = value < 0 ? kOpts[k].dflt : value;
+      return KQ4_OK;
+    }
+  return fail(KQ4_EINVAL, "set_option: unknown option %s", name);
 }
 
 int kq4_quantize_dev(int8_t *xq, float *xd, float *xde, const float *x, int n_batch, int cols,
@@ -675,11 +779,13 @@ int kq4_matmul_dev(float *out, const float *x, const float *residual, const uint
 int kq4_matmul_noalloc_dev(float *out, const float *x, const float *residual, const uint8_t *w,
                            int rows, int cols, int n_batch, int chain, void *stream) {
   if (!x && n_batch) return fail(KQ4_EINVAL, "null x");
-  if (n_batch > 0 && cols > 0 && cols % 32 == 0 &&
-      qa_bytes(n_batch, cols) > (size_t)KQ4_NOALLOC_SCRATCH_BYTES)
+  const size_t need = n_batch > 0 && cols > 0 && cols % 32 == 0
+                         ? kCntBytes + qa_bytes(n_batch, cols) +
+                               (n_batch <= KQ4_GEMV_MAX_M ? kPartMax : 0)
+                         : 0;
+  if (need > (size_t)KQ4_NOALLOC_SCRATCH_BYTES)
     return fail(KQ4_EINVAL, "matmul_noalloc: %d tokens x %d columns need %zu B of scratch; the "
-                "maximum is %u B", n_batch, cols, qa_bytes(n_batch, cols),
-                (unsigned)KQ4_NOALLOC_SCRATCH_BYTES);
+                "maximum is %u B", n_batch, cols, need, (unsigned)KQ4_NOALLOC_SCRATCH_BYTES);
   DevState *ds = nullptr;
   int rc = cur_dev(&ds);
   if (rc) return rc;
@@ -748,7 +854,7 @@ int kq4_rmsnorm_matmul_multi_dev(int n_mats, float *const *out, const float *con
       if ((rc = ensure_ws(Ws{&ds->ws, ds}, qbytes + al256((size_t)cols * sizeof(float)),
                           (hipStream_t)stream)))
         return rc;
-      nx = reinterpret_cast<float *>(static_cast<char *>(ds->ws.p) + qbytes);
+      nx = reinterpret_cast<float *>(static_cast<char *>(ds->ws.p) + kCntBytes + qbytes);
     }
     KQ4_HIP((hipError_t)kq4_launch_rms_norm(x, norm_w, nx, nullptr, nullptr, 1, cols, eps,
                                             order == KQ4_RMS_SERIAL, (hipStream_t)stream));

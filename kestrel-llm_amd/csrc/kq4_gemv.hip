@@ -1,581 +1,31 @@
-// kq4_gemv.hip - decode GEMV (1..8 tokens) over q4 weights in the kq4 stream layout x int8
-// activations, gfx950; plus the repack from the VQF 4x4 layout into that stream layout.
-//
-// Computes out[m][n] = [res +] sum_b S[m,n,b] * fl(wd[n,b] * xs[m,b]), the op of
-// q4x4_gemm_batched / dyn_matvec_q4_q8 (kestrel-llm src/model/vllm_safetensors.c:4593-4631,
-// 6147-6174): S is the exact integer dot of row n's 32 nibble weights (n-8) with the token's
-// int8 block, xs the token's block scale (f16-rounded for ASM-chain tokens, as the reference's
-// asm path multiplies by the f16 scale it repacks, :4104-4105). Every per-block term is the
-// reference's; the blocks of one output are summed serially within each wave's share of K and
-// the shares are then added in wave order, so outputs agree with the reference's single serial
-// chain to a few ulp of the row magnitude.
-//
-// The weights are in the stream layout (kq4_common.h): per (32-row set, 16-block stage) one
-// 9216-B chunk in which lane l of a wave finds, at 16-B units l, l+64, .. (1 KB apart), the
-// nibbles of its row (l%32) and K-half (l/32) for the stage's 16 blocks, and at 8192+16*l the
-// f16 scales. So a stage is 9 + 1 full-width coalesced loads per lane (the second scale load
-// reads the other half's 8 scales of the same row) and every lane then holds its own operands:
-// no weight bytes pass through LDS.
-//
-// Work decomposition (the weight stream is the whole cost):
-//   * a workgroup = one 32-row set (or, when a launch has fewer sets than the chip has CUs, half
-//     of one: 16 rows, so twice the workgroups) over the whole K, W <= 16 waves; wave w takes the
-//     stages w, w + W, .., each issued as (activations, weights).
-//   * each wave stages its own activations (int8 codes + per-block scales) in a small LDS slab,
-//     quantizing them from fp32 itself (FQ) or copying a pre-quantized buffer, so the stage loop
-//     has no workgroup barrier.
-//   * the integer dot, two kinds:
-//       DOT4: lane (row, half) dots its 16 weights of each block with v_dot4_i32_i8 against the
-//             token's 16 codes (an LDS broadcast read) and keeps one fp32 chain per token and
-//             half (the C-tile kernel's lo/hi split, :4180-4216); each wave adds its halves
-//             before the waves' sums are added. Cost grows with M.
-//       MFMA: per block one v_mfma_i32_32x32x32_i8 with A = the tokens' codes (32 rows, M <= 8
-//             used) and B = the lanes' weight operands as they are; the result 16*S is at lane
-//             (row = lane%32, token = 4*(lane/32) + v). Cost independent of M.
-//   * at the end the partials of an output are added in a fixed order, each wave's lanes by lane
-//     swaps, then the waves' sums through LDS: deterministic, one launch, no cross-workgroup
-//     communication.
-#include "kq4_common.h"
-#include "kq4_internal.h"
+// kq4_gemv.hip - the decode GEMV's dispatch over its per-token-count instantiations
+// (kq4_gemv_m<M>.hip, kernel in kq4_gemv_impl.h), the repack from the VQF 4x4 layout into the
+// stream layout the kernels read, and the verification kernel of the exact block sums.
+#include "kq4_gemv_impl.h"
 
-#define KQ4_GV_CB KQ4_STREAM_CB       // blocks per stage
-#define KQ4_GV_CHUNK KQ4_STREAM_CHUNK // bytes per (32-row set, stage)
-#define KQ4_GV_QTS 672                // LDS bytes per token row of a stage's int8 codes
-#define KQ4_GV_XS (KQ4_GV_CB * 8 * 4) // LDS bytes of a stage's scales [16 blocks][8 tokens]
-
-// Weight formats: 0 = q4 (kq4 stream layout); 1 = q8 (q8 stream layout) with the fused VDOT
-// chain acc = fma(S, fl(wd*xs), acc); 2 = q8 with the unfused GEMM chain
-// acc = fl(acc + fl(fl(wd*xs) * S)) (xs f16-rounded through asm_tokens).
-template <int WF>
-struct KQ4Wf {
-  static constexpr int CB = WF ? KQ8_STREAM_CB : KQ4_STREAM_CB;          // blocks per stage
-  static constexpr int CHUNK = WF ? KQ8_STREAM_CHUNK : KQ4_STREAM_CHUNK;
-  static constexpr int BPU = WF ? 1 : 2;                                  // blocks per 16-B unit
-  static constexpr float XS = WF ? 1.0f : 0.0625f;  // q4 enters the MFMA as 16*(n-8): undo it
-};
-
-typedef int kq4_v4i __attribute__((ext_vector_type(4)));
-typedef int kq4_v16i __attribute__((ext_vector_type(16)));
-
-// LDS bytes of one wave's slab: [activation codes][scales]; it also holds the wave's partial
-// sums at the end (at most 8 tokens x 32 floats).
 template <int M>
-constexpr int kq4_gv_slab() {
-  return M * KQ4_GV_QTS + KQ4_GV_XS;
-}
-
-// Byte offset of block blk's 32 codes in a token row: block pairs at an 80-B pitch (16-B pad),
-// which spreads the two halves' 16-B reads over the banks.
-KQ4_DEV int kq4_gv_qpos(int blk) { return (blk >> 1) * 80 + (blk & 1) * 32; }
-
-KQ4_DEV kq4_v16i kq4_gv_mfma(kq4_v4i a, kq4_v4i b) {
-  const kq4_v16i z = {0};
-  return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, z, 0, 0, 0);
-}
-
-// ---- weights of one stage -------------------------------------------------------------------
-// A workgroup takes NR = 32 >> HS rows of a set (rows NR*hs .. +NR-1): HS = 0 the full set, 1 a
-// half, 2 a quarter. Lane (r, p, h) = (lane % NR, (lane / NR) % NP, lane / 32) with NP = 1 << HS
-// parities holds row NR*hs + r's half h of the units i = NP*u + p (u = 0 .. NU-1, NU = 8 >> HS
-// unit loads; a q4 unit is 2 blocks, a q8 unit 1), so one load instruction covers NP units at
-// 16*NR-byte runs. In every mode the row's scales (2 loads for q4, 1 for q8; the lanes of one
-// row share them).
-
-template <int HS>
-struct KQ4GvStage {
-  static constexpr int NU = 8 >> HS;      // 16-B nibble loads per lane
-  uint32_t n[4 * NU];                     // lane block jb (0 .. 2*NU-1): n[2jb], n[2jb+1]
-  uint32_t sc[8];                         // stage block b: f16 at sc[b/2] >> 16*(b%2)
-};
-
-// Scales first: the loads complete in issue order, so the first block then waits only for the
-// scales and its own unit, and each later block for one more unit.
-// q8 (WF > 0): the same unit loads, one block per unit, and the row's 8 scales in one load.
-template <int HS, int WF>
-KQ4_DEV void kq4_gv_load(KQ4GvStage<HS> &st, const uint8_t *__restrict__ chunk, int rr, int h,
-                         int p) {
-  // the weights are read once per launch: non-temporal loads
-  const uint4 *sc = reinterpret_cast<const uint4 *>(chunk + 8192) + rr;
-  const uint4 a = kq4_ld_nt(sc);
-  st.sc[0] = a.x; st.sc[1] = a.y; st.sc[2] = a.z; st.sc[3] = a.w;
-  if (WF == 0) {
-    const uint4 b = kq4_ld_nt(sc + 32);
-    st.sc[4] = b.x; st.sc[5] = b.y; st.sc[6] = b.z; st.sc[7] = b.w;
-  }
-  const uint4 *src = reinterpret_cast<const uint4 *>(chunk) + rr + 32 * h;
-#pragma unroll
-  for (int u = 0; u < KQ4GvStage<HS>::NU; ++u) {
-    const int i = (u << HS) + p;
-    const uint4 v = kq4_ld_nt(src + 64 * i);
-    st.n[4 * u] = v.x; st.n[4 * u + 1] = v.y; st.n[4 * u + 2] = v.z; st.n[4 * u + 3] = v.w;
-  }
-}
-
-// Stage block of lane block jb (p = the lane's unit parity).
-template <int HS, int WF>
-KQ4_DEV int kq4_gv_blk(int jb, int p) {
-  if (WF) return (jb << HS) + p;
-  return 2 * (((jb >> 1) << HS) + p) + (jb & 1);
-}
-
-// a if p == 0, b if p == 1 (p in {0, 1}), by masks: a select between two elements of one register
-// array would be folded into a lane-dependent index, which puts the array in scratch memory.
-KQ4_DEV uint32_t kq4_gv_pick(uint32_t a, uint32_t b, int p) {
-  const uint32_t m = 0u - (uint32_t)p;
-  return (a & ~m) | (b & m);
-}
-
-// v[p] of the NP = 1 << HS registers v[0 .. NP-1] (p < NP), by masks.
-template <int HS>
-KQ4_DEV uint32_t kq4_gv_pickn(const uint32_t *v, int p) {
-  if (HS == 0) return v[0];
-  if (HS == 1) return kq4_gv_pick(v[0], v[1], p);
-  return kq4_gv_pick(kq4_gv_pick(v[0], v[1], p & 1), kq4_gv_pick(v[2], v[3], p & 1), p >> 1);
-}
-
-// Row scale (f32) of lane block jb; the register index is compile-time in all modes.
-// q8: block b = NP*jb + p, its scale at sc[b/2] >> 16*(b%2); q4: block 2*(NP*(jb/2) + p) + jb%2,
-// at sc[NP*(jb/2) + p] >> 16*(jb%2).
-template <int HS, int WF>
-KQ4_DEV float kq4_gv_wd(const KQ4GvStage<HS> &st, int jb, int p) {
-  if (WF) {
-    if (HS == 0) return kq4_h2f(st.sc[jb >> 1] >> (16 * (jb & 1)));
-    if (HS == 1) return kq4_h2f(st.sc[jb] >> (16 * p));
-    return kq4_h2f(kq4_gv_pick(st.sc[2 * jb], st.sc[2 * jb + 1], p >> 1) >> (16 * (p & 1)));
-  }
-  const uint32_t w = kq4_gv_pickn<HS>(&st.sc[(jb >> 1) << HS], p);
-  return kq4_h2f(w >> (16 * (jb & 1)));
-}
-
-// The MFMA B operand of lane block jb: q4 unpacks its 8 nibble bytes to 16*(n-8); q8 is the
-// 16-B unit as loaded.
-template <int WF>
-KQ4_DEV void kq4_gv_bop(const uint32_t *n, int jb, uint32_t *o) {
-  if (WF) {
-    o[0] = n[4 * jb]; o[1] = n[4 * jb + 1]; o[2] = n[4 * jb + 2]; o[3] = n[4 * jb + 3];
-  } else {
-    kq4_unpack_half(n[2 * jb], n[2 * jb + 1], o);
-  }
-}
-
-// ---- activations of a stage -------------------------------------------------------------------
-// Loaded into registers together with (just before) the stage's weights, then written to the
-// wave's slab as int8 codes (token row m at m*KQ4_GV_QTS, block at kq4_gv_qpos) and the
-// effective per-block scale sx[blk][m] = xs/16 for q4 (xs = f16-rounded xd for ASM-chain tokens;
-// the /16 undoes the 16*(n-8) weight scaling exactly), xs for q8. A stage is 16 blocks of q4 or 8
-// of q8. Issuing them before the weights keeps the in-order load counter from making the
-// quantization wait for the weights.
-//
-// FQ = 0: pre-quantized; 1: fp32 activations; 2: fp32 gate and up, activation = silu_mul(g, u)
-// (kq4_silu_mul, the dense FFN's down input, vllm_safetensors.c:10932-10958).
-// FQ 1, 2 (M <= KQ4_GEMV_FQ_MAX_M): lane quad (4q .. 4q+3) owns block q for one token per pass, 8
-// fp32 each; the quantization restates quantize_row_q8_0_act (vllm_safetensors.c:7893-7920):
-// d = amax/127 is a true division, x/d the Markstein-corrected quotient q = x*y,
-// q += fma(-q, d, x)*y with y = RN(1/d), which is the correctly rounded x/d for these normal
-// operands, so the codes are the reference's bit for bit.
-// Pre-quantized: lane i copies 16-B units i, i+64, .. of the stage's codes and scales i, i+64.
-template <int M, int FQ, int WF>
-struct KQ4GvAct {
-  static constexpr int CB = KQ4Wf<WF>::CB;
-  static constexpr int NQ = FQ ? 1 : (2 * CB * M + 63) / 64;   // uint4 per lane
-  static constexpr int NX = FQ ? 1 : (CB * M + 63) / 64;       // scales per lane
-  float4 f[FQ ? 2 * M : 1];
-  float4 u[FQ == 2 ? 2 * M : 1];
-  uint4 q[NQ];
-  float x[NX];
-};
-
-template <int M, int FQ, int WF>
-KQ4_DEV void kq4_gv_act_load(KQ4GvAct<M, FQ, WF> &r, const KQ4GemvArgs &a, int st, int lane) {
-  constexpr int CB = KQ4Wf<WF>::CB;
-  const int nb = a.nb, cols = a.cols;
-  const int kb = st * CB;
-  if (FQ) {
-    const int b = kb + (lane >> 2), qq = lane & 3;
-    const bool live = (lane >> 2) < CB && b < nb;
-#pragma unroll
-    for (int m = 0; m < M; ++m) {
-      if (live) {
-        const float4 *src =
-            reinterpret_cast<const float4 *>(a.xf + (size_t)m * cols + (size_t)b * 32 + 8 * qq);
-        r.f[2 * m] = src[0];
-        r.f[2 * m + 1] = src[1];
-        if (FQ == 2) {
-          const float4 *su = reinterpret_cast<const float4 *>(a.xu + (size_t)m * cols +
-                                                              (size_t)b * 32 + 8 * qq);
-          r.u[2 * m] = su[0];
-          r.u[2 * m + 1] = su[1];
-        }
-      } else {
-        r.f[2 * m] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        r.f[2 * m + 1] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        if (FQ == 2) {
-          r.u[2 * m] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-          r.u[2 * m + 1] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        }
-      }
-    }
-  } else {
-#pragma unroll
-    for (int c = 0; c < KQ4GvAct<M, FQ, WF>::NQ; ++c) {
-      const int i = lane + 64 * c;
-      const int m = i / (2 * CB), u = i % (2 * CB), b = kb + (u >> 1), hh = u & 1;
-      r.q[c] = make_uint4(0, 0, 0, 0);
-      if (m < M && b < nb)
-        r.q[c] = *reinterpret_cast<const uint4 *>(a.xq + (size_t)m * cols + (size_t)b * 32 + 16 * hh);
-    }
-#pragma unroll
-    for (int c = 0; c < KQ4GvAct<M, FQ, WF>::NX; ++c) {
-      const int i = lane + 64 * c;
-      const int m = i / CB, b = kb + i % CB;
-      r.x[c] = (m < M && b < nb) ? a.xd[(size_t)m * nb + b] : 0.0f;
-    }
-  }
-}
-
-template <int M, int FQ, int WF>
-KQ4_DEV void kq4_gv_act_put(const KQ4GvAct<M, FQ, WF> &r, const KQ4GemvArgs &a, int lane,
-                            uint8_t *sq, float (*sx)[8]) {
-  constexpr int CB = KQ4Wf<WF>::CB;
-  constexpr float XS = KQ4Wf<WF>::XS;
-  if (FQ) {
-    const int blk = lane >> 2, qq = lane & 3;
-#pragma unroll
-    for (int m = 0; m < M; ++m) {
-      float v[8] = {r.f[2 * m].x, r.f[2 * m].y, r.f[2 * m].z, r.f[2 * m].w,
-                    r.f[2 * m + 1].x, r.f[2 * m + 1].y, r.f[2 * m + 1].z, r.f[2 * m + 1].w};
-      if (FQ == 2) {
-        const float u[8] = {r.u[2 * m].x, r.u[2 * m].y, r.u[2 * m].z, r.u[2 * m].w,
-                            r.u[2 * m + 1].x, r.u[2 * m + 1].y, r.u[2 * m + 1].z, r.u[2 * m + 1].w};
-#pragma unroll
-        for (int i = 0; i < 8; ++i) v[i] = kq4_silu_mul(v[i], u[i]);
-      }
-      float amax = 1e-10f;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
-      amax = kq4_quad_max(amax);
-      const float d = amax / 127.0f;
-      const float y = 1.0f / d;
-      uint32_t pk[2] = {0, 0};
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        float q = v[i] * y;
-        const float e = fmaf(-q, d, v[i]);
-        q = fmaf(e, y, q);
-        int c = (int)(q + 0.5f);
-        c = c > 127 ? 127 : (c < -127 ? -127 : c);
-        pk[i >> 2] |= ((uint32_t)c & 0xFFu) << (8 * (i & 3));
-      }
-      if (blk < CB) {   // q8 stages have 8 blocks: lanes 32-63 hold nothing
-        *reinterpret_cast<uint2 *>(sq + m * KQ4_GV_QTS + kq4_gv_qpos(blk) + 8 * qq) =
-            make_uint2(pk[0], pk[1]);
-        if (qq == 0) sx[blk][m] = ((m < a.asm_tokens) ? kq4_f16_round(d) : d) * XS;
-      }
-    }
-  } else {
-#pragma unroll
-    for (int c = 0; c < KQ4GvAct<M, FQ, WF>::NQ; ++c) {
-      const int i = lane + 64 * c;
-      const int m = i / (2 * CB), u = i % (2 * CB);
-      if (m < M)
-        *reinterpret_cast<uint4 *>(sq + m * KQ4_GV_QTS + kq4_gv_qpos(u >> 1) + 16 * (u & 1)) = r.q[c];
-    }
-#pragma unroll
-    for (int c = 0; c < KQ4GvAct<M, FQ, WF>::NX; ++c) {
-      const int i = lane + 64 * c;
-      const int m = i / CB, blk = i % CB;
-      if (m < M) sx[blk][m] = ((m < a.asm_tokens) ? kq4_f16_round(r.x[c]) : r.x[c]) * XS;
-    }
-  }
-}
-
-// ---- compute ---------------------------------------------------------------------------------
-
-// Materialises x here: the unrolled block loops below would otherwise have every block's product
-// sunk to the end of the stage, keeping all blocks' operands live at once (far more registers
-// than a wave has).
-KQ4_DEV void kq4_gv_pin(float &x) { asm volatile("" : "+v"(x)); }
-
-// DOT4: acc[m] = token m's chain over this lane's blocks of its row and half.
-// One token in half- or quarter-set mode (the decode shapes with few row sets): all the lane's
-// blocks' codes and scales are read from LDS first (40 or 20 registers), so the blocks do not wait
-// for LDS one by one once the weights are in.
-template <int M, int HS>
-KQ4_DEV void kq4_gv_dot4(const KQ4GvStage<HS> &st, const uint8_t *sq, const float (*sx)[8], int h,
-                         int p, float *acc) {
-  constexpr int NJB = 2 * KQ4GvStage<HS>::NU;
-  constexpr bool PRE = M == 1 && HS >= 1;
-  uint4 qv[PRE ? NJB : 1];
-  float xv[PRE ? NJB : 1];
-  if (PRE) {
-#pragma unroll
-    for (int jb = 0; jb < NJB; ++jb) {
-      const int b = kq4_gv_blk<HS, 0>(jb, p);
-      qv[jb] = *reinterpret_cast<const uint4 *>(sq + kq4_gv_qpos(b) + 16 * h);
-      xv[jb] = sx[b][0];
-    }
-  }
-#pragma unroll
-  for (int jb = 0; jb < NJB; ++jb) {
-    const int b = kq4_gv_blk<HS, 0>(jb, p);
-    uint32_t o[4];
-    kq4_unpack_half(st.n[2 * jb], st.n[2 * jb + 1], o);
-    const float wd = kq4_gv_wd<HS, 0>(st, jb, p);
-#pragma unroll
-    for (int m = 0; m < M; ++m) {
-      const uint4 q = PRE ? qv[jb]
-                          : *reinterpret_cast<const uint4 *>(sq + m * KQ4_GV_QTS + kq4_gv_qpos(b) +
-                                                             16 * h);
-      int s = kq4_dot4(o[0], q.x, 0);
-      s = kq4_dot4(o[1], q.y, s);
-      s = kq4_dot4(o[2], q.z, s);
-      s = kq4_dot4(o[3], q.w, s);
-      acc[m] = fmaf((float)s, wd * (PRE ? xv[jb] : sx[b][m]), acc[m]);
-      kq4_gv_pin(acc[m]);
-    }
-  }
-}
-
-// MFMA: one v_mfma_i32_32x32x32_i8 per lane block. B column = lane%32 = row + NR*p (the NP
-// parities hold different blocks), k half = lane/32. A row = lane%32 holds the codes of token
-// min(lane % NR, M-1) for the lane's own block, so output (token row T, column c) is valid where
-// T's block matches c's: T = token + NR*p, which the 32x32 output layout puts in result register
-// (NR/2)*p + v for token 4h+v. acc[v] = token 4h+v of the lane's row (and parity).
-template <int M, int HS, int WF>
-KQ4_DEV void kq4_gv_mfma_stage(const KQ4GvStage<HS> &st, const uint8_t *sq, const float (*sx)[8],
-                               int lane, int p, float *acc) {
-  constexpr int VT = M < 4 ? M : 4;
-  const int h = lane >> 5;
-  constexpr int NR = 32 >> HS;
-  const int tr = lane & (NR - 1);
-  const int t = tr < M ? tr : M - 1;
-  const uint8_t *qb = sq + t * KQ4_GV_QTS + 16 * h;
-#pragma unroll
-  for (int jb = 0; jb < KQ4GvStage<HS>::NU * KQ4Wf<WF>::BPU; ++jb) {
-    const int b = kq4_gv_blk<HS, WF>(jb, p);
-    uint32_t o[4];
-    kq4_gv_bop<WF>(st.n, jb, o);
-    const kq4_v4i B = {(int)o[0], (int)o[1], (int)o[2], (int)o[3]};
-    const kq4_v4i A = *reinterpret_cast<const kq4_v4i *>(qb + kq4_gv_qpos(b));
-    const kq4_v16i C = kq4_gv_mfma(A, B);
-    const float wd = kq4_gv_wd<HS, WF>(st, jb, p);
-    const float4 xs = *reinterpret_cast<const float4 *>(&sx[b][4 * h]);
-    const float xv[4] = {xs.x, xs.y, xs.z, xs.w};
-#pragma unroll
-    for (int v = 0; v < VT; ++v) {
-      uint32_t cv[1 << HS];
-#pragma unroll
-      for (int pp = 0; pp < (1 << HS); ++pp) cv[pp] = (uint32_t)C[(NR / 2) * pp + v];
-      const int c = (int)kq4_gv_pickn<HS>(cv, p);
-      if (WF == 2) acc[v] = acc[v] + (wd * xv[v]) * (float)c;   // the q8 GEMM chain, unfused
-      else acc[v] = fmaf((float)c, wd * xv[v], acc[v]);
-      kq4_gv_pin(acc[v]);
-    }
-  }
-}
-
-// The matrix of workgroup wg (a launch covers up to KQ4_MAXMAT matrices, each a contiguous range
-// of workgroups). Every entry's fields are read first and then chosen by compares: indexing the
-// argument array by the chosen entry would be a second scalar load that waits for the first, and
-// the weight loads wait for both (the empty asm keeps the compiler from turning the selects back
-// into an indexed load).
-// The pointers are kept in the global address space (kernel arguments are global memory; a
-// generic pointer out of the asm would make every weight load a flat load, which also counts
-// against the LDS wait counter).
-typedef const __attribute__((address_space(1))) uint8_t *kq4_gw_t;
-typedef __attribute__((address_space(1))) float *kq4_go_t;
-typedef const __attribute__((address_space(1))) float *kq4_gr_t;
-
-struct KQ4GvMatSel {
-  kq4_gw_t w;
-  kq4_go_t out;
-  kq4_gr_t res;
-  int rows, wg_begin;
-};
-
-KQ4_DEV KQ4GvMatSel kq4_gv_select(const KQ4GemvArgs &a, int wg) {
-  static_assert(KQ4_MAXMAT == 4, "kq4_gv_select reads 4 entries");
-  kq4_gw_t w1 = (kq4_gw_t)a.mat[1].w, w2 = (kq4_gw_t)a.mat[2].w, w3 = (kq4_gw_t)a.mat[3].w;
-  kq4_go_t o1 = (kq4_go_t)a.mat[1].out, o2 = (kq4_go_t)a.mat[2].out, o3 = (kq4_go_t)a.mat[3].out;
-  kq4_gr_t r1 = (kq4_gr_t)a.mat[1].res, r2 = (kq4_gr_t)a.mat[2].res, r3 = (kq4_gr_t)a.mat[3].res;
-  int n1 = a.mat[1].rows, n2 = a.mat[2].rows, n3 = a.mat[3].rows;
-  int b1 = a.mat[1].wg_begin, b2 = a.mat[2].wg_begin, b3 = a.mat[3].wg_begin;
-  asm volatile("" : "+s"(w1), "+s"(w2), "+s"(w3), "+s"(o1), "+s"(o2), "+s"(o3), "+s"(r1),
-               "+s"(r2), "+s"(r3), "+s"(n1), "+s"(n2), "+s"(n3), "+s"(b1), "+s"(b2), "+s"(b3));
-  KQ4GvMatSel s{(kq4_gw_t)a.mat[0].w, (kq4_go_t)a.mat[0].out, (kq4_gr_t)a.mat[0].res,
-                a.mat[0].rows, 0};
-  const int nm = a.nmat;
-  if (nm > 1 && wg >= b1) s = KQ4GvMatSel{w1, o1, r1, n1, b1};
-  if (nm > 2 && wg >= b2) s = KQ4GvMatSel{w2, o2, r2, n2, b2};
-  if (nm > 3 && wg >= b3) s = KQ4GvMatSel{w3, o3, r3, n3, b3};
-  return s;
-}
-
-// One workgroup per 32-row set (HS = 0), half set (HS = 1) or quarter set (HS = 2), up to 16
-// waves splitting K (every variant fits the 128 VGPRs that allows).
-template <int M, int FQ, int KIND, int HS, int WF>
-__global__ __launch_bounds__(1024) void kq4_gemv_kernel(const KQ4GemvArgs a) {
-  extern __shared__ __align__(16) uint8_t kq4_gv_lds[];
-  constexpr int SLAB = kq4_gv_slab<M>();
-  constexpr int NACC = KIND == 0 ? M : 4;
-  constexpr int NR = 32 >> HS;                     // output rows of the workgroup
-  constexpr int NP = 1 << HS;                      // lane parities
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int nw = a.nw;   // = blockDim.x / 64 (an argument: the dispatch's own field sits on another line)
-  const int wg = blockIdx.x;
-  const KQ4GvMatSel ms = kq4_gv_select(a, wg);
-  const int wl = wg - ms.wg_begin;
-  const int rs = wl >> HS;                         // 32-row set within the matrix
-  const int hs = wl & (NP - 1);                    // the workgroup's part of the set
-  const int rows = ms.rows;
-  const int row0 = rs * 32 + hs * NR;              // first output row of the workgroup
-  const int nb = a.nb;
-  constexpr int CB = KQ4Wf<WF>::CB, CHUNK = KQ4Wf<WF>::CHUNK;
-  const int nst = (nb + CB - 1) / CB;
-  const uint8_t *__restrict__ wset = (const uint8_t *)ms.w + (size_t)rs * nst * CHUNK;
-  uint8_t *slab = kq4_gv_lds + wave * SLAB;
-  uint8_t *sq = slab;
-  float (*sx)[8] = reinterpret_cast<float (*)[8]>(sq + M * KQ4_GV_QTS);
-  const int h = lane >> 5;
-  const int p = (lane >> (5 - HS)) & (NP - 1);
-  const int r = lane & (NR - 1);                   // row within the workgroup
-  const int rr = hs * NR + r;                      // row within the set
-
-  float acc[NACC];
-#pragma unroll
-  for (int i = 0; i < NACC; ++i) acc[i] = 0.0f;
-  for (int st = wave; st < nst; st += nw) {
-    // issued as (activations, weights), so quantizing the activations waits only for them
-    KQ4GvAct<M, FQ, WF> ra;
-    KQ4GvStage<HS> rw;
-    kq4_gv_act_load<M, FQ, WF>(ra, a, st, lane);
-    kq4_gv_load<HS, WF>(rw, wset + (size_t)st * CHUNK, rr, h, p);
-    // One token, fp32 activations: every load is issued before the quantization waits for the
-    // activations (the compiler otherwise sinks the weight loads below it, and the two memory
-    // latencies add up). Measured: the Qwen3-VL-2B decode GEMVs 0.1-0.3 us faster each, the
-    // Qwen3-8B down 0.5 us; with more tokens or the SiLU form it measured slower, so there the
-    // compiler's order stays.
-    if constexpr (M == 1 && FQ == 1) __builtin_amdgcn_sched_barrier(0);
-    kq4_gv_act_put<M, FQ, WF>(ra, a, lane, sq, sx);
-    if (KIND == 0) kq4_gv_dot4<M, HS>(rw, sq, sx, h, p, acc);
-    else kq4_gv_mfma_stage<M, HS, WF>(rw, sq, sx, lane, p, acc);
-  }
-
-  // Each output's lane partials are first added inside the wave by a fixed tree of lane swaps
-  // (DOT4: the two K halves' chains, then the parities; MFMA: the parities; lane bits 3 and 4 of
-  // quarter sets, bit 4 of half sets), and the wave's sum goes to its slab at red[m*NR + r]; one
-  // thread per output then adds the waves' sums in wave order. The order is fixed, so results
-  // are deterministic.
-  float *__restrict__ out = (float *)ms.out;
-  const float *__restrict__ res = (const float *)ms.res;
-  float *red = reinterpret_cast<float *>(slab);   // only this wave used its slab so far
-  if (KIND == 0) {
-#pragma unroll
-    for (int m = 0; m < M; ++m) {
-      float v = kq4_xor_add<32>(acc[m]);
-      if (HS == 2) v = kq4_xor_add<8>(v);
-      if (HS >= 1) v = kq4_xor_add<16>(v);
-      if (lane < NR) red[m * NR + r] = v;
-    }
-  } else {
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      float t = acc[v];
-      if (HS == 2) t = kq4_xor_add<8>(t);
-      if (HS >= 1) t = kq4_xor_add<16>(t);
-      if (p == 0 && 4 * h + v < M) red[(4 * h + v) * NR + r] = t;
-    }
-  }
-  // The first pass's residual is loaded before the barrier, so its latency hides behind the
-  // wait (measured: 2B down and O with residual 0.04-0.08 us faster per launch at one token).
-  float res0 = 0.0f;
-  {
-    const int i = threadIdx.x, row = row0 + (i & (NR - 1));
-    if (res && i < NR * M && row < rows) res0 = res[(size_t)(i / NR) * rows + row];
-  }
-  __syncthreads();
-  for (int i = threadIdx.x; i < NR * M; i += 64 * nw) {
-    const int row = row0 + (i & (NR - 1));
-    if (row >= rows) continue;
-    float s = 0.0f;
-    for (int w = 0; w < nw; ++w) {
-      const float *rv = reinterpret_cast<const float *>(kq4_gv_lds + w * SLAB);
-      if (KIND == 0) {
-        s += rv[i];
-      } else {
-        s += rv[i];
-      }
-    }
-    const size_t o = (size_t)(i / NR) * rows + row;
-    out[o] = res ? (i == (int)threadIdx.x ? res0 : res[o]) + s : s;
-  }
-}
-
-template <int M, int FQ, int KIND, int HS, int WF>
-static hipError_t gv_launch(const KQ4GemvArgs &a, int nw, int grid, hipStream_t s) {
-  const size_t lds = (size_t)nw * kq4_gv_slab<M>();
-  static bool attr = false;   // allow more than 64 KB of dynamic LDS, once per variant
-  if (!attr) {
-    hipError_t e = hipFuncSetAttribute(
-        reinterpret_cast<const void *>(&kq4_gemv_kernel<M, FQ, KIND, HS, WF>),
-        hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-    if (e != hipSuccess) return e;
-    attr = true;
-  }
-  KQ4GemvArgs b = a;
-  b.nw = nw;
-  hipLaunchKernelGGL((kq4_gemv_kernel<M, FQ, KIND, HS, WF>), dim3(grid), dim3(64 * nw), lds, s,
-                     b);
-  return hipGetLastError();
-}
-
-template <int M, int FQ, int KIND, int WF>
-static hipError_t gv_launch_hs(const KQ4GemvArgs &a, int hs, int nw, int grid, hipStream_t s) {
-  if (hs == 2) return gv_launch<M, FQ, KIND, 2, WF>(a, nw, grid, s);
-  if (hs == 1) return gv_launch<M, FQ, KIND, 1, WF>(a, nw, grid, s);
-  return gv_launch<M, FQ, KIND, 0, WF>(a, nw, grid, s);
-}
-
-template <int M, int FQ>
-static hipError_t gv_launch_k(const KQ4GemvArgs &a, int kind, int hs, int nw, int grid,
-                              hipStream_t s) {
-  if (a.wf == 1)   // q8: the MFMA kind only (its block sums span both K halves)
-    return gv_launch_hs<M, FQ, 1, 1>(a, hs, nw, grid, s);
-  if (a.wf == 2)
-    return gv_launch_hs<M, FQ, 1, 2>(a, hs, nw, grid, s);
-  if (kind == 0)
-    return gv_launch_hs<M, FQ, 0, 0>(a, hs, nw, grid, s);
-  return gv_launch_hs<M, FQ, 1, 0>(a, hs, nw, grid, s);
-}
-
-// In-kernel quantization exists for M <= KQ4_GEMV_FQ_MAX_M, the SiLU form for q4 and
-// M <= KQ4_GEMV_SILU_FQ_MAX_M (its fp32 gate and up registers would spill beyond).
-template <int M>
-static hipError_t gv_launch_m(const KQ4GemvArgs &a, int kind, int fq, int hs, int nw, int grid,
-                              hipStream_t s) {
-  constexpr int MF = M <= KQ4_GEMV_FQ_MAX_M ? M : 1;
-  constexpr int MS = M <= KQ4_GEMV_SILU_FQ_MAX_M ? M : 1;
-  if (fq) {
-    if (M > KQ4_GEMV_FQ_MAX_M) return hipErrorInvalidValue;
-    if (fq == 2) {
-      if (a.wf || M > KQ4_GEMV_SILU_FQ_MAX_M) return hipErrorInvalidValue;
-      if (kind == 0)
-        return gv_launch_hs<MS, 2, 0, 0>(a, hs, nw, grid, s);
-      return gv_launch_hs<MS, 2, 1, 0>(a, hs, nw, grid, s);
-    }
-    return gv_launch_k<MF, 1>(a, kind, hs, nw, grid, s);
-  }
-  return gv_launch_k<M, 0>(a, kind, hs, nw, grid, s);
-}
+hipError_t kq4_gv_launch_m(const KQ4GemvArgs &a, int kind, int fq, int hs, int rps, int grid,
+                           hipStream_t s);
+extern template hipError_t kq4_gv_launch_m<1>(const KQ4GemvArgs &, int, int, int, int, int, hipStream_t);
+extern template hipError_t kq4_gv_launch_m<2>(const KQ4GemvArgs &, int, int, int, int, int, hipStream_t);
+extern template hipError_t kq4_gv_launch_m<3>(const KQ4GemvArgs &, int, int, int, int, int, hipStream_t);
+extern template hipError_t kq4_gv_launch_m<4>(const KQ4GemvArgs &, int, int, int, int, int, hipStream_t);
+extern template hipError_t kq4_gv_launch_m<5>(const KQ4GemvArgs &, int, int, int, int, int, hipStream_t);
+extern template hipError_t kq4_gv_launch_m<6>(const KQ4GemvArgs &, int, int, int, int, int, hipStream_t);
+extern template hipError_t kq4_gv_launch_m<7>(const KQ4GemvArgs &, int, int, int, int, int, hipStream_t);
+extern template hipError_t kq4_gv_launch_m<8>(const KQ4GemvArgs &, int, int, int, int, int, hipStream_t);
 
 int kq4_gemv_slab_bytes(int n_batch) { return n_batch * KQ4_GV_QTS + KQ4_GV_XS; }
 
-int kq4_launch_gemv(const KQ4GemvArgs &a, int n_batch, int kind, int half_sets, int nw,
-                    int total_wg, hipStream_t s) {
-  if (n_batch < 1 || n_batch > KQ4_GEMV_MAX_M || total_wg <= 0 || nw < 1 || nw > 16 ||
-      kind < 0 || kind > 1 || half_sets < 0 || half_sets > 2 ||
-      (size_t)nw * kq4_gemv_slab_bytes(n_batch) > 160 * 1024)
+int kq4_launch_gemv(const KQ4GemvArgs &a, int n_batch, int kind, int half_sets, int rps,
+                    int grid, hipStream_t s) {
+  const int nw = a.nw;
+  if (n_batch < 1 || n_batch > KQ4_GEMV_MAX_M || grid <= 0 || nw < 1 || nw > 16 || kind < 0 ||
+      kind > 1 || (kind == 0 && n_batch > KQ4_GEMV_DOT4_MAX_M) || half_sets < 0 ||
+      half_sets > 2 || rps < 1 || rps > KQ4_GEMV_MAX_RPS || (half_sets && rps != 1) ||
+      (rps > 1 && nw > KQ4_GEMV_RPS_MAX_WAVES) ||
+      a.ksl < 1 || a.spk < 1 || (a.ksl > 1 && (!a.part || !a.cnt)) || grid % a.ksl ||
+      (size_t)nw * kq4_gemv_slab_bytes(n_batch) > 160 * 1024 - 64)
     return (int)hipErrorInvalidValue;
   for (int i = 0; i < a.nmat; ++i)
     if ((uintptr_t)a.mat[i].w % 16) return (int)hipErrorInvalidValue;
@@ -584,14 +34,14 @@ int kq4_launch_gemv(const KQ4GemvArgs &a, int n_batch, int kind, int half_sets, 
   const int hs = half_sets;
   hipError_t e;
   switch (n_batch) {
-    case 1: e = gv_launch_m<1>(a, kind, fq, hs, nw, total_wg, s); break;
-    case 2: e = gv_launch_m<2>(a, kind, fq, hs, nw, total_wg, s); break;
-    case 3: e = gv_launch_m<3>(a, kind, fq, hs, nw, total_wg, s); break;
-    case 4: e = gv_launch_m<4>(a, kind, fq, hs, nw, total_wg, s); break;
-    case 5: e = gv_launch_m<5>(a, kind, fq, hs, nw, total_wg, s); break;
-    case 6: e = gv_launch_m<6>(a, kind, fq, hs, nw, total_wg, s); break;
-    case 7: e = gv_launch_m<7>(a, kind, fq, hs, nw, total_wg, s); break;
-    default: e = gv_launch_m<8>(a, kind, fq, hs, nw, total_wg, s); break;
+    case 1: e = kq4_gv_launch_m<1>(a, kind, fq, hs, rps, grid, s); break;
+    case 2: e = kq4_gv_launch_m<2>(a, kind, fq, hs, rps, grid, s); break;
+    case 3: e = kq4_gv_launch_m<3>(a, kind, fq, hs, rps, grid, s); break;
+    case 4: e = kq4_gv_launch_m<4>(a, kind, fq, hs, rps, grid, s); break;
+    case 5: e = kq4_gv_launch_m<5>(a, kind, fq, hs, rps, grid, s); break;
+    case 6: e = kq4_gv_launch_m<6>(a, kind, fq, hs, rps, grid, s); break;
+    case 7: e = kq4_gv_launch_m<7>(a, kind, fq, hs, rps, grid, s); break;
+    default: e = kq4_gv_launch_m<8>(a, kind, fq, hs, rps, grid, s); break;
   }
   return (int)e;
 }

@@ -1,0 +1,5 @@
+// kq4_gemv_m8.hip - the decode GEMV kernels for 8 token(s) (kq4_gemv_impl.h), a translation unit
+// of its own so the instantiations compile in parallel.
+#include "kq4_gemv_impl.h"
+
+template hipError_t kq4_gv_launch_m<8>(const KQ4GemvArgs &, int, int, int, int, int, hipStream_t);

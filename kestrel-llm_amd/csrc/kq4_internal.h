@@ -6,8 +6,6 @@
 
 #define KQ4_GEMV_MAX_M 8
 #define KQ4_MAXMAT 4
-#define KQ4_GEMV_FQ_MAX_M 4   // largest token count the GEMV quantizes in-kernel
-#define KQ4_GEMV_SILU_FQ_MAX_M 3   // .. and forms the SiLU product in-kernel (registers)
 
 // Every kernel reads q4 weights in the stream layout (kq4_common.h): a VQF 4x4 matrix repacked
 // once by kq4_launch_repack into kq4_stream_bytes(rows, cols) bytes.
@@ -25,7 +23,7 @@ struct KQ4GemvMat {
   float *out;           // [M][rows]
   const float *res;     // [M][rows] or nullptr
   int rows;
-  int wg_begin;         // first workgroup (row set or half set) of this matrix in the launch
+  int wg_begin;         // first group (R row sets, or a half / quarter set) of this matrix
 };
 
 struct KQ4GemvArgs {
@@ -40,7 +38,11 @@ struct KQ4GemvArgs {
                         // 1 fused VDOT or 2 unfused GEMM chain
   int cols;
   int nb;
-  int nw;               // waves per workgroup (set by kq4_launch_gemv)
+  int nw;               // waves per workgroup
+  int ksl;              // K slices: workgroups per group (1 = each workgroup takes the whole K)
+  int spk;              // stages per K slice
+  float *part;          // ksl > 1: partial sums [groups][ksl][R * M * rows per set part]
+  unsigned *cnt;        // ksl > 1: per-group arrival counters, zero before and after a launch
 };
 
 // up != nullptr: quantizes silu_mul(x, up) instead of x (the dense FFN's down input).
@@ -56,13 +58,15 @@ size_t kq4_rms_norm_lds(int d, int serial);
 int kq4_launch_rms_norm(const float *x, const float *w, float *out, int8_t *xq, float *xd,
                         int n_batch, int d, float eps, int serial, hipStream_t stream);
 
-// n_batch in [1, KQ4_GEMV_MAX_M]; one workgroup per 32-row set, or per 16-row half set when
-// half_sets = 1, per 8-row quarter set when 2 (total_wg over all matrices, each matrix's wg_begin
-// counted in those units),
-// nw (1..16) waves splitting K in 16-block stages; kind 0 = per-lane v_dot4 dots, 1 = v_mfma
-// dots. args.xf (in-kernel quantization) requires n_batch <= KQ4_GEMV_FQ_MAX_M.
-int kq4_launch_gemv(const KQ4GemvArgs &args, int n_batch, int kind, int half_sets, int nw,
-                    int total_wg, hipStream_t stream);
+// One GEMV launch (kq4_gemv_impl.h): n_batch in [1, KQ4_GEMV_MAX_M]; kind 0 = per-lane v_dot4
+// dots (n_batch <= KQ4_GEMV_DOT4_MAX_M), 1 = v_mfma dots; half_sets 0 (whole 32-row sets, rps of
+// them per group), 1 (16-row halves) or 2 (8-row quarters, rps = 1); grid = groups * args.ksl
+// workgroups of args.nw (1..16) waves. args.xf (in-kernel quantization) for every n_batch.
+#define KQ4_GEMV_DOT4_MAX_M 4
+#define KQ4_GEMV_MAX_RPS 3
+#define KQ4_GEMV_RPS_MAX_WAVES 8   // waves per workgroup when it takes several row sets
+int kq4_launch_gemv(const KQ4GemvArgs &args, int n_batch, int kind, int half_sets, int rps,
+                    int grid, hipStream_t stream);
 int kq4_gemv_slab_bytes(int n_batch);
 
 int kq4_launch_block_sums(int32_t *s_lo, int32_t *s_hi, const int8_t *xq, const uint8_t *w,

@@ -26,6 +26,7 @@ SIGNATURES = [
     ("kq4_shutdown", None, []),
     ("kq4_last_error", ctypes.c_char_p, []),
     ("kq4_version", ctypes.c_char_p, []),
+    ("kq4_set_option", _I, [ctypes.c_char_p, _I]),
     ("kq4_weights_upload", _I, [_U64, _P, _I, _I]),
     ("kq4_weights_evict", _I, [_U64]),
     ("kq4_weights_clear", _I, []),
@@ -172,6 +173,27 @@ def check_done(rc, what):
 
 def init(device=0):
     check(lib().kq4_init(device), "kq4_init")
+
+
+def set_option(name, value):
+    """A launch-planner option (include/kq4.h kq4_set_option); value < 0 restores the default."""
+    check(lib().kq4_set_option(name.encode(), int(value)), f"kq4_set_option({name})")
+
+
+class options:
+    """Context manager setting planner options and restoring their defaults on exit."""
+
+    def __init__(self, **kv):
+        self.kv = kv
+
+    def __enter__(self):
+        for k, v in self.kv.items():
+            set_option(k, v)
+        return self
+
+    def __exit__(self, *a):
+        for k in self.kv:
+            set_option(k, -1)
 
 
 def _np_ptr(a):

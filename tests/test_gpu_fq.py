@@ -1,8 +1,9 @@
 """The decode GEMV's in-kernel activation quantization, pinned code for code.
 
-For M <= 4 tokens the GEMV quantizes its fp32 activations itself, every wave for its own stage
-(the FQ form of kq4_gemv_kernel), and with the SiLU product (FQ = 2) for M <= 3. That is the path
-the decode hot path runs, including the headline benchmark. These tests run it against the same
+The decode GEMV quantizes its fp32 activations itself, every wave for its own stage (the FQ form
+of kq4_gemv_kernel, in passes of up to 4 tokens), and with the SiLU product (FQ = 2, passes of
+2 tokens). That is the path the decode hot path runs, including the headline benchmark; the
+tests force it on (planner option gemv_fq = 1) at every token count 1..8. These tests run it against the same
 kernel, same plan and same dot kind, fed with the oracle's codes through the pre-quantized entry
 point (kq4_matmul_q_dev): the two launches differ only in where the codes come from, so the
 outputs are bit-identical exactly when the in-kernel codes and scales are the oracle's
@@ -40,7 +41,7 @@ def bits(t):
 # rows 256 (8 row sets): quarter-set workgroups; 4096 (128): half sets; 16384 (512): full sets;
 # all within the in-kernel quantization's work limit at cols = 256
 @pytest.mark.parametrize("rows", [256, 4096, 16384])
-@pytest.mark.parametrize("m", [1, 2, 3, 4])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8])
 def test_fq_codes_match_reference_quantizer(kq4, torch_dev, orc, rows, m):
     torch = torch_dev
     xs = quant_rows()
@@ -51,13 +52,14 @@ def test_fq_codes_match_reference_quantizer(kq4, torch_dev, orc, rows, m):
         xq, xd = orc.quantize(x, cols)
         a = torch.empty((m, rows), dtype=torch.float32, device="cuda")
         b = torch.empty_like(a)
-        kq4.matmul_dev(a, to_dev(torch, x), w, rows, cols)
+        with kq4.options(gemv_fq=1):
+            kq4.matmul_dev(a, to_dev(torch, x), w, rows, cols)
         kq4.matmul_q_dev(b, to_dev(torch, xq), to_dev(torch, xd), w, rows, cols, m)
         torch.cuda.synchronize()
         assert np.array_equal(bits(a), bits(b)), (rows, m, start)
 
 
-@pytest.mark.parametrize("m", [1, 2, 3])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 7, 8])
 def test_fq_silu_codes_match_oracle(kq4, torch_dev, orc, m):
     """FQ = 2: the down projection forms silu_mul(gate, up) and quantizes it in the kernel; fed
     with the oracle's codes of the oracle's product instead, the outputs are bit-identical."""
@@ -73,17 +75,18 @@ def test_fq_silu_codes_match_oracle(kq4, torch_dev, orc, m):
         xq, xd = orc.quantize(orc.silu_mul(g, u), cols)
         a = torch.empty((m, rows), dtype=torch.float32, device="cuda")
         b = torch.empty_like(a)
-        kq4.matmul_silu_dev(a, to_dev(torch, g), to_dev(torch, u), w, rows, cols)
+        with kq4.options(gemv_fq=1):
+            kq4.matmul_silu_dev(a, to_dev(torch, g), to_dev(torch, u), w, rows, cols)
         kq4.matmul_q_dev(b, to_dev(torch, xq), to_dev(torch, xd), w, rows, cols, m)
         torch.cuda.synchronize()
         assert np.array_equal(bits(a), bits(b)), (m, start)
 
 
-@pytest.mark.parametrize("m", [1, 2, 3, 4])
+@pytest.mark.parametrize("m", [1, 2, 4, 8])
 def test_fq_full_size_gate_up(kq4, torch_dev, orc, m):
-    """The Qwen3-8B fused gate/up at M = 1..4 (in-kernel quantization up to M = 3 there, the
-    separate quantizer launch at 4), with the fixture's edge rows in its first blocks: the
-    fp32-input launch is bit-identical to the one fed with the oracle's codes."""
+    """The Qwen3-8B fused gate/up at M = 1, 2, 4, 8 with the planner's own launch shape, with the
+    fixture's edge rows in its first blocks: the fp32-input launch is bit-identical to the one
+    fed with the oracle's codes."""
     torch = torch_dev
     h, f = synth.QWEN3_8B["hidden"], synth.QWEN3_8B["ffn"]
     x = synth.make_activations(m, h, 960 + m)

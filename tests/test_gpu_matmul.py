@@ -181,3 +181,53 @@ def test_gemm_from_prequantized(kq4, torch_dev, orc):
                      rows, cols, n)
     torch.cuda.synchronize()
     assert np.array_equal(host(out), want)
+
+
+# Launch shapes of the GEMV set through the planner options (include/kq4.h kq4_set_option):
+# whole sets grouped 2 or 3 per workgroup (the last group short), half / quarter sets, and K
+# split into slices whose sums the last-arriving slice adds (the last slice short), with the
+# activations quantized in the kernel or apart, with a residual.
+GEMV_PLANS = [dict(gemv_hs=0, gemv_rps=2), dict(gemv_hs=0, gemv_rps=3),
+              dict(gemv_hs=0, gemv_rps=3, gemv_ksl=2), dict(gemv_hs=0, gemv_ksl=3),
+              dict(gemv_hs=1, gemv_ksl=4), dict(gemv_hs=2, gemv_ksl=6),
+              dict(gemv_hs=0, gemv_rps=2, gemv_ksl=5, gemv_fq=0)]
+
+
+@pytest.mark.parametrize("n", [1, 2, 3, 5, 8])
+@pytest.mark.parametrize("plan", range(len(GEMV_PLANS)))
+def test_gemv_plans(kq4, torch_dev, orc, plan, n):
+    torch = torch_dev
+    rows, cols = 32 * 7 + 4, 32 * 16 * 5 + 64            # 8 row sets (last short), 6 stages
+    w, x = case(rows, cols, n, 1000 + plan + n)
+    res = np.random.default_rng(plan).standard_normal((n, rows)).astype(np.float32)
+    want = orc.matmul(w, x, rows, cols, residual=res)
+    wd = wdev(kq4, torch, w, rows, cols)
+    out = torch.empty((n, rows), dtype=torch.float32, device="cuda")
+    again = torch.empty_like(out)
+    with kq4.options(**GEMV_PLANS[plan]):
+        kq4.matmul_dev(out, to_dev(torch, x), wd, rows, cols, residual=to_dev(torch, res))
+        kq4.matmul_dev(again, to_dev(torch, x), wd, rows, cols, residual=to_dev(torch, res))
+    torch.cuda.synchronize()
+    got = host(out)
+    r, a = rel_err(got, want)
+    print(f"plan {GEMV_PLANS[plan]} n={n}: rel={r:.3e} maxabs={a:.3e}")
+    assert r <= TOL
+    assert np.array_equal(got.view(np.uint32), host(again).view(np.uint32))   # deterministic
+
+
+@pytest.mark.parametrize("plan", range(len(GEMV_PLANS)))
+def test_gemv_plans_multi_matrix(kq4, torch_dev, orc, plan):
+    """Three matrices in one launch (fused QKV): groups of each matrix stay within it."""
+    torch = torch_dev
+    cols, n = 2048, 4
+    rows = [2048 + 96, 1024 + 32, 1024 + 32]
+    ws = [synth.make_q4_weights(r, cols, 1200 + i) for i, r in enumerate(rows)]
+    x = synth.make_activations(n, cols, 1300 + plan)
+    outs = [torch.empty((n, r), dtype=torch.float32, device="cuda") for r in rows]
+    with kq4.options(**GEMV_PLANS[plan]):
+        kq4.matmul_multi_dev(outs, to_dev(torch, x),
+                             [wdev(kq4, torch, w, r, cols) for w, r in zip(ws, rows)], rows, cols)
+    torch.cuda.synchronize()
+    for o, w, r in zip(outs, ws, rows):
+        rr, _ = rel_err(host(o), orc.matmul(w, x, r, cols))
+        assert rr <= TOL
