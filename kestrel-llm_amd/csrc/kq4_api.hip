@@ -167,9 +167,12 @@ struct Carve {   // bump allocator over a workspace, above its counter area
 };
 
 // Bytes of a matmul's quantized activations (int8 codes + f32 scales, token-major) in the
-// workspace.
+// workspace, and of the fp8 GEMM's operand pairs (64 B per token and block) + scales.
 size_t qa_bytes(int n, int cols) {
   return al256((size_t)n * cols) + al256((size_t)n * (cols / 32) * sizeof(float));
+}
+size_t f8_bytes(int n, int cols) {
+  return al256((size_t)n * (cols / 32) * 64) + al256((size_t)n * (cols / 32) * sizeof(float));
 }
 
 bool shape_ok(int rows, int cols) { return rows > 0 && rows % 4 == 0 && cols > 0 && cols % 32 == 0; }
@@ -184,7 +187,7 @@ int env_int(const char *name, int dflt) {
 // choice where a planner chooses.
 enum OptId {
   kGemvKind, kGemvMfmaFrom, kGemvHs, kGemvRps, kGemvKsl, kGemvWaves, kGemvWpcu, kGemvMaxw,
-  kGemvFq, kGemvFqWork, kGemvSiluFqWork, kOptCount
+  kGemvFq, kGemvFqWork, kGemvSiluFqWork, kGemmKind, kOptCount
 };
 struct OptDef {
   const char *name, *env;
@@ -197,6 +200,7 @@ const OptDef kOpts[kOptCount] = {
     {"gemv_wpcu", "KQ4_GEMV_WPCU", 32},          {"gemv_maxw", "KQ4_GEMV_MAXW", 16},
     {"gemv_fq", "KQ4_GEMV_FQ", -1},              {"gemv_fq_work", "KQ4_GEMV_FQ_WORK", 45000},
     {"gemv_silu_fq_work", "KQ4_GEMV_SILU_FQ_WORK", 15000},
+    {"gemm_kind", "KQ4_GEMM_KIND", -1},
 };
 std::atomic<int> g_opt[kOptCount];
 std::once_flag g_opt_once;
@@ -427,10 +431,32 @@ int matmul_impl(int n_mats, float *const *out, const float *const *res, const ui
     return run_gemv(ds, ws, n_mats, out, res, w, rows, cols, x, xu, xq_in, xd_in, n,
                     asm_tokens_for(chain, n), s);
 
-  // prefill: int8-MFMA GEMM on the main segment, GEMV on the 1..3-token CTILE tail (AUTO)
+  // prefill: MFMA GEMM on the main segment, GEMV on the 1..3-token CTILE tail (AUTO)
   const int main_n = chain == KQ4_CHAIN_AUTO ? (n & ~3) : n;
   const int tail = n - main_n;
   const int main_chain = chain == KQ4_CHAIN_AUTO ? KQ4_CHAIN_ASM : chain;
+  if (x && (main_chain == KQ4_CHAIN_ASM || main_chain == KQ4_CHAIN_GEMV32) && opt(kGemmKind) == 1) {
+    // fp8 operands (kq4_launch_gemm_f8): the main segment's activations quantized once into
+    // e4m3 operand pairs, the tail tokens by the GEMV from their fp32 rows
+    if ((rc = ensure_ws(ws, f8_bytes(main_n, cols), s))) return rc;
+    Carve cv{static_cast<char *>(ws.b->p)};
+    uint8_t *xp = cv.take<uint8_t>((size_t)main_n * nb * 64);
+    float *d = cv.take<float>((size_t)main_n * nb);
+    KQ4_HIP((hipError_t)kq4_launch_quantize(x, reinterpret_cast<int8_t *>(xp), d, nullptr, main_n,
+                                            cols, 0, s, 2, xu));
+    for (int i = 0; i < n_mats; ++i)
+      KQ4_HIP((hipError_t)kq4_launch_gemm_f8(out[i], res ? res[i] : nullptr, w[i], xp, d,
+                                             rows[i], cols, main_n, main_chain, ds->ncu, s));
+    if (!tail) return KQ4_OK;
+    float *o2[KQ4_MAX_MATS];
+    const float *r2[KQ4_MAX_MATS];
+    for (int i = 0; i < n_mats; ++i) {
+      o2[i] = out[i] + (size_t)main_n * rows[i];
+      r2[i] = (res && res[i]) ? res[i] + (size_t)main_n * rows[i] : nullptr;
+    }
+    return run_gemv(ds, ws, n_mats, o2, r2, w, rows, cols, x + (size_t)main_n * cols,
+                    xu ? xu + (size_t)main_n * cols : nullptr, nullptr, nullptr, tail, 0, s);
+  }
   if ((rc = ensure_ws(ws, qbytes, s))) return rc;
   Carve cv{static_cast<char *>(ws.b->p)};
   KQ4GemmAct act;
@@ -642,7 +668,8 @@ size_t kq4_matmul_workspace_bytes(int n_batch, int cols) {
   if (n_batch < 0 || cols <= 0 || cols % 32) return 0;
   // quantized activations, the one-token RMSNorm row, the split-K GEMV's partial sums (at most
   // one float per output row, token and K stage)
-  return kCntBytes + qa_bytes(n_batch, cols) + al256((size_t)cols * sizeof(float)) +
+  const size_t q = qa_bytes(n_batch, cols), f = f8_bytes(n_batch, cols);
+  return kCntBytes + (q > f ? q : f) + al256((size_t)cols * sizeof(float)) +
          (n_batch <= KQ4_GEMV_MAX_M ? gemv_part_bound(n_batch, cols) : 0);
 }
 
@@ -780,8 +807,8 @@ int kq4_matmul_noalloc_dev(float *out, const float *x, const float *residual, co
                            int rows, int cols, int n_batch, int chain, void *stream) {
   if (!x && n_batch) return fail(KQ4_EINVAL, "null x");
   const size_t need = n_batch > 0 && cols > 0 && cols % 32 == 0
-                         ? kCntBytes + qa_bytes(n_batch, cols) +
-                               (n_batch <= KQ4_GEMV_MAX_M ? kPartMax : 0)
+                         ? kCntBytes + (n_batch <= KQ4_GEMV_MAX_M ? qa_bytes(n_batch, cols) + kPartMax
+                                                                  : f8_bytes(n_batch, cols))
                          : 0;
   if (need > (size_t)KQ4_NOALLOC_SCRATCH_BYTES)
     return fail(KQ4_EINVAL, "matmul_noalloc: %d tokens x %d columns need %zu B of scratch; the "

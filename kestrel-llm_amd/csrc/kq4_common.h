@@ -127,6 +127,65 @@ KQ4_DEV int kq4_dot4(uint32_t a, uint32_t b, int c) {
   return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
 }
 
+// ---- fp8 (OCP e4m3) operands of the prefill GEMM -------------------------------------------
+// The GEMM's matrix-core operands hold small integers exactly in e4m3 (sign, 4 exponent bits with
+// bias 7, 3 mantissa bits): weights w = n - 8 in [-8, 7]; activations q in [-127, 127] split as
+// q = 16*qh + ql with qh = q >> 4 in [-8, 7] and ql = q & 15 in [0, 15], entering as 16*qh and
+// ql. Every product and every partial sum of a block is an integer below 2^24, so the fp32
+// result of the fp8 MFMA is the exact block sum S.
+// e4m3 bytes of v = -8 .. 7 (index v + 8): the low 8 and the high 8 of the table.
+#define KQ4_E4M3_NEG 0xb8c0c4c8caccced0ull   // v = -8 .. -1
+#define KQ4_E4M3_POS 0x4e4c4a4844403800ull   // v =  0 ..  7
+
+// e4m3 byte of the integer v in [-8, 7].
+KQ4_DEV uint32_t kq4_e4m3_i4(int v) {
+  const uint64_t t = v < 0 ? KQ4_E4M3_NEG : KQ4_E4M3_POS;
+  return (uint32_t)(t >> (8 * (v & 7))) & 0xFFu;
+}
+
+// e4m3 bytes of 16*qh and ql for an int8 code q (16*qh is qh's e4m3 with the exponent 4 higher;
+// ql >= 8 lies in the binade [8, 16) whose step is 1: byte 0x48 + ql).
+KQ4_DEV uint32_t kq4_e4m3_hi(int q) {
+  const int qh = q >> 4;
+  return qh ? kq4_e4m3_i4(qh) + 0x20u : 0u;
+}
+KQ4_DEV uint32_t kq4_e4m3_lo(int q) {
+  const int ql = q & 15;
+  return ql < 8 ? kq4_e4m3_i4(ql) : 0x48u + (uint32_t)ql;
+}
+
+// The e4m3 bytes of the four 4-bit two's complement codes in the low nibbles of t's bytes (t's
+// high nibbles zero): a byte permute picks each from the table of its sign, a third one the
+// right table per byte.
+KQ4_DEV uint32_t kq4_e4m3_nib4(uint32_t t) {
+  const uint32_t pos = __builtin_amdgcn_perm((uint32_t)(KQ4_E4M3_POS >> 32), (uint32_t)KQ4_E4M3_POS, t);
+  const uint32_t neg = __builtin_amdgcn_perm((uint32_t)(KQ4_E4M3_NEG >> 32), (uint32_t)KQ4_E4M3_NEG,
+                                             t & 0x07070707u);
+  const uint32_t sel = ((t >> 1) & 0x04040404u) | 0x03020100u;   // byte k: k (pos) or 4 + k (neg)
+  return __builtin_amdgcn_perm(neg, pos, sel);
+}
+
+// ---- raw buffer loads -------------------------------------------------------------------------
+// Loads through a buffer resource of `bytes` bytes: the hardware's range check returns zeros for
+// offsets at or past the end, so loads of tiles that overhang a matrix need no branches (an
+// offset of KQ4_OOB reads zeros too).
+#define KQ4_OOB 0xFFFFFFF0u
+KQ4_DEV __amdgpu_buffer_rsrc_t kq4_rsrc(const void *p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes,
+                                           0x00020000);   // gfx9 raw buffer, 32-bit data
+}
+KQ4_DEV uint4 kq4_bload16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+  return make_uint4((uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3]);
+}
+KQ4_DEV uint2 kq4_bload8(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+  return make_uint2((uint32_t)v[0], (uint32_t)v[1]);
+}
+KQ4_DEV uint32_t kq4_bload4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+}
+
 // ---- stream layout of the device weights -------------------------------------------------
 // A q4 matrix lives in HBM as 9216-B chunks, one per (32-row set, 16-block stage), in
 // [set][stage] order. In a chunk, "lane" l = row + 32*h (row = row within the set, h = half of

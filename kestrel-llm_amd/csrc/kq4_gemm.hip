@@ -32,6 +32,8 @@
 
 typedef int kq4_v4i __attribute__((ext_vector_type(4)));
 typedef int kq4_v16i __attribute__((ext_vector_type(16)));
+typedef float kq4_v16f __attribute__((ext_vector_type(16)));
+typedef float kq4_v32f __attribute__((ext_vector_type(32)));
 
 #define KQ4_GEMM_KB 4
 #define KQ4_LDS_ROW 48
@@ -45,7 +47,8 @@ KQ4_DEV int kq4_mfma_tok(int v, int half) { return 8 * (v >> 2) + 4 * half + (v 
 template <int CHAIN, int TM, int TN, int WF>
 __global__ __launch_bounds__(256, 2) void kq4_gemm_kernel(
     float *__restrict__ out, const float *__restrict__ res, const uint8_t *__restrict__ w,
-    const KQ4GemmAct act, int rows, int n_tok, int nb, int nst, int mtiles, int ntiles) {
+    const KQ4GemmAct act, int rows, int n_tok, int nb, int nst, int mtiles, int ntiles,
+    uint32_t wbytes) {
   constexpr int KQ4_GEMM_BM = 64 * TM, KQ4_GEMM_BN = 64 * TN;
   __shared__ __align__(16) int8_t sA[KQ4_GEMM_KB][KQ4_GEMM_BM * KQ4_LDS_ROW];
   __shared__ __align__(16) int8_t sB[KQ4_GEMM_KB][KQ4_GEMM_BN * KQ4_LDS_ROW];
@@ -94,44 +97,49 @@ __global__ __launch_bounds__(256, 2) void kq4_gemm_kernel(
     uint2 sw;
     float x[KQ4_GEMM_KB * KQ4_GEMM_BM / 256];
   };
+  // Buffer loads (kq4_rsrc): tokens past n_tok, row sets past the matrix and blocks past nb read
+  // zeros without branches. The stream layouts hold zero codes and zero scales for the blocks
+  // between nb and the end of their last stage, so a stage that overhangs K contributes
+  // fma(0, 0, acc) = acc (acc is never -0: it starts at +0 and RN sums are -0 only when both
+  // addends are), and the compute needs no per-block bound.
+  const __amdgpu_buffer_rsrc_t ra = kq4_rsrc(
+      act.xq, (uint32_t)((n_tok - 1) * act.q_ts + (long)(nb - 1) * act.q_bs + 32));
+  const __amdgpu_buffer_rsrc_t rx = kq4_rsrc(
+      act.xd, (uint32_t)(((n_tok - 1) * act.d_ts + (long)(nb - 1) * act.d_bs + 1) * 4));
+  const __amdgpu_buffer_rsrc_t rw = kq4_rsrc(w, wbytes);
   auto load = [&](Regs &rg, int b0) {
 #pragma unroll
     for (int u = 0; u < KQ4_GEMM_KB; ++u) {
       const int tok = t >> 1, hh = t & 1;
-      const int b = b0 + u;
-      rg.a[u] = make_uint4(0, 0, 0, 0);
-      if (tok < KQ4_GEMM_BM && b < nb && m0 + tok < n_tok)
-        rg.a[u] = *reinterpret_cast<const uint4 *>(act.xq + (long)(m0 + tok) * act.q_ts +
-                                                   (long)b * act.q_bs + hh * 16);
+      const bool ok = tok < KQ4_GEMM_BM && b0 + u < nb && m0 + tok < n_tok;
+      rg.a[u] = kq4_bload16(
+          ra, ok ? (uint32_t)((m0 + tok) * act.q_ts + (long)(b0 + u) * act.q_bs + hh * 16) : KQ4_OOB);
     }
 #pragma unroll
     for (int u = 0; u < NB; ++u) {
       const int idx = t + 256 * u;
+      uint32_t off;
       if (WF) {   // (set sl, block iu of the stage, lane ln): 16 int8 codes
         const int ln = idx & 63, iu = (idx >> 6) & 3, sl = idx >> 8;
         const int rl = 32 * sl + (ln & 31), h = ln >> 5;
-        rg.b[u] = make_uint4(0, 0, 0, 0);
-        if (n0 + 32 * sl < rows)
-          rg.b[u] = *reinterpret_cast<const uint4 *>(w + kq8_stream_code(n0 + rl, b0 + iu, h, nst));
+        off = n0 + 32 * sl < rows ? (uint32_t)kq8_stream_code(n0 + rl, b0 + iu, h, nst) : KQ4_OOB;
       } else {    // (set sl, nibble unit iu = 2 blocks, lane ln)
         const int ln = idx & 63, iu = (idx >> 6) & 1, sl = idx >> 7;
         const int rl = 32 * sl + (ln & 31), h = ln >> 5;
-        rg.b[u] = make_uint4(0, 0, 0, 0);          // row sets past the matrix: weight 0
-        if (n0 + 32 * sl < rows)
-          rg.b[u] = *reinterpret_cast<const uint4 *>(w + kq4_stream_nib(n0 + rl, b0 + 2 * iu, h, nst));
+        off = n0 + 32 * sl < rows ? (uint32_t)kq4_stream_nib(n0 + rl, b0 + 2 * iu, h, nst) : KQ4_OOB;
       }
+      rg.b[u] = kq4_bload16(rw, off);   // row sets past the matrix: weight 0
     }
-    rg.sw = make_uint2(0, 0);
-    if (t < KQ4_GEMM_BN && n0 + (t & ~31) < rows)
-      rg.sw = *reinterpret_cast<const uint2 *>(
-          w + (WF ? kq8_stream_scale(n0 + t, b0, nst) : kq4_stream_scale(n0 + t, b0, nst)));
+    const bool sok = t < KQ4_GEMM_BN && n0 + (t & ~31) < rows;
+    const uint32_t so = (uint32_t)(WF ? kq8_stream_scale(n0 + t, b0, nst) : kq4_stream_scale(n0 + t, b0, nst));
+    rg.sw = kq4_bload8(rw, sok ? so : KQ4_OOB);
 #pragma unroll
     for (int u = 0; u < KQ4_GEMM_KB * KQ4_GEMM_BM / 256; ++u) {
       const int c = t + 256 * u;
       const int bl = c / KQ4_GEMM_BM, tok = c % KQ4_GEMM_BM;
-      const int b = b0 + bl;
-      rg.x[u] = 0.0f;
-      if (b < nb && m0 + tok < n_tok) rg.x[u] = act.xd[(long)(m0 + tok) * act.d_ts + (long)b * act.d_bs];
+      const bool ok = b0 + bl < nb && m0 + tok < n_tok;
+      rg.x[u] = __uint_as_float(kq4_bload4(
+          rx, ok ? (uint32_t)(((m0 + tok) * act.d_ts + (long)(b0 + bl) * act.d_bs) * 4) : KQ4_OOB));
     }
   };
   auto store = [&](const Regs &rg) {
@@ -189,35 +197,41 @@ __global__ __launch_bounds__(256, 2) void kq4_gemm_kernel(
     // ---- compute: per block, 2 x 2 MFMA tiles per wave + exact per-block epilogue
 #pragma unroll
     for (int bl = 0; bl < KQ4_GEMM_KB; ++bl) {
-      if (b0 + bl >= nb) break;
       kq4_v4i af[TM], bf[TN];
-      float wdv[TN];
-      float xsv[TM][16];
 #pragma unroll
-      for (int i = 0; i < TM; ++i) {
+      for (int i = 0; i < TM; ++i)
         af[i] = *reinterpret_cast<const kq4_v4i *>(
             &sA[bl][(32 * TM * wm + 32 * i + l32) * KQ4_LDS_ROW + 16 * half]);
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const float4 x4 = *reinterpret_cast<const float4 *>(
-              &sX[bl][32 * TM * wm + 32 * i + 8 * q + 4 * half]);
-          xsv[i][4 * q + 0] = x4.x;
-          xsv[i][4 * q + 1] = x4.y;
-          xsv[i][4 * q + 2] = x4.z;
-          xsv[i][4 * q + 3] = x4.w;
-        }
-      }
-#pragma unroll
-      for (int jn = 0; jn < TN; ++jn) {
+      for (int jn = 0; jn < TN; ++jn)
         bf[jn] = *reinterpret_cast<const kq4_v4i *>(
             &sB[bl][(32 * TN * wn + 32 * jn + l32) * KQ4_LDS_ROW + 16 * half]);
-        wdv[jn] = sW[bl][32 * TN * wn + 32 * jn + l32];
+      // Scale products fl(wd * xs) from the matrix core: v_mfma_f32_32x32x1_2b_f32 is a rank-1
+      // update of two 32 x 32 blocks, each output one product rounded once (with a zero
+      // addend), in the MFMA output layout. With two token tiles its blocks are the tiles of
+      // one row tile (one product set per jn); with one token tile they are the two row tiles.
+      const kq4_v32f z32 = {0};
+      kq4_v32f sc[TM == 2 ? TN : 1];
+      if constexpr (TM == 2) {
+        const float xv = sX[bl][64 * wm + lane];
+#pragma unroll
+        for (int jn = 0; jn < TN; ++jn)
+          sc[jn] = __builtin_amdgcn_mfma_f32_32x32x1f32(
+              xv, sW[bl][32 * TN * wn + 32 * jn + l32], z32, 0, 0, 0);
+      } else {
+        const float xv = sX[bl][32 * wm + l32];
+        const float wv = sW[bl][32 * TN * wn + (TN == 2 ? lane : l32)];
+        sc[0] = __builtin_amdgcn_mfma_f32_32x32x1f32(xv, wv, z32, 0, 0, 0);
       }
       const kq4_v16i zero = {0};
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int jn = 0; jn < TN; ++jn) {
+          auto cs = [&](int v) {
+            if constexpr (TM == 2) return sc[jn % (TM == 2 ? TN : 1)][16 * i + v];
+            else return sc[0][16 * jn + v];
+          };
           if (CHAIN == KQ4_CHAIN_CTILE) {
             // lane half 0 carries elements 0..15 (low nibbles), half 1 elements 16..31
             const kq4_v4i z = {0, 0, 0, 0};
@@ -227,18 +241,17 @@ __global__ __launch_bounds__(256, 2) void kq4_gemm_kernel(
             const kq4_v16i chi = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bhi, zero, 0, 0, 0);
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
-              const float sc = wdv[jn] * xsv[i][v];
-              acc[i][jn][v] = fmaf((float)clo[v], sc, acc[i][jn][v]);
-              acc_hi[i][jn][v] = fmaf((float)chi[v], sc, acc_hi[i][jn][v]);
+              acc[i][jn][v] = fmaf((float)clo[v], cs(v), acc[i][jn][v]);
+              acc_hi[i][jn][v] = fmaf((float)chi[v], cs(v), acc_hi[i][jn][v]);
             }
           } else {
             const kq4_v16i c = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[jn], zero, 0, 0, 0);
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
               if (CHAIN == KQ4_CHAIN_Q8GEMM)
-                acc[i][jn][v] = acc[i][jn][v] + (wdv[jn] * xsv[i][v]) * (float)c[v];
+                acc[i][jn][v] = acc[i][jn][v] + cs(v) * (float)c[v];
               else
-                acc[i][jn][v] = fmaf((float)c[v], wdv[jn] * xsv[i][v], acc[i][jn][v]);
+                acc[i][jn][v] = fmaf((float)c[v], cs(v), acc[i][jn][v]);
             }
           }
         }
@@ -264,33 +277,272 @@ __global__ __launch_bounds__(256, 2) void kq4_gemm_kernel(
     }
 }
 
+// ---- fp8 formulation (ASM and GEMV32 chains over q4 weights) -----------------------------
+// The block sums come from v_mfma_f32_32x32x64_f8f6f4 on exactly representable integers (see
+// kq4_common.h): A = the activations' operand pairs [16*qh | ql] (64 e4m3 bytes per token and
+// block, written by the quantizer), B = [w | w] (the weights' 32 e4m3 bytes, read by both lane
+// halves), so the MFMA's fp32 result is S itself, exact; the scale products fl(wd * xs) of a
+// 32 x 32 tile come from v_mfma_f32_32x32x1_2b_f32 as outer products (one product per output,
+// rounded once: exactly the VALU's fl(wd * xs)); each output then takes one fma per block:
+// acc = fma(S, fl(wd * xs), acc), the same chain as the int8 kernel above, bit for bit. One
+// 32 x 32 tile per block costs 64 + 32 matrix-core cycles and 16 VALU fmas, against 32 and 48
+// (convert, product, fma) for the int8 form, so the VALU no longer bounds the kernel.
+// Stages of 2 blocks, double-buffered in LDS (one barrier per stage): activations 64 B per
+// (token, block) at an 80-B pitch, weights unpacked to e4m3 when stored (kq4_e4m3_nib4) at a
+// 48-B pitch, f32 row and token scales.
+#define KQ4_F8_KB 2
+#define KQ4_F8_AP 80
+#define KQ4_F8_BP 48
+
+typedef int kq4_v8i __attribute__((ext_vector_type(8)));
+KQ4_DEV kq4_v8i kq4_lds8(const uint8_t *p) {
+  const uint4 u0 = *reinterpret_cast<const uint4 *>(p);
+  const uint4 u1 = *reinterpret_cast<const uint4 *>(p + 16);
+  return kq4_v8i{(int)u0.x, (int)u0.y, (int)u0.z, (int)u0.w,
+                 (int)u1.x, (int)u1.y, (int)u1.z, (int)u1.w};
+}
+
+template <int CHAIN, int TM, int TN>
+__global__ __launch_bounds__(256, 2) void kq4_gemm_f8_kernel(
+    float *__restrict__ out, const float *__restrict__ res, const uint8_t *__restrict__ w,
+    const uint8_t *__restrict__ xp, const float *__restrict__ xd, int rows, int n_tok, int nb,
+    int nst, int mtiles, int ntiles, long wbytes) {
+  constexpr int BM = 64 * TM, BN = 64 * TN;
+  constexpr int NA = BM / 32;   // 16-B activation pieces per thread and stage
+  __shared__ __align__(16) uint8_t sA[2][KQ4_F8_KB][BM * KQ4_F8_AP];
+  __shared__ __align__(16) uint8_t sB[2][KQ4_F8_KB][BN * KQ4_F8_BP];
+  __shared__ __align__(16) float sX[2][KQ4_F8_KB][BM];
+  __shared__ __align__(16) float sW[2][KQ4_F8_KB][BN];
+
+  // XCD-aware tile order, as the int8 kernel
+  const int ntile = mtiles * ntiles;
+  const int wg = blockIdx.x;
+  const int xcd = wg & 7, q8 = ntile >> 3, r8 = ntile & 7;
+  const int tile = xcd * q8 + (xcd < r8 ? xcd : r8) + (wg >> 3);
+  const int m0 = (tile % mtiles) * BM;
+  const int n0 = (tile / mtiles) * BN;
+  const int t = threadIdx.x;
+  const int lane = t & 63;
+  const int wave = t >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int l32 = lane & 31, half = lane >> 5;
+
+  float acc[TM][TN][16];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+
+  struct Regs {
+    uint4 a[NA];
+    uint4 b;
+    uint32_t sw;
+    float x0, x1;
+  };
+  // global -> registers for the stage at block b0 (even): activation pieces (token idx >> 3,
+  // block (idx >> 2) & 1, 16-B piece idx & 3); one stream-layout unit per thread of the first
+  // 2 * BN (row set t >> 6, lane t & 63: the half-row of blocks b0 and b0 + 1); row scales (the
+  // two f16 of blocks b0, b0 + 1, adjacent) for t < BN, token scales for t in [128, 128 + BM)
+  // Buffer loads (kq4_rsrc): tokens past n_tok, rows past the matrix and the block past an odd
+  // nb read zeros without branches.
+  const __amdgpu_buffer_rsrc_t ra = kq4_rsrc(xp, (uint32_t)((size_t)n_tok * nb * 64));
+  const __amdgpu_buffer_rsrc_t rw = kq4_rsrc(w, (uint32_t)wbytes);
+  const __amdgpu_buffer_rsrc_t rx = kq4_rsrc(xd, (uint32_t)((size_t)n_tok * nb * 4));
+  auto load = [&](Regs &rg, int b0) {
+#pragma unroll
+    for (int u = 0; u < NA; ++u) {
+      const int idx = t + 256 * u;
+      const int tok = idx >> 3, bl = (idx >> 2) & 1, pc = idx & 3;
+      const uint32_t off =
+          b0 + bl < nb ? ((uint32_t)(m0 + tok) * nb + b0 + bl) * 64u + 16u * pc : KQ4_OOB;
+      rg.a[u] = kq4_bload16(ra, off);
+    }
+    rg.b = kq4_bload16(rw, t < 2 * BN ? (uint32_t)kq4_stream_nib(n0 + 32 * (t >> 6) + (lane & 31),
+                                                                  b0, lane >> 5, nst)
+                                       : KQ4_OOB);
+    rg.sw = kq4_bload4(rw, t < BN ? (uint32_t)kq4_stream_scale(n0 + t, b0, nst) : KQ4_OOB);
+    const int tok = t - 128;
+    const uint32_t xo = ((uint32_t)(m0 + tok) * nb + b0) * 4u;
+    const bool xt = t >= 128 && t < 128 + BM;
+    rg.x0 = __uint_as_float(kq4_bload4(rx, xt ? xo : KQ4_OOB));
+    rg.x1 = __uint_as_float(kq4_bload4(rx, xt && b0 + 1 < nb ? xo + 4 : KQ4_OOB));
+  };
+  auto store = [&](const Regs &rg, int buf) {
+#pragma unroll
+    for (int u = 0; u < NA; ++u) {
+      const int idx = t + 256 * u;
+      const int tok = idx >> 3, bl = (idx >> 2) & 1, pc = idx & 3;
+      *reinterpret_cast<uint4 *>(&sA[buf][bl][tok * KQ4_F8_AP + 16 * pc]) = rg.a[u];
+    }
+    if (t < 2 * BN) {
+      const int row = 32 * (t >> 6) + (lane & 31), h = lane >> 5;
+      // dword d of a block's half-row: low nibbles = elements 8d .. 8d+3, high = 8d+4 .. 8d+7
+      const uint32_t d[4] = {rg.b.x, rg.b.y, rg.b.z, rg.b.w};
+#pragma unroll
+      for (int bl = 0; bl < 2; ++bl) {
+        uint4 o;
+        o.x = kq4_e4m3_nib4(d[2 * bl] & 0x0F0F0F0Fu);
+        o.y = kq4_e4m3_nib4((d[2 * bl] >> 4) & 0x0F0F0F0Fu);
+        o.z = kq4_e4m3_nib4(d[2 * bl + 1] & 0x0F0F0F0Fu);
+        o.w = kq4_e4m3_nib4((d[2 * bl + 1] >> 4) & 0x0F0F0F0Fu);
+        *reinterpret_cast<uint4 *>(&sB[buf][bl][row * KQ4_F8_BP + 16 * h]) = o;
+      }
+    }
+    if (t < BN) {
+      sW[buf][0][t] = kq4_h2f(rg.sw);
+      sW[buf][1][t] = kq4_h2f(rg.sw >> 16);
+    } else if (t >= 128 && t < 128 + BM) {
+      // ASM chain: the reference multiplies by the f16-rounded activation scale
+      sX[buf][0][t - 128] = CHAIN == KQ4_CHAIN_ASM ? kq4_f16_round(rg.x0) : rg.x0;
+      sX[buf][1][t - 128] = CHAIN == KQ4_CHAIN_ASM ? kq4_f16_round(rg.x1) : rg.x1;
+    }
+  };
+  auto compute = [&](int buf, int b0) {
+#pragma unroll
+    for (int bl = 0; bl < KQ4_F8_KB; ++bl) {
+      if (b0 + bl >= nb) break;
+      kq4_v8i a[TM], bq[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+        a[i] = kq4_lds8(&sA[buf][bl][(32 * TM * wm + 32 * i + l32) * KQ4_F8_AP + 32 * half]);
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        bq[j] = kq4_lds8(&sB[buf][bl][(32 * TN * wn + 32 * j + l32) * KQ4_F8_BP]);
+      const kq4_v32f z32 = {0};
+      const kq4_v16f z16 = {0};
+      if constexpr (TM == 2) {
+        // the outer product's two blocks are the wave's two token tiles (lanes 0-31, 32-63)
+        const float xv = sX[buf][bl][64 * wm + lane];
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          const float wv = sW[buf][bl][32 * TN * wn + 32 * j + l32];
+          const kq4_v32f c = __builtin_amdgcn_mfma_f32_32x32x1f32(xv, wv, z32, 0, 0, 0);
+#pragma unroll
+          for (int i = 0; i < 2; ++i) {
+            const kq4_v16f sb =
+                __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a[i], bq[j], z16, 0, 0, 0, 0, 0, 0);
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[i][j][v] = fmaf(sb[v], c[16 * i + v], acc[i][j][v]);
+          }
+        }
+      } else {
+        // one token tile: the outer product's two blocks are the wave's row tiles
+        const float xv = sX[buf][bl][32 * wm + l32];
+        const float wv = sW[buf][bl][32 * TN * wn + (TN == 2 ? lane : l32)];
+        const kq4_v32f c = __builtin_amdgcn_mfma_f32_32x32x1f32(xv, wv, z32, 0, 0, 0);
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          const kq4_v16f sb =
+              __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a[0], bq[j], z16, 0, 0, 0, 0, 0, 0);
+#pragma unroll
+          for (int v = 0; v < 16; ++v) acc[0][j][v] = fmaf(sb[v], c[16 * j + v], acc[0][j][v]);
+        }
+      }
+    }
+  };
+
+  Regs rg;
+  load(rg, 0);
+  store(rg, 0);
+  __syncthreads();
+  int buf = 0;
+  for (int b0 = 0; b0 < nb; b0 += KQ4_F8_KB) {
+    const bool more = b0 + KQ4_F8_KB < nb;
+    if (more) load(rg, b0 + KQ4_F8_KB);   // in flight during the compute
+    compute(buf, b0);
+    if (more) store(rg, buf ^ 1);         // the other buffer: nobody reads it this stage
+    __syncthreads();
+    buf ^= 1;
+  }
+
+  // out = [res +] acc
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int row = n0 + 32 * TN * wn + 32 * j + l32;
+      if (row >= rows) continue;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int tok = m0 + 32 * TM * wm + 32 * i + kq4_mfma_tok(v, half);
+        if (tok >= n_tok) continue;
+        const size_t o = (size_t)tok * rows + row;
+        out[o] = res ? res[o] + acc[i][j][v] : acc[i][j][v];
+      }
+    }
+}
+
+template <int TM, int TN>
+static hipError_t gemm_f8_launch(float *out, const float *res, const uint8_t *w, const uint8_t *xp,
+                                 const float *xd, int rows, int n_tok, int nb, int nst, int chain,
+                                 hipStream_t s) {
+  const int mtiles = (n_tok + 64 * TM - 1) / (64 * TM);
+  const int ntiles = (rows + 64 * TN - 1) / (64 * TN);
+  const dim3 grid((unsigned)(mtiles * ntiles));
+  const long wbytes = (long)kq4_stream_bytes(rows, nb * 32);
+  if (chain == KQ4_CHAIN_ASM)
+    hipLaunchKernelGGL((kq4_gemm_f8_kernel<KQ4_CHAIN_ASM, TM, TN>), grid, dim3(256), 0, s, out, res,
+                       w, xp, xd, rows, n_tok, nb, nst, mtiles, ntiles, wbytes);
+  else if (chain == KQ4_CHAIN_GEMV32)
+    hipLaunchKernelGGL((kq4_gemm_f8_kernel<KQ4_CHAIN_GEMV32, TM, TN>), grid, dim3(256), 0, s, out,
+                       res, w, xp, xd, rows, n_tok, nb, nst, mtiles, ntiles, wbytes);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+int kq4_launch_gemm_f8(float *out, const float *res, const uint8_t *w, const uint8_t *xp,
+                       const float *xd, int rows, int cols, int n_tok, int chain, int ncu,
+                       hipStream_t s) {
+  const int nb = cols / 32;
+  const int nst = (nb + KQ4_STREAM_CB - 1) / KQ4_STREAM_CB;
+  if (n_tok <= 0 || rows <= 0) return 0;
+  if (chain != KQ4_CHAIN_ASM && chain != KQ4_CHAIN_GEMV32) return (int)hipErrorInvalidValue;
+  // 32-bit buffer offsets: operand pairs and weights below 4 GB
+  if (((size_t)n_tok + 128) * nb * 64 >= KQ4_OOB || kq4_stream_bytes(rows, cols) >= KQ4_OOB)
+    return (int)hipErrorInvalidValue;
+  auto tiles = [&](int bm, int bn) {
+    return (long)((n_tok + bm - 1) / bm) * ((rows + bn - 1) / bn);
+  };
+  static const int force = [] { const char *e = getenv("KQ4_GEMM_TILE"); return e ? atoi(e) : 0; }();
+  const int pick = force >= 1 && force <= 3 ? force
+                   : tiles(128, 128) >= 2L * ncu ? 1 : (tiles(64, 128) >= 2L * ncu ? 2 : 3);
+  hipError_t e;
+  if (pick == 1) e = gemm_f8_launch<2, 2>(out, res, w, xp, xd, rows, n_tok, nb, nst, chain, s);
+  else if (pick == 2) e = gemm_f8_launch<1, 2>(out, res, w, xp, xd, rows, n_tok, nb, nst, chain, s);
+  else e = gemm_f8_launch<1, 1>(out, res, w, xp, xd, rows, n_tok, nb, nst, chain, s);
+  return (int)e;
+}
+
 template <int TM, int TN>
 static hipError_t gemm_launch(float *out, const float *res, const uint8_t *w,
                               const KQ4GemmAct &act, int rows, int n_tok, int nb, int nst,
-                              int chain, int wf, hipStream_t s) {
+                              int chain, int wf, uint32_t wbytes, hipStream_t s) {
   const int mtiles = (n_tok + 64 * TM - 1) / (64 * TM);
   const int ntiles = (rows + 64 * TN - 1) / (64 * TN);
   const dim3 grid((unsigned)(mtiles * ntiles));
   if (wf) {
     if (chain == KQ4_CHAIN_GEMV32)
       hipLaunchKernelGGL((kq4_gemm_kernel<KQ4_CHAIN_GEMV32, TM, TN, 1>), grid, dim3(256), 0, s,
-                         out, res, w, act, rows, n_tok, nb, nst, mtiles, ntiles);
+                         out, res, w, act, rows, n_tok, nb, nst, mtiles, ntiles, wbytes);
     else if (chain == KQ4_CHAIN_Q8GEMM)
       hipLaunchKernelGGL((kq4_gemm_kernel<KQ4_CHAIN_Q8GEMM, TM, TN, 1>), grid, dim3(256), 0, s,
-                         out, res, w, act, rows, n_tok, nb, nst, mtiles, ntiles);
+                         out, res, w, act, rows, n_tok, nb, nst, mtiles, ntiles, wbytes);
     else
       return hipErrorInvalidValue;
   } else if (chain == KQ4_CHAIN_CTILE) {
     if constexpr (TM == 2 && TN == 2) return hipErrorInvalidValue;   // capped by the planner
     else
       hipLaunchKernelGGL((kq4_gemm_kernel<KQ4_CHAIN_CTILE, TM, TN, 0>), grid, dim3(256), 0, s,
-                         out, res, w, act, rows, n_tok, nb, nst, mtiles, ntiles);
+                         out, res, w, act, rows, n_tok, nb, nst, mtiles, ntiles, wbytes);
   } else if (chain == KQ4_CHAIN_GEMV32) {
     hipLaunchKernelGGL((kq4_gemm_kernel<KQ4_CHAIN_GEMV32, TM, TN, 0>), grid, dim3(256), 0, s, out,
-                       res, w, act, rows, n_tok, nb, nst, mtiles, ntiles);
+                       res, w, act, rows, n_tok, nb, nst, mtiles, ntiles, wbytes);
   } else if (chain == KQ4_CHAIN_ASM) {
     hipLaunchKernelGGL((kq4_gemm_kernel<KQ4_CHAIN_ASM, TM, TN, 0>), grid, dim3(256), 0, s, out,
-                       res, w, act, rows, n_tok, nb, nst, mtiles, ntiles);
+                       res, w, act, rows, n_tok, nb, nst, mtiles, ntiles, wbytes);
   } else {
     return hipErrorInvalidValue;
   }
@@ -314,9 +566,15 @@ int kq4_launch_gemm(float *out, const float *res, const uint8_t *w, const KQ4Gem
   int pick = force >= 1 && force <= 3 ? force
              : tiles(128, 128) >= 2L * ncu ? 1 : (tiles(64, 128) >= 2L * ncu ? 2 : 3);
   if (chain == KQ4_CHAIN_CTILE && pick == 1) pick = 2;
+  // 32-bit buffer offsets: weights and activation operands below 4 GB
+  const size_t wb = wf ? kq8_stream_bytes(rows, cols) : kq4_stream_bytes(rows, cols);
+  const long ab = (n_tok - 1) * act.q_ts + (long)(nb - 1) * act.q_bs + 32;
+  const long db = ((n_tok - 1) * act.d_ts + (long)(nb - 1) * act.d_bs + 1) * 4;
+  if (wb >= KQ4_OOB || ab >= (long)KQ4_OOB || db >= (long)KQ4_OOB) return (int)hipErrorInvalidValue;
+  const uint32_t wbytes = (uint32_t)wb;
   hipError_t e;
-  if (pick == 1) e = gemm_launch<2, 2>(out, res, w, act, rows, n_tok, nb, nst, chain, wf, s);
-  else if (pick == 2) e = gemm_launch<1, 2>(out, res, w, act, rows, n_tok, nb, nst, chain, wf, s);
-  else e = gemm_launch<1, 1>(out, res, w, act, rows, n_tok, nb, nst, chain, wf, s);
+  if (pick == 1) e = gemm_launch<2, 2>(out, res, w, act, rows, n_tok, nb, nst, chain, wf, wbytes, s);
+  else if (pick == 2) e = gemm_launch<1, 2>(out, res, w, act, rows, n_tok, nb, nst, chain, wf, wbytes, s);
+  else e = gemm_launch<1, 1>(out, res, w, act, rows, n_tok, nb, nst, chain, wf, wbytes, s);
   return (int)e;
 }

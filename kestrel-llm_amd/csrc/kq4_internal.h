@@ -86,6 +86,13 @@ int kq4_launch_gemm(float *out, const float *res, const uint8_t *w, const KQ4Gem
                     int rows, int cols, int n_tok, int chain, int ncu, hipStream_t stream,
                     int wf = 0);
 
+// Prefill GEMM on fp8 matrix-core operands (ASM or GEMV32 chain, q4 weights, bit-identical to
+// kq4_launch_gemm): xp = the activations' e4m3 operand pairs [n_tok][cols/32][64] (the
+// quantizer's block_major = 2 output), xd their f32 scales [n_tok][cols/32].
+int kq4_launch_gemm_f8(float *out, const float *res, const uint8_t *w, const uint8_t *xp,
+                       const float *xd, int rows, int cols, int n_tok, int chain, int ncu,
+                       hipStream_t stream);
+
 // MoE
 int kq4_launch_moe_route(int *sel, float *pr, const float *logits, int T, int ne, int tk,
                          hipStream_t stream);

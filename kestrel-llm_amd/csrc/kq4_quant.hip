@@ -48,10 +48,25 @@ __global__ __launch_bounds__(256) void kq4_quantize_kernel(const float *__restri
     q = q > 127 ? 127 : (q < -127 ? -127 : q);
     pk[i >> 2] |= ((uint32_t)q & 0xFFu) << (8 * (i & 3));
   }
-  // token-major [m][cols] / [m][nb], or block-major [b][m][32] / [b][m] for the GEMM
-  const size_t qo = block_major ? ((size_t)b * n_batch + m) * 32 + 8 * qq : off;
-  const size_t so = block_major ? (size_t)b * n_batch + m : (size_t)blk;
-  *reinterpret_cast<uint2 *>(xq + qo) = make_uint2(pk[0], pk[1]);
+  // token-major [m][cols] / [m][nb], block-major [b][m][32] / [b][m], or (block_major = 2) the
+  // fp8 GEMM's operand pairs [m][nb][64]: the e4m3 bytes of 16*(q >> 4) for the block's 32
+  // elements, then those of q & 15 (kq4_e4m3_hi / _lo), scales token-major
+  const size_t so = block_major == 1 ? (size_t)b * n_batch + m : (size_t)blk;
+  if (block_major == 2) {
+    uint32_t hi[2] = {0, 0}, lo[2] = {0, 0};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int q = (int)(int8_t)(pk[i >> 2] >> (8 * (i & 3)));
+      hi[i >> 2] |= kq4_e4m3_hi(q) << (8 * (i & 3));
+      lo[i >> 2] |= kq4_e4m3_lo(q) << (8 * (i & 3));
+    }
+    uint8_t *pair = reinterpret_cast<uint8_t *>(xq) + (size_t)blk * 64 + 8 * qq;
+    *reinterpret_cast<uint2 *>(pair) = make_uint2(hi[0], hi[1]);
+    *reinterpret_cast<uint2 *>(pair + 32) = make_uint2(lo[0], lo[1]);
+  } else {
+    const size_t qo = block_major ? ((size_t)b * n_batch + m) * 32 + 8 * qq : off;
+    *reinterpret_cast<uint2 *>(xq + qo) = make_uint2(pk[0], pk[1]);
+  }
   if (qq == 0) {
     xd[so] = d;
     if (xde) xde[so] = (m < asm_tokens) ? kq4_f16_round(d) : d;

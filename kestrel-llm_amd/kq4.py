@@ -421,7 +421,7 @@ def matmul_dev(out, x, w, rows, cols, residual=None, chain=CHAIN_AUTO, stream=No
                                _stream_ptr(stream)), "kq4_matmul_dev")
 
 
-NOALLOC_SCRATCH_BYTES = 32 << 20
+NOALLOC_SCRATCH_BYTES = 64 << 20
 
 
 def matmul_noalloc_dev(out, x, w, rows, cols, residual=None, chain=CHAIN_AUTO, stream=None):

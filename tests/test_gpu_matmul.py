@@ -148,24 +148,28 @@ def test_gemm_bit_exact(kq4, torch_dev, orc, n, chain):
 # 4-block stages with the next stage's registers prefetched, over two stream-layout stages (the
 # second one partial). The oracle is evaluated on sampled outputs: one per 64 x 64 cell (every
 # tile, every XCD's range), the last token and row, and random pairs.
+@pytest.mark.parametrize("kind", [0, 1])
 @pytest.mark.parametrize("n,rows,chain", [(2048, 4096, 0), (2048, 4096, 1), (2048, 4096, 3),
-                                          (2048, 2048, 2), (2048, 2048, 3)])
-def test_gemm_large_tiles_bit_exact(kq4, torch_dev, orc, n, rows, chain):
+                                          (2048, 2048, 2), (2048, 2048, 3), (300, 2048, 0)])
+def test_gemm_large_tiles_bit_exact(kq4, torch_dev, orc, n, rows, chain, kind):
+    """Both GEMM forms (planner option gemm_kind: 0 int8 MFMA, 1 fp8 operands; the C-tile chain
+    always takes the int8 one) are bit-identical to the oracle."""
     torch = torch_dev
     cols = 640
     w, x = case(rows, cols, n, 700 + rows + chain)
     out = torch.empty((n, rows), dtype=torch.float32, device="cuda")
-    kq4.matmul_dev(out, to_dev(torch, x), wdev(kq4, torch, w, rows, cols), rows, cols,
-                   chain=chain)
+    with kq4.options(gemm_kind=kind):
+        kq4.matmul_dev(out, to_dev(torch, x), wdev(kq4, torch, w, rows, cols), rows, cols,
+                       chain=chain)
     torch.cuda.synchronize()
     got = host(out)
     xq, xd = orc.quantize(x, cols)
     rng = np.random.default_rng(rows + chain)
     t0, r0 = np.meshgrid(np.arange(0, n, 64), np.arange(0, rows, 64), indexing="ij")
-    tok = np.concatenate([t0.ravel() + rng.integers(0, 64, t0.size), [n - 1] * 64,
-                          rng.integers(0, n, 2048)]).astype(np.int32)
-    row = np.concatenate([r0.ravel() + rng.integers(0, 64, r0.size), rng.integers(0, rows, 64),
-                          rng.integers(0, rows, 2048)]).astype(np.int32)
+    tok = np.concatenate([np.minimum(t0.ravel() + rng.integers(0, 64, t0.size), n - 1),
+                          [n - 1] * 64, rng.integers(0, n, 2048)]).astype(np.int32)
+    row = np.concatenate([np.minimum(r0.ravel() + rng.integers(0, 64, r0.size), rows - 1),
+                          rng.integers(0, rows, 64), rng.integers(0, rows, 2048)]).astype(np.int32)
     want = orc.matmul_q_sample(w, xq, xd, rows, cols, n, tok, row, chain=chain)
     assert np.array_equal(got[tok, row].view(np.uint32), want.view(np.uint32))
 

@@ -35,7 +35,7 @@ def run_both(kq4, torch, rows, cols, n, seed, residual):
 
 def test_noalloc_matches_matmul_dev(kq4, torch_dev):
     torch = torch_dev
-    # 1: prefill GEMM, 512 tokens x 4096 columns (2.4 MB of scratch)
+    # 1: prefill GEMM, 512 tokens x 4096 columns (4.5 MB of scratch)
     a, b = run_both(kq4, torch, 1024, 4096, 512, 11, residual=True)
     assert np.array_equal(bits(a), bits(b))
     # 2: smaller, right after: a 6-token GEMV from the separate quantizer launch
@@ -48,10 +48,11 @@ def test_noalloc_matches_matmul_dev(kq4, torch_dev):
 
 def test_noalloc_largest_fits_and_beyond_is_refused(kq4, torch_dev):
     torch = torch_dev
-    # 2048 tokens x 12288 columns (the Qwen3-8B down prefill): 28.3 MB, within the 32 MiB scratch
+    # 2048 tokens x 12288 columns (the Qwen3-8B down prefill): 53.5 MB of fp8 GEMM operands,
+    # within the 64 MiB scratch
     a, b = run_both(kq4, torch, 128, 12288, 2048, 41, residual=False)
     assert np.array_equal(bits(a), bits(b))
-    rows, cols, n = 128, 16384, 2048                     # 37.8 MB: refused
+    rows, cols, n = 128, 16384, 2048                     # 71.3 MB: refused
     w = torch.zeros(kq4.stream_bytes(rows, cols), dtype=torch.uint8, device="cuda")
     x = torch.empty((n, cols), dtype=torch.float32, device="cuda")
     out = torch.empty((n, rows), dtype=torch.float32, device="cuda")
