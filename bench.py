@@ -14,9 +14,12 @@ region.
 value = algorithmic bytes per step (weights N*K*18/32 + activations M*K*4 + outputs M*N*4 +
 residuals M*N*4) / step time, in GB/s. roofline: the dominant kernel (the fused gate/up GEMV,
 launched exactly as in the step, once per layer's weights), its launches captured back to back
-as a graph and replayed between HIP events on their stream, against MI355X HBM peak 8 TB/s. extras: BASELINE.json configs 3-5 (Qwen3-8B decode GEMVs, prefill GEMM,
-MoE FFN). cpu_baseline: the reference's own x86-64 path (oracle/_ref, built from
-/root/reference) on a bounded sample.
+as a graph and replayed between HIP events on their stream, against MI355X HBM peak 8 TB/s.
+extras: the other BASELINE.json configs, each with a roofline block per op (config 1 single
+GEMV, config 2 at M = 4, Qwen3-8B decode GEMVs, prefill GEMM against int8 dense peak, MoE FFN).
+cpu_baseline: the reference's own x86-64 code for every config (oracle/cpu_bench.py over
+oracle/_ref, built from /root/reference): median of >= 20 reps at all physical cores and at
+the reference's default thread count.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--m 1] [--no-cpu] [--no-extras]
     python bench.py --calibrate-copy      (512 MiB copy for PMC byte-counter scaling)
@@ -225,16 +228,53 @@ def _copies(torch, arr, rows, cols):
     return [t] + [t.clone() for _ in range(n - 1)]
 
 
-def run_extras():
-    """BASELINE.json configs 3-5 (reported beside the headline line, each on its own):
-    Qwen3-8B decode GEMVs at M in {1,2,4,8} (us/call, GB/s), prefill GEMM at M in {512, 2048}
-    (int8 TOPS vs 5.0 POPS dense), Qwen3-30B-A3B MoE FFN at T in {1, 64}. Every measured op
-    cycles through > 640 MB of distinct weight copies, so its weights stream from HBM; each is
-    timed as a graph replay (_time_graph)."""
+INT8_PEAK_TOPS = 5000.0
+
+
+def roof_hbm(byts, us):
+    a = byts / us / 1e3
+    return {"bound": "hbm", "achieved": round(a, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(a / HBM_PEAK_GBS, 4)}
+
+
+def roof_mfma(ops, us):
+    a = ops / us / 1e6
+    return {"bound": "mfma", "achieved": round(a, 1), "peak": INT8_PEAK_TOPS, "unit": "TOPS",
+            "frac": round(a / INT8_PEAK_TOPS, 4)}
+
+
+def run_extras(args):
+    """The other BASELINE.json configs, each with its own roofline block (reported beside the
+    headline line): config 1 (one 2B GEMV, M = 1), config 2 at M = 4 (the headline step),
+    config 3 (Qwen3-8B decode GEMVs at M in {1,2,4,8}: us/call, GB/s against HBM peak, per op),
+    config 4 (prefill GEMM at M in {512, 2048}: int8 TOPS against 5.0 POPS dense, per op) and
+    config 5 (Qwen3-30B-A3B MoE FFN at T in {1, 64}), plus the Q8_0 weight form. Every measured
+    op cycles through > 640 MB of distinct weight copies, so its weights stream from HBM; each
+    is timed as a graph replay between HIP events on its stream (_time_graph)."""
     import torch
 
     import kq4
 
+    out = {}
+    # config 1: one q4 GEMV, M = 1, K = 2048 -> N = 6144 (the 2B FFN up-projection)
+    rows1, cols1 = CFG["ffn"], CFG["hidden"]
+    W1 = _copies(torch, synth.make_q4_weights(rows1, cols1, 11, **synth.SCALE_2B), rows1, cols1)
+    x1 = torch.from_numpy(synth.make_activations(1, cols1, 7)).cuda()
+    o1 = torch.empty((1, rows1), device="cuda")
+    t1 = _time_graph(torch, lambda i, st: kq4.matmul_dev(o1, x1, W1[i], rows1, cols1, stream=st),
+                     len(W1))
+    b1 = rows1 * cols1 * 18 // 32 + cols1 * 4 + rows1 * 4
+    out["config1_gemv_m1"] = {"us_per_call": round(t1, 3), "bytes": b1, "roofline": roof_hbm(b1, t1)}
+    del W1
+    # config 2 at M = 4: the headline step (28 layers' linear sets, one graph replay per step)
+    g4 = run_gpu(argparse.Namespace(m=4, steps=max(10, args.steps // 2), warmup=args.warmup))
+    out["config2_step_m4"] = {"ms_per_step": round(g4["ms_per_step"], 4),
+                              "GBs": round(g4["value"], 1), "bytes_per_step": g4["total_bytes"],
+                              "roofline": {"bound": "hbm", "achieved": round(g4["value"], 1),
+                                           "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                           "frac": round(g4["value"] / HBM_PEAK_GBS, 4)},
+                              "gate_up_us_per_call": round(g4["us_gate_up"], 3)}
+    torch.cuda.empty_cache()
     cfg = synth.QWEN3_8B
     h, f = cfg["hidden"], cfg["ffn"]
     qkv = (cfg["q_heads"] + 2 * cfg["kv_heads"]) * cfg["head_dim"]
@@ -242,7 +282,6 @@ def run_extras():
     U = [g.clone() for g in G]
     D = _copies(torch, synth.make_q4_weights(h, f, 13, **synth.SCALE_8B), h, f)
     Q = _copies(torch, synth.make_q4_weights(qkv, h, 14, **synth.SCALE_8B), qkv, h)
-    out = {}
     dec = {}
     for m in (1, 2, 4, 8):
         x = torch.from_numpy(synth.make_activations(m, h, 20 + m)).cuda()
@@ -288,7 +327,9 @@ def run_extras():
             "silu_down_us": round(t_sd, 2),
             "silu_down_GBs": round((b_dn + m * f * 4) / t_sd / 1e3, 1),
             "silu_then_down_us": round(t_su, 2),
-            "rmsnorm_qkv_us": round(t_nq, 2), "rmsnorm_then_qkv_us": round(t_nu, 2)}
+            "rmsnorm_qkv_us": round(t_nq, 2), "rmsnorm_then_qkv_us": round(t_nu, 2),
+            "roofline_gate_up": roof_hbm(b_gu, t_gu), "roofline_down": roof_hbm(b_dn, t_dn),
+            "roofline_qkv": roof_hbm(b_q, t_q)}
     out["qwen3_8b_decode"] = dec
     pre = {}
     for m in (512, 2048):
@@ -304,7 +345,7 @@ def run_extras():
         ops = 2.0 * m * f * h
         pre[f"M{m}"] = {"gate_us": round(t_g, 1), "gate_TOPS": round(ops / t_g / 1e6, 1),
                         "down_us": round(t_d, 1), "down_TOPS": round(ops / t_d / 1e6, 1),
-                        "frac_int8_peak": round(ops / min(t_g, t_d) / 1e6 / 5000.0, 4)}
+                        "roofline_gate": roof_mfma(ops, t_g), "roofline_down": roof_mfma(ops, t_d)}
     out["qwen3_8b_prefill"] = pre
     del G, U, D, Q
     torch.cuda.empty_cache()
@@ -336,7 +377,8 @@ def run_extras():
             ops = 2.0 * m * f * h
             q8[f"M{m}"] = {"gate_us": round(t_g, 1), "gate_TOPS": round(ops / t_g / 1e6, 1),
                            "down_us": round(t_d, 1), "down_TOPS": round(ops / t_d / 1e6, 1),
-                           "frac_int8_peak": round(ops / min(t_g, t_d) / 1e6 / 5000.0, 4)}
+                           "gate_frac_int8_peak": round(ops / t_g / 1e6 / INT8_PEAK_TOPS, 4),
+                           "down_frac_int8_peak": round(ops / t_d / 1e6 / INT8_PEAK_TOPS, 4)}
     out["qwen3_8b_q8_0"] = q8
     del G8, D8
     torch.cuda.empty_cache()
@@ -366,70 +408,41 @@ def run_extras():
         t_l = _time_graph(torch, lambda i, st: kq4.moe_layer_dev(
             Y, X, R, *layers[i], ne, tk, d, ef, stream=st), len(layers))
         moe[f"T{T}"] = {"us": round(t, 2), "experts": n_exp, "GBs": round(byts / t / 1e3, 1),
+                        "roofline": roof_hbm(byts, t),
                         "router_logits_us": round(t_lg, 2), "layer_us": round(t_l, 2)}
     out["qwen3_30b_a3b_moe"] = moe
     return out
 
 
 def cpu_baseline(m, budget_s=12.0):
-    """The reference's x86-64 op wrappers (fp32/int16 activation arithmetic; a timing
-    baseline, not a parity reference) on a bounded sample: layers cycled over enough distinct
-    weight copies to exceed the host LLC, for ~budget_s seconds."""
+    """The reference's own x86-64 code for every config (oracle/cpu_bench.py: seeded weights,
+    median of >= 20 reps, all physical cores and the reference's nc - 2 default, MoE in both
+    activation tracks). Without the reference build (oracle/_ref) it falls back to timing the
+    oracle's scalar restatement of the headline step (kind "port", one thread, ~budget_s)."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle
-
-    threads = int(os.environ.get("KQ4_CPU_THREADS", os.cpu_count() or 1))
-    kind = "reference" if oracle.ref_available() else "port"
+    if oracle.ref_available():
+        import cpu_bench
+        return cpu_bench.run(m)
     s = layer_mats()
-    h, q, kv, f = CFG["hidden"], s["q"][0], s["k"][0], CFG["ffn"]
-    n_copies = CFG["layers"]                          # 28 x 28.3 MB: beyond any host LLC
-    rng = np.random.default_rng(3)
-    layers = [{k: rng.integers(0, 256, size=v.size, dtype=np.uint8) for k, v in
-               {n: np.empty(r * c * 18 // 32, np.uint8) for n, (r, c) in s.items()}.items()}
-              for _ in range(n_copies)]
-    scales = np.frombuffer(np.float16([0.02] * 4).tobytes(), np.uint8)
-    for L in layers:                                   # random nibbles, finite f16 scales
-        for name, (r, c) in s.items():
-            L[name].reshape(r // 4, c // 32, 72)[:, :, :8] = scales
-    x = synth.make_activations(m, h, 7)
-    attn = synth.make_activations(m, q, 8)
-    actv = synth.make_activations(m, f, 9)
-    res = synth.make_activations(m, h, 10)
-    bufs = {k: np.empty((m, n), np.float32) for k, n in
-            dict(q=q, k=kv, v=kv, o=h, g=f, u=f, d=h).items()}
-    P = lambda a: a.ctypes.data  # noqa: E731
-    if kind == "reference":
-        r = oracle.ref(threads)
-
-        def layer(L):
-            r.kref_qkv_batched(P(bufs["q"]), P(bufs["k"]), P(bufs["v"]), P(L["q"]), P(L["k"]),
-                               P(L["v"]), P(x), q, kv, h, m)
-            r.kref_o_residual_batched(P(bufs["o"]), P(res), P(L["o"]), P(attn), h, q, m)
-            r.kref_gate_up_batched(P(bufs["g"]), P(bufs["u"]), P(L["gate"]), P(L["up"]), P(x),
-                                   f, h, m)
-            r.kref_down_residual_batched(P(bufs["d"]), P(res), P(L["down"]), P(actv), h, f, m)
-    else:
-        threads = 1
-
-        def layer(L):
-            for name, (rr, cc) in s.items():
-                src = {"q": x, "k": x, "v": x, "o": attn, "gate": x, "up": x, "down": actv}[name]
-                oracle.matmul(L[name], src, rr, cc)
-
-    layer(layers[0])
+    h, q, f = CFG["hidden"], s["q"][0], CFG["ffn"]
+    w = {n: synth.make_q4_weights(r, c, 1 + i, **synth.SCALE_2B)
+         for i, (n, (r, c)) in enumerate(s.items())}
+    src = {"q": synth.make_activations(m, h, 7), "o": synth.make_activations(m, q, 8),
+           "down": synth.make_activations(m, f, 9)}
     n = 0
     t0 = time.perf_counter()
-    while time.perf_counter() - t0 < budget_s:
-        layer(layers[n % n_copies])
+    while time.perf_counter() - t0 < budget_s or n == 0:
+        for name, (rr, cc) in s.items():
+            oracle.matmul(w[name], src.get(name, src["q"]), rr, cc)
         n += 1
     dt = (time.perf_counter() - t0) / n
-    gbs = step_bytes(m) / dt / 1e9
-    return dict(value=round(gbs, 3), unit="GB/s", cores=threads, kind=kind,
-                sample=f"{n} layer linear sets (QKV+O+gate/up+down, M={m}) over {n_copies} "
-                       f"distinct weight copies, {dt * 1e3:.2f} ms per layer")
+    return dict(value=round(step_bytes(m) / dt / 1e9, 3), unit="GB/s", cores=1, kind="port",
+                sample=f"{n} layer linear sets (M={m}) through the oracle's scalar C, "
+                       f"{dt * 1e3:.2f} ms per layer")
 
 
-PROFILE_OPS = ("gemv_gate_up_2b", "gemv_gate_up_8b", "gemv_down_8b", "gemm_gate_8b",
+PROFILE_OPS = ("gemv_up_2b", "gemv_gate_up_2b", "gemv_gate_up_8b", "gemv_down_8b", "gemm_gate_8b",
                "gemm_down_8b", "moe_30b_a3b", "moe_layer_30b_a3b", "silu_down_8b",
                "rmsnorm_qkv_8b", "q8_gate_8b", "q8_down_8b", "gemv_8b_sweep")
 
@@ -592,7 +605,7 @@ def main():
                      "kernel": "kq4_gemv_kernel (fused gate/up, 2 x 6144x2048)"},
     }
     if not args.no_extras:
-        line["extras"] = run_extras()
+        line["extras"] = run_extras(args)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(args.m, args.cpu_seconds)
     print(json.dumps(line))

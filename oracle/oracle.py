@@ -70,6 +70,9 @@ _REF_SIGS = [
     ("kref_repack_q8_0_8x8", _I, [_P, _I, _I]),
     ("kref_repack_q8_0_4x4", _I, [_P, _I, _I]),
     ("kref_rms_norm_batch", None, [_P, _P, _P, _I, _I, ctypes.c_float]),
+    ("kref_gemm_mat", _I, [_P, _P, _P, _P, _I, _I, _I]),
+    ("kref_num_cpus", ctypes.c_long, []),
+    ("kref_threads", _I, []),
 ]
 
 _oracle = None

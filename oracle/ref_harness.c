@@ -85,6 +85,15 @@ void kref_down_residual_batched(float *x, const float *res, const uint8_t *wd, c
                                 int hidden, int ffn, int n_batch) {
     dyn_matvec_q4_q8_fused_down_residual_batched(x, res, wd, act, hidden, ffn, n_batch, NULL);
 }
+/* q4g_gemm_mat (vllm_safetensors.c:1130-1187): the x86 q4 GEMM over int16 activations that the
+ * batched wrappers take for n_batch > 1 (:1583-1588, :1699-1702, :1649, :1754); 0 = done. */
+int kref_gemm_mat(float *out, const float *resid, const uint8_t *w, const float *x, int rows,
+                  int cols, int nb) {
+    return q4g_gemm_mat(out, resid, w, x, rows, cols, nb);
+}
+/* The reference's logical-CPU count (include/common/vllm_platform.h:354-357) and its pool size. */
+long kref_num_cpus(void) { return st_num_cpus(); }
+int kref_threads(void) { return vllm_tp_threads(); }
 void kref_matvec(float *out, const uint8_t *w, const float *x, int rows, int cols) {
     dyn_matvec_q4_q8(out, w, x, rows, cols);
 }

@@ -149,13 +149,15 @@ def test_gemm_bit_exact(kq4, torch_dev, orc, n, chain):
 # second one partial). The oracle is evaluated on sampled outputs: one per 64 x 64 cell (every
 # tile, every XCD's range), the last token and row, and random pairs.
 @pytest.mark.parametrize("kind", [0, 1])
-@pytest.mark.parametrize("n,rows,chain", [(2048, 4096, 0), (2048, 4096, 1), (2048, 4096, 3),
-                                          (2048, 2048, 2), (2048, 2048, 3), (300, 2048, 0)])
-def test_gemm_large_tiles_bit_exact(kq4, torch_dev, orc, n, rows, chain, kind):
+@pytest.mark.parametrize("n,rows,chain,cols", [(2048, 4096, 0, 640), (2048, 4096, 1, 640),
+                                               (2048, 4096, 3, 640), (2048, 2048, 2, 640),
+                                               (2048, 2048, 3, 640), (300, 2048, 0, 640),
+                                               (300, 2000, 0, 672), (1000, 4000, 3, 672)])
+def test_gemm_large_tiles_bit_exact(kq4, torch_dev, orc, n, rows, chain, cols, kind):
     """Both GEMM forms (planner option gemm_kind: 0 int8 MFMA, 1 fp8 operands; the C-tile chain
-    always takes the int8 one) are bit-identical to the oracle."""
+    always takes the int8 one) are bit-identical to the oracle, also with an odd block count
+    (K = 672: the last 4-block and 2-block stages run past K) and a partial last row set."""
     torch = torch_dev
-    cols = 640
     w, x = case(rows, cols, n, 700 + rows + chain)
     out = torch.empty((n, rows), dtype=torch.float32, device="cuda")
     with kq4.options(gemm_kind=kind):
