@@ -101,11 +101,11 @@ const char *kq4_version(void);
 
 /* Sets one of the launch planner's options, for measurement and tests (no counterpart in the
  * reference): gemv_kind (0 v_dot4 / 1 MFMA dots), gemv_mfma_from, gemv_hs (0 whole 32-row sets,
- * 1 halves, 2 quarters per workgroup), gemv_rps (row sets per workgroup, 1..3), gemv_ksl (K
- * slices), gemv_waves, gemv_wpcu, gemv_maxw, gemv_fq (0 / 1: activations quantized by a separate
- * launch / in the GEMV), gemv_fq_work, gemv_silu_fq_work, gemm_kind (0: the prefill GEMM on
- * int8 MFMA, the default; 1: on fp8 operands; the same outputs). value < 0 restores the default (for
- * most, the planner's own choice). The initial values come from the environment variables KQ4_
+ * 1 halves, 2 quarters per workgroup), gemv_rps (row sets per workgroup, 1..3), gemv_waves,
+ * gemv_wpcu, gemv_maxw, gemv_fq (0 / 1: activations quantized by a separate launch / in the
+ * GEMV), gemv_fq_work, gemv_silu_fq_work, gemm_kind (0: the prefill GEMM on int8 MFMA, the
+ * default; 1: on fp8 operands; the same outputs). value < 0 restores the default (for most, the
+ * planner's own choice). The initial values come from the environment variables KQ4_
  * + the upper-case name. Takes effect for launches planned after it returns. */
 int kq4_set_option(const char *name, int value);
 
@@ -227,8 +227,8 @@ int kq4_matmul_dev(float *out, const float *x, const float *residual, const uint
  * reference. Same arguments, kernels and results as kq4_matmul_dev; the quantized activations go
  * to a fixed per-device scratch array of KQ4_NOALLOC_SCRATCH_BYTES (held by each GPU the library
  * runs on until the process ends) instead of the growable workspace. Beyond 8 tokens the
- * prefill GEMM's operands, n_batch * cols * 17/8 bytes (rounded up to 256-byte pieces), and
- * 64 KiB of counters must fit in it (2048 x 12288 does), else KQ4_EINVAL. Every call on a GPU
+ * prefill GEMM's operands, n_batch * cols * 17/8 bytes (rounded up to 256-byte pieces), must
+ * fit in it (2048 x 12288 does), else KQ4_EINVAL. Every call on a GPU
  * shares that GPU's scratch: calls that overlap on one GPU (other streams or threads) race. */
 #define KQ4_NOALLOC_SCRATCH_BYTES (64u << 20)
 int kq4_matmul_noalloc_dev(float *out, const float *x, const float *residual, const uint8_t *w,

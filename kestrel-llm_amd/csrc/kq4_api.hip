@@ -92,11 +92,6 @@ int cur_dev(DevState **out) {
   return KQ4_OK;
 }
 
-// Every workspace starts with kCntBytes of counters (the split-K GEMV's per-group arrival
-// counters), zero when it is allocated and zero again after every launch that uses them; the
-// carves of a call start after it.
-const size_t kCntBytes = 64 * 1024;
-
 size_t grow_size(size_t bytes) { return al256(bytes > 4096 ? bytes + bytes / 4 : 4096); }
 
 // Staging buffers of the host-pointer API, whose calls are synchronous and cannot be captured
@@ -132,7 +127,7 @@ struct Ws {
 // before it launches anything (kq4_workspace_reserve sizes it beforehand).
 int ensure_ws(const Ws &ws, size_t payload, hipStream_t s) {
   Buf &b = *ws.b;
-  const size_t bytes = kCntBytes + payload;
+  const size_t bytes = payload;
   if (b.cap >= bytes) return KQ4_OK;
   if (!ws.ds)
     return fail(KQ4_EINVAL, "the call needs %zu B of workspace; its fixed buffer holds %zu B",
@@ -145,19 +140,15 @@ int ensure_ws(const Ws &ws, size_t payload, hipStream_t s) {
   const size_t n = grow_size(bytes);
   void *p = nullptr;
   if (hipMalloc(&p, n) != hipSuccess) return fail(KQ4_ENOMEM, "hipMalloc(%zu) failed", n);
-  if (hipMemsetAsync(p, 0, kCntBytes, s) != hipSuccess) {   // the counters start at zero
-    (void)hipFree(p);
-    return fail(KQ4_EHIP, "clearing a new workspace failed");
-  }
   if (b.p) ws.ds->retired.push_back(b.p);
   b.p = p;
   b.cap = n;
   return KQ4_OK;
 }
 
-struct Carve {   // bump allocator over a workspace, above its counter area
+struct Carve {   // bump allocator over a workspace
   char *base;
-  size_t off = kCntBytes;
+  size_t off = 0;
   template <class T>
   T *take(size_t count) {
     T *p = reinterpret_cast<T *>(base + off);
@@ -186,7 +177,7 @@ int env_int(const char *name, int dflt) {
 // (KQ4_ + the name in upper case), changed at run time by kq4_set_option. -1 = the planner's
 // choice where a planner chooses.
 enum OptId {
-  kGemvKind, kGemvMfmaFrom, kGemvHs, kGemvRps, kGemvKsl, kGemvWaves, kGemvWpcu, kGemvMaxw,
+  kGemvKind, kGemvMfmaFrom, kGemvHs, kGemvRps, kGemvWaves, kGemvWpcu, kGemvMaxw,
   kGemvFq, kGemvFqWork, kGemvSiluFqWork, kGemmKind, kOptCount
 };
 struct OptDef {
@@ -196,7 +187,7 @@ struct OptDef {
 const OptDef kOpts[kOptCount] = {
     {"gemv_kind", "KQ4_GEMV_KIND", -1},          {"gemv_mfma_from", "KQ4_GEMV_MFMA_FROM", 2},
     {"gemv_hs", "KQ4_GEMV_HS", -1},              {"gemv_rps", "KQ4_GEMV_RPS", -1},
-    {"gemv_ksl", "KQ4_GEMV_KSL", -1},            {"gemv_waves", "KQ4_GEMV_WAVES", -1},
+    {"gemv_waves", "KQ4_GEMV_WAVES", -1},
     {"gemv_wpcu", "KQ4_GEMV_WPCU", 32},          {"gemv_maxw", "KQ4_GEMV_MAXW", 16},
     {"gemv_fq", "KQ4_GEMV_FQ", -1},              {"gemv_fq_work", "KQ4_GEMV_FQ_WORK", 45000},
     {"gemv_silu_fq_work", "KQ4_GEMV_SILU_FQ_WORK", 15000},
@@ -227,14 +218,9 @@ int gemv_kind(int n) {
   return n >= opt(kGemvMfmaFrom) || n > KQ4_GEMV_DOT4_MAX_M ? 1 : 0;
 }
 
-// Largest partial-sum buffer a split-K GEMV takes (else it runs unsplit).
-const size_t kPartMax = 4u << 20;
-
-size_t gemv_part_bound(int, int) { return kPartMax; }
-
 // GEMV launch shape (kq4_gemv_impl.h). A group of output rows is R whole 32-row sets (rps), or
-// half (hs = 1) or a quarter (hs = 2) of one set; each group is split into ksl K slices, one
-// workgroup each, of nw waves that take the slice's 16-block stages in turn. Chosen from a
+// half (hs = 1) or a quarter (hs = 2) of one set, one workgroup each, of nw waves that take the
+// K stages (16 blocks of q4) in turn. Chosen from a
 // sweep of every combination over the Qwen3-8B and Qwen3-VL-2B decode shapes at M = 1, 2, 4, 8
 // on MI355X (graph replay, weights streamed from HBM):
 //   * hs: quarter sets when the launch has at most one set per 4 CUs, half sets below two sets
@@ -244,19 +230,16 @@ size_t gemv_part_bound(int, int) { return kPartMax; }
 //   * rps: 3 sets per workgroup from 4 tokens on when whole sets fill the chip, with the
 //     activations quantized in the kernel, once for the 3 sets (Qwen3-8B gate/up pair at M = 4:
 //     14.7 against 16.0 us); 1 otherwise (at fewer tokens the lower wave count costs more);
-//   * ksl: 1. Splitting K across workgroups (each slice's sums combined by the last slice to
-//     arrive, with device-scope fences) measured 2-4x slower at every shape; it stays available
-//     as an option;
 //   * waves: about gemv_wpcu (32) per CU over the launch, at most one per stage and 16 per
 //     workgroup (8 with rps > 1), balanced so that no wave has more stages than another by more
 //     than one.
-// Options gemv_hs / _rps / _ksl / _waves / _maxw / _wpcu override it (measurement, tests).
+// Options gemv_hs / _rps / _waves / _maxw / _wpcu override it (measurement, tests).
 struct GemvPlan {
-  int hs, rps, ksl, spk, nw, groups;
+  int hs, rps, nw, groups;
 };
 
 GemvPlan plan_gemv(int n_mats, const int *rows, int nst, int ncu, int n) {
-  const int force_hs = opt(kGemvHs), force_r = opt(kGemvRps), force_k = opt(kGemvKsl);
+  const int force_hs = opt(kGemvHs), force_r = opt(kGemvRps);
   const int force_w = opt(kGemvWaves), per_cu = opt(kGemvWpcu);
   const int max_w = opt(kGemvMaxw) >= 1 && opt(kGemvMaxw) <= 16 ? opt(kGemvMaxw) : 16;
   int sets = 0;
@@ -270,18 +253,15 @@ GemvPlan plan_gemv(int n_mats, const int *rows, int nst, int ncu, int n) {
           : n >= 4 && sets >= 2 * ncu                 ? 3
                                                       : 1;
   if (p.hs) p.rps = 1;
-  p.ksl = force_k >= 1 ? (force_k < nst ? force_k : nst) : 1;
-  p.spk = (nst + p.ksl - 1) / p.ksl;
-  p.ksl = (nst + p.spk - 1) / p.spk;   // no empty slice
   p.groups = 0;
   for (int i = 0; i < n_mats; ++i) p.groups += ((rows[i] + 31) / 32 + p.rps - 1) / p.rps << p.hs;
-  const int wgs = p.groups * p.ksl;
+  const int wgs = p.groups;
   int want = force_w > 0 ? force_w : (per_cu * ncu + wgs - 1) / wgs;
   const int mw = p.rps > 1 && max_w > KQ4_GEMV_RPS_MAX_WAVES ? KQ4_GEMV_RPS_MAX_WAVES : max_w;
-  const int cap = p.spk < mw ? p.spk : mw;
+  const int cap = nst < mw ? nst : mw;
   want = want < 1 ? 1 : (want > cap ? cap : want);
-  const int spw = (p.spk + want - 1) / want;   // stages per wave
-  p.nw = (p.spk + spw - 1) / spw;
+  const int spw = (nst + want - 1) / want;   // stages per wave
+  p.nw = (nst + spw - 1) / spw;
   return p;
 }
 
@@ -314,29 +294,16 @@ int run_gemv(DevState *ds, const Ws &wsp, int n_mats, float *const *out, const f
   memset(&a, 0, sizeof(a));
   GemvPlan pl = plan_gemv(n_mats, rows, nst, ds->ncu, n);
   const int kind = wf ? 1 : gemv_kind(n);
-  // the split-K partial sums and the quantized activations (when quantized apart) in the
-  // workspace; the per-group counters in its fixed counter area
-  const size_t nout = (size_t)pl.rps * n * (32 >> pl.hs);
-  size_t pbytes = al256((size_t)pl.groups * pl.ksl * nout * sizeof(float));
-  if (pl.ksl > 1 && (pl.groups > (int)(kCntBytes / sizeof(unsigned)) || pbytes > kPartMax)) {
-    pl.ksl = 1;   // too many groups or partial sums for the split: whole K per workgroup
-    pl.spk = nst;
-  }
-  if (pl.ksl == 1) pbytes = 0;
-  const int wgs = pl.groups * pl.ksl;
+  // the quantized activations (when quantized apart) in the workspace
+  const int wgs = pl.groups;
   bool fq = false;
   if (x) {
     const long per_cu = ((long)wgs + ds->ncu - 1) / ds->ncu;
-    fq = gemv_fq(per_cu * n * ((long)pl.spk * cb * 32 < cols ? (long)pl.spk * cb * 32 : cols), n,
-                 pl.rps, xu != nullptr);
+    fq = gemv_fq(per_cu * n * cols, n, pl.rps, xu != nullptr);
   }
   const size_t qbytes = x && !fq ? qa_bytes(n, cols) : 0;
-  if (pbytes + qbytes && (rc = ensure_ws(wsp, pbytes + qbytes, s))) return rc;
+  if (qbytes && (rc = ensure_ws(wsp, qbytes, s))) return rc;
   Carve cv{static_cast<char *>(wsp.b->p)};
-  if (pl.ksl > 1) {
-    a.part = cv.take<float>((size_t)pl.groups * pl.ksl * nout);
-    a.cnt = reinterpret_cast<unsigned *>(wsp.b->p);
-  }
   if (x) {
     if (fq) {
       a.xf = x;
@@ -357,8 +324,6 @@ int run_gemv(DevState *ds, const Ws &wsp, int n_mats, float *const *out, const f
   a.nb = nb;
   a.wf = wf;
   a.nw = pl.nw;
-  a.ksl = pl.ksl;
-  a.spk = pl.spk;
   int g = 0;
   for (int i = 0; i < n_mats; ++i) {
     KQ4GemvMat &m = a.mat[i];
@@ -526,7 +491,7 @@ int moe_impl(float *Y, const float *X, const int *sel, const float *pr, int T, i
   if (rc) return rc;
   const size_t np = (size_t)T * tk;
   if ((rc = ensure_ws(Ws{&ds->ws, ds}, off + moe_stage_bytes(T, tk, ne, d, ef), s))) return rc;
-  Carve cv{static_cast<char *>(ds->ws.p), kCntBytes + off};
+  Carve cv{static_cast<char *>(ds->ws.p), off};
   KQ4MoeWs ws;
   ws.ex_off = cv.take<int>(ne + 1);
   ws.ex_pair = cv.take<int>(np);
@@ -666,23 +631,21 @@ void kq4_shutdown(void) {
 
 size_t kq4_matmul_workspace_bytes(int n_batch, int cols) {
   if (n_batch < 0 || cols <= 0 || cols % 32) return 0;
-  // quantized activations, the one-token RMSNorm row, the split-K GEMV's partial sums (at most
-  // one float per output row, token and K stage)
+  // quantized activations (int8 or the fp8 GEMM's operand pairs) and the one-token RMSNorm row
   const size_t q = qa_bytes(n_batch, cols), f = f8_bytes(n_batch, cols);
-  return kCntBytes + (q > f ? q : f) + al256((size_t)cols * sizeof(float)) +
-         (n_batch <= KQ4_GEMV_MAX_M ? gemv_part_bound(n_batch, cols) : 0);
+  return (q > f ? q : f) + al256((size_t)cols * sizeof(float));
 }
 
 size_t kq4_moe_workspace_bytes(int T, int tk, int ne, int d, int ef) {
   if (T < 0 || tk < 1 || tk > 32 || ne < 1 || !kq4_moe_shape_ok(d, ef)) return 0;
-  return kCntBytes + moe_route_bytes(T, tk, ne) + moe_stage_bytes(T, tk, ne, d, ef);
+  return moe_route_bytes(T, tk, ne) + moe_stage_bytes(T, tk, ne, d, ef);
 }
 
 int kq4_workspace_reserve(size_t bytes) {
   DevState *ds = nullptr;
   int rc = cur_dev(&ds);
   if (rc) return rc;
-  return ensure_ws(Ws{&ds->ws, ds}, bytes > kCntBytes ? bytes - kCntBytes : 0, nullptr);
+  return ensure_ws(Ws{&ds->ws, ds}, bytes, nullptr);
 }
 
 int kq4_set_option(const char *name, int value) {
@@ -807,8 +770,8 @@ int kq4_matmul_noalloc_dev(float *out, const float *x, const float *residual, co
                            int rows, int cols, int n_batch, int chain, void *stream) {
   if (!x && n_batch) return fail(KQ4_EINVAL, "null x");
   const size_t need = n_batch > 0 && cols > 0 && cols % 32 == 0
-                         ? kCntBytes + (n_batch <= KQ4_GEMV_MAX_M ? qa_bytes(n_batch, cols) + kPartMax
-                                                                  : f8_bytes(n_batch, cols))
+                         ? (n_batch <= KQ4_GEMV_MAX_M ? qa_bytes(n_batch, cols)
+                                                      : f8_bytes(n_batch, cols))
                          : 0;
   if (need > (size_t)KQ4_NOALLOC_SCRATCH_BYTES)
     return fail(KQ4_EINVAL, "matmul_noalloc: %d tokens x %d columns need %zu B of scratch; the "
@@ -881,7 +844,7 @@ int kq4_rmsnorm_matmul_multi_dev(int n_mats, float *const *out, const float *con
       if ((rc = ensure_ws(Ws{&ds->ws, ds}, qbytes + al256((size_t)cols * sizeof(float)),
                           (hipStream_t)stream)))
         return rc;
-      nx = reinterpret_cast<float *>(static_cast<char *>(ds->ws.p) + kCntBytes + qbytes);
+      nx = reinterpret_cast<float *>(static_cast<char *>(ds->ws.p) + qbytes);
     }
     KQ4_HIP((hipError_t)kq4_launch_rms_norm(x, norm_w, nx, nullptr, nullptr, 1, cols, eps,
                                             order == KQ4_RMS_SERIAL, (hipStream_t)stream));

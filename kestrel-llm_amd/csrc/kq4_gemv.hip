@@ -24,7 +24,6 @@ int kq4_launch_gemv(const KQ4GemvArgs &a, int n_batch, int kind, int half_sets, 
       kind > 1 || (kind == 0 && n_batch > KQ4_GEMV_DOT4_MAX_M) || half_sets < 0 ||
       half_sets > 2 || rps < 1 || rps > KQ4_GEMV_MAX_RPS || (half_sets && rps != 1) ||
       (rps > 1 && nw > KQ4_GEMV_RPS_MAX_WAVES) ||
-      a.ksl < 1 || a.spk < 1 || (a.ksl > 1 && (!a.part || !a.cnt)) || grid % a.ksl ||
       (size_t)nw * kq4_gemv_slab_bytes(n_batch) > 160 * 1024 - 64)
     return (int)hipErrorInvalidValue;
   for (int i = 0; i < a.nmat; ++i)

@@ -428,24 +428,19 @@ constexpr int kq4_gv_mq() {
   return FQ == 0 ? M : (FQ == 2 ? (M < 2 ? M : 2) : (M < 4 ? M : 4));
 }
 
-// Workgroup -> work. Launch workgroup wg = g * ksl + k takes K slice k (stages k * spk ..
-// k * spk + spk - 1) of group g. Groups are numbered over the launch's matrices, each matrix a
-// contiguous range from its wg_begin; within a matrix, group gl = sg * NP + hs covers the R row
-// sets sg * R .. sg * R + R - 1 (HS = 0), or part hs of row set sg (half / quarter sets, R = 1).
-// Each wave takes the slice's stages wave, wave + nw, ..; for each stage it stages (quantizes)
-// the activations once into its LDS slab and then streams the stage's chunk of every one of the
-// group's R row sets, the next set's loads issued before the current set's dots.
-// At the end each output's partials are added in a fixed order (lane swaps, then the waves
-// through LDS); with K slices (ksl > 1) every slice stores its sums to a.part, and the slice that
-// arrives last at the group's counter adds the ksl partials in slice order and writes the output,
-// so results are deterministic whatever the arrival order, and the counter is reset for the
-// next launch.
+// Workgroup -> work. Workgroups are numbered over the launch's matrices, each matrix a
+// contiguous range from its wg_begin; within a matrix, workgroup gl = sg * NP + hs covers the R
+// row sets sg * R .. sg * R + R - 1 (HS = 0), or part hs of row set sg (half / quarter sets,
+// R = 1), over the whole K. Each wave takes the stages wave, wave + nw, ..; for each stage it
+// stages (quantizes) the activations once into its LDS slab and then streams the stage's chunk
+// of every one of the group's R row sets, the next set's loads issued before the current set's
+// dots. At the end each output's partials are added in a fixed order (lane swaps, then the
+// waves through LDS), so results are deterministic.
 // Up to 16 waves per workgroup for single-set groups (128 VGPRs), 8 for R > 1 (whose prefetched
 // second set needs more registers).
 template <int M, int FQ, int KIND, int HS, int WF, int R>
 __global__ __launch_bounds__(R > 1 ? 512 : 1024) void kq4_gemv_kernel(const KQ4GemvArgs a) {
   extern __shared__ __align__(16) uint8_t kq4_gv_lds[];
-  __shared__ int kq4_gv_last;
   constexpr int SLAB = kq4_gv_slab<M>();
   constexpr int NACC = KIND == 0 ? M : 4;
   constexpr int NR = 32 >> HS;                     // output rows per row set of the workgroup
@@ -458,9 +453,7 @@ __global__ __launch_bounds__(R > 1 ? 512 : 1024) void kq4_gemv_kernel(const KQ4G
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int nw = a.nw;
-  const int ksl = a.ksl;
-  const int gg = (int)blockIdx.x / ksl;            // group over the launch
-  const int ks = (int)blockIdx.x - gg * ksl;       // K slice
+  const int gg = (int)blockIdx.x;                  // group over the launch
   const KQ4GvMatSel ms = kq4_gv_select(a, gg);
   const int gl = gg - ms.wg_begin;
   const int set0 = (gl >> HS) * R;                 // first row set of the group
@@ -470,7 +463,6 @@ __global__ __launch_bounds__(R > 1 ? 512 : 1024) void kq4_gemv_kernel(const KQ4G
   const int nb = a.nb;
   constexpr int CB = KQ4Wf<WF>::CB, CHUNK = KQ4Wf<WF>::CHUNK;
   const int nst = (nb + CB - 1) / CB;
-  const int st_end = min(nst, (ks + 1) * a.spk);
   const uint8_t *__restrict__ wb = (const uint8_t *)ms.w;
   uint8_t *slab = kq4_gv_lds + wave * SLAB;
   uint8_t *sq = slab;
@@ -485,7 +477,7 @@ __global__ __launch_bounds__(R > 1 ? 512 : 1024) void kq4_gemv_kernel(const KQ4G
   for (int q = 0; q < R; ++q)
 #pragma unroll
     for (int i = 0; i < NACC; ++i) acc[q][i] = 0.0f;
-  for (int st = ks * a.spk + wave; st < st_end; st += nw) {
+  for (int st = wave; st < nst; st += nw) {
     // issued as (activations, weights), so quantizing the activations waits only for them
     KQ4GvAct<MQ, FQ, WF> ra;
     KQ4GvStage<HS> rw[R > 1 ? 2 : 1];
@@ -551,42 +543,21 @@ __global__ __launch_bounds__(R > 1 ? 512 : 1024) void kq4_gemv_kernel(const KQ4G
     for (int w = 0; w < nw; ++w) s += reinterpret_cast<const float *>(kq4_gv_lds + w * SLAB)[i];
     return s;
   };
-  if (ksl == 1) {
-    // the first pass's residual is loaded before the barrier, so its latency hides behind the
-    // wait (measured: 2B down and O with residual 0.04-0.08 us faster per launch at one token)
-    float res0 = 0.0f;
-    {
-      const int i = threadIdx.x, row = out_row(i);
-      if (res && i < NOUT && row < rows) res0 = res[(size_t)((i / NR) % M) * rows + row];
-    }
-    __syncthreads();
-    for (int i = threadIdx.x; i < NOUT; i += 64 * nw) {
-      const int row = out_row(i);
-      if (row >= rows) continue;
-      const float s = wave_sum(i);
-      const size_t o = (size_t)((i / NR) % M) * rows + row;
-      out[o] = res ? (i == (int)threadIdx.x ? res0 : res[o]) + s : s;
-    }
-    return;
+  // the first pass's residual is loaded before the barrier, so its latency hides behind the
+  // wait (measured: 2B down and O with residual 0.04-0.08 us faster per launch at one token)
+  float res0 = 0.0f;
+  {
+    const int i = threadIdx.x, row = out_row(i);
+    if (res && i < NOUT && row < rows) res0 = res[(size_t)((i / NR) % M) * rows + row];
   }
   __syncthreads();
-  float *__restrict__ part = a.part + (size_t)gg * ksl * NOUT;
-  for (int i = threadIdx.x; i < NOUT; i += 64 * nw) part[(size_t)ks * NOUT + i] = wave_sum(i);
-  __threadfence();   // the sums are visible device-wide before the arrival is counted
-  __syncthreads();
-  if (threadIdx.x == 0) kq4_gv_last = atomicAdd(&a.cnt[gg], 1u) == (unsigned)(ksl - 1);
-  __syncthreads();
-  if (!kq4_gv_last) return;
-  __threadfence();   // and the other slices' sums are read after their arrivals
   for (int i = threadIdx.x; i < NOUT; i += 64 * nw) {
     const int row = out_row(i);
     if (row >= rows) continue;
-    float s = 0.0f;
-    for (int k = 0; k < ksl; ++k) s += __builtin_nontemporal_load(part + (size_t)k * NOUT + i);
+    const float s = wave_sum(i);
     const size_t o = (size_t)((i / NR) % M) * rows + row;
-    out[o] = res ? res[o] + s : s;
+    out[o] = res ? (i == (int)threadIdx.x ? res0 : res[o]) + s : s;
   }
-  if (threadIdx.x == 0) a.cnt[gg] = 0u;   // every slice has arrived: ready for the next launch
 }
 
 template <int M, int FQ, int KIND, int HS, int WF, int R>

@@ -39,10 +39,6 @@ struct KQ4GemvArgs {
   int cols;
   int nb;
   int nw;               // waves per workgroup
-  int ksl;              // K slices: workgroups per group (1 = each workgroup takes the whole K)
-  int spk;              // stages per K slice
-  float *part;          // ksl > 1: partial sums [groups][ksl][R * M * rows per set part]
-  unsigned *cnt;        // ksl > 1: per-group arrival counters, zero before and after a launch
 };
 
 // up != nullptr: quantizes silu_mul(x, up) instead of x (the dense FFN's down input).
@@ -60,8 +56,8 @@ int kq4_launch_rms_norm(const float *x, const float *w, float *out, int8_t *xq, 
 
 // One GEMV launch (kq4_gemv_impl.h): n_batch in [1, KQ4_GEMV_MAX_M]; kind 0 = per-lane v_dot4
 // dots (n_batch <= KQ4_GEMV_DOT4_MAX_M), 1 = v_mfma dots; half_sets 0 (whole 32-row sets, rps of
-// them per group), 1 (16-row halves) or 2 (8-row quarters, rps = 1); grid = groups * args.ksl
-// workgroups of args.nw (1..16) waves. args.xf (in-kernel quantization) for every n_batch.
+// them per group), 1 (16-row halves) or 2 (8-row quarters, rps = 1); grid = groups workgroups
+// of args.nw (1..16) waves. args.xf (in-kernel quantization) for every n_batch.
 #define KQ4_GEMV_DOT4_MAX_M 4
 #define KQ4_GEMV_MAX_RPS 3
 #define KQ4_GEMV_RPS_MAX_WAVES 8   // waves per workgroup when it takes several row sets

@@ -190,13 +190,12 @@ def test_gemm_from_prequantized(kq4, torch_dev, orc):
 
 
 # Launch shapes of the GEMV set through the planner options (include/kq4.h kq4_set_option):
-# whole sets grouped 2 or 3 per workgroup (the last group short), half / quarter sets, and K
-# split into slices whose sums the last-arriving slice adds (the last slice short), with the
-# activations quantized in the kernel or apart, with a residual.
+# whole sets grouped 2 or 3 per workgroup (the last group short), half / quarter sets, wave
+# counts that leave a wave with fewer stages than the others, with the activations quantized in
+# the kernel or apart, with a residual.
 GEMV_PLANS = [dict(gemv_hs=0, gemv_rps=2), dict(gemv_hs=0, gemv_rps=3),
-              dict(gemv_hs=0, gemv_rps=3, gemv_ksl=2), dict(gemv_hs=0, gemv_ksl=3),
-              dict(gemv_hs=1, gemv_ksl=4), dict(gemv_hs=2, gemv_ksl=6),
-              dict(gemv_hs=0, gemv_rps=2, gemv_ksl=5, gemv_fq=0)]
+              dict(gemv_hs=0, gemv_rps=3, gemv_waves=2), dict(gemv_hs=1, gemv_waves=3),
+              dict(gemv_hs=2, gemv_waves=5), dict(gemv_hs=0, gemv_rps=2, gemv_fq=0)]
 
 
 @pytest.mark.parametrize("n", [1, 2, 3, 5, 8])

@@ -112,6 +112,35 @@ def test_moe_stages(kq4, torch_dev, orc, shape, T):
                            av_in=to_dev(torch, st["av"]))
     torch.cuda.synchronize()
     assert np.array_equal(host(Y2).view(np.uint32), Y_o.view(np.uint32))
+    # the FFN without stage outputs gives the same bits
+    Y3 = torch.empty_like(Y)
+    kq4.moe_ffn_dev(Y3, dX, dsel, dpr, dG, dU, dD, ne, d, ef)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(Y3).view(np.uint32), host(Y).view(np.uint32))
+
+
+@pytest.mark.parametrize("shape", ["small", "qwen3_30b_a3b"])
+def test_moe_one_token_all_ids_invalid(kq4, torch_dev, orc, shape):
+    """No valid rank at one token: the output is zero (the combine adds nothing), with and
+    without stage outputs."""
+    torch = torch_dev
+    cfg = SHAPES[shape]
+    d, ne, tk, ef = cfg["hidden"], cfg["experts"], cfg["top_k"], cfg["ef"]
+    G, U, D = synth.make_moe(cfg, 93)
+    dG, dU = (kq4.prepare_dev(to_dev(torch, a), ne * ef, d) for a in (G, U))
+    dD = kq4.prepare_dev(to_dev(torch, D), d, ne * ef)
+    dX = to_dev(torch, synth.make_activations(1, d, 94))
+    dsel = to_dev(torch, np.array([[-1] * (tk - 1) + [ne]], np.int32))
+    dpr = to_dev(torch, np.full((1, tk), 0.25, np.float32))
+    Y = torch.full((1, d), float("nan"), dtype=torch.float32, device="cuda")
+    kq4.moe_ffn_dev(Y, dX, dsel, dpr, dG, dU, dD, ne, d, ef)
+    gate = torch.zeros((tk, ef), dtype=torch.float32, device="cuda")
+    up = torch.zeros_like(gate)
+    Y2 = torch.full((1, d), float("nan"), dtype=torch.float32, device="cuda")
+    kq4.moe_ffn_stages_dev(Y2, dX, dsel, dpr, dG, dU, dD, ne, d, ef, gate=gate, up=up)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(Y), np.zeros((1, d), np.float32))
+    assert np.array_equal(host(Y2), np.zeros((1, d), np.float32))
 
 
 @pytest.mark.parametrize("T", [1, 3])   # T = 1 takes the kernels' one-token mode (no grouping)
