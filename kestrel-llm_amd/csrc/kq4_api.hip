@@ -511,15 +511,26 @@ int moe_impl(float *Y, const float *X, const int *sel, const float *pr, int T, i
 
 size_t wbytes(int rows, int cols) { return (size_t)(rows / 4) * (cols / 32) * 72; }
 
-// Cheap fingerprint of a host weight buffer (FNV-1a over 3 x 64 sampled bytes + size): a cache
-// entry whose key was reused for different bytes (e.g. a freed and reallocated host buffer) is
-// re-uploaded instead of served stale.
+// Fingerprint of a host weight buffer: FNV-1a over the size and 64 spans of 64 bytes spread
+// evenly from the first byte to the last (4 KB read per call; every byte when the buffer is at
+// most 4 KB). A cache entry whose key was reused for different weights (e.g. a freed and
+// reallocated host buffer) is re-uploaded instead of served stale whenever one sampled span
+// differs. The key is the caller's promise, as it is for the reference's NPU weight cache
+// (include/npu/vllm_npu.h:135-159); the fingerprint catches a broken promise for any two
+// different matrices (they differ throughout), not a change confined to unsampled bytes.
 uint64_t fingerprint(const uint8_t *w, size_t bytes) {
-  uint64_t h = 1469598103934665603ull ^ bytes;
-  const size_t span = bytes < 64 ? bytes : 64;
-  const size_t offs[3] = {0, bytes / 2 - (bytes / 2 >= span / 2 ? span / 2 : 0), bytes - span};
-  for (size_t o : offs)
-    for (size_t i = 0; i < span; ++i) h = (h ^ w[o + i]) * 1099511628211ull;
+  constexpr size_t kSpans = 64, kSpan = 64;
+  uint64_t h = 1469598103934665603ull;
+  for (int i = 0; i < 8; ++i) h = (h ^ ((bytes >> (8 * i)) & 0xFF)) * 1099511628211ull;
+  auto mix = [&](size_t o, size_t n) {
+    for (size_t i = 0; i < n; ++i) h = (h ^ w[o + i]) * 1099511628211ull;
+  };
+  if (bytes <= kSpans * kSpan) {
+    mix(0, bytes);
+    return h;
+  }
+  for (size_t k = 0; k < kSpans; ++k)   // span k starts at k/(kSpans-1) of the way to the end
+    mix((bytes - kSpan) / (kSpans - 1) * k, kSpan);
   return h;
 }
 

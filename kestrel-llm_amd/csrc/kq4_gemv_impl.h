@@ -564,9 +564,9 @@ template <int M, int FQ, int KIND, int HS, int WF, int R>
 static hipError_t kq4_gv_launch1(const KQ4GemvArgs &a, int grid, hipStream_t s) {
   const size_t lds = (size_t)a.nw * kq4_gv_slab<M>();
   const void *fn = reinterpret_cast<const void *>(&kq4_gemv_kernel<M, FQ, KIND, HS, WF, R>);
-  if (lds > 64 * 1024) {   // above the default dynamic LDS limit: raise it (idempotent)
-    hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       160 * 1024 - 64);
+  if (lds > 64 * 1024) {   // above the default dynamic LDS limit: raise it
+    static std::atomic<unsigned long long> attr{0};
+    hipError_t e = kq4_lds_limit_once(fn, 160 * 1024 - 64, attr);
     if (e != hipSuccess) return e;
   }
   hipLaunchKernelGGL((kq4_gemv_kernel<M, FQ, KIND, HS, WF, R>), dim3(grid), dim3(64 * a.nw), lds,

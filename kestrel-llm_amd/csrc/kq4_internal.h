@@ -4,6 +4,23 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
+
+// Raises kernel fn's dynamic LDS limit to `bytes` on the current device once per (kernel,
+// device): `done`, one per kernel, holds a bit per device id below 64 (devices beyond make the
+// call every time). Thread-safe: threads that race both make the idempotent call.
+inline hipError_t kq4_lds_limit_once(const void *fn, int bytes,
+                                     std::atomic<unsigned long long> &done) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  const unsigned long long bit = dev >= 0 && dev < 64 ? 1ull << dev : 0;
+  if (bit && (done.load(std::memory_order_acquire) & bit)) return hipSuccess;
+  e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  if (e == hipSuccess && bit) done.fetch_or(bit, std::memory_order_acq_rel);
+  return e;
+}
+
 #define KQ4_GEMV_MAX_M 8
 #define KQ4_MAXMAT 4
 

@@ -288,13 +288,10 @@ int kq4_launch_moe_logits(float *logits, const float *router, const float *X, in
   if (T <= 0) return 0;
   if (d % 32) return (int)hipErrorInvalidValue;
   const size_t lds = (2 * KQ4_RT_E * KQ4_RT_P + 32) * sizeof(float);
-  static bool attr = false;   // 66 KB of LDS
-  if (!attr) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&kq4_moe_logits_kernel),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) return (int)e;
-    attr = true;
-  }
+  static std::atomic<unsigned long long> attr{0};   // 66 KB of LDS
+  hipError_t e = kq4_lds_limit_once(reinterpret_cast<const void *>(&kq4_moe_logits_kernel),
+                                    (int)lds, attr);
+  if (e != hipSuccess) return (int)e;
   hipLaunchKernelGGL(kq4_moe_logits_kernel,
                      dim3((unsigned)((ne + KQ4_RT_E - 1) / KQ4_RT_E), (unsigned)T), dim3(320),
                      lds, s, logits, router, X, ne, d);

@@ -277,14 +277,10 @@ static hipError_t rms_launch_h(const float *x, const float *w, float *out, int8_
                                int n_batch, int d, float eps, int serial, hipStream_t s) {
   // the serial order keeps d squares in LDS (64 KB at d = 16384); the kernel's static LDS (the
   // broadcast rms) comes off the 160 KB a workgroup may hold
-  static bool attr = false;
-  if (!attr) {
-    hipError_t e = hipFuncSetAttribute(
-        reinterpret_cast<const void *>(&kq4_rms_norm_kernel<CPT, HOLD>),
-        hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024 - 1024);
-    if (e != hipSuccess) return e;
-    attr = true;
-  }
+  static std::atomic<unsigned long long> attr{0};
+  hipError_t e = kq4_lds_limit_once(
+      reinterpret_cast<const void *>(&kq4_rms_norm_kernel<CPT, HOLD>), 160 * 1024 - 1024, attr);
+  if (e != hipSuccess) return e;
   hipLaunchKernelGGL((kq4_rms_norm_kernel<CPT, HOLD>), dim3(n_batch), dim3(KQ4_RMS_THREADS),
                      kq4_rms_norm_lds(d, serial), s, x, w, out, xq, xd, d, eps, serial);
   return hipGetLastError();

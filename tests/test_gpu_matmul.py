@@ -193,9 +193,12 @@ def test_gemm_from_prequantized(kq4, torch_dev, orc):
 # whole sets grouped 2 or 3 per workgroup (the last group short), half / quarter sets, wave
 # counts that leave a wave with fewer stages than the others, with the activations quantized in
 # the kernel or apart, with a residual.
+# The last three: waves taking 3 of the 6 stages, all 6, and a mix of 2 and 1 (pre-quantized).
 GEMV_PLANS = [dict(gemv_hs=0, gemv_rps=2), dict(gemv_hs=0, gemv_rps=3),
               dict(gemv_hs=0, gemv_rps=3, gemv_waves=2), dict(gemv_hs=1, gemv_waves=3),
-              dict(gemv_hs=2, gemv_waves=5), dict(gemv_hs=0, gemv_rps=2, gemv_fq=0)]
+              dict(gemv_hs=2, gemv_waves=5), dict(gemv_hs=0, gemv_rps=2, gemv_fq=0),
+              dict(gemv_hs=1, gemv_waves=2), dict(gemv_hs=2, gemv_waves=1),
+              dict(gemv_hs=0, gemv_waves=4, gemv_fq=0)]
 
 
 @pytest.mark.parametrize("n", [1, 2, 3, 5, 8])
