@@ -245,7 +245,8 @@ def roof_mfma(ops, us):
 
 def run_extras(args):
     """The other BASELINE.json configs, each with its own roofline block (reported beside the
-    headline line): config 1 (one 2B GEMV, M = 1), config 2 at M = 4 (the headline step),
+    headline line): config 1 (one 2B GEMV, M = 1), the 2B lm_head GEMV (M = 1), config 2 at
+    M = 4 (the headline step),
     config 3 (Qwen3-8B decode GEMVs at M in {1,2,4,8}: us/call, GB/s against HBM peak, per op),
     config 4 (prefill GEMM at M in {512, 2048}: int8 TOPS against 5.0 POPS dense, per op) and
     config 5 (Qwen3-30B-A3B MoE FFN at T in {1, 64}), plus the Q8_0 weight form. Every measured
@@ -266,6 +267,18 @@ def run_extras(args):
     b1 = rows1 * cols1 * 18 // 32 + cols1 * 4 + rows1 * 4
     out["config1_gemv_m1"] = {"us_per_call": round(t1, 3), "bytes": b1, "roofline": roof_hbm(b1, t1)}
     del W1
+    # the 2B lm_head (vocab x hidden, 175 MB of q4 weights), one token on its M4f chain: the
+    # largest decode GEMV of the model (vllm_safetensors.c:16844)
+    rows_l = CFG["vocab"]
+    WL = _copies(torch, synth.make_q4_weights(rows_l, cols1, 31, **synth.SCALE_2B), rows_l, cols1)
+    ol = torch.empty((1, rows_l), device="cuda")
+    tl = _time_graph(torch, lambda i, st: kq4.matmul_dev(ol, x1, WL[i], rows_l, cols1,
+                                                        chain=kq4.CHAIN_GEMV32, stream=st),
+                     len(WL))
+    bl = rows_l * cols1 * 18 // 32 + cols1 * 4 + rows_l * 4
+    out["lm_head_2b_m1"] = {"us_per_call": round(tl, 3), "bytes": bl, "roofline": roof_hbm(bl, tl)}
+    del WL
+    torch.cuda.empty_cache()
     # config 2 at M = 4: the headline step (28 layers' linear sets, one graph replay per step)
     g4 = run_gpu(argparse.Namespace(m=4, steps=max(10, args.steps // 2), warmup=args.warmup))
     out["config2_step_m4"] = {"ms_per_step": round(g4["ms_per_step"], 4),

@@ -188,7 +188,7 @@ const OptDef kOpts[kOptCount] = {
     {"gemv_kind", "KQ4_GEMV_KIND", -1},          {"gemv_mfma_from", "KQ4_GEMV_MFMA_FROM", 2},
     {"gemv_hs", "KQ4_GEMV_HS", -1},              {"gemv_rps", "KQ4_GEMV_RPS", -1},
     {"gemv_waves", "KQ4_GEMV_WAVES", -1},
-    {"gemv_wpcu", "KQ4_GEMV_WPCU", 32},          {"gemv_maxw", "KQ4_GEMV_MAXW", 16},
+    {"gemv_wpcu", "KQ4_GEMV_WPCU", 64},          {"gemv_maxw", "KQ4_GEMV_MAXW", 16},
     {"gemv_fq", "KQ4_GEMV_FQ", -1},              {"gemv_fq_work", "KQ4_GEMV_FQ_WORK", 45000},
     {"gemv_silu_fq_work", "KQ4_GEMV_SILU_FQ_WORK", 15000},
     {"gemm_kind", "KQ4_GEMM_KIND", -1},
@@ -230,7 +230,7 @@ int gemv_kind(int n) {
 //   * rps: 3 sets per workgroup from 4 tokens on when whole sets fill the chip, with the
 //     activations quantized in the kernel, once for the 3 sets (Qwen3-8B gate/up pair at M = 4:
 //     14.7 against 16.0 us); 1 otherwise (at fewer tokens the lower wave count costs more);
-//   * waves: about gemv_wpcu (32) per CU over the launch, at most one per stage and 16 per
+//   * waves: about gemv_wpcu (64) per CU over the launch, at most one per stage and 16 per
 //     workgroup (8 with rps > 1), balanced so that no wave has more stages than another by more
 //     than one.
 // Options gemv_hs / _rps / _waves / _maxw / _wpcu override it (measurement, tests).

@@ -10,8 +10,10 @@ numpy's PCG64 (np.random.default_rng(seed)), so a seed names the same bytes on e
 import numpy as np
 
 # Shapes of the BASELINE.json configurations.
-QWEN3VL_2B = dict(hidden=2048, q_heads=16, kv_heads=8, head_dim=128, ffn=6144, layers=28)
-QWEN3_8B = dict(hidden=4096, q_heads=32, kv_heads=8, head_dim=128, ffn=12288, layers=36)
+QWEN3VL_2B = dict(hidden=2048, q_heads=16, kv_heads=8, head_dim=128, ffn=6144, layers=28,
+                  vocab=151936)
+QWEN3_8B = dict(hidden=4096, q_heads=32, kv_heads=8, head_dim=128, ffn=12288, layers=36,
+                vocab=151936)
 QWEN3_30B_A3B_MOE = dict(hidden=2048, experts=128, top_k=8, ef=768)
 
 SCALE_2B = dict(sigma=0.02, floor=1e-4)

@@ -146,3 +146,26 @@ def test_config4_prefill_with_ctile_tail(kq4, torch_dev, orc, mats):
     r, a = rel_err(got[tail, trow], want_t)
     print(f"tail tokens 2048..{m - 1}: rel={r:.3e} maxabs={a:.3e}")
     assert r <= TOL
+
+
+@pytest.mark.parametrize("chain", ["gemv32", "auto"])
+def test_lm_head_full(kq4, torch_dev, orc, chain):
+    """The largest decode GEMV on the path: the lm_head, vocab x hidden = 151936 x 2048 for
+    Qwen3-VL-2B (175 MB of q4 weights), one token, which the reference runs as
+    dyn_matvec_q4_q8(logits, q4_lm_weight, normed, vocab, d) (vllm_safetensors.c:16844) on the
+    M4f chain (GEMV32); every one of the 151936 outputs against the oracle, on that chain and on
+    the default one."""
+    torch = torch_dev
+    cfg = synth.QWEN3VL_2B
+    rows, cols = cfg["vocab"], cfg["hidden"]
+    w = synth.make_q4_weights(rows, cols, 31, **synth.SCALE_2B)
+    wd = kq4.prepare_dev(to_dev(torch, w), rows, cols)
+    x = synth.make_activations(1, cols, 32)
+    ch = kq4.CHAIN_GEMV32 if chain == "gemv32" else kq4.CHAIN_AUTO
+    out = torch.empty((1, rows), dtype=torch.float32, device="cuda")
+    kq4.matmul_dev(out, to_dev(torch, x), wd, rows, cols, chain=ch)
+    torch.cuda.synchronize()
+    want = orc.matmul(w, x, rows, cols, chain=ch)
+    r, a = rel_err(out.cpu().numpy(), want)
+    print(f"lm_head {rows}x{cols} chain={chain}: rel={r:.3e} maxabs={a:.3e}")
+    assert r <= TOL
