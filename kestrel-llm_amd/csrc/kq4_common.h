@@ -185,6 +185,20 @@ KQ4_DEV uint2 kq4_bload8(__amdgpu_buffer_rsrc_t r, uint32_t off) {
 KQ4_DEV uint32_t kq4_bload4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
 }
+// The same with the offset split into a per-lane part (voff) and a wave-uniform one (soff, the
+// instruction's scalar offset): loads whose uniform part changes per loop step cost no vector
+// arithmetic.
+KQ4_DEV uint4 kq4_bload16s(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, (int)soff, 0);
+  return make_uint4((uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3]);
+}
+KQ4_DEV uint2 kq4_bload8s(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, voff, (int)soff, 0);
+  return make_uint2((uint32_t)v[0], (uint32_t)v[1]);
+}
+KQ4_DEV uint32_t kq4_bload4s(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, voff, (int)soff, 0);
+}
 
 // ---- stream layout of the device weights -------------------------------------------------
 // A q4 matrix lives in HBM as 9216-B chunks, one per (32-row set, 16-block stage), in

@@ -107,7 +107,56 @@ __global__ __launch_bounds__(256, 2) void kq4_gemm_kernel(
   const __amdgpu_buffer_rsrc_t rx = kq4_rsrc(
       act.xd, (uint32_t)(((n_tok - 1) * act.d_ts + (long)(nb - 1) * act.d_bs + 1) * 4));
   const __amdgpu_buffer_rsrc_t rw = kq4_rsrc(w, wbytes);
+  // q4 weights: the offsets of a stage's loads are a per-thread part, computed once here, plus
+  // a wave-uniform part per stage (the buffer instructions' scalar offset), so issuing a stage's
+  // loads costs no vector arithmetic (the waves' VALU issue slots are the epilogue's). Every
+  // address stays inside its buffer whether or not the hardware's range check counts the scalar
+  // offset: the per-thread part alone is past the end for what must read zero, and the scalar
+  // part never carries an address past the end.
+  //  - activations (token-major, checked by the launcher): a token past n_tok starts past its
+  //    buffer's end; a block past nb (a last stage that overhangs K) is clamped to block nb-1,
+  //    whose finite codes and scale meet that block's zero weights and zero scale;
+  //  - weights: a row set past the matrix starts past the weights' end; the scalar part stays
+  //    inside a row set's stripe of nst stages.
+  uint32_t va = 0, vs = 0, vb[NB], vx[KQ4_GEMM_KB * KQ4_GEMM_BM / 256];
+  int xbl[KQ4_GEMM_KB * KQ4_GEMM_BM / 256];   // wave-uniform block of the stage per scale load
+  if constexpr (WF == 0) {
+    va = (uint32_t)((m0 + (t >> 1)) * act.q_ts + (t & 1) * 16);
+#pragma unroll
+    for (int u = 0; u < NB; ++u) {
+      const int idx = t + 256 * u;
+      const int ln = idx & 63, iu = (idx >> 6) & 1, sl = idx >> 7;
+      const int rl = 32 * sl + (ln & 31), h = ln >> 5;
+      vb[u] = (uint32_t)((size_t)((n0 + rl) >> 5) * nst * KQ4_STREAM_CHUNK + 1024 * iu +
+                         16 * ((rl & 31) + 32 * h));
+    }
+    vs = (uint32_t)((size_t)((n0 + t) >> 5) * nst * KQ4_STREAM_CHUNK + 8192 + 16 * (t & 31));
+#pragma unroll
+    for (int u = 0; u < KQ4_GEMM_KB * KQ4_GEMM_BM / 256; ++u) {
+      const int c = t + 256 * u;
+      vx[u] = (uint32_t)((m0 + c % KQ4_GEMM_BM) * act.d_ts * 4);
+      xbl[u] = __builtin_amdgcn_readfirstlane(c / KQ4_GEMM_BM);   // BM is a multiple of 64
+    }
+  }
   auto load = [&](Regs &rg, int b0) {
+    if constexpr (WF == 0) {
+      if (t < 2 * KQ4_GEMM_BM) {   // a whole wave's choice
+#pragma unroll
+        for (int u = 0; u < KQ4_GEMM_KB; ++u)
+          rg.a[u] = kq4_bload16s(ra, va, (uint32_t)(min(b0 + u, nb - 1) * act.q_bs));
+      }
+      const uint32_t sw = (uint32_t)((b0 >> 4) * KQ4_STREAM_CHUNK + 1024 * ((b0 & 15) >> 1));
+#pragma unroll
+      for (int u = 0; u < NB; ++u) rg.b[u] = kq4_bload16s(rw, vb[u], sw);
+      if (t < KQ4_GEMM_BN)   // a whole wave's choice
+        rg.sw = kq4_bload8s(rw, vs, (uint32_t)((b0 >> 4) * KQ4_STREAM_CHUNK +
+                                               512 * ((b0 & 15) >> 3) + 2 * (b0 & 7)));
+#pragma unroll
+      for (int u = 0; u < KQ4_GEMM_KB * KQ4_GEMM_BM / 256; ++u)
+        rg.x[u] = __uint_as_float(
+            kq4_bload4s(rx, vx[u], (uint32_t)(min(b0 + xbl[u], nb - 1) * act.d_bs * 4)));
+      return;
+    }
 #pragma unroll
     for (int u = 0; u < KQ4_GEMM_KB; ++u) {
       const int tok = t >> 1, hh = t & 1;
@@ -185,7 +234,7 @@ __global__ __launch_bounds__(256, 2) void kq4_gemm_kernel(
   // The C-tile chain keeps two accumulator sets; it has no registers left for the prefetch and
   // loads each stage just before storing it.
   constexpr bool PREFETCH = CHAIN != KQ4_CHAIN_CTILE;
-  Regs rg;
+  Regs rg{};
   if (PREFETCH) load(rg, 0);
   for (int b0 = 0; b0 < nb; b0 += KQ4_GEMM_KB) {
     __syncthreads();              // the previous stage's compute is done with the LDS tiles
@@ -568,9 +617,14 @@ int kq4_launch_gemm(float *out, const float *res, const uint8_t *w, const KQ4Gem
   if (chain == KQ4_CHAIN_CTILE && pick == 1) pick = 2;
   // 32-bit buffer offsets: weights and activation operands below 4 GB
   const size_t wb = wf ? kq8_stream_bytes(rows, cols) : kq4_stream_bytes(rows, cols);
-  const long ab = (n_tok - 1) * act.q_ts + (long)(nb - 1) * act.q_bs + 32;
-  const long db = ((n_tok - 1) * act.d_ts + (long)(nb - 1) * act.d_bs + 1) * 4;
+  // (the last token tile's padding tokens, up to 127 past n_tok, address past the buffers' ends)
+  const long ab = (n_tok + 127) * act.q_ts + (long)(nb - 1) * act.q_bs + 32;
+  const long db = ((n_tok + 127) * act.d_ts + (long)(nb - 1) * act.d_bs + 1) * 4;
   if (wb >= KQ4_OOB || ab >= (long)KQ4_OOB || db >= (long)KQ4_OOB) return (int)hipErrorInvalidValue;
+  // token-major activations: token t+1 starts past token t's last block (the q4 kernel's
+  // zero reads for padding tokens rest on it)
+  if (act.q_ts < (nb - 1) * act.q_bs + 32 || act.d_ts < (nb - 1) * act.d_bs + 1)
+    return (int)hipErrorInvalidValue;
   const uint32_t wbytes = (uint32_t)wb;
   hipError_t e;
   if (pick == 1) e = gemm_launch<2, 2>(out, res, w, act, rows, n_tok, nb, nst, chain, wf, wbytes, s);

@@ -87,7 +87,8 @@ int kq4_launch_block_sums(int32_t *s_lo, int32_t *s_hi, const int8_t *xq, const 
 
 // Prefill GEMM (int8 MFMA) with the exact reference chain `chain` (ASM, GEMV32 or CTILE) for
 // tokens [0, n_tok). Activation (token t, block b) is at xq + t*q_ts + b*q_bs (bytes) and its
-// scale at xd + t*d_ts + b*d_bs, so token-major and block-major layouts both work.
+// scale at xd + t*d_ts + b*d_bs; the layout must be token-major (q_ts >= (nb-1)*q_bs + 32 and
+// d_ts >= (nb-1)*d_bs + 1), which the launcher checks.
 struct KQ4GemmAct {
   const int8_t *xq;
   long q_ts, q_bs;
