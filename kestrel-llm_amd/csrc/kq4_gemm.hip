@@ -243,7 +243,77 @@ __global__ __launch_bounds__(256, 2) void kq4_gemm_kernel(
     __syncthreads();
     if (PREFETCH && b0 + KQ4_GEMM_KB < nb) load(rg, b0 + KQ4_GEMM_KB);   // during the compute
 
-    // ---- compute: per block, 2 x 2 MFMA tiles per wave + exact per-block epilogue
+    // ---- compute: per block, TM x TN MFMA tiles per wave + exact per-block epilogue
+    if constexpr (CHAIN != KQ4_CHAIN_CTILE && WF == 0 && TM == 2) {
+      // Software-pipelined over the stage's blocks, tiles in the order q = NT*bl + k: the
+      // integer MFMA of tile q+1 is issued before tile q's epilogue (two sum slots alternate),
+      // and a row tile's scale products for the next block are issued right after that row
+      // tile's second (last) epilogue of the current block. Each MFMA result is first read one
+      // or two tile epilogues (32 VALU instructions each) after its issue, so the matrix core's
+      // latency hides behind the wave's own VALU work (2.5 % at M = 2048 against the in-order
+      // form); scheduling barriers keep that order. Only for two token tiles: with one, the
+      // second scale set it needs costs the third wave per SIMD that its register count allows.
+      constexpr int NT = 2 * TN;              // MFMA tiles per wave and block: k = i + 2 * jn
+      constexpr int NQ = KQ4_GEMM_KB * NT;
+      kq4_v4i af[2], bf[TN];
+      float xv, wv[TN];
+      kq4_v16i sacc[2];
+      kq4_v32f sc[TN];
+      const kq4_v16i zero = {0};
+      const kq4_v32f z32 = {0};
+      auto frag_ab = [&](int bl) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+          af[i] = *reinterpret_cast<const kq4_v4i *>(
+              &sA[bl][(64 * wm + 32 * i + l32) * KQ4_LDS_ROW + 16 * half]);
+#pragma unroll
+        for (int jn = 0; jn < TN; ++jn)
+          bf[jn] = *reinterpret_cast<const kq4_v4i *>(
+              &sB[bl][(32 * TN * wn + 32 * jn + l32) * KQ4_LDS_ROW + 16 * half]);
+      };
+      auto frag_s = [&](int bl) {
+        xv = sX[bl][64 * wm + lane];
+#pragma unroll
+        for (int jn = 0; jn < TN; ++jn) wv[jn] = sW[bl][32 * TN * wn + 32 * jn + l32];
+      };
+      // Scale products fl(wd * xs) from the matrix core: v_mfma_f32_32x32x1_2b_f32 is a rank-1
+      // update of two 32 x 32 blocks, each output one product rounded once (with a zero
+      // addend), in the MFMA output layout; its blocks are the two token tiles of row tile jn.
+      auto issue_sc = [&](int jn) {
+        sc[jn] = __builtin_amdgcn_mfma_f32_32x32x1f32(xv, wv[jn], z32, 0, 0, 0);
+      };
+      auto issue_s = [&](int q) {
+        const int k = q % NT;
+        sacc[q & 1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[k & 1], bf[k >> 1], zero, 0, 0, 0);
+      };
+      auto epi = [&](int q) {
+        const int k = q % NT, i = k & 1, jn = k >> 1;
+#pragma unroll
+        for (int v = 0; v < 16; ++v)
+          acc[i][jn][v] = fmaf((float)sacc[q & 1][v], sc[jn][16 * i + v], acc[i][jn][v]);
+      };
+      frag_s(0);
+      frag_ab(0);
+#pragma unroll
+      for (int jn = 0; jn < TN; ++jn) issue_sc(jn);
+      issue_s(0);
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) {
+        const int bl = q / NT, k = q % NT;
+        __builtin_amdgcn_sched_barrier(0);
+        if (k == 0 && bl + 1 < KQ4_GEMM_KB) frag_s(bl + 1);
+        if (q + 1 < NQ) {
+          issue_s(q + 1);
+          // the fragments of tile q+1's block are done with once its block's last tile is issued
+          if ((q + 1) % NT == NT - 1 && (q + 1) / NT + 1 < KQ4_GEMM_KB) frag_ab((q + 1) / NT + 1);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        epi(q);
+        __builtin_amdgcn_sched_barrier(0);
+        if (bl + 1 < KQ4_GEMM_KB && (k & 1)) issue_sc(k >> 1);
+      }
+      continue;
+    }
 #pragma unroll
     for (int bl = 0; bl < KQ4_GEMM_KB; ++bl) {
       kq4_v4i af[TM], bf[TN];
