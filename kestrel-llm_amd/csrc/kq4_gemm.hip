@@ -138,6 +138,29 @@ __global__ __launch_bounds__(256, 2) void kq4_gemm_kernel(
       xbl[u] = __builtin_amdgcn_readfirstlane(c / KQ4_GEMM_BM);   // BM is a multiple of 64
     }
   }
+  // The two-token-tile q4 form issues a stage's loads one at a time between the tile epilogues
+  // of the previous stage's compute (piece p after epilogue p): issued all at once, the eight
+  // waves of a CU queue 72 loads at the address unit and each wave stalls there for about a
+  // tenth of the stage. Weights first (the longest way), then row scales (every wave: waves
+  // past BN read rows they do not store), activations, token scales.
+  constexpr int NX = KQ4_GEMM_KB * KQ4_GEMM_BM / 256;
+  constexpr int NPIECE = NB + 1 + KQ4_GEMM_KB + NX;
+  auto load_piece = [&](Regs &rg, int b0, int p) {
+    if (p < NB) {
+      rg.b[p] = kq4_bload16s(rw, vb[p], (uint32_t)((b0 >> 4) * KQ4_STREAM_CHUNK +
+                                                   1024 * ((b0 & 15) >> 1)));
+    } else if (p == NB) {
+      rg.sw = kq4_bload8s(rw, vs, (uint32_t)((b0 >> 4) * KQ4_STREAM_CHUNK +
+                                             512 * ((b0 & 15) >> 3) + 2 * (b0 & 7)));
+    } else if (p < NB + 1 + KQ4_GEMM_KB) {
+      const int u = p - NB - 1;
+      rg.a[u] = kq4_bload16s(ra, va, (uint32_t)(min(b0 + u, nb - 1) * act.q_bs));
+    } else {
+      const int u = p - NB - 1 - KQ4_GEMM_KB;
+      rg.x[u] = __uint_as_float(
+          kq4_bload4s(rx, vx[u], (uint32_t)(min(b0 + xbl[u], nb - 1) * act.d_bs * 4)));
+    }
+  };
   auto load = [&](Regs &rg, int b0) {
     if constexpr (WF == 0) {
       if (t < 2 * KQ4_GEMM_BM) {   // a whole wave's choice
@@ -234,6 +257,8 @@ __global__ __launch_bounds__(256, 2) void kq4_gemm_kernel(
   // The C-tile chain keeps two accumulator sets; it has no registers left for the prefetch and
   // loads each stage just before storing it.
   constexpr bool PREFETCH = CHAIN != KQ4_CHAIN_CTILE;
+  constexpr bool ROT = CHAIN != KQ4_CHAIN_CTILE && WF == 0 && TM == 2;
+  const int lastb = (nb - 1) / KQ4_GEMM_KB * KQ4_GEMM_KB;   // the last stage's first block
   Regs rg{};
   if (PREFETCH) load(rg, 0);
   for (int b0 = 0; b0 < nb; b0 += KQ4_GEMM_KB) {
@@ -241,10 +266,12 @@ __global__ __launch_bounds__(256, 2) void kq4_gemm_kernel(
     if (!PREFETCH) load(rg, b0);
     store(rg);
     __syncthreads();
-    if (PREFETCH && b0 + KQ4_GEMM_KB < nb) load(rg, b0 + KQ4_GEMM_KB);   // during the compute
+    // during the compute (spread over it for ROT, where the last stage reloads itself: unused)
+    if (!ROT && PREFETCH && b0 + KQ4_GEMM_KB < nb) load(rg, b0 + KQ4_GEMM_KB);
+    [[maybe_unused]] const int bn = min(b0 + KQ4_GEMM_KB, lastb);
 
     // ---- compute: per block, TM x TN MFMA tiles per wave + exact per-block epilogue
-    if constexpr (CHAIN != KQ4_CHAIN_CTILE && WF == 0 && TM == 2) {
+    if constexpr (ROT) {
       // Software-pipelined over the stage's blocks, tiles in the order q = NT*bl + k: the
       // integer MFMA of tile q+1 is issued before tile q's epilogue (two sum slots alternate),
       // and a row tile's scale products for the next block are issued right after that row
@@ -255,6 +282,7 @@ __global__ __launch_bounds__(256, 2) void kq4_gemm_kernel(
       // second scale set it needs costs the third wave per SIMD that its register count allows.
       constexpr int NT = 2 * TN;              // MFMA tiles per wave and block: k = i + 2 * jn
       constexpr int NQ = KQ4_GEMM_KB * NT;
+      static_assert(NPIECE <= NQ, "a stage's loads must fit between its tile epilogues");
       kq4_v4i af[2], bf[TN];
       float xv, wv[TN];
       kq4_v16i sacc[2];
@@ -311,6 +339,7 @@ __global__ __launch_bounds__(256, 2) void kq4_gemm_kernel(
         epi(q);
         __builtin_amdgcn_sched_barrier(0);
         if (bl + 1 < KQ4_GEMM_KB && (k & 1)) issue_sc(k >> 1);
+        if (q < NPIECE) load_piece(rg, bn, q);
       }
       continue;
     }
