@@ -50,10 +50,23 @@ __global__ __launch_bounds__(256, 2) void kq4_gemm_kernel(
     const KQ4GemmAct act, int rows, int n_tok, int nb, int nst, int mtiles, int ntiles,
     uint32_t wbytes) {
   constexpr int KQ4_GEMM_BM = 64 * TM, KQ4_GEMM_BN = 64 * TN;
-  __shared__ __align__(16) int8_t sA[KQ4_GEMM_KB][KQ4_GEMM_BM * KQ4_LDS_ROW];
-  __shared__ __align__(16) int8_t sB[KQ4_GEMM_KB][KQ4_GEMM_BN * KQ4_LDS_ROW];
-  __shared__ __align__(16) float sW[KQ4_GEMM_KB][KQ4_GEMM_BN];
-  __shared__ __align__(16) float sX[KQ4_GEMM_KB][KQ4_GEMM_BM];
+  // ROT: the two-token-tile q4 form, software-pipelined (see the compute below). It keeps two
+  // stages in LDS at a 32-B row pitch, the two 16-B halves of row r swapped when bit 3 of r is
+  // set (so the 16-B fragment reads and the stores stay bank-conflict free without padding):
+  // 2 x 36 KB, two workgroups per CU. The other forms stage once at a 48-B pitch.
+  constexpr bool ROT = CHAIN != KQ4_CHAIN_CTILE && WF == 0 && TM == 2 && TN == 2;
+  constexpr int PITCH = ROT ? 32 : KQ4_LDS_ROW;
+  struct Stage {
+    int8_t a[KQ4_GEMM_KB][KQ4_GEMM_BM * PITCH];
+    int8_t b[KQ4_GEMM_KB][KQ4_GEMM_BN * PITCH];
+    float w[KQ4_GEMM_KB][KQ4_GEMM_BN];
+    float x[KQ4_GEMM_KB][KQ4_GEMM_BM];
+  };
+  __shared__ __align__(16) Stage stg[ROT ? 2 : 1];
+  auto &sA = stg[0].a;
+  auto &sB = stg[0].b;
+  auto &sW = stg[0].w;
+  auto &sX = stg[0].x;
 
   // XCD-aware tile order: workgroup ids go round-robin over the 8 XCDs; give XCD x the
   // contiguous tile range [start(x), start(x) + count(x)) (a bijection for any tile count).
@@ -130,7 +143,10 @@ __global__ __launch_bounds__(256, 2) void kq4_gemm_kernel(
       vb[u] = (uint32_t)((size_t)((n0 + rl) >> 5) * nst * KQ4_STREAM_CHUNK + 1024 * iu +
                          16 * ((rl & 31) + 32 * h));
     }
-    vs = (uint32_t)((size_t)((n0 + t) >> 5) * nst * KQ4_STREAM_CHUNK + 8192 + 16 * (t & 31));
+    // (ROT: thread t takes the scales of blocks 2*(t/128), +1 of row t%128: 4 B)
+    const int sr = ROT ? (t & 127) : t;
+    vs = (uint32_t)((size_t)((n0 + sr) >> 5) * nst * KQ4_STREAM_CHUNK + 8192 + 16 * (sr & 31) +
+                    (ROT ? 4 * (t >> 7) : 0));
 #pragma unroll
     for (int u = 0; u < KQ4_GEMM_KB * KQ4_GEMM_BM / 256; ++u) {
       const int c = t + 256 * u;
@@ -138,11 +154,12 @@ __global__ __launch_bounds__(256, 2) void kq4_gemm_kernel(
       xbl[u] = __builtin_amdgcn_readfirstlane(c / KQ4_GEMM_BM);   // BM is a multiple of 64
     }
   }
-  // The two-token-tile q4 form issues a stage's loads one at a time between the tile epilogues
-  // of the previous stage's compute (piece p after epilogue p): issued all at once, the eight
-  // waves of a CU queue 72 loads at the address unit and each wave stalls there for about a
-  // tenth of the stage. Weights first (the longest way), then row scales (every wave: waves
-  // past BN read rows they do not store), activations, token scales.
+  // ROT moves a stage from global memory to registers and from registers to LDS in pieces, one
+  // piece between two tile epilogues of the compute (piece p after epilogue p): issued all at
+  // once after a barrier, the eight waves of a CU queue 72 loads at the address unit and each
+  // wave stalls there for about a tenth of the stage. Weights first (the longest way), then row
+  // scales, activations, token scales. No piece branches on the thread (a branch there costs
+  // the pipelined compute ~30 registers).
   constexpr int NX = KQ4_GEMM_KB * KQ4_GEMM_BM / 256;
   constexpr int NPIECE = NB + 1 + KQ4_GEMM_KB + NX;
   auto load_piece = [&](Regs &rg, int b0, int p) {
@@ -150,8 +167,8 @@ __global__ __launch_bounds__(256, 2) void kq4_gemm_kernel(
       rg.b[p] = kq4_bload16s(rw, vb[p], (uint32_t)((b0 >> 4) * KQ4_STREAM_CHUNK +
                                                    1024 * ((b0 & 15) >> 1)));
     } else if (p == NB) {
-      rg.sw = kq4_bload8s(rw, vs, (uint32_t)((b0 >> 4) * KQ4_STREAM_CHUNK +
-                                             512 * ((b0 & 15) >> 3) + 2 * (b0 & 7)));
+      rg.sw.x = kq4_bload4s(rw, vs, (uint32_t)((b0 >> 4) * KQ4_STREAM_CHUNK +
+                                               512 * ((b0 & 15) >> 3) + 2 * (b0 & 7)));
     } else if (p < NB + 1 + KQ4_GEMM_KB) {
       const int u = p - NB - 1;
       rg.a[u] = kq4_bload16s(ra, va, (uint32_t)(min(b0 + u, nb - 1) * act.q_bs));
@@ -159,6 +176,34 @@ __global__ __launch_bounds__(256, 2) void kq4_gemm_kernel(
       const int u = p - NB - 1 - KQ4_GEMM_KB;
       rg.x[u] = __uint_as_float(
           kq4_bload4s(rx, vx[u], (uint32_t)(min(b0 + xbl[u], nb - 1) * act.d_bs * 4)));
+    }
+  };
+  // ROT: piece p of a stage from registers into LDS stage buffer S (same piece order).
+  auto swz = [](int row, int hh) { return 16 * (hh ^ ((row >> 3) & 1)); };
+  auto store_piece = [&](const Regs &rg, Stage &S, int p) {
+    if (p < NB) {
+      const int idx = t + 256 * p;
+      const int ln = idx & 63, iu = (idx >> 6) & 1, sl = idx >> 7;
+      const int rl = 32 * sl + (ln & 31), h = ln >> 5;
+      uint32_t o[4];
+      kq4_unpack_half(rg.b[p].x, rg.b[p].y, o);
+      *reinterpret_cast<uint4 *>(&S.b[2 * iu][rl * PITCH + swz(rl, h)]) =
+          make_uint4(o[0], o[1], o[2], o[3]);
+      kq4_unpack_half(rg.b[p].z, rg.b[p].w, o);
+      *reinterpret_cast<uint4 *>(&S.b[2 * iu + 1][rl * PITCH + swz(rl, h)]) =
+          make_uint4(o[0], o[1], o[2], o[3]);
+    } else if (p == NB) {      // no branch: every thread stores two (q4 enters as 16*(n-8))
+      const int j = 2 * (t >> 7);
+      S.w[j][t & 127] = kq4_h2f(rg.sw.x) * 0.0625f;
+      S.w[j + 1][t & 127] = kq4_h2f(rg.sw.x >> 16) * 0.0625f;
+    } else if (p < NB + 1 + KQ4_GEMM_KB) {
+      const int u = p - NB - 1, r = t >> 1;   // BM = 128: every thread holds a half row
+      *reinterpret_cast<uint4 *>(&S.a[u][r * PITCH + swz(r, t & 1)]) = rg.a[u];
+    } else {
+      const int u = p - NB - 1 - KQ4_GEMM_KB, c = t + 256 * u;
+      // ASM chain: the reference multiplies by the f16-rounded activation scale
+      S.x[c / KQ4_GEMM_BM][c % KQ4_GEMM_BM] =
+          CHAIN == KQ4_CHAIN_ASM ? kq4_f16_round(rg.x[u]) : rg.x[u];
     }
   };
   auto load = [&](Regs &rg, int b0) {
@@ -257,21 +302,23 @@ __global__ __launch_bounds__(256, 2) void kq4_gemm_kernel(
   // The C-tile chain keeps two accumulator sets; it has no registers left for the prefetch and
   // loads each stage just before storing it.
   constexpr bool PREFETCH = CHAIN != KQ4_CHAIN_CTILE;
-  constexpr bool ROT = CHAIN != KQ4_CHAIN_CTILE && WF == 0 && TM == 2;
   const int lastb = (nb - 1) / KQ4_GEMM_KB * KQ4_GEMM_KB;   // the last stage's first block
   Regs rg{};
-  if (PREFETCH) load(rg, 0);
-  for (int b0 = 0; b0 < nb; b0 += KQ4_GEMM_KB) {
-    __syncthreads();              // the previous stage's compute is done with the LDS tiles
-    if (!PREFETCH) load(rg, b0);
-    store(rg);
+  if constexpr (ROT) {
+    // Stage s is computed from LDS buffer s%2 while stage s+1 moves from registers into buffer
+    // (s+1)%2 and stage s+2 from global memory into the registers, piece by piece between the
+    // tile epilogues; one barrier per stage. The last stages reload the last one (unused), so
+    // every issue is unconditional.
+#pragma unroll
+    for (int p = 0; p < NPIECE; ++p) load_piece(rg, 0, p);
+#pragma unroll
+    for (int p = 0; p < NPIECE; ++p) store_piece(rg, stg[0], p);
     __syncthreads();
-    // during the compute (spread over it for ROT, where the last stage reloads itself: unused)
-    if (!ROT && PREFETCH && b0 + KQ4_GEMM_KB < nb) load(rg, b0 + KQ4_GEMM_KB);
-    [[maybe_unused]] const int bn = min(b0 + KQ4_GEMM_KB, lastb);
-
-    // ---- compute: per block, TM x TN MFMA tiles per wave + exact per-block epilogue
-    if constexpr (ROT) {
+#pragma unroll
+    for (int p = 0; p < NPIECE; ++p) load_piece(rg, min(KQ4_GEMM_KB, lastb), p);
+    // (unrolled by two stages, so that each buffer's LDS addresses are constants)
+    auto stage = [&](Stage &C, Stage &N, int b0) __attribute__((always_inline)) {
+      const int bn = min(b0 + 2 * KQ4_GEMM_KB, lastb);
       // Software-pipelined over the stage's blocks, tiles in the order q = NT*bl + k: the
       // integer MFMA of tile q+1 is issued before tile q's epilogue (two sum slots alternate),
       // and a row tile's scale products for the next block are issued right after that row
@@ -293,16 +340,16 @@ __global__ __launch_bounds__(256, 2) void kq4_gemm_kernel(
 #pragma unroll
         for (int i = 0; i < 2; ++i)
           af[i] = *reinterpret_cast<const kq4_v4i *>(
-              &sA[bl][(64 * wm + 32 * i + l32) * KQ4_LDS_ROW + 16 * half]);
+              &C.a[bl][(64 * wm + 32 * i + l32) * PITCH + swz(l32, half)]);
 #pragma unroll
         for (int jn = 0; jn < TN; ++jn)
           bf[jn] = *reinterpret_cast<const kq4_v4i *>(
-              &sB[bl][(32 * TN * wn + 32 * jn + l32) * KQ4_LDS_ROW + 16 * half]);
+              &C.b[bl][(32 * TN * wn + 32 * jn + l32) * PITCH + swz(l32, half)]);
       };
       auto frag_s = [&](int bl) {
-        xv = sX[bl][64 * wm + lane];
+        xv = C.x[bl][64 * wm + lane];
 #pragma unroll
-        for (int jn = 0; jn < TN; ++jn) wv[jn] = sW[bl][32 * TN * wn + 32 * jn + l32];
+        for (int jn = 0; jn < TN; ++jn) wv[jn] = C.w[bl][32 * TN * wn + 32 * jn + l32];
       };
       // Scale products fl(wd * xs) from the matrix core: v_mfma_f32_32x32x1_2b_f32 is a rank-1
       // update of two 32 x 32 blocks, each output one product rounded once (with a zero
@@ -339,70 +386,88 @@ __global__ __launch_bounds__(256, 2) void kq4_gemm_kernel(
         epi(q);
         __builtin_amdgcn_sched_barrier(0);
         if (bl + 1 < KQ4_GEMM_KB && (k & 1)) issue_sc(k >> 1);
-        if (q < NPIECE) load_piece(rg, bn, q);
+        if (q < NPIECE) {
+          store_piece(rg, N, q);
+          load_piece(rg, bn, q);
+        }
       }
-      continue;
+      __syncthreads();
+    };
+    for (int b0 = 0; b0 < nb; b0 += 2 * KQ4_GEMM_KB) {
+      stage(stg[0], stg[1], b0);
+      if (b0 + KQ4_GEMM_KB < nb) stage(stg[1], stg[0], b0 + KQ4_GEMM_KB);
     }
+  } else {
+    if (PREFETCH) load(rg, 0);
+    for (int b0 = 0; b0 < nb; b0 += KQ4_GEMM_KB) {
+      __syncthreads();              // the previous stage's compute is done with the LDS tiles
+      if (!PREFETCH) load(rg, b0);
+      store(rg);
+      __syncthreads();
+      if (PREFETCH && b0 + KQ4_GEMM_KB < nb) load(rg, b0 + KQ4_GEMM_KB);   // during the compute
+
+      // ---- compute: per block, TM x TN MFMA tiles per wave + exact per-block epilogue
 #pragma unroll
-    for (int bl = 0; bl < KQ4_GEMM_KB; ++bl) {
-      kq4_v4i af[TM], bf[TN];
+      for (int bl = 0; bl < KQ4_GEMM_KB; ++bl) {
+        kq4_v4i af[TM], bf[TN];
 #pragma unroll
-      for (int i = 0; i < TM; ++i)
-        af[i] = *reinterpret_cast<const kq4_v4i *>(
-            &sA[bl][(32 * TM * wm + 32 * i + l32) * KQ4_LDS_ROW + 16 * half]);
-#pragma unroll
-      for (int jn = 0; jn < TN; ++jn)
-        bf[jn] = *reinterpret_cast<const kq4_v4i *>(
-            &sB[bl][(32 * TN * wn + 32 * jn + l32) * KQ4_LDS_ROW + 16 * half]);
-      // Scale products fl(wd * xs) from the matrix core: v_mfma_f32_32x32x1_2b_f32 is a rank-1
-      // update of two 32 x 32 blocks, each output one product rounded once (with a zero
-      // addend), in the MFMA output layout. With two token tiles its blocks are the tiles of
-      // one row tile (one product set per jn); with one token tile they are the two row tiles.
-      const kq4_v32f z32 = {0};
-      kq4_v32f sc[TM == 2 ? TN : 1];
-      if constexpr (TM == 2) {
-        const float xv = sX[bl][64 * wm + lane];
+        for (int i = 0; i < TM; ++i)
+          af[i] = *reinterpret_cast<const kq4_v4i *>(
+              &sA[bl][(32 * TM * wm + 32 * i + l32) * KQ4_LDS_ROW + 16 * half]);
 #pragma unroll
         for (int jn = 0; jn < TN; ++jn)
-          sc[jn] = __builtin_amdgcn_mfma_f32_32x32x1f32(
-              xv, sW[bl][32 * TN * wn + 32 * jn + l32], z32, 0, 0, 0);
-      } else {
-        const float xv = sX[bl][32 * wm + l32];
-        const float wv = sW[bl][32 * TN * wn + (TN == 2 ? lane : l32)];
-        sc[0] = __builtin_amdgcn_mfma_f32_32x32x1f32(xv, wv, z32, 0, 0, 0);
-      }
-      const kq4_v16i zero = {0};
+          bf[jn] = *reinterpret_cast<const kq4_v4i *>(
+              &sB[bl][(32 * TN * wn + 32 * jn + l32) * KQ4_LDS_ROW + 16 * half]);
+        // Scale products fl(wd * xs) from the matrix core: v_mfma_f32_32x32x1_2b_f32 is a rank-1
+        // update of two 32 x 32 blocks, each output one product rounded once (with a zero
+        // addend), in the MFMA output layout. With two token tiles its blocks are the tiles of
+        // one row tile (one product set per jn); with one token tile they are the two row tiles.
+        const kq4_v32f z32 = {0};
+        kq4_v32f sc[TM == 2 ? TN : 1];
+        if constexpr (TM == 2) {
+          const float xv = sX[bl][64 * wm + lane];
 #pragma unroll
-      for (int i = 0; i < TM; ++i)
+          for (int jn = 0; jn < TN; ++jn)
+            sc[jn] = __builtin_amdgcn_mfma_f32_32x32x1f32(
+                xv, sW[bl][32 * TN * wn + 32 * jn + l32], z32, 0, 0, 0);
+        } else {
+          const float xv = sX[bl][32 * wm + l32];
+          const float wv = sW[bl][32 * TN * wn + (TN == 2 ? lane : l32)];
+          sc[0] = __builtin_amdgcn_mfma_f32_32x32x1f32(xv, wv, z32, 0, 0, 0);
+        }
+        const kq4_v16i zero = {0};
 #pragma unroll
-        for (int jn = 0; jn < TN; ++jn) {
-          auto cs = [&](int v) {
-            if constexpr (TM == 2) return sc[jn % (TM == 2 ? TN : 1)][16 * i + v];
-            else return sc[0][16 * jn + v];
-          };
-          if (CHAIN == KQ4_CHAIN_CTILE) {
-            // lane half 0 carries elements 0..15 (low nibbles), half 1 elements 16..31
-            const kq4_v4i z = {0, 0, 0, 0};
-            const kq4_v4i blo = half == 0 ? bf[jn] : z;
-            const kq4_v4i bhi = half == 1 ? bf[jn] : z;
-            const kq4_v16i clo = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], blo, zero, 0, 0, 0);
-            const kq4_v16i chi = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bhi, zero, 0, 0, 0);
+        for (int i = 0; i < TM; ++i)
 #pragma unroll
-            for (int v = 0; v < 16; ++v) {
-              acc[i][jn][v] = fmaf((float)clo[v], cs(v), acc[i][jn][v]);
-              acc_hi[i][jn][v] = fmaf((float)chi[v], cs(v), acc_hi[i][jn][v]);
-            }
-          } else {
-            const kq4_v16i c = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[jn], zero, 0, 0, 0);
+          for (int jn = 0; jn < TN; ++jn) {
+            auto cs = [&](int v) {
+              if constexpr (TM == 2) return sc[jn % (TM == 2 ? TN : 1)][16 * i + v];
+              else return sc[0][16 * jn + v];
+            };
+            if (CHAIN == KQ4_CHAIN_CTILE) {
+              // lane half 0 carries elements 0..15 (low nibbles), half 1 elements 16..31
+              const kq4_v4i z = {0, 0, 0, 0};
+              const kq4_v4i blo = half == 0 ? bf[jn] : z;
+              const kq4_v4i bhi = half == 1 ? bf[jn] : z;
+              const kq4_v16i clo = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], blo, zero, 0, 0, 0);
+              const kq4_v16i chi = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bhi, zero, 0, 0, 0);
 #pragma unroll
-            for (int v = 0; v < 16; ++v) {
-              if (CHAIN == KQ4_CHAIN_Q8GEMM)
-                acc[i][jn][v] = acc[i][jn][v] + cs(v) * (float)c[v];
-              else
-                acc[i][jn][v] = fmaf((float)c[v], cs(v), acc[i][jn][v]);
+              for (int v = 0; v < 16; ++v) {
+                acc[i][jn][v] = fmaf((float)clo[v], cs(v), acc[i][jn][v]);
+                acc_hi[i][jn][v] = fmaf((float)chi[v], cs(v), acc_hi[i][jn][v]);
+              }
+            } else {
+              const kq4_v16i c = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[jn], zero, 0, 0, 0);
+#pragma unroll
+              for (int v = 0; v < 16; ++v) {
+                if (CHAIN == KQ4_CHAIN_Q8GEMM)
+                  acc[i][jn][v] = acc[i][jn][v] + cs(v) * (float)c[v];
+                else
+                  acc[i][jn][v] = fmaf((float)c[v], cs(v), acc[i][jn][v]);
+              }
             }
           }
-        }
+      }
     }
   }
 
