@@ -100,6 +100,27 @@ KQ4_DEV float kq4_quad_max(float v) {
   return v;
 }
 
+// The same maximum for a non-negative, never-NaN v (a block's amax built by fmaxf from 1e-10 or
+// +0): such floats order as their bit patterns, so an integer maximum with the DPP operand folds
+// into one instruction per step (the float form adds a move and a canonicalizing max per step).
+KQ4_DEV float kq4_quad_max_pos(float v) {
+  uint32_t u = __float_as_uint(v);
+  u = max(u, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)u, 0xB1, 0xf, 0xf, false));
+  u = max(u, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)u, 0x4E, 0xf, 0xf, false));
+  return __uint_as_float(u);
+}
+
+// Lane m's value (m = 0..3, a constant after unrolling) broadcast to every lane of its quad.
+KQ4_DEV float kq4_quad_bcast(float v, int m) {
+  const int u = __float_as_int(v);
+  switch (m) {
+    case 0: return __int_as_float(__builtin_amdgcn_update_dpp(0, u, 0x00, 0xf, 0xf, false));
+    case 1: return __int_as_float(__builtin_amdgcn_update_dpp(0, u, 0x55, 0xf, 0xf, false));
+    case 2: return __int_as_float(__builtin_amdgcn_update_dpp(0, u, 0xAA, 0xf, 0xf, false));
+    default: return __int_as_float(__builtin_amdgcn_update_dpp(0, u, 0xFF, 0xf, 0xf, false));
+  }
+}
+
 // 16-byte load with the non-temporal hint (global_load_dwordx4 ... nt), for data read once per
 // launch (weight streams): measured on MI355X, plain streaming reads of 7-56 MB run 9-14 %
 // faster with it than without.

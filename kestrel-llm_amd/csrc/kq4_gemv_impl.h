@@ -246,40 +246,61 @@ KQ4_DEV void kq4_gv_act_put(const KQ4GvAct<M, FQ, WF> &r, const KQ4GemvArgs &a, 
                             uint8_t *sq, float (*sx)[8], int t0) {
   constexpr int CB = KQ4Wf<WF>::CB;
   constexpr float XS = KQ4Wf<WF>::XS;
-  if (FQ) {
+  if constexpr (FQ != 0) {
     const int blk = lane >> 2, qq = lane & 3;
+    static_assert(M <= 4, "one token of a pass per lane of the quad");
+    float v[M][8];
+    float amax[M];
 #pragma unroll
     for (int m = 0; m < M; ++m) {
-      float v[8] = {r.f[2 * m].x, r.f[2 * m].y, r.f[2 * m].z, r.f[2 * m].w,
-                    r.f[2 * m + 1].x, r.f[2 * m + 1].y, r.f[2 * m + 1].z, r.f[2 * m + 1].w};
+      const float f[8] = {r.f[2 * m].x, r.f[2 * m].y, r.f[2 * m].z, r.f[2 * m].w,
+                          r.f[2 * m + 1].x, r.f[2 * m + 1].y, r.f[2 * m + 1].z, r.f[2 * m + 1].w};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[m][i] = f[i];
       if (FQ == 2) {
         const float u[8] = {r.u[2 * m].x, r.u[2 * m].y, r.u[2 * m].z, r.u[2 * m].w,
                             r.u[2 * m + 1].x, r.u[2 * m + 1].y, r.u[2 * m + 1].z, r.u[2 * m + 1].w};
 #pragma unroll
-        for (int i = 0; i < 8; ++i) v[i] = kq4_silu_mul(v[i], u[i]);
+        for (int i = 0; i < 8; ++i) v[m][i] = kq4_silu_mul(v[m][i], u[i]);
       }
-      float amax = 1e-10f;
+      amax[m] = 1e-10f;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
-      amax = kq4_quad_max(amax);
-      const float d = amax / 127.0f;
-      const float y = 1.0f / d;
-      uint32_t pk[2] = {0, 0};
+      for (int i = 0; i < 8; ++i) amax[m] = fmaxf(amax[m], fabsf(v[m][i]));
+      amax[m] = kq4_quad_max_pos(amax[m]);
+    }
+    // The two true divisions of a (block, token) are done once per quad: lane qq of the quad
+    // divides for token qq of the pass, and every lane of the quad takes token m's d and 1/d
+    // from lane m (a DPP broadcast), instead of each lane dividing for every token.
+    float am = amax[0];
+#pragma unroll
+    for (int m = 1; m < M; ++m) am = qq == m ? amax[m] : am;
+    const float dq = am / 127.0f;
+    const float yq = 1.0f / dq;
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      const float d = M == 1 ? dq : kq4_quad_bcast(dq, m);
+      const float y = M == 1 ? yq : kq4_quad_bcast(yq, m);
+      int c[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        float q = v[i] * y;
-        const float e = fmaf(-q, d, v[i]);
+        float q = v[m][i] * y;
+        const float e = fmaf(-q, d, v[m][i]);
         q = fmaf(e, y, q);
-        int c = (int)(q + 0.5f);
-        c = c > 127 ? 127 : (c < -127 ? -127 : c);
-        pk[i >> 2] |= ((uint32_t)c & 0xFFu) << (8 * (i & 3));
+        c[i] = (int)(q + 0.5f);
+        c[i] = c[i] > 127 ? 127 : (c[i] < -127 ? -127 : c[i]);
       }
-      if (blk < CB) {   // q8 stages have 8 blocks: lanes 32-63 hold nothing
+      // low bytes of c[0..3], c[4..7] into one dword each: two byte selects and an or
+      uint32_t pk[2];
+#pragma unroll
+      for (int k = 0; k < 2; ++k)
+        pk[k] = __builtin_amdgcn_perm((uint32_t)c[4 * k + 1], (uint32_t)c[4 * k], 0x0c0c0400u) |
+                __builtin_amdgcn_perm((uint32_t)c[4 * k + 3], (uint32_t)c[4 * k + 2], 0x04000c0cu);
+      if (blk < CB)   // q8 stages have 8 blocks: lanes 32-63 hold nothing
         *reinterpret_cast<uint2 *>(sq + (t0 + m) * KQ4_GV_QTS + kq4_gv_qpos(blk) + 8 * qq) =
             make_uint2(pk[0], pk[1]);
-        if (qq == 0) sx[blk][t0 + m] = ((t0 + m < a.asm_tokens) ? kq4_f16_round(d) : d) * XS;
-      }
     }
+    if (blk < CB && qq < M)
+      sx[blk][t0 + qq] = ((t0 + qq < a.asm_tokens) ? kq4_f16_round(dq) : dq) * XS;
   } else {
 #pragma unroll
     for (int c = 0; c < KQ4GvAct<M, FQ, WF>::NQ; ++c) {
@@ -485,7 +506,10 @@ __global__ __launch_bounds__(R > 1 ? 512 : 1024) void kq4_gemv_kernel(const KQ4G
     kq4_gv_load<HS, WF>(rw[0], wb + ((size_t)set0 * nst + st) * CHUNK, rr, h, p);
     // One token, fp32 activations: every load is issued before the quantization waits for the
     // activations (the compiler otherwise sinks the weight loads below it, and the two memory
-    // latencies add up).
+    // latencies add up). Not from two tokens on: there, issuing the weights before the
+    // quantization costs a wave per SIMD (110-120 VGPRs instead of 82-83 at four tokens) and
+    // measured slower for every Qwen3-8B decode shape (8B gate/up at 2 tokens 12.15 -> 13.0 us),
+    // faster only for the 2B QKV and O launches (one workgroup per CU: 4.7 -> 4.1 us at 4 tokens).
     if constexpr (M == 1 && FQ == 1) __builtin_amdgcn_sched_barrier(0);
     kq4_gv_act_put<MQ, FQ, WF>(ra, a, lane, sq, sx, 0);
 #pragma unroll
