@@ -50,11 +50,11 @@ __global__ __launch_bounds__(256, 2) void kq4_gemm_kernel(
     const KQ4GemmAct act, int rows, int n_tok, int nb, int nst, int mtiles, int ntiles,
     uint32_t wbytes) {
   constexpr int KQ4_GEMM_BM = 64 * TM, KQ4_GEMM_BN = 64 * TN;
-  // ROT: the two-token-tile q4 form, software-pipelined (see the compute below). It keeps two
+  // ROT: the two-token-tile form, software-pipelined (see the compute below). It keeps two
   // stages in LDS at a 32-B row pitch, the two 16-B halves of row r swapped when bit 3 of r is
   // set (so the 16-B fragment reads and the stores stay bank-conflict free without padding):
   // 2 x 36 KB, two workgroups per CU. The other forms stage once at a 48-B pitch.
-  constexpr bool ROT = CHAIN != KQ4_CHAIN_CTILE && WF == 0 && TM == 2 && TN == 2;
+  constexpr bool ROT = CHAIN != KQ4_CHAIN_CTILE && TM == 2 && TN == 2;
   constexpr int PITCH = ROT ? 32 : KQ4_LDS_ROW;
   struct Stage {
     int8_t a[KQ4_GEMM_KB][KQ4_GEMM_BM * PITCH];
@@ -120,7 +120,8 @@ __global__ __launch_bounds__(256, 2) void kq4_gemm_kernel(
   const __amdgpu_buffer_rsrc_t rx = kq4_rsrc(
       act.xd, (uint32_t)(((n_tok - 1) * act.d_ts + (long)(nb - 1) * act.d_bs + 1) * 4));
   const __amdgpu_buffer_rsrc_t rw = kq4_rsrc(w, wbytes);
-  // q4 weights: the offsets of a stage's loads are a per-thread part, computed once here, plus
+  // q4 weights, and q8 weights in ROT: the offsets of a stage's loads are a per-thread part,
+  // computed once here, plus
   // a wave-uniform part per stage (the buffer instructions' scalar offset), so issuing a stage's
   // loads costs no vector arithmetic (the waves' VALU issue slots are the epilogue's). Every
   // address stays inside its buffer whether or not the hardware's range check counts the scalar
@@ -133,19 +134,22 @@ __global__ __launch_bounds__(256, 2) void kq4_gemm_kernel(
   //    inside a row set's stripe of nst stages.
   uint32_t va = 0, vs = 0, vb[NB], vx[KQ4_GEMM_KB * KQ4_GEMM_BM / 256];
   int xbl[KQ4_GEMM_KB * KQ4_GEMM_BM / 256];   // wave-uniform block of the stage per scale load
-  if constexpr (WF == 0) {
+  if constexpr (WF == 0 || ROT) {
+    constexpr int CHUNK = WF ? KQ8_STREAM_CHUNK : KQ4_STREAM_CHUNK;
     va = (uint32_t)((m0 + (t >> 1)) * act.q_ts + (t & 1) * 16);
 #pragma unroll
     for (int u = 0; u < NB; ++u) {
+      // q4: (set sl, nibble unit iu = 2 blocks, lane ln); q8: (set sl, block iu, lane ln)
       const int idx = t + 256 * u;
-      const int ln = idx & 63, iu = (idx >> 6) & 1, sl = idx >> 7;
+      const int ln = idx & 63, iu = WF ? (idx >> 6) & 3 : (idx >> 6) & 1;
+      const int sl = WF ? idx >> 8 : idx >> 7;
       const int rl = 32 * sl + (ln & 31), h = ln >> 5;
-      vb[u] = (uint32_t)((size_t)((n0 + rl) >> 5) * nst * KQ4_STREAM_CHUNK + 1024 * iu +
+      vb[u] = (uint32_t)((size_t)((n0 + rl) >> 5) * nst * CHUNK + 1024 * iu +
                          16 * ((rl & 31) + 32 * h));
     }
     // (ROT: thread t takes the scales of blocks 2*(t/128), +1 of row t%128: 4 B)
     const int sr = ROT ? (t & 127) : t;
-    vs = (uint32_t)((size_t)((n0 + sr) >> 5) * nst * KQ4_STREAM_CHUNK + 8192 + 16 * (sr & 31) +
+    vs = (uint32_t)((size_t)((n0 + sr) >> 5) * nst * CHUNK + 8192 + 16 * (sr & 31) +
                     (ROT ? 4 * (t >> 7) : 0));
 #pragma unroll
     for (int u = 0; u < KQ4_GEMM_KB * KQ4_GEMM_BM / 256; ++u) {
@@ -164,11 +168,13 @@ __global__ __launch_bounds__(256, 2) void kq4_gemm_kernel(
   constexpr int NPIECE = NB + 1 + KQ4_GEMM_KB + NX;
   auto load_piece = [&](Regs &rg, int b0, int p) {
     if (p < NB) {
-      rg.b[p] = kq4_bload16s(rw, vb[p], (uint32_t)((b0 >> 4) * KQ4_STREAM_CHUNK +
-                                                   1024 * ((b0 & 15) >> 1)));
+      rg.b[p] = kq4_bload16s(rw, vb[p], WF ? (uint32_t)((b0 >> 3) * KQ8_STREAM_CHUNK + 1024 * (b0 & 7))
+                                           : (uint32_t)((b0 >> 4) * KQ4_STREAM_CHUNK +
+                                                        1024 * ((b0 & 15) >> 1)));
     } else if (p == NB) {
-      rg.sw.x = kq4_bload4s(rw, vs, (uint32_t)((b0 >> 4) * KQ4_STREAM_CHUNK +
-                                               512 * ((b0 & 15) >> 3) + 2 * (b0 & 7)));
+      rg.sw.x = kq4_bload4s(rw, vs, WF ? (uint32_t)((b0 >> 3) * KQ8_STREAM_CHUNK + 2 * (b0 & 7))
+                                       : (uint32_t)((b0 >> 4) * KQ4_STREAM_CHUNK +
+                                                    512 * ((b0 & 15) >> 3) + 2 * (b0 & 7)));
     } else if (p < NB + 1 + KQ4_GEMM_KB) {
       const int u = p - NB - 1;
       rg.a[u] = kq4_bload16s(ra, va, (uint32_t)(min(b0 + u, nb - 1) * act.q_bs));
@@ -181,7 +187,12 @@ __global__ __launch_bounds__(256, 2) void kq4_gemm_kernel(
   // ROT: piece p of a stage from registers into LDS stage buffer S (same piece order).
   auto swz = [](int row, int hh) { return 16 * (hh ^ ((row >> 3) & 1)); };
   auto store_piece = [&](const Regs &rg, Stage &S, int p) {
-    if (p < NB) {
+    if (p < NB && WF) {        // q8: the 16 codes as they are
+      const int idx = t + 256 * p;
+      const int ln = idx & 63, iu = (idx >> 6) & 3, sl = idx >> 8;
+      const int rl = 32 * sl + (ln & 31), h = ln >> 5;
+      *reinterpret_cast<uint4 *>(&S.b[iu][rl * PITCH + swz(rl, h)]) = rg.b[p];
+    } else if (p < NB) {
       const int idx = t + 256 * p;
       const int ln = idx & 63, iu = (idx >> 6) & 1, sl = idx >> 7;
       const int rl = 32 * sl + (ln & 31), h = ln >> 5;
@@ -193,17 +204,18 @@ __global__ __launch_bounds__(256, 2) void kq4_gemm_kernel(
       *reinterpret_cast<uint4 *>(&S.b[2 * iu + 1][rl * PITCH + swz(rl, h)]) =
           make_uint4(o[0], o[1], o[2], o[3]);
     } else if (p == NB) {      // no branch: every thread stores two (q4 enters as 16*(n-8))
+      constexpr float WS = WF ? 1.0f : 0.0625f;
       const int j = 2 * (t >> 7);
-      S.w[j][t & 127] = kq4_h2f(rg.sw.x) * 0.0625f;
-      S.w[j + 1][t & 127] = kq4_h2f(rg.sw.x >> 16) * 0.0625f;
+      S.w[j][t & 127] = kq4_h2f(rg.sw.x) * WS;
+      S.w[j + 1][t & 127] = kq4_h2f(rg.sw.x >> 16) * WS;
     } else if (p < NB + 1 + KQ4_GEMM_KB) {
       const int u = p - NB - 1, r = t >> 1;   // BM = 128: every thread holds a half row
       *reinterpret_cast<uint4 *>(&S.a[u][r * PITCH + swz(r, t & 1)]) = rg.a[u];
     } else {
       const int u = p - NB - 1 - KQ4_GEMM_KB, c = t + 256 * u;
-      // ASM chain: the reference multiplies by the f16-rounded activation scale
+      // ASM and Q8GEMM chains: the reference multiplies by the f16-rounded activation scale
       S.x[c / KQ4_GEMM_BM][c % KQ4_GEMM_BM] =
-          CHAIN == KQ4_CHAIN_ASM ? kq4_f16_round(rg.x[u]) : rg.x[u];
+          (CHAIN == KQ4_CHAIN_ASM || CHAIN == KQ4_CHAIN_Q8GEMM) ? kq4_f16_round(rg.x[u]) : rg.x[u];
     }
   };
   auto load = [&](Regs &rg, int b0) {
@@ -364,8 +376,12 @@ __global__ __launch_bounds__(256, 2) void kq4_gemm_kernel(
       auto epi = [&](int q) {
         const int k = q % NT, i = k & 1, jn = k >> 1;
 #pragma unroll
-        for (int v = 0; v < 16; ++v)
-          acc[i][jn][v] = fmaf((float)sacc[q & 1][v], sc[jn][16 * i + v], acc[i][jn][v]);
+        for (int v = 0; v < 16; ++v) {
+          if (CHAIN == KQ4_CHAIN_Q8GEMM)   // unfused: fl(acc + fl(scale * S))
+            acc[i][jn][v] = acc[i][jn][v] + sc[jn][16 * i + v] * (float)sacc[q & 1][v];
+          else
+            acc[i][jn][v] = fmaf((float)sacc[q & 1][v], sc[jn][16 * i + v], acc[i][jn][v]);
+        }
       };
       frag_s(0);
       frag_ab(0);
