@@ -876,6 +876,110 @@ __global__ __launch_bounds__(1024) void kq4_moe_down_kernel(
   }
 }
 
+// ---- one token: down projection and combine in one launch ------------------------------------
+// A workgroup takes 8 rows of Y (a quarter row set) and every rank: wave w handles ranks w,
+// w + nw, .., so the combine's rank order is within the workgroup and needs no cross-workgroup
+// step. For rank j (expert e, band of cbe blocks from B0 = e*cbe, B0 even): lane (k, r) =
+// (lane/8, lane%8) takes row r's 16-B stream lines L = k, k+8, .. (unit L/2 of the band, K half
+// L%2: the halves of two blocks), 8 rows' lines of one unit being 128 contiguous bytes. Its
+// integer dots (v_dot4 on the 16*(n-8) operand against the rank's av codes) give half-block
+// sums; the partner lane (k+1, same row) holds the other half, one DPP add makes the exact block
+// sums, and the even-k lanes form the terms fl(fl(sc*xs) * S) as the down kernel does. The
+// terms go to LDS and lane r of the wave adds them in block order from 0 (the reference's
+// chain, v4_row), giving P[j][row]; after a barrier wave 0's lanes 0..7 run the combine
+// y = fl(y + fl(p * P)) over the ranks in order, skipping invalid expert ids, as
+// kq4_moe_combine_kernel does.
+#define KQ4_MOE_D1_ROWS 8
+#define KQ4_MOE_D1_MAXL 4   // lines per lane (NL): cbe <= 32
+template <int NL>
+__global__ __launch_bounds__(1024) void kq4_moe_down1_kernel(
+    float *__restrict__ Y, const uint8_t *__restrict__ D, const int8_t *__restrict__ avq,
+    const float *__restrict__ avd, const int *__restrict__ sel, const float *__restrict__ pr,
+    int tk, int ne, int d, int ef) {
+  extern __shared__ __align__(16) uint8_t kq4_moe_lds[];
+  const int cbe = ef / 32, nstD = (ne * cbe + 15) / 16;
+  const int row0 = blockIdx.x * KQ4_MOE_D1_ROWS;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nw = blockDim.x >> 6;
+  const int r = lane & 7, k = lane >> 3;
+  const int n = row0 + r;
+  float *terms = reinterpret_cast<float *>(kq4_moe_lds) + wave * KQ4_MOE_D1_ROWS * cbe;
+  float *sP = reinterpret_cast<float *>(kq4_moe_lds) + nw * KQ4_MOE_D1_ROWS * cbe;   // [tk][8]
+  for (int j = wave; j < tk; j += nw) {
+    const int e = __builtin_amdgcn_readfirstlane(sel[j]);
+    if (e < 0 || e >= ne) continue;                  // skipped by the combine
+    const int B0 = e * cbe;
+    const int8_t *aq = avq + (size_t)j * ef;
+    const float *ad = avd + (size_t)j * cbe;
+    // all loads first: the lane's lines, their two blocks' scales and av codes and scales
+    uint4 wl[NL], a0[NL], a1[NL];
+    uint32_t sw[NL];
+    float2 xs[NL];
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+      const int L = k + 8 * i;
+      if (L < cbe) {
+        const int uu = L >> 1, h = L & 1, Bu = B0 + 2 * uu;
+        wl[i] = *reinterpret_cast<const uint4 *>(D + kq4_stream_nib(n, Bu, h, nstD));
+        sw[i] = *reinterpret_cast<const uint32_t *>(D + kq4_stream_scale(n, Bu, nstD));
+        a0[i] = *reinterpret_cast<const uint4 *>(aq + 64 * uu + 16 * h);
+        a1[i] = *reinterpret_cast<const uint4 *>(aq + 64 * uu + 32 + 16 * h);
+        xs[i] = *reinterpret_cast<const float2 *>(ad + 2 * uu);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+      const int L = k + 8 * i;
+      {   // every lane takes part in the exchange; a lane and its partner (L, L+1, cbe even)
+          // are both inside the band or both past it
+        // half-block sums 16*S of the two blocks: bytes 0-7 block 2uu, 8-15 block 2uu+1
+        int s0 = 0, s1 = 0;
+        if (L < cbe) {
+          const uint32_t q0[4] = {a0[i].x, a0[i].y, a0[i].z, a0[i].w};
+          const uint32_t q1[4] = {a1[i].x, a1[i].y, a1[i].z, a1[i].w};
+          uint32_t o[4];
+          kq4_unpack_half(wl[i].x, wl[i].y, o);
+#pragma unroll
+          for (int c = 0; c < 4; ++c) s0 = kq4_dot4(o[c], q0[c], s0);
+          kq4_unpack_half(wl[i].z, wl[i].w, o);
+#pragma unroll
+          for (int c = 0; c < 4; ++c) s1 = kq4_dot4(o[c], q1[c], s1);
+        }
+        // the other K half from lane (k ^ 1, r): DPP row_ror:8 within each 16-lane row
+        const int p0 = __builtin_amdgcn_update_dpp(0, s0, 0x128, 0xf, 0xf, false);
+        const int p1 = __builtin_amdgcn_update_dpp(0, s1, 0x128, 0xf, 0xf, false);
+        if ((k & 1) == 0 && L < cbe) {
+          const int uu = L >> 1;
+          const int S0 = (s0 + p0) >> 4, S1 = (s1 + p1) >> 4;   // exact: 16*S
+          terms[r * cbe + 2 * uu] = (kq4_h2f(sw[i]) * xs[i].x) * (float)S0;
+          terms[r * cbe + 2 * uu + 1] = (kq4_h2f(sw[i] >> 16) * xs[i].y) * (float)S1;
+        }
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (k == 0) {
+      float acc = 0.0f;
+      for (int b = 0; b < cbe; ++b) acc = acc + terms[r * cbe + b];
+      sP[j * KQ4_MOE_D1_ROWS + r] = acc;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");   // terms reused by the next rank
+  }
+  __syncthreads();
+  if (wave == 0 && lane < KQ4_MOE_D1_ROWS) {
+    float y = 0.0f;
+    for (int j = 0; j < tk; ++j) {
+      const int e = sel[j];
+      if (e >= 0 && e < ne) y = y + pr[j] * sP[j * KQ4_MOE_D1_ROWS + lane];
+    }
+    Y[row0 + lane] = y;
+  }
+}
+
 // y = fl(y + fl(p * P)) over the ranks in order, skipping invalid expert ids. The loads of all
 // ranks are issued before the chain (P rows of skipped ranks are read but not used).
 __global__ __launch_bounds__(256) void kq4_moe_combine_kernel(float *__restrict__ Y,
@@ -944,6 +1048,26 @@ int kq4_launch_moe_dbg(float *Y, const float *X, const int *sel, const float *pr
     const long nblk = (long)n_pairs * cbe;
     hipLaunchKernelGGL(kq4_moe_avq_kernel, dim3((unsigned)((nblk + 7) / 8)), dim3(256), 0, s,
                        av_in, ws.avq, ws.avd, nblk);
+  }
+  // one token with an even band (every band starts on a stream unit) and at most 16 ranks: down
+  // and combine in one launch
+  const int cbe_ = ef / 32;
+  if (t1 && cbe_ % 2 == 0 && cbe_ <= 8 * KQ4_MOE_D1_MAXL && tk <= 16) {
+    const int nw = tk;
+    const size_t lds = ((size_t)nw * KQ4_MOE_D1_ROWS * cbe_ + (size_t)tk * KQ4_MOE_D1_ROWS) *
+                       sizeof(float);
+    const dim3 grid((unsigned)(d / KQ4_MOE_D1_ROWS)), block(64 * nw);
+    switch ((cbe_ + 7) / 8) {
+      case 1: hipLaunchKernelGGL(kq4_moe_down1_kernel<1>, grid, block, lds, s, Y, D, ws.avq,
+                                 ws.avd, sel, pr, tk, ne, d, ef); break;
+      case 2: hipLaunchKernelGGL(kq4_moe_down1_kernel<2>, grid, block, lds, s, Y, D, ws.avq,
+                                 ws.avd, sel, pr, tk, ne, d, ef); break;
+      case 3: hipLaunchKernelGGL(kq4_moe_down1_kernel<3>, grid, block, lds, s, Y, D, ws.avq,
+                                 ws.avd, sel, pr, tk, ne, d, ef); break;
+      default: hipLaunchKernelGGL(kq4_moe_down1_kernel<4>, grid, block, lds, s, Y, D, ws.avq,
+                                  ws.avd, sel, pr, tk, ne, d, ef); break;
+    }
+    return (int)hipGetLastError();
   }
   // half stages a band can meet (the most over the experts), and row sets per workgroup
   int nhl = 1;
