@@ -33,7 +33,10 @@ def ulps(a, b):
 SHAPES = {"small": dict(hidden=256, experts=16, top_k=4, ef=64),
           "qwen3_30b_a3b": synth.QWEN3_30B_A3B_MOE,
           # the largest hidden size the kernels take (8 stages of 16 blocks)
-          "wide": dict(hidden=4096, experts=12, top_k=3, ef=96)}
+          "wide": dict(hidden=4096, experts=12, top_k=3, ef=96),
+          # top-16 and 32-block bands: the one-token down + combine kernel at its limits
+          # (16 waves, four band lines per lane)
+          "k16": dict(hidden=512, experts=32, top_k=16, ef=1024)}
 
 
 def test_route(kq4, torch_dev, orc):
@@ -77,7 +80,7 @@ def test_route_edge_cases(kq4, torch_dev, orc, ne, tk):
 
 
 @pytest.mark.parametrize("T", [1, 7, 64])
-@pytest.mark.parametrize("shape", ["small", "qwen3_30b_a3b", "wide"])
+@pytest.mark.parametrize("shape", ["small", "qwen3_30b_a3b", "wide", "k16"])
 def test_moe_stages(kq4, torch_dev, orc, shape, T):
     torch = torch_dev
     cfg = SHAPES[shape]
