@@ -220,6 +220,9 @@ KQ4_DEV uint2 kq4_bload8s(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff
 KQ4_DEV uint32_t kq4_bload4s(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
   return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, voff, (int)soff, 0);
 }
+KQ4_DEV uint32_t kq4_bload2s(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, voff, (int)soff, 0);
+}
 
 // ---- stream layout of the device weights -------------------------------------------------
 // A q4 matrix lives in HBM as 9216-B chunks, one per (32-row set, 16-block stage), in

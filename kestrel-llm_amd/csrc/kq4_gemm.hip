@@ -29,6 +29,7 @@
 #include "../../include/kq4.h"
 
 #include <stdlib.h>
+#include <type_traits>
 
 typedef int kq4_v4i __attribute__((ext_vector_type(4)));
 typedef int kq4_v16i __attribute__((ext_vector_type(16)));
@@ -45,7 +46,7 @@ KQ4_DEV int kq4_mfma_tok(int v, int half) { return 8 * (v >> 2) + 4 * half + (v 
 // TM / TN = MFMA token / row tiles per wave: a workgroup covers BM = 64*TM tokens x BN = 64*TN
 // rows (128 x 128, or smaller when the launch would otherwise have fewer than two tiles per CU).
 template <int CHAIN, int TM, int TN, int WF>
-__global__ __launch_bounds__(256, 2) void kq4_gemm_kernel(
+__global__ __launch_bounds__(256, (TM == 2 && TN == 1) ? 3 : 2) void kq4_gemm_kernel(
     float *__restrict__ out, const float *__restrict__ res, const uint8_t *__restrict__ w,
     const KQ4GemmAct act, int rows, int n_tok, int nb, int nst, int mtiles, int ntiles,
     uint32_t wbytes) {
@@ -54,12 +55,14 @@ __global__ __launch_bounds__(256, 2) void kq4_gemm_kernel(
   // stages in LDS at a 32-B row pitch, the two 16-B halves of row r swapped when bit 3 of r is
   // set (so the 16-B fragment reads and the stores stay bank-conflict free without padding):
   // 2 x 36 KB, two workgroups per CU. The other forms stage once at a 48-B pitch.
-  constexpr bool ROT = CHAIN != KQ4_CHAIN_CTILE && TM == 2 && TN == 2;
+  constexpr bool ROT = CHAIN != KQ4_CHAIN_CTILE && TM == 2;
+  constexpr int SPT = KQ4_GEMM_KB * KQ4_GEMM_BN / 256;   // ROT: row scales per thread (2 or 1)
   constexpr int PITCH = ROT ? 32 : KQ4_LDS_ROW;
   struct Stage {
     int8_t a[KQ4_GEMM_KB][KQ4_GEMM_BM * PITCH];
     int8_t b[KQ4_GEMM_KB][KQ4_GEMM_BN * PITCH];
-    float w[KQ4_GEMM_KB][KQ4_GEMM_BN];
+    // 128 x 64: the raw f16 row scales (scaled when read), so that three workgroups fit
+    std::conditional_t<ROT && TN == 1, uint16_t, float> w[KQ4_GEMM_KB][KQ4_GEMM_BN];
     float x[KQ4_GEMM_KB][KQ4_GEMM_BM];
   };
   __shared__ __align__(16) Stage stg[ROT ? 2 : 1];
@@ -147,10 +150,10 @@ __global__ __launch_bounds__(256, 2) void kq4_gemm_kernel(
       vb[u] = (uint32_t)((size_t)((n0 + rl) >> 5) * nst * CHUNK + 1024 * iu +
                          16 * ((rl & 31) + 32 * h));
     }
-    // (ROT: thread t takes the scales of blocks 2*(t/128), +1 of row t%128: 4 B)
-    const int sr = ROT ? (t & 127) : t;
+    // (ROT: thread t takes the SPT scales of row t % BN from block SPT * (t / BN) on)
+    const int sr = ROT ? t % KQ4_GEMM_BN : t;
     vs = (uint32_t)((size_t)((n0 + sr) >> 5) * nst * CHUNK + 8192 + 16 * (sr & 31) +
-                    (ROT ? 4 * (t >> 7) : 0));
+                    (ROT ? 2 * SPT * (t / KQ4_GEMM_BN) : 0));
 #pragma unroll
     for (int u = 0; u < KQ4_GEMM_KB * KQ4_GEMM_BM / 256; ++u) {
       const int c = t + 256 * u;
@@ -172,9 +175,10 @@ __global__ __launch_bounds__(256, 2) void kq4_gemm_kernel(
                                            : (uint32_t)((b0 >> 4) * KQ4_STREAM_CHUNK +
                                                         1024 * ((b0 & 15) >> 1)));
     } else if (p == NB) {
-      rg.sw.x = kq4_bload4s(rw, vs, WF ? (uint32_t)((b0 >> 3) * KQ8_STREAM_CHUNK + 2 * (b0 & 7))
-                                       : (uint32_t)((b0 >> 4) * KQ4_STREAM_CHUNK +
-                                                    512 * ((b0 & 15) >> 3) + 2 * (b0 & 7)));
+      const uint32_t so = WF ? (uint32_t)((b0 >> 3) * KQ8_STREAM_CHUNK + 2 * (b0 & 7))
+                             : (uint32_t)((b0 >> 4) * KQ4_STREAM_CHUNK +
+                                          512 * ((b0 & 15) >> 3) + 2 * (b0 & 7));
+      rg.sw.x = SPT == 2 ? kq4_bload4s(rw, vs, so) : kq4_bload2s(rw, vs, so);
     } else if (p < NB + 1 + KQ4_GEMM_KB) {
       const int u = p - NB - 1;
       rg.a[u] = kq4_bload16s(ra, va, (uint32_t)(min(b0 + u, nb - 1) * act.q_bs));
@@ -203,11 +207,15 @@ __global__ __launch_bounds__(256, 2) void kq4_gemm_kernel(
       kq4_unpack_half(rg.b[p].z, rg.b[p].w, o);
       *reinterpret_cast<uint4 *>(&S.b[2 * iu + 1][rl * PITCH + swz(rl, h)]) =
           make_uint4(o[0], o[1], o[2], o[3]);
-    } else if (p == NB) {      // no branch: every thread stores two (q4 enters as 16*(n-8))
-      constexpr float WS = WF ? 1.0f : 0.0625f;
-      const int j = 2 * (t >> 7);
-      S.w[j][t & 127] = kq4_h2f(rg.sw.x) * WS;
-      S.w[j + 1][t & 127] = kq4_h2f(rg.sw.x >> 16) * WS;
+    } else if (p == NB) {      // no branch: every thread stores SPT (q4 enters as 16*(n-8))
+      const int j = SPT * (t / KQ4_GEMM_BN), r = t % KQ4_GEMM_BN;
+      if constexpr (TN == 1) {
+        S.w[j][r] = (uint16_t)rg.sw.x;
+      } else {
+        constexpr float WS = WF ? 1.0f : 0.0625f;
+        S.w[j][r] = kq4_h2f(rg.sw.x) * WS;
+        S.w[j + 1][r] = kq4_h2f(rg.sw.x >> 16) * WS;
+      }
     } else if (p < NB + 1 + KQ4_GEMM_KB) {
       const int u = p - NB - 1, r = t >> 1;   // BM = 128: every thread holds a half row
       *reinterpret_cast<uint4 *>(&S.a[u][r * PITCH + swz(r, t & 1)]) = rg.a[u];
@@ -341,7 +349,6 @@ __global__ __launch_bounds__(256, 2) void kq4_gemm_kernel(
       // second scale set it needs costs the third wave per SIMD that its register count allows.
       constexpr int NT = 2 * TN;              // MFMA tiles per wave and block: k = i + 2 * jn
       constexpr int NQ = KQ4_GEMM_KB * NT;
-      static_assert(NPIECE <= NQ, "a stage's loads must fit between its tile epilogues");
       kq4_v4i af[2], bf[TN];
       float xv, wv[TN];
       kq4_v16i sacc[2];
@@ -361,7 +368,12 @@ __global__ __launch_bounds__(256, 2) void kq4_gemm_kernel(
       auto frag_s = [&](int bl) {
         xv = C.x[bl][64 * wm + lane];
 #pragma unroll
-        for (int jn = 0; jn < TN; ++jn) wv[jn] = C.w[bl][32 * TN * wn + 32 * jn + l32];
+        for (int jn = 0; jn < TN; ++jn) {
+          if constexpr (TN == 1)   // q4 enters the MFMA as 16*(n-8): wd/16 (exact)
+            wv[jn] = kq4_h2f(C.w[bl][32 * TN * wn + 32 * jn + l32]) * (WF ? 1.0f : 0.0625f);
+          else
+            wv[jn] = C.w[bl][32 * TN * wn + 32 * jn + l32];
+        }
       };
       // Scale products fl(wd * xs) from the matrix core: v_mfma_f32_32x32x1_2b_f32 is a rank-1
       // update of two 32 x 32 blocks, each output one product rounded once (with a zero
@@ -402,9 +414,17 @@ __global__ __launch_bounds__(256, 2) void kq4_gemm_kernel(
         epi(q);
         __builtin_amdgcn_sched_barrier(0);
         if (bl + 1 < KQ4_GEMM_KB && (k & 1)) issue_sc(k >> 1);
-        if (q < NPIECE) {
-          store_piece(rg, N, q);
-          load_piece(rg, bn, q);
+        if constexpr (NPIECE <= NQ) {   // one piece after each of the first NPIECE epilogues
+          if (q < NPIECE) {
+            store_piece(rg, N, q);
+            load_piece(rg, bn, q);
+          }
+        } else {                         // (q8, one row tile: 9 pieces over 8 epilogues)
+#pragma unroll
+          for (int pc = q * NPIECE / NQ; pc < (q + 1) * NPIECE / NQ; ++pc) {
+            store_piece(rg, N, pc);
+            load_piece(rg, bn, pc);
+          }
         }
       }
       __syncthreads();
@@ -762,7 +782,7 @@ static hipError_t gemm_launch(float *out, const float *res, const uint8_t *w,
     else
       return hipErrorInvalidValue;
   } else if (chain == KQ4_CHAIN_CTILE) {
-    if constexpr (TM == 2 && TN == 2) return hipErrorInvalidValue;   // capped by the planner
+    if constexpr (TM == 2) return hipErrorInvalidValue;   // capped by the planner
     else
       hipLaunchKernelGGL((kq4_gemm_kernel<KQ4_CHAIN_CTILE, TM, TN, 0>), grid, dim3(256), 0, s,
                          out, res, w, act, rows, n_tok, nb, nst, mtiles, ntiles, wbytes);
@@ -779,8 +799,9 @@ static hipError_t gemm_launch(float *out, const float *res, const uint8_t *w,
 }
 
 // The largest of the 128x128, 64x128 and 64x64 (tokens x rows) tiles that gives at least two
-// tiles per CU (else 64x64). The C-tile chain (two accumulator sets) takes 64x128 at most: at
-// 128x128 it needs more than 256 registers and spills. KQ4_GEMM_TILE = 1/2/3 forces one (for
+// tiles per CU (else 64x64), with 128x64 before the 64-token forms for long K (below). The C-tile
+// chain (two accumulator sets) takes 64x128 at most: at 128x128 it needs more than 256 registers
+// and spills. KQ4_GEMM_TILE = 1/2/3/4 (128x128, 64x128, 64x64, 128x64) forces one (for
 // measurement; the C-tile chain still caps it).
 int kq4_launch_gemm(float *out, const float *res, const uint8_t *w, const KQ4GemmAct &act,
                     int rows, int cols, int n_tok, int chain, int ncu, hipStream_t s, int wf) {
@@ -792,9 +813,15 @@ int kq4_launch_gemm(float *out, const float *res, const uint8_t *w, const KQ4Gem
     return (long)((n_tok + bm - 1) / bm) * ((rows + bn - 1) / bn);
   };
   static const int force = [] { const char *e = getenv("KQ4_GEMM_TILE"); return e ? atoi(e) : 0; }();
-  int pick = force >= 1 && force <= 3 ? force
-             : tiles(128, 128) >= 2L * ncu ? 1 : (tiles(64, 128) >= 2L * ncu ? 2 : 3);
-  if (chain == KQ4_CHAIN_CTILE && pick == 1) pick = 2;
+  // Long K (>= 256 blocks) with fewer than two 128 x 128 tiles per CU: the pipelined 128 x 64
+  // form as soon as it has a tile per CU (Qwen3-8B down, K = 12288: M = 512 131.6 -> 121.4 us,
+  // M = 1024 211 -> 192 us; at K = 4096 the 64-token forms stay faster).
+  int pick = force >= 1 && force <= 4           ? force
+             : tiles(128, 128) >= 2L * ncu       ? 1
+             : nb >= 256 && tiles(128, 64) >= ncu ? 4
+             : tiles(64, 128) >= 2L * ncu        ? 2
+                                                 : 3;
+  if (chain == KQ4_CHAIN_CTILE && (pick == 1 || pick == 4)) pick = 2;
   // 32-bit buffer offsets: weights and activation operands below 4 GB
   const size_t wb = wf ? kq8_stream_bytes(rows, cols) : kq4_stream_bytes(rows, cols);
   // (the last token tile's padding tokens, up to 127 past n_tok, address past the buffers' ends)
@@ -809,6 +836,7 @@ int kq4_launch_gemm(float *out, const float *res, const uint8_t *w, const KQ4Gem
   hipError_t e;
   if (pick == 1) e = gemm_launch<2, 2>(out, res, w, act, rows, n_tok, nb, nst, chain, wf, wbytes, s);
   else if (pick == 2) e = gemm_launch<1, 2>(out, res, w, act, rows, n_tok, nb, nst, chain, wf, wbytes, s);
+  else if (pick == 4) e = gemm_launch<2, 1>(out, res, w, act, rows, n_tok, nb, nst, chain, wf, wbytes, s);
   else e = gemm_launch<1, 1>(out, res, w, act, rows, n_tok, nb, nst, chain, wf, wbytes, s);
   return (int)e;
 }
