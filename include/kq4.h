@@ -104,7 +104,9 @@ const char *kq4_version(void);
  * 1 halves, 2 quarters per workgroup), gemv_rps (row sets per workgroup, 1..3), gemv_waves,
  * gemv_wpcu, gemv_maxw, gemv_fq (0 / 1: activations quantized by a separate launch / in the
  * GEMV), gemv_fq_work, gemv_silu_fq_work, gemm_kind (0: the prefill GEMM on int8 MFMA, the
- * default; 1: on fp8 operands; the same outputs). value < 0 restores the default (for most, the
+ * default; 1: on fp8 operands; the same outputs), gemm_tile (0: the planner's choice; 1 / 2 / 3 /
+ * 4: 128x128 / 64x128 / 64x64 / 128x64 token x row tiles; the same outputs). value < 0 restores
+ * the default (for most, the
  * planner's own choice). The initial values come from the environment variables KQ4_
  * + the upper-case name. Takes effect for launches planned after it returns. */
 int kq4_set_option(const char *name, int value);

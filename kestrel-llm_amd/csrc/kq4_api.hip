@@ -178,7 +178,7 @@ int env_int(const char *name, int dflt) {
 // choice where a planner chooses.
 enum OptId {
   kGemvKind, kGemvMfmaFrom, kGemvHs, kGemvRps, kGemvWaves, kGemvWpcu, kGemvMaxw,
-  kGemvFq, kGemvFqWork, kGemvSiluFqWork, kGemmKind, kOptCount
+  kGemvFq, kGemvFqWork, kGemvSiluFqWork, kGemmKind, kGemmTile, kOptCount
 };
 struct OptDef {
   const char *name, *env;
@@ -191,7 +191,7 @@ const OptDef kOpts[kOptCount] = {
     {"gemv_wpcu", "KQ4_GEMV_WPCU", 64},          {"gemv_maxw", "KQ4_GEMV_MAXW", 16},
     {"gemv_fq", "KQ4_GEMV_FQ", -1},              {"gemv_fq_work", "KQ4_GEMV_FQ_WORK", 45000},
     {"gemv_silu_fq_work", "KQ4_GEMV_SILU_FQ_WORK", 15000},
-    {"gemm_kind", "KQ4_GEMM_KIND", -1},
+    {"gemm_kind", "KQ4_GEMM_KIND", -1},          {"gemm_tile", "KQ4_GEMM_TILE", 0},
 };
 std::atomic<int> g_opt[kOptCount];
 std::once_flag g_opt_once;
@@ -388,7 +388,7 @@ int matmul_impl(int n_mats, float *const *out, const float *const *res, const ui
     for (int i = 0; i < n_mats; ++i)
       KQ4_HIP((hipError_t)kq4_launch_gemm(out[i], res ? res[i] : nullptr, w[i], act, rows[i],
                                           cols, n, gchain ? KQ4_CHAIN_Q8GEMM : KQ4_CHAIN_GEMV32,
-                                          ds->ncu, s, 1));
+                                          ds->ncu, s, 1, opt(kGemmTile)));
     return KQ4_OK;
   }
 
@@ -411,7 +411,8 @@ int matmul_impl(int n_mats, float *const *out, const float *const *res, const ui
                                             cols, 0, s, 2, xu));
     for (int i = 0; i < n_mats; ++i)
       KQ4_HIP((hipError_t)kq4_launch_gemm_f8(out[i], res ? res[i] : nullptr, w[i], xp, d,
-                                             rows[i], cols, main_n, main_chain, ds->ncu, s));
+                                             rows[i], cols, main_n, main_chain, ds->ncu, s,
+                                             opt(kGemmTile)));
     if (!tail) return KQ4_OK;
     float *o2[KQ4_MAX_MATS];
     const float *r2[KQ4_MAX_MATS];
@@ -444,7 +445,7 @@ int matmul_impl(int n_mats, float *const *out, const float *const *res, const ui
   }
   for (int i = 0; i < n_mats; ++i)
     KQ4_HIP((hipError_t)kq4_launch_gemm(out[i], res ? res[i] : nullptr, w[i], act, rows[i], cols,
-                                        main_n, main_chain, ds->ncu, s));
+                                        main_n, main_chain, ds->ncu, s, 0, opt(kGemmTile)));
   if (tail) {
     float *o2[KQ4_MAX_MATS];
     const float *r2[KQ4_MAX_MATS];

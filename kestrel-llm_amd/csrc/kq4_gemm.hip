@@ -744,7 +744,7 @@ static hipError_t gemm_f8_launch(float *out, const float *res, const uint8_t *w,
 
 int kq4_launch_gemm_f8(float *out, const float *res, const uint8_t *w, const uint8_t *xp,
                        const float *xd, int rows, int cols, int n_tok, int chain, int ncu,
-                       hipStream_t s) {
+                       hipStream_t s, int tile) {
   const int nb = cols / 32;
   const int nst = (nb + KQ4_STREAM_CB - 1) / KQ4_STREAM_CB;
   if (n_tok <= 0 || rows <= 0) return 0;
@@ -755,8 +755,7 @@ int kq4_launch_gemm_f8(float *out, const float *res, const uint8_t *w, const uin
   auto tiles = [&](int bm, int bn) {
     return (long)((n_tok + bm - 1) / bm) * ((rows + bn - 1) / bn);
   };
-  static const int force = [] { const char *e = getenv("KQ4_GEMM_TILE"); return e ? atoi(e) : 0; }();
-  const int pick = force >= 1 && force <= 3 ? force
+  const int pick = tile >= 1 && tile <= 3 ? tile
                    : tiles(128, 128) >= 2L * ncu ? 1 : (tiles(64, 128) >= 2L * ncu ? 2 : 3);
   hipError_t e;
   if (pick == 1) e = gemm_f8_launch<2, 2>(out, res, w, xp, xd, rows, n_tok, nb, nst, chain, s);
@@ -801,10 +800,11 @@ static hipError_t gemm_launch(float *out, const float *res, const uint8_t *w,
 // The largest of the 128x128, 64x128 and 64x64 (tokens x rows) tiles that gives at least two
 // tiles per CU (else 64x64), with 128x64 before the 64-token forms for long K (below). The C-tile
 // chain (two accumulator sets) takes 64x128 at most: at 128x128 it needs more than 256 registers
-// and spills. KQ4_GEMM_TILE = 1/2/3/4 (128x128, 64x128, 64x64, 128x64) forces one (for
-// measurement; the C-tile chain still caps it).
+// and spills. `tile` = 1/2/3/4 (128x128, 64x128, 64x64, 128x64; planner option gemm_tile)
+// forces one (for measurement and tests; the C-tile chain still caps it).
 int kq4_launch_gemm(float *out, const float *res, const uint8_t *w, const KQ4GemmAct &act,
-                    int rows, int cols, int n_tok, int chain, int ncu, hipStream_t s, int wf) {
+                    int rows, int cols, int n_tok, int chain, int ncu, hipStream_t s, int wf,
+                    int tile) {
   const int nb = cols / 32;
   const int cb = wf ? KQ8_STREAM_CB : KQ4_STREAM_CB;
   const int nst = (nb + cb - 1) / cb;
@@ -812,11 +812,10 @@ int kq4_launch_gemm(float *out, const float *res, const uint8_t *w, const KQ4Gem
   auto tiles = [&](int bm, int bn) {
     return (long)((n_tok + bm - 1) / bm) * ((rows + bn - 1) / bn);
   };
-  static const int force = [] { const char *e = getenv("KQ4_GEMM_TILE"); return e ? atoi(e) : 0; }();
   // Long K (>= 256 blocks) with fewer than two 128 x 128 tiles per CU: the pipelined 128 x 64
   // form as soon as it has a tile per CU (Qwen3-8B down, K = 12288: M = 512 131.6 -> 121.4 us,
   // M = 1024 211 -> 192 us; at K = 4096 the 64-token forms stay faster).
-  int pick = force >= 1 && force <= 4           ? force
+  int pick = tile >= 1 && tile <= 4             ? tile
              : tiles(128, 128) >= 2L * ncu       ? 1
              : nb >= 256 && tiles(128, 64) >= ncu ? 4
              : tiles(64, 128) >= 2L * ncu        ? 2

@@ -96,16 +96,18 @@ struct KQ4GemmAct {
   long d_ts, d_bs;
 };
 // wf = 1: Q8_0 weights in the q8 stream layout, chain KQ4_CHAIN_Q8GEMM or KQ4_CHAIN_GEMV32.
+// tile: 0 the planner's choice; 1 / 2 / 3 / 4 force 128x128 / 64x128 / 64x64 / 128x64 (tokens x
+// rows; the C-tile chain is capped at 64x128).
 int kq4_launch_gemm(float *out, const float *res, const uint8_t *w, const KQ4GemmAct &act,
                     int rows, int cols, int n_tok, int chain, int ncu, hipStream_t stream,
-                    int wf = 0);
+                    int wf = 0, int tile = 0);
 
 // Prefill GEMM on fp8 matrix-core operands (ASM or GEMV32 chain, q4 weights, bit-identical to
 // kq4_launch_gemm): xp = the activations' e4m3 operand pairs [n_tok][cols/32][64] (the
 // quantizer's block_major = 2 output), xd their f32 scales [n_tok][cols/32].
 int kq4_launch_gemm_f8(float *out, const float *res, const uint8_t *w, const uint8_t *xp,
                        const float *xd, int rows, int cols, int n_tok, int chain, int ncu,
-                       hipStream_t stream);
+                       hipStream_t stream, int tile = 0);
 
 // MoE
 int kq4_launch_moe_route(int *sel, float *pr, const float *logits, int T, int ne, int tk,

@@ -176,6 +176,32 @@ def test_gemm_large_tiles_bit_exact(kq4, torch_dev, orc, n, rows, chain, cols, k
     assert np.array_equal(got[tok, row].view(np.uint32), want.view(np.uint32))
 
 
+@pytest.mark.parametrize("tile", [1, 2, 3, 4])
+@pytest.mark.parametrize("chain", [0, 1, 2, 3])
+def test_gemm_tile_forms_bit_exact(kq4, torch_dev, orc, tile, chain):
+    """Every tile form forced through the planner option gemm_tile (128x128, 64x128, 64x64,
+    128x64 tokens x rows; the C-tile chain is capped at 64x128) is bit-identical to the oracle,
+    with an odd block count (K = 672) and a partial last row set and token tile."""
+    torch = torch_dev
+    n, rows, cols = 300, 2000, 672
+    w, x = case(rows, cols, n, 900 + 10 * tile + chain)
+    out = torch.empty((n, rows), dtype=torch.float32, device="cuda")
+    with kq4.options(gemm_tile=tile):
+        kq4.matmul_dev(out, to_dev(torch, x), wdev(kq4, torch, w, rows, cols), rows, cols,
+                       chain=chain)
+    torch.cuda.synchronize()
+    got = host(out)
+    xq, xd = orc.quantize(x, cols)
+    rng = np.random.default_rng(tile + chain)
+    t0, r0 = np.meshgrid(np.arange(0, n, 32), np.arange(0, rows, 32), indexing="ij")
+    tok = np.concatenate([np.minimum(t0.ravel() + rng.integers(0, 32, t0.size), n - 1),
+                          [n - 1] * 64, rng.integers(0, n, 1024)]).astype(np.int32)
+    row = np.concatenate([np.minimum(r0.ravel() + rng.integers(0, 32, r0.size), rows - 1),
+                          rng.integers(0, rows, 64), rng.integers(0, rows, 1024)]).astype(np.int32)
+    want = orc.matmul_q_sample(w, xq, xd, rows, cols, n, tok, row, chain=chain)
+    assert np.array_equal(got[tok, row].view(np.uint32), want.view(np.uint32))
+
+
 def test_gemm_from_prequantized(kq4, torch_dev, orc):
     torch = torch_dev
     rows, cols, n = 128, 1024, 40

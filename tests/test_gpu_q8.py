@@ -60,9 +60,10 @@ def test_q8_gemm_bit_exact(kq4, torch_dev, orc, rows, cols, g, n, chain):
 
 
 # 128x128 tiles (2048 tokens x 4096 rows: 512 tiles) and 64x128 (2048 rows); short K keeps the
-# oracle quick
+# oracle quick; tile 4 forces the 128x64 form (planner option gemm_tile)
+@pytest.mark.parametrize("tile", [0, 4])
 @pytest.mark.parametrize("n,rows,chain", [(2048, 4096, 0), (2048, 4096, 4), (2048, 2048, 2)])
-def test_q8_gemm_large_tiles_bit_exact(kq4, torch_dev, orc, n, rows, chain):
+def test_q8_gemm_large_tiles_bit_exact(kq4, torch_dev, orc, n, rows, chain, tile):
     torch = torch_dev
     cols = 256
     w = q8_tiles_synth(rows, cols, 8, rows + chain)
@@ -70,7 +71,8 @@ def test_q8_gemm_large_tiles_bit_exact(kq4, torch_dev, orc, n, rows, chain):
     want = orc.q8_matmul(w, x, rows, cols, chain=chain, g=8)
     W = kq4.q8_prepare_dev(w, rows, cols, g=8)
     out = torch.empty((n, rows), dtype=torch.float32, device="cuda")
-    kq4.q8_matmul_dev(out, to_dev(torch, x), W, rows, cols, chain=chain)
+    with kq4.options(gemm_tile=tile):
+        kq4.q8_matmul_dev(out, to_dev(torch, x), W, rows, cols, chain=chain)
     torch.cuda.synchronize()
     assert np.array_equal(out.cpu().numpy().view(np.uint32), want.view(np.uint32))
 
