@@ -547,6 +547,22 @@ __global__ __launch_bounds__(1024) void kq4_moe_gu_kernel(
   constexpr int SLAB = kq4_moe_slab(16, PC);
   const int rbs = ef / 32;
   const int slot = blockIdx.x / rbs, rs = blockIdx.x - slot * rbs;
+  const int nb = d / 32, nst = (nb + 15) / 16;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int m = wave >= nst ? 1 : 0;                  // 0 = gate, 1 = up
+  const int k = wave - m * nst;                       // stage
+  const int nblk = nb - 16 * k < 16 ? nb - 16 * k : 16;
+  // T1: a gate wave's share of X (lane quad per block, 8 values per lane), loaded before the
+  // routing and the weights, so that its quantization waits only for these loads (the loads
+  // complete in issue order)
+  float4 x0 = make_float4(0, 0, 0, 0), x1 = x0;
+  if (T1 && m == 0 && (lane >> 2) < nblk) {
+    const float4 *src = reinterpret_cast<const float4 *>(X + (size_t)(16 * k + (lane >> 2)) * 32 +
+                                                         8 * (lane & 3));
+    x0 = src[0];
+    x1 = src[1];
+  }
   KQ4MoeSlot<0> sr{};   // header only: inline ids spill here
   int e, cnt;
   if (T1) {
@@ -560,11 +576,6 @@ __global__ __launch_bounds__(1024) void kq4_moe_gu_kernel(
     cnt = sr.r[2];
   }
   auto pair = [&](int j) { return T1 ? slot : kq4_moe_pair<0>(sr, ex_pair, j); };
-  const int nb = d / 32, nst = (nb + 15) / 16;
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int m = wave >= nst ? 1 : 0;                  // 0 = gate, 1 = up
-  const int k = wave - m * nst;                       // stage
   const int h = lane >> 5, r = lane & 31;
   uint8_t *slab = kq4_moe_lds + k * SLAB;
   float *sx = reinterpret_cast<float *>(slab + PC * KQ4_MOE_QTS);     // [16][PC]
@@ -572,7 +583,6 @@ __global__ __launch_bounds__(1024) void kq4_moe_gu_kernel(
   KQ4MoeW<8, 2> w;
   kq4_moe_wload<8, 2>(w, (m ? U : G) + ((size_t)((e * ef) / 32 + rs) * nst + k) * KQ4_STREAM_CHUNK,
                       lane, 0, 0);
-  const int nblk = nb - 16 * k < 16 ? nb - 16 * k : 16;
 
   for (int c0 = 0; c0 < cnt; c0 += PC) {
     const int np = cnt - c0 < PC ? cnt - c0 : PC;
@@ -582,12 +592,6 @@ __global__ __launch_bounds__(1024) void kq4_moe_gu_kernel(
       // clamped to +-127; pairs 1-3 and blocks past K get zero codes and scales
       const int bb = lane >> 2, qq = lane & 3;
       const bool live = bb < nblk;
-      float4 x0 = make_float4(0, 0, 0, 0), x1 = x0;
-      if (live) {
-        const float4 *src = reinterpret_cast<const float4 *>(X + (size_t)(16 * k + bb) * 32 + 8 * qq);
-        x0 = src[0];
-        x1 = src[1];
-      }
       const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
       float am = 1e-10f;
 #pragma unroll
