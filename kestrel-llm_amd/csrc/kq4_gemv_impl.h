@@ -96,9 +96,11 @@ struct KQ4GvStage {
 // Scales first: the loads complete in issue order, so the first block then waits only for the
 // scales and its own unit, and each later block for one more unit.
 // q8 (WF > 0): the same unit loads, one block per unit, and the row's 8 scales in one load.
-// ORD: a scheduling barrier after each load keeps that issue order (left to itself the compiler
-// may issue unit 0 near the end, and the first block then waits for nearly all of them).
-template <int HS, int WF, bool ORD = false>
+// ORD: keep that issue order (left to itself the compiler may issue unit 0 near the end, and the
+// first block then waits for nearly all of them): 1 = a scheduling barrier after each load, which
+// also keeps every later instruction below the loads; 2 = a compiler memory barrier after each,
+// which orders only the memory operations (the quantization's VALU work can still move above).
+template <int HS, int WF, int ORD = 0>
 KQ4_DEV void kq4_gv_load(KQ4GvStage<HS> &st, const uint8_t *__restrict__ chunk, int rr, int h,
                          int p) {
   // the weights are read once per launch: non-temporal loads
@@ -109,15 +111,28 @@ KQ4_DEV void kq4_gv_load(KQ4GvStage<HS> &st, const uint8_t *__restrict__ chunk, 
     const uint4 b = kq4_ld_nt(sc + 32);
     st.sc[4] = b.x; st.sc[5] = b.y; st.sc[6] = b.z; st.sc[7] = b.w;
   }
-  if constexpr (ORD) __builtin_amdgcn_sched_barrier(0);
+  if constexpr (ORD == 1) __builtin_amdgcn_sched_barrier(0);
+  if constexpr (ORD == 2) asm volatile("" ::: "memory");
   const uint4 *src = reinterpret_cast<const uint4 *>(chunk) + rr + 32 * h;
 #pragma unroll
   for (int u = 0; u < KQ4GvStage<HS>::NU; ++u) {
     const int i = (u << HS) + p;
     const uint4 v = kq4_ld_nt(src + 64 * i);
     st.n[4 * u] = v.x; st.n[4 * u + 1] = v.y; st.n[4 * u + 2] = v.z; st.n[4 * u + 3] = v.w;
-    if constexpr (ORD) __builtin_amdgcn_sched_barrier(0);
+    if constexpr (ORD == 1) __builtin_amdgcn_sched_barrier(0);
+    if constexpr (ORD == 2) asm volatile("" ::: "memory");
   }
+}
+
+// Load-order mode of kq4_gv_load for the first row set of a stage: a scheduling barrier for one
+// token from fp32 activations, a memory barrier for two and three (Qwen3-8B gate/up and QKV at
+// M = 2: 12.2-12.5 -> 11.7-12.0 and 5.8-5.9 -> 5.3-5.5 us). Not from four tokens on: there it
+// measured mixed (8B down at M = 4 0.5 us slower, the 2B QKV 0.3 us faster), and for 4-6 tokens
+// in single-set kernels it costs a wave per SIMD (74-96 -> 100-101 VGPRs).
+template <int M, int FQ>
+constexpr int kq4_gv_ord() {
+  if (FQ != 1) return 0;
+  return M == 1 ? 1 : (M <= 3 ? 2 : 0);
 }
 
 // Stage block of lane block jb (p = the lane's unit parity).
@@ -507,8 +522,8 @@ __global__ __launch_bounds__(R > 1 ? 512 : 1024) void kq4_gemv_kernel(const KQ4G
     KQ4GvAct<MQ, FQ, WF> ra;
     KQ4GvStage<HS> rw[R > 1 ? 2 : 1];
     kq4_gv_act_load<MQ, FQ, WF>(ra, a, st, lane, 0);
-    kq4_gv_load<HS, WF, M == 1 && FQ == 1>(rw[0], wb + ((size_t)set0 * nst + st) * CHUNK, rr,
-                                           h, p);
+    kq4_gv_load<HS, WF, kq4_gv_ord<M, FQ>()>(rw[0], wb + ((size_t)set0 * nst + st) * CHUNK, rr,
+                                             h, p);
     // One token, fp32 activations: every load is issued before the quantization waits for the
     // activations (the compiler otherwise sinks the weight loads below it, and the two memory
     // latencies add up). Not from two tokens on: there, issuing the weights before the
