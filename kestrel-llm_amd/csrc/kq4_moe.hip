@@ -28,6 +28,7 @@
 #include "kq4_internal.h"
 
 #include <stdlib.h>
+#include <type_traits>
 
 #define KQ4_MOE_MAXTK 32
 #define KQ4_MOE_MAXNE 2048  // routing: a lane's experts fit one 32-bit mask
@@ -580,11 +581,46 @@ __global__ __launch_bounds__(1024) void kq4_moe_gu_kernel(
   uint8_t *slab = kq4_moe_lds + k * SLAB;
   float *sx = reinterpret_cast<float *>(slab + PC * KQ4_MOE_QTS);     // [16][PC]
   float *accb = reinterpret_cast<float *>(kq4_moe_lds + nst * SLAB);   // [2][PC][32]
+  // Several tokens: a gate wave stages stage k's codes and scales of a pass's pairs (zeros past
+  // them and past K): 4 pairs x 16 blocks x 2 halves = 128 units of 16 B (two per lane) and 64
+  // scales (one per lane). The first pass's are loaded before the weights (their pair ids from
+  // the slot record), so that staging them waits only for these loads: the loads complete in
+  // issue order, and issued after the weights they held the stage barrier until every weight
+  // load was in.
+  uint4 pv[2] = {make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0)};
+  float px = 0.0f;
+  auto stage_load = [&](int c0, auto &&pid) {
+    const int np = cnt - c0 < PC ? cnt - c0 : PC;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int i = lane + 64 * u;
+      const int p = i >> 5, bb = (i >> 1) & 15, hh = i & 1;
+      pv[u] = make_uint4(0, 0, 0, 0);
+      if (p < np && bb < nblk) {
+        const int tok = pid(c0 + p) / tk;
+        pv[u] = *reinterpret_cast<const uint4 *>(xq + (size_t)tok * d + (size_t)(16 * k + bb) * 32 +
+                                                 16 * hh);
+      }
+    }
+    // a buffer load with a 32-bit offset: a 64-bit per-lane address of this read, hoisted out of
+    // the passes' loop by the compiler, spilled
+    const int p = lane >> 4, bb = lane & 15;
+    px = p < np && bb < nblk
+             ? __uint_as_float(kq4_bload4(kq4_rsrc(xd, 0xFFFFFFFFu),
+                                          4u * (uint32_t)((pid(c0 + p) / tk) * nb + 16 * k + bb)))
+             : 0.0f;
+  };
+  if (!T1 && m == 0) {
+    const KQ4MoeSlot<4> s4 = kq4_moe_slot<4>(rec, slot);
+    stage_load(0, [&](int j) { return kq4_moe_pair<4>(s4, ex_pair, j); });
+  }
   KQ4MoeW<8, 2> w;
   kq4_moe_wload<8, 2>(w, (m ? U : G) + ((size_t)((e * ef) / 32 + rs) * nst + k) * KQ4_STREAM_CHUNK,
                       lane, 0, 0);
 
-  for (int c0 = 0; c0 < cnt; c0 += PC) {
+  // one pass of up to PC pairs; the first pass is a call of its own, so that its staged values
+  // are not kept live around the loop of the later ones
+  auto run_pass = [&](int c0, auto first) {
     const int np = cnt - c0 < PC ? cnt - c0 : PC;
     if (m == 0 && T1) {
       // token 0's stage k quantized here, a lane quad per block (8 values per lane), as the prep
@@ -616,25 +652,15 @@ __global__ __launch_bounds__(1024) void kq4_moe_gu_kernel(
               make_uint4(0, 0, 0, 0);
       }
       if (lane >= 16) sx[(lane & 15) * PC + (lane >> 4)] = 0.0f;
-    } else if (m == 0) {   // stage k's codes and scales of the pass's pairs (zeros past them and past K)
+    } else if (m == 0) {
+      if constexpr (!decltype(first)::value) stage_load(c0, pair);
 #pragma unroll
-      for (int u = 0; u < 2; ++u) {   // 4 pairs x 16 blocks x 2 halves = 128 units of 16 B
+      for (int u = 0; u < 2; ++u) {
         const int i = lane + 64 * u;
         const int p = i >> 5, bb = (i >> 1) & 15, hh = i & 1;
-        uint4 v = make_uint4(0, 0, 0, 0);
-        if (p < np && bb < nblk) {
-          const int tok = pair(c0 + p) / tk;
-          v = *reinterpret_cast<const uint4 *>(xq + (size_t)tok * d + (size_t)(16 * k + bb) * 32 +
-                                               16 * hh);
-        }
-        *reinterpret_cast<uint4 *>(slab + p * KQ4_MOE_QTS + kq4_moe_qpos(bb) + 16 * hh) = v;
+        *reinterpret_cast<uint4 *>(slab + p * KQ4_MOE_QTS + kq4_moe_qpos(bb) + 16 * hh) = pv[u];
       }
-      {
-        const int p = lane >> 4, bb = lane & 15;      // 64 scales
-        float x = 0.0f;
-        if (p < np && bb < nblk) x = xd[(size_t)(pair(c0 + p) / tk) * nb + 16 * k + bb];
-        sx[bb * PC + p] = x;
-      }
+      sx[(lane & 15) * PC + (lane >> 4)] = px;
     }
     __syncthreads();
     float t[16][VT];
@@ -701,7 +727,9 @@ __global__ __launch_bounds__(1024) void kq4_moe_gu_kernel(
       }
     }
     __syncthreads();   // before the next pass overwrites the slabs and sums
-  }
+  };
+  run_pass(0, std::true_type{});
+  for (int c0 = PC; c0 < cnt; c0 += PC) run_pass(c0, std::false_type{});
 }
 
 // Re-quantize caller-provided av (stage-wise verification of the down projection).
