@@ -544,9 +544,13 @@ __global__ __launch_bounds__(R > 1 ? 512 : 1024) void kq4_gemv_kernel(const KQ4G
     }
 #pragma unroll
     for (int q = 0; q < R; ++q) {
-      if (q + 1 < R && set0 + q + 1 < sets)
-        kq4_gv_load<HS, WF>(rw[(q + 1) & 1], wb + ((size_t)(set0 + q + 1) * nst + st) * CHUNK,
-                            rr, h, p);
+      // the next set's loads are unconditional (a group's sets past the matrix reload its last
+      // set, computed on but not stored): behind a branch, the wait counts at the join had to
+      // hold for both paths, and the current set's blocks waited for some of the next set's loads
+      if (q + 1 < R) {
+        const int sn = set0 + q + 1 < sets ? set0 + q + 1 : sets - 1;
+        kq4_gv_load<HS, WF>(rw[(q + 1) & 1], wb + ((size_t)sn * nst + st) * CHUNK, rr, h, p);
+      }
       if (q == 0 || set0 + q < sets) {
         if (KIND == 0) kq4_gv_dot4<M, HS>(rw[q & 1], sq, sx, h, p, acc[q]);
         else kq4_gv_mfma_stage<M, HS, WF>(rw[q & 1], sq, sx, lane, p, acc[q]);
