@@ -944,21 +944,23 @@ __global__ __launch_bounds__(1024) void kq4_moe_down1_kernel(
     const int B0 = e * cbe;
     const int8_t *aq = avq + (size_t)j * ef;
     const float *ad = avd + (size_t)j * cbe;
-    // all loads first: the lane's lines, their two blocks' scales and av codes and scales
+    // all loads first: the lane's lines, their two blocks' scales and av codes and scales.
+    // Unconditional (a line past the band reloads the band's last line, not used): loads behind
+    // a branch made the wait counts at its join hold for both paths, and line 0's dots waited
+    // for nearly every load of the later lines.
     uint4 wl[NL], a0[NL], a1[NL];
     uint32_t sw[NL];
     float2 xs[NL];
 #pragma unroll
     for (int i = 0; i < NL; ++i) {
-      const int L = k + 8 * i;
-      if (L < cbe) {
-        const int uu = L >> 1, h = L & 1, Bu = B0 + 2 * uu;
-        wl[i] = *reinterpret_cast<const uint4 *>(D + kq4_stream_nib(n, Bu, h, nstD));
-        sw[i] = *reinterpret_cast<const uint32_t *>(D + kq4_stream_scale(n, Bu, nstD));
-        a0[i] = *reinterpret_cast<const uint4 *>(aq + 64 * uu + 16 * h);
-        a1[i] = *reinterpret_cast<const uint4 *>(aq + 64 * uu + 32 + 16 * h);
-        xs[i] = *reinterpret_cast<const float2 *>(ad + 2 * uu);
-      }
+      const int L = k + 8 * i < cbe ? k + 8 * i : cbe - 1;
+      const int uu = L >> 1, h = L & 1, Bu = B0 + 2 * uu;
+      wl[i] = *reinterpret_cast<const uint4 *>(D + kq4_stream_nib(n, Bu, h, nstD));
+      sw[i] = *reinterpret_cast<const uint32_t *>(D + kq4_stream_scale(n, Bu, nstD));
+      a0[i] = *reinterpret_cast<const uint4 *>(aq + 64 * uu + 16 * h);
+      a1[i] = *reinterpret_cast<const uint4 *>(aq + 64 * uu + 32 + 16 * h);
+      xs[i] = *reinterpret_cast<const float2 *>(ad + 2 * uu);
+      asm volatile("" ::: "memory");   // the lines' loads in line order, as they are consumed
     }
 #pragma unroll
     for (int i = 0; i < NL; ++i) {
