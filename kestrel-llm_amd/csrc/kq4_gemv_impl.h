@@ -105,11 +105,19 @@ KQ4_DEV void kq4_gv_load(KQ4GvStage<HS> &st, const uint8_t *__restrict__ chunk, 
                          int p) {
   // the weights are read once per launch: non-temporal loads
   const uint4 *sc = reinterpret_cast<const uint4 *>(chunk + 8192) + rr;
-  const uint4 a = kq4_ld_nt(sc);
-  st.sc[0] = a.x; st.sc[1] = a.y; st.sc[2] = a.z; st.sc[3] = a.w;
-  if (WF == 0) {
-    const uint4 b = kq4_ld_nt(sc + 32);
-    st.sc[4] = b.x; st.sc[5] = b.y; st.sc[6] = b.z; st.sc[7] = b.w;
+  if constexpr (WF == 0 && HS == 2) {
+    // quarter sets: the lane's blocks use one scale pair of each 8-block line (pair p), so it
+    // loads those 4 bytes, not the lines (which 16 lanes share)
+    const uint32_t *sw = reinterpret_cast<const uint32_t *>(sc) + p;
+    st.sc[0] = __builtin_nontemporal_load(sw);
+    st.sc[1] = __builtin_nontemporal_load(sw + 128);
+  } else {
+    const uint4 a = kq4_ld_nt(sc);
+    st.sc[0] = a.x; st.sc[1] = a.y; st.sc[2] = a.z; st.sc[3] = a.w;
+    if (WF == 0) {
+      const uint4 b = kq4_ld_nt(sc + 32);
+      st.sc[4] = b.x; st.sc[5] = b.y; st.sc[6] = b.z; st.sc[7] = b.w;
+    }
   }
   if constexpr (ORD == 1) __builtin_amdgcn_sched_barrier(0);
   if constexpr (ORD == 2) asm volatile("" ::: "memory");
@@ -167,7 +175,8 @@ KQ4_DEV float kq4_gv_wd(const KQ4GvStage<HS> &st, int jb, int p) {
     if (HS == 1) return kq4_h2f(st.sc[jb] >> (16 * p));
     return kq4_h2f(kq4_gv_pick(st.sc[2 * jb], st.sc[2 * jb + 1], p >> 1) >> (16 * (p & 1)));
   }
-  const uint32_t w = kq4_gv_pickn<HS>(&st.sc[(jb >> 1) << HS], p);
+  // quarter sets hold only the lane's pair of each line (kq4_gv_load)
+  const uint32_t w = HS == 2 ? st.sc[jb >> 1] : kq4_gv_pickn<HS>(&st.sc[(jb >> 1) << HS], p);
   return kq4_h2f(w >> (16 * (jb & 1)));
 }
 
