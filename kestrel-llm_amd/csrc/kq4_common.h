@@ -125,6 +125,7 @@ KQ4_DEV float kq4_quad_bcast(float v, int m) {
 // launch (weight streams): measured on MI355X, plain streaming reads of 7-56 MB run 9-14 %
 // faster with it than without.
 typedef unsigned int kq4_v4u __attribute__((ext_vector_type(4)));
+typedef unsigned int kq4_v2u __attribute__((ext_vector_type(2)));
 KQ4_DEV uint4 kq4_ld_nt(const void *p) {
   const kq4_v4u v = __builtin_nontemporal_load(reinterpret_cast<const kq4_v4u *>(p));
   return make_uint4(v.x, v.y, v.z, v.w);

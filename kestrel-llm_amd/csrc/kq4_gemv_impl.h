@@ -90,7 +90,7 @@ template <int HS>
 struct KQ4GvStage {
   static constexpr int NU = 8 >> HS;      // 16-B nibble loads per lane
   uint32_t n[4 * NU];                     // lane block jb (0 .. 2*NU-1): n[2jb], n[2jb+1]
-  uint32_t sc[8];                         // stage block b: f16 at sc[b/2] >> 16*(b%2)
+  uint32_t sc[8];                         // scale pairs (kq4_gv_load, kq4_gv_wd)
 };
 
 // Scales first: the loads complete in issue order, so the first block then waits only for the
@@ -100,6 +100,14 @@ struct KQ4GvStage {
 // first block then waits for nearly all of them): 1 = a scheduling barrier after each load, which
 // also keeps every later instruction below the loads; 2 = a compiler memory barrier after each,
 // which orders only the memory operations (the quantization's VALU work can still move above).
+// Stage unit (2 blocks of q4, 1 of q8) held in load slot u by a lane of parity p: u*NP + p, but
+// for q4 half sets units 2p, 2p+1, 4+2p, 5+2p (blocks 4p .. 4p+3 of each 8-block scale line).
+template <int HS, int WF>
+KQ4_DEV int kq4_gv_unit(int u, int p) {
+  if (WF == 0 && HS == 1) return 2 * p + (u & 1) + 4 * (u >> 1);
+  return (u << HS) + p;
+}
+
 template <int HS, int WF, int ORD = 0>
 KQ4_DEV void kq4_gv_load(KQ4GvStage<HS> &st, const uint8_t *__restrict__ chunk, int rr, int h,
                          int p) {
@@ -111,6 +119,13 @@ KQ4_DEV void kq4_gv_load(KQ4GvStage<HS> &st, const uint8_t *__restrict__ chunk, 
     const uint32_t *sw = reinterpret_cast<const uint32_t *>(sc) + p;
     st.sc[0] = __builtin_nontemporal_load(sw);
     st.sc[1] = __builtin_nontemporal_load(sw + 128);
+  } else if constexpr (WF == 0 && HS == 1) {
+    // half sets: parity p takes blocks 4p .. 4p+3 of each 8-block line (kq4_gv_unit), whose
+    // scales are the 8 bytes at 8p of the line
+    const uint2 *sw = reinterpret_cast<const uint2 *>(sc) + p;
+    const kq4_v2u a = __builtin_nontemporal_load(reinterpret_cast<const kq4_v2u *>(sw));
+    const kq4_v2u b = __builtin_nontemporal_load(reinterpret_cast<const kq4_v2u *>(sw + 64));
+    st.sc[0] = a.x; st.sc[1] = a.y; st.sc[2] = b.x; st.sc[3] = b.y;
   } else {
     const uint4 a = kq4_ld_nt(sc);
     st.sc[0] = a.x; st.sc[1] = a.y; st.sc[2] = a.z; st.sc[3] = a.w;
@@ -124,7 +139,7 @@ KQ4_DEV void kq4_gv_load(KQ4GvStage<HS> &st, const uint8_t *__restrict__ chunk, 
   const uint4 *src = reinterpret_cast<const uint4 *>(chunk) + rr + 32 * h;
 #pragma unroll
   for (int u = 0; u < KQ4GvStage<HS>::NU; ++u) {
-    const int i = (u << HS) + p;
+    const int i = kq4_gv_unit<HS, WF>(u, p);
     const uint4 v = kq4_ld_nt(src + 64 * i);
     st.n[4 * u] = v.x; st.n[4 * u + 1] = v.y; st.n[4 * u + 2] = v.z; st.n[4 * u + 3] = v.w;
     if constexpr (ORD == 1) __builtin_amdgcn_sched_barrier(0);
@@ -147,7 +162,7 @@ constexpr int kq4_gv_ord() {
 template <int HS, int WF>
 KQ4_DEV int kq4_gv_blk(int jb, int p) {
   if (WF) return (jb << HS) + p;
-  return 2 * (((jb >> 1) << HS) + p) + (jb & 1);
+  return 2 * kq4_gv_unit<HS, WF>(jb >> 1, p) + (jb & 1);
 }
 
 // a if p == 0, b if p == 1 (p in {0, 1}), by masks: a select between two elements of one register
@@ -166,8 +181,9 @@ KQ4_DEV uint32_t kq4_gv_pickn(const uint32_t *v, int p) {
 }
 
 // Row scale (f32) of lane block jb; the register index is compile-time in all modes.
-// q8: block b = NP*jb + p, its scale at sc[b/2] >> 16*(b%2); q4: block 2*(NP*(jb/2) + p) + jb%2,
-// at sc[NP*(jb/2) + p] >> 16*(jb%2).
+// q8: block b = NP*jb + p, its scale at sc[b/2] >> 16*(b%2) (the row's line as loaded); q4:
+// block kq4_gv_blk(jb, p), full sets at sc[jb/2] >> 16*(jb%2) of the row's two lines, half and
+// quarter sets at sc[jb/2] >> 16*(jb%2) of the lane's own pairs.
 template <int HS, int WF>
 KQ4_DEV float kq4_gv_wd(const KQ4GvStage<HS> &st, int jb, int p) {
   if (WF) {
@@ -175,8 +191,8 @@ KQ4_DEV float kq4_gv_wd(const KQ4GvStage<HS> &st, int jb, int p) {
     if (HS == 1) return kq4_h2f(st.sc[jb] >> (16 * p));
     return kq4_h2f(kq4_gv_pick(st.sc[2 * jb], st.sc[2 * jb + 1], p >> 1) >> (16 * (p & 1)));
   }
-  // quarter sets hold only the lane's pair of each line (kq4_gv_load)
-  const uint32_t w = HS == 2 ? st.sc[jb >> 1] : kq4_gv_pickn<HS>(&st.sc[(jb >> 1) << HS], p);
+  // half and quarter sets hold only the lane's scales (kq4_gv_load), in load-slot order
+  const uint32_t w = HS >= 1 ? st.sc[jb >> 1] : kq4_gv_pickn<HS>(&st.sc[(jb >> 1) << HS], p);
   return kq4_h2f(w >> (16 * (jb & 1)));
 }
 
