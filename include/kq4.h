@@ -34,7 +34,11 @@
  * whatever calls run after its capture. The workspace cannot grow while a stream is being
  * captured (that needs hipMalloc): such a call returns KQ4_EINVAL and launches nothing. Size it
  * before capturing with kq4_workspace_reserve (kq4_matmul_workspace_bytes,
- * kq4_moe_workspace_bytes), or by running the same calls once eagerly.
+ * kq4_moe_workspace_bytes), or by running the same calls once eagerly. kq4_workspace_trim frees
+ * the outgrown workspaces once the graphs captured before the growth are destroyed. Only the
+ * call's own stream is asked whether it is capturing: a call that grows the workspace on
+ * another stream while some stream captures in hipStreamCaptureModeGlobal fails in hipMalloc
+ * (KQ4_ENOMEM) and invalidates that capture, so reserve first in that mode too.
  *
  * Error convention: device-pointer calls return KQ4_OK (0) or a negative KQ4_E* code;
  * host-pointer drop-in calls return 1 (done on the GPU) or 0 (not done: the caller runs its
@@ -105,11 +109,13 @@ const char *kq4_version(void);
  * gemv_wpcu, gemv_maxw, gemv_fq (0 / 1: activations quantized by a separate launch / in the
  * GEMV), gemv_fq_work, gemv_silu_fq_work, gemm_kind (0: the prefill GEMM on int8 MFMA, the
  * default; 1: on fp8 operands; the same outputs), gemm_tile (0: the planner's choice; 1 / 2 / 3 /
- * 4: 128x128 / 64x128 / 64x64 / 128x64 token x row tiles; the same outputs). value < 0 restores
- * the default (for most, the
- * planner's own choice). The initial values come from the environment variables KQ4_
- * + the upper-case name. Takes effect for launches planned after it returns. */
+ * 4: 128x128 / 64x128 / 64x64 / 128x64 token x row tiles; the same outputs). The initial value
+ * of each comes from the environment variable KQ4_ + its upper-case name, else the built-in
+ * default (for most, the planner's own choice); value < 0 restores that initial value. Takes
+ * effect for launches planned after it returns. */
 int kq4_set_option(const char *name, int value);
+/* The option's current value in *value (-1: the planner's choice). */
+int kq4_get_option(const char *name, int *value);
 
 /* ---- host-pointer drop-in API (synchronous; 1 = done, 0 = caller falls back) -------------- */
 
@@ -178,6 +184,11 @@ size_t kq4_moe_workspace_bytes(int T, int tk, int ne, int d, int ef);
 /* Grows the current device's workspace to at least `bytes` now (not while the calling thread's
  * stream is being captured). */
 int kq4_workspace_reserve(size_t bytes);
+/* Frees the current device's outgrown workspaces (kept since they grew, for graphs captured
+ * before the growth) after waiting for the device to go idle. Call it only once every graph
+ * captured before the last growth has been destroyed (a replay would read freed memory), and
+ * not while a stream captures. No counterpart in the reference. */
+int kq4_workspace_trim(void);
 
 /* Size in bytes of the stream-layout copy of a rows x cols q4 matrix (0 for a bad shape):
  * 9216 B per (32-row set, 16-block stage), rows rounded up to 32, blocks up to 16. */

@@ -194,11 +194,15 @@ const OptDef kOpts[kOptCount] = {
     {"gemm_kind", "KQ4_GEMM_KIND", -1},          {"gemm_tile", "KQ4_GEMM_TILE", 0},
 };
 std::atomic<int> g_opt[kOptCount];
+int g_opt_init[kOptCount];   // each option's value at load: its environment variable or default
 std::once_flag g_opt_once;
 
 int opt(OptId i) {
   std::call_once(g_opt_once, [] {
-    for (int k = 0; k < kOptCount; ++k) g_opt[k] = env_int(kOpts[k].env, kOpts[k].dflt);
+    for (int k = 0; k < kOptCount; ++k) {
+      g_opt_init[k] = env_int(kOpts[k].env, kOpts[k].dflt);
+      g_opt[k] = g_opt_init[k];
+    }
   });
   return g_opt[i].load(std::memory_order_relaxed);
 }
@@ -660,12 +664,39 @@ int kq4_workspace_reserve(size_t bytes) {
   return ensure_ws(Ws{&ds->ws, ds}, bytes, nullptr);
 }
 
+int kq4_workspace_trim(void) {
+  DevState *ds = nullptr;
+  int rc = cur_dev(&ds);
+  if (rc) return rc;
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (ds->retired.empty()) return KQ4_OK;
+  KQ4_HIP(hipDeviceSynchronize());   // work queued before the call may still read them
+  hipError_t e = hipSuccess;
+  for (void *p : ds->retired) {
+    const hipError_t f = hipFree(p);
+    if (e == hipSuccess) e = f;
+  }
+  ds->retired.clear();   // freed or not, never freed again
+  if (e != hipSuccess) return fail(KQ4_EHIP, "workspace_trim: hipFree: %s", hipGetErrorString(e));
+  return KQ4_OK;
+}
+
+int kq4_get_option(const char *name, int *value) {
+  if (!name || !value) return fail(KQ4_EINVAL, "get_option: null argument");
+  for (int k = 0; k < kOptCount; ++k)
+    if (strcmp(name, kOpts[k].name) == 0) {
+      *value = opt(static_cast<OptId>(k));
+      return KQ4_OK;
+    }
+  return fail(KQ4_EINVAL, "get_option: unknown option %s", name);
+}
+
 int kq4_set_option(const char *name, int value) {
   if (!name) return fail(KQ4_EINVAL, "set_option: null name");
   (void)opt(kGemvKind);   // the environment's values first
   for (int k = 0; k < kOptCount; ++k)
     if (strcmp(name, kOpts[k].name) == 0) {
-      g_opt[k] = value < 0 ? kOpts[k].dflt : value;
+      g_opt[k] = value < 0 ? g_opt_init[k] : value;
       return KQ4_OK;
     }
   return fail(KQ4_EINVAL, "set_option: unknown option %s", name);

@@ -755,11 +755,13 @@ int kq4_launch_gemm_f8(float *out, const float *res, const uint8_t *w, const uin
   auto tiles = [&](int bm, int bn) {
     return (long)((n_tok + bm - 1) / bm) * ((rows + bn - 1) / bn);
   };
-  const int pick = tile >= 1 && tile <= 3 ? tile
+  // tile: 1 / 2 / 3 / 4 = 128x128 / 64x128 / 64x64 / 128x64 (tokens x rows), as the int8 form
+  const int pick = tile >= 1 && tile <= 4 ? tile
                    : tiles(128, 128) >= 2L * ncu ? 1 : (tiles(64, 128) >= 2L * ncu ? 2 : 3);
   hipError_t e;
   if (pick == 1) e = gemm_f8_launch<2, 2>(out, res, w, xp, xd, rows, n_tok, nb, nst, chain, s);
   else if (pick == 2) e = gemm_f8_launch<1, 2>(out, res, w, xp, xd, rows, n_tok, nb, nst, chain, s);
+  else if (pick == 4) e = gemm_f8_launch<2, 1>(out, res, w, xp, xd, rows, n_tok, nb, nst, chain, s);
   else e = gemm_f8_launch<1, 1>(out, res, w, xp, xd, rows, n_tok, nb, nst, chain, s);
   return (int)e;
 }

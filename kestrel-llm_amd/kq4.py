@@ -27,6 +27,7 @@ SIGNATURES = [
     ("kq4_last_error", ctypes.c_char_p, []),
     ("kq4_version", ctypes.c_char_p, []),
     ("kq4_set_option", _I, [ctypes.c_char_p, _I]),
+    ("kq4_get_option", _I, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_int)]),
     ("kq4_weights_upload", _I, [_U64, _P, _I, _I]),
     ("kq4_weights_evict", _I, [_U64]),
     ("kq4_weights_clear", _I, []),
@@ -45,6 +46,7 @@ SIGNATURES = [
     ("kq4_matmul_workspace_bytes", ctypes.c_size_t, [_I, _I]),
     ("kq4_moe_workspace_bytes", ctypes.c_size_t, [_I, _I, _I, _I, _I]),
     ("kq4_workspace_reserve", _I, [ctypes.c_size_t]),
+    ("kq4_workspace_trim", _I, []),
     ("kq4_weights_prepare_dev", _I, [_P, _P, _I, _I, _P]),
     ("kq4_quantize_dev", _I, [_P, _P, _P, _P, _I, _I, _I, _P]),
     ("kq4_matmul_dev", _I, [_P, _P, _P, _P, _I, _I, _I, _I, _P]),
@@ -176,12 +178,19 @@ def init(device=0):
 
 
 def set_option(name, value):
-    """A launch-planner option (include/kq4.h kq4_set_option); value < 0 restores the default."""
+    """A launch-planner option (include/kq4.h kq4_set_option); value < 0 restores its initial
+    value (the KQ4_* environment variable, else the built-in default)."""
     check(lib().kq4_set_option(name.encode(), int(value)), f"kq4_set_option({name})")
 
 
+def get_option(name):
+    v = ctypes.c_int(0)
+    check(lib().kq4_get_option(name.encode(), ctypes.byref(v)), f"kq4_get_option({name})")
+    return v.value
+
+
 class options:
-    """Context manager setting planner options and restoring their defaults on exit."""
+    """Context manager setting planner options and restoring their initial values on exit."""
 
     def __init__(self, **kv):
         self.kv = kv
@@ -337,6 +346,11 @@ def moe_workspace_bytes(T, tk, ne, d, ef):
 def workspace_reserve(nbytes):
     """Grows the device workspace before a HIP graph capture (see include/kq4.h)."""
     check(lib().kq4_workspace_reserve(nbytes), "kq4_workspace_reserve")
+
+
+def workspace_trim():
+    """Frees the outgrown workspaces once no graph captured before their growth is alive."""
+    check(lib().kq4_workspace_trim(), "kq4_workspace_trim")
 
 
 def stream_bytes(rows, cols):

@@ -1,5 +1,6 @@
 import os
 import sys
+from fractions import Fraction
 
 import numpy as np
 import pytest
@@ -64,3 +65,12 @@ def rel_err(got, ref):
     d = np.abs(got - ref).max() if ref.size else 0.0
     m = np.abs(ref).max() if ref.size else 0.0
     return (d / m if m > 0 else d), d
+
+
+def rn32(q):
+    """A rational rounded to binary32, nearest with ties to even (the one rounding of an
+    IEEE-754 single-precision instruction)."""
+    f = np.float32(float(q))
+    c = [f, np.nextafter(f, np.float32(np.inf)), np.nextafter(f, np.float32(-np.inf))]
+    return min(c, key=lambda v: (abs(Fraction(float(v)) - q),
+                                 int(np.array(v, np.float32).view(np.uint32)) & 1))

@@ -1,7 +1,11 @@
 """The Python binding refuses tensors the library would read out of bounds (wrong device, dtype
 or size) before any call reaches libkq4; these checks need no GPU."""
+import os
+
 import numpy as np
 import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
 def test_host_tensor_refused(kq4_cpu):
@@ -31,3 +35,24 @@ def test_workspace_sizes(kq4_cpu):
     b64 = kq4_cpu.moe_workspace_bytes(64, 8, 128, 2048, 768)
     assert 0 < b1 < b64 and b64 >= 64 * 8 * 2048 * 4
     assert np.uint64(b64) > 0
+
+
+def test_option_reset_restores_environment_value():
+    """kq4_set_option(name, -1) restores the value the KQ4_* environment variable gave at load,
+    not the built-in default (no device needed; a child process, since the environment is read
+    once per process)."""
+    import subprocess
+    import sys
+    code = (
+        "import kq4\n"
+        "assert kq4.get_option('gemv_wpcu') == 40\n"
+        "assert kq4.get_option('gemm_tile') == 0\n"
+        "with kq4.options(gemv_wpcu=16, gemm_tile=2):\n"
+        "    assert kq4.get_option('gemv_wpcu') == 16 and kq4.get_option('gemm_tile') == 2\n"
+        "assert kq4.get_option('gemv_wpcu') == 40 and kq4.get_option('gemm_tile') == 0\n"
+        "print('ok')\n")
+    env = dict(os.environ, KQ4_GEMV_WPCU="40")
+    env.pop("KQ4_GEMM_TILE", None)
+    r = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True,
+                       cwd=os.path.join(ROOT, "kestrel-llm_amd"), timeout=120)
+    assert r.returncode == 0 and r.stdout.strip() == "ok", r.stderr

@@ -123,3 +123,28 @@ def test_growth_during_capture_is_refused(kq4, torch_dev):
     graph.replay()
     torch.cuda.synchronize()
     assert float(marker.sum()) == 7.0 * 16
+
+
+def test_workspace_trim_frees_outgrown_workspaces(kq4, torch_dev, orc):
+    """Growth keeps every outgrown workspace for graphs captured before it; once no such graph is
+    alive kq4_workspace_trim frees them (the device's free memory rises by at least the 1.25 GiB
+    buffer that the second growth retired), and calls after it run in the current workspace."""
+    torch = torch_dev
+    kq4.workspace_reserve(1 << 30)            # the workspace is now >= 1.25 GiB
+    kq4.workspace_reserve(2 << 30)            # ... and that one is retired
+    torch.cuda.synchronize()
+    free0, _ = torch.cuda.mem_get_info()
+    kq4.workspace_trim()
+    free1, _ = torch.cuda.mem_get_info()
+    print(f"trim freed {(free1 - free0) / 2**30:.2f} GiB")
+    assert free1 - free0 >= (5 << 30) // 4
+    kq4.workspace_trim()                      # nothing left to free
+    rows, cols, n = 256, 2048, 64
+    w = synth.make_q4_weights(rows, cols, 31)
+    x = synth.make_activations(n, cols, 32)
+    out = torch.empty((n, rows), device="cuda")
+    kq4.matmul_dev(out, to_dev(torch, x), kq4.prepare_dev(to_dev(torch, w), rows, cols), rows,
+                   cols)
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy().view(np.uint32),
+                          orc.matmul(w, x, rows, cols).view(np.uint32))

@@ -176,17 +176,21 @@ def test_gemm_large_tiles_bit_exact(kq4, torch_dev, orc, n, rows, chain, cols, k
     assert np.array_equal(got[tok, row].view(np.uint32), want.view(np.uint32))
 
 
+@pytest.mark.parametrize("kind", [0, 1])
 @pytest.mark.parametrize("tile", [1, 2, 3, 4])
 @pytest.mark.parametrize("chain", [0, 1, 2, 3])
-def test_gemm_tile_forms_bit_exact(kq4, torch_dev, orc, tile, chain):
+def test_gemm_tile_forms_bit_exact(kq4, torch_dev, orc, tile, chain, kind):
     """Every tile form forced through the planner option gemm_tile (128x128, 64x128, 64x64,
-    128x64 tokens x rows; the C-tile chain is capped at 64x128) is bit-identical to the oracle,
-    with an odd block count (K = 672) and a partial last row set and token tile."""
+    128x64 tokens x rows; the C-tile chain is capped at 64x128), in both GEMM forms (gemm_kind
+    0 int8 MFMA, 1 fp8 operands; the C-tile chain always takes the int8 one), is bit-identical to
+    the oracle, with an odd block count (K = 672) and a partial last row set and token tile."""
+    if kind == 1 and chain == 1:
+        pytest.skip("the C-tile chain has no fp8 form: the int8 case covers it")
     torch = torch_dev
     n, rows, cols = 300, 2000, 672
     w, x = case(rows, cols, n, 900 + 10 * tile + chain)
     out = torch.empty((n, rows), dtype=torch.float32, device="cuda")
-    with kq4.options(gemm_tile=tile):
+    with kq4.options(gemm_tile=tile, gemm_kind=kind):
         kq4.matmul_dev(out, to_dev(torch, x), wdev(kq4, torch, w, rows, cols), rows, cols,
                        chain=chain)
     torch.cuda.synchronize()
@@ -200,6 +204,44 @@ def test_gemm_tile_forms_bit_exact(kq4, torch_dev, orc, tile, chain):
                           rng.integers(0, rows, 64), rng.integers(0, rows, 1024)]).astype(np.int32)
     want = orc.matmul_q_sample(w, xq, xd, rows, cols, n, tok, row, chain=chain)
     assert np.array_equal(got[tok, row].view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("form", ["matmul", "silu", "multi"])
+def test_gemm_f8_auto_tail(kq4, torch_dev, orc, form):
+    """The fp8-operand GEMM (gemm_kind = 1) with an AUTO-chain tail: 301 tokens are 300 on fp8
+    operands (the asm chain, bit-exact) and one C-tile token that the GEMV quantizes from its
+    fp32 row into the workspace the operands occupy (within 1e-5), for the plain, SiLU and
+    several-matrix calls."""
+    torch = torch_dev
+    n, cols = 301, 1024
+    rows = [512, 256] if form == "multi" else [512]
+    ws = [synth.make_q4_weights(r, cols, 950 + i) for i, r in enumerate(rows)]
+    x = synth.make_activations(n, cols, 960)
+    up = synth.make_activations(n, cols, 961)
+    res = [synth.make_activations(n, r, 970 + i) for i, r in enumerate(rows)]
+    outs = [torch.empty((n, r), dtype=torch.float32, device="cuda") for r in rows]
+    W = [wdev(kq4, torch, w, r, cols) for w, r in zip(ws, rows)]
+    with kq4.options(gemm_kind=1):
+        if form == "matmul":
+            kq4.matmul_dev(outs[0], to_dev(torch, x), W[0], rows[0], cols,
+                           residual=to_dev(torch, res[0]))
+        elif form == "silu":
+            kq4.matmul_silu_dev(outs[0], to_dev(torch, x), to_dev(torch, up), W[0], rows[0],
+                                cols, residual=to_dev(torch, res[0]))
+        else:
+            kq4.matmul_multi_dev(outs, to_dev(torch, x), W, rows, cols,
+                                 residuals=[to_dev(torch, r) for r in res])
+    torch.cuda.synchronize()
+    for o, w, r, rr in zip(outs, ws, rows, res):
+        if form == "silu":
+            want = orc.matmul_silu(w, x, up, r, cols, residual=rr)
+        else:
+            want = orc.matmul(w, x, r, cols, residual=rr)
+        got = host(o)
+        assert np.array_equal(got[:300].view(np.uint32), want[:300].view(np.uint32)), form
+        e, a = rel_err(got[300:], want[300:])
+        print(f"f8 tail {form} rows={r}: tail rel={e:.3e} maxabs={a:.3e}")
+        assert e <= TOL
 
 
 def test_gemm_from_prequantized(kq4, torch_dev, orc):

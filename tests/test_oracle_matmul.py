@@ -6,10 +6,13 @@ fixes: brute-force integer sums, exact-arithmetic cases (power-of-two scales: ev
 exact, so any correct chain equals the exact sum), constructed cases where the lo/hi split and
 the f16-rounded activation scale change the fp32 result, and the float64 error budget.
 """
+from fractions import Fraction
+
 import numpy as np
 import pytest
 
 import synth
+from conftest import rn32
 
 
 def rand_case(rows, cols, n, seed, **kw):
@@ -141,3 +144,71 @@ def test_sample_matches_full(orc):
     row = np.array([0, 15, 7, 1, 14], np.int32)
     s = orc.matmul_q_sample(w, xq, xd, rows, cols, n, tok, row)
     assert np.array_equal(s, full[tok, row])
+
+
+def q4_chain_emul(s_lo, s_hi, wd, xd, chain, fused=True):
+    """One output (token, row) of the reference's q4 chain in exact rationals, one binary32
+    rounding per NEON instruction:
+      V1 C-tile (q4x4_dot1_group16, vllm_safetensors.c:4190-4216, collapse :4250):
+         dsv = fmul(wd, xd); lo = fmla(lo, scvtf(16*S_lo, #4), dsv); hi likewise; lo + hi
+      V2 M4f (q4x4_dot1_group16_gemv, :4233-4251): one fmla chain over S_lo + S_hi
+      V3 asm (llama_gemm_q4_0_4x4_asm.c:151-161): fcvtl of the f16 activation scale,
+         fmul by the weight scale, scvtf #4, fmla
+    scvtf(16*S, #4) = S exactly. fused=False is a planted mistake: fmla as fmul then fadd."""
+    R = lambda v: Fraction(float(v))  # noqa: E731
+
+    def fmla(acc, s, d):
+        if fused:
+            return rn32(R(s) * R(d) + R(acc))
+        return rn32(R(rn32(R(s) * R(d))) + R(acc))
+
+    if chain == 1:
+        lo = hi = np.float32(0)
+        for sl, sh, w, x in zip(s_lo, s_hi, wd, xd):
+            dsv = rn32(R(w) * R(x))
+            lo = fmla(lo, int(sl), dsv)
+            hi = fmla(hi, int(sh), dsv)
+        return rn32(R(lo) + R(hi))
+    acc = np.float32(0)
+    for sl, sh, w, x in zip(s_lo, s_hi, wd, xd):
+        xs = np.float32(np.float16(x)) if chain == 3 else x
+        acc = fmla(acc, int(sl) + int(sh), rn32(R(w) * R(xs)))
+    return acc
+
+
+@pytest.mark.parametrize("chain", [1, 2, 3])
+def test_chains_against_instruction_emulation(orc, chain):
+    """Every output of each q4 chain equals the exact-rational emulation of its instruction
+    sequence, and a planted unfused multiply-add (fmul + fadd: two roundings) disagrees with the
+    oracle on some output, so the oracle's fmaf is what the reference's fmla computes. Scales
+    near 1 with many blocks make the products inexact."""
+    rows, cols, n = 8, 1024, 2
+    w, x = rand_case(rows, cols, n, 50 + chain, sigma=0.5, floor=0.25)
+    xq, xd = orc.quantize(x, cols)
+    lo, hi = orc.block_sums(w, xq, rows, cols)
+    wd = synth.tile_scales(w, rows, cols)
+    res = np.random.default_rng(chain).standard_normal((n, rows)).astype(np.float32)
+    got = orc.matmul_q(w, xq, xd, rows, cols, chain=chain)
+    got_r = orc.matmul_q(w, xq, xd, rows, cols, residual=res, chain=chain)
+    unfused_differs = 0
+    for t in range(n):
+        for r in range(rows):
+            e = q4_chain_emul(lo[t, r], hi[t, r], wd[r], xd[t], chain)
+            assert got[t, r] == e, (t, r, got[t, r], e)
+            assert got_r[t, r] == rn32(Fraction(float(res[t, r])) + Fraction(float(e)))
+            u = q4_chain_emul(lo[t, r], hi[t, r], wd[r], xd[t], chain, fused=False)
+            unfused_differs += int(u != got[t, r])
+    assert unfused_differs > 0
+
+
+def test_chain_emulation_separates_the_chains(orc):
+    """The three emulated chains give three different results on one case, so a chain swapped
+    for another (e.g. V2's single accumulator where V1 keeps lo and hi apart) fails the test
+    above."""
+    rows, cols, n = 8, 1024, 1
+    w, x = rand_case(rows, cols, n, 60, sigma=0.5, floor=0.25)
+    xq, xd = orc.quantize(x, cols)
+    outs = [orc.matmul_q(w, xq, xd, rows, cols, chain=c) for c in (1, 2, 3)]
+    assert not np.array_equal(outs[0], outs[1])
+    assert not np.array_equal(outs[1], outs[2])
+    assert not np.array_equal(outs[0], outs[2])

@@ -13,6 +13,8 @@ from fractions import Fraction
 import numpy as np
 import pytest
 
+from conftest import rn32
+
 F32 = np.float32
 
 
@@ -54,12 +56,6 @@ def decode(tiles, rows, cols, g):
     q = t[:, :, 2 * g:].view(np.int8).reshape(rows // g, nb, 8, g, 4)      # k, m, i
     codes = q.transpose(0, 3, 1, 2, 4).reshape(rows, cols)
     return codes, sc.transpose(0, 2, 1).reshape(rows, nb)
-
-
-def rn32(q):
-    f = F32(float(q))
-    c = [f, np.nextafter(f, F32(np.inf)), np.nextafter(f, F32(-np.inf))]
-    return min(c, key=lambda v: (abs(Fraction(float(v)) - q), int(np.array(v, F32).view(np.uint32)) & 1))
 
 
 def chain_emul(S, wd, xs, gemm):
