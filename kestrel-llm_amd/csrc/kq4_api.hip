@@ -178,7 +178,7 @@ int env_int(const char *name, int dflt) {
 // choice where a planner chooses.
 enum OptId {
   kGemvKind, kGemvMfmaFrom, kGemvHs, kGemvRps, kGemvWaves, kGemvWpcu, kGemvMaxw,
-  kGemvFq, kGemvFqWork, kGemvSiluFqWork, kGemmKind, kGemmTile, kOptCount
+  kGemvFq, kGemvFqWork, kGemvSiluFqWork, kGemmKind, kGemmTile, kGemmSplit, kOptCount
 };
 struct OptDef {
   const char *name, *env;
@@ -192,6 +192,7 @@ const OptDef kOpts[kOptCount] = {
     {"gemv_fq", "KQ4_GEMV_FQ", -1},              {"gemv_fq_work", "KQ4_GEMV_FQ_WORK", 45000},
     {"gemv_silu_fq_work", "KQ4_GEMV_SILU_FQ_WORK", 15000},
     {"gemm_kind", "KQ4_GEMM_KIND", -1},          {"gemm_tile", "KQ4_GEMM_TILE", 0},
+    {"gemm_split", "KQ4_GEMM_SPLIT", -1},
 };
 std::atomic<int> g_opt[kOptCount];
 int g_opt_init[kOptCount];   // each option's value at load: its environment variable or default
@@ -282,6 +283,20 @@ bool gemv_fq(long work, int n, int rps, bool silu) {
   if (force == 0 || force == 1) return force;
   if (silu) return work <= opt(kGemvSiluFqWork);
   return rps > 1 || work <= (n <= 4 ? opt(kGemvFqWork) : opt(kGemvFqWork) * 4 / 9);
+}
+
+// K slices of each matrix's prefill GEMM (kq4_gemm_ksplit) into ksp[], and the workspace bytes
+// of their partial sums: one buffer for the largest, reused matrix after matrix (the launches
+// are stream-ordered).
+size_t split_bytes(int n_mats, const int *rows, int cols, int n, int wf, int chain, int ncu,
+                   int *ksp) {
+  size_t mx = 0;
+  for (int i = 0; i < n_mats; ++i) {
+    ksp[i] = kq4_gemm_ksplit(n, rows[i], cols, wf, chain, ncu, opt(kGemmSplit));
+    const size_t b = (size_t)(ksp[i] - 1) * n * rows[i] * sizeof(float);
+    mx = b > mx ? b : mx;
+  }
+  return al256(mx);
 }
 
 // GEMV over n_mats matrices for n tokens (n <= 8): from fp32 x (quantized in the kernel or by a
@@ -380,7 +395,10 @@ int matmul_impl(int n_mats, float *const *out, const float *const *res, const ui
     if (n <= KQ4_GEMV_MAX_M)
       return run_gemv(ds, ws, n_mats, out, res, w, rows, cols, x, nullptr, xq_in, xd_in, n,
                       gchain ? n : 0, s, gchain ? 2 : 1);
-    if ((rc = ensure_ws(ws, qbytes, s))) return rc;
+    const int qc = gchain ? KQ4_CHAIN_Q8GEMM : KQ4_CHAIN_GEMV32;
+    int ksp[KQ4_MAX_MATS];
+    const size_t pbytes = split_bytes(n_mats, rows, cols, n, 1, qc, ds->ncu, ksp);
+    if ((rc = ensure_ws(ws, qbytes + pbytes, s))) return rc;
     Carve cv{static_cast<char *>(ws.b->p)};
     KQ4GemmAct act{xq_in, cols, 32, xd_in, nb, 1};
     if (x) {
@@ -388,11 +406,14 @@ int matmul_impl(int n_mats, float *const *out, const float *const *res, const ui
       float *d = cv.take<float>((size_t)n * nb);
       KQ4_HIP((hipError_t)kq4_launch_quantize(x, q, d, nullptr, n, cols, 0, s, 0));
       act = KQ4GemmAct{q, cols, 32, d, nb, 1};
+    } else {
+      cv.off = qbytes;
     }
+    float *part = pbytes ? cv.take<float>(pbytes / sizeof(float)) : nullptr;
     for (int i = 0; i < n_mats; ++i)
       KQ4_HIP((hipError_t)kq4_launch_gemm(out[i], res ? res[i] : nullptr, w[i], act, rows[i],
-                                          cols, n, gchain ? KQ4_CHAIN_Q8GEMM : KQ4_CHAIN_GEMV32,
-                                          ds->ncu, s, 1, opt(kGemmTile)));
+                                          cols, n, qc, ds->ncu, s, 1, opt(kGemmTile), ksp[i],
+                                          part));
     return KQ4_OK;
   }
 
@@ -427,7 +448,9 @@ int matmul_impl(int n_mats, float *const *out, const float *const *res, const ui
     return run_gemv(ds, ws, n_mats, o2, r2, w, rows, cols, x + (size_t)main_n * cols,
                     xu ? xu + (size_t)main_n * cols : nullptr, nullptr, nullptr, tail, 0, s);
   }
-  if ((rc = ensure_ws(ws, qbytes, s))) return rc;
+  int ksp[KQ4_MAX_MATS];
+  const size_t pbytes = split_bytes(n_mats, rows, cols, main_n, 0, main_chain, ds->ncu, ksp);
+  if ((rc = ensure_ws(ws, qbytes + pbytes, s))) return rc;
   Carve cv{static_cast<char *>(ws.b->p)};
   KQ4GemmAct act;
   const int8_t *xq_t = nullptr;
@@ -447,9 +470,11 @@ int matmul_impl(int n_mats, float *const *out, const float *const *res, const ui
     xq_t = xq_in + (size_t)main_n * cols;
     xd_t = xd_in + (size_t)main_n * nb;
   }
+  float *part = pbytes ? cv.take<float>(pbytes / sizeof(float)) : nullptr;
   for (int i = 0; i < n_mats; ++i)
     KQ4_HIP((hipError_t)kq4_launch_gemm(out[i], res ? res[i] : nullptr, w[i], act, rows[i], cols,
-                                        main_n, main_chain, ds->ncu, s, 0, opt(kGemmTile)));
+                                        main_n, main_chain, ds->ncu, s, 0, opt(kGemmTile), ksp[i],
+                                        part));
   if (tail) {
     float *o2[KQ4_MAX_MATS];
     const float *r2[KQ4_MAX_MATS];
@@ -647,9 +672,11 @@ void kq4_shutdown(void) {
 
 size_t kq4_matmul_workspace_bytes(int n_batch, int cols) {
   if (n_batch < 0 || cols <= 0 || cols % 32) return 0;
-  // quantized activations (int8 or the fp8 GEMM's operand pairs) and the one-token RMSNorm row
+  // quantized activations (int8 or the fp8 GEMM's operand pairs) and the one-token RMSNorm row;
+  // beyond the GEMV's tokens the planner's K-split partial sums, at most KQ4_SPLIT_PART_MAX
   const size_t q = qa_bytes(n_batch, cols), f = f8_bytes(n_batch, cols);
-  return (q > f ? q : f) + al256((size_t)cols * sizeof(float));
+  const size_t part = n_batch > KQ4_GEMV_MAX_M ? (size_t)KQ4_SPLIT_PART_MAX : 0;
+  return (q + part > f ? q + part : f) + al256((size_t)cols * sizeof(float));
 }
 
 size_t kq4_moe_workspace_bytes(int T, int tk, int ne, int d, int ef) {
@@ -812,16 +839,26 @@ int kq4_matmul_dev(float *out, const float *x, const float *residual, const uint
 int kq4_matmul_noalloc_dev(float *out, const float *x, const float *residual, const uint8_t *w,
                            int rows, int cols, int n_batch, int chain, void *stream) {
   if (!x && n_batch) return fail(KQ4_EINVAL, "null x");
-  const size_t need = n_batch > 0 && cols > 0 && cols % 32 == 0
-                         ? (n_batch <= KQ4_GEMV_MAX_M ? qa_bytes(n_batch, cols)
-                                                      : f8_bytes(n_batch, cols))
-                         : 0;
-  if (need > (size_t)KQ4_NOALLOC_SCRATCH_BYTES)
-    return fail(KQ4_EINVAL, "matmul_noalloc: %d tokens x %d columns need %zu B of scratch; the "
-                "maximum is %u B", n_batch, cols, need, (unsigned)KQ4_NOALLOC_SCRATCH_BYTES);
   DevState *ds = nullptr;
   int rc = cur_dev(&ds);
   if (rc) return rc;
+  size_t need = 0;
+  if (n_batch > 0 && cols > 0 && cols % 32 == 0) {
+    if (n_batch <= KQ4_GEMV_MAX_M) {
+      need = qa_bytes(n_batch, cols);
+    } else {   // fp8 operands, or int8 operands and the K-split partial sums
+      const int main_n = chain == KQ4_CHAIN_AUTO ? (n_batch & ~3) : n_batch;
+      const int mc = chain == KQ4_CHAIN_AUTO ? KQ4_CHAIN_ASM : chain;
+      int ksp = 1;
+      const size_t q = qa_bytes(n_batch, cols) + split_bytes(1, &rows, cols, main_n, 0, mc,
+                                                             ds->ncu, &ksp);
+      const size_t f = f8_bytes(n_batch, cols);
+      need = q > f ? q : f;
+    }
+  }
+  if (need > (size_t)KQ4_NOALLOC_SCRATCH_BYTES)
+    return fail(KQ4_EINVAL, "matmul_noalloc: %d tokens x %d columns need %zu B of scratch; the "
+                "maximum is %u B", n_batch, cols, need, (unsigned)KQ4_NOALLOC_SCRATCH_BYTES);
   Buf b;   // the device's copy of kq4_scratch, fixed: matmul_impl carves it and never grows it
   b.p = ds->scratch;
   b.cap = KQ4_NOALLOC_SCRATCH_BYTES;

@@ -45,11 +45,17 @@ KQ4_DEV int kq4_mfma_tok(int v, int half) { return 8 * (v >> 2) + 4 * half + (v 
 
 // TM / TN = MFMA token / row tiles per wave: a workgroup covers BM = 64*TM tokens x BN = 64*TN
 // rows (128 x 128, or smaller when the launch would otherwise have fewer than two tiles per CU).
+// Split K (ksplit > 1): the launch covers ksplit K slices of ks blocks (a multiple of the
+// stream layout's stage, so a slice's weights start at a chunk boundary), each slice a GEMM of
+// its own over blocks [s*ks, min((s+1)*ks, nb)) with the chain started at zero: slice 0 writes
+// `out`, slice s > 0 writes part + (s-1)*pstride, and kq4_split_reduce_kernel adds them in slice
+// order. A slice is the same kernel on offset pointers: weights + (first block / stage) chunks
+// (the set stride stays nst), activations + first block, with nb the slice's block count.
 template <int CHAIN, int TM, int TN, int WF>
 __global__ __launch_bounds__(256, (TM == 2 && TN == 1) ? 3 : 2) void kq4_gemm_kernel(
     float *__restrict__ out, const float *__restrict__ res, const uint8_t *__restrict__ w,
-    const KQ4GemmAct act, int rows, int n_tok, int nb, int nst, int mtiles, int ntiles,
-    uint32_t wbytes) {
+    KQ4GemmAct act, int rows, int n_tok, int nb, int nst, int mtiles, int ntiles,
+    uint32_t wbytes, int ksplit, int ks, float *__restrict__ part, long pstride) {
   constexpr int KQ4_GEMM_BM = 64 * TM, KQ4_GEMM_BN = 64 * TN;
   // ROT: the two-token-tile form, software-pipelined (see the compute below). It keeps two
   // stages in LDS at a 32-B row pitch, the two 16-B halves of row r swapped when bit 3 of r is
@@ -73,12 +79,29 @@ __global__ __launch_bounds__(256, (TM == 2 && TN == 1) ? 3 : 2) void kq4_gemm_ke
 
   // XCD-aware tile order: workgroup ids go round-robin over the 8 XCDs; give XCD x the
   // contiguous tile range [start(x), start(x) + count(x)) (a bijection for any tile count).
-  const int ntile = mtiles * ntiles;
+  // With split K the range runs over (slice, tile), slices slowest.
+  const int ntile = mtiles * ntiles * ksplit;
   const int wg = blockIdx.x;
   const int xcd = wg & 7, q8 = ntile >> 3, r8 = ntile & 7;
-  const int tile = xcd * q8 + (xcd < r8 ? xcd : r8) + (wg >> 3);
+  const int vtile = xcd * q8 + (xcd < r8 ? xcd : r8) + (wg >> 3);
+  const int tile = vtile % (mtiles * ntiles);
   const int mt = tile % mtiles;
   const int nt = tile / mtiles;
+  if (ksplit > 1) {
+    const int sl = vtile / (mtiles * ntiles);
+    const int k0 = sl * ks;   // a multiple of the stage's blocks
+    constexpr int CBK = WF ? KQ8_STREAM_CB : KQ4_STREAM_CB;
+    constexpr int CHK = WF ? KQ8_STREAM_CHUNK : KQ4_STREAM_CHUNK;
+    w += (size_t)(k0 / CBK) * CHK;
+    wbytes -= (uint32_t)((k0 / CBK) * CHK);
+    act.xq += k0 * act.q_bs;
+    act.xd += k0 * act.d_bs;
+    nb = min(ks, nb - k0);
+    if (sl > 0) {
+      out = part + (size_t)(sl - 1) * pstride;
+      res = nullptr;
+    }
+  }
   const int m0 = mt * KQ4_GEMM_BM;
   const int n0 = nt * KQ4_GEMM_BN;
 
@@ -766,33 +789,65 @@ int kq4_launch_gemm_f8(float *out, const float *res, const uint8_t *w, const uin
   return (int)e;
 }
 
+// out[i] = [res[i] +] (..((out[i] + part[0][i]) + part[1][i]) .. + part[np-1][i]): the K
+// slices' outputs added in slice order, 4 floats per thread (n4 = elements / 4).
+__global__ __launch_bounds__(256) void kq4_split_reduce_kernel(float *__restrict__ out,
+                                                               const float *__restrict__ res,
+                                                               const float *__restrict__ part,
+                                                               int np, long pstride, long n4) {
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n4) return;
+  float4 v = reinterpret_cast<const float4 *>(out)[i];
+  for (int p = 0; p < np; ++p) {
+    const float4 q = reinterpret_cast<const float4 *>(part + (size_t)p * pstride)[i];
+    v.x = v.x + q.x;
+    v.y = v.y + q.y;
+    v.z = v.z + q.z;
+    v.w = v.w + q.w;
+  }
+  if (res) {
+    const float4 r = reinterpret_cast<const float4 *>(res)[i];
+    v.x = r.x + v.x;
+    v.y = r.y + v.y;
+    v.z = r.z + v.z;
+    v.w = r.w + v.w;
+  }
+  reinterpret_cast<float4 *>(out)[i] = v;
+}
+
 template <int TM, int TN>
 static hipError_t gemm_launch(float *out, const float *res, const uint8_t *w,
                               const KQ4GemmAct &act, int rows, int n_tok, int nb, int nst,
-                              int chain, int wf, uint32_t wbytes, hipStream_t s) {
+                              int chain, int wf, uint32_t wbytes, hipStream_t s, int ksplit = 1,
+                              int ks = 0, float *part = nullptr, long pstride = 0) {
   const int mtiles = (n_tok + 64 * TM - 1) / (64 * TM);
   const int ntiles = (rows + 64 * TN - 1) / (64 * TN);
-  const dim3 grid((unsigned)(mtiles * ntiles));
+  const dim3 grid((unsigned)(mtiles * ntiles * ksplit));
   if (wf) {
     if (chain == KQ4_CHAIN_GEMV32)
       hipLaunchKernelGGL((kq4_gemm_kernel<KQ4_CHAIN_GEMV32, TM, TN, 1>), grid, dim3(256), 0, s,
-                         out, res, w, act, rows, n_tok, nb, nst, mtiles, ntiles, wbytes);
+                         out, res, w, act, rows, n_tok, nb, nst, mtiles, ntiles, wbytes, ksplit, ks,
+                         part, pstride);
     else if (chain == KQ4_CHAIN_Q8GEMM)
       hipLaunchKernelGGL((kq4_gemm_kernel<KQ4_CHAIN_Q8GEMM, TM, TN, 1>), grid, dim3(256), 0, s,
-                         out, res, w, act, rows, n_tok, nb, nst, mtiles, ntiles, wbytes);
+                         out, res, w, act, rows, n_tok, nb, nst, mtiles, ntiles, wbytes, ksplit, ks,
+                         part, pstride);
     else
       return hipErrorInvalidValue;
   } else if (chain == KQ4_CHAIN_CTILE) {
     if constexpr (TM == 2) return hipErrorInvalidValue;   // capped by the planner
     else
       hipLaunchKernelGGL((kq4_gemm_kernel<KQ4_CHAIN_CTILE, TM, TN, 0>), grid, dim3(256), 0, s,
-                         out, res, w, act, rows, n_tok, nb, nst, mtiles, ntiles, wbytes);
+                         out, res, w, act, rows, n_tok, nb, nst, mtiles, ntiles, wbytes, ksplit, ks,
+                         part, pstride);
   } else if (chain == KQ4_CHAIN_GEMV32) {
     hipLaunchKernelGGL((kq4_gemm_kernel<KQ4_CHAIN_GEMV32, TM, TN, 0>), grid, dim3(256), 0, s, out,
-                       res, w, act, rows, n_tok, nb, nst, mtiles, ntiles, wbytes);
+                       res, w, act, rows, n_tok, nb, nst, mtiles, ntiles, wbytes, ksplit, ks, part,
+                       pstride);
   } else if (chain == KQ4_CHAIN_ASM) {
     hipLaunchKernelGGL((kq4_gemm_kernel<KQ4_CHAIN_ASM, TM, TN, 0>), grid, dim3(256), 0, s, out,
-                       res, w, act, rows, n_tok, nb, nst, mtiles, ntiles, wbytes);
+                       res, w, act, rows, n_tok, nb, nst, mtiles, ntiles, wbytes, ksplit, ks, part,
+                       pstride);
   } else {
     return hipErrorInvalidValue;
   }
@@ -804,9 +859,39 @@ static hipError_t gemm_launch(float *out, const float *res, const uint8_t *w,
 // chain (two accumulator sets) takes 64x128 at most: at 128x128 it needs more than 256 registers
 // and spills. `tile` = 1/2/3/4 (128x128, 64x128, 64x64, 128x64; planner option gemm_tile)
 // forces one (for measurement and tests; the C-tile chain still caps it).
+// Blocks per K slice for ksplit slices: ceil(nb / ksplit) rounded up to whole stream-layout
+// stages; 0 when ksplit slices of that length do not all hold blocks.
+static int split_len(int nb, int cb, int ksplit) {
+  if (ksplit < 2) return nb;
+  const int ks = ((nb + ksplit - 1) / ksplit + cb - 1) / cb * cb;
+  return (long)(ksplit - 1) * ks < nb ? ks : 0;
+}
+
+// K slices of a prefill GEMM launch. Split only where the launch leaves the chip short of work:
+// fewer 128 x 128 tiles than CUs and a long K (>= 256 blocks), into the most slices (at most
+// KQ4_GEMM_SPLIT_MAX, each >= 64 blocks) that keep slices x tiles within two per CU (Qwen3-8B
+// down, K = 12288, at M = 512: 128 tiles -> 4 slices of 96 blocks, 512 workgroups). The C-tile
+// chain is never split by the planner. force: planner option gemm_split (-1 the planner, 0 / 1
+// no split, 2 .. KQ4_GEMM_SPLIT_MAX that many slices where the blocks allow it).
+// (P - 1) * n_tok * rows * 4 bytes of partial sums go to the workspace: P * tiles <= 2 * 256
+// keeps that below 24 MiB.
+int kq4_gemm_ksplit(int n_tok, int rows, int cols, int wf, int chain, int ncu, int force) {
+  if (n_tok <= 0 || rows <= 0 || cols <= 0) return 1;
+  const int nb = cols / 32;
+  const int cb = wf ? KQ8_STREAM_CB : KQ4_STREAM_CB;
+  if (force == 0 || force == 1) return 1;
+  if (force >= 2) return force <= KQ4_GEMM_SPLIT_MAX && split_len(nb, cb, force) ? force : 1;
+  const long t = (long)((n_tok + 127) / 128) * ((rows + 127) / 128);
+  const int cu = ncu < 256 ? ncu : 256;
+  if (chain == KQ4_CHAIN_CTILE || t > cu || nb < 256) return 1;
+  for (int p = KQ4_GEMM_SPLIT_MAX; p >= 2; --p)
+    if (p * t <= 2L * cu && split_len(nb, cb, p) >= 64) return p;
+  return 1;
+}
+
 int kq4_launch_gemm(float *out, const float *res, const uint8_t *w, const KQ4GemmAct &act,
                     int rows, int cols, int n_tok, int chain, int ncu, hipStream_t s, int wf,
-                    int tile) {
+                    int tile, int ksplit, float *part) {
   const int nb = cols / 32;
   const int cb = wf ? KQ8_STREAM_CB : KQ4_STREAM_CB;
   const int nst = (nb + cb - 1) / cb;
@@ -814,11 +899,14 @@ int kq4_launch_gemm(float *out, const float *res, const uint8_t *w, const KQ4Gem
   auto tiles = [&](int bm, int bn) {
     return (long)((n_tok + bm - 1) / bm) * ((rows + bn - 1) / bn);
   };
+  const int ks = split_len(nb, cb, ksplit);
+  if (ksplit < 1 || ksplit > KQ4_GEMM_SPLIT_MAX || !ks || (ksplit > 1 && !part))
+    return (int)hipErrorInvalidValue;
   // Long K (>= 256 blocks) with fewer than two 128 x 128 tiles per CU: the pipelined 128 x 64
   // form as soon as it has a tile per CU (Qwen3-8B down, K = 12288: M = 512 131.6 -> 121.4 us,
   // M = 1024 211 -> 192 us; at K = 4096 the 64-token forms stay faster).
   int pick = tile >= 1 && tile <= 4             ? tile
-             : tiles(128, 128) >= 2L * ncu       ? 1
+             : ksplit > 1 || tiles(128, 128) >= 2L * ncu ? 1
              : nb >= 256 && tiles(128, 64) >= ncu ? 4
              : tiles(64, 128) >= 2L * ncu        ? 2
                                                  : 3;
@@ -834,10 +922,23 @@ int kq4_launch_gemm(float *out, const float *res, const uint8_t *w, const KQ4Gem
   if (act.q_ts < (nb - 1) * act.q_bs + 32 || act.d_ts < (nb - 1) * act.d_bs + 1)
     return (int)hipErrorInvalidValue;
   const uint32_t wbytes = (uint32_t)wb;
+  const long ps = (long)n_tok * rows;   // floats per slice output
   hipError_t e;
-  if (pick == 1) e = gemm_launch<2, 2>(out, res, w, act, rows, n_tok, nb, nst, chain, wf, wbytes, s);
-  else if (pick == 2) e = gemm_launch<1, 2>(out, res, w, act, rows, n_tok, nb, nst, chain, wf, wbytes, s);
-  else if (pick == 4) e = gemm_launch<2, 1>(out, res, w, act, rows, n_tok, nb, nst, chain, wf, wbytes, s);
-  else e = gemm_launch<1, 1>(out, res, w, act, rows, n_tok, nb, nst, chain, wf, wbytes, s);
-  return (int)e;
+  if (pick == 1)
+    e = gemm_launch<2, 2>(out, ksplit > 1 ? nullptr : res, w, act, rows, n_tok, nb, nst, chain,
+                          wf, wbytes, s, ksplit, ks, part, ps);
+  else if (pick == 2)
+    e = gemm_launch<1, 2>(out, ksplit > 1 ? nullptr : res, w, act, rows, n_tok, nb, nst, chain,
+                          wf, wbytes, s, ksplit, ks, part, ps);
+  else if (pick == 4)
+    e = gemm_launch<2, 1>(out, ksplit > 1 ? nullptr : res, w, act, rows, n_tok, nb, nst, chain,
+                          wf, wbytes, s, ksplit, ks, part, ps);
+  else
+    e = gemm_launch<1, 1>(out, ksplit > 1 ? nullptr : res, w, act, rows, n_tok, nb, nst, chain,
+                          wf, wbytes, s, ksplit, ks, part, ps);
+  if (e != hipSuccess || ksplit < 2) return (int)e;
+  const long n4 = ps / 4;   // rows % 4 == 0
+  hipLaunchKernelGGL(kq4_split_reduce_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, s,
+                     out, res, part, ksplit - 1, ps, n4);
+  return (int)hipGetLastError();
 }

@@ -11,8 +11,9 @@ activations for M > 1 and the default MoE track; a timing baseline, never a pari
             down + residual) over 28 layers at M = 1 and 4 (the batched wrappers; from M = 2 on
             they take q4g_gemm_mat, :1583-1588, :1649, :1699-1702, :1754)
   config 3  Qwen3-8B gate (4096 -> 12288) and down (12288 -> 4096) at M = 1 (dense workers) and
-            M = 4 (q4g_gemm_mat, :1130-1187)
-  config 4  q4g_gemm_mat at M = 512 (gate and down; 2048 is the same kernel four times longer)
+            M = 2, 4, 8 (q4g_gemm_mat, :1130-1187)
+  config 4  q4g_gemm_mat at M = 512 and 2048 (gate and down; M = 2048 takes the median of
+            REPS_LONG calls, each a few hundred ms)
   config 5  st_moe_ffn_sparse_q4 (T = 1, :12921) and st_moe_ffn_sparse_q4_batch (T = 64,
             :14426) on the Qwen3-30B-A3B shape, in the default int16-activation track and in
             the int8 track (VLLM_ACTQ=1 VLLM_ACTQ16=0, :11431-11435). The track switch is read
@@ -43,6 +44,8 @@ import synth  # noqa: E402
 
 REPS = 20
 WARM = 2
+REPS_LONG = 5      # config 4 at M = 2048
+WARM_LONG = 1
 ROTATE_MIN = 512 << 20
 
 
@@ -170,17 +173,20 @@ def dense_configs(r, threads, llc, m_step):
     D = synth.make_q4_weights(h, f, 13, **synth.SCALE_8B)
     nr = n_rot(G.nbytes, llc)
     Gs, Ds = copies(G, nr), copies(D, nr)
-    for m in (1, 4, 512):
+    for m in (1, 2, 4, 8, 512, 2048):
         xg = synth.make_activations(m, h, 20 + m)
         xd = synth.make_activations(m, f, 30 + m)
         og, od = np.empty((m, f), np.float32), np.empty((m, h), np.float32)
         gs, ds = (Gs, Ds) if m <= 8 else (Gs[:2], Ds[:2])
+        rw = dict(reps=REPS_LONG, warm=WARM_LONG) if m >= 2048 else {}
         if m == 1:
             tg = median_us(Cycle(gs, lambda W: r.kref_matvec(P(og), P(W), P(xg), f, h)))
             td = median_us(Cycle(ds, lambda W: r.kref_matvec(P(od), P(W), P(xd), h, f)))
         else:
-            tg = median_us(Cycle(gs, lambda W: r.kref_gemm_mat(P(og), None, P(W), P(xg), f, h, m)))
-            td = median_us(Cycle(ds, lambda W: r.kref_gemm_mat(P(od), None, P(W), P(xd), h, f, m)))
+            tg = median_us(Cycle(gs, lambda W: r.kref_gemm_mat(P(og), None, P(W), P(xg), f, h, m)),
+                           **rw)
+            td = median_us(Cycle(ds, lambda W: r.kref_gemm_mat(P(od), None, P(W), P(xd), h, f, m)),
+                           **rw)
         if m <= 8:
             out[f"config3_m{m}"] = {
                 "gate_us": round(tg, 1), "gate_GBs": round((G.nbytes + m * 4 * (h + f)) / tg / 1e3, 2),
@@ -284,16 +290,25 @@ def _run(m_step):
         os.unlink(moe_file)
     wall = time.perf_counter() - t0
     head = dense[str(phys)][f"config2_step_m{m_step}"]
+    alt = ""
+    if len(threads) > 1:
+        h2 = dense[str(threads[1])][f"config2_step_m{m_step}"]
+        alt = (f"; at the reference's own default of nc - 2 = {threads[1]} threads "
+               f"(src/core/vllm_tp.c:339) {h2['GBs']} GB/s, {h2['us'] / 1e3:.2f} ms per step")
     return {
         "value": head["GBs"], "unit": "GB/s", "cores": phys, "kind": "reference",
         "sample": (f"config 2 (Qwen3-VL-2B decode-step linear set, 28 layers, M={m_step}): median "
-                   f"of {REPS} steps of the reference's x86 wrappers, {head['us'] / 1e3:.2f} ms "
-                   f"per step, at {phys} threads; the other configs below, {wall:.0f} s in all"),
+                   f"of {REPS} steps of the reference's x86 wrappers; value is the run at every "
+                   f"physical core ({phys} threads), {head['us'] / 1e3:.2f} ms per step{alt}; "
+                   f"the other configs below, {wall:.0f} s in all"),
         "host": dict(host, nc_sysconf=nc_sys, nc=nc, threads=threads),
         "method": f"median of {REPS} calls after {WARM} warm-up calls; seeded weights as the GPU "
                   "run, cycled over copies beyond the LLC; reference x86 flags",
         "by_threads": dense,
         "moe_config5": moe,
+        "moe_note": ("the int8 track's times sit on 4-ms steps: they measure the reference "
+                     "thread pool's park/wake (src/core/vllm_tp.c), not its kernels; the int16 "
+                     "track (the reference's x86 default) is the MoE figure to compare"),
     }
 
 

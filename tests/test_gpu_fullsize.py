@@ -10,7 +10,8 @@ the main segment n & ~3 on the asm GEMM chain (st_gemm_q4_0_4x4_batched :4328-43
 llama_gemm_q4_0_4x4_asm.c:151-161). The oracle is evaluated on sampled outputs
 (kqo_matmul_q_sample): one (token, row) in every 64 x 64 cell of the output, so every tile of
 every tile size the planner picks and every XCD's tile range is hit, plus the last token and row
-and a random spread; the main segment must be bit-identical. A 2051-token case adds the
+and a random spread; the main segment must be bit-identical, except where the planner splits K
+(down at M = 512: 1e-5 bar; bit-identical again with the split off). A 2051-token case adds the
 1..3-token C-tile tail (GEMV path, 1e-5 bar).
 
 Weights: config 3's seeded distribution (f16 |N(0, 0.015)| scales, no floor: f16 subnormal and
@@ -100,15 +101,21 @@ def samples(n_tok, rows, seed):
     return t, r
 
 
+# The planner splits K only for down at M = 512 (128 tiles of 128 x 128 for 256 CUs): 4 slices,
+# each its own chain, added in slice order (1e-5 bar); every other launch, and the same one with
+# the split turned off (planner option gemm_split = 1), is the reference's single chain, bit for
+# bit.
+@pytest.mark.parametrize("split", ["planner", "off"])
 @pytest.mark.parametrize("m", [512, 2048])
 @pytest.mark.parametrize("name", ["gate", "down"])
-def test_config4_prefill_sampled_bit_exact(kq4, torch_dev, orc, mats, name, m):
+def test_config4_prefill_sampled(kq4, torch_dev, orc, mats, name, m, split):
     torch = torch_dev
     host, dev = mats
     w, rows, cols = host[name]
     x = synth.make_activations(m, cols, 40 + m + (name == "down"))
     out = torch.empty((m, rows), dtype=torch.float32, device="cuda")
-    kq4.matmul_dev(out, to_dev(torch, x), dev[name], rows, cols)
+    with kq4.options(gemm_split=-1 if split == "planner" else 1):
+        kq4.matmul_dev(out, to_dev(torch, x), dev[name], rows, cols)
     torch.cuda.synchronize()
     got = out.cpu().numpy()
     assert np.isfinite(got).all()
@@ -119,9 +126,12 @@ def test_config4_prefill_sampled_bit_exact(kq4, torch_dev, orc, mats, name, m):
     g = got[tok, row]
     same = g.view(np.uint32) == want.view(np.uint32)
     r, a = rel_err(g, want)
-    print(f"8B prefill {name} M={m}: {tok.size} samples, bit-identical {same.sum()}, "
-          f"rel={r:.3e} maxabs={a:.3e}")
-    assert same.all(), (tok[~same][:8], row[~same][:8])
+    print(f"8B prefill {name} M={m} split={split}: {tok.size} samples, bit-identical "
+          f"{same.sum()}, rel={r:.3e} maxabs={a:.3e}")
+    if split == "planner" and name == "down" and m == 512:
+        assert r <= TOL
+    else:
+        assert same.all(), (tok[~same][:8], row[~same][:8])
 
 
 def test_config4_prefill_with_ctile_tail(kq4, torch_dev, orc, mats):

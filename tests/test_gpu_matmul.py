@@ -244,6 +244,63 @@ def test_gemm_f8_auto_tail(kq4, torch_dev, orc, form):
         assert e <= TOL
 
 
+@pytest.mark.parametrize("split", [2, 3, 4])
+@pytest.mark.parametrize("chain", [0, 1, 2, 3])
+def test_gemm_split_k(kq4, torch_dev, orc, chain, split):
+    """Split K forced through the planner option gemm_split: K = 4096 (128 blocks) in 2 slices of
+    64 blocks, 3 of 48 (the last one 32) or 4 of 32, each slice its own chain from zero, added in
+    slice order with the residual last. Every output within 1e-5 of the oracle's single chain
+    (the split is not bit-identical to it), repeat calls bit-identical, for
+    every chain, a 301-token batch (AUTO: a 1-token C-tile tail on the GEMV) and two matrices of
+    different heights in one call."""
+    torch = torch_dev
+    n, cols = 301, 4096
+    rows = [384, 136]
+    ws = [synth.make_q4_weights(r, cols, 1000 + r + chain) for r in rows]
+    x = synth.make_activations(n, cols, 1010 + split)
+    res = [synth.make_activations(n, r, 1020 + i) for i, r in enumerate(rows)]
+    W = [wdev(kq4, torch, w, r, cols) for w, r in zip(ws, rows)]
+    X = to_dev(torch, x)
+    R = [to_dev(torch, r) for r in res]
+    outs = [torch.empty((n, r), dtype=torch.float32, device="cuda") for r in rows]
+    again = [torch.empty_like(o) for o in outs]
+    with kq4.options(gemm_split=split):
+        kq4.matmul_multi_dev(outs, X, W, rows, cols, residuals=R, chain=chain)
+        kq4.matmul_multi_dev(again, X, W, rows, cols, residuals=R, chain=chain)
+    torch.cuda.synchronize()
+    for o, a2, w, r, rr in zip(outs, again, ws, rows, res):
+        got = host(o)
+        assert np.array_equal(got.view(np.uint32), host(a2).view(np.uint32))
+        want = orc.matmul(w, x, r, cols, residual=rr, chain=chain)
+        e, a = rel_err(got, want)
+        same = (got.view(np.uint32) == want.view(np.uint32)).mean()
+        print(f"split={split} chain={chain} rows={r}: rel={e:.3e} maxabs={a:.3e} "
+              f"bit-identical {same:.3f}")
+        assert e <= TOL
+
+
+@pytest.mark.parametrize("split", [1, 4])
+def test_q8_gemm_split_k(kq4, torch_dev, orc, split):
+    """Q8_0 weights (8-block stages): K = 4096 in 4 slices of 32 blocks, within 1e-5 of the
+    oracle's GEMM chain; unsplit, bit-identical."""
+    torch = torch_dev
+    n, rows, cols = 96, 256, 4096
+    tiles = synth.make_q8_weights(rows, cols, 1030)
+    x = synth.make_activations(n, cols, 1031)
+    W = kq4.q8_prepare_dev(tiles, rows, cols)
+    out = torch.empty((n, rows), dtype=torch.float32, device="cuda")
+    with kq4.options(gemm_split=split):
+        kq4.q8_matmul_dev(out, to_dev(torch, x), W, rows, cols)
+    torch.cuda.synchronize()
+    got = host(out)
+    want = orc.q8_matmul(tiles, x, rows, cols)
+    e, a = rel_err(got, want)
+    print(f"q8 split={split}: rel={e:.3e} maxabs={a:.3e}")
+    if split == 1:
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert e <= TOL
+
+
 def test_gemm_from_prequantized(kq4, torch_dev, orc):
     torch = torch_dev
     rows, cols, n = 128, 1024, 40
