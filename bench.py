@@ -48,17 +48,23 @@ TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "pmc_hbm_traffic_gemv_qwen3vl2b
 
 def profiled_traffic(m):
     """HBM bytes per launch of the dominant kernel at M = 1, from the committed rocprofv3
-    FETCH_SIZE / WRITE_SIZE summary (copy-calibrated); None for other M or without it."""
+    FETCH_SIZE / WRITE_SIZE summary (copy-calibrated), and the commit of the kernel sources it
+    was measured on (the summary's `measured_at_commit:` line); (None, None) for other M or
+    without it. The counters cannot be read inside a timed run, so the figure is only as current
+    as that commit."""
     if m != 1:
-        return None
+        return None, None
+    byts = commit = None
     try:
         with open(TRAFFIC_PROFILE) as fh:
             for line in fh:
                 if line.startswith("traffic_bytes_per_launch:"):
-                    return int(line.split(":")[1])
+                    byts = int(line.split(":")[1])
+                elif line.startswith("measured_at_commit:"):
+                    commit = line.split(":")[1].strip()
     except OSError:
         pass
-    return None
+    return byts, commit
 
 
 def layer_mats():
@@ -493,7 +499,9 @@ def profile_op(op, m, reps):
     """Launches one op `reps` times back to back (eager) for rocprofv3 runs: the 2B / 8B decode
     GEMVs, the 8B prefill GEMMs (m tokens), the Qwen3-30B-A3B MoE FFN or whole layer (router
     included; m tokens), the 8B SiLU-multiply + down and RMSNorm + QKV ops, or the 8B gate / down
-    with Q8_0 weights (m tokens: GEMV up to 8, GEMM beyond)."""
+    with Q8_0 weights (m tokens: GEMV up to 8, GEMM beyond). Launch i takes weight copy
+    i % copies, the copies together over 640 MB (above the 256 MB Infinity Cache), so every
+    launch streams its weights from HBM as in the timed extras."""
     import torch
 
     import kq4
@@ -504,8 +512,8 @@ def profile_op(op, m, reps):
         cfg = synth.QWEN3_30B_A3B_MOE
         d, ne, tk, ef = cfg["hidden"], cfg["experts"], cfg["top_k"], cfg["ef"]
         G, U, D = synth.make_moe(cfg, 50)
-        Gd, Ud = (kq4.prepare_dev(torch.from_numpy(a).cuda(), ne * ef, d) for a in (G, U))
-        Dd = kq4.prepare_dev(torch.from_numpy(D).cuda(), d, ne * ef)
+        layers = list(zip(_copies(torch, G, ne * ef, d), _copies(torch, U, ne * ef, d),
+                          _copies(torch, D, d, ne * ef)))
         X = torch.from_numpy(synth.make_activations(m, d, 60)).cuda()
         lg = torch.from_numpy(synth.make_logits(m, ne, 61)).cuda()
         sel = torch.empty((m, tk), dtype=torch.int32, device="cuda")
@@ -513,7 +521,8 @@ def profile_op(op, m, reps):
         Y = torch.empty((m, d), device="cuda")
         kq4.moe_route_dev(sel, pr, lg, tk, stream=st)
         R = torch.randn((ne, d), device="cuda") * 0.02
-        for _ in range(reps):
+        for i in range(reps):
+            Gd, Ud, Dd = layers[i % len(layers)]
             if op == "moe_layer_30b_a3b":
                 kq4.moe_layer_dev(Y, X, R, Gd, Ud, Dd, ne, tk, d, ef, stream=st)
             else:
@@ -522,39 +531,42 @@ def profile_op(op, m, reps):
         h, f = synth.QWEN3_8B["hidden"], synth.QWEN3_8B["ffn"]
         rows, cols = (h, f) if "down" in op else (f, h)
         w = kq4.q8_prepare_dev(synth.make_q8_weights(rows, cols, 15), rows, cols)
+        ws = [w] + [w.clone() for _ in range(max(1, int(ROTATE_BYTES // w.numel())))]
         x = torch.from_numpy(synth.make_activations(m, cols, 20)).cuda()
         out = torch.empty((m, rows), device="cuda")
-        for _ in range(reps):
-            kq4.q8_matmul_dev(out, x, w, rows, cols, stream=st)
+        for i in range(reps):
+            kq4.q8_matmul_dev(out, x, ws[i % len(ws)], rows, cols, stream=st)
     elif op in ("silu_down_8b", "rmsnorm_qkv_8b"):
         cfg = synth.QWEN3_8B
         h, f = cfg["hidden"], cfg["ffn"]
         if op == "silu_down_8b":
-            w = kq4.prepare_dev(torch.from_numpy(synth.make_q4_weights(h, f, 13)).cuda(), h, f)
+            ws = _copies(torch, synth.make_q4_weights(h, f, 13), h, f)
             g = torch.from_numpy(synth.make_activations(m, f, 21)).cuda()
             u = torch.rand((m, f), device="cuda") * 2 - 1
             out = torch.empty((m, h), device="cuda")
-            for _ in range(reps):
-                kq4.matmul_silu_dev(out, g, u, w, h, f, stream=st)
+            for i in range(reps):
+                kq4.matmul_silu_dev(out, g, u, ws[i % len(ws)], h, f, stream=st)
         else:
             qkv = (cfg["q_heads"] + 2 * cfg["kv_heads"]) * cfg["head_dim"]
-            w = kq4.prepare_dev(torch.from_numpy(synth.make_q4_weights(qkv, h, 14)).cuda(), qkv, h)
+            ws = _copies(torch, synth.make_q4_weights(qkv, h, 14), qkv, h)
             x = torch.from_numpy(synth.make_activations(m, h, 22)).cuda()
             nw = torch.rand(h, device="cuda") + 0.5
             out = torch.empty((m, qkv), device="cuda")
-            for _ in range(reps):
-                kq4.rmsnorm_matmul_multi_dev([out], x, nw, 1e-6, [w], [qkv], h, stream=st)
+            for i in range(reps):
+                kq4.rmsnorm_matmul_multi_dev([out], x, nw, 1e-6, [ws[i % len(ws)]], [qkv], h,
+                                             stream=st)
     else:
         cfg = CFG if op.endswith("2b") else synth.QWEN3_8B
         h, f = cfg["hidden"], cfg["ffn"]
         rows, cols = (h, f) if "down" in op else (f, h)
         nmat = 2 if "gate_up" in op else 1
-        ws = [kq4.prepare_dev(torch.from_numpy(synth.make_q4_weights(rows, cols, 11 + i)).cuda(),
-                              rows, cols) for i in range(nmat)]
+        mats = [_copies(torch, synth.make_q4_weights(rows, cols, 11 + i), rows, cols)
+                for i in range(nmat)]
         x = torch.from_numpy(synth.make_activations(m, cols, 20)).cuda()
         outs = [torch.empty((m, rows), device="cuda") for _ in range(nmat)]
-        for _ in range(reps):
-            kq4.matmul_multi_dev(outs, x, ws, [rows] * nmat, cols, stream=st)
+        for i in range(reps):
+            kq4.matmul_multi_dev(outs, x, [c[i % len(c)] for c in mats], [rows] * nmat, cols,
+                                 stream=st)
     torch.cuda.synchronize()
     return dict(op=op, m=m, reps=reps)
 
@@ -591,6 +603,7 @@ def main():
         print(json.dumps(profile_op(args.profile_op, args.m, args.reps)))
         return
     g = run_gpu(args)
+    traffic, traffic_commit = profiled_traffic(args.m)
     line = {
         "metric": METRIC,
         "value": round(g["value"], 2),
@@ -614,7 +627,8 @@ def main():
         "gate_up_us_per_call": round(g["us_gate_up"], 3),
         "roofline": {"bound": "hbm", "achieved": round(g["achieved"], 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(g["achieved"] / HBM_PEAK_GBS, 4),
-                     "traffic": profiled_traffic(args.m),
+                     "traffic": traffic,
+                     "traffic_measured_at_commit": traffic_commit,
                      "kernel": "kq4_gemv_kernel (fused gate/up, 2 x 6144x2048)"},
     }
     if not args.no_extras:
