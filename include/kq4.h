@@ -65,7 +65,10 @@ extern "C" {
  * same in all of them). AUTO is the reference's dispatch (q4x4_gemm_batched
  * vllm_safetensors.c:4593-4631): n_batch <= 3 -> CTILE; n_batch > 3 -> ASM on the first
  * n_batch & ~3 tokens and CTILE on the rest.
- * The prefill GEMM (n_batch > 8) replays the selected chain per output bit for bit. The decode
+ * The prefill GEMM (n_batch > 8) replays the selected chain per output bit for bit, except where
+ * the planner splits K (launches with fewer 128x128 tiles than CUs and K >= 256 blocks; option
+ * gemm_split): each K slice then runs the chain from zero and the slices' outputs are added in
+ * slice order, within 1e-5 of the single chain. The decode
  * GEMV (n_batch <= 8, and the 1..3-token AUTO tail) takes from the chain only its activation
  * scale (f16-rounded for ASM tokens, f32 otherwise): it splits K over waves and sums each
  * wave's terms in block order (one token: a lo and a hi chain per half block, as CTILE; two or
@@ -109,7 +112,9 @@ const char *kq4_version(void);
  * gemv_wpcu, gemv_maxw, gemv_fq (0 / 1: activations quantized by a separate launch / in the
  * GEMV), gemv_fq_work, gemv_silu_fq_work, gemm_kind (0: the prefill GEMM on int8 MFMA, the
  * default; 1: on fp8 operands; the same outputs), gemm_tile (0: the planner's choice; 1 / 2 / 3 /
- * 4: 128x128 / 64x128 / 64x64 / 128x64 token x row tiles; the same outputs). The initial value
+ * 4: 128x128 / 64x128 / 64x64 / 128x64 token x row tiles; the same outputs), gemm_split (K slices
+ * of the int8 GEMM: 0 or 1 none, every output the single chain bit for bit; 2..4 that many;
+ * -1 the planner's choice, the default). The initial value
  * of each comes from the environment variable KQ4_ + its upper-case name, else the built-in
  * default (for most, the planner's own choice); value < 0 restores that initial value. Takes
  * effect for launches planned after it returns. */
@@ -176,9 +181,11 @@ int kq4_moe_ffn(float *Y, const float *X, const int *sel, const float *pr, int T
 /* Workspace bytes the device-pointer matmuls (kq4_matmul_dev, _multi_dev, _silu_dev,
  * kq4_rmsnorm_matmul_multi_dev and the q8 twins) need for n_batch tokens of cols columns, and
  * the MoE calls (kq4_moe_ffn_dev, kq4_moe_ffn_stages_dev, kq4_moe_layer_dev) for T tokens; 0 for
- * a bad shape. The workspace is shared: reserve the largest any call will need. No counterpart
- * in the reference (its scratch grows inside the op, xq_scratch_ensure
- * vllm_safetensors.c:4670-4695); for callers that capture HIP graphs. */
+ * a bad shape. The workspace is shared: reserve the largest any call will need. Beyond 8 tokens
+ * the matmul figure includes up to 24 MiB for the partial sums of a K-split GEMM (the planner's
+ * splits never need more; a split forced through gemm_split may). No counterpart in the
+ * reference (its scratch grows inside the op, xq_scratch_ensure vllm_safetensors.c:4670-4695);
+ * for callers that capture HIP graphs. */
 size_t kq4_matmul_workspace_bytes(int n_batch, int cols);
 size_t kq4_moe_workspace_bytes(int T, int tk, int ne, int d, int ef);
 /* Grows the current device's workspace to at least `bytes` now (not while the calling thread's
@@ -241,7 +248,8 @@ int kq4_matmul_dev(float *out, const float *x, const float *residual, const uint
  * to a fixed per-device scratch array of KQ4_NOALLOC_SCRATCH_BYTES (held by each GPU the library
  * runs on until the process ends) instead of the growable workspace. Beyond 8 tokens the
  * prefill GEMM's operands, n_batch * cols * 17/8 bytes (rounded up to 256-byte pieces), must
- * fit in it (2048 x 12288 does), else KQ4_EINVAL. Every call on a GPU
+ * fit in it (2048 x 12288 does; the int8 operands and the planner's K-split partial sums then
+ * fit too), else KQ4_EINVAL. Every call on a GPU
  * shares that GPU's scratch: calls that overlap on one GPU (other streams or threads) race. */
 #define KQ4_NOALLOC_SCRATCH_BYTES (64u << 20)
 int kq4_matmul_noalloc_dev(float *out, const float *x, const float *residual, const uint8_t *w,
