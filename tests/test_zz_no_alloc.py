@@ -67,7 +67,8 @@ def test_noalloc_largest_fits_and_beyond_is_refused(kq4, torch_dev):
 
 
 def test_noalloc_under_graph_capture(kq4, torch_dev):
-    """2048 tokens x 15392 columns on fp8 operands: 64 MiB less 128 KiB of scratch. torch
+    """2048 tokens x 15392 columns, first on int8 operands with the K-split partial sums in the
+    scratch, then on fp8 operands: 64 MiB less 128 KiB of scratch. torch
     captures in the global mode, in which HIP refuses a hipMalloc from any thread and the
     capture fails, so a capture that succeeds and replays shows that the call allocated
     nothing. The graph is replayed three times, with eager calls of other shapes in between that
@@ -80,6 +81,22 @@ def test_noalloc_under_graph_capture(kq4, torch_dev):
     x = to_dev(torch, synth.make_activations(n, cols, 52))
     res = to_dev(torch, synth.make_activations(n, rows, 53))
     got = torch.full((n, rows), float("nan"), dtype=torch.float32, device="cuda")
+    # the int8 form: 35.5 MB of operands and the K-split partial sums (16 tiles, 4 slices)
+    g8 = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g8):
+        kq4.matmul_noalloc_dev(got, x, w, rows, cols, residual=res,
+                               stream=torch.cuda.current_stream())
+    want8 = torch.empty_like(got)
+    kq4.matmul_dev(want8, x, w, rows, cols, residual=res)
+    torch.cuda.synchronize()
+    for rep in range(2):
+        got.fill_(float("nan"))
+        a, b = run_both(kq4, torch, 256, 4096, 96 + 32 * rep, 70 + rep, residual=True)
+        assert np.array_equal(bits(a), bits(b))
+        g8.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(bits(got), bits(want8)), rep
+    del g8
     with kq4.options(gemm_kind=1):
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
