@@ -178,7 +178,7 @@ int env_int(const char *name, int dflt) {
 // choice where a planner chooses.
 enum OptId {
   kGemvKind, kGemvMfmaFrom, kGemvHs, kGemvRps, kGemvWaves, kGemvWpcu, kGemvMaxw,
-  kGemvFq, kGemvFqWork, kGemvSiluFqWork, kGemmKind, kGemmTile, kGemmSplit, kOptCount
+  kGemvFq, kGemvFqWork, kGemvSiluFqWork, kGemmKind, kGemmTile, kGemmSplit, kGemmPrio, kOptCount
 };
 struct OptDef {
   const char *name, *env;
@@ -192,7 +192,7 @@ const OptDef kOpts[kOptCount] = {
     {"gemv_fq", "KQ4_GEMV_FQ", -1},              {"gemv_fq_work", "KQ4_GEMV_FQ_WORK", 45000},
     {"gemv_silu_fq_work", "KQ4_GEMV_SILU_FQ_WORK", 15000},
     {"gemm_kind", "KQ4_GEMM_KIND", -1},          {"gemm_tile", "KQ4_GEMM_TILE", 0},
-    {"gemm_split", "KQ4_GEMM_SPLIT", -1},
+    {"gemm_split", "KQ4_GEMM_SPLIT", -1},        {"gemm_prio", "KQ4_GEMM_PRIO", -1},
 };
 std::atomic<int> g_opt[kOptCount];
 int g_opt_init[kOptCount];   // each option's value at load: its environment variable or default
@@ -413,7 +413,7 @@ int matmul_impl(int n_mats, float *const *out, const float *const *res, const ui
     for (int i = 0; i < n_mats; ++i)
       KQ4_HIP((hipError_t)kq4_launch_gemm(out[i], res ? res[i] : nullptr, w[i], act, rows[i],
                                           cols, n, qc, ds->ncu, s, 1, opt(kGemmTile), ksp[i],
-                                          part));
+                                          part, opt(kGemmPrio)));
     return KQ4_OK;
   }
 
@@ -474,7 +474,7 @@ int matmul_impl(int n_mats, float *const *out, const float *const *res, const ui
   for (int i = 0; i < n_mats; ++i)
     KQ4_HIP((hipError_t)kq4_launch_gemm(out[i], res ? res[i] : nullptr, w[i], act, rows[i], cols,
                                         main_n, main_chain, ds->ncu, s, 0, opt(kGemmTile), ksp[i],
-                                        part));
+                                        part, opt(kGemmPrio)));
   if (tail) {
     float *o2[KQ4_MAX_MATS];
     const float *r2[KQ4_MAX_MATS];

@@ -43,6 +43,23 @@ typedef float kq4_v32f __attribute__((ext_vector_type(32)));
 // row = 8*(v/4) + 4*(lane/32) + v%4 (token).
 KQ4_DEV int kq4_mfma_tok(int v, int half) { return 8 * (v >> 2) + 4 * half + (v & 3); }
 
+// Issue priority by progress through K (q8 = eighths done). Two workgroups share each CU and
+// each SIMD's arbiter issues from the oldest wave first, so without this the CU's first
+// workgroup runs at nearly its lone speed, its partner gets the gaps (about half its speed), and
+// once the first ends the partner finishes alone at ~0.7 of the pair's throughput (Qwen3-8B
+// down, M = 2048: half the workgroups end at ~235 us, the rest at ~330 us). Lowering a
+// workgroup's priority as it passes 1/2, 3/4 and 7/8 of K hands the issue slots to a partner
+// that is behind, so the two end closer together (graph replays, Qwen3-8B: down M = 512, split
+// into 512 workgroups, 104 -> 98.5 us; down M = 2048, 512 workgroups, 330 -> 322 us; gate
+// M = 2048, three rounds, 291 -> 286 us). Results do not depend on it. The launcher turns it on
+// only for whole rounds.
+KQ4_DEV void kq4_prio_by_progress(int q8) {
+  if (q8 < 4) __builtin_amdgcn_s_setprio(3);
+  else if (q8 < 6) __builtin_amdgcn_s_setprio(2);
+  else if (q8 < 7) __builtin_amdgcn_s_setprio(1);
+  else __builtin_amdgcn_s_setprio(0);
+}
+
 // TM / TN = MFMA token / row tiles per wave: a workgroup covers BM = 64*TM tokens x BN = 64*TN
 // rows (128 x 128, or smaller when the launch would otherwise have fewer than two tiles per CU).
 // Split K (ksplit > 1): the launch covers ksplit K slices of ks blocks (a multiple of the
@@ -55,7 +72,7 @@ template <int CHAIN, int TM, int TN, int WF>
 __global__ __launch_bounds__(256, (TM == 2 && TN == 1) ? 3 : 2) void kq4_gemm_kernel(
     float *__restrict__ out, const float *__restrict__ res, const uint8_t *__restrict__ w,
     KQ4GemmAct act, int rows, int n_tok, int nb, int nst, int mtiles, int ntiles,
-    uint32_t wbytes, int ksplit, int ks, float *__restrict__ part, long pstride) {
+    uint32_t wbytes, int ksplit, int ks, float *__restrict__ part, long pstride, int prio) {
   constexpr int KQ4_GEMM_BM = 64 * TM, KQ4_GEMM_BN = 64 * TN;
   // ROT: the two-token-tile form, software-pipelined (see the compute below). It keeps two
   // stages in LDS at a 32-B row pitch, the two 16-B halves of row r swapped when bit 3 of r is
@@ -453,6 +470,7 @@ __global__ __launch_bounds__(256, (TM == 2 && TN == 1) ? 3 : 2) void kq4_gemm_ke
       __syncthreads();
     };
     for (int b0 = 0; b0 < nb; b0 += 2 * KQ4_GEMM_KB) {
+      if (prio) kq4_prio_by_progress(8 * b0 / nb);
       stage(stg[0], stg[1], b0);
       if (b0 + KQ4_GEMM_KB < nb) stage(stg[1], stg[0], b0 + KQ4_GEMM_KB);
     }
@@ -819,7 +837,7 @@ template <int TM, int TN>
 static hipError_t gemm_launch(float *out, const float *res, const uint8_t *w,
                               const KQ4GemmAct &act, int rows, int n_tok, int nb, int nst,
                               int chain, int wf, uint32_t wbytes, hipStream_t s, int ksplit = 1,
-                              int ks = 0, float *part = nullptr, long pstride = 0) {
+                              int ks = 0, float *part = nullptr, long pstride = 0, int prio = 0) {
   const int mtiles = (n_tok + 64 * TM - 1) / (64 * TM);
   const int ntiles = (rows + 64 * TN - 1) / (64 * TN);
   const dim3 grid((unsigned)(mtiles * ntiles * ksplit));
@@ -827,11 +845,11 @@ static hipError_t gemm_launch(float *out, const float *res, const uint8_t *w,
     if (chain == KQ4_CHAIN_GEMV32)
       hipLaunchKernelGGL((kq4_gemm_kernel<KQ4_CHAIN_GEMV32, TM, TN, 1>), grid, dim3(256), 0, s,
                          out, res, w, act, rows, n_tok, nb, nst, mtiles, ntiles, wbytes, ksplit, ks,
-                         part, pstride);
+                         part, pstride, prio);
     else if (chain == KQ4_CHAIN_Q8GEMM)
       hipLaunchKernelGGL((kq4_gemm_kernel<KQ4_CHAIN_Q8GEMM, TM, TN, 1>), grid, dim3(256), 0, s,
                          out, res, w, act, rows, n_tok, nb, nst, mtiles, ntiles, wbytes, ksplit, ks,
-                         part, pstride);
+                         part, pstride, prio);
     else
       return hipErrorInvalidValue;
   } else if (chain == KQ4_CHAIN_CTILE) {
@@ -839,15 +857,15 @@ static hipError_t gemm_launch(float *out, const float *res, const uint8_t *w,
     else
       hipLaunchKernelGGL((kq4_gemm_kernel<KQ4_CHAIN_CTILE, TM, TN, 0>), grid, dim3(256), 0, s,
                          out, res, w, act, rows, n_tok, nb, nst, mtiles, ntiles, wbytes, ksplit, ks,
-                         part, pstride);
+                         part, pstride, prio);
   } else if (chain == KQ4_CHAIN_GEMV32) {
     hipLaunchKernelGGL((kq4_gemm_kernel<KQ4_CHAIN_GEMV32, TM, TN, 0>), grid, dim3(256), 0, s, out,
                        res, w, act, rows, n_tok, nb, nst, mtiles, ntiles, wbytes, ksplit, ks, part,
-                       pstride);
+                       pstride, prio);
   } else if (chain == KQ4_CHAIN_ASM) {
     hipLaunchKernelGGL((kq4_gemm_kernel<KQ4_CHAIN_ASM, TM, TN, 0>), grid, dim3(256), 0, s, out,
                        res, w, act, rows, n_tok, nb, nst, mtiles, ntiles, wbytes, ksplit, ks, part,
-                       pstride);
+                       pstride, prio);
   } else {
     return hipErrorInvalidValue;
   }
@@ -891,7 +909,7 @@ int kq4_gemm_ksplit(int n_tok, int rows, int cols, int wf, int chain, int ncu, i
 
 int kq4_launch_gemm(float *out, const float *res, const uint8_t *w, const KQ4GemmAct &act,
                     int rows, int cols, int n_tok, int chain, int ncu, hipStream_t s, int wf,
-                    int tile, int ksplit, float *part) {
+                    int tile, int ksplit, float *part, int prio_opt) {
   const int nb = cols / 32;
   const int cb = wf ? KQ8_STREAM_CB : KQ4_STREAM_CB;
   const int nst = (nb + cb - 1) / cb;
@@ -923,10 +941,18 @@ int kq4_launch_gemm(float *out, const float *res, const uint8_t *w, const KQ4Gem
     return (int)hipErrorInvalidValue;
   const uint32_t wbytes = (uint32_t)wb;
   const long ps = (long)n_tok * rows;   // floats per slice output
+  // The progress priority (kq4_prio_by_progress; planner option gemm_prio) for 128 x 128
+  // launches of whole rounds (a multiple of two workgroups per CU), where every CU's last pair
+  // should end together. With a part round left over it costs time: balanced pairs end together
+  // and the rest then runs one workgroup per CU (Qwen3-8B gate, M = 1024: 768 workgroups,
+  // 162 -> 167 us with it).
+  const long wgs = tiles(128, 128) * ksplit;
+  const bool whole = ncu > 0 && wgs % (2L * ncu) == 0;
+  const int prio = pick == 1 && (prio_opt == 1 || (prio_opt < 0 && whole));
   hipError_t e;
   if (pick == 1)
     e = gemm_launch<2, 2>(out, ksplit > 1 ? nullptr : res, w, act, rows, n_tok, nb, nst, chain,
-                          wf, wbytes, s, ksplit, ks, part, ps);
+                          wf, wbytes, s, ksplit, ks, part, ps, prio);
   else if (pick == 2)
     e = gemm_launch<1, 2>(out, ksplit > 1 ? nullptr : res, w, act, rows, n_tok, nb, nst, chain,
                           wf, wbytes, s, ksplit, ks, part, ps);

@@ -102,12 +102,16 @@ struct KQ4GemmAct {
 // slice order by a second launch; part = (ksplit - 1) * n_tok * rows floats of workspace
 // (16-byte aligned) for slices 1 .. ksplit - 1. Within 1e-5 of the single chain, not
 // bit-identical to it.
+// prio: the 128x128 form's issue priority by progress through K (kq4_prio_by_progress): 0 off,
+// 1 on, -1 on for launches of whole rounds (a multiple of two workgroups per CU). Outputs do
+// not depend on it.
 #define KQ4_GEMM_SPLIT_MAX 4
 #define KQ4_SPLIT_PART_MAX (24u << 20)   // partial-sum bytes of the planner's splits, at most
 int kq4_gemm_ksplit(int n_tok, int rows, int cols, int wf, int chain, int ncu, int force);
 int kq4_launch_gemm(float *out, const float *res, const uint8_t *w, const KQ4GemmAct &act,
                     int rows, int cols, int n_tok, int chain, int ncu, hipStream_t stream,
-                    int wf = 0, int tile = 0, int ksplit = 1, float *part = nullptr);
+                    int wf = 0, int tile = 0, int ksplit = 1, float *part = nullptr,
+                    int prio = -1);
 
 // Prefill GEMM on fp8 matrix-core operands (ASM or GEMV32 chain, q4 weights, bit-identical to
 // kq4_launch_gemm): xp = the activations' e4m3 operand pairs [n_tok][cols/32][64] (the

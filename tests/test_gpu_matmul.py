@@ -279,6 +279,38 @@ def test_gemm_split_k(kq4, torch_dev, orc, chain, split):
         assert e <= TOL
 
 
+@pytest.mark.parametrize("split", [1, 2])
+def test_gemm_prio_same_outputs(kq4, torch_dev, orc, split):
+    """The 128 x 128 GEMM's issue priority by progress through K (planner option gemm_prio: 0
+    off, 1 on, -1 the planner's choice) only reorders the SIMDs' issue between workgroups: the
+    outputs of the three settings are bit-identical, on a small launch (the planner leaves it
+    off; checked against the oracle, bit for bit unsplit, within 1e-5 in 2 K slices) and on a
+    whole round of two workgroups per CU (the planner turns it on)."""
+    torch = torch_dev
+    ncu = torch.cuda.get_device_properties(0).multi_processor_count
+    cases = [(301, 384, 4096, True), (256, 128 * ncu, 2048, False)]
+    for n, rows, cols, check in cases:
+        w = synth.make_q4_weights(rows, cols, 1040 + rows)
+        x = synth.make_activations(n, cols, 1041)
+        W, X = wdev(kq4, torch, w, rows, cols), to_dev(torch, x)
+        got = {}
+        for prio in (0, 1, -1):
+            out = torch.empty((n, rows), dtype=torch.float32, device="cuda")
+            with kq4.options(gemm_prio=prio, gemm_split=split, gemm_tile=1):
+                kq4.matmul_dev(out, X, W, rows, cols, chain=kq4.CHAIN_ASM)
+            torch.cuda.synchronize()
+            got[prio] = host(out)
+        for prio in (1, -1):
+            assert np.array_equal(got[prio].view(np.uint32), got[0].view(np.uint32)), (n, rows, prio)
+        if check:
+            want = orc.matmul(w, x, rows, cols, chain=kq4.CHAIN_ASM)
+            e, a = rel_err(got[1], want)
+            print(f"prio split={split} n={n} rows={rows}: rel={e:.3e} maxabs={a:.3e}")
+            if split == 1:
+                assert np.array_equal(got[1].view(np.uint32), want.view(np.uint32))
+            assert e <= TOL
+
+
 @pytest.mark.parametrize("split", [1, 4])
 def test_q8_gemm_split_k(kq4, torch_dev, orc, split):
     """Q8_0 weights (8-block stages): K = 4096 in 4 slices of 32 blocks, within 1e-5 of the
