@@ -37,8 +37,16 @@ static const char *kName[NMIX] = {"mfma", "valu", "indep", "int8", "fp8", "f16"}
 static const double kSum[NMIX] = {128, 256, 384, 768, 640, 640};
 
 template <int MIX>
-__global__ __launch_bounds__(256, 2) void probe(float *out, int iters, float c1, float c2) {
+__global__ __launch_bounds__(256, 2) void probe(float *out, unsigned long long *clk, int iters,
+                                                 float c1, float c2) {
   const int t = threadIdx.x;
+  // shader-clock and 100 MHz real-time counters around the loop (the first wave of each
+  // workgroup), so the cycles per iteration and the clock need no calibration
+  unsigned long long c0 = 0, r0 = 0;
+  if (t == 0) {
+    c0 = __builtin_amdgcn_s_memtime();
+    r0 = __builtin_amdgcn_s_memrealtime();
+  }
   v4i a = {t, 3 * t, 5 * t, 7 * t};
   const v4i b = {t ^ 1, t ^ 2, t ^ 3, t ^ 4};
   v8i a8;
@@ -109,6 +117,12 @@ __global__ __launch_bounds__(256, 2) void probe(float *out, int iters, float c1,
 #pragma unroll
   for (int v = 0; v < 32; ++v) r += sc0[v] + sc1[v];
   out[blockIdx.x * 256 + t] = r;
+  if (t == 0) {
+    const unsigned long long c1t = __builtin_amdgcn_s_memtime();
+    const unsigned long long r1t = __builtin_amdgcn_s_memrealtime();
+    clk[2 * blockIdx.x] = c1t - c0;
+    clk[2 * blockIdx.x + 1] = r1t - r0;
+  }
 }
 
 #define CHECK(x)                                                                   \
@@ -120,16 +134,22 @@ __global__ __launch_bounds__(256, 2) void probe(float *out, int iters, float c1,
     }                                                                              \
   } while (0)
 
+struct Res {
+  float ms;          // per launch, host events
+  double cyc_iter;   // shader cycles per iteration of one wave (median over workgroups)
+  double ghz;        // shader clock (median)
+};
+
 template <int MIX>
-static float run(float *out, int blocks, int iters, int reps) {
+static Res run(float *out, unsigned long long *clk, int blocks, int iters, int reps) {
   hipEvent_t e0, e1;
   CHECK(hipEventCreate(&e0));
   CHECK(hipEventCreate(&e1));
-  hipLaunchKernelGGL(probe<MIX>, dim3(blocks), dim3(256), 0, 0, out, iters, 1.0001f, 0.5f);
+  hipLaunchKernelGGL(probe<MIX>, dim3(blocks), dim3(256), 0, 0, out, clk, iters, 1.0001f, 0.5f);
   CHECK(hipGetLastError());
   CHECK(hipEventRecord(e0));
   for (int r = 0; r < reps; ++r)
-    hipLaunchKernelGGL(probe<MIX>, dim3(blocks), dim3(256), 0, 0, out, iters, 1.0001f, 0.5f);
+    hipLaunchKernelGGL(probe<MIX>, dim3(blocks), dim3(256), 0, 0, out, clk, iters, 1.0001f, 0.5f);
   CHECK(hipGetLastError());
   CHECK(hipEventRecord(e1));
   CHECK(hipEventSynchronize(e1));
@@ -137,7 +157,28 @@ static float run(float *out, int blocks, int iters, int reps) {
   CHECK(hipEventElapsedTime(&ms, e0, e1));
   CHECK(hipEventDestroy(e0));
   CHECK(hipEventDestroy(e1));
-  return ms / reps;
+  // the last launch's per-workgroup counters
+  unsigned long long *h = (unsigned long long *)malloc((size_t)blocks * 2 * sizeof(*h));
+  CHECK(hipMemcpy(h, clk, (size_t)blocks * 2 * sizeof(*h), hipMemcpyDeviceToHost));
+  double *cy = (double *)malloc(blocks * sizeof(double)), *gz = (double *)malloc(blocks * sizeof(double));
+  for (int b = 0; b < blocks; ++b) {
+    cy[b] = (double)h[2 * b] / iters;
+    gz[b] = (double)h[2 * b] / ((double)h[2 * b + 1] * 10.0);   // real-time counter: 100 MHz
+  }
+  auto median = [&](double *v) {
+    for (int i = 1; i < blocks; ++i)
+      for (int j = i; j > 0 && v[j - 1] > v[j]; --j) {
+        const double x = v[j];
+        v[j] = v[j - 1];
+        v[j - 1] = x;
+      }
+    return v[blocks / 2];
+  };
+  Res r{ms / reps, median(cy), median(gz)};
+  free(h);
+  free(cy);
+  free(gz);
+  return r;
 }
 
 int main() {
@@ -145,25 +186,31 @@ int main() {
   CHECK(hipGetDevice(&dev));
   CHECK(hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev));
   const int iters = 4000, reps = 5;
-  printf("CUs %d; cycles per wave and iteration (calibrated: valu = 256); sum = MFMA + VALU cycles\n",
+  printf("CUs %d. Per mix: SIMD cycles per wave and iteration (the shader clock's count over the\n"
+         "loop / iterations / waves per SIMD), the same from host events and the VALU mix's\n"
+         "calibration (256), the clock, and the sum of MFMA and VALU cycles\n",
          ncu);
   for (int w = 1; w <= 2; ++w) {
     const int blocks = ncu * w;   // 4 waves per workgroup, one per SIMD
     float *out = nullptr;
+    unsigned long long *clk = nullptr;
     CHECK(hipMalloc(&out, (size_t)blocks * 256 * sizeof(float)));
-    float ms[NMIX];
-    ms[MFMA] = run<MFMA>(out, blocks, iters, reps);
-    ms[VALU] = run<VALU>(out, blocks, iters, reps);
-    ms[INDEP] = run<INDEP>(out, blocks, iters, reps);
-    ms[INT8] = run<INT8>(out, blocks, iters, reps);
-    ms[FP8] = run<FP8>(out, blocks, iters, reps);
-    ms[F16] = run<F16>(out, blocks, iters, reps);
-    printf("waves/SIMD %d (valu mix %.3f ms -> %.2f GHz)\n", w, ms[VALU],
-           256.0 * w * iters / (ms[VALU] * 1e-3) * 1e-9);
+    CHECK(hipMalloc(&clk, (size_t)blocks * 2 * sizeof(unsigned long long)));
+    Res r[NMIX];
+    r[MFMA] = run<MFMA>(out, clk, blocks, iters, reps);
+    r[VALU] = run<VALU>(out, clk, blocks, iters, reps);
+    r[INDEP] = run<INDEP>(out, clk, blocks, iters, reps);
+    r[INT8] = run<INT8>(out, clk, blocks, iters, reps);
+    r[FP8] = run<FP8>(out, clk, blocks, iters, reps);
+    r[F16] = run<F16>(out, clk, blocks, iters, reps);
+    printf("waves/SIMD %d\n", w);
     for (int m = 0; m < NMIX; ++m)
-      printf("  %-6s %7.1f cycles   sum %5.0f   ratio %.3f\n", kName[m], 256.0 * ms[m] / ms[VALU],
-             kSum[m], 256.0 * ms[m] / ms[VALU] / kSum[m]);
+      printf("  %-6s %7.1f cycles (counter)  %7.1f (events, calibrated)  %.2f GHz   sum %5.0f   "
+             "counter / sum %.3f\n",
+             kName[m], r[m].cyc_iter / w, 256.0 * r[m].ms / r[VALU].ms, r[m].ghz, kSum[m],
+             r[m].cyc_iter / w / kSum[m]);
     CHECK(hipFree(out));
+    CHECK(hipFree(clk));
   }
   return 0;
 }
