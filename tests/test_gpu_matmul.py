@@ -311,6 +311,31 @@ def test_gemm_prio_same_outputs(kq4, torch_dev, orc, split):
             assert e <= TOL
 
 
+def test_q8_gemm_prio_same_outputs(kq4, torch_dev, orc):
+    """The progress priority on the q8 GEMM (Q8_0 weights, the unfused GEMM chain): every
+    gemm_prio setting gives the same bits, on a whole round of two workgroups per CU (the planner
+    turns it on) and on a small launch checked against the oracle."""
+    torch = torch_dev
+    ncu = torch.cuda.get_device_properties(0).multi_processor_count
+    for n, rows, cols, check in [(96, 256, 2048, True), (256, 128 * ncu, 1024, False)]:
+        tiles = synth.make_q8_weights(rows, cols, 1050 + rows)
+        x = synth.make_activations(n, cols, 1051)
+        W = kq4.q8_prepare_dev(tiles, rows, cols)
+        X = to_dev(torch, x)
+        got = {}
+        for prio in (0, 1, -1):
+            out = torch.empty((n, rows), dtype=torch.float32, device="cuda")
+            with kq4.options(gemm_prio=prio, gemm_tile=1):
+                kq4.q8_matmul_dev(out, X, W, rows, cols)
+            torch.cuda.synchronize()
+            got[prio] = host(out)
+        for prio in (1, -1):
+            assert np.array_equal(got[prio].view(np.uint32), got[0].view(np.uint32)), (n, rows, prio)
+        if check:
+            want = orc.q8_matmul(tiles, x, rows, cols)
+            assert np.array_equal(got[1].view(np.uint32), want.view(np.uint32))
+
+
 @pytest.mark.parametrize("split", [1, 4])
 def test_q8_gemm_split_k(kq4, torch_dev, orc, split):
     """Q8_0 weights (8-block stages): K = 4096 in 4 slices of 32 blocks, within 1e-5 of the
