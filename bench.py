@@ -196,11 +196,13 @@ def copy_calibration(mib=512, reps=10):
     return dict(copy_mib=mib, reps=reps)
 
 
-def _time_graph(torch, fn, n, reps=5):
+def _time_graph(torch, fn, n, reps=5, warm_ms=20.0):
     """Average us per call of fn(0..n-1) (one call per rotated weight copy): the n calls are
     captured as one HIP graph and replayed reps times between events on the capture stream, so
     no host launch cost is in the timed region. An eager pass first sizes the library's
-    workspaces and touches every copy."""
+    workspaces and touches every copy; untimed replays for at least warm_ms then let the clock
+    settle under the load (the first milliseconds of a heavy graph after lighter work run up to
+    ~15 % slower)."""
     st = torch.cuda.Stream()
     with torch.cuda.stream(st):
         for i in range(n):
@@ -212,6 +214,12 @@ def _time_graph(torch, fn, n, reps=5):
             fn(i, st)
     g.replay()
     torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(1000):
+        if (time.perf_counter() - t0) * 1e3 >= warm_ms:
+            break
+        g.replay()
+        torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record(st)
     for _ in range(reps):
