@@ -10,9 +10,18 @@
 
 #include <stdlib.h>
 
-// A lane quad per block: each lane reads 8 consecutive floats (two 16-B loads; a wave's load
-// instruction covers 16 blocks = 1 KB), the quad's max takes two DPP quad permutes, and each lane
-// writes its 8 codes as one 8-byte store.
+// A lane quad per (token, block): each lane reads 8 consecutive floats (two 16-B loads), the
+// quad's maximum takes two DPP quad permutes (an integer maximum: amax is non-negative and never
+// NaN), and each lane writes its 8 codes as one 8-byte store. Each x/d is the Markstein-corrected
+// quotient q = RN(x*y), q = RN(q + RN(x - q*d)*y) with y = RN(1/d): two IEEE divisions per lane
+// (d and 1/d) instead of nine. It equals the IEEE quotient for every pair of float32
+// significands (all 2^46, kestrel-llm_amd/probe/kq4_div_probe.hip), hence for all operands here
+// whose residual stays normal; where it would not (|x| < 2^-102, while d >= 1e-10/127), |x/d| is
+// below 2^-61 and both give code 0.
+// Token-major output: a wave's 16 quads take 16 consecutive blocks of a token. Block-major
+// output ([b][m][32]): a wave's 16 quads take 4 tokens x 4 blocks, so each block's 128 B of
+// codes for the 4 tokens is written whole by one store instruction (one quad per block in
+// token-major order would leave each 128-B line to four workgroups, on different XCDs).
 __global__ __launch_bounds__(256) void kq4_quantize_kernel(const float *__restrict__ x,
                                                            const float *__restrict__ up,
                                                            int8_t *__restrict__ xq,
@@ -21,10 +30,20 @@ __global__ __launch_bounds__(256) void kq4_quantize_kernel(const float *__restri
                                                            int cols, int nb, int asm_tokens,
                                                            int block_major) {
   const int qq = threadIdx.x & 3;
-  const long blk = (long)blockIdx.x * (blockDim.x >> 2) + (threadIdx.x >> 2);
-  if (blk >= (long)n_batch * nb) return;  // whole quads exit together
-  const int m = (int)(blk / nb);
-  const int b = (int)(blk - (long)m * nb);
+  const long gq = (long)blockIdx.x * (blockDim.x >> 2) + (threadIdx.x >> 2);
+  int m, b;
+  if (block_major == 1) {
+    const long g = gq >> 4;
+    const int qi = (int)(gq & 15), nbg = (nb + 3) >> 2;
+    m = (int)(g / nbg) * 4 + (qi & 3);
+    b = (int)(g % nbg) * 4 + (qi >> 2);
+    if (m >= n_batch || b >= nb) return;   // whole quads exit together
+  } else {
+    if (gq >= (long)n_batch * nb) return;
+    m = (int)(gq / nb);
+    b = (int)(gq - (long)m * nb);
+  }
+  const long blk = (long)m * nb + b;
   const size_t off = (size_t)m * cols + (size_t)b * 32 + 8 * qq;
   const float4 v0 = *reinterpret_cast<const float4 *>(x + off);
   const float4 v1 = *reinterpret_cast<const float4 *>(x + off + 4);
@@ -39,15 +58,24 @@ __global__ __launch_bounds__(256) void kq4_quantize_kernel(const float *__restri
   float a = 1e-10f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) a = fmaxf(a, fabsf(v[i]));
-  a = kq4_quad_max(a);
+  a = kq4_quad_max_pos(a);
   const float d = a / 127.0f;
-  uint32_t pk[2] = {0, 0};
+  const float y = 1.0f / d;
+  int c[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    int q = (int)(v[i] / d + 0.5f);
-    q = q > 127 ? 127 : (q < -127 ? -127 : q);
-    pk[i >> 2] |= ((uint32_t)q & 0xFFu) << (8 * (i & 3));
+    float q = v[i] * y;
+    const float e = fmaf(-q, d, v[i]);
+    q = fmaf(e, y, q);
+    c[i] = (int)(q + 0.5f);
+    c[i] = c[i] > 127 ? 127 : (c[i] < -127 ? -127 : c[i]);
   }
+  // low bytes of c[0..3], c[4..7] into one dword each: two byte selects and an or
+  uint32_t pk[2];
+#pragma unroll
+  for (int k = 0; k < 2; ++k)
+    pk[k] = __builtin_amdgcn_perm((uint32_t)c[4 * k + 1], (uint32_t)c[4 * k], 0x0c0c0400u) |
+            __builtin_amdgcn_perm((uint32_t)c[4 * k + 3], (uint32_t)c[4 * k + 2], 0x04000c0cu);
   // token-major [m][cols] / [m][nb], block-major [b][m][32] / [b][m], or (block_major = 2) the
   // fp8 GEMM's operand pairs [m][nb][64]: the e4m3 bytes of 16*(q >> 4) for the block's 32
   // elements, then those of q & 15 (kq4_e4m3_hi / _lo), scales token-major
@@ -79,7 +107,9 @@ int kq4_launch_quantize(const float *x, int8_t *xq, float *xd, float *xde, int n
   const long nblk = (long)n_batch * nb;
   if (nblk <= 0) return 0;
   const int per_wg = 256 / 4;
-  const long grid = (nblk + per_wg - 1) / per_wg;
+  // block-major: whole groups of 4 tokens x 4 blocks
+  const long quads = block_major == 1 ? (long)((n_batch + 3) / 4) * ((nb + 3) / 4) * 16 : nblk;
+  const long grid = (quads + per_wg - 1) / per_wg;
   hipLaunchKernelGGL(kq4_quantize_kernel, dim3((unsigned)grid), dim3(256), 0, stream, x, up, xq, xd,
                      xde, n_batch, cols, nb, asm_tokens, block_major);
   return (int)hipGetLastError();
