@@ -36,6 +36,7 @@
 #define KQ4_MOE_PCD 8       // down pairs per pass: token rows 4*(lane/32)+v, v < 4
 #define KQ4_MOE_QTS 672     // LDS bytes per pair row of a 16-block stage's codes
 #define KQ4_MOE_QTS8 320    // the same for an 8-block half stage
+#define KQ4_MOE_DOWNW_DEFAULT 4   // row sets (waves) per workgroup of kq4_moe_downw_kernel
 
 typedef int kq4_v4i __attribute__((ext_vector_type(4)));
 typedef int kq4_v16i __attribute__((ext_vector_type(16)));
@@ -908,6 +909,99 @@ __global__ __launch_bounds__(1024) void kq4_moe_down_kernel(
   }
 }
 
+// ---- down projection, one wave per (expert slot, row set) -------------------------------------
+// For bands of whole 8-block half stages (cbe % 8 == 0, up to 32 blocks; Qwen3-30B-A3B: 24
+// blocks, 3 half stages) from two tokens on. A wave holds its row set's whole band: NH half
+// stages of 4 stream units and 8 scales each, loaded at the start. Each output's chain over the
+// band runs in the lane's registers in block order: acc = fl(acc + fl(fl(sc*xd)*S)), the V4
+// chain. No LDS hand-off and no barrier between waves is needed. A workgroup's W waves take W
+// consecutive row sets of one expert. They share the staging of each pass's av codes and scales
+// (one barrier per pass). kq4_moe_down_kernel instead spreads the band's half stages over NH
+// waves of one workgroup and passes the chain between them through LDS; here a CU holds NH
+// times as many (expert, row set) items.
+template <int NH>
+__global__ __launch_bounds__(256) void kq4_moe_downw_kernel(
+    const uint8_t *__restrict__ D, const int8_t *__restrict__ avq, const float *__restrict__ avd,
+    const int *__restrict__ rec, const int *__restrict__ ex_pair, float *__restrict__ P, int ne,
+    int d) {
+  extern __shared__ __align__(16) uint8_t kq4_moe_lds[];
+  constexpr int PC = KQ4_MOE_PCD, VT = PC / 2, CBE = 8 * NH, QTS = (CBE / 2) * 80;
+  const int W = blockDim.x >> 6;
+  const int nrs = d / 32, ngrp = (nrs + W - 1) / W;
+  const int slot = blockIdx.x / ngrp, grp = blockIdx.x - slot * ngrp;
+  const KQ4MoeSlot<PC> sr = kq4_moe_slot<PC>(rec, slot);
+  const int e = sr.r[0];
+  if (e < 0) return;   // uniform over the workgroup
+  const int cnt = sr.r[2];
+  auto pair = [&](int j) { return kq4_moe_pair<PC>(sr, ex_pair, j); };
+  const int nstD = (ne * CBE + 15) / 16;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int rs = grp * W + wave;
+  const bool live = rs < nrs;
+  const int h = lane >> 5, r = lane & 31;
+  uint8_t *codes = kq4_moe_lds;                                     // [PC][QTS]
+  float *sxb = reinterpret_cast<float *>(kq4_moe_lds + PC * QTS);   // [CBE][PC]
+  // the band's half stages e*NH .. e*NH + NH - 1 of row set rs
+  KQ4MoeW<4, 1> wt[NH];
+  if (live) {
+#pragma unroll
+    for (int k = 0; k < NH; ++k) {
+      const int hq = e * NH + k;
+      kq4_moe_wload<4, 1>(wt[k], D + ((size_t)rs * nstD + (hq >> 1)) * KQ4_STREAM_CHUNK, lane,
+                          4 * (hq & 1), hq & 1);
+    }
+  }
+  const int pr = r < 8 ? r : 0;   // A row -> pair (rows 0..7 hold pairs 0..7)
+  for (int c0 = 0; c0 < cnt; c0 += PC) {
+    const int np = cnt - c0 < PC ? cnt - c0 : PC;
+    if (c0) __syncthreads();   // every wave is done with the previous pass's codes
+    for (int i = threadIdx.x; i < PC * CBE * 2; i += blockDim.x) {
+      const int p = i / (2 * CBE), rem = i - p * 2 * CBE, cb = rem >> 1, hh = rem & 1;
+      uint4 v = make_uint4(0, 0, 0, 0);
+      if (p < np)
+        v = *reinterpret_cast<const uint4 *>(avq + (size_t)pair(c0 + p) * (32 * CBE) +
+                                             (size_t)cb * 32 + 16 * hh);
+      *reinterpret_cast<uint4 *>(codes + p * QTS + kq4_moe_qpos(cb) + 16 * hh) = v;
+    }
+    for (int i = threadIdx.x; i < PC * CBE; i += blockDim.x) {
+      const int cb = i / PC, p = i - cb * PC;
+      sxb[i] = p < np ? avd[(size_t)pair(c0 + p) * CBE + cb] : 0.0f;
+    }
+    __syncthreads();
+    if (!live) continue;
+    float acc[VT];
+#pragma unroll
+    for (int v = 0; v < VT; ++v) acc[v] = 0.0f;
+#pragma unroll
+    for (int k = 0; k < NH; ++k) {
+      kq4_moe_touch(wt[k].n);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int cb = 8 * k + j;
+        uint32_t o[4];
+        kq4_unpack_half(wt[k].n[2 * j], wt[k].n[2 * j + 1], o);
+        const kq4_v4i B = {(int)o[0], (int)o[1], (int)o[2], (int)o[3]};
+        const kq4_v4i A =
+            *reinterpret_cast<const kq4_v4i *>(codes + pr * QTS + kq4_moe_qpos(cb) + 16 * h);
+        const kq4_v16i C = kq4_moe_mfma(A, B);
+        // C = 16*S: fl(fl((sc/16)*xd) * 16S) = fl(fl(sc*xd) * S), every step scaled by a power
+        // of two far from underflow (sc >= 2^-24, xd >= 1e-10/127)
+        const float sc = kq4_h2f(wt[k].sc[j >> 1] >> (16 * (j & 1))) * 0.0625f;
+        const float *xs = sxb + cb * PC + VT * h;
+#pragma unroll
+        for (int v = 0; v < VT; ++v) {
+          acc[v] = acc[v] + (sc * xs[v]) * (float)C[v];
+          kq4_moe_pin(acc[v]);
+        }
+      }
+    }
+#pragma unroll
+    for (int v = 0; v < VT; ++v)
+      if (VT * h + v < np) P[(size_t)pair(c0 + VT * h + v) * d + (size_t)rs * 32 + r] = acc[v];
+  }
+}
+
 // ---- one token: down projection and combine in one launch ------------------------------------
 // A workgroup takes 8 rows of Y (a quarter row set) and every rank: wave w handles ranks w,
 // w + nw, .., so the combine's rank order is within the workgroup and needs no cross-workgroup
@@ -1101,6 +1195,31 @@ int kq4_launch_moe_dbg(float *Y, const float *X, const int *sel, const float *pr
       default: hipLaunchKernelGGL(kq4_moe_down1_kernel<4>, grid, block, lds, s, Y, D, ws.avq,
                                   ws.avd, sel, pr, tk, ne, d, ef); break;
     }
+    return (int)hipGetLastError();
+  }
+  // bands of whole half stages, two tokens on: one wave per (slot, row set), W row sets per
+  // workgroup (KQ4_MOE_DOWNW: W; 0 = the kernel below)
+  static const int downw = [] {
+    const char *v = getenv("KQ4_MOE_DOWNW");
+    return v ? atoi(v) : KQ4_MOE_DOWNW_DEFAULT;
+  }();
+  if (!t1 && cbe % 8 == 0 && cbe <= 32 && downw >= 1 && downw <= 4) {
+    const int W = downw, nrs = d / 32, ngrp = (nrs + W - 1) / W;
+    const size_t lds = (size_t)KQ4_MOE_PCD * ((cbe / 2) * 80) + (size_t)cbe * KQ4_MOE_PCD * 4;
+    const dim3 grid((unsigned)(slots * ngrp)), block(64 * W);
+    switch (cbe / 8) {
+      case 1: hipLaunchKernelGGL(kq4_moe_downw_kernel<1>, grid, block, lds, s, D, ws.avq, ws.avd,
+                                 ws.rec, ws.ex_pair, ws.P, ne, d); break;
+      case 2: hipLaunchKernelGGL(kq4_moe_downw_kernel<2>, grid, block, lds, s, D, ws.avq, ws.avd,
+                                 ws.rec, ws.ex_pair, ws.P, ne, d); break;
+      case 3: hipLaunchKernelGGL(kq4_moe_downw_kernel<3>, grid, block, lds, s, D, ws.avq, ws.avd,
+                                 ws.rec, ws.ex_pair, ws.P, ne, d); break;
+      default: hipLaunchKernelGGL(kq4_moe_downw_kernel<4>, grid, block, lds, s, D, ws.avq,
+                                  ws.avd, ws.rec, ws.ex_pair, ws.P, ne, d); break;
+    }
+    const long n = (long)T * d;
+    hipLaunchKernelGGL(kq4_moe_combine_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                       s, Y, ws.P, sel, pr, T, tk, d, ne);
     return (int)hipGetLastError();
   }
   // half stages a band can meet (the most over the experts), and row sets per workgroup

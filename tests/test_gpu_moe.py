@@ -36,7 +36,11 @@ SHAPES = {"small": dict(hidden=256, experts=16, top_k=4, ef=64),
           "wide": dict(hidden=4096, experts=12, top_k=3, ef=96),
           # top-16 and 32-block bands: the one-token down + combine kernel at its limits
           # (16 waves, four band lines per lane)
-          "k16": dict(hidden=512, experts=32, top_k=16, ef=1024)}
+          "k16": dict(hidden=512, experts=32, top_k=16, ef=1024),
+          # bands of one and two 8-block half stages (the one-wave-per-row-set down kernel's
+          # other instantiations; Qwen3-30B-A3B has three, k16 four)
+          "nh1": dict(hidden=512, experts=32, top_k=8, ef=256),
+          "nh2": dict(hidden=1024, experts=16, top_k=4, ef=512)}
 
 
 def test_route(kq4, torch_dev, orc):
@@ -80,7 +84,7 @@ def test_route_edge_cases(kq4, torch_dev, orc, ne, tk):
 
 
 @pytest.mark.parametrize("T", [1, 7, 64])
-@pytest.mark.parametrize("shape", ["small", "qwen3_30b_a3b", "wide", "k16"])
+@pytest.mark.parametrize("shape", ["small", "qwen3_30b_a3b", "wide", "k16", "nh1", "nh2"])
 def test_moe_stages(kq4, torch_dev, orc, shape, T):
     torch = torch_dev
     cfg = SHAPES[shape]
