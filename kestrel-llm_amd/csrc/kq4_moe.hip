@@ -918,14 +918,16 @@ __global__ __launch_bounds__(1024) void kq4_moe_down_kernel(
 // consecutive row sets of one expert. They share the staging of each pass's av codes and scales
 // (one barrier per pass). kq4_moe_down_kernel instead spreads the band's half stages over NH
 // waves of one workgroup and passes the chain between them through LDS; here a CU holds NH
-// times as many (expert, row set) items.
-template <int NH>
+// times as many (expert, row set) items. PC: pairs per pass, 8 (4 per wave half) or 4 (2 per
+// half, half the epilogue's VALU work; chosen when the launch averages at most 4 pairs per
+// expert, the band's weights staying in registers across the passes).
+template <int NH, int PC>
 __global__ __launch_bounds__(256) void kq4_moe_downw_kernel(
     const uint8_t *__restrict__ D, const int8_t *__restrict__ avq, const float *__restrict__ avd,
     const int *__restrict__ rec, const int *__restrict__ ex_pair, float *__restrict__ P, int ne,
     int d) {
   extern __shared__ __align__(16) uint8_t kq4_moe_lds[];
-  constexpr int PC = KQ4_MOE_PCD, VT = PC / 2, CBE = 8 * NH, QTS = (CBE / 2) * 80;
+  constexpr int VT = PC / 2, CBE = 8 * NH, QTS = (CBE / 2) * 80;
   const int W = blockDim.x >> 6;
   const int nrs = d / 32, ngrp = (nrs + W - 1) / W;
   const int slot = blockIdx.x / ngrp, grp = blockIdx.x - slot * ngrp;
@@ -952,7 +954,7 @@ __global__ __launch_bounds__(256) void kq4_moe_downw_kernel(
                           4 * (hq & 1), hq & 1);
     }
   }
-  const int pr = r < 8 ? r : 0;   // A row -> pair (rows 0..7 hold pairs 0..7)
+  const int pr = (r < 8 && (r & 3) < VT) ? VT * (r >> 2) + (r & 3) : 0;   // A row 4i+v: pair VT*i+v
   for (int c0 = 0; c0 < cnt; c0 += PC) {
     const int np = cnt - c0 < PC ? cnt - c0 : PC;
     if (c0) __syncthreads();   // every wave is done with the previous pass's codes
@@ -1205,18 +1207,33 @@ int kq4_launch_moe_dbg(float *Y, const float *X, const int *sel, const float *pr
   }();
   if (!t1 && cbe % 8 == 0 && cbe <= 32 && downw >= 1 && downw <= 4) {
     const int W = downw, nrs = d / 32, ngrp = (nrs + W - 1) / W;
-    const size_t lds = (size_t)KQ4_MOE_PCD * ((cbe / 2) * 80) + (size_t)cbe * KQ4_MOE_PCD * 4;
+    // 4 pairs per pass when the pairs average at most 4 per expert slot (Qwen3-30B-A3B: T = 8
+    // and 64; 8 from T = 256 on, where the extra passes' staging costs more than the smaller
+    // epilogue saves); KQ4_MOE_DOWNW_PC = 4 / 8 forces one (for measurement)
+    static const int pc_force = [] {
+      const char *v = getenv("KQ4_MOE_DOWNW_PC");
+      return v ? atoi(v) : 0;
+    }();
+    const int pc = pc_force == 4 || pc_force == 8 ? pc_force : (n_pairs <= 4 * slots ? 4 : 8);
+    const size_t lds = (size_t)pc * ((cbe / 2) * 80) + (size_t)cbe * pc * 4;
     const dim3 grid((unsigned)(slots * ngrp)), block(64 * W);
-    switch (cbe / 8) {
-      case 1: hipLaunchKernelGGL(kq4_moe_downw_kernel<1>, grid, block, lds, s, D, ws.avq, ws.avd,
-                                 ws.rec, ws.ex_pair, ws.P, ne, d); break;
-      case 2: hipLaunchKernelGGL(kq4_moe_downw_kernel<2>, grid, block, lds, s, D, ws.avq, ws.avd,
-                                 ws.rec, ws.ex_pair, ws.P, ne, d); break;
-      case 3: hipLaunchKernelGGL(kq4_moe_downw_kernel<3>, grid, block, lds, s, D, ws.avq, ws.avd,
-                                 ws.rec, ws.ex_pair, ws.P, ne, d); break;
-      default: hipLaunchKernelGGL(kq4_moe_downw_kernel<4>, grid, block, lds, s, D, ws.avq,
-                                  ws.avd, ws.rec, ws.ex_pair, ws.P, ne, d); break;
+#define KQ4_DOWNW(NH, PC)                                                                       \
+  {                                                                                             \
+    auto kern = kq4_moe_downw_kernel<NH, PC>;                                                   \
+    hipLaunchKernelGGL(kern, grid, block, lds, s, D, ws.avq, ws.avd, ws.rec, ws.ex_pair, ws.P,  \
+                       ne, d);                                                                  \
+  }
+    switch (cbe / 8 * 16 + pc) {
+      case 1 * 16 + 4: KQ4_DOWNW(1, 4); break;
+      case 1 * 16 + 8: KQ4_DOWNW(1, 8); break;
+      case 2 * 16 + 4: KQ4_DOWNW(2, 4); break;
+      case 2 * 16 + 8: KQ4_DOWNW(2, 8); break;
+      case 3 * 16 + 4: KQ4_DOWNW(3, 4); break;
+      case 3 * 16 + 8: KQ4_DOWNW(3, 8); break;
+      case 4 * 16 + 4: KQ4_DOWNW(4, 4); break;
+      default: KQ4_DOWNW(4, 8); break;
     }
+#undef KQ4_DOWNW
     const long n = (long)T * d;
     hipLaunchKernelGGL(kq4_moe_combine_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
                        s, Y, ws.P, sel, pr, T, tk, d, ne);
