@@ -40,7 +40,10 @@ SHAPES = {"small": dict(hidden=256, experts=16, top_k=4, ef=64),
           # bands of one and two 8-block half stages (the one-wave-per-row-set down kernel's
           # other instantiations; Qwen3-30B-A3B has three, k16 four)
           "nh1": dict(hidden=512, experts=32, top_k=8, ef=256),
-          "nh2": dict(hidden=1024, experts=16, top_k=4, ef=512)}
+          "nh2": dict(hidden=1024, experts=16, top_k=4, ef=512),
+          # Qwen3-30B-A3B's 24-block bands with many pairs per expert: the down kernel's
+          # 8-pair passes (the launch averages more than 4 pairs per expert slot at T = 64)
+          "nh3_dense": dict(hidden=512, experts=8, top_k=4, ef=768)}
 
 
 def test_route(kq4, torch_dev, orc):
@@ -84,7 +87,8 @@ def test_route_edge_cases(kq4, torch_dev, orc, ne, tk):
 
 
 @pytest.mark.parametrize("T", [1, 7, 64])
-@pytest.mark.parametrize("shape", ["small", "qwen3_30b_a3b", "wide", "k16", "nh1", "nh2"])
+@pytest.mark.parametrize("shape", ["small", "qwen3_30b_a3b", "wide", "k16", "nh1", "nh2",
+                                   "nh3_dense"])
 def test_moe_stages(kq4, torch_dev, orc, shape, T):
     torch = torch_dev
     cfg = SHAPES[shape]
