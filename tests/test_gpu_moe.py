@@ -90,12 +90,16 @@ def test_route_edge_cases(kq4, torch_dev, orc, ne, tk):
 @pytest.mark.parametrize("shape", ["small", "qwen3_30b_a3b", "wide", "k16", "nh1", "nh2",
                                    "nh3_dense"])
 def test_moe_stages(kq4, torch_dev, orc, shape, T):
-    torch = torch_dev
-    cfg = SHAPES[shape]
+    check_stages(kq4, torch_dev, orc, SHAPES[shape], T, 40 + T, shape)
+
+
+def check_stages(kq4, torch, orc, cfg, T, seed, name):
+    """Stage by stage against the oracle: gate and up bit-exact, av within 4 ulp, Y within 1e-5;
+    the down stage fed the oracle's av bit-exact; the FFN without stage outputs the same bits."""
     d, ne, tk, ef = cfg["hidden"], cfg["experts"], cfg["top_k"], cfg["ef"]
-    G, U, D = synth.make_moe(cfg, 40 + T)
-    X = synth.make_activations(T, d, 50 + T)
-    sel, pr = orc.moe_route(synth.make_logits(T, ne, 60 + T), tk)
+    G, U, D = synth.make_moe(cfg, seed)
+    X = synth.make_activations(T, d, seed + 10)
+    sel, pr = orc.moe_route(synth.make_logits(T, ne, seed + 20), tk)
     Y_o, st = orc.moe_ffn(X, sel, pr, G, U, D, ne, d, ef, stages=True)
 
     dG, dU = (kq4.prepare_dev(to_dev(torch, a), ne * ef, d) for a in (G, U))
@@ -113,7 +117,7 @@ def test_moe_stages(kq4, torch_dev, orc, shape, T):
     # fl(g / fl(1 + e)) * u by a few ulp
     assert ulps(host(av), st["av"]) <= 4
     r, a = rel_err(host(Y), Y_o)
-    print(f"moe {shape} T={T}: Y rel={r:.3e} maxabs={a:.3e} "
+    print(f"moe {name} T={T}: Y rel={r:.3e} maxabs={a:.3e} "
           f"bit-exact={np.array_equal(host(Y), Y_o)}")
     assert r <= 1e-5
 
@@ -128,6 +132,20 @@ def test_moe_stages(kq4, torch_dev, orc, shape, T):
     kq4.moe_ffn_dev(Y3, dX, dsel, dpr, dG, dU, dD, ne, d, ef)
     torch.cuda.synchronize()
     assert np.array_equal(host(Y3).view(np.uint32), host(Y).view(np.uint32))
+
+
+# Seeded random shapes: hidden a multiple of 32 up to 1024 (partial stream stages), expert width
+# a multiple of 32 up to 1024 (bands of any block count: both down kernels, odd bands, the
+# one-token down + combine and its fallback), 2-40 experts, top-k up to min(16, experts), 1-40
+# tokens.
+@pytest.mark.parametrize("i", range(12))
+def test_moe_random_shapes(kq4, torch_dev, orc, i):
+    rng = np.random.default_rng(8000 + i)
+    ne = int(rng.integers(2, 41))
+    cfg = dict(hidden=32 * int(rng.integers(1, 33)), experts=ne,
+               top_k=int(rng.integers(1, min(16, ne) + 1)), ef=32 * int(rng.integers(1, 33)))
+    T = 1 if i % 4 == 0 else int(rng.integers(2, 41))
+    check_stages(kq4, torch_dev, orc, cfg, T, 8100 + 30 * i, f"random {i} {cfg}")
 
 
 @pytest.mark.parametrize("shape", ["small", "qwen3_30b_a3b"])
