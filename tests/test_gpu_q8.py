@@ -118,3 +118,32 @@ def test_q8_multi_and_host_wrappers(kq4, orc):
     assert rc == 1 and rel_err(out, want)[0] <= TOL
     got1 = kq4.q8_matmul(wd, x[:1], 128, 1024, residual=res[:1], wkey=0x77)
     assert rel_err(got1, orc.q8_matmul(wd, x[:1], 128, 1024, residual=res[:1]))[0] <= TOL
+
+
+# Seeded random shapes: 4x4 or 8x8 tiles, rows a multiple of the tile, K a multiple of 32 up to
+# 3072 (partial 8-block stages), 1-8 tokens (GEMV, within 1e-5) or 9-300 (GEMM, bit-exact; K
+# stays below the planner's split threshold), chains AUTO / VDOT / GEMM, with a residual.
+@pytest.mark.parametrize("i", range(16))
+def test_q8_random_shapes(kq4, torch_dev, orc, i):
+    torch = torch_dev
+    rng = np.random.default_rng(9000 + i)
+    g = 4 if i % 2 else 8
+    rows = g * int(rng.integers(1, 1024 // g + 1))
+    cols = 32 * int(rng.integers(1, 97))
+    n = int(rng.integers(1, 9)) if i % 4 < 2 else int(rng.integers(9, 301))
+    chain = (0, 2, 4)[int(rng.integers(0, 3))]
+    w = q8_tiles_synth(rows, cols, g, 9100 + i)
+    x = synth.make_activations(n, cols, 9200 + i)
+    res = synth.make_activations(n, rows, 9300 + i)
+    want = orc.q8_matmul(w, x, rows, cols, residual=res, chain=chain, g=g)
+    W = kq4.q8_prepare_dev(w, rows, cols, g=g)
+    out = torch.empty((n, rows), dtype=torch.float32, device="cuda")
+    kq4.q8_matmul_dev(out, to_dev(torch, x), W, rows, cols, residual=to_dev(torch, res),
+                      chain=chain)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    rel, mx = rel_err(got, want)
+    print(f"q8 random {i}: g={g} rows={rows} cols={cols} n={n} chain={chain}: rel={rel:.3e}")
+    if n > 8:
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert rel <= TOL, (rel, mx)
