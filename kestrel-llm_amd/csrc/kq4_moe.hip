@@ -499,10 +499,12 @@ KQ4_DEV void kq4_moe_terms(const KQ4MoeW<NU, NS> &w, const uint8_t *slab, int qt
       if (b + 1 < NB) Cn = mf(b + 1, Aq[(b + 1) % 3]);
       // block b+1's MFMA is issued before block b's result is read (two result sets live)
       __builtin_amdgcn_sched_barrier(0);
-      const float sc = kq4_h2f(w.sc[b >> 1] >> (16 * (b & 1)));
+      // C = 16*S: fl(fl((sc/16)*xd) * 16S) = fl(fl(sc*xd) * S), every step scaled by a power of
+      // two far from underflow (sc >= 2^-24, xd >= 1e-10/127)
+      const float sc = kq4_h2f(w.sc[b >> 1] >> (16 * (b & 1))) * 0.0625f;
 #pragma unroll
       for (int v = 0; v < VT; ++v) {
-        t[b][v] = v < VTC ? (sc * xsv[b][v < VTC ? v : 0]) * (float)(C[v] >> 4) : 0.0f;
+        t[b][v] = v < VTC ? (sc * xsv[b][v < VTC ? v : 0]) * (float)C[v] : 0.0f;
         kq4_moe_pin(t[b][v]);
       }
       C = Cn;
@@ -517,11 +519,11 @@ KQ4_DEV void kq4_moe_terms(const KQ4MoeW<NU, NS> &w, const uint8_t *slab, int qt
     const kq4_v4i B = {(int)o[0], (int)o[1], (int)o[2], (int)o[3]};
     const kq4_v4i A = *reinterpret_cast<const kq4_v4i *>(qb + kq4_moe_qpos(b));
     const kq4_v16i C = kq4_moe_mfma(A, B);
-    const float sc = kq4_h2f(w.sc[b >> 1] >> (16 * (b & 1)));
+    const float sc = kq4_h2f(w.sc[b >> 1] >> (16 * (b & 1))) * 0.0625f;   // C = 16*S (as above)
     const float *xs = sx + b * 2 * VT + VT * h;
 #pragma unroll
     for (int v = 0; v < VT; ++v) {
-      t[b][v] = (sc * xs[v]) * (float)(C[v] >> 4);   // C = 16*S exactly
+      t[b][v] = (sc * xs[v]) * (float)C[v];
       kq4_moe_pin(t[b][v]);
     }
     // one block's MFMA in flight at a time: each holds 16 result registers
@@ -854,8 +856,9 @@ __global__ __launch_bounds__(1024) void kq4_moe_down_kernel(
         kq4_v16i Cn = C;
         if (j + 1 < 8) Cn = mf(j + 1, Aq[(j + 1) % 3]);
         __builtin_amdgcn_sched_barrier(0);
-        const float sc = kq4_h2f(wt.sc[j >> 1] >> (16 * (j & 1)));
-        t[j][0] = (sc * xs0[j]) * (float)(C[0] >> 4);   // C = 16*S exactly
+        // C = 16*S: fl(fl((sc/16)*xd) * 16S) = fl(fl(sc*xd) * S), as in kq4_moe_terms
+        const float sc = kq4_h2f(wt.sc[j >> 1] >> (16 * (j & 1))) * 0.0625f;
+        t[j][0] = (sc * xs0[j]) * (float)C[0];
         kq4_moe_pin(t[j][0]);
 #pragma unroll
         for (int v = 1; v < VT; ++v) t[j][v] = 0.0f;
@@ -874,11 +877,11 @@ __global__ __launch_bounds__(1024) void kq4_moe_down_kernel(
         const kq4_v4i A =
             *reinterpret_cast<const kq4_v4i *>(codes + pr * qts + kq4_moe_qpos(cbs) + 16 * h);
         const kq4_v16i C = kq4_moe_mfma(A, B);
-        const float sc = kq4_h2f(wt.sc[j >> 1] >> (16 * (j & 1)));
+        const float sc = kq4_h2f(wt.sc[j >> 1] >> (16 * (j & 1))) * 0.0625f;   // C = 16*S
         const float *xs = sxb + cbs * PC + VT * h;
 #pragma unroll
         for (int v = 0; v < VT; ++v) {
-          t[j][v] = (sc * xs[v]) * (float)(C[v] >> 4);   // C = 16*S exactly
+          t[j][v] = (sc * xs[v]) * (float)C[v];
           kq4_moe_pin(t[j][v]);
         }
         __builtin_amdgcn_sched_barrier(0);
