@@ -914,22 +914,34 @@ int kq4_rmsnorm_matmul_multi_dev(int n_mats, float *const *out, const float *con
   // the normalised activations are quantized where they are formed; the matmul then reads the
   // codes (the same workspace carve matmul_impl makes for its own quantization, so it stays)
   const size_t qbytes = qa_bytes(n_batch, cols);
-  if (n_batch == 1) {
-    // One token: the norm is written in fp32 and the matmul quantizes it in its own kernel (the
-    // same codes), the cheaper GEMV form at one token (measured 0.2-0.3 us per call, Qwen3-8B and
-    // Qwen3-VL-2B QKV). Without a caller buffer the fp32 row sits above the carve matmul_impl
-    // makes for its own quantization, reserved first so that matmul_impl does not reallocate.
+  // Where the GEMV would quantize fp32 activations in its own kernel (gemv_fq: one to a few
+  // tokens), the norm is written in fp32 and the matmul quantizes it there (the same codes):
+  // measured faster than reading the norm kernel's codes (Qwen3-8B QKV, graph replay: M = 1 by
+  // 0.2-0.3 us, M = 2 9.98 -> 9.46 us, M = 4 10.47 -> 10.27 us). Where it would take a separate
+  // quantizer launch instead (Qwen3-8B QKV from 5 tokens on), the norm kernel writes the codes
+  // and saves that launch (M = 8 12.15 -> 10.48 us).
+  bool fp32_path = false;
+  if (n_batch <= KQ4_GEMV_MAX_M) {
+    const GemvPlan pl = plan_gemv(n_mats, rows, (cols / 32 + KQ4_STREAM_CB - 1) / KQ4_STREAM_CB,
+                                  ds->ncu, n_batch);
+    const long per_cu = ((long)pl.groups + ds->ncu - 1) / ds->ncu;
+    fp32_path = gemv_fq(per_cu * n_batch * cols, n_batch, pl.rps, false);
+  }
+  if (fp32_path) {
+    // Without a caller buffer the fp32 rows sit above the carve matmul_impl makes for its own
+    // quantization, reserved first so that matmul_impl does not reallocate.
     float *nx = normed;
     if (!nx) {
-      if ((rc = ensure_ws(Ws{&ds->ws, ds}, qbytes + al256((size_t)cols * sizeof(float)),
+      if ((rc = ensure_ws(Ws{&ds->ws, ds},
+                          qbytes + al256((size_t)n_batch * cols * sizeof(float)),
                           (hipStream_t)stream)))
         return rc;
       nx = reinterpret_cast<float *>(static_cast<char *>(ds->ws.p) + qbytes);
     }
-    KQ4_HIP((hipError_t)kq4_launch_rms_norm(x, norm_w, nx, nullptr, nullptr, 1, cols, eps,
+    KQ4_HIP((hipError_t)kq4_launch_rms_norm(x, norm_w, nx, nullptr, nullptr, n_batch, cols, eps,
                                             order == KQ4_RMS_SERIAL, (hipStream_t)stream));
-    return matmul_impl(n_mats, out, residual, w, rows, cols, nx, nullptr, nullptr, 1, chain,
-                       (hipStream_t)stream);
+    return matmul_impl(n_mats, out, residual, w, rows, cols, nx, nullptr, nullptr, n_batch,
+                       chain, (hipStream_t)stream);
   }
   if ((rc = ensure_ws(Ws{&ds->ws, ds}, qbytes, (hipStream_t)stream))) return rc;
   Carve cv{static_cast<char *>(ds->ws.p)};
