@@ -69,23 +69,25 @@ KQ4_DEV void kq4_prio_by_progress(int q8) {
 // order. A slice is the same kernel on offset pointers: weights + (first block / stage) chunks
 // (the set stride stays nst), activations + first block, with nb the slice's block count.
 template <int CHAIN, int TM, int TN, int WF>
-__global__ __launch_bounds__(256, (TM == 2 && TN == 1) ? 3 : 2) void kq4_gemm_kernel(
+__global__ __launch_bounds__(256, (TM == 2 && TN == 1) || (TM == 1 && TN == 2 && CHAIN != KQ4_CHAIN_CTILE) ? 3 : 2) void kq4_gemm_kernel(
     float *__restrict__ out, const float *__restrict__ res, const uint8_t *__restrict__ w,
     KQ4GemmAct act, int rows, int n_tok, int nb, int nst, int mtiles, int ntiles,
     uint32_t wbytes, int ksplit, int ks, float *__restrict__ part, long pstride, int prio) {
   constexpr int KQ4_GEMM_BM = 64 * TM, KQ4_GEMM_BN = 64 * TN;
-  // ROT: the two-token-tile form, software-pipelined (see the compute below). It keeps two
-  // stages in LDS at a 32-B row pitch, the two 16-B halves of row r swapped when bit 3 of r is
-  // set (so the 16-B fragment reads and the stores stay bank-conflict free without padding):
-  // 2 x 36 KB, two workgroups per CU. The other forms stage once at a 48-B pitch.
-  constexpr bool ROT = CHAIN != KQ4_CHAIN_CTILE && TM == 2;
+  // ROT: the software-pipelined form (128 x 128, 128 x 64, 64 x 128; see the compute below).
+  // It keeps two stages in LDS at a 32-B row pitch, the two 16-B halves of row r swapped when
+  // bit 3 of r is set (so the 16-B fragment reads and the stores stay bank-conflict free
+  // without padding): 2 x 36 KB at 128 x 128 (two workgroups per CU), 2 x 26 KB otherwise
+  // (three). The other forms (64 x 64, and the C-tile chain) stage once at a 48-B pitch.
+  constexpr bool ROT = CHAIN != KQ4_CHAIN_CTILE && (TM == 2 || TN == 2);
   constexpr int SPT = KQ4_GEMM_KB * KQ4_GEMM_BN / 256;   // ROT: row scales per thread (2 or 1)
   constexpr int PITCH = ROT ? 32 : KQ4_LDS_ROW;
   struct Stage {
     int8_t a[KQ4_GEMM_KB][KQ4_GEMM_BM * PITCH];
     int8_t b[KQ4_GEMM_KB][KQ4_GEMM_BN * PITCH];
-    // 128 x 64: the raw f16 row scales (scaled when read), so that three workgroups fit
-    std::conditional_t<ROT && TN == 1, uint16_t, float> w[KQ4_GEMM_KB][KQ4_GEMM_BN];
+    // 128 x 64 and 64 x 128: the raw f16 row scales (scaled when read), so that three
+    // workgroups fit
+    std::conditional_t<ROT && (TN == 1 || TM == 1), uint16_t, float> w[KQ4_GEMM_KB][KQ4_GEMM_BN];
     float x[KQ4_GEMM_KB][KQ4_GEMM_BM];
   };
   __shared__ __align__(16) Stage stg[ROT ? 2 : 1];
@@ -148,7 +150,7 @@ __global__ __launch_bounds__(256, (TM == 2 && TN == 1) ? 3 : 2) void kq4_gemm_ke
   // q8: per stage 4 blocks x BN rows x 2 halves of 16 B, 2*TN loads per thread
   constexpr int NB = WF ? 2 * TN : TN;
   struct Regs {
-    uint4 a[KQ4_GEMM_KB];
+    std::conditional_t<ROT && TM == 1, uint2, uint4> a[KQ4_GEMM_KB];   // 64 tokens: 8 B per thread
     uint4 b[NB];
     uint2 sw;
     float x[KQ4_GEMM_KB * KQ4_GEMM_BM / 256];
@@ -179,7 +181,8 @@ __global__ __launch_bounds__(256, (TM == 2 && TN == 1) ? 3 : 2) void kq4_gemm_ke
   int xbl[KQ4_GEMM_KB * KQ4_GEMM_BM / 256];   // wave-uniform block of the stage per scale load
   if constexpr (WF == 0 || ROT) {
     constexpr int CHUNK = WF ? KQ8_STREAM_CHUNK : KQ4_STREAM_CHUNK;
-    va = (uint32_t)((m0 + (t >> 1)) * act.q_ts + (t & 1) * 16);
+    va = ROT && TM == 1 ? (uint32_t)((m0 + (t >> 2)) * act.q_ts + (t & 3) * 8)
+                        : (uint32_t)((m0 + (t >> 1)) * act.q_ts + (t & 1) * 16);
 #pragma unroll
     for (int u = 0; u < NB; ++u) {
       // q4: (set sl, nibble unit iu = 2 blocks, lane ln); q8: (set sl, block iu, lane ln)
@@ -221,7 +224,10 @@ __global__ __launch_bounds__(256, (TM == 2 && TN == 1) ? 3 : 2) void kq4_gemm_ke
       rg.sw.x = SPT == 2 ? kq4_bload4s(rw, vs, so) : kq4_bload2s(rw, vs, so);
     } else if (p < NB + 1 + KQ4_GEMM_KB) {
       const int u = p - NB - 1;
-      rg.a[u] = kq4_bload16s(ra, va, (uint32_t)(min(b0 + u, nb - 1) * act.q_bs));
+      if constexpr (ROT && TM == 1)
+        rg.a[u] = kq4_bload8s(ra, va, (uint32_t)(min(b0 + u, nb - 1) * act.q_bs));
+      else
+        rg.a[u] = kq4_bload16s(ra, va, (uint32_t)(min(b0 + u, nb - 1) * act.q_bs));
     } else {
       const int u = p - NB - 1 - KQ4_GEMM_KB;
       rg.x[u] = __uint_as_float(
@@ -251,14 +257,23 @@ __global__ __launch_bounds__(256, (TM == 2 && TN == 1) ? 3 : 2) void kq4_gemm_ke
       const int j = SPT * (t / KQ4_GEMM_BN), r = t % KQ4_GEMM_BN;
       if constexpr (TN == 1) {
         S.w[j][r] = (uint16_t)rg.sw.x;
+      } else if constexpr (TM == 1) {   // raw f16 (64 x 128)
+        S.w[j][r] = (uint16_t)rg.sw.x;
+        S.w[j + 1][r] = (uint16_t)(rg.sw.x >> 16);
       } else {
         constexpr float WS = WF ? 1.0f : 0.0625f;
         S.w[j][r] = kq4_h2f(rg.sw.x) * WS;
         S.w[j + 1][r] = kq4_h2f(rg.sw.x >> 16) * WS;
       }
     } else if (p < NB + 1 + KQ4_GEMM_KB) {
-      const int u = p - NB - 1, r = t >> 1;   // BM = 128: every thread holds a half row
-      *reinterpret_cast<uint4 *>(&S.a[u][r * PITCH + swz(r, t & 1)]) = rg.a[u];
+      const int u = p - NB - 1;
+      if constexpr (ROT && TM == 1) {   // BM = 64: every thread holds a quarter row (8 B)
+        const int r = t >> 2;
+        *reinterpret_cast<uint2 *>(&S.a[u][r * PITCH + swz(r, (t >> 1) & 1) + 8 * (t & 1)]) = rg.a[u];
+      } else {                   // BM = 128: every thread holds a half row
+        const int r = t >> 1;
+        *reinterpret_cast<uint4 *>(&S.a[u][r * PITCH + swz(r, t & 1)]) = rg.a[u];
+      }
     } else {
       const int u = p - NB - 1 - KQ4_GEMM_KB, c = t + 256 * u;
       // ASM and Q8GEMM chains: the reference multiplies by the f16-rounded activation scale
@@ -267,95 +282,99 @@ __global__ __launch_bounds__(256, (TM == 2 && TN == 1) ? 3 : 2) void kq4_gemm_ke
     }
   };
   auto load = [&](Regs &rg, int b0) {
-    if constexpr (WF == 0) {
-      if (t < 2 * KQ4_GEMM_BM) {   // a whole wave's choice
+    if constexpr (!ROT) {   // (the pipelined forms stage in pieces)
+      if constexpr (WF == 0) {
+        if (t < 2 * KQ4_GEMM_BM) {   // a whole wave's choice
 #pragma unroll
-        for (int u = 0; u < KQ4_GEMM_KB; ++u)
-          rg.a[u] = kq4_bload16s(ra, va, (uint32_t)(min(b0 + u, nb - 1) * act.q_bs));
+          for (int u = 0; u < KQ4_GEMM_KB; ++u)
+            rg.a[u] = kq4_bload16s(ra, va, (uint32_t)(min(b0 + u, nb - 1) * act.q_bs));
+        }
+        const uint32_t sw = (uint32_t)((b0 >> 4) * KQ4_STREAM_CHUNK + 1024 * ((b0 & 15) >> 1));
+#pragma unroll
+        for (int u = 0; u < NB; ++u) rg.b[u] = kq4_bload16s(rw, vb[u], sw);
+        if (t < KQ4_GEMM_BN)   // a whole wave's choice
+          rg.sw = kq4_bload8s(rw, vs, (uint32_t)((b0 >> 4) * KQ4_STREAM_CHUNK +
+                                                 512 * ((b0 & 15) >> 3) + 2 * (b0 & 7)));
+#pragma unroll
+        for (int u = 0; u < KQ4_GEMM_KB * KQ4_GEMM_BM / 256; ++u)
+          rg.x[u] = __uint_as_float(
+              kq4_bload4s(rx, vx[u], (uint32_t)(min(b0 + xbl[u], nb - 1) * act.d_bs * 4)));
+        return;
       }
-      const uint32_t sw = (uint32_t)((b0 >> 4) * KQ4_STREAM_CHUNK + 1024 * ((b0 & 15) >> 1));
 #pragma unroll
-      for (int u = 0; u < NB; ++u) rg.b[u] = kq4_bload16s(rw, vb[u], sw);
-      if (t < KQ4_GEMM_BN)   // a whole wave's choice
-        rg.sw = kq4_bload8s(rw, vs, (uint32_t)((b0 >> 4) * KQ4_STREAM_CHUNK +
-                                               512 * ((b0 & 15) >> 3) + 2 * (b0 & 7)));
-#pragma unroll
-      for (int u = 0; u < KQ4_GEMM_KB * KQ4_GEMM_BM / 256; ++u)
-        rg.x[u] = __uint_as_float(
-            kq4_bload4s(rx, vx[u], (uint32_t)(min(b0 + xbl[u], nb - 1) * act.d_bs * 4)));
-      return;
-    }
-#pragma unroll
-    for (int u = 0; u < KQ4_GEMM_KB; ++u) {
-      const int tok = t >> 1, hh = t & 1;
-      const bool ok = tok < KQ4_GEMM_BM && b0 + u < nb && m0 + tok < n_tok;
-      rg.a[u] = kq4_bload16(
-          ra, ok ? (uint32_t)((m0 + tok) * act.q_ts + (long)(b0 + u) * act.q_bs + hh * 16) : KQ4_OOB);
-    }
-#pragma unroll
-    for (int u = 0; u < NB; ++u) {
-      const int idx = t + 256 * u;
-      uint32_t off;
-      if (WF) {   // (set sl, block iu of the stage, lane ln): 16 int8 codes
-        const int ln = idx & 63, iu = (idx >> 6) & 3, sl = idx >> 8;
-        const int rl = 32 * sl + (ln & 31), h = ln >> 5;
-        off = n0 + 32 * sl < rows ? (uint32_t)kq8_stream_code(n0 + rl, b0 + iu, h, nst) : KQ4_OOB;
-      } else {    // (set sl, nibble unit iu = 2 blocks, lane ln)
-        const int ln = idx & 63, iu = (idx >> 6) & 1, sl = idx >> 7;
-        const int rl = 32 * sl + (ln & 31), h = ln >> 5;
-        off = n0 + 32 * sl < rows ? (uint32_t)kq4_stream_nib(n0 + rl, b0 + 2 * iu, h, nst) : KQ4_OOB;
+      for (int u = 0; u < KQ4_GEMM_KB; ++u) {
+        const int tok = t >> 1, hh = t & 1;
+        const bool ok = tok < KQ4_GEMM_BM && b0 + u < nb && m0 + tok < n_tok;
+        rg.a[u] = kq4_bload16(
+            ra, ok ? (uint32_t)((m0 + tok) * act.q_ts + (long)(b0 + u) * act.q_bs + hh * 16) : KQ4_OOB);
       }
-      rg.b[u] = kq4_bload16(rw, off);   // row sets past the matrix: weight 0
-    }
-    const bool sok = t < KQ4_GEMM_BN && n0 + (t & ~31) < rows;
-    const uint32_t so = (uint32_t)(WF ? kq8_stream_scale(n0 + t, b0, nst) : kq4_stream_scale(n0 + t, b0, nst));
-    rg.sw = kq4_bload8(rw, sok ? so : KQ4_OOB);
 #pragma unroll
-    for (int u = 0; u < KQ4_GEMM_KB * KQ4_GEMM_BM / 256; ++u) {
-      const int c = t + 256 * u;
-      const int bl = c / KQ4_GEMM_BM, tok = c % KQ4_GEMM_BM;
-      const bool ok = b0 + bl < nb && m0 + tok < n_tok;
-      rg.x[u] = __uint_as_float(kq4_bload4(
-          rx, ok ? (uint32_t)(((m0 + tok) * act.d_ts + (long)(b0 + bl) * act.d_bs) * 4) : KQ4_OOB));
+      for (int u = 0; u < NB; ++u) {
+        const int idx = t + 256 * u;
+        uint32_t off;
+        if (WF) {   // (set sl, block iu of the stage, lane ln): 16 int8 codes
+          const int ln = idx & 63, iu = (idx >> 6) & 3, sl = idx >> 8;
+          const int rl = 32 * sl + (ln & 31), h = ln >> 5;
+          off = n0 + 32 * sl < rows ? (uint32_t)kq8_stream_code(n0 + rl, b0 + iu, h, nst) : KQ4_OOB;
+        } else {    // (set sl, nibble unit iu = 2 blocks, lane ln)
+          const int ln = idx & 63, iu = (idx >> 6) & 1, sl = idx >> 7;
+          const int rl = 32 * sl + (ln & 31), h = ln >> 5;
+          off = n0 + 32 * sl < rows ? (uint32_t)kq4_stream_nib(n0 + rl, b0 + 2 * iu, h, nst) : KQ4_OOB;
+        }
+        rg.b[u] = kq4_bload16(rw, off);   // row sets past the matrix: weight 0
+      }
+      const bool sok = t < KQ4_GEMM_BN && n0 + (t & ~31) < rows;
+      const uint32_t so = (uint32_t)(WF ? kq8_stream_scale(n0 + t, b0, nst) : kq4_stream_scale(n0 + t, b0, nst));
+      rg.sw = kq4_bload8(rw, sok ? so : KQ4_OOB);
+#pragma unroll
+      for (int u = 0; u < KQ4_GEMM_KB * KQ4_GEMM_BM / 256; ++u) {
+        const int c = t + 256 * u;
+        const int bl = c / KQ4_GEMM_BM, tok = c % KQ4_GEMM_BM;
+        const bool ok = b0 + bl < nb && m0 + tok < n_tok;
+        rg.x[u] = __uint_as_float(kq4_bload4(
+            rx, ok ? (uint32_t)(((m0 + tok) * act.d_ts + (long)(b0 + bl) * act.d_bs) * 4) : KQ4_OOB));
+      }
     }
   };
   auto store = [&](const Regs &rg) {
+    if constexpr (!ROT) {   // (the pipelined forms stage in pieces)
 #pragma unroll
-    for (int u = 0; u < KQ4_GEMM_KB; ++u)
-      if ((t >> 1) < KQ4_GEMM_BM)
-        *reinterpret_cast<uint4 *>(&sA[u][(t >> 1) * KQ4_LDS_ROW + (t & 1) * 16]) = rg.a[u];
+      for (int u = 0; u < KQ4_GEMM_KB; ++u)
+        if ((t >> 1) < KQ4_GEMM_BM)
+          *reinterpret_cast<uint4 *>(&sA[u][(t >> 1) * KQ4_LDS_ROW + (t & 1) * 16]) = rg.a[u];
 #pragma unroll
-    for (int u = 0; u < NB; ++u) {
-      const int idx = t + 256 * u;
-      if (WF) {
-        const int ln = idx & 63, iu = (idx >> 6) & 3, sl = idx >> 8;
-        const int rl = 32 * sl + (ln & 31), h = ln >> 5;
-        *reinterpret_cast<uint4 *>(&sB[iu][rl * KQ4_LDS_ROW + 16 * h]) = rg.b[u];
-      } else {
-        const int ln = idx & 63, iu = (idx >> 6) & 1, sl = idx >> 7;
-        const int rl = 32 * sl + (ln & 31), h = ln >> 5;
-        uint32_t o[4];
-        kq4_unpack_half(rg.b[u].x, rg.b[u].y, o);
-        *reinterpret_cast<uint4 *>(&sB[2 * iu][rl * KQ4_LDS_ROW + 16 * h]) =
-            make_uint4(o[0], o[1], o[2], o[3]);
-        kq4_unpack_half(rg.b[u].z, rg.b[u].w, o);
-        *reinterpret_cast<uint4 *>(&sB[2 * iu + 1][rl * KQ4_LDS_ROW + 16 * h]) =
-            make_uint4(o[0], o[1], o[2], o[3]);
+      for (int u = 0; u < NB; ++u) {
+        const int idx = t + 256 * u;
+        if (WF) {
+          const int ln = idx & 63, iu = (idx >> 6) & 3, sl = idx >> 8;
+          const int rl = 32 * sl + (ln & 31), h = ln >> 5;
+          *reinterpret_cast<uint4 *>(&sB[iu][rl * KQ4_LDS_ROW + 16 * h]) = rg.b[u];
+        } else {
+          const int ln = idx & 63, iu = (idx >> 6) & 1, sl = idx >> 7;
+          const int rl = 32 * sl + (ln & 31), h = ln >> 5;
+          uint32_t o[4];
+          kq4_unpack_half(rg.b[u].x, rg.b[u].y, o);
+          *reinterpret_cast<uint4 *>(&sB[2 * iu][rl * KQ4_LDS_ROW + 16 * h]) =
+              make_uint4(o[0], o[1], o[2], o[3]);
+          kq4_unpack_half(rg.b[u].z, rg.b[u].w, o);
+          *reinterpret_cast<uint4 *>(&sB[2 * iu + 1][rl * KQ4_LDS_ROW + 16 * h]) =
+              make_uint4(o[0], o[1], o[2], o[3]);
+        }
       }
-    }
-    if (t < KQ4_GEMM_BN) {
-      constexpr float WS = WF ? 1.0f : 0.0625f;   // q4 enters the MFMA as 16*(n-8)
-      sW[0][t] = kq4_h2f(rg.sw.x) * WS;
-      sW[1][t] = kq4_h2f(rg.sw.x >> 16) * WS;
-      sW[2][t] = kq4_h2f(rg.sw.y) * WS;
-      sW[3][t] = kq4_h2f(rg.sw.y >> 16) * WS;
-    }
+      if (t < KQ4_GEMM_BN) {
+        constexpr float WS = WF ? 1.0f : 0.0625f;   // q4 enters the MFMA as 16*(n-8)
+        sW[0][t] = kq4_h2f(rg.sw.x) * WS;
+        sW[1][t] = kq4_h2f(rg.sw.x >> 16) * WS;
+        sW[2][t] = kq4_h2f(rg.sw.y) * WS;
+        sW[3][t] = kq4_h2f(rg.sw.y >> 16) * WS;
+      }
 #pragma unroll
-    for (int u = 0; u < KQ4_GEMM_KB * KQ4_GEMM_BM / 256; ++u) {
-      const int c = t + 256 * u;
-      // ASM and Q8GEMM chains: the reference multiplies by the f16-rounded activation scale
-      sX[c / KQ4_GEMM_BM][c % KQ4_GEMM_BM] =
-          (CHAIN == KQ4_CHAIN_ASM || CHAIN == KQ4_CHAIN_Q8GEMM) ? kq4_f16_round(rg.x[u]) : rg.x[u];
+      for (int u = 0; u < KQ4_GEMM_KB * KQ4_GEMM_BM / 256; ++u) {
+        const int c = t + 256 * u;
+        // ASM and Q8GEMM chains: the reference multiplies by the f16-rounded activation scale
+        sX[c / KQ4_GEMM_BM][c % KQ4_GEMM_BM] =
+            (CHAIN == KQ4_CHAIN_ASM || CHAIN == KQ4_CHAIN_Q8GEMM) ? kq4_f16_round(rg.x[u]) : rg.x[u];
+      }
     }
   };
 
@@ -385,27 +404,33 @@ __global__ __launch_bounds__(256, (TM == 2 && TN == 1) ? 3 : 2) void kq4_gemm_ke
       // tile's second (last) epilogue of the current block. Each MFMA result is first read one
       // or two tile epilogues (32 VALU instructions each) after its issue, so the matrix core's
       // latency hides behind the wave's own VALU work (2.5 % at M = 2048 against the in-order
-      // form); scheduling barriers keep that order. Only for two token tiles: with one, the
-      // second scale set it needs costs the third wave per SIMD that its register count allows.
-      constexpr int NT = 2 * TN;              // MFMA tiles per wave and block: k = i + 2 * jn
+      // form); scheduling barriers keep that order. With one token tile (64 x 128) one scale
+      // set serves both row tiles of a block and is reissued after the block's last epilogue
+      // (a second set, to issue it earlier, would cost the third wave per SIMD).
+      constexpr int NT = TM * TN;             // MFMA tiles per wave and block: k = i + TM * jn
       constexpr int NQ = KQ4_GEMM_KB * NT;
-      kq4_v4i af[2], bf[TN];
+      kq4_v4i af[TM], bf[TN];
       float xv, wv[TN];
       kq4_v16i sacc[2];
-      kq4_v32f sc[TN];
+      kq4_v32f sc[TM == 2 ? TN : 1];
       const kq4_v16i zero = {0};
       const kq4_v32f z32 = {0};
       auto frag_ab = [&](int bl) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < TM; ++i)
           af[i] = *reinterpret_cast<const kq4_v4i *>(
-              &C.a[bl][(64 * wm + 32 * i + l32) * PITCH + swz(l32, half)]);
+              &C.a[bl][(32 * TM * wm + 32 * i + l32) * PITCH + swz(l32, half)]);
 #pragma unroll
         for (int jn = 0; jn < TN; ++jn)
           bf[jn] = *reinterpret_cast<const kq4_v4i *>(
               &C.b[bl][(32 * TN * wn + 32 * jn + l32) * PITCH + swz(l32, half)]);
       };
       auto frag_s = [&](int bl) {
+        if constexpr (TM == 1) {   // the outer product's two blocks are the wave's row tiles
+          xv = C.x[bl][32 * wm + l32];
+          wv[0] = kq4_h2f(C.w[bl][32 * TN * wn + lane]) * (WF ? 1.0f : 0.0625f);
+          return;
+        }
         xv = C.x[bl][64 * wm + lane];
 #pragma unroll
         for (int jn = 0; jn < TN; ++jn) {
@@ -417,28 +442,32 @@ __global__ __launch_bounds__(256, (TM == 2 && TN == 1) ? 3 : 2) void kq4_gemm_ke
       };
       // Scale products fl(wd * xs) from the matrix core: v_mfma_f32_32x32x1_2b_f32 is a rank-1
       // update of two 32 x 32 blocks, each output one product rounded once (with a zero
-      // addend), in the MFMA output layout; its blocks are the two token tiles of row tile jn.
+      // addend), in the MFMA output layout; its blocks are the two token tiles of row tile jn
+      // (one token tile: the wave's two row tiles, one product set for both).
       auto issue_sc = [&](int jn) {
-        sc[jn] = __builtin_amdgcn_mfma_f32_32x32x1f32(xv, wv[jn], z32, 0, 0, 0);
+        if constexpr (TM == 1) sc[0] = __builtin_amdgcn_mfma_f32_32x32x1f32(xv, wv[0], z32, 0, 0, 0);
+        else sc[jn] = __builtin_amdgcn_mfma_f32_32x32x1f32(xv, wv[jn], z32, 0, 0, 0);
       };
       auto issue_s = [&](int q) {
         const int k = q % NT;
-        sacc[q & 1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[k & 1], bf[k >> 1], zero, 0, 0, 0);
+        sacc[q & 1] =
+            __builtin_amdgcn_mfma_i32_32x32x32_i8(af[k % TM], bf[k / TM], zero, 0, 0, 0);
       };
       auto epi = [&](int q) {
-        const int k = q % NT, i = k & 1, jn = k >> 1;
+        const int k = q % NT, i = k % TM, jn = k / TM;
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
+          const float s = TM == 2 ? sc[TM == 2 ? jn : 0][16 * i + v] : sc[0][16 * jn + v];
           if (CHAIN == KQ4_CHAIN_Q8GEMM)   // unfused: fl(acc + fl(scale * S))
-            acc[i][jn][v] = acc[i][jn][v] + sc[jn][16 * i + v] * (float)sacc[q & 1][v];
+            acc[i][jn][v] = acc[i][jn][v] + s * (float)sacc[q & 1][v];
           else
-            acc[i][jn][v] = fmaf((float)sacc[q & 1][v], sc[jn][16 * i + v], acc[i][jn][v]);
+            acc[i][jn][v] = fmaf((float)sacc[q & 1][v], s, acc[i][jn][v]);
         }
       };
       frag_s(0);
       frag_ab(0);
 #pragma unroll
-      for (int jn = 0; jn < TN; ++jn) issue_sc(jn);
+      for (int jn = 0; jn < (TM == 2 ? TN : 1); ++jn) issue_sc(jn);
       issue_s(0);
 #pragma unroll
       for (int q = 0; q < NQ; ++q) {
