@@ -60,8 +60,8 @@ def test_q8_gemm_bit_exact(kq4, torch_dev, orc, rows, cols, g, n, chain):
 
 
 # 128x128 tiles (2048 tokens x 4096 rows: 512 tiles) and 64x128 (2048 rows); short K keeps the
-# oracle quick; tile 4 forces the 128x64 form (planner option gemm_tile)
-@pytest.mark.parametrize("tile", [0, 4])
+# oracle quick; tiles 2 and 4 force the 64x128 and 128x64 forms (planner option gemm_tile)
+@pytest.mark.parametrize("tile", [0, 2, 4])
 @pytest.mark.parametrize("n,rows,chain", [(2048, 4096, 0), (2048, 4096, 4), (2048, 2048, 2)])
 def test_q8_gemm_large_tiles_bit_exact(kq4, torch_dev, orc, n, rows, chain, tile):
     torch = torch_dev
