@@ -66,9 +66,10 @@ extern "C" {
  * vllm_safetensors.c:4593-4631): n_batch <= 3 -> CTILE; n_batch > 3 -> ASM on the first
  * n_batch & ~3 tokens and CTILE on the rest.
  * The prefill GEMM (n_batch > 8) replays the selected chain per output bit for bit, except where
- * the planner splits K (launches with fewer 128x128 tiles than CUs and K >= 256 blocks; option
- * gemm_split): each K slice then runs the chain from zero and the slices' outputs are added in
- * slice order, within 1e-5 of the single chain. The decode
+ * the planner splits K (launches that leave CUs idle: fewer 128x128 tiles than CUs with K >= 256
+ * blocks, or K >= 128 blocks with fewer 64-token tiles than three per CU; never the CTILE chain;
+ * option gemm_split): each K slice then runs the chain from zero and the slices' outputs are
+ * added in slice order, within 1e-5 of the single chain. The decode
  * GEMV (n_batch <= 8, and the 1..3-token AUTO tail) takes from the chain only its activation
  * scale (f16-rounded for ASM tokens, f32 otherwise): it splits K over waves and sums each
  * wave's terms in block order (one token: a lo and a hi chain per half block, as CTILE; two or
@@ -113,7 +114,7 @@ const char *kq4_version(void);
  * GEMV), gemv_fq_work, gemv_silu_fq_work, gemm_kind (0: the prefill GEMM on int8 MFMA, the
  * default; 1: on fp8 operands; the same outputs), gemm_tile (0: the planner's choice; 1 / 2 / 3 /
  * 4: 128x128 / 64x128 / 64x64 / 128x64 token x row tiles; the same outputs), gemm_split (K slices
- * of the int8 GEMM: 0 or 1 none, every output the single chain bit for bit; 2..4 that many;
+ * of the int8 GEMM: 0 or 1 none, every output the single chain bit for bit; 2..8 that many;
  * -1 the planner's choice, the default), gemm_prio (the 128x128 int8 GEMM's issue priority
  * falling with progress through K, so the two workgroups sharing a CU end together: 0 off, 1 on,
  * -1 the planner's choice, on for launches of whole rounds of two workgroups per CU; the same

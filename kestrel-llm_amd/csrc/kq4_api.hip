@@ -285,15 +285,17 @@ bool gemv_fq(long work, int n, int rps, bool silu) {
   return rps > 1 || work <= (n <= 4 ? opt(kGemvFqWork) : opt(kGemvFqWork) * 4 / 9);
 }
 
-// K slices of each matrix's prefill GEMM (kq4_gemm_ksplit) into ksp[], and the workspace bytes
-// of their partial sums: one buffer for the largest, reused matrix after matrix (the launches
-// are stream-ordered).
+// Tile and K slices of each matrix's prefill GEMM (kq4_gemm_plan) into pl[], and the workspace
+// bytes of their partial sums: one buffer for the largest, reused matrix after matrix (the
+// launches are stream-ordered).
 size_t split_bytes(int n_mats, const int *rows, int cols, int n, int wf, int chain, int ncu,
-                   int *ksp) {
+                   KQ4GemmPlan *pl) {
   size_t mx = 0;
   for (int i = 0; i < n_mats; ++i) {
-    ksp[i] = kq4_gemm_ksplit(n, rows[i], cols, wf, chain, ncu, opt(kGemmSplit));
-    const size_t b = (size_t)(ksp[i] - 1) * n * rows[i] * sizeof(float);
+    const int ft = opt(kGemmTile);
+    pl[i] = kq4_gemm_plan(n, rows[i], cols, wf, chain, ncu, ft >= 1 && ft <= 4 ? ft : -1,
+                          opt(kGemmSplit));
+    const size_t b = (size_t)(pl[i].ksplit - 1) * n * rows[i] * sizeof(float);
     mx = b > mx ? b : mx;
   }
   return al256(mx);
@@ -396,8 +398,8 @@ int matmul_impl(int n_mats, float *const *out, const float *const *res, const ui
       return run_gemv(ds, ws, n_mats, out, res, w, rows, cols, x, nullptr, xq_in, xd_in, n,
                       gchain ? n : 0, s, gchain ? 2 : 1);
     const int qc = gchain ? KQ4_CHAIN_Q8GEMM : KQ4_CHAIN_GEMV32;
-    int ksp[KQ4_MAX_MATS];
-    const size_t pbytes = split_bytes(n_mats, rows, cols, n, 1, qc, ds->ncu, ksp);
+    KQ4GemmPlan pl[KQ4_MAX_MATS];
+    const size_t pbytes = split_bytes(n_mats, rows, cols, n, 1, qc, ds->ncu, pl);
     if ((rc = ensure_ws(ws, qbytes + pbytes, s))) return rc;
     Carve cv{static_cast<char *>(ws.b->p)};
     KQ4GemmAct act{xq_in, cols, 32, xd_in, nb, 1};
@@ -412,7 +414,7 @@ int matmul_impl(int n_mats, float *const *out, const float *const *res, const ui
     float *part = pbytes ? cv.take<float>(pbytes / sizeof(float)) : nullptr;
     for (int i = 0; i < n_mats; ++i)
       KQ4_HIP((hipError_t)kq4_launch_gemm(out[i], res ? res[i] : nullptr, w[i], act, rows[i],
-                                          cols, n, qc, ds->ncu, s, 1, opt(kGemmTile), ksp[i],
+                                          cols, n, qc, ds->ncu, s, 1, pl[i].tile, pl[i].ksplit,
                                           part, opt(kGemmPrio)));
     return KQ4_OK;
   }
@@ -448,8 +450,8 @@ int matmul_impl(int n_mats, float *const *out, const float *const *res, const ui
     return run_gemv(ds, ws, n_mats, o2, r2, w, rows, cols, x + (size_t)main_n * cols,
                     xu ? xu + (size_t)main_n * cols : nullptr, nullptr, nullptr, tail, 0, s);
   }
-  int ksp[KQ4_MAX_MATS];
-  const size_t pbytes = split_bytes(n_mats, rows, cols, main_n, 0, main_chain, ds->ncu, ksp);
+  KQ4GemmPlan pl[KQ4_MAX_MATS];
+  const size_t pbytes = split_bytes(n_mats, rows, cols, main_n, 0, main_chain, ds->ncu, pl);
   if ((rc = ensure_ws(ws, qbytes + pbytes, s))) return rc;
   Carve cv{static_cast<char *>(ws.b->p)};
   KQ4GemmAct act;
@@ -473,8 +475,8 @@ int matmul_impl(int n_mats, float *const *out, const float *const *res, const ui
   float *part = pbytes ? cv.take<float>(pbytes / sizeof(float)) : nullptr;
   for (int i = 0; i < n_mats; ++i)
     KQ4_HIP((hipError_t)kq4_launch_gemm(out[i], res ? res[i] : nullptr, w[i], act, rows[i], cols,
-                                        main_n, main_chain, ds->ncu, s, 0, opt(kGemmTile), ksp[i],
-                                        part, opt(kGemmPrio)));
+                                        main_n, main_chain, ds->ncu, s, 0, pl[i].tile,
+                                        pl[i].ksplit, part, opt(kGemmPrio)));
   if (tail) {
     float *o2[KQ4_MAX_MATS];
     const float *r2[KQ4_MAX_MATS];
@@ -849,9 +851,9 @@ int kq4_matmul_noalloc_dev(float *out, const float *x, const float *residual, co
     } else {   // fp8 operands, or int8 operands and the K-split partial sums
       const int main_n = chain == KQ4_CHAIN_AUTO ? (n_batch & ~3) : n_batch;
       const int mc = chain == KQ4_CHAIN_AUTO ? KQ4_CHAIN_ASM : chain;
-      int ksp = 1;
+      KQ4GemmPlan pl;
       const size_t q = qa_bytes(n_batch, cols) + split_bytes(1, &rows, cols, main_n, 0, mc,
-                                                             ds->ncu, &ksp);
+                                                             ds->ncu, &pl);
       const size_t f = f8_bytes(n_batch, cols);
       need = q > f ? q : f;
     }

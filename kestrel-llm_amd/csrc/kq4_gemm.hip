@@ -901,11 +901,6 @@ static hipError_t gemm_launch(float *out, const float *res, const uint8_t *w,
   return hipGetLastError();
 }
 
-// The largest of the 128x128, 64x128 and 64x64 (tokens x rows) tiles that gives at least two
-// tiles per CU (else 64x64), with 128x64 before the 64-token forms for long K (below). The C-tile
-// chain (two accumulator sets) takes 64x128 at most: at 128x128 it needs more than 256 registers
-// and spills. `tile` = 1/2/3/4 (128x128, 64x128, 64x64, 128x64; planner option gemm_tile)
-// forces one (for measurement and tests; the C-tile chain still caps it).
 // Blocks per K slice for ksplit slices: ceil(nb / ksplit) rounded up to whole stream-layout
 // stages; 0 when ksplit slices of that length do not all hold blocks.
 static int split_len(int nb, int cb, int ksplit) {
@@ -914,26 +909,69 @@ static int split_len(int nb, int cb, int ksplit) {
   return (long)(ksplit - 1) * ks < nb ? ks : 0;
 }
 
-// K slices of a prefill GEMM launch. Split only where the launch leaves the chip short of work:
-// fewer 128 x 128 tiles than CUs and a long K (>= 256 blocks), into the most slices (at most
-// KQ4_GEMM_SPLIT_MAX, each >= 64 blocks) that keep slices x tiles within two per CU (Qwen3-8B
-// down, K = 12288, at M = 512: 128 tiles -> 4 slices of 96 blocks, 512 workgroups). The C-tile
-// chain is never split by the planner. force: planner option gemm_split (-1 the planner, 0 / 1
-// no split, 2 .. KQ4_GEMM_SPLIT_MAX that many slices where the blocks allow it).
-// (P - 1) * n_tok * rows * 4 bytes of partial sums go to the workspace: P * tiles <= 2 * 256
-// keeps that below 24 MiB.
-int kq4_gemm_ksplit(int n_tok, int rows, int cols, int wf, int chain, int ncu, int force) {
-  if (n_tok <= 0 || rows <= 0 || cols <= 0) return 1;
+// The planner. A launch runs in rounds of workgroups, two per CU for the 128 x 128 form and three
+// for the 64-token forms (their LDS rings and registers), so it chooses the form that fills its
+// rounds best, splitting K where the tiles alone leave CUs idle:
+//   * 128 x 128 tiles from two per CU;
+//   * K split over 128 x 128 tiles (KA: fewer tiles than CUs, K >= 256 blocks): the most slices
+//     of >= 64 blocks with slices x tiles <= two per CU (Qwen3-8B down at M = 512: 128 tiles,
+//     4 slices of 96 blocks, 512 workgroups, one whole round);
+//   * K split over 64-token tiles (KB: K >= 128 blocks, 64 x 64 tiles for one token tile, else
+//     64 x 128): the most slices (<= 8) of >= 32 blocks with slices x tiles <= three per CU;
+//     taken over KA where it fills more of its round (Qwen3-8B down at M = 768: KA 384 of 512,
+//     KB 768 of 768 workgroups, 145 -> 123 us; at M = 512 and 1024 both fill one round and KA
+//     stays) and in place of the unsplit forms below (gate, K = 4096, M = 64 / 128 / 256: 64 x 64
+//     tiles unsplit 34.6 / 43.3 / 54.3 us, KB 24.7 / 35.4 / 51.2 us; down at M = 32-128 39-44 ->
+//     25-34 us);
+//   * the pipelined 128 x 64 form for long K (>= 256 blocks) from one tile per CU;
+//   * else 64 x 128 from one tile per CU for K >= 128 blocks (Qwen3-8B gate at M = 320: 74.3 us
+//     as 64 x 64, 59.1 us as 64 x 128), from two per CU for shorter K (Qwen3-VL-2B gate,
+//     K = 2048, at M = 384: 30.5 us as 64 x 64, 33.2 us as 64 x 128), else 64 x 64.
+// The C-tile chain (two accumulator sets) takes 64 x 128 at most (at 128 x 128 it spills) and
+// is never split by the planner. The options force a tile and / or a slice count (the planner
+// then picks the other part for it). KB's partial sums stay within 24 MiB: three 64 x 128 tiles
+// per CU are 768 x 8192 outputs.
+KQ4GemmPlan kq4_gemm_plan(int n_tok, int rows, int cols, int wf, int chain, int ncu,
+                          int force_tile, int force_split) {
+  KQ4GemmPlan p{3, 1};
+  if (n_tok <= 0 || rows <= 0 || cols <= 0) return p;
   const int nb = cols / 32;
   const int cb = wf ? KQ8_STREAM_CB : KQ4_STREAM_CB;
-  if (force == 0 || force == 1) return 1;
-  if (force >= 2) return force <= KQ4_GEMM_SPLIT_MAX && split_len(nb, cb, force) ? force : 1;
-  const long t = (long)((n_tok + 127) / 128) * ((rows + 127) / 128);
-  const int cu = ncu < 256 ? ncu : 256;
-  if (chain == KQ4_CHAIN_CTILE || t > cu || nb < 256) return 1;
-  for (int p = KQ4_GEMM_SPLIT_MAX; p >= 2; --p)
-    if (p * t <= 2L * cu && split_len(nb, cb, p) >= 64) return p;
-  return 1;
+  const long cu = ncu < 1 ? 1 : (ncu < 256 ? ncu : 256);
+  auto tiles = [&](int t) {
+    const int bm = t == 1 || t == 4 ? 128 : 64, bn = t == 3 || t == 4 ? 64 : 128;
+    return (long)((n_tok + bm - 1) / bm) * ((rows + bn - 1) / bn);
+  };
+  // the most slices of >= minb blocks with slices x tiles <= cap
+  auto most = [&](long t, long cap, int minb) {
+    for (int k = KQ4_GEMM_SPLIT_MAX; k >= 2; --k)
+      if (k * t <= cap && split_len(nb, cb, k) >= minb) return k;
+    return 1;
+  };
+  const bool ctile = chain == KQ4_CHAIN_CTILE;
+  const int tb = n_tok <= 64 ? 3 : 2;                           // KB's tile
+  const int ka = !ctile && tiles(1) <= cu && nb >= 256 ? most(tiles(1), 2 * cu, 64) : 1;
+  const int kb = !ctile && nb >= 128 ? most(tiles(tb), 3 * cu, 32) : 1;
+  // forced slices: 0 / 1 none; counts the blocks do not allow are taken as none
+  int fk = force_split;
+  if (fk >= 0 && (fk <= 1 || fk > KQ4_GEMM_SPLIT_MAX || !split_len(nb, cb, fk))) fk = 1;
+  if (force_tile >= 1 && force_tile <= 4) {
+    p.tile = force_tile;
+    p.ksplit = fk >= 1 ? fk : force_tile == 1 ? ka : force_tile == tb ? kb : 1;
+  } else if (fk > 1) {
+    p = KQ4GemmPlan{1, fk};
+  } else if (fk < 0 && ka > 1 && ka * tiles(1) * 3 >= kb * tiles(tb) * 2) {
+    p = KQ4GemmPlan{1, ka};   // KA fills as much of its round as KB
+  } else if (fk < 0 && kb > 1 && tiles(1) < 2 * cu) {
+    p = KQ4GemmPlan{tb, kb};
+  } else {
+    p.tile = tiles(1) >= 2 * cu                            ? 1
+             : nb >= 256 && tiles(4) >= cu                 ? 4
+             : tiles(2) >= (nb >= 128 ? cu : 2 * cu) ? 2
+                                                           : 3;
+  }
+  if (ctile && (p.tile == 1 || p.tile == 4)) p.tile = 2;
+  return p;
 }
 
 int kq4_launch_gemm(float *out, const float *res, const uint8_t *w, const KQ4GemmAct &act,
@@ -949,14 +987,8 @@ int kq4_launch_gemm(float *out, const float *res, const uint8_t *w, const KQ4Gem
   const int ks = split_len(nb, cb, ksplit);
   if (ksplit < 1 || ksplit > KQ4_GEMM_SPLIT_MAX || !ks || (ksplit > 1 && !part))
     return (int)hipErrorInvalidValue;
-  // Long K (>= 256 blocks) with fewer than two 128 x 128 tiles per CU: the pipelined 128 x 64
-  // form as soon as it has a tile per CU (Qwen3-8B down, K = 12288: M = 512 131.6 -> 121.4 us,
-  // M = 1024 211 -> 192 us; at K = 4096 the 64-token forms stay faster).
-  int pick = tile >= 1 && tile <= 4             ? tile
-             : ksplit > 1 || tiles(128, 128) >= 2L * ncu ? 1
-             : nb >= 256 && tiles(128, 64) >= ncu ? 4
-             : tiles(64, 128) >= 2L * ncu        ? 2
-                                                 : 3;
+  int pick = tile >= 1 && tile <= 4 ? tile
+                                    : kq4_gemm_plan(n_tok, rows, cols, wf, chain, ncu, -1, ksplit).tile;
   if (chain == KQ4_CHAIN_CTILE && (pick == 1 || pick == 4)) pick = 2;
   // 32-bit buffer offsets: weights and activation operands below 4 GB
   const size_t wb = wf ? kq8_stream_bytes(rows, cols) : kq4_stream_bytes(rows, cols);

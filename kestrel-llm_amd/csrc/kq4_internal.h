@@ -96,18 +96,23 @@ struct KQ4GemmAct {
   long d_ts, d_bs;
 };
 // wf = 1: Q8_0 weights in the q8 stream layout, chain KQ4_CHAIN_Q8GEMM or KQ4_CHAIN_GEMV32.
-// tile: 0 the planner's choice; 1 / 2 / 3 / 4 force 128x128 / 64x128 / 64x64 / 128x64 (tokens x
-// rows; the C-tile chain is capped at 64x128).
-// ksplit > 1 (kq4_gemm_ksplit): K in that many slices, each its own chain from zero, added in
-// slice order by a second launch; part = (ksplit - 1) * n_tok * rows floats of workspace
-// (16-byte aligned) for slices 1 .. ksplit - 1. Within 1e-5 of the single chain, not
-// bit-identical to it.
+// tile: 1 / 2 / 3 / 4 = 128x128 / 64x128 / 64x64 / 128x64 (tokens x rows; the C-tile chain is
+// capped at 64x128), 0 the planner's choice (kq4_gemm_plan).
+// ksplit > 1: K in that many slices, each its own chain from zero, added in slice order by a
+// second launch; part = (ksplit - 1) * n_tok * rows floats of workspace (16-byte aligned) for
+// slices 1 .. ksplit - 1. Within 1e-5 of the single chain, not bit-identical to it.
 // prio: the 128x128 form's issue priority by progress through K (kq4_prio_by_progress): 0 off,
 // 1 on, -1 on for launches of whole rounds (a multiple of two workgroups per CU). Outputs do
 // not depend on it.
-#define KQ4_GEMM_SPLIT_MAX 4
+#define KQ4_GEMM_SPLIT_MAX 8
 #define KQ4_SPLIT_PART_MAX (24u << 20)   // partial-sum bytes of the planner's splits, at most
-int kq4_gemm_ksplit(int n_tok, int rows, int cols, int wf, int chain, int ncu, int force);
+// The planner's tile and K slices of one prefill GEMM launch; force_tile / force_split are the
+// planner options gemm_tile and gemm_split (-1: the planner's choice).
+struct KQ4GemmPlan {
+  int tile, ksplit;
+};
+KQ4GemmPlan kq4_gemm_plan(int n_tok, int rows, int cols, int wf, int chain, int ncu,
+                          int force_tile, int force_split);
 int kq4_launch_gemm(float *out, const float *res, const uint8_t *w, const KQ4GemmAct &act,
                     int rows, int cols, int n_tok, int chain, int ncu, hipStream_t stream,
                     int wf = 0, int tile = 0, int ksplit = 1, float *part = nullptr,

@@ -151,7 +151,7 @@ def test_workspace_trim_frees_outgrown_workspaces(kq4, torch_dev, orc):
 
 
 def test_graph_split_k_gemm(kq4, torch_dev, orc):
-    """A K-split prefill GEMM (planner: 32 tiles of 128 x 128, K = 8192 in 4 slices; the slices'
+    """A K-split prefill GEMM (planner: 64 tiles of 64 x 128, K = 8192 in 8 slices; the slices'
     partial sums in the workspace, a reduction launch adding them and the residual) captured in
     a graph: every replay, with eager work of other shapes between them, reproduces the eager
     result bit for bit, which is within 1e-5 of the oracle's single chain."""

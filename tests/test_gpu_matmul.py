@@ -244,11 +244,11 @@ def test_gemm_f8_auto_tail(kq4, torch_dev, orc, form):
         assert e <= TOL
 
 
-@pytest.mark.parametrize("split", [2, 3, 4])
+@pytest.mark.parametrize("split", [2, 3, 4, 8])
 @pytest.mark.parametrize("chain", [0, 1, 2, 3])
 def test_gemm_split_k(kq4, torch_dev, orc, chain, split):
     """Split K forced through the planner option gemm_split: K = 4096 (128 blocks) in 2 slices of
-    64 blocks, 3 of 48 (the last one 32) or 4 of 32, each slice its own chain from zero, added in
+    64 blocks, 3 of 48 (the last one 32), 4 of 32 or 8 of 16, each slice its own chain from zero, added in
     slice order with the residual last. Every output within 1e-5 of the oracle's single chain
     (the split is not bit-identical to it), repeat calls bit-identical, for
     every chain, a 301-token batch (AUTO: a 1-token C-tile tail on the GEMV) and two matrices of
@@ -277,6 +277,41 @@ def test_gemm_split_k(kq4, torch_dev, orc, chain, split):
         print(f"split={split} chain={chain} rows={r}: rel={e:.3e} maxabs={a:.3e} "
               f"bit-identical {same:.3f}")
         assert e <= TOL
+
+
+# The planner's K splits over 64-token tiles (small token counts, K >= 128 blocks: 64 x 64 tiles
+# for one token tile, 64 x 128 beyond, up to 8 slices of >= 32 blocks), and the same forms
+# forced: sampled outputs (every 64 x 64 cell, the last token and row, random pairs) within 1e-5
+# of the oracle's single chain, repeat calls bit-identical.
+@pytest.mark.parametrize("form", ["planner", (2, 8), (3, 4), (2, 3)])
+@pytest.mark.parametrize("n,rows,cols,chain", [(16, 1024, 12288, 0), (64, 2048, 6144, 3),
+                                               (100, 4096, 4096, 2), (200, 1000, 8192, 0),
+                                               (33, 640, 4096, 3)])
+def test_gemm_small_batch_splits(kq4, torch_dev, orc, n, rows, cols, chain, form):
+    torch = torch_dev
+    w, x = case(rows, cols, n, 1100 + n + rows)
+    res = synth.make_activations(n, rows, 1101 + n)
+    W, X, R = wdev(kq4, torch, w, rows, cols), to_dev(torch, x), to_dev(torch, res)
+    out = torch.empty((n, rows), dtype=torch.float32, device="cuda")
+    again = torch.empty_like(out)
+    opts = {} if form == "planner" else dict(gemm_tile=form[0], gemm_split=form[1])
+    with kq4.options(**opts):
+        kq4.matmul_dev(out, X, W, rows, cols, residual=R, chain=chain)
+        kq4.matmul_dev(again, X, W, rows, cols, residual=R, chain=chain)
+    torch.cuda.synchronize()
+    got = host(out)
+    assert np.array_equal(got.view(np.uint32), host(again).view(np.uint32))
+    xq, xd = orc.quantize(x, cols)
+    rng = np.random.default_rng(n + rows)
+    t0, r0 = np.meshgrid(np.arange(0, n, 64), np.arange(0, rows, 64), indexing="ij")
+    tok = np.concatenate([np.minimum(t0.ravel() + rng.integers(0, 64, t0.size), n - 1),
+                          [n - 1] * 64, rng.integers(0, n, 2048)]).astype(np.int32)
+    row = np.concatenate([np.minimum(r0.ravel() + rng.integers(0, 64, r0.size), rows - 1),
+                          rng.integers(0, rows, 64), rng.integers(0, rows, 2048)]).astype(np.int32)
+    want = orc.matmul_q_sample(w, xq, xd, rows, cols, n, tok, row, residual=res, chain=chain)
+    e = np.abs(got[tok, row].astype(np.float64) - want).max() / np.abs(want).max()
+    print(f"small-batch split {form} n={n} rows={rows} cols={cols} chain={chain}: rel={e:.3e}")
+    assert e <= TOL
 
 
 @pytest.mark.parametrize("split", [1, 2])
