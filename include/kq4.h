@@ -65,12 +65,14 @@ extern "C" {
  * same in all of them). AUTO is the reference's dispatch (q4x4_gemm_batched
  * vllm_safetensors.c:4593-4631): n_batch <= 3 -> CTILE; n_batch > 3 -> ASM on the first
  * n_batch & ~3 tokens and CTILE on the rest.
- * The prefill GEMM (n_batch > 8) replays the selected chain per output bit for bit, except where
+ * The prefill GEMM (n_batch > 16; option gemv_chunk_max) replays the selected chain per output
+ * bit for bit, except where
  * the planner splits K (launches that leave CUs idle: fewer 128x128 tiles than CUs with K >= 256
  * blocks, or K >= 128 blocks with fewer 64-token tiles than three per CU; never the CTILE chain;
  * option gemm_split): each K slice then runs the chain from zero and the slices' outputs are
  * added in slice order, within 1e-5 of the single chain. The decode
- * GEMV (n_batch <= 8, and the 1..3-token AUTO tail) takes from the chain only its activation
+ * GEMV (n_batch <= 8; 9..16 in launches of 8 tokens; and the GEMM's 1..3-token AUTO tail)
+ * takes from the chain only its activation
  * scale (f16-rounded for ASM tokens, f32 otherwise): it splits K over waves and sums each
  * wave's terms in block order (one token: a lo and a hi chain per half block, as CTILE; two or
  * more: one term per block, as GEMV32), then adds the waves' sums in a fixed order. So CTILE and
@@ -111,7 +113,9 @@ const char *kq4_version(void);
  * reference): gemv_kind (0 v_dot4 / 1 MFMA dots), gemv_mfma_from, gemv_hs (0 whole 32-row sets,
  * 1 halves, 2 quarters per workgroup), gemv_rps (row sets per workgroup, 1..3), gemv_waves,
  * gemv_wpcu, gemv_maxw, gemv_fq (0 / 1: activations quantized by a separate launch / in the
- * GEMV), gemv_fq_work, gemv_silu_fq_work, gemm_kind (0: the prefill GEMM on int8 MFMA, the
+ * GEMV), gemv_fq_work, gemv_silu_fq_work, gemv_chunk_max (the largest batch the decode GEMV
+ * takes, in launches of up to 8 tokens, 16 by default; 8 or less: every batch beyond 8 tokens
+ * on the prefill GEMM), gemm_kind (0: the prefill GEMM on int8 MFMA, the
  * default; 1: on fp8 operands; the same outputs), gemm_tile (0: the planner's choice; 1 / 2 / 3 /
  * 4: 128x128 / 64x128 / 64x64 / 128x64 token x row tiles; the same outputs), gemm_split (K slices
  * of the int8 GEMM: 0 or 1 none, every output the single chain bit for bit; 2..8 that many;

@@ -178,7 +178,8 @@ int env_int(const char *name, int dflt) {
 // choice where a planner chooses.
 enum OptId {
   kGemvKind, kGemvMfmaFrom, kGemvHs, kGemvRps, kGemvWaves, kGemvWpcu, kGemvMaxw,
-  kGemvFq, kGemvFqWork, kGemvSiluFqWork, kGemmKind, kGemmTile, kGemmSplit, kGemmPrio, kOptCount
+  kGemvFq, kGemvFqWork, kGemvSiluFqWork, kGemvChunkMax, kGemmKind, kGemmTile, kGemmSplit,
+  kGemmPrio, kOptCount
 };
 struct OptDef {
   const char *name, *env;
@@ -191,6 +192,7 @@ const OptDef kOpts[kOptCount] = {
     {"gemv_wpcu", "KQ4_GEMV_WPCU", 64},          {"gemv_maxw", "KQ4_GEMV_MAXW", 16},
     {"gemv_fq", "KQ4_GEMV_FQ", -1},              {"gemv_fq_work", "KQ4_GEMV_FQ_WORK", 45000},
     {"gemv_silu_fq_work", "KQ4_GEMV_SILU_FQ_WORK", 15000},
+    {"gemv_chunk_max", "KQ4_GEMV_CHUNK_MAX", 16},
     {"gemm_kind", "KQ4_GEMM_KIND", -1},          {"gemm_tile", "KQ4_GEMM_TILE", 0},
     {"gemm_split", "KQ4_GEMM_SPLIT", -1},        {"gemm_prio", "KQ4_GEMM_PRIO", -1},
 };
@@ -388,6 +390,38 @@ int matmul_impl(int n_mats, float *const *out, const float *const *res, const ui
   const Ws ws = wsp ? *wsp : Ws{&ds->ws, ds};
   const int nb = cols / 32;
   const size_t qbytes = qa_bytes(n, cols);
+
+  // Up to gemv_chunk_max tokens (16) the decode GEMV takes the batch in launches of 8 tokens,
+  // each reading the weights once more (the later ones mostly from the 256 MB Infinity Cache):
+  // below ~24 tokens the prefill GEMM's per-tile stage chain is latency-bound and slower
+  // (graph replay, 16 tokens: Qwen3-VL-2B gate 19.1 -> 13.7 us, O 18.9 -> 9.7 us, Qwen3-8B
+  // QKV 17.6 -> 16.1 us; at 24 tokens the GEMM is ahead for all but the 2048 x 2048 O). The
+  // chunks start at multiples of 4 tokens, so the AUTO chain puts the same tokens on the ASM
+  // scale rounding as the reference's dispatch over the whole batch (the first n & ~3); q8's
+  // AUTO chain is chosen for the whole batch as well. Outputs as the GEMV's: within 1e-5 of the
+  // reference chain, not bit-identical to it.
+  if (n > KQ4_GEMV_MAX_M && n <= opt(kGemvChunkMax)) {
+    const bool gchain = wf && (chain == KQ4_CHAIN_Q8GEMM || (chain == KQ4_CHAIN_AUTO && n >= 2));
+    for (int c = 0; c < n; c += KQ4_GEMV_MAX_M) {
+      const int m = n - c < KQ4_GEMV_MAX_M ? n - c : KQ4_GEMV_MAX_M;
+      float *o2[KQ4_MAX_MATS];
+      const float *r2[KQ4_MAX_MATS];
+      for (int i = 0; i < n_mats; ++i) {
+        o2[i] = out[i] + (size_t)c * rows[i];
+        r2[i] = (res && res[i]) ? res[i] + (size_t)c * rows[i] : nullptr;
+      }
+      const float *x2 = x ? x + (size_t)c * cols : nullptr;
+      const float *u2 = xu ? xu + (size_t)c * cols : nullptr;
+      const int8_t *q2 = xq_in ? xq_in + (size_t)c * cols : nullptr;
+      const float *d2 = xd_in ? xd_in + (size_t)c * nb : nullptr;
+      rc = wf ? run_gemv(ds, ws, n_mats, o2, r2, w, rows, cols, x2, nullptr, q2, d2, m,
+                         gchain ? m : 0, s, gchain ? 2 : 1)
+              : run_gemv(ds, ws, n_mats, o2, r2, w, rows, cols, x2, u2, q2, d2, m,
+                         asm_tokens_for(chain, m), s);
+      if (rc) return rc;
+    }
+    return KQ4_OK;
+  }
 
   if (wf) {
     // Q8_0: the VDOT chain (f32 activation scale, fused) or the GEMM chain (f16-rounded scale,

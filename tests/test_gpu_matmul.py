@@ -131,8 +131,9 @@ def test_gemm_bit_exact(kq4, torch_dev, orc, n, chain):
     res = np.random.default_rng(n).standard_normal((n, rows)).astype(np.float32)
     want = orc.matmul(w, x, rows, cols, residual=res, chain=chain)
     out = torch.empty((n, rows), dtype=torch.float32, device="cuda")
-    kq4.matmul_dev(out, to_dev(torch, x), wdev(kq4, torch, w, rows, cols), rows, cols,
-                   residual=to_dev(torch, res), chain=chain)
+    with kq4.options(gemv_chunk_max=8):   # 12 tokens on the GEMM, not two GEMV launches
+        kq4.matmul_dev(out, to_dev(torch, x), wdev(kq4, torch, w, rows, cols), rows, cols,
+                       residual=to_dev(torch, res), chain=chain)
     torch.cuda.synchronize()
     got = host(out)
     main = (n & ~3) if chain == 0 else n
@@ -284,7 +285,7 @@ def test_gemm_split_k(kq4, torch_dev, orc, chain, split):
 # forced: sampled outputs (every 64 x 64 cell, the last token and row, random pairs) within 1e-5
 # of the oracle's single chain, repeat calls bit-identical.
 @pytest.mark.parametrize("form", ["planner", (2, 8), (3, 4), (2, 3)])
-@pytest.mark.parametrize("n,rows,cols,chain", [(16, 1024, 12288, 0), (64, 2048, 6144, 3),
+@pytest.mark.parametrize("n,rows,cols,chain", [(24, 1024, 12288, 0), (64, 2048, 6144, 3),
                                                (100, 4096, 4096, 2), (200, 1000, 8192, 0),
                                                (33, 640, 4096, 3)])
 def test_gemm_small_batch_splits(kq4, torch_dev, orc, n, rows, cols, chain, form):
@@ -393,6 +394,41 @@ def test_q8_gemm_split_k(kq4, torch_dev, orc, split):
     assert e <= TOL
 
 
+# 9-16 tokens: the decode GEMV in launches of 8 tokens (planner option gemv_chunk_max), for
+# every chain, several matrices with residuals, fp32 and pre-quantized activations: the call's
+# outputs are the per-chunk calls' bit for bit (so the AUTO chain puts the same tokens on the ASM
+# scale rounding as the reference's whole-batch dispatch) and within 1e-5 of the oracle.
+@pytest.mark.parametrize("n", [9, 12, 13, 16])
+@pytest.mark.parametrize("chain", [0, 1, 2, 3])
+def test_gemv_chunks(kq4, torch_dev, orc, n, chain):
+    torch = torch_dev
+    rows, cols = [256, 100], 2080
+    ws = [synth.make_q4_weights(r, cols, 1400 + r + n) for r in rows]
+    x = synth.make_activations(n, cols, 1410 + n + chain)
+    res = [synth.make_activations(n, r, 1420 + i) for i, r in enumerate(rows)]
+    W = [wdev(kq4, torch, w, r, cols) for w, r in zip(ws, rows)]
+    X, R = to_dev(torch, x), [to_dev(torch, r) for r in res]
+    outs = [torch.empty((n, r), dtype=torch.float32, device="cuda") for r in rows]
+    kq4.matmul_multi_dev(outs, X, W, rows, cols, residuals=R, chain=chain)
+    parts = [torch.empty_like(o) for o in outs]
+    for c in range(0, n, 8):
+        e = min(n, c + 8)
+        kq4.matmul_multi_dev([p[c:e] for p in parts], X[c:e], W, rows, cols,
+                             residuals=[r[c:e] for r in R], chain=chain)
+    xq, xd = orc.quantize(x, cols)
+    outq = torch.empty((n, rows[0]), dtype=torch.float32, device="cuda")
+    kq4.matmul_q_dev(outq, to_dev(torch, xq), to_dev(torch, xd), W[0], rows[0], cols, n,
+                     residual=R[0], chain=chain)
+    torch.cuda.synchronize()
+    for o, p, w, r, rr in zip(outs, parts, ws, rows, res):
+        got = host(o)
+        assert np.array_equal(got.view(np.uint32), host(p).view(np.uint32))
+        e, a = rel_err(got, orc.matmul(w, x, r, cols, residual=rr, chain=chain))
+        print(f"gemv chunks n={n} chain={chain} rows={r}: rel={e:.3e} maxabs={a:.3e}")
+        assert e <= TOL
+    assert np.array_equal(host(outq).view(np.uint32), host(outs[0]).view(np.uint32))
+
+
 def test_gemm_from_prequantized(kq4, torch_dev, orc):
     torch = torch_dev
     rows, cols, n = 128, 1024, 40
@@ -460,9 +496,9 @@ def test_gemv_plans_multi_matrix(kq4, torch_dev, orc, plan):
 
 # Seeded random shapes across the dense op's whole surface: rows a multiple of 4 (partial row
 # sets and tiles), K a multiple of 32 from one block up (partial stream stages), 1-300 tokens
-# (the decode GEMV up to 8, the prefill GEMM beyond, with the AUTO chain's C-tile tail), every
-# chain, with and without a residual. K stays below the planner's split threshold, so the GEMM's
-# main segment is checked bit for bit; every output within 1e-5.
+# (the decode GEMV up to 16, in launches of 8 beyond 8, the prefill GEMM beyond, with the AUTO
+# chain's C-tile tail), every chain, with and without a residual. K stays below the planner's
+# split threshold, so the GEMM's main segment is checked bit for bit; every output within 1e-5.
 RANDOM_CASES = 32
 
 
@@ -484,7 +520,7 @@ def test_random_shapes(kq4, torch_dev, orc, i):
     got = host(out)
     r, a = rel_err(got, want)
     exact = None
-    if n > 8:
+    if n > kq4.get_option("gemv_chunk_max"):   # on the GEMM
         main = (n & ~3) if chain == 0 else n
         exact = np.array_equal(got[:main].view(np.uint32), want[:main].view(np.uint32))
     print(f"random case {i}: rows={rows} cols={cols} n={n} chain={chain} "

@@ -61,9 +61,9 @@ def test_q8_prepare_and_gemm_from_vqf(kq4, torch_dev, orc, proj, layer):
         W, _, _ = v.prepare_q8_dev(proj, layer)
     torch.cuda.synchronize()
     assert np.array_equal(W.cpu().numpy(), q8_stream_layout(tiles, g, rows, cols))
-    x = synth.make_activations(16, cols, proj + 3 * layer)
+    x = synth.make_activations(24, cols, proj + 3 * layer)   # a GEMM batch (over 16 tokens)
     want = orc.q8_matmul(tiles, x, rows, cols, g=g)
-    out = torch.empty((16, rows), dtype=torch.float32, device="cuda")
+    out = torch.empty((24, rows), dtype=torch.float32, device="cuda")
     kq4.q8_matmul_dev(out, torch.from_numpy(x).cuda(), W, rows, cols)
     torch.cuda.synchronize()
     assert np.array_equal(out.cpu().numpy().view(np.uint32), want.view(np.uint32))
