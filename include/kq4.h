@@ -68,8 +68,9 @@ extern "C" {
  * The prefill GEMM (n_batch > 16; option gemv_chunk_max) replays the selected chain per output
  * bit for bit, except where
  * the planner splits K (launches that leave CUs idle: fewer 128x128 tiles than CUs with K >= 256
- * blocks, or K >= 128 blocks with fewer 64-token tiles than three per CU; never the CTILE chain;
- * option gemm_split): each K slice then runs the chain from zero and the slices' outputs are
+ * blocks, K >= 128 blocks with fewer 64-token tiles than three per CU, or K of 64-127 blocks
+ * with at most one 64x64 tile per two CUs; never the CTILE chain; option gemm_split, 1 keeps
+ * every output the single chain): each K slice then runs the chain from zero and the slices' outputs are
  * added in slice order, within 1e-5 of the single chain. The decode
  * GEMV (n_batch <= 8; 9..16 in launches of 8 tokens; and the GEMM's 1..3-token AUTO tail)
  * takes from the chain only its activation

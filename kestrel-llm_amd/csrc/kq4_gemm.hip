@@ -922,7 +922,10 @@ static int split_len(int nb, int cb, int ksplit) {
 //     KB 768 of 768 workgroups, 145 -> 123 us; at M = 512 and 1024 both fill one round and KA
 //     stays) and in place of the unsplit forms below (gate, K = 4096, M = 64 / 128 / 256: 64 x 64
 //     tiles unsplit 34.6 / 43.3 / 54.3 us, KB 24.7 / 35.4 / 51.2 us; down at M = 32-128 39-44 ->
-//     25-34 us);
+//     25-34 us); for 64-127 blocks (K = 2048-4064) over 64 x 64 tiles only, up to 4 slices of
+//     >= 16 blocks while the tiles are at most one per two CUs (Qwen3-VL-2B QKV 4096 x 2048 at
+//     M = 24: 19.1 -> 12.2 us, O 2048 x 2048 at M = 128: 19.3 -> 13.0 us; the gate, 6144 rows,
+//     at M = 128: 192 tiles, split no faster);
 //   * the pipelined 128 x 64 form for long K (>= 256 blocks) from one tile per CU;
 //   * else 64 x 128 from one tile per CU for K >= 128 blocks (Qwen3-8B gate at M = 320: 74.3 us
 //     as 64 x 64, 59.1 us as 64 x 128), from two per CU for shorter K (Qwen3-VL-2B gate,
@@ -949,9 +952,13 @@ KQ4GemmPlan kq4_gemm_plan(int n_tok, int rows, int cols, int wf, int chain, int 
     return 1;
   };
   const bool ctile = chain == KQ4_CHAIN_CTILE;
-  const int tb = n_tok <= 64 ? 3 : 2;                           // KB's tile
+  const bool shortk = nb >= 64 && nb < 128;
+  const int tb = n_tok <= 64 || shortk ? 3 : 2;                 // KB's tile
   const int ka = !ctile && tiles(1) <= cu && nb >= 256 ? most(tiles(1), 2 * cu, 64) : 1;
-  const int kb = !ctile && nb >= 128 ? most(tiles(tb), 3 * cu, 32) : 1;
+  const int kb = ctile                                ? 1
+                 : nb >= 128                          ? most(tiles(tb), 3 * cu, 32)
+                 : shortk && 2 * tiles(3) <= cu ? most(tiles(3), 2 * cu, 16)
+                                                      : 1;
   // forced slices: 0 / 1 none; counts the blocks do not allow are taken as none
   int fk = force_split;
   if (fk >= 0 && (fk <= 1 || fk > KQ4_GEMM_SPLIT_MAX || !split_len(nb, cb, fk))) fk = 1;

@@ -143,8 +143,9 @@ def test_workspace_trim_frees_outgrown_workspaces(kq4, torch_dev, orc):
     w = synth.make_q4_weights(rows, cols, 31)
     x = synth.make_activations(n, cols, 32)
     out = torch.empty((n, rows), device="cuda")
-    kq4.matmul_dev(out, to_dev(torch, x), kq4.prepare_dev(to_dev(torch, w), rows, cols), rows,
-                   cols)
+    with kq4.options(gemm_split=1):   # the single chain, bit for bit
+        kq4.matmul_dev(out, to_dev(torch, x), kq4.prepare_dev(to_dev(torch, w), rows, cols),
+                       rows, cols)
     torch.cuda.synchronize()
     assert np.array_equal(out.cpu().numpy().view(np.uint32),
                           orc.matmul(w, x, rows, cols).view(np.uint32))

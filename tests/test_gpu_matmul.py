@@ -497,8 +497,9 @@ def test_gemv_plans_multi_matrix(kq4, torch_dev, orc, plan):
 # Seeded random shapes across the dense op's whole surface: rows a multiple of 4 (partial row
 # sets and tiles), K a multiple of 32 from one block up (partial stream stages), 1-300 tokens
 # (the decode GEMV up to 16, in launches of 8 beyond 8, the prefill GEMM beyond, with the AUTO
-# chain's C-tile tail), every chain, with and without a residual. K stays below the planner's
-# split threshold, so the GEMM's main segment is checked bit for bit; every output within 1e-5.
+# chain's C-tile tail), every chain, with and without a residual. Below K = 2048 the planner
+# never splits K, so there the GEMM's main segment is checked bit for bit; every output within
+# 1e-5.
 RANDOM_CASES = 32
 
 
@@ -520,7 +521,7 @@ def test_random_shapes(kq4, torch_dev, orc, i):
     got = host(out)
     r, a = rel_err(got, want)
     exact = None
-    if n > kq4.get_option("gemv_chunk_max"):   # on the GEMM
+    if n > kq4.get_option("gemv_chunk_max") and cols < 2048:   # on the GEMM, K unsplit
         main = (n & ~3) if chain == 0 else n
         exact = np.array_equal(got[:main].view(np.uint32), want[:main].view(np.uint32))
     print(f"random case {i}: rows={rows} cols={cols} n={n} chain={chain} "
