@@ -228,7 +228,8 @@ int kq4_weights_prepare_host(uint8_t *dst, const uint8_t *w4x4_host, int rows, i
 
 /* Q8_0 weights on the device: the q8 stream layout (8704 B per 32-row set and 8-block stage)
  * made once from the reference's tiles (device or host memory), and the matmuls over it
- * (decode GEMV up to 8 tokens, int8-MFMA GEMM beyond). g = 8 or 4 tile rows, rows % g == 0. */
+ * (decode GEMV up to 8 tokens, 9-16 in launches of 8, int8-MFMA GEMM beyond; option
+ * gemv_chunk_max). g = 8 or 4 tile rows, rows % g == 0. */
 size_t kq4_q8_weights_stream_bytes(int rows, int cols);
 int kq4_q8_weights_prepare_dev(uint8_t *dst, const uint8_t *w_tiles, int g, int rows, int cols,
                                void *stream);
