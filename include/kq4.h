@@ -130,6 +130,14 @@ const char *kq4_version(void);
 int kq4_set_option(const char *name, int value);
 /* The option's current value in *value (-1: the planner's choice). */
 int kq4_get_option(const char *name, int *value);
+/* How the current options and planner would run an n_batch-token matmul of rows x cols (q8: Q8_0
+ * weights; chain as for kq4_matmul; ncu: the CUs to plan for, 0 = the current device's):
+ * *tile = 0 and *ksplit = 0 for the decode GEMV (up to gemv_chunk_max tokens), else the prefill
+ * GEMM's tile (1 / 2 / 3 / 4: 128x128 / 64x128 / 64x64 / 128x64 tokens x rows) and its K
+ * slices (1 = unsplit: the single chain, bit for bit). For tests and measurement; no counterpart
+ * in the reference. */
+int kq4_gemm_plan_info(int n_batch, int rows, int cols, int q8, int chain, int ncu, int *tile,
+                       int *ksplit);
 
 /* ---- host-pointer drop-in API (synchronous; 1 = done, 0 = caller falls back) -------------- */
 

@@ -754,6 +754,36 @@ int kq4_get_option(const char *name, int *value) {
   return fail(KQ4_EINVAL, "get_option: unknown option %s", name);
 }
 
+int kq4_gemm_plan_info(int n_batch, int rows, int cols, int q8, int chain, int ncu, int *tile,
+                       int *ksplit) {
+  if (!tile || !ksplit || n_batch < 1 || !shape_ok(rows, cols))
+    return fail(KQ4_EINVAL, "gemm_plan_info: n_batch=%d rows=%d cols=%d", n_batch, rows, cols);
+  if (q8 ? (chain != KQ4_CHAIN_AUTO && chain != KQ4_CHAIN_GEMV32 && chain != KQ4_CHAIN_Q8GEMM)
+         : (chain < KQ4_CHAIN_AUTO || chain > KQ4_CHAIN_ASM))
+    return fail(KQ4_EINVAL, "gemm_plan_info: chain=%d", chain);
+  if (n_batch <= KQ4_GEMV_MAX_M || n_batch <= opt(kGemvChunkMax)) {
+    *tile = *ksplit = 0;
+    return KQ4_OK;
+  }
+  if (ncu <= 0) {
+    DevState *ds = nullptr;
+    int rc = cur_dev(&ds);
+    if (rc) return rc;
+    ncu = ds->ncu;
+  }
+  // the GEMM's operands as matmul_impl forms them: q8 takes one chain for every token; q4's AUTO
+  // runs ASM on the first n & ~3 tokens (the rest on the GEMV)
+  const bool gchain = chain == KQ4_CHAIN_Q8GEMM || (chain == KQ4_CHAIN_AUTO && n_batch >= 2);
+  const int main_n = !q8 && chain == KQ4_CHAIN_AUTO ? (n_batch & ~3) : n_batch;
+  const int mc = q8 ? (gchain ? KQ4_CHAIN_Q8GEMM : KQ4_CHAIN_GEMV32)
+                    : (chain == KQ4_CHAIN_AUTO ? KQ4_CHAIN_ASM : chain);
+  KQ4GemmPlan pl;
+  split_bytes(1, &rows, cols, main_n, q8 ? 1 : 0, mc, ncu, &pl);
+  *tile = pl.tile;
+  *ksplit = pl.ksplit;
+  return KQ4_OK;
+}
+
 int kq4_set_option(const char *name, int value) {
   if (!name) return fail(KQ4_EINVAL, "set_option: null name");
   (void)opt(kGemvKind);   // the environment's values first

@@ -932,8 +932,8 @@ static int split_len(int nb, int cb, int ksplit) {
 //     K = 2048, at M = 384: 30.5 us as 64 x 64, 33.2 us as 64 x 128), else 64 x 64.
 // The C-tile chain (two accumulator sets) takes 64 x 128 at most (at 128 x 128 it spills) and
 // is never split by the planner. The options force a tile and / or a slice count (the planner
-// then picks the other part for it). KB's partial sums stay within 24 MiB: three 64 x 128 tiles
-// per CU are 768 x 8192 outputs.
+// then picks the other part for it). Every planner split keeps its partial sums within
+// KQ4_SPLIT_PART_MAX (24 MiB, what the workspace reserves beyond 8 tokens).
 KQ4GemmPlan kq4_gemm_plan(int n_tok, int rows, int cols, int wf, int chain, int ncu,
                           int force_tile, int force_split) {
   KQ4GemmPlan p{3, 1};
@@ -945,10 +945,13 @@ KQ4GemmPlan kq4_gemm_plan(int n_tok, int rows, int cols, int wf, int chain, int 
     const int bm = t == 1 || t == 4 ? 128 : 64, bn = t == 3 || t == 4 ? 64 : 128;
     return (long)((n_tok + bm - 1) / bm) * ((rows + bn - 1) / bn);
   };
-  // the most slices of >= minb blocks with slices x tiles <= cap
+  // the most slices of >= minb blocks with slices x tiles <= cap whose partial sums fit the
+  // workspace's KQ4_SPLIT_PART_MAX
   auto most = [&](long t, long cap, int minb) {
     for (int k = KQ4_GEMM_SPLIT_MAX; k >= 2; --k)
-      if (k * t <= cap && split_len(nb, cb, k) >= minb) return k;
+      if (k * t <= cap && split_len(nb, cb, k) >= minb &&
+          (long)(k - 1) * n_tok * rows * 4 <= (long)KQ4_SPLIT_PART_MAX)
+        return k;
     return 1;
   };
   const bool ctile = chain == KQ4_CHAIN_CTILE;

@@ -28,6 +28,7 @@ SIGNATURES = [
     ("kq4_version", ctypes.c_char_p, []),
     ("kq4_set_option", _I, [ctypes.c_char_p, _I]),
     ("kq4_get_option", _I, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_int)]),
+    ("kq4_gemm_plan_info", _I, [_I, _I, _I, _I, _I, _I, ctypes.POINTER(_I), ctypes.POINTER(_I)]),
     ("kq4_weights_upload", _I, [_U64, _P, _I, _I]),
     ("kq4_weights_evict", _I, [_U64]),
     ("kq4_weights_clear", _I, []),
@@ -187,6 +188,16 @@ def get_option(name):
     v = ctypes.c_int(0)
     check(lib().kq4_get_option(name.encode(), ctypes.byref(v)), f"kq4_get_option({name})")
     return v.value
+
+
+def gemm_plan(n_batch, rows, cols, q8=False, chain=0, ncu=0):
+    """(tile, K slices) of an n_batch-token matmul under the current options: (0, 0) for the
+    decode GEMV, else the prefill GEMM's tile (1-4 as option gemm_tile) and slices (include/kq4.h
+    kq4_gemm_plan_info; ncu 0 = the current device's CUs)."""
+    t, k = ctypes.c_int(), ctypes.c_int()
+    check(lib().kq4_gemm_plan_info(n_batch, rows, cols, int(q8), chain, ncu, ctypes.byref(t),
+                                   ctypes.byref(k)), "kq4_gemm_plan_info")
+    return t.value, k.value
 
 
 class options:
