@@ -120,10 +120,10 @@ const char *kq4_version(void);
  * default; 1: on fp8 operands; the same outputs), gemm_tile (0: the planner's choice; 1 / 2 / 3 /
  * 4: 128x128 / 64x128 / 64x64 / 128x64 token x row tiles; the same outputs), gemm_split (K slices
  * of the int8 GEMM: 0 or 1 none, every output the single chain bit for bit; 2..8 that many;
- * -1 the planner's choice, the default), gemm_prio (the 128x128 int8 GEMM's issue priority
- * falling with progress through K, so the two workgroups sharing a CU end together: 0 off, 1 on,
- * -1 the planner's choice, on for launches of whole rounds of two workgroups per CU; the same
- * outputs). The initial value
+ * -1 the planner's choice, the default), gemm_prio (the pipelined int8 GEMM's issue priority
+ * falling with progress through K, so the workgroups sharing a CU end together: 0 off, 1 on,
+ * -1 the planner's choice: on for 128x128 launches of whole rounds of two workgroups per CU and
+ * for every 64x128 launch; the same outputs). The initial value
  * of each comes from the environment variable KQ4_ + its upper-case name, else the built-in
  * default (for most, the planner's own choice); value < 0 restores that initial value. Takes
  * effect for launches planned after it returns. */

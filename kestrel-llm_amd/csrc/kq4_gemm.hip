@@ -43,7 +43,7 @@ typedef float kq4_v32f __attribute__((ext_vector_type(32)));
 // row = 8*(v/4) + 4*(lane/32) + v%4 (token).
 KQ4_DEV int kq4_mfma_tok(int v, int half) { return 8 * (v >> 2) + 4 * half + (v & 3); }
 
-// Issue priority by progress through K (q8 = eighths done). Two workgroups share each CU and
+// Issue priority by progress through K (q8 = eighths done). Two (or three) workgroups share each CU and
 // each SIMD's arbiter issues from the oldest wave first, so without this the CU's first
 // workgroup runs at nearly its lone speed, its partner gets the gaps (about half its speed), and
 // once the first ends the partner finishes alone at ~0.7 of the pair's throughput (Qwen3-8B
@@ -52,7 +52,7 @@ KQ4_DEV int kq4_mfma_tok(int v, int half) { return 8 * (v >> 2) + 4 * half + (v 
 // that is behind, so the two end closer together (graph replays, Qwen3-8B: down M = 512, split
 // into 512 workgroups, 104 -> 98.5 us; down M = 2048, 512 workgroups, 330 -> 322 us; gate
 // M = 2048, three rounds, 291 -> 286 us). Results do not depend on it. The launcher turns it on
-// only for whole rounds.
+// for 128 x 128 launches of whole rounds and for every pipelined 64 x 128 launch.
 KQ4_DEV void kq4_prio_by_progress(int q8) {
   if (q8 < 4) __builtin_amdgcn_s_setprio(3);
   else if (q8 < 6) __builtin_amdgcn_s_setprio(2);
@@ -1017,16 +1017,21 @@ int kq4_launch_gemm(float *out, const float *res, const uint8_t *w, const KQ4Gem
   // should end together. With a part round left over it costs time: balanced pairs end together
   // and the rest then runs one workgroup per CU (Qwen3-8B gate, M = 1024: 768 workgroups,
   // 162 -> 167 us with it).
+  // The pipelined 64 x 128 form (three workgroups per CU) gains from it on every launch, whole
+  // rounds or not (Qwen3-8B, graph replays: gate M = 512, one round of 768 workgroups, 80.7 ->
+  // 75.8 us; gate M = 448, 672 workgroups, 77.7 -> 72.0 us; QKV M = 768, 576, 77.5 -> 71.5 us;
+  // the K-split launches at M = 128-768 3-6 %), so it is on there unless the option is 0.
   const long wgs = tiles(128, 128) * ksplit;
   const bool whole = ncu > 0 && wgs % (2L * ncu) == 0;
   const int prio = pick == 1 && (prio_opt == 1 || (prio_opt < 0 && whole));
+  const int prio2 = pick == 2 && chain != KQ4_CHAIN_CTILE && prio_opt != 0;
   hipError_t e;
   if (pick == 1)
     e = gemm_launch<2, 2>(out, ksplit > 1 ? nullptr : res, w, act, rows, n_tok, nb, nst, chain,
                           wf, wbytes, s, ksplit, ks, part, ps, prio);
   else if (pick == 2)
     e = gemm_launch<1, 2>(out, ksplit > 1 ? nullptr : res, w, act, rows, n_tok, nb, nst, chain,
-                          wf, wbytes, s, ksplit, ks, part, ps);
+                          wf, wbytes, s, ksplit, ks, part, ps, prio2);
   else if (pick == 4)
     e = gemm_launch<2, 1>(out, ksplit > 1 ? nullptr : res, w, act, rows, n_tok, nb, nst, chain,
                           wf, wbytes, s, ksplit, ks, part, ps);

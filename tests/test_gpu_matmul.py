@@ -315,13 +315,14 @@ def test_gemm_small_batch_splits(kq4, torch_dev, orc, n, rows, cols, chain, form
     assert e <= TOL
 
 
+@pytest.mark.parametrize("tile", [1, 2])
 @pytest.mark.parametrize("split", [1, 2])
-def test_gemm_prio_same_outputs(kq4, torch_dev, orc, split):
-    """The 128 x 128 GEMM's issue priority by progress through K (planner option gemm_prio: 0
-    off, 1 on, -1 the planner's choice) only reorders the SIMDs' issue between workgroups: the
-    outputs of the three settings are bit-identical, on a small launch (the planner leaves it
-    off; checked against the oracle, bit for bit unsplit, within 1e-5 in 2 K slices) and on a
-    whole round of two workgroups per CU (the planner turns it on)."""
+def test_gemm_prio_same_outputs(kq4, torch_dev, orc, split, tile):
+    """The pipelined GEMM's issue priority by progress through K (planner option gemm_prio: 0
+    off, 1 on, -1 the planner's choice), on the 128 x 128 and 64 x 128 forms, only reorders the
+    SIMDs' issue between workgroups: the outputs of the three settings are bit-identical, on a
+    small launch (128 x 128: the planner leaves it off; checked against the oracle, bit for bit
+    unsplit, within 1e-5 in 2 K slices) and on a whole round of workgroups."""
     torch = torch_dev
     ncu = torch.cuda.get_device_properties(0).multi_processor_count
     cases = [(301, 384, 4096, True), (256, 128 * ncu, 2048, False)]
@@ -332,7 +333,7 @@ def test_gemm_prio_same_outputs(kq4, torch_dev, orc, split):
         got = {}
         for prio in (0, 1, -1):
             out = torch.empty((n, rows), dtype=torch.float32, device="cuda")
-            with kq4.options(gemm_prio=prio, gemm_split=split, gemm_tile=1):
+            with kq4.options(gemm_prio=prio, gemm_split=split, gemm_tile=tile):
                 kq4.matmul_dev(out, X, W, rows, cols, chain=kq4.CHAIN_ASM)
             torch.cuda.synchronize()
             got[prio] = host(out)
@@ -341,7 +342,7 @@ def test_gemm_prio_same_outputs(kq4, torch_dev, orc, split):
         if check:
             want = orc.matmul(w, x, rows, cols, chain=kq4.CHAIN_ASM)
             e, a = rel_err(got[1], want)
-            print(f"prio split={split} n={n} rows={rows}: rel={e:.3e} maxabs={a:.3e}")
+            print(f"prio tile={tile} split={split} n={n} rows={rows}: rel={e:.3e} maxabs={a:.3e}")
             if split == 1:
                 assert np.array_equal(got[1].view(np.uint32), want.view(np.uint32))
             assert e <= TOL
