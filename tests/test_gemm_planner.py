@@ -27,7 +27,8 @@ PLANS = [
     ((12288, 4096), 320, (2, 1)), ((12288, 4096), 512, (2, 1)), ((12288, 4096), 2048, (1, 1)),
     ((4096, 12288), 32, (3, 8)), ((4096, 12288), 128, (2, 8)), ((4096, 12288), 256, (2, 6)),
     ((4096, 12288), 512, (1, 4)), ((4096, 12288), 768, (2, 2)), ((4096, 12288), 1024, (1, 2)),
-    ((4096, 12288), 1536, (4, 1)), ((4096, 12288), 2048, (1, 1)),
+    ((4096, 12288), 1152, (2, 1)), ((4096, 12288), 1536, (2, 1)), ((4096, 12288), 1792, (1, 1)),
+    ((4096, 12288), 2048, (1, 1)),
     ((6144, 4096), 512, (2, 2)),
     ((4096, 2048), 24, (3, 4)), ((4096, 2048), 256, (3, 1)),
     ((6144, 2048), 128, (3, 1)), ((6144, 2048), 768, (2, 1)),
@@ -87,5 +88,5 @@ def test_plan_invariants(kq4, q8):
                     if k > 1:
                         assert split_ok(cols // 32, cb, k), (n, rows, cols, k)
                         assert (k - 1) * main * rows * 4 <= PART_MAX, (n, rows, cols, tile, k)
-    assert {t for t, _ in seen} == {1, 2, 3, 4}
+    assert {t for t, _ in seen} == {1, 2, 3}      # 128 x 64 only when forced
     assert max(k for _, k in seen) == 8

@@ -145,7 +145,8 @@ def test_gemm_bit_exact(kq4, torch_dev, orc, n, chain):
 
 
 # The tile planner takes 128x128 tiles from 2 per CU (n = 2048, 4096 rows: 512 tiles), 64x128
-# below that (2048 rows); the C-tile chain is capped at 64x128. K = 640 (20 blocks) runs five
+# below that (2048 rows; and n = 1152 at K = 8192: 288 tiles of 128x128, one round of 576
+# 64x128 tiles); the C-tile chain is capped at 64x128. K = 640 (20 blocks) runs five
 # 4-block stages with the next stage's registers prefetched, over two stream-layout stages (the
 # second one partial). The oracle is evaluated on sampled outputs: one per 64 x 64 cell (every
 # tile, every XCD's range), the last token and row, and random pairs.
@@ -153,7 +154,8 @@ def test_gemm_bit_exact(kq4, torch_dev, orc, n, chain):
 @pytest.mark.parametrize("n,rows,chain,cols", [(2048, 4096, 0, 640), (2048, 4096, 1, 640),
                                                (2048, 4096, 3, 640), (2048, 2048, 2, 640),
                                                (2048, 2048, 3, 640), (300, 2048, 0, 640),
-                                               (300, 2000, 0, 672), (1000, 4000, 3, 672)])
+                                               (300, 2000, 0, 672), (1000, 4000, 3, 672),
+                                               (1152, 4096, 3, 8192)])
 def test_gemm_large_tiles_bit_exact(kq4, torch_dev, orc, n, rows, chain, cols, kind):
     """Both GEMM forms (planner option gemm_kind: 0 int8 MFMA, 1 fp8 operands; the C-tile chain
     always takes the int8 one) are bit-identical to the oracle, also with an odd block count
