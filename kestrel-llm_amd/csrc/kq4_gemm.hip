@@ -926,10 +926,12 @@ static int split_len(int nb, int cb, int ksplit) {
 //     >= 16 blocks while the tiles are at most one per two CUs (Qwen3-VL-2B QKV 4096 x 2048 at
 //     M = 24: 19.1 -> 12.2 us, O 2048 x 2048 at M = 128: 19.3 -> 13.0 us; the gate, 6144 rows,
 //     at M = 128: 192 tiles, split no faster);
-//   * for long K (>= 256 blocks) between one and two 128 x 128 tiles per CU (too many to split
-//     by KA), 64 x 128 while it fits one round of three per CU, else 128 x 128 (Qwen3-8B down,
-//     µs: M = 1152 / 1280 / 1536 64 x 128 192.9 / 198.8 / 218.0 against 246.6 / 248.3 / 263.8
-//     for the 128 x 64 form this used to take; M = 1792 128 x 128 271.3, 64 x 128 305.4);
+//   * unsplit, K >= 128 blocks and more 128 x 128 tiles than CUs: 64 x 128 (three workgroups
+//     per CU, progress priority) when 0.82 of its rounds is fewer than 128 x 128's rounds of
+//     two per CU, else 128 x 128 (Qwen3-8B, graph replays, 128 x 128 / 64 x 128 µs: gate M = 768
+//     138.5 / 117.9, M = 1536 218.7 / 203.0, M = 2048 264 / 274; QKV M = 1536 139.6 / 119.4;
+//     down M = 1152 / 1536 (64 x 128 one round) 257.9 / 264.5 against 192.9 / 218.0, where the
+//     128 x 64 form this replaced took 246.6 / 263.8; down M = 1792 271.3 / 305.4);
 //   * else 64 x 128 from one tile per CU for K >= 128 blocks (Qwen3-8B gate at M = 320: 74.3 us
 //     as 64 x 64, 59.1 us as 64 x 128), from two per CU for shorter K (Qwen3-VL-2B gate,
 //     K = 2048, at M = 384: 30.5 us as 64 x 64, 33.2 us as 64 x 128), else 64 x 64.
@@ -977,9 +979,12 @@ KQ4GemmPlan kq4_gemm_plan(int n_tok, int rows, int cols, int wf, int chain, int 
     p = KQ4GemmPlan{1, ka};   // KA fills as much of its round as KB
   } else if (fk < 0 && kb > 1 && tiles(1) < 2 * cu) {
     p = KQ4GemmPlan{tb, kb};
+  } else if (nb >= 128 && tiles(1) > cu) {
+    // rounds of each form; a 64 x 128 workgroup takes ~0.82 of a 128 x 128 one's time
+    const long r1 = (tiles(1) + 2 * cu - 1) / (2 * cu), r2 = (tiles(2) + 3 * cu - 1) / (3 * cu);
+    p.tile = 82 * r2 < 100 * r1 ? 2 : 1;
   } else {
     p.tile = tiles(1) >= 2 * cu                            ? 1
-             : nb >= 256 && tiles(1) > cu                  ? (tiles(2) <= 3 * cu ? 2 : 1)
              : tiles(2) >= (nb >= 128 ? cu : 2 * cu) ? 2
                                                            : 3;
   }

@@ -24,7 +24,9 @@ def kq4():
 # 4096 x 2048, gate 6144 x 2048, down 2048 x 6144)
 PLANS = [
     ((12288, 4096), 32, (3, 4)), ((12288, 4096), 128, (2, 4)), ((12288, 4096), 256, (2, 2)),
-    ((12288, 4096), 320, (2, 1)), ((12288, 4096), 512, (2, 1)), ((12288, 4096), 2048, (1, 1)),
+    ((12288, 4096), 320, (2, 1)), ((12288, 4096), 512, (2, 1)), ((12288, 4096), 640, (1, 1)),
+    ((12288, 4096), 768, (2, 1)),
+    ((12288, 4096), 1536, (2, 1)), ((12288, 4096), 2048, (1, 1)), ((6144, 4096), 1536, (2, 1)),
     ((4096, 12288), 32, (3, 8)), ((4096, 12288), 128, (2, 8)), ((4096, 12288), 256, (2, 6)),
     ((4096, 12288), 512, (1, 4)), ((4096, 12288), 768, (2, 2)), ((4096, 12288), 1024, (1, 2)),
     ((4096, 12288), 1152, (2, 1)), ((4096, 12288), 1536, (2, 1)), ((4096, 12288), 1792, (1, 1)),
