@@ -61,6 +61,35 @@ def test_q8_gemm_bit_exact(kq4, torch_dev, orc, rows, cols, g, n, chain):
     assert np.array_equal(out.cpu().numpy().view(np.uint32), want.view(np.uint32))
 
 
+# 9-16 tokens: the q8 GEMV in launches of 8 tokens, the chain chosen for the whole batch (AUTO:
+# the GEMM chain, f16-rounded activation scales, for every token): equal to the explicit
+# per-chunk calls with that chain, bit for bit, and within 1e-5 of the oracle.
+@pytest.mark.parametrize("n", [9, 12, 16])
+@pytest.mark.parametrize("chain", [0, 2, 4])
+def test_q8_gemv_chunks(kq4, torch_dev, orc, n, chain):
+    torch = torch_dev
+    rows, cols, g = 200, 2080, 4
+    w = q8_tiles_synth(rows, cols, g, 1500 + n)
+    x = synth.make_activations(n, cols, 1510 + n + chain)
+    res = synth.make_activations(n, rows, 1520 + n)
+    want = orc.q8_matmul(w, x, rows, cols, residual=res, chain=chain, g=g)
+    W = kq4.q8_prepare_dev(w, rows, cols, g=g)
+    X, R = to_dev(torch, x), to_dev(torch, res)
+    out = torch.empty((n, rows), dtype=torch.float32, device="cuda")
+    kq4.q8_matmul_dev(out, X, W, rows, cols, residual=R, chain=chain)
+    part = torch.empty_like(out)
+    whole = 4 if chain == 0 else chain          # AUTO over the batch: the GEMM chain
+    for c in range(0, n, 8):
+        e = min(n, c + 8)
+        kq4.q8_matmul_dev(part[c:e], X[c:e], W, rows, cols, residual=R[c:e], chain=whole)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), part.cpu().numpy().view(np.uint32))
+    rel, mx = rel_err(got, want)
+    print(f"q8 chunks n={n} chain={chain}: rel={rel:.3e}")
+    assert rel <= TOL, (rel, mx)
+
+
 # 128x128 tiles (2048 tokens x 4096 rows: 512 tiles) and 64x128 (2048 rows); short K keeps the
 # oracle quick; tiles 2 and 4 force the 64x128 and 128x64 forms (planner option gemm_tile)
 @pytest.mark.parametrize("tile", [0, 2, 4])
