@@ -114,9 +114,9 @@ const char *kq4_version(void);
  * reference): gemv_kind (0 v_dot4 / 1 MFMA dots), gemv_mfma_from, gemv_hs (0 whole 32-row sets,
  * 1 halves, 2 quarters per workgroup), gemv_rps (row sets per workgroup, 1..3), gemv_waves,
  * gemv_wpcu, gemv_maxw, gemv_fq (0 / 1: activations quantized by a separate launch / in the
- * GEMV), gemv_fq_work, gemv_silu_fq_work, gemv_chunk_max (the largest batch the decode GEMV
+ * GEMV), gemv_fq_work, gemv_silu_fq_work, gemv_chunk_max (the largest q4 batch the decode GEMV
  * takes, in launches of up to 8 tokens, 16 by default; 8 or less: every batch beyond 8 tokens
- * on the prefill GEMM), gemm_kind (0: the prefill GEMM on int8 MFMA, the
+ * on the prefill GEMM; Q8_0 batches beyond 8 tokens always take the GEMM), gemm_kind (0: the prefill GEMM on int8 MFMA, the
  * default; 1: on fp8 operands; the same outputs), gemm_tile (0: the planner's choice; 1 / 2 / 3 /
  * 4: 128x128 / 64x128 / 64x64 / 128x64 token x row tiles; the same outputs), gemm_split (K slices
  * of the int8 GEMM: 0 or 1 none, every output the single chain bit for bit; 2..8 that many;
@@ -132,7 +132,7 @@ int kq4_set_option(const char *name, int value);
 int kq4_get_option(const char *name, int *value);
 /* How the current options and planner would run an n_batch-token matmul of rows x cols (q8: Q8_0
  * weights; chain as for kq4_matmul; ncu: the CUs to plan for, 0 = the current device's):
- * *tile = 0 and *ksplit = 0 for the decode GEMV (up to gemv_chunk_max tokens), else the prefill
+ * *tile = 0 and *ksplit = 0 for the decode GEMV (up to 8 tokens; q4 up to gemv_chunk_max), else the prefill
  * GEMM's tile (1 / 2 / 3 / 4: 128x128 / 64x128 / 64x64 / 128x64 tokens x rows) and its K
  * slices (1 = unsplit: the single chain, bit for bit). For tests and measurement; no counterpart
  * in the reference. */
@@ -236,8 +236,7 @@ int kq4_weights_prepare_host(uint8_t *dst, const uint8_t *w4x4_host, int rows, i
 
 /* Q8_0 weights on the device: the q8 stream layout (8704 B per 32-row set and 8-block stage)
  * made once from the reference's tiles (device or host memory), and the matmuls over it
- * (decode GEMV up to 8 tokens, 9-16 in launches of 8, int8-MFMA GEMM beyond; option
- * gemv_chunk_max). g = 8 or 4 tile rows, rows % g == 0. */
+ * (decode GEMV up to 8 tokens, int8-MFMA GEMM beyond). g = 8 or 4 tile rows, rows % g == 0. */
 size_t kq4_q8_weights_stream_bytes(int rows, int cols);
 int kq4_q8_weights_prepare_dev(uint8_t *dst, const uint8_t *w_tiles, int g, int rows, int cols,
                                void *stream);

@@ -391,17 +391,17 @@ int matmul_impl(int n_mats, float *const *out, const float *const *res, const ui
   const int nb = cols / 32;
   const size_t qbytes = qa_bytes(n, cols);
 
-  // Up to gemv_chunk_max tokens (16) the decode GEMV takes the batch in launches of 8 tokens,
-  // each reading the weights once more (the later ones mostly from the 256 MB Infinity Cache):
-  // below ~24 tokens the prefill GEMM's per-tile stage chain is latency-bound and slower
+  // q4 weights, up to gemv_chunk_max tokens (16): the decode GEMV takes the batch in launches of
+  // 8 tokens, each reading the weights once more (the later ones mostly from the 256 MB Infinity
+  // Cache): below ~24 tokens the prefill GEMM's per-tile stage chain is latency-bound and slower
   // (graph replay, 16 tokens: Qwen3-VL-2B gate 19.1 -> 13.7 us, O 18.9 -> 9.7 us, Qwen3-8B
   // QKV 17.6 -> 16.1 us; at 24 tokens the GEMM is ahead for all but the 2048 x 2048 O). The
   // chunks start at multiples of 4 tokens, so the AUTO chain puts the same tokens on the ASM
-  // scale rounding as the reference's dispatch over the whole batch (the first n & ~3); q8's
-  // AUTO chain is chosen for the whole batch as well. Outputs as the GEMV's: within 1e-5 of the
-  // reference chain, not bit-identical to it.
-  if (n > KQ4_GEMV_MAX_M && n <= opt(kGemvChunkMax)) {
-    const bool gchain = wf && (chain == KQ4_CHAIN_Q8GEMM || (chain == KQ4_CHAIN_AUTO && n >= 2));
+  // scale rounding as the reference's dispatch over the whole batch (the first n & ~3). Outputs
+  // as the GEMV's: within 1e-5 of the reference chain, not bit-identical to it. Q8_0 weights
+  // stay on the GEMM: their GEMV launches at twice the bytes measured slower (Qwen3-8B gate at
+  // 9-16 tokens 26.8-30.9 against 23.1-23.7 us; down even).
+  if (!wf && n > KQ4_GEMV_MAX_M && n <= opt(kGemvChunkMax)) {
     for (int c = 0; c < n; c += KQ4_GEMV_MAX_M) {
       const int m = n - c < KQ4_GEMV_MAX_M ? n - c : KQ4_GEMV_MAX_M;
       float *o2[KQ4_MAX_MATS];
@@ -414,10 +414,8 @@ int matmul_impl(int n_mats, float *const *out, const float *const *res, const ui
       const float *u2 = xu ? xu + (size_t)c * cols : nullptr;
       const int8_t *q2 = xq_in ? xq_in + (size_t)c * cols : nullptr;
       const float *d2 = xd_in ? xd_in + (size_t)c * nb : nullptr;
-      rc = wf ? run_gemv(ds, ws, n_mats, o2, r2, w, rows, cols, x2, nullptr, q2, d2, m,
-                         gchain ? m : 0, s, gchain ? 2 : 1)
-              : run_gemv(ds, ws, n_mats, o2, r2, w, rows, cols, x2, u2, q2, d2, m,
-                         asm_tokens_for(chain, m), s);
+      rc = run_gemv(ds, ws, n_mats, o2, r2, w, rows, cols, x2, u2, q2, d2, m,
+                    asm_tokens_for(chain, m), s);
       if (rc) return rc;
     }
     return KQ4_OK;
@@ -761,7 +759,7 @@ int kq4_gemm_plan_info(int n_batch, int rows, int cols, int q8, int chain, int n
   if (q8 ? (chain != KQ4_CHAIN_AUTO && chain != KQ4_CHAIN_GEMV32 && chain != KQ4_CHAIN_Q8GEMM)
          : (chain < KQ4_CHAIN_AUTO || chain > KQ4_CHAIN_ASM))
     return fail(KQ4_EINVAL, "gemm_plan_info: chain=%d", chain);
-  if (n_batch <= KQ4_GEMV_MAX_M || n_batch <= opt(kGemvChunkMax)) {
+  if (n_batch <= KQ4_GEMV_MAX_M || (!q8 && n_batch <= opt(kGemvChunkMax))) {
     *tile = *ksplit = 0;
     return KQ4_OK;
   }

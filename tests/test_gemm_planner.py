@@ -50,6 +50,7 @@ def test_small_batches_on_the_gemv(kq4):
     assert kq4.gemm_plan(17, 4096, 12288, ncu=CU) != (0, 0)
     with kq4.options(gemv_chunk_max=8):
         assert kq4.gemm_plan(12, 4096, 12288, chain=kq4.CHAIN_ASM, ncu=CU) == (3, 8)
+    assert kq4.gemm_plan(12, 4096, 12288, q8=True, ncu=CU) != (0, 0)   # Q8_0: the GEMM
 
 
 def test_forced_forms(kq4):

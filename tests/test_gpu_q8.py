@@ -53,41 +53,11 @@ def test_q8_gemm_bit_exact(kq4, torch_dev, orc, rows, cols, g, n, chain):
     want = orc.q8_matmul(w, x, rows, cols, residual=res, chain=chain, g=g)
     W = kq4.q8_prepare_dev(w, rows, cols, g=g)
     out = torch.empty((n, rows), dtype=torch.float32, device="cuda")
-    # 9 tokens on the GEMM (not two GEMV launches), K unsplit: the single chain, bit for bit
-    with kq4.options(gemv_chunk_max=8, gemm_split=1):
+    with kq4.options(gemm_split=1):   # K unsplit: the single chain, bit for bit
         kq4.q8_matmul_dev(out, to_dev(torch, x), W, rows, cols, residual=to_dev(torch, res),
                           chain=chain)
     torch.cuda.synchronize()
     assert np.array_equal(out.cpu().numpy().view(np.uint32), want.view(np.uint32))
-
-
-# 9-16 tokens: the q8 GEMV in launches of 8 tokens, the chain chosen for the whole batch (AUTO:
-# the GEMM chain, f16-rounded activation scales, for every token): equal to the explicit
-# per-chunk calls with that chain, bit for bit, and within 1e-5 of the oracle.
-@pytest.mark.parametrize("n", [9, 12, 16])
-@pytest.mark.parametrize("chain", [0, 2, 4])
-def test_q8_gemv_chunks(kq4, torch_dev, orc, n, chain):
-    torch = torch_dev
-    rows, cols, g = 200, 2080, 4
-    w = q8_tiles_synth(rows, cols, g, 1500 + n)
-    x = synth.make_activations(n, cols, 1510 + n + chain)
-    res = synth.make_activations(n, rows, 1520 + n)
-    want = orc.q8_matmul(w, x, rows, cols, residual=res, chain=chain, g=g)
-    W = kq4.q8_prepare_dev(w, rows, cols, g=g)
-    X, R = to_dev(torch, x), to_dev(torch, res)
-    out = torch.empty((n, rows), dtype=torch.float32, device="cuda")
-    kq4.q8_matmul_dev(out, X, W, rows, cols, residual=R, chain=chain)
-    part = torch.empty_like(out)
-    whole = 4 if chain == 0 else chain          # AUTO over the batch: the GEMM chain
-    for c in range(0, n, 8):
-        e = min(n, c + 8)
-        kq4.q8_matmul_dev(part[c:e], X[c:e], W, rows, cols, residual=R[c:e], chain=whole)
-    torch.cuda.synchronize()
-    got = out.cpu().numpy()
-    assert np.array_equal(got.view(np.uint32), part.cpu().numpy().view(np.uint32))
-    rel, mx = rel_err(got, want)
-    print(f"q8 chunks n={n} chain={chain}: rel={rel:.3e}")
-    assert rel <= TOL, (rel, mx)
 
 
 # 128x128 tiles (2048 tokens x 4096 rows: 512 tiles) and 64x128 (2048 rows); short K keeps the
@@ -152,9 +122,8 @@ def test_q8_multi_and_host_wrappers(kq4, orc):
 
 
 # Seeded random shapes: 4x4 or 8x8 tiles, rows a multiple of the tile, K a multiple of 32 up to
-# 3072 (partial 8-block stages), 1-8 tokens (GEMV, within 1e-5) or 9-300 (GEMM, bit-exact from
-# 17 tokens below K = 2048, where the planner never splits K; 9-16 on the GEMV in launches of 8),
-# chains AUTO / VDOT / GEMM, with a residual.
+# 3072 (partial 8-block stages), 1-8 tokens (GEMV, within 1e-5) or 9-300 (GEMM, bit-exact below
+# K = 2048, where the planner never splits K), chains AUTO / VDOT / GEMM, with a residual.
 @pytest.mark.parametrize("i", range(16))
 def test_q8_random_shapes(kq4, torch_dev, orc, i):
     torch = torch_dev
@@ -176,6 +145,6 @@ def test_q8_random_shapes(kq4, torch_dev, orc, i):
     got = out.cpu().numpy()
     rel, mx = rel_err(got, want)
     print(f"q8 random {i}: g={g} rows={rows} cols={cols} n={n} chain={chain}: rel={rel:.3e}")
-    if n > kq4.get_option("gemv_chunk_max") and cols < 2048:   # on the GEMM, K unsplit
+    if n > 8 and cols < 2048:   # on the GEMM, K unsplit
         assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
     assert rel <= TOL, (rel, mx)
