@@ -6,6 +6,7 @@ import numpy as np
 import pytest
 
 import synth
+from conftest import rel_err
 
 pytestmark = pytest.mark.gpu
 
@@ -185,3 +186,46 @@ def test_graph_split_k_gemm(kq4, torch_dev, orc):
         graph.replay()
         torch.cuda.synchronize()
         assert np.array_equal(out.cpu().numpy().view(np.uint32), want.view(np.uint32)), rep
+
+
+def test_graph_gemv_chunks_and_small_batch_split(kq4, torch_dev, orc):
+    """A 12-token q4 matmul (two 8-token GEMV launches sharing the workspace's quantized
+    activations) and a 40-token one the planner splits over 64 x 64 tiles (K = 4096 in 4 slices,
+    partial sums in the workspace, a reduction launch) captured in one graph: every replay, with
+    eager calls of other shapes on the same workspace between them, reproduces the eager result
+    bit for bit, and both are within 1e-5 of the oracle."""
+    torch = torch_dev
+    rows, cols = 1024, 4096
+    w = synth.make_q4_weights(rows, cols, 51)
+    W = kq4.prepare_dev(to_dev(torch, w), rows, cols)
+    xs = {n: synth.make_activations(n, cols, 52 + n) for n in (12, 40)}
+    X = {n: to_dev(torch, x) for n, x in xs.items()}
+    out = {n: torch.empty((n, rows), device="cuda") for n in xs}
+    assert kq4.gemm_plan(12, rows, cols) == (0, 0)
+    assert kq4.gemm_plan(40, rows, cols, chain=kq4.CHAIN_ASM)[1] > 1
+
+    def work():
+        st = torch.cuda.current_stream()
+        for n in xs:
+            kq4.matmul_dev(out[n], X[n], W, rows, cols, stream=st)
+
+    work()
+    torch.cuda.synchronize()
+    want = {n: out[n].cpu().numpy().copy() for n in xs}
+    for n, x in xs.items():
+        e, _ = rel_err(want[n], orc.matmul(w, x, rows, cols))
+        assert e <= 1e-5, (n, e)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        work()
+    other = torch.empty((300, rows), device="cuda")
+    xo = to_dev(torch, synth.make_activations(300, cols, 59))
+    for rep in range(3):
+        for n in xs:
+            out[n].fill_(float("nan"))
+        kq4.matmul_dev(other, xo, W, rows, cols)   # eager, the same workspace
+        graph.replay()
+        torch.cuda.synchronize()
+        for n in xs:
+            assert np.array_equal(out[n].cpu().numpy().view(np.uint32),
+                                  want[n].view(np.uint32)), (rep, n)
