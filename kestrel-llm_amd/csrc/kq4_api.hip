@@ -190,7 +190,7 @@ const OptDef kOpts[kOptCount] = {
     {"gemv_hs", "KQ4_GEMV_HS", -1},              {"gemv_rps", "KQ4_GEMV_RPS", -1},
     {"gemv_waves", "KQ4_GEMV_WAVES", -1},
     {"gemv_wpcu", "KQ4_GEMV_WPCU", 64},          {"gemv_maxw", "KQ4_GEMV_MAXW", 16},
-    {"gemv_fq", "KQ4_GEMV_FQ", -1},              {"gemv_fq_work", "KQ4_GEMV_FQ_WORK", 45000},
+    {"gemv_fq", "KQ4_GEMV_FQ", -1},              {"gemv_fq_work", "KQ4_GEMV_FQ_WORK", 50000},
     {"gemv_silu_fq_work", "KQ4_GEMV_SILU_FQ_WORK", 15000},
     {"gemv_chunk_max", "KQ4_GEMV_CHUNK_MAX", 16},
     {"gemm_kind", "KQ4_GEMM_KIND", -1},          {"gemm_tile", "KQ4_GEMM_TILE", 0},
@@ -276,15 +276,18 @@ GemvPlan plan_gemv(int n_mats, const int *rows, int nst, int ncu, int n) {
 // a separate quantize launch (about 2 us more per op in a graph). Every workgroup quantizes its
 // K slice of the activation for itself, so a CU spends VALU time on that many elements per
 // workgroup it runs: work = n * (K slice) * ceil(workgroups / CUs). From the sweep above, the
-// in-kernel path is faster up to about 45K such elements at 1-4 tokens and 20K at 5-8 (two
+// in-kernel path is faster up to about 50K such elements at 1-4 tokens and 33K at 5-8 (two
 // quantization passes), always with several sets per workgroup, and with the SiLU product
-// (about 30 more instructions per element) up to about 15K. Option gemv_fq = 0 / 1 forces it
-// off / on; gemv_fq_work and gemv_silu_fq_work set the 1-4-token limits.
+// (about 30 more instructions per element) up to about 15K. (Re-measured with the faster
+// quantizer launch: raising the limits from 45K / 20K moved Qwen3-8B QKV at 5-8 tokens and
+// down at 4, Qwen3-VL-2B gate/up and down at 5 into the kernel, each 0.4-1.6 us faster.)
+// Option gemv_fq = 0 / 1 forces it off / on; gemv_fq_work (the 1-4-token limit; 2/3 of it
+// from 5 tokens) and gemv_silu_fq_work set the limits.
 bool gemv_fq(long work, int n, int rps, bool silu) {
   const int force = opt(kGemvFq);
   if (force == 0 || force == 1) return force;
   if (silu) return work <= opt(kGemvSiluFqWork);
-  return rps > 1 || work <= (n <= 4 ? opt(kGemvFqWork) : opt(kGemvFqWork) * 4 / 9);
+  return rps > 1 || work <= (n <= 4 ? opt(kGemvFqWork) : opt(kGemvFqWork) * 2 / 3);
 }
 
 // Tile and K slices of each matrix's prefill GEMM (kq4_gemm_plan) into pl[], and the workspace
@@ -985,7 +988,10 @@ int kq4_rmsnorm_matmul_multi_dev(int n_mats, float *const *out, const float *con
   // quantizer launch instead (Qwen3-8B QKV from 5 tokens on), the norm kernel writes the codes
   // and saves that launch (M = 8 12.15 -> 10.48 us).
   bool fp32_path = false;
-  if (n_batch <= KQ4_GEMV_MAX_M) {
+  // up to 4 tokens: from 5 the norm kernel's codes measured faster even where the GEMV would
+  // quantize in its own kernel (Qwen3-8B QKV, M = 5 / 6 / 8: 11.1 / 11.1 / 11.1 against
+  // 11.5 / 11.9 / 12.7 us)
+  if (n_batch <= 4) {
     const GemvPlan pl = plan_gemv(n_mats, rows, (cols / 32 + KQ4_STREAM_CB - 1) / KQ4_STREAM_CB,
                                   ds->ncu, n_batch);
     const long per_cu = ((long)pl.groups + ds->ncu - 1) / ds->ncu;
