@@ -134,8 +134,9 @@ int kq4_get_option(const char *name, int *value);
  * weights; chain as for kq4_matmul; ncu: the CUs to plan for, 0 = the current device's):
  * *tile = 0 and *ksplit = 0 for the decode GEMV (up to 8 tokens; q4 up to gemv_chunk_max), else the prefill
  * GEMM's tile (1 / 2 / 3 / 4: 128x128 / 64x128 / 64x64 / 128x64 tokens x rows) and its K
- * slices (1 = unsplit: the single chain, bit for bit). For tests and measurement; no counterpart
- * in the reference. */
+ * slices (1 = unsplit: the single chain, bit for bit); the int8 GEMM's plan (the fp8-operand
+ * form of gemm_kind 1 picks its tile apart and never splits K). For tests and measurement; no
+ * counterpart in the reference. */
 int kq4_gemm_plan_info(int n_batch, int rows, int cols, int q8, int chain, int ncu, int *tile,
                        int *ksplit);
 
