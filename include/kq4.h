@@ -72,7 +72,7 @@ extern "C" {
  * with at most one 64x64 tile per two CUs; never the CTILE chain; option gemm_split, 1 keeps
  * every output the single chain): each K slice then runs the chain from zero and the slices' outputs are
  * added in slice order, within 1e-5 of the single chain. The decode
- * GEMV (n_batch <= 8; 9..16 in launches of 8 tokens; and the GEMM's 1..3-token AUTO tail)
+ * GEMV (n_batch <= 8; q4 9..16 in one 16-token launch; and the GEMM's 1..3-token AUTO tail)
  * takes from the chain only its activation
  * scale (f16-rounded for ASM tokens, f32 otherwise): it splits K over waves and sums each
  * wave's terms in block order (one token: a lo and a hi chain per half block, as CTILE; two or
@@ -115,7 +115,7 @@ const char *kq4_version(void);
  * 1 halves, 2 quarters per workgroup), gemv_rps (row sets per workgroup, 1..3), gemv_waves,
  * gemv_wpcu, gemv_maxw, gemv_fq (0 / 1: activations quantized by a separate launch / in the
  * GEMV), gemv_fq_work, gemv_silu_fq_work, gemv_chunk_max (the largest q4 batch the decode GEMV
- * takes, in launches of up to 8 tokens, 16 by default; 8 or less: every batch beyond 8 tokens
+ * takes, 9..16 tokens in one launch of its 16-token kernel, 16 by default; 8 or less: every batch beyond 8 tokens
  * on the prefill GEMM; Q8_0 batches beyond 8 tokens always take the GEMM), gemm_kind (0: the prefill GEMM on int8 MFMA, the
  * default; 1: on fp8 operands; the same outputs), gemm_tile (0: the planner's choice; 1 / 2 / 3 /
  * 4: 128x128 / 64x128 / 64x64 / 128x64 token x row tiles; the same outputs), gemm_split (K slices

@@ -219,6 +219,12 @@ int asm_tokens_for(int chain, int n) {
 // Integer-dot kind of the GEMV: per-lane v_dot4 for one token, v_mfma from two tokens on (the
 // dot4 work grows with M, the MFMA's does not; at one token both measure the same).
 // Option gemv_kind = 0/1 forces one (for measurement).
+// Most q4 tokens the GEMV takes (its 16-token kernel from 9 on): option gemv_chunk_max, at most 16.
+int gemv_q4_max() {
+  const int c = opt(kGemvChunkMax);
+  return c < KQ4_GEMV_WIDE_M ? c : KQ4_GEMV_WIDE_M;
+}
+
 int gemv_kind(int n) {
   const int force = opt(kGemvKind);
   if (force == 1 || (force == 0 && n <= KQ4_GEMV_DOT4_MAX_M)) return force;
@@ -260,11 +266,17 @@ GemvPlan plan_gemv(int n_mats, const int *rows, int nst, int ncu, int n) {
           : n >= 4 && sets >= 2 * ncu                 ? 3
                                                       : 1;
   if (p.hs) p.rps = 1;
+  if (n > KQ4_GEMV_MAX_M) {   // the 16-token kernel: single whole or half sets
+    p.hs = p.hs > 1 ? 1 : p.hs;
+    p.rps = 1;
+  }
   p.groups = 0;
   for (int i = 0; i < n_mats; ++i) p.groups += ((rows[i] + 31) / 32 + p.rps - 1) / p.rps << p.hs;
   const int wgs = p.groups;
   int want = force_w > 0 ? force_w : (per_cu * ncu + wgs - 1) / wgs;
-  const int mw = p.rps > 1 && max_w > KQ4_GEMV_RPS_MAX_WAVES ? KQ4_GEMV_RPS_MAX_WAVES : max_w;
+  int mw = p.rps > 1 && max_w > KQ4_GEMV_RPS_MAX_WAVES ? KQ4_GEMV_RPS_MAX_WAVES : max_w;
+  const int lds_w = (160 * 1024 - 64) / kq4_gemv_slab_bytes(n);   // slabs that fit a CU's LDS
+  mw = mw < lds_w ? mw : lds_w;
   const int cap = nst < mw ? nst : mw;
   want = want < 1 ? 1 : (want > cap ? cap : want);
   const int spw = (nst + want - 1) / want;   // stages per wave
@@ -306,8 +318,9 @@ size_t split_bytes(int n_mats, const int *rows, int cols, int n, int wf, int cha
   return al256(mx);
 }
 
-// GEMV over n_mats matrices for n tokens (n <= 8): from fp32 x (quantized in the kernel or by a
-// separate launch; with xu the activation is silu_mul(x, xu)) or from token-major xq/xd.
+// GEMV over n_mats matrices for n tokens (n <= 8; q4 up to 16 in the 16-token kernel): from fp32
+// x (quantized in the kernel or by a separate launch; with xu the activation is
+// silu_mul(x, xu), quantized apart beyond 8 tokens) or from token-major xq/xd.
 int run_gemv(DevState *ds, const Ws &wsp, int n_mats, float *const *out, const float *const *res,
              const uint8_t *const *w, const int *rows, int cols, const float *x, const float *xu,
              const int8_t *xq, const float *xd, int n, int asm_tokens, hipStream_t s,
@@ -330,6 +343,7 @@ int run_gemv(DevState *ds, const Ws &wsp, int n_mats, float *const *out, const f
     // 32K / 49K elements: 16.3 / 14.6 us in the kernel against 15.4 / 14.3 us with the quantizer
     // launch; at M = 2 the kernel form 13.3 / 12.6 against 14.9 / 14.0 us)
     fq = gemv_fq(per_cu * n * cols * (wf ? 5 : 3) / 3, n, pl.rps, xu != nullptr);
+    if (n > KQ4_GEMV_MAX_M && xu) fq = false;   // the 16-token kernel quantizes plain x only
   }
   const size_t qbytes = x && !fq ? qa_bytes(n, cols) : 0;
   if (qbytes && (rc = ensure_ws(wsp, qbytes, s))) return rc;
@@ -354,6 +368,7 @@ int run_gemv(DevState *ds, const Ws &wsp, int n_mats, float *const *out, const f
   a.nb = nb;
   a.wf = wf;
   a.nw = pl.nw;
+  a.ntok = n;
   int g = 0;
   for (int i = 0; i < n_mats; ++i) {
     KQ4GemvMat &m = a.mat[i];
@@ -398,35 +413,16 @@ int matmul_impl(int n_mats, float *const *out, const float *const *res, const ui
   const int nb = cols / 32;
   const size_t qbytes = qa_bytes(n, cols);
 
-  // q4 weights, up to gemv_chunk_max tokens (16): the decode GEMV takes the batch in launches of
-  // 8 tokens, each reading the weights once more (the later ones mostly from the 256 MB Infinity
-  // Cache): below ~24 tokens the prefill GEMM's per-tile stage chain is latency-bound and slower
-  // (graph replay, 16 tokens: Qwen3-VL-2B gate 19.1 -> 13.7 us, O 18.9 -> 9.7 us, Qwen3-8B
-  // QKV 17.6 -> 16.1 us; at 24 tokens the GEMM is ahead for all but the 2048 x 2048 O). The
-  // chunks start at multiples of 4 tokens, so the AUTO chain puts the same tokens on the ASM
-  // scale rounding as the reference's dispatch over the whole batch (the first n & ~3). Outputs
-  // as the GEMV's: within 1e-5 of the reference chain, not bit-identical to it. Q8_0 weights
-  // stay on the GEMM: their GEMV launches at twice the bytes measured slower (Qwen3-8B gate at
-  // 9-16 tokens 26.8-30.9 against 23.1-23.7 us; down even).
-  if (!wf && n > KQ4_GEMV_MAX_M && n <= opt(kGemvChunkMax)) {
-    for (int c = 0; c < n; c += KQ4_GEMV_MAX_M) {
-      const int m = n - c < KQ4_GEMV_MAX_M ? n - c : KQ4_GEMV_MAX_M;
-      float *o2[KQ4_MAX_MATS];
-      const float *r2[KQ4_MAX_MATS];
-      for (int i = 0; i < n_mats; ++i) {
-        o2[i] = out[i] + (size_t)c * rows[i];
-        r2[i] = (res && res[i]) ? res[i] + (size_t)c * rows[i] : nullptr;
-      }
-      const float *x2 = x ? x + (size_t)c * cols : nullptr;
-      const float *u2 = xu ? xu + (size_t)c * cols : nullptr;
-      const int8_t *q2 = xq_in ? xq_in + (size_t)c * cols : nullptr;
-      const float *d2 = xd_in ? xd_in + (size_t)c * nb : nullptr;
-      rc = run_gemv(ds, ws, n_mats, o2, r2, w, rows, cols, x2, u2, q2, d2, m,
-                    asm_tokens_for(chain, m), s);
-      if (rc) return rc;
-    }
-    return KQ4_OK;
-  }
+  // q4 weights, 9 to gemv_chunk_max tokens (16): the decode GEMV's 16-token kernel, one launch
+  // that reads the weights once (the rows past n padding): below ~24 tokens the prefill GEMM's
+  // per-tile stage chain is latency-bound and slower. Its int8 work is the MFMA's 32 rows
+  // either way, so 16 tokens cost about what 8 do. The AUTO chain puts the first n & ~3 tokens on
+  // the ASM scale rounding, as the reference's dispatch over the whole batch does. Outputs as the
+  // GEMV's: within 1e-5 of the reference chain, not bit-identical to it. Q8_0 weights stay on the
+  // GEMM (their 8-token GEMV launches at twice the bytes measured slower there).
+  if (!wf && n > KQ4_GEMV_MAX_M && n <= gemv_q4_max())
+    return run_gemv(ds, ws, n_mats, out, res, w, rows, cols, x, xu, xq_in, xd_in, n,
+                    asm_tokens_for(chain, n), s);
 
   if (wf) {
     // Q8_0: the VDOT chain (f32 activation scale, fused) or the GEMM chain (f16-rounded scale,
@@ -766,7 +762,7 @@ int kq4_gemm_plan_info(int n_batch, int rows, int cols, int q8, int chain, int n
   if (q8 ? (chain != KQ4_CHAIN_AUTO && chain != KQ4_CHAIN_GEMV32 && chain != KQ4_CHAIN_Q8GEMM)
          : (chain < KQ4_CHAIN_AUTO || chain > KQ4_CHAIN_ASM))
     return fail(KQ4_EINVAL, "gemm_plan_info: chain=%d", chain);
-  if (n_batch <= KQ4_GEMV_MAX_M || (!q8 && n_batch <= opt(kGemvChunkMax))) {
+  if (n_batch <= KQ4_GEMV_MAX_M || (!q8 && n_batch <= gemv_q4_max())) {
     *tile = *ksplit = 0;
     return KQ4_OK;
   }

@@ -65,8 +65,12 @@ typedef int kq4_v16i __attribute__((ext_vector_type(16)));
 // LDS bytes of one wave's slab: [activation codes][scales]; it also holds the wave's partial
 // sums at the end (at most 8 tokens x 32 floats).
 template <int M>
+constexpr int kq4_gv_mx() {   // scale row width of the slab: 8 tokens, 16 in the wide kernel
+  return M > 8 ? 16 : 8;
+}
+template <int M>
 constexpr int kq4_gv_slab() {
-  return M * KQ4_GV_QTS + KQ4_GV_XS;
+  return M * KQ4_GV_QTS + KQ4_GV_CB * kq4_gv_mx<M>() * 4;
 }
 
 // Byte offset of block blk's 32 codes in a token row: block pairs at an 80-B pitch (16-B pad),
@@ -236,18 +240,19 @@ struct KQ4GvAct {
 
 // M = tokens of this pass; the in-kernel quantization (FQ) takes the tokens in passes of up to
 // kq4_gv_mq<> tokens from token t0 on (registers), the pre-quantized copy all of them at t0 = 0.
-template <int M, int FQ, int WF>
+template <int M, int FQ, int WF, bool WIDE = false>
 KQ4_DEV void kq4_gv_act_load(KQ4GvAct<M, FQ, WF> &r, const KQ4GemvArgs &a, int st, int lane,
                              int t0) {
   constexpr int CB = KQ4Wf<WF>::CB;
   const int nb = a.nb, cols = a.cols;
   const int kb = st * CB;
+  const int mlim = WIDE ? a.ntok - t0 : M;   // the wide kernel's padding tokens read nothing
   if (FQ) {
     const int b = kb + (lane >> 2), qq = lane & 3;
     const bool live = (lane >> 2) < CB && b < nb;
 #pragma unroll
     for (int m = 0; m < M; ++m) {
-      if (live) {
+      if (live && m < mlim) {
         const float4 *src = reinterpret_cast<const float4 *>(a.xf + (size_t)(t0 + m) * cols +
                                                              (size_t)b * 32 + 8 * qq);
         r.f[2 * m] = src[0];
@@ -273,21 +278,21 @@ KQ4_DEV void kq4_gv_act_load(KQ4GvAct<M, FQ, WF> &r, const KQ4GemvArgs &a, int s
       const int i = lane + 64 * c;
       const int m = i / (2 * CB), u = i % (2 * CB), b = kb + (u >> 1), hh = u & 1;
       r.q[c] = make_uint4(0, 0, 0, 0);
-      if (m < M && b < nb)
+      if (m < M && m < mlim && b < nb)
         r.q[c] = *reinterpret_cast<const uint4 *>(a.xq + (size_t)m * cols + (size_t)b * 32 + 16 * hh);
     }
 #pragma unroll
     for (int c = 0; c < KQ4GvAct<M, FQ, WF>::NX; ++c) {
       const int i = lane + 64 * c;
       const int m = i / CB, b = kb + i % CB;
-      r.x[c] = (m < M && b < nb) ? a.xd[(size_t)m * nb + b] : 0.0f;
+      r.x[c] = (m < M && m < mlim && b < nb) ? a.xd[(size_t)m * nb + b] : 0.0f;
     }
   }
 }
 
-template <int M, int FQ, int WF>
+template <int M, int FQ, int WF, int MX = 8>
 KQ4_DEV void kq4_gv_act_put(const KQ4GvAct<M, FQ, WF> &r, const KQ4GemvArgs &a, int lane,
-                            uint8_t *sq, float (*sx)[8], int t0) {
+                            uint8_t *sq, float (*sx)[MX], int t0) {
   constexpr int CB = KQ4Wf<WF>::CB;
   constexpr float XS = KQ4Wf<WF>::XS;
   if constexpr (FQ != 0) {
@@ -414,10 +419,11 @@ KQ4_DEV void kq4_gv_dot4(const KQ4GvStage<HS> &st, const uint8_t *sq, const floa
 // min(lane % NR, M-1) for the lane's own block, so output (token row T, column c) is valid where
 // T's block matches c's: T = token + NR*p, which the 32x32 output layout puts in result register
 // (NR/2)*p + v for token 4h+v. acc[v] = token 4h+v of the lane's row (and parity).
-template <int M, int HS, int WF>
-KQ4_DEV void kq4_gv_mfma_stage(const KQ4GvStage<HS> &st, const uint8_t *sq, const float (*sx)[8],
+template <int M, int HS, int WF, int MX = 8>
+KQ4_DEV void kq4_gv_mfma_stage(const KQ4GvStage<HS> &st, const uint8_t *sq, const float (*sx)[MX],
                                int lane, int p, float *acc) {
   constexpr int VT = M < 4 ? M : 4;
+  constexpr int NG = M > 8 ? 2 : 1;   // token groups 0-7, 8-15 (result registers 4j + v)
   const int h = lane >> 5;
   constexpr int NR = 32 >> HS;
   const int tr = lane & (NR - 1);
@@ -432,17 +438,21 @@ KQ4_DEV void kq4_gv_mfma_stage(const KQ4GvStage<HS> &st, const uint8_t *sq, cons
     const kq4_v4i A = *reinterpret_cast<const kq4_v4i *>(qb + kq4_gv_qpos(b));
     const kq4_v16i C = kq4_gv_mfma(A, B);
     const float wd = kq4_gv_wd<HS, WF>(st, jb, p);
-    const float4 xs = *reinterpret_cast<const float4 *>(&sx[b][4 * h]);
-    const float xv[4] = {xs.x, xs.y, xs.z, xs.w};
 #pragma unroll
-    for (int v = 0; v < VT; ++v) {
-      uint32_t cv[1 << HS];
+    for (int j = 0; j < NG; ++j) {
+      const float4 xs = *reinterpret_cast<const float4 *>(&sx[b][8 * j + 4 * h]);
+      const float xv[4] = {xs.x, xs.y, xs.z, xs.w};
 #pragma unroll
-      for (int pp = 0; pp < (1 << HS); ++pp) cv[pp] = (uint32_t)C[(NR / 2) * pp + v];
-      const int c = (int)kq4_gv_pickn<HS>(cv, p);
-      if (WF == 2) acc[v] = acc[v] + (wd * xv[v]) * (float)c;   // the q8 GEMM chain, unfused
-      else acc[v] = fmaf((float)c, wd * xv[v], acc[v]);
-      kq4_gv_pin(acc[v]);
+      for (int v = 0; v < VT; ++v) {
+        uint32_t cv[1 << HS];
+#pragma unroll
+        for (int pp = 0; pp < (1 << HS); ++pp) cv[pp] = (uint32_t)C[(NR / 2) * pp + 4 * j + v];
+        const int c = (int)kq4_gv_pickn<HS>(cv, p);
+        float &ac = acc[4 * j + v];
+        if (WF == 2) ac = ac + (wd * xv[v]) * (float)c;   // the q8 GEMM chain, unfused
+        else ac = fmaf((float)c, wd * xv[v], ac);
+        kq4_gv_pin(ac);
+      }
     }
   }
 }
@@ -507,13 +517,17 @@ template <int M, int FQ, int KIND, int HS, int WF, int R>
 __global__ __launch_bounds__(R > 1 ? 512 : 1024) void kq4_gemv_kernel(const KQ4GemvArgs a) {
   extern __shared__ __align__(16) uint8_t kq4_gv_lds[];
   constexpr int SLAB = kq4_gv_slab<M>();
-  constexpr int NACC = KIND == 0 ? M : 4;
+  constexpr int MX = kq4_gv_mx<M>();               // scale row width of the slab
+  constexpr bool WIDE = M > 8;                     // 16-token kernel: a.ntok tokens, the rest padding
+  constexpr int NACC = KIND == 0 ? M : (WIDE ? 8 : 4);
   constexpr int NR = 32 >> HS;                     // output rows per row set of the workgroup
   constexpr int NP = 1 << HS;                      // lane parities
   constexpr int MQ = kq4_gv_mq<M, FQ>();           // tokens per quantization pass
   constexpr int MT = M % MQ;                       // tokens of the last, shorter pass
   constexpr int NOUT = R * M * NR;                 // outputs of the workgroup
   static_assert(R == 1 || HS == 0, "several row sets per workgroup take whole sets");
+  static_assert(!WIDE || (KIND == 1 && R == 1 && HS <= 1 && M == 16),
+                "16 tokens: MFMA kind, single full or half sets (A rows 16p + token)");
   static_assert(NOUT * 4 <= SLAB, "a wave's partials fit its slab");
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -531,7 +545,7 @@ __global__ __launch_bounds__(R > 1 ? 512 : 1024) void kq4_gemv_kernel(const KQ4G
   const uint8_t *__restrict__ wb = (const uint8_t *)ms.w;
   uint8_t *slab = kq4_gv_lds + wave * SLAB;
   uint8_t *sq = slab;
-  float (*sx)[8] = reinterpret_cast<float (*)[8]>(sq + M * KQ4_GV_QTS);
+  float (*sx)[MX] = reinterpret_cast<float (*)[MX]>(sq + M * KQ4_GV_QTS);
   const int h = lane >> 5;
   const int p = (lane >> (5 - HS)) & (NP - 1);
   const int r = lane & (NR - 1);                   // row within the set part
@@ -546,7 +560,7 @@ __global__ __launch_bounds__(R > 1 ? 512 : 1024) void kq4_gemv_kernel(const KQ4G
     // issued as (activations, weights), so quantizing the activations waits only for them
     KQ4GvAct<MQ, FQ, WF> ra;
     KQ4GvStage<HS> rw[R > 1 ? 2 : 1];
-    kq4_gv_act_load<MQ, FQ, WF>(ra, a, st, lane, 0);
+    kq4_gv_act_load<MQ, FQ, WF, WIDE>(ra, a, st, lane, 0);
     kq4_gv_load<HS, WF, kq4_gv_ord<M, FQ>()>(rw[0], wb + ((size_t)set0 * nst + st) * CHUNK, rr,
                                              h, p);
     // One token, fp32 activations: every load is issued before the quantization waits for the
@@ -556,11 +570,13 @@ __global__ __launch_bounds__(R > 1 ? 512 : 1024) void kq4_gemv_kernel(const KQ4G
     // measured slower for every Qwen3-8B decode shape (8B gate/up at 2 tokens 12.15 -> 13.0 us),
     // faster only for the 2B QKV and O launches (one workgroup per CU: 4.7 -> 4.1 us at 4 tokens).
     if constexpr (M == 1 && FQ == 1) __builtin_amdgcn_sched_barrier(0);
-    kq4_gv_act_put<MQ, FQ, WF>(ra, a, lane, sq, sx, 0);
+    kq4_gv_act_put<MQ, FQ, WF, MX>(ra, a, lane, sq, sx, 0);
 #pragma unroll
     for (int t0 = MQ; t0 + MQ <= M; t0 += MQ) {
-      kq4_gv_act_load<MQ, FQ, WF>(ra, a, st, lane, t0);
-      kq4_gv_act_put<MQ, FQ, WF>(ra, a, lane, sq, sx, t0);
+      if (WIDE && t0 >= a.ntok) break;   // passes of padding tokens only: their outputs are not
+                                         // stored, so their stale slab rows are never read back
+      kq4_gv_act_load<MQ, FQ, WF, WIDE>(ra, a, st, lane, t0);
+      kq4_gv_act_put<MQ, FQ, WF, MX>(ra, a, lane, sq, sx, t0);
     }
     if constexpr (MT > 0) {
       KQ4GvAct<MT, FQ, WF> rt;
@@ -577,7 +593,8 @@ __global__ __launch_bounds__(R > 1 ? 512 : 1024) void kq4_gemv_kernel(const KQ4G
         kq4_gv_load<HS, WF>(rw[(q + 1) & 1], wb + ((size_t)sn * nst + st) * CHUNK, rr, h, p);
       }
       if (q == 0 || set0 + q < sets) {
-        if (KIND == 0) kq4_gv_dot4<M, HS>(rw[q & 1], sq, sx, h, p, acc[q]);
+        if constexpr (WIDE) kq4_gv_mfma_stage<M, HS, WF, MX>(rw[q & 1], sq, sx, lane, p, acc[q]);
+        else if (KIND == 0) kq4_gv_dot4<M, HS>(rw[q & 1], sq, sx, h, p, acc[q]);
         else kq4_gv_mfma_stage<M, HS, WF>(rw[q & 1], sq, sx, lane, p, acc[q]);
       }
     }
@@ -602,11 +619,12 @@ __global__ __launch_bounds__(R > 1 ? 512 : 1024) void kq4_gemv_kernel(const KQ4G
       }
     } else {
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
+      for (int v = 0; v < NACC; ++v) {   // register v: token 8 * (v / 4) + 4h + v % 4
         float t = acc[q][v];
         if (HS == 2) t = kq4_xor_add<8>(t);
         if (HS >= 1) t = kq4_xor_add<16>(t);
-        if (p == 0 && 4 * h + v < M) red[(q * M + 4 * h + v) * NR + r] = t;
+        const int tk = 8 * (v >> 2) + 4 * h + (v & 3);
+        if (p == 0 && tk < M) red[(q * M + tk) * NR + r] = t;
       }
     }
   }
@@ -618,15 +636,17 @@ __global__ __launch_bounds__(R > 1 ? 512 : 1024) void kq4_gemv_kernel(const KQ4G
   };
   // the first pass's residual is loaded before the barrier, so its latency hides behind the
   // wait (measured: 2B down and O with residual 0.04-0.08 us faster per launch at one token)
+  const int mstore = WIDE ? a.ntok : M;            // tokens whose outputs are stored
   float res0 = 0.0f;
   {
     const int i = threadIdx.x, row = out_row(i);
-    if (res && i < NOUT && row < rows) res0 = res[(size_t)((i / NR) % M) * rows + row];
+    if (res && i < NOUT && row < rows && (i / NR) % M < mstore)
+      res0 = res[(size_t)((i / NR) % M) * rows + row];
   }
   __syncthreads();
   for (int i = threadIdx.x; i < NOUT; i += 64 * nw) {
     const int row = out_row(i);
-    if (row >= rows) continue;
+    if (row >= rows || (i / NR) % M >= mstore) continue;
     const float s = wave_sum(i);
     const size_t o = (size_t)((i / NR) % M) * rows + row;
     out[o] = res ? (i == (int)threadIdx.x ? res0 : res[o]) + s : s;

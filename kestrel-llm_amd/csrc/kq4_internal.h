@@ -22,6 +22,7 @@ inline hipError_t kq4_lds_limit_once(const void *fn, int bytes,
 }
 
 #define KQ4_GEMV_MAX_M 8
+#define KQ4_GEMV_WIDE_M 16   // q4 batches of 9-16 tokens: one launch of the 16-token kernel
 #define KQ4_MAXMAT 4
 
 // Every kernel reads q4 weights in the stream layout (kq4_common.h): a VQF 4x4 matrix repacked
@@ -56,6 +57,7 @@ struct KQ4GemvArgs {
   int cols;
   int nb;
   int nw;               // waves per workgroup
+  int ntok;             // tokens of the 16-token kernel (9-16; the rows past it are padding)
 };
 
 // up != nullptr: quantizes silu_mul(x, up) instead of x (the dense FFN's down input).

@@ -189,8 +189,8 @@ def test_graph_split_k_gemm(kq4, torch_dev, orc):
 
 
 def test_graph_gemv_chunks_and_small_batch_split(kq4, torch_dev, orc):
-    """A 12-token q4 matmul (two 8-token GEMV launches sharing the workspace's quantized
-    activations) and a 40-token one the planner splits over 64 x 64 tiles (K = 4096 in 4 slices,
+    """A 12-token q4 matmul (one launch of the 16-token GEMV kernel) and a 40-token one the
+    planner splits over 64 x 64 tiles (K = 4096 in 4 slices,
     partial sums in the workspace, a reduction launch) captured in one graph: every replay, with
     eager calls of other shapes on the same workspace between them, reproduces the eager result
     bit for bit, and both are within 1e-5 of the oracle."""
