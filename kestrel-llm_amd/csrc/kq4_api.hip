@@ -266,10 +266,7 @@ GemvPlan plan_gemv(int n_mats, const int *rows, int nst, int ncu, int n) {
           : n >= 4 && sets >= 2 * ncu                 ? 3
                                                       : 1;
   if (p.hs) p.rps = 1;
-  if (n > KQ4_GEMV_MAX_M) {   // the 16-token kernel: single whole or half sets
-    p.hs = p.hs > 1 ? 1 : p.hs;
-    p.rps = 1;
-  }
+  if (n > KQ4_GEMV_MAX_M && p.hs > 1) p.hs = 1;   // the 16-token kernel: whole or half sets
   p.groups = 0;
   for (int i = 0; i < n_mats; ++i) p.groups += ((rows[i] + 31) / 32 + p.rps - 1) / p.rps << p.hs;
   const int wgs = p.groups;

@@ -14,7 +14,8 @@ extern template hipError_t kq4_gv_launch_m<5>(const KQ4GemvArgs &, int, int, int
 extern template hipError_t kq4_gv_launch_m<6>(const KQ4GemvArgs &, int, int, int, int, int, hipStream_t);
 extern template hipError_t kq4_gv_launch_m<7>(const KQ4GemvArgs &, int, int, int, int, int, hipStream_t);
 extern template hipError_t kq4_gv_launch_m<8>(const KQ4GemvArgs &, int, int, int, int, int, hipStream_t);
-hipError_t kq4_gv_launch_wide(const KQ4GemvArgs &a, int fq, int hs, int grid, hipStream_t s);
+hipError_t kq4_gv_launch_wide(const KQ4GemvArgs &a, int fq, int hs, int rps, int grid,
+                              hipStream_t s);
 
 // a wave's LDS slab: the 16-token kernel (9-16 tokens) holds 16 token rows and 16-wide scales
 int kq4_gemv_slab_bytes(int n_batch) {
@@ -26,7 +27,7 @@ int kq4_launch_gemv(const KQ4GemvArgs &a, int n_batch, int kind, int half_sets, 
   const int nw = a.nw;
   const bool wide = n_batch > KQ4_GEMV_MAX_M;   // the 16-token kernel: q4, MFMA, single sets
   if (wide && (n_batch > KQ4_GEMV_WIDE_M || a.ntok != n_batch || a.wf || kind != 1 ||
-               half_sets > 1 || rps != 1 || (a.xu != nullptr)))
+               half_sets > 1 || (a.xu != nullptr)))
     return (int)hipErrorInvalidValue;
   if (n_batch < 1 || n_batch > KQ4_GEMV_WIDE_M || grid <= 0 || nw < 1 || nw > 16 || kind < 0 ||
       kind > 1 || (kind == 0 && n_batch > KQ4_GEMV_DOT4_MAX_M) || half_sets < 0 ||
@@ -40,7 +41,7 @@ int kq4_launch_gemv(const KQ4GemvArgs &a, int n_batch, int kind, int half_sets, 
   const int fq = a.xf ? (a.xu ? 2 : 1) : 0;
   const int hs = half_sets;
   hipError_t e;
-  if (wide) return (int)kq4_gv_launch_wide(a, fq, hs, grid, s);
+  if (wide) return (int)kq4_gv_launch_wide(a, fq, hs, rps, grid, s);
   switch (n_batch) {
     case 1: e = kq4_gv_launch_m<1>(a, kind, fq, hs, rps, grid, s); break;
     case 2: e = kq4_gv_launch_m<2>(a, kind, fq, hs, rps, grid, s); break;

@@ -526,8 +526,8 @@ __global__ __launch_bounds__(R > 1 ? 512 : 1024) void kq4_gemv_kernel(const KQ4G
   constexpr int MT = M % MQ;                       // tokens of the last, shorter pass
   constexpr int NOUT = R * M * NR;                 // outputs of the workgroup
   static_assert(R == 1 || HS == 0, "several row sets per workgroup take whole sets");
-  static_assert(!WIDE || (KIND == 1 && R == 1 && HS <= 1 && M == 16),
-                "16 tokens: MFMA kind, single full or half sets (A rows 16p + token)");
+  static_assert(!WIDE || (KIND == 1 && HS <= 1 && M == 16),
+                "16 tokens: MFMA kind, whole or half sets (A rows 16p + token)");
   static_assert(NOUT * 4 <= SLAB, "a wave's partials fit its slab");
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);

@@ -433,6 +433,31 @@ def test_gemv_wide(kq4, torch_dev, orc, n, chain):
     assert np.array_equal(host(outq).view(np.uint32), host(outs[0][:n]).view(np.uint32))
 
 
+# The 16-token kernel's launch shapes through the planner options: 2 or 3 whole sets per
+# workgroup (the last group short), half sets, fewer waves than stages, with the activations
+# quantized in the kernel or apart.
+@pytest.mark.parametrize("plan", [dict(gemv_hs=0, gemv_rps=2), dict(gemv_hs=0, gemv_rps=3),
+                                  dict(gemv_hs=0, gemv_rps=3, gemv_fq=0, gemv_waves=2),
+                                  dict(gemv_hs=1, gemv_waves=3), dict(gemv_hs=0, gemv_rps=1)])
+@pytest.mark.parametrize("n", [11, 16])
+def test_gemv_wide_plans(kq4, torch_dev, orc, n, plan):
+    torch = torch_dev
+    rows, cols = [256, 100], 2080
+    ws = [synth.make_q4_weights(r, cols, 1500 + r + n) for r in rows]
+    x = synth.make_activations(n, cols, 1510 + n)
+    res = [synth.make_activations(n, r, 1520 + i) for i, r in enumerate(rows)]
+    W = [wdev(kq4, torch, w, r, cols) for w, r in zip(ws, rows)]
+    X, R = to_dev(torch, x), [to_dev(torch, r) for r in res]
+    outs = [torch.empty((n, r), dtype=torch.float32, device="cuda") for r in rows]
+    with kq4.options(**plan):
+        kq4.matmul_multi_dev(outs, X, W, rows, cols, residuals=R)
+    torch.cuda.synchronize()
+    for o, w, r, rr in zip(outs, ws, rows, res):
+        e, a = rel_err(host(o), orc.matmul(w, x, r, cols, residual=rr))
+        print(f"gemv wide plan {plan} n={n} rows={r}: rel={e:.3e} maxabs={a:.3e}")
+        assert e <= TOL
+
+
 def test_gemm_from_prequantized(kq4, torch_dev, orc):
     torch = torch_dev
     rows, cols, n = 128, 1024, 40
